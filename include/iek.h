@@ -1,0 +1,145 @@
+/*
+ * iek.h — C ABI of the MI355X-native token loop (libiek.so).
+ *
+ * Drop-in for the GPU side of AntoineKhoury/inference_engine_rust's greedy prefill/decode path.
+ * Every entry point names the reference interface it replaces (paths relative to the reference
+ * repository root). Conventions:
+ *   - Every function returns an iek_status (0 = OK); iek_last_error() gives a thread-local
+ *     message. Status values are the reference's EngineError variants (src/error.rs:5-38).
+ *   - Engine-level calls take host buffers and are synchronous on return.
+ *   - Op-level calls take DEVICE pointers plus an optional hipStream_t (NULL = the library's
+ *     default stream) and are asynchronous, like any HIP launch; iek_synchronize() waits.
+ *   - Handles are not thread-safe; one session per host thread.
+ */
+#ifndef IEK_H
+#define IEK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum iek_status {
+  IEK_OK = 0,
+  IEK_ERR_IO = 1,        /* EngineError::Io */
+  IEK_ERR_UTF8 = 2,      /* EngineError::Utf8 */
+  IEK_ERR_GGUF = 3,      /* EngineError::Gguf */
+  IEK_ERR_TENSOR = 4,    /* EngineError::Tensor */
+  IEK_ERR_MATMUL = 5,    /* EngineError::MatMul */
+  IEK_ERR_MODEL = 6,     /* EngineError::Model */
+  IEK_ERR_TOKENIZER = 7, /* EngineError::Tokenizer */
+  IEK_ERR_KV_CACHE = 8,  /* EngineError::KvCache (src/layers/attention.rs:113-126) */
+  IEK_ERR_SAMPLING = 9,  /* EngineError::Sampling (src/engine/sampling.rs:8-21) */
+  IEK_ERR_OP = 10,       /* EngineError::Op */
+  IEK_ERR_DEVICE = 11    /* HIP runtime failure (no reference counterpart: the reference is CPU-only) */
+} iek_status;
+
+/* Tensor dtypes: the reference's TensorType (src/core/tensor.rs:13-23). */
+typedef enum iek_dtype { IEK_F32 = 0, IEK_Q4K = 1, IEK_Q6K = 2, IEK_Q8_0 = 3 } iek_dtype;
+
+typedef struct iek_model iek_model;
+typedef struct iek_session iek_session;
+
+/* ModelConfig (src/model_config.rs:102-140), fields the token loop depends on. */
+typedef struct iek_model_config {
+  int32_t family; /* 0 MistralLlama, 1 Gemma4 (ModelFamily, model_config.rs:62-70) */
+  uint64_t context_length, hidden_dim, n_layers, n_heads, n_kv_heads, head_dim, ffn_dim, vocab_size;
+  float rope_theta, rms_norm_eps;
+  int32_t unpack_llama_gguf_qk;
+  uint64_t embedding_length_per_layer;
+  int32_t has_final_logit_softcapping;
+  float final_logit_softcapping;
+} iek_model_config;
+
+/* Last error message of the calling thread. */
+const char* iek_last_error(void);
+
+/* ---- model ---------------------------------------------------------------------------------
+ * Replaces LoadedModel::load (src/loaded_model.rs:23-50): GGUF parse (file_loader.rs:26-65),
+ * ModelConfig::from_gguf (model_config.rs:143-306), ModelWeightNames::resolve/load_all
+ * (names.rs:52-276), then one upload of every tensor's native blocks to HBM on `device`. */
+iek_status iek_model_load(const char* gguf_path, int device, iek_model** out);
+void iek_model_free(iek_model* model);
+/* LoadedModel::config (src/loaded_model.rs:51-53). */
+iek_status iek_model_config_get(const iek_model* model, iek_model_config* out);
+/* Per-layer LayerAttentionSpec + LayerDims (model_config.rs:72-100, :484-629): window -1 = none,
+ * kv_borrow -1 = none. */
+iek_status iek_model_layer_spec(const iek_model* model, uint64_t layer, int64_t* sliding_window, float* rope_theta,
+                                uint64_t* rotary_dim, int64_t* kv_borrow, uint64_t* head_dim, uint64_t* ffn_dim);
+
+/* GGUFData::get_tensor (src/model_loader/gguf_types.rs:343-346): the HBM address, dtype, ggml
+ * dims ([ne0, ne1], ne1 = 1 for vectors) and byte length of a loaded tensor. IEK_ERR_MODEL when
+ * the name was not loaded. */
+iek_status iek_model_tensor(const iek_model* model, const char* name, const void** dev_ptr, int* dtype,
+                            uint64_t* ne0, uint64_t* ne1, uint64_t* bytes);
+
+/* ---- session (src/engine/session.rs:12-75) -------------------------------------------------- */
+/* InferenceSession::new: KV caches of context_length positions per layer (fp16 in HBM). */
+iek_status iek_session_create(iek_model* model, iek_session** out);
+void iek_session_free(iek_session* s);
+/* InferenceSession::reset (session.rs:40-42). */
+iek_status iek_session_reset(iek_session* s);
+/* InferenceSession::prefill (session.rs:44-56) = prefill_from_tokens_loaded + prefill_forward
+ * (embed.rs:104-138, runtime.rs:14-32). */
+iek_status iek_session_prefill(iek_session* s, const uint32_t* token_ids, size_t n);
+/* InferenceSession::decode_token (session.rs:58-69) = embedding row + decode_forward
+ * (embed.rs:53-98, runtime.rs:37-61). */
+iek_status iek_session_decode_token(iek_session* s, uint32_t token_id);
+/* InferenceSession::logits_last_token -> final_logits_last_token (runtime.rs:76-116).
+ * `out` holds at least vocab_size floats. */
+iek_status iek_session_logits_last_token(iek_session* s, float* out, size_t out_len);
+/* greedy_next_token (src/engine/generation.rs:10-16) with argmax on the device
+ * (sampling.rs:25-49: first maximal index; IEK_ERR_SAMPLING on any non-finite logit). */
+iek_status iek_greedy_next_token(iek_session* s, uint32_t* out_token);
+/* n iterations of { id = greedy_next_token; decode_token(id) } — the loop of src/main.rs:100-116
+ * and EngineBench::run_decode_throughput (src/bench_metrics.rs:178-182) — replayed as one
+ * captured decode-step graph; token ids never leave the device until the end. */
+iek_status iek_session_generate_greedy(iek_session* s, size_t n_steps, uint32_t* out_ids);
+/* KVCache::current_pos (attention.rs:49-52). */
+iek_status iek_session_kv_len(const iek_session* s, uint64_t* out);
+/* Hidden rows of the current ForwardState ([rows, hidden], src/engine/state.rs:7-175). */
+iek_status iek_session_hidden(iek_session* s, float* out, size_t cap, uint64_t* rows);
+/* KVCache::get_k_slice/get_v_slice for every stored position (attention.rs:77-110), widened to
+ * f32 as [n_kv][kv_len][head_dim]. */
+iek_status iek_session_kv(iek_session* s, uint64_t layer, int which_v, float* out, size_t cap);
+
+/* ---- op level (device pointers) ------------------------------------------------------------ */
+/* dequantize_{q4k,q6k,q8_0}_block over n consecutive blocks (quant_k_handler.rs:21-135). */
+iek_status iek_dequantize(int dtype, const void* blocks, size_t nblocks, float* out, void* stream);
+/* matmul (src/ops/matmul.rs:18-415): out[m,n] = sum_k a[m,k] * W(k,n), W in ggml layout
+ * (element (k,n) at flat k + n*K) and native block bytes. w_bytes is checked against
+ * div_ceil(K*N, block) * block_bytes like the reference. */
+iek_status iek_matmul(const float* a, size_t m, size_t k, int w_dtype, const void* w, size_t w_bytes, size_t n,
+                      float* out, void* stream);
+/* rmsnorm over `rows` rows of `dim` (src/ops/rmsnorm.rs:25-50). */
+iek_status iek_rmsnorm(const float* in, const float* weight, size_t rows, size_t dim, float eps, float* out,
+                       void* stream);
+/* rope (src/ops/rope.rs:11-59) on n_heads contiguous heads of head_dim, at position `pos`;
+ * freq_factors: HOST pointer or NULL. */
+iek_status iek_rope(float* vec, size_t n_heads, uint32_t head_dim, uint32_t rotary_dim, float base, uint32_t pos,
+                    const float* freq_factors, size_t ff_len, void* stream);
+/* softmax (src/ops/softmax.rs:3-28). */
+iek_status iek_softmax(const float* in, float* out, size_t n, void* stream);
+/* swiglu (src/ops/swiglu.rs:24-36). */
+iek_status iek_swiglu(const float* gate, const float* up, float* out, size_t n, void* stream);
+/* out = gelu_tanh(gate) * up, or gelu_tanh(gate) when up is NULL (src/ops/gelu.rs:5-11). */
+iek_status iek_gelu_tanh(const float* gate, const float* up, float* out, size_t n, void* stream);
+/* residual_add (src/ops/residual_add.rs:3-12). */
+iek_status iek_residual_add(const float* a, const float* b, float* out, size_t n, void* stream);
+/* argmax_index / sample_greedy (src/engine/sampling.rs:25-49). Synchronous; *out_index gets the
+ * first maximal index. IEK_ERR_SAMPLING when n == 0 or any logit is non-finite. */
+iek_status iek_argmax(const float* logits, size_t n, uint32_t* out_index, void* stream);
+
+/* ---- device memory helpers for FFI callers without a HIP binding ---------------------------- */
+iek_status iek_device_alloc(size_t bytes, void** out);
+iek_status iek_device_free(void* p);
+iek_status iek_memcpy_h2d(void* dst, const void* src, size_t bytes);
+iek_status iek_memcpy_d2h(void* dst, const void* src, size_t bytes);
+iek_status iek_synchronize(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* IEK_H */

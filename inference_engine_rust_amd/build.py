@@ -1,0 +1,81 @@
+"""Build recipe for the native libraries (in-tree, so they travel with the repository snapshot).
+
+* ``libiek.so``        — the product: HIP kernels for gfx950 + the C++ host runtime + C ABI.
+* ``libiek_synth.so``  — seeded synthetic GGUF writer / quantisers (host C++).
+
+Objects go to ``inference_engine_rust_amd/_build``; each translation unit compiles in its own
+process so the build parallelises across cores.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(PKG, "csrc")
+BUILD = os.path.join(PKG, "_build")
+LIB = os.path.join(PKG, "libiek.so")
+SYNTH_LIB = os.path.join(PKG, "libiek_synth.so")
+ARCH = os.environ.get("IEK_OFFLOAD_ARCH", "gfx950")
+
+HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+# Packed-FP32 VALU ops are disabled for all device code ("Build flags").
+HIP_FLAGS = ["-std=c++17", "-O3", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
+             "-packed-fp32-ops", "-Wall", "-Wno-unused-function", "-Wno-unused-result"]
+
+SOURCES = [
+    "kernels/matvec.hip",
+    "kernels/ops.hip",
+    "kernels/attention.hip",
+    "kernels/gemm.hip",
+    "model.cpp",
+    "session.cpp",
+    "api.cpp",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in r.stdout.splitlines() if "unknown target feature" not in l and
+                    "warning: feature flag" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"command failed ({r.returncode}): {' '.join(cmd)}\n{out}")
+    if out.strip():
+        sys.stderr.write(out + "\n")
+
+
+def _compile(src: str) -> str:
+    obj = os.path.join(BUILD, src.replace("/", "_").rsplit(".", 1)[0] + ".o")
+    lang = ["-x", "hip"]
+    _run([HIPCC, *lang, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+    return obj
+
+
+def build_synth() -> str:
+    _run(["g++", "-std=c++17", "-O2", "-march=x86-64-v3", "-fPIC", "-shared", "-pthread", "-Wall",
+          "-Wno-unused-function", "-o", SYNTH_LIB, os.path.join(CSRC, "synth", "gguf_synth.cpp")])
+    return SYNTH_LIB
+
+
+def build_lib(jobs: int | None = None) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    jobs = jobs or min(len(SOURCES), os.cpu_count() or 1)
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(_compile, SOURCES))
+    tmp = LIB + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_all() -> None:
+    build_synth()
+    build_lib()
+
+
+if __name__ == "__main__":
+    build_all()
+    print(LIB)

@@ -1,0 +1,74 @@
+// Internal declarations shared by the host runtime (C++) and the HIP kernel launchers.
+#pragma once
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+#include <string>
+
+namespace iek {
+
+// Status codes: the reference's EngineError variants (src/error.rs:5-38) plus a device class.
+enum Status : int {
+  ST_OK = 0, ST_IO = 1, ST_UTF8 = 2, ST_GGUF = 3, ST_TENSOR = 4, ST_MATMUL = 5, ST_MODEL = 6,
+  ST_TOKENIZER = 7, ST_KVCACHE = 8, ST_SAMPLING = 9, ST_OP = 10, ST_DEVICE = 11,
+};
+
+// dtype ids follow the reference's TensorType (src/core/tensor.rs:13-23).
+enum DType : int { DT_F32 = 0, DT_Q4K = 1, DT_Q6K = 2, DT_Q8_0 = 3 };
+
+struct Error {
+  int code;
+  std::string msg;
+};
+
+[[noreturn]] void fail(int code, const std::string& msg);
+void check_hip(hipError_t e, const char* what);
+#define IEK_HIP(call) ::iek::check_hip((call), #call)
+
+struct MvSegDesc {
+  const void* w;
+  float* out;
+  const float* resid;
+  int n;
+};
+
+// ---- kernel launchers (all asynchronous on `st`) ----
+// epi: 0 store, 1 residual add (out = resid + dot), 2 SwiGLU over a (gate, up) segment pair.
+void launch_matvec(int dt, const MvSegDesc* segs, int nseg, const float* x, int K, int epi, hipStream_t st);
+void launch_gemm(int dt, const void* w, const float* a, int M, int K, int N, float* out, const float* resid,
+                 hipStream_t st);
+void launch_dequant(int dt, const void* blocks, size_t nblocks, float* out, hipStream_t st);
+void launch_embed(int dt, const void* table, size_t hidden, const uint32_t* ids, int n, float scale, float* out,
+                  hipStream_t st);
+void launch_rmsnorm(const float* in, const float* w, int rows, int dim, float eps, float* out, hipStream_t st);
+void launch_rope_rows(float* v, int rows, int row_stride, int n_heads, int head_dim, int pos0, const float* cs,
+                      int half_pairs, hipStream_t st);
+void launch_rope_table(float* v, int n_heads, int head_dim, int npairs, const float* cs, const int* pos_dev,
+                       hipStream_t st);
+void launch_kv_store(const float* k, const float* v, int rows, int kv_dim, __half* kc, __half* vc, int n_kv,
+                     int head_dim, int ctx, const int* pos_dev, int pos0, hipStream_t st);
+void launch_swiglu(const float* g, const float* u, float* out, size_t n, hipStream_t st);
+void launch_gelu_mul(const float* g, const float* u, float* out, size_t n, hipStream_t st);
+void launch_residual_add(const float* a, const float* b, float* out, size_t n, hipStream_t st);
+void launch_softmax(const float* in, float* out, int n, hipStream_t st);
+// Greedy argmax: atomicMax of packed (value, first-index) keys; non-finite logits set flags[*step].
+void launch_argmax(const float* logits, int n, unsigned long long* key_out, int* flags, const int* step, hipStream_t st);
+// tok[0] = argmax index; with a step counter also list[*step] = index and ++*step.
+void launch_argmax_finish(const unsigned long long* key, uint32_t* tok, uint32_t* list, int* step, hipStream_t st);
+void launch_softcap(float* z, int n, float cap, hipStream_t st);
+void launch_unpack_qk(const float* src, float* dst, int rows, int row_stride, int n_groups, int head_dim,
+                      hipStream_t st);
+void launch_copy_f32(const float* src, float* dst, size_t n, hipStream_t st);
+void launch_fill_i32(int* p, int v, int n, hipStream_t st);
+void launch_attn_decode(const float* q, const __half* kc, const __half* vc, float* out, float* part, int n_heads,
+                        int n_kv, int head_dim, int ctx, const int* pos_dev, int window, float scale, int max_len,
+                        hipStream_t st);
+void launch_attn_prefill(const float* q, const float* k, const float* v, float* out, int M, int n_heads, int n_kv,
+                         int head_dim, int window, float scale, hipStream_t st);
+void launch_fill_u64(unsigned long long* p, unsigned long long v, int n, hipStream_t st);
+void launch_set_int(int* p, int v, hipStream_t st);
+void launch_add_int(int* p, int v, hipStream_t st);
+
+}  // namespace iek

@@ -1,0 +1,115 @@
+// Device helpers shared by the CDNA4 (gfx950) kernels: wave64 reductions, block dequant
+// primitives matching the reference's arithmetic, and the ggml block geometry.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "../iek_internal.h"
+
+#define IEK_DEV __device__ __forceinline__
+
+namespace iek {
+
+constexpr int WAVE = 64;
+constexpr int QK_K = 256;
+constexpr int Q4K_BYTES = 144;
+constexpr int Q6K_BYTES = 210;
+constexpr int Q8_0_ELEMS = 32;
+constexpr int Q8_0_BYTES = 34;
+
+// IEEE half bits -> f32. Exact for every non-NaN input (subnormals included), which is what the
+// reference's hand-rolled f16_to_f32 computes (src/ops/quant/utils.rs:2-32).
+IEK_DEV float half_bits_to_float(uint32_t bits16) {
+  return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xFFFFu)));
+}
+
+IEK_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, WAVE);
+  return v;
+}
+
+IEK_DEV float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, WAVE));
+  return v;
+}
+
+IEK_DEV uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xFFu; }
+
+// get_scale_min_k4 over the 12 packed scale bytes held as three dwords
+// (src/ops/quant/quant_k_handler.rs:138-155).
+IEK_DEV void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2, float* sc, float* m) {
+  if (j < 4) {
+    *sc = (float)(byte_of(s0, j) & 63u);
+    *m = (float)(byte_of(s1, j) & 63u);
+  } else {
+    uint32_t lo = byte_of(s2, j - 4);
+    *sc = (float)((lo & 0xFu) | ((byte_of(s0, j - 4) >> 6) << 4));
+    *m = (float)((lo >> 4) | ((byte_of(s1, j - 4) >> 6) << 4));
+  }
+}
+
+// One dequantised element of a Q4_K block: (d*sc)*q - dmin*m with the reference's q == 0 -> 0
+// convention (quant_k_handler.rs:6-8, :38-82). Every product is exact in f32 (at most 21
+// significant bits), so the single f32 rounding of the subtraction equals the reference's
+// f64-then-f32 result.
+IEK_DEV float q4k_value(float d, float dmin, float sc, float m, uint32_t q) {
+#pragma clang fp contract(off)
+  float ds = __fmul_rn(d, sc);
+  float dq = q == 0 ? 0.0f : __fmul_rn(ds, (float)q);
+  return __fsub_rn(dq, __fmul_rn(dmin, m));
+}
+
+// Unaligned little-endian u16 from a byte pointer (Q6_K / Q8_0 blocks are only 2-byte aligned).
+IEK_DEV uint32_t load_u16(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
+
+// Single element `o` (0..255) of a Q4_K block.
+IEK_DEV float q4k_elem(const uint8_t* blk, int o) {
+  float d = half_bits_to_float(load_u16(blk)), dmin = half_bits_to_float(load_u16(blk + 2));
+  const uint8_t* s = blk + 4;
+  int g = o >> 6, r = o & 63, is = 2 * g + (r >= 32 ? 1 : 0), l = r & 31;
+  uint32_t byte = blk[16 + 32 * g + l];
+  uint32_t q = r < 32 ? (byte & 0xFu) : (byte >> 4);
+  float sc, m;
+  if (is < 4) {
+    sc = (float)(s[is] & 63);
+    m = (float)(s[is + 4] & 63);
+  } else {
+    sc = (float)((s[is + 4] & 0xF) | ((s[is - 4] >> 6) << 4));
+    m = (float)((s[is + 4] >> 4) | ((s[is] >> 6) << 4));
+  }
+  return q4k_value(d, dmin, sc, m, q);
+}
+
+// Single element of a Q6_K block (quant_k_handler.rs:85-135): y = (d*s)*q, int8 s, q in [-32,31].
+IEK_DEV float q6k_elem(const uint8_t* blk, int o) {
+  float d = half_bits_to_float(load_u16(blk + 208));
+  int h = o >> 7, r = o & 127, quarter = r >> 5, l = r & 31;
+  uint32_t qlb = blk[64 * h + l + ((quarter & 1) ? 32 : 0)];
+  uint32_t nib = quarter < 2 ? (qlb & 0xFu) : (qlb >> 4);
+  uint32_t hb = (blk[128 + 32 * h + l] >> (2 * quarter)) & 3u;
+  int q = (int)(nib | (hb << 4)) - 32;
+  float s = (float)(int8_t)blk[192 + 8 * h + (l >> 4) + 2 * quarter];
+  float ds = __fmul_rn(d, s);
+  return q == 0 ? 0.0f : __fmul_rn(ds, (float)q);
+}
+
+// Single element of a Q8_0 block (quant_k_handler.rs:21-35).
+IEK_DEV float q80_elem(const uint8_t* blk, int o) {
+  float d = half_bits_to_float(load_u16(blk));
+  return __fmul_rn(d, (float)(int8_t)blk[2 + o]);
+}
+
+// Element at flat index `f` of a tensor stored as consecutive blocks of type `dt`.
+IEK_DEV float flat_elem(int dt, const uint8_t* base, size_t f) {
+  switch (dt) {
+    case DT_Q4K: return q4k_elem(base + (f / QK_K) * Q4K_BYTES, (int)(f % QK_K));
+    case DT_Q6K: return q6k_elem(base + (f / QK_K) * Q6K_BYTES, (int)(f % QK_K));
+    case DT_Q8_0: return q80_elem(base + (f / Q8_0_ELEMS) * Q8_0_BYTES, (int)(f % Q8_0_ELEMS));
+    default: return reinterpret_cast<const float*>(base)[f];
+  }
+}
+
+}  // namespace iek

@@ -1,0 +1,66 @@
+// Prefill matmul (M > 1): out[m, n] = sum_k a[m, k] * W(k, n) with W in its native GGUF blocks.
+// Tiled SIMT kernel: a 64x64 output tile per 256-thread block; each 32-wide K slab of W is
+// dequantised into LDS once and reused by all 64 rows of the tile.
+#include "common.cuh"
+#include "../iek_internal.h"
+
+namespace iek {
+
+constexpr int GBM = 64, GBN = 64, GBK = 32;
+
+__global__ __launch_bounds__(256) void gemm_simt_kernel(int dt, const uint8_t* __restrict__ w,
+                                                        const float* __restrict__ a, int M, int K, int N,
+                                                        float* __restrict__ out, const float* __restrict__ resid) {
+  __shared__ float As[GBK][GBM + 4];
+  __shared__ float Ws[GBK][GBN + 4];
+  const int tid = threadIdx.x;
+  const int m0 = blockIdx.y * GBM, n0 = blockIdx.x * GBN;
+  const int tm = (tid / 16) * 4, tn = (tid % 16) * 4;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < K; k0 += GBK) {
+    for (int e = tid; e < GBM * GBK; e += 256) {
+      int r = e / GBK, c = e % GBK;
+      int gm = m0 + r, gk = k0 + c;
+      As[c][r] = (gm < M && gk < K) ? a[(size_t)gm * K + gk] : 0.f;
+    }
+    for (int e = tid; e < GBN * GBK; e += 256) {
+      int cn = e / GBK, c = e % GBK;
+      int gn = n0 + cn, gk = k0 + c;
+      Ws[c][cn] = (gn < N && gk < K) ? flat_elem(dt, w, (size_t)gk + (size_t)gn * K) : 0.f;
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int kk = 0; kk < GBK; ++kk) {
+      float av[4], wv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        av[i] = As[kk][tm + i];
+        wv[i] = Ws[kk][tn + i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += av[i] * wv[j];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int gm = m0 + tm + i, gn = n0 + tn + j;
+      if (gm < M && gn < N) {
+        float v = acc[i][j];
+        if (resid) v = resid[(size_t)gm * N + gn] + v;
+        out[(size_t)gm * N + gn] = v;
+      }
+    }
+}
+
+void launch_gemm(int dt, const void* w, const float* a, int M, int K, int N, float* out, const float* resid,
+                 hipStream_t st) {
+  dim3 grid((N + GBN - 1) / GBN, (M + GBM - 1) / GBM);
+  hipLaunchKernelGGL(gemm_simt_kernel, grid, dim3(256), 0, st, dt, (const uint8_t*)w, a, M, K, N, out, resid);
+}
+
+}  // namespace iek

@@ -1,0 +1,332 @@
+// Small ops: block dequant, embedding gather, RMSNorm, RoPE (+fp16 KV append), gated
+// activations, residual add, softmax and the on-device greedy argmax.
+// Each follows the reference op it replaces (src/ops/*.rs). HIP's __fmul_rn/__fadd_rn are plain
+// operators that clang may still fuse into FMAs, so functions whose f32 steps the reference rounds
+// separately also turn contraction off (#pragma clang fp contract(off)).
+#include "common.cuh"
+#include "../iek_internal.h"
+
+namespace iek {
+
+__global__ void dequant_kernel(int dt, const uint8_t* blocks, size_t n, float* out) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = flat_elem(dt, blocks, i);
+}
+
+void launch_dequant(int dt, const void* blocks, size_t nblocks, float* out, hipStream_t st) {
+  size_t be = dt == DT_Q8_0 ? Q8_0_ELEMS : QK_K;
+  size_t n = nblocks * be;
+  if (n == 0) return;
+  hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, dt,
+                     (const uint8_t*)blocks, n, out);
+}
+
+// Token-row gather (src/layers/embeddings.rs:95-210): element h of token t sits at flat index
+// t*hidden + h. `ids` lives in device memory so a captured decode step can read the token that
+// the previous step's argmax produced.
+__global__ void embed_kernel(int dt, const uint8_t* table, size_t hidden, const uint32_t* ids, float scale, float* out) {
+  const int r = blockIdx.x;
+  const size_t base = (size_t)ids[r] * hidden;
+  for (size_t h = threadIdx.x; h < hidden; h += blockDim.x) {
+    float v = flat_elem(dt, table, base + h);
+    if (scale != 1.0f) v = __fmul_rn(v, scale);
+    out[(size_t)r * hidden + h] = v;
+  }
+}
+
+void launch_embed(int dt, const void* table, size_t hidden, const uint32_t* ids, int n, float scale, float* out,
+                  hipStream_t st) {
+  hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, st, dt, (const uint8_t*)table, hidden, ids, scale, out);
+}
+
+// Block-wide sum for 256-thread blocks.
+IEK_DEV float block_sum256(float v, float* sh) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  if (l == 0) sh[w] = v;
+  __syncthreads();
+  float t = 0.f;
+  if (threadIdx.x < 64) {
+    t = threadIdx.x < (blockDim.x >> 6) ? sh[threadIdx.x] : 0.f;
+    t = wave_sum(t);
+    if (threadIdx.x == 0) sh[0] = t;
+  }
+  __syncthreads();
+  t = sh[0];
+  __syncthreads();
+  return t;
+}
+
+// rmsnorm (src/ops/rmsnorm.rs:25-50): rms = sqrt(sum(x^2)/dim + eps); y = (x*w)/rms.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* in, const float* w, int dim, float eps, float* out) {
+#pragma clang fp contract(off)
+  __shared__ float sh[8];
+  const float* x = in + (size_t)blockIdx.x * dim;
+  float* y = out + (size_t)blockIdx.x * dim;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < dim; i += blockDim.x) ss += __fmul_rn(x[i], x[i]);
+  ss = block_sum256(ss, sh);
+  const float rms = __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)dim), eps));
+  for (int i = threadIdx.x; i < dim; i += blockDim.x) y[i] = __fdiv_rn(__fmul_rn(x[i], w[i]), rms);
+}
+
+void launch_rmsnorm(const float* in, const float* w, int rows, int dim, float eps, float* out, hipStream_t st) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, st, in, w, dim, eps, out);
+}
+
+// RoPE on adjacent pairs (src/ops/rope.rs:11-59). `cs` holds (cos, sin) per (position, pair),
+// built on the host with the reference's f32 running-product angles and libm cosf/sinf.
+IEK_DEV void rotate(float* v, int p, float c, float s) {
+#pragma clang fp contract(off)
+  float t0 = v[p], t1 = v[p + 1];
+  v[p] = __fsub_rn(__fmul_rn(t0, c), __fmul_rn(t1, s));
+  v[p + 1] = __fadd_rn(__fmul_rn(t0, s), __fmul_rn(t1, c));
+}
+
+__global__ void rope_rows_kernel(float* v, int rows, int row_stride, int n_heads, int head_dim, int pos0,
+                                 const float* cs, int npairs) {
+  const size_t total = (size_t)rows * n_heads * npairs;
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int k = (int)(i % npairs);
+  const int h = (int)((i / npairs) % n_heads);
+  const int r = (int)(i / ((size_t)npairs * n_heads));
+  const float* e = cs + ((size_t)(pos0 + r) * npairs + k) * 2;
+  rotate(v + (size_t)r * row_stride + (size_t)h * head_dim, 2 * k, e[0], e[1]);
+}
+
+void launch_rope_rows(float* v, int rows, int row_stride, int n_heads, int head_dim, int pos0, const float* cs,
+                      int npairs, hipStream_t st) {
+  size_t total = (size_t)rows * n_heads * npairs;
+  if (total == 0) return;
+  hipLaunchKernelGGL(rope_rows_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, v, rows, row_stride,
+                     n_heads, head_dim, pos0, cs, npairs);
+}
+
+// Decode-step RoPE: position read from device memory.
+__global__ void rope_dev_kernel(float* v, int n_heads, int head_dim, int npairs, const float* cs, const int* pos_dev) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_heads * npairs) return;
+  const int k = i % npairs, h = i / npairs;
+  const float* e = cs + ((size_t)(*pos_dev) * npairs + k) * 2;
+  rotate(v + (size_t)h * head_dim, 2 * k, e[0], e[1]);
+}
+
+void launch_rope_table(float* v, int n_heads, int head_dim, int npairs, const float* cs, const int* pos_dev,
+                       hipStream_t st) {
+  int total = n_heads * npairs;
+  if (total == 0) return;
+  hipLaunchKernelGGL(rope_dev_kernel, dim3((total + 255) / 256), dim3(256), 0, st, v, n_heads, head_dim, npairs, cs,
+                     pos_dev);
+}
+
+// KV append: rows [r] of k/v ([rows][kv_dim], f32) go to cache position (pos + r) as fp16.
+// Cache layout per layer: [n_kv][ctx][head_dim], so one head's keys are one contiguous stream.
+__global__ void kv_store_kernel(const float* k, const float* v, int rows, int kv_dim, __half* kc, __half* vc,
+                                int head_dim, int ctx, const int* pos_dev, int pos0) {
+  const size_t total = (size_t)rows * kv_dim;
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int r = (int)(i / kv_dim), c = (int)(i % kv_dim);
+  const int h = c / head_dim, d = c % head_dim;
+  const int pos = (pos_dev ? *pos_dev : pos0) + r;
+  const size_t dst = ((size_t)h * ctx + pos) * head_dim + d;
+  kc[dst] = __float2half_rn(k[i]);
+  vc[dst] = __float2half_rn(v[i]);
+}
+
+void launch_kv_store(const float* k, const float* v, int rows, int kv_dim, __half* kc, __half* vc, int n_kv,
+                     int head_dim, int ctx, const int* pos_dev, int pos0, hipStream_t st) {
+  (void)n_kv;
+  size_t total = (size_t)rows * kv_dim;
+  if (total == 0) return;
+  hipLaunchKernelGGL(kv_store_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, k, v, rows, kv_dim, kc,
+                     vc, head_dim, ctx, pos_dev, pos0);
+}
+
+// swiglu (src/ops/swiglu.rs:24-36): out = (g * sigmoid(g)) * u, two-branch stable sigmoid.
+__global__ void swiglu_kernel(const float* g, const float* u, float* out, size_t n) {
+#pragma clang fp contract(off)
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float x = g[i], s;
+  if (x >= 0.0f) {
+    float z = expf(-x);
+    s = __fdiv_rn(1.0f, __fadd_rn(1.0f, z));
+  } else {
+    float z = expf(x);
+    s = __fdiv_rn(z, __fadd_rn(1.0f, z));
+  }
+  out[i] = __fmul_rn(__fmul_rn(x, s), u[i]);
+}
+
+void launch_swiglu(const float* g, const float* u, float* out, size_t n, hipStream_t st) {
+  if (n == 0) return;
+  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, u, out, n);
+}
+
+// gelu_tanh(g) * u (src/ops/gelu.rs:5-11, src/layers/ffn.rs:49-53).
+IEK_DEV float gelu_tanh_dev(float x) {
+#pragma clang fp contract(off)
+  const float k = 1.12837916709551257390f * 0.707106781186547524401f;
+  float x3 = __fmul_rn(__fmul_rn(x, x), x);
+  float inner = __fmul_rn(k, __fadd_rn(x, __fmul_rn(0.044715f, x3)));
+  return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanhf(inner)));
+}
+
+__global__ void gelu_mul_kernel(const float* g, const float* u, float* out, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = __fmul_rn(gelu_tanh_dev(g[i]), u ? u[i] : 1.0f);
+}
+
+void launch_gelu_mul(const float* g, const float* u, float* out, size_t n, hipStream_t st) {
+  if (n == 0) return;
+  hipLaunchKernelGGL(gelu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, u, out, n);
+}
+
+__global__ void residual_add_kernel(const float* a, const float* b, float* out, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = __fadd_rn(a[i], b[i]);
+}
+
+void launch_residual_add(const float* a, const float* b, float* out, size_t n, hipStream_t st) {
+  if (n == 0) return;
+  hipLaunchKernelGGL(residual_add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a, b, out, n);
+}
+
+// softmax (src/ops/softmax.rs:3-28), one 256-thread block.
+__global__ __launch_bounds__(256) void softmax_kernel(const float* in, float* out, int n) {
+#pragma clang fp contract(off)
+  __shared__ float sh[8];
+  float m = -INFINITY;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) m = fmaxf(m, in[i]);
+  m = wave_max(m);
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  if (l == 0) sh[w] = m;
+  __syncthreads();
+  float mm = sh[0];
+  for (int i = 1; i < (int)(blockDim.x >> 6); ++i) mm = fmaxf(mm, sh[i]);
+  __syncthreads();
+  float s = 0.f;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) s += expf(in[i] - mm);
+  s = block_sum256(s, sh);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = __fdiv_rn(expf(in[i] - mm), s);
+}
+
+void launch_softmax(const float* in, float* out, int n, hipStream_t st) {
+  hipLaunchKernelGGL(softmax_kernel, dim3(1), dim3(256), 0, st, in, out, n);
+}
+
+// Greedy argmax (src/engine/sampling.rs:25-49): first index of the maximum; any non-finite logit
+// raises a flag (the reference returns InvalidLogits). The (value, index) pair is packed into one
+// u64 whose unsigned order is (value ascending, index descending), so a single atomicMax picks the
+// first maximal index.
+IEK_DEV unsigned long long argmax_key(float v, uint32_t idx) {
+  uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(const float* logits, int n, unsigned long long* key, int* flags,
+                                                     const int* step) {
+  unsigned long long best = 0;
+  bool bad = false;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    float v = logits[i];
+    if (!isfinite(v)) bad = true;
+    unsigned long long k = argmax_key(v, (uint32_t)i);
+    best = k > best ? k : best;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    unsigned long long o = __shfl_xor(best, off, WAVE);
+    best = o > best ? o : best;
+  }
+  if ((threadIdx.x & 63) == 0) atomicMax(key, best);
+  if (bad) atomicOr(&flags[step ? *step : 0], 1);
+}
+
+void launch_argmax(const float* logits, int n, unsigned long long* key_out, int* flags, const int* step, hipStream_t st) {
+  int blocks = std::min(256, (n + 255) / 256);
+  hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(256), 0, st, logits, n, key_out, flags, step);
+}
+
+// Publishes the chosen token: tok[0] feeds the next embedding gather; with a step counter the id
+// is also appended to the generated-token list and the counter advances.
+__global__ void argmax_finish_kernel(const unsigned long long* key, uint32_t* tok, uint32_t* list, int* step) {
+  uint32_t idx = 0xFFFFFFFFu - (uint32_t)(*key & 0xFFFFFFFFull);
+  tok[0] = idx;
+  if (step) {
+    list[*step] = idx;
+    *step += 1;
+  }
+}
+
+void launch_argmax_finish(const unsigned long long* key, uint32_t* tok, uint32_t* list, int* step, hipStream_t st) {
+  hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(1), 0, st, key, tok, list, step);
+}
+
+// Final-logit soft cap z -> cap * tanh(z / cap) (src/engine/runtime.rs:110-114).
+__global__ void softcap_kernel(float* z, int n, float cap) {
+#pragma clang fp contract(off)
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) z[i] = __fmul_rn(cap, tanhf(__fdiv_rn(z[i], cap)));
+}
+void launch_softcap(float* z, int n, float cap, hipStream_t st) {
+  hipLaunchKernelGGL(softcap_kernel, dim3((n + 255) / 256), dim3(256), 0, st, z, n, cap);
+}
+
+// Inverse HF->GGUF Q/K permutation on activation rows (src/layers/attention.rs:149-172):
+// logical b*(d/2)+h <- stored h*2+b inside every head.
+__global__ void unpack_qk_kernel(const float* src, float* dst, int rows, int row_stride, int n_groups, int head_dim) {
+  const int half = head_dim / 2;
+  size_t total = (size_t)rows * n_groups * head_dim;
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  int e = (int)(i % head_dim);
+  int g = (int)((i / head_dim) % n_groups);
+  int r = (int)(i / ((size_t)head_dim * n_groups));
+  int b = e / half, h = e % half;
+  size_t base = (size_t)r * row_stride + (size_t)g * head_dim;
+  dst[base + e] = src[base + h * 2 + b];
+}
+void launch_unpack_qk(const float* src, float* dst, int rows, int row_stride, int n_groups, int head_dim,
+                      hipStream_t st) {
+  size_t total = (size_t)rows * n_groups * head_dim;
+  if (total == 0) return;
+  hipLaunchKernelGGL(unpack_qk_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, src, dst, rows,
+                     row_stride, n_groups, head_dim);
+}
+
+__global__ void copy_f32_kernel(const float* src, float* dst, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = src[i];
+}
+void launch_copy_f32(const float* src, float* dst, size_t n, hipStream_t st) {
+  if (n == 0) return;
+  hipLaunchKernelGGL(copy_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, src, dst, n);
+}
+
+__global__ void fill_i32_kernel(int* p, int v, int n) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+void launch_fill_i32(int* p, int v, int n, hipStream_t st) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(fill_i32_kernel, dim3((n + 255) / 256), dim3(256), 0, st, p, v, n);
+}
+
+__global__ void fill_u64_kernel(unsigned long long* p, unsigned long long v, int n) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+void launch_fill_u64(unsigned long long* p, unsigned long long v, int n, hipStream_t st) {
+  hipLaunchKernelGGL(fill_u64_kernel, dim3((n + 255) / 256), dim3(256), 0, st, p, v, n);
+}
+__global__ void set_int_kernel(int* p, int v) { *p = v; }
+void launch_set_int(int* p, int v, hipStream_t st) { hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, st, p, v); }
+__global__ void add_int_kernel(int* p, int v) { *p += v; }
+void launch_add_int(int* p, int v, hipStream_t st) { hipLaunchKernelGGL(add_int_kernel, dim3(1), dim3(1), 0, st, p, v); }
+
+}  // namespace iek

@@ -1,0 +1,387 @@
+// Session forward passes. Layer order and numerics follow the reference's layer code:
+//   prefill_layer_block / decode_layer_block     src/layers/block.rs:12-89
+//   mistral_*_attention_with_norm                src/layers/attention.rs:713-890
+//   prefill_attention_layer / decode_attention   src/layers/attention.rs:175-655
+//   mistral_prefill_ffn_with_norm / prefill_ffn  src/layers/ffn.rs:16-117
+//   final_logits_last_token                      src/engine/runtime.rs:76-116
+#include "session.h"
+
+#include <cmath>
+#include <cstring>
+
+namespace iek {
+
+namespace {
+
+template <class T>
+T* dev_alloc(size_t n) {
+  void* p = nullptr;
+  IEK_HIP(hipMalloc(&p, std::max<size_t>(n * sizeof(T), 16)));
+  return static_cast<T*>(p);
+}
+
+void dev_free(void* p) {
+  if (p) (void)hipFree(p);
+}
+
+}  // namespace
+
+Session::Session(Model* m) : m_(m) {
+  const Config& c = m->cfg;
+  if (c.family != FAM_MISTRAL_LLAMA)
+    fail(ST_MODEL, "device session: the Gemma 4 family is not supported by the device engine yet");
+  IEK_HIP(hipSetDevice(m->device));
+  IEK_HIP(hipStreamCreateWithFlags(&st_, hipStreamNonBlocking));
+  ctx_ = c.context_length;
+  H_ = c.hidden;
+  // KV cache (fp16): per layer K and V as [n_kv][ctx][head_dim] (kv_caches_for_config,
+  // attention.rs:129-135, sizes every cache to context_length).
+  size_t total = 0;
+  for (auto& L : c.layers) total += 2 * (size_t)c.n_kv_heads * ctx_ * L.head_dim;
+  IEK_HIP(hipMalloc(&kv_blob_, std::max<size_t>(total * sizeof(__half), 16)));
+  __half* p = static_cast<__half*>(kv_blob_);
+  for (auto& L : c.layers) {
+    size_t per = (size_t)c.n_kv_heads * ctx_ * L.head_dim;
+    kc_.push_back(p);
+    vc_.push_back(p + per);
+    p += 2 * per;
+  }
+  int qmax = 0, kvmax = 0, fmax = 0, hdmax = 0;
+  for (auto& L : c.layers) {
+    qmax = std::max(qmax, L.q_dim);
+    kvmax = std::max(kvmax, L.kv_dim);
+    fmax = std::max(fmax, L.ffn_dim);
+    hdmax = std::max(hdmax, L.head_dim);
+  }
+  xdec_ = dev_alloc<float>(H_);
+  xndec_ = dev_alloc<float>(std::max(H_, qmax));
+  qd_ = dev_alloc<float>(qmax);
+  kd_ = dev_alloc<float>(kvmax);
+  vd_ = dev_alloc<float>(kvmax);
+  attd_ = dev_alloc<float>(qmax);
+  actd_ = dev_alloc<float>(fmax);
+  tmpd_ = dev_alloc<float>(std::max(qmax, fmax));
+  logits_ = dev_alloc<float>(c.vocab);
+  const int nsplit = (ctx_ + 63) / 64;
+  part_ = dev_alloc<float>((size_t)c.n_heads * nsplit * (hdmax + 2));
+  d_pos_ = dev_alloc<int>(1);
+  d_step_ = dev_alloc<int>(1);
+  d_flags_ = dev_alloc<int>(ctx_ + 1);
+  d_tok_ = dev_alloc<uint32_t>(1);
+  d_ids_ = dev_alloc<uint32_t>(ctx_);
+  d_gen_ = dev_alloc<uint32_t>(ctx_ + 1);
+  d_key_ = dev_alloc<unsigned long long>(1);
+  reset();
+}
+
+Session::~Session() {
+  if (step_exec_) (void)hipGraphExecDestroy(step_exec_);
+  if (step_graph_) (void)hipGraphDestroy(step_graph_);
+  if (st_) (void)hipStreamSynchronize(st_);
+  for (void* p : {(void*)x_, (void*)xn_, (void*)q_, (void*)k_, (void*)v_, (void*)att_, (void*)g_, (void*)u_,
+                  (void*)act_, (void*)tmp_, (void*)xdec_, (void*)xndec_, (void*)qd_, (void*)kd_, (void*)vd_,
+                  (void*)attd_, (void*)actd_, (void*)logits_, (void*)part_, (void*)tmpd_, (void*)d_pos_,
+                  (void*)d_step_, (void*)d_flags_, (void*)d_tok_, (void*)d_ids_, (void*)d_gen_, (void*)d_key_,
+                  kv_blob_})
+    dev_free(p);
+  if (st_) (void)hipStreamDestroy(st_);
+}
+
+void Session::sync() {
+  IEK_HIP(hipGetLastError());
+  IEK_HIP(hipStreamSynchronize(st_));
+}
+
+void Session::reset() {
+  launch_set_int(d_pos_, 0, st_);
+  pos_ = 0;
+  state_rows_ = 0;
+  state_prefill_ = false;
+  sync();
+}
+
+void Session::ensure_rows(int rows) {
+  if (rows <= rows_cap_) return;
+  sync();
+  for (float** b : {&x_, &xn_, &q_, &k_, &v_, &att_, &g_, &u_, &act_, &tmp_}) {
+    dev_free(*b);
+    *b = nullptr;
+  }
+  const Config& c = m_->cfg;
+  int qmax = 0, kvmax = 0, fmax = 0;
+  for (auto& L : c.layers) {
+    qmax = std::max(qmax, L.q_dim);
+    kvmax = std::max(kvmax, L.kv_dim);
+    fmax = std::max(fmax, L.ffn_dim);
+  }
+  size_t R = (size_t)rows;
+  x_ = dev_alloc<float>(R * H_);
+  xn_ = dev_alloc<float>(R * std::max(H_, qmax));
+  q_ = dev_alloc<float>(R * qmax);
+  k_ = dev_alloc<float>(R * kvmax);
+  v_ = dev_alloc<float>(R * kvmax);
+  att_ = dev_alloc<float>(R * qmax);
+  g_ = dev_alloc<float>(R * fmax);
+  u_ = dev_alloc<float>(R * fmax);
+  act_ = dev_alloc<float>(R * fmax);
+  tmp_ = dev_alloc<float>(R * std::max(qmax, fmax));
+  rows_cap_ = rows;
+}
+
+// One projection over `rows` activation rows: matvec for a single row, GEMM otherwise.
+static void project(const DevTensor& w, const float* a, int rows, int K, int N, float* out, const float* resid,
+                    hipStream_t st) {
+  if (w.dims.size() != 2 || (int)w.dims[0] != K || (int)w.dims[1] != N)
+    fail(ST_MATMUL, "inner dim mismatch: weight dims do not match the activation width");
+  if (rows == 1) {
+    MvSegDesc s{w.dev, out, resid, N};
+    launch_matvec(w.dtype, &s, 1, a, K, resid ? 1 : 0, st);
+  } else {
+    launch_gemm(w.dtype, w.dev, a, rows, K, N, out, resid, st);
+  }
+}
+
+void Session::layer_prefill(int li, int M) {
+  const Config& c = m_->cfg;
+  const LayerSpec& S = c.layers[li];
+  const LayerTensors& L = m_->layers[li];
+  const int hd = S.head_dim, qd = S.q_dim, kvd = S.kv_dim;
+  const float eps = c.rms_eps;
+  // attention sub-layer: pre-norm, projections, RoPE at prompt positions 0..M-1, KV append at the
+  // cache's current length, causal attention within the prompt, O projection + residual.
+  launch_rmsnorm(x_, (const float*)L.attn_norm.dev, M, H_, eps, xn_, st_);
+  project(L.wq, xn_, M, H_, qd, q_, nullptr, st_);
+  project(L.wk, xn_, M, H_, kvd, k_, nullptr, st_);
+  project(L.wv, xn_, M, H_, kvd, v_, nullptr, st_);
+  if (c.unpack_qk) {
+    launch_unpack_qk(q_, tmp_, M, qd, c.n_heads, hd, st_);
+    launch_copy_f32(tmp_, q_, (size_t)M * qd, st_);
+    launch_unpack_qk(k_, tmp_, M, kvd, c.n_kv_heads, hd, st_);
+    launch_copy_f32(tmp_, k_, (size_t)M * kvd, st_);
+  }
+  const RopeTable& rt = m_->rope_tables[L.rope_table];
+  launch_rope_rows(q_, M, qd, c.n_heads, hd, 0, rt.dev, S.rotary_dim / 2, st_);
+  launch_rope_rows(k_, M, kvd, c.n_kv_heads, hd, 0, rt.dev, S.rotary_dim / 2, st_);
+  launch_kv_store(k_, v_, M, kvd, kc_[li], vc_[li], c.n_kv_heads, hd, ctx_, nullptr, pos_, st_);
+  const float scale = 1.0f / sqrtf((float)hd);
+  launch_attn_prefill(q_, k_, v_, att_, M, c.n_heads, c.n_kv_heads, hd, S.window, scale, st_);
+  project(L.wo, att_, M, qd, H_, x_, x_, st_);
+  // FFN sub-layer: pre-norm, gate/up, SwiGLU, down + residual.
+  launch_rmsnorm(x_, (const float*)L.ffn_norm.dev, M, H_, eps, xn_, st_);
+  if (M == 1 && L.gate.dtype == L.up.dtype) {
+    MvSegDesc s[2] = {{L.gate.dev, act_, nullptr, S.ffn_dim}, {L.up.dev, nullptr, nullptr, S.ffn_dim}};
+    launch_matvec(L.gate.dtype, s, 2, xn_, H_, 2, st_);
+  } else {
+    project(L.gate, xn_, M, H_, S.ffn_dim, g_, nullptr, st_);
+    project(L.up, xn_, M, H_, S.ffn_dim, u_, nullptr, st_);
+    launch_swiglu(g_, u_, act_, (size_t)M * S.ffn_dim, st_);
+  }
+  project(L.down, act_, M, S.ffn_dim, H_, x_, x_, st_);
+}
+
+void Session::layer_decode(int li) {
+  const Config& c = m_->cfg;
+  const LayerSpec& S = c.layers[li];
+  const LayerTensors& L = m_->layers[li];
+  const int hd = S.head_dim, qd = S.q_dim, kvd = S.kv_dim;
+  launch_rmsnorm(xdec_, (const float*)L.attn_norm.dev, 1, H_, c.rms_eps, xndec_, st_);
+  // Q/K/V in one launch when they share a dtype (each wave's rows stay inside one weight).
+  if (L.wq.dtype == L.wk.dtype && L.wq.dtype == L.wv.dtype) {
+    MvSegDesc s[3] = {{L.wq.dev, qd_, nullptr, qd}, {L.wk.dev, kd_, nullptr, kvd}, {L.wv.dev, vd_, nullptr, kvd}};
+    launch_matvec(L.wq.dtype, s, 3, xndec_, H_, 0, st_);
+  } else {
+    project(L.wq, xndec_, 1, H_, qd, qd_, nullptr, st_);
+    project(L.wk, xndec_, 1, H_, kvd, kd_, nullptr, st_);
+    project(L.wv, xndec_, 1, H_, kvd, vd_, nullptr, st_);
+  }
+  if (c.unpack_qk) {
+    launch_unpack_qk(qd_, tmpd_, 1, qd, c.n_heads, hd, st_);
+    launch_copy_f32(tmpd_, qd_, qd, st_);
+    launch_unpack_qk(kd_, tmpd_, 1, kvd, c.n_kv_heads, hd, st_);
+    launch_copy_f32(tmpd_, kd_, kvd, st_);
+  }
+  const RopeTable& rt = m_->rope_tables[L.rope_table];
+  launch_rope_table(qd_, c.n_heads, hd, S.rotary_dim / 2, rt.dev, d_pos_, st_);
+  launch_rope_table(kd_, c.n_kv_heads, hd, S.rotary_dim / 2, rt.dev, d_pos_, st_);
+  launch_kv_store(kd_, vd_, 1, kvd, kc_[li], vc_[li], c.n_kv_heads, hd, ctx_, d_pos_, 0, st_);
+  const float scale = 1.0f / sqrtf((float)hd);
+  launch_attn_decode(qd_, kc_[li], vc_[li], attd_, part_, c.n_heads, c.n_kv_heads, hd, ctx_, d_pos_, S.window, scale,
+                     ctx_, st_);
+  project(L.wo, attd_, 1, qd, H_, xdec_, xdec_, st_);
+  launch_rmsnorm(xdec_, (const float*)L.ffn_norm.dev, 1, H_, c.rms_eps, xndec_, st_);
+  if (L.gate.dtype == L.up.dtype) {
+    MvSegDesc s[2] = {{L.gate.dev, actd_, nullptr, S.ffn_dim}, {L.up.dev, nullptr, nullptr, S.ffn_dim}};
+    launch_matvec(L.gate.dtype, s, 2, xndec_, H_, 2, st_);
+  } else {
+    project(L.gate, xndec_, 1, H_, S.ffn_dim, tmpd_, nullptr, st_);
+    project(L.up, xndec_, 1, H_, S.ffn_dim, actd_, nullptr, st_);
+    launch_swiglu(tmpd_, actd_, actd_, S.ffn_dim, st_);
+  }
+  project(L.down, actd_, 1, S.ffn_dim, H_, xdec_, xdec_, st_);
+}
+
+static size_t embedding_hidden(const DevTensor& t, size_t* vocab) {
+  // lookup_embedding_rows (embeddings.rs:108-116): hidden = the smaller dim.
+  if (t.dims.size() != 2) fail(ST_TENSOR, "expected 2D embedding tensor");
+  size_t h = std::min(t.dims[0], t.dims[1]);
+  *vocab = std::max(t.dims[0], t.dims[1]);
+  return h;
+}
+
+void Session::prefill(const uint32_t* ids, int n) {
+  const Config& c = m_->cfg;
+  // prefill_from_tokens_loaded (embed.rs:104-138) checks, then the vocabulary range check of
+  // lookup_embedding_rows (embeddings.rs:118-125).
+  if (n <= 0) fail(ST_MODEL, "prefill: empty token list");
+  if (n > c.context_length)
+    fail(ST_MODEL, "prefill: token length " + std::to_string(n) + " exceeds context length " +
+                       std::to_string(c.context_length));
+  size_t vocab;
+  size_t hid = embedding_hidden(m_->token_embd, &vocab);
+  for (int i = 0; i < n; ++i)
+    if ((size_t)ids[i] >= vocab)
+      fail(ST_MODEL, "token ID " + std::to_string(ids[i]) + " out of vocabulary range [0, " + std::to_string(vocab) + ")");
+  if ((int)hid != H_) fail(ST_MODEL, "ForwardState: embedding dim mismatch");
+  if (pos_ + n > ctx_) fail(ST_KVCACHE, "KVCache is Full: max len is " + std::to_string(ctx_) + ".");
+  ensure_rows(n);
+  IEK_HIP(hipMemcpyAsync(d_ids_, ids, (size_t)n * 4, hipMemcpyHostToDevice, st_));
+  launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, d_ids_, n, c.embed_scale, x_, st_);
+  for (int li = 0; li < c.n_layers; ++li) layer_prefill(li, n);
+  launch_copy_f32(x_ + (size_t)(n - 1) * H_, xdec_, H_, st_);
+  pos_ += n;
+  launch_set_int(d_pos_, pos_, st_);
+  state_rows_ = n;
+  state_prefill_ = true;
+  sync();
+}
+
+void Session::decode_body() {
+  const Config& c = m_->cfg;
+  size_t vocab;
+  size_t hid = embedding_hidden(m_->token_embd, &vocab);
+  launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, d_tok_, 1, c.embed_scale, xdec_, st_);
+  for (int li = 0; li < c.n_layers; ++li) layer_decode(li);
+  launch_add_int(d_pos_, 1, st_);
+}
+
+void Session::decode_token(uint32_t id) {
+  size_t vocab;
+  embedding_hidden(m_->token_embd, &vocab);
+  if ((size_t)id >= vocab)
+    fail(ST_MODEL, "token ID " + std::to_string(id) + " out of vocabulary range [0, " + std::to_string(vocab) + ")");
+  if (pos_ >= ctx_) fail(ST_KVCACHE, "KVCache is Full: max len is " + std::to_string(ctx_) + ".");
+  IEK_HIP(hipMemcpyAsync(d_tok_, &id, 4, hipMemcpyHostToDevice, st_));
+  decode_body();
+  pos_ += 1;
+  state_rows_ = 1;
+  state_prefill_ = false;
+  sync();
+}
+
+void Session::check_state() const {
+  if (state_rows_ == 0) fail(ST_MODEL, "final_logits_last_token: empty input");
+}
+
+void Session::logits_body() {
+  const Config& c = m_->cfg;
+  launch_rmsnorm(xdec_, (const float*)m_->output_norm.dev, 1, H_, c.rms_eps, xndec_, st_);
+  project(m_->lm_head, xndec_, 1, H_, c.vocab, logits_, nullptr, st_);
+  if (c.has_softcap) launch_softcap(logits_, c.vocab, c.softcap, st_);
+}
+
+void Session::logits_last_token(float* out, int n) {
+  check_state();
+  if (n < m_->cfg.vocab) fail(ST_OP, "logits buffer smaller than vocab_size");
+  logits_body();
+  IEK_HIP(hipMemcpyAsync(out, logits_, (size_t)m_->cfg.vocab * 4, hipMemcpyDeviceToHost, st_));
+  sync();
+}
+
+void Session::argmax_body(bool record) {
+  launch_fill_u64(d_key_, 0ull, 1, st_);
+  launch_argmax(logits_, m_->cfg.vocab, d_key_, d_flags_, record ? d_step_ : nullptr, st_);
+  launch_argmax_finish(d_key_, d_tok_, d_gen_, record ? d_step_ : nullptr, st_);
+}
+
+uint32_t Session::greedy_next_token() {
+  check_state();
+  if (m_->cfg.vocab == 0) fail(ST_SAMPLING, "logits slice is empty");
+  launch_fill_i32(d_flags_, 0, 1, st_);
+  logits_body();
+  argmax_body(false);
+  uint32_t tok = 0;
+  int flag = 0;
+  IEK_HIP(hipMemcpyAsync(&tok, d_tok_, 4, hipMemcpyDeviceToHost, st_));
+  IEK_HIP(hipMemcpyAsync(&flag, d_flags_, 4, hipMemcpyDeviceToHost, st_));
+  sync();
+  if (flag) fail(ST_SAMPLING, "invalid logits for argmax (empty or non-finite)");
+  return tok;
+}
+
+void Session::generate_greedy(int n, uint32_t* out_ids, bool use_graph) {
+  if (n <= 0) return;
+  check_state();
+  if (pos_ + n > ctx_) fail(ST_KVCACHE, "KVCache is Full: max len is " + std::to_string(ctx_) + ".");
+  launch_fill_i32(d_flags_, 0, n + 1, st_);
+  launch_set_int(d_step_, 0, st_);
+  if (use_graph) {
+    if (!step_exec_) {
+      sync();
+      IEK_HIP(hipStreamBeginCapture(st_, hipStreamCaptureModeThreadLocal));
+      try {
+        logits_body();
+        argmax_body(true);
+        decode_body();
+      } catch (...) {
+        hipGraph_t g;
+        (void)hipStreamEndCapture(st_, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+      }
+      IEK_HIP(hipStreamEndCapture(st_, &step_graph_));
+      IEK_HIP(hipGraphInstantiate(&step_exec_, step_graph_, nullptr, nullptr, 0));
+    }
+    for (int i = 0; i < n; ++i) IEK_HIP(hipGraphLaunch(step_exec_, st_));
+  } else {
+    for (int i = 0; i < n; ++i) {
+      logits_body();
+      argmax_body(true);
+      decode_body();
+    }
+  }
+  std::vector<int> flags(n);
+  IEK_HIP(hipMemcpyAsync(out_ids, d_gen_, (size_t)n * 4, hipMemcpyDeviceToHost, st_));
+  IEK_HIP(hipMemcpyAsync(flags.data(), d_flags_, (size_t)n * 4, hipMemcpyDeviceToHost, st_));
+  sync();
+  pos_ += n;
+  state_rows_ = 1;
+  state_prefill_ = false;
+  for (int i = 0; i < n; ++i)
+    if (flags[i]) fail(ST_SAMPLING, "invalid logits for argmax (empty or non-finite) at step " + std::to_string(i));
+}
+
+void Session::copy_hidden(float* out, size_t cap, int* rows) {
+  *rows = state_rows_;
+  size_t n = (size_t)state_rows_ * H_;
+  if (cap < n) fail(ST_OP, "hidden buffer too small");
+  const float* src = state_prefill_ ? x_ : xdec_;
+  if (n) IEK_HIP(hipMemcpyAsync(out, src, n * 4, hipMemcpyDeviceToHost, st_));
+  sync();
+}
+
+void Session::copy_kv(int layer, bool v, float* out, size_t cap) {
+  const Config& c = m_->cfg;
+  if (layer < 0 || layer >= c.n_layers) fail(ST_MODEL, "layer index out of range");
+  const int hd = c.layers[layer].head_dim;
+  size_t n = (size_t)c.n_kv_heads * pos_ * hd;
+  if (cap < n) fail(ST_OP, "kv buffer too small");
+  std::vector<__half> host((size_t)c.n_kv_heads * ctx_ * hd);
+  IEK_HIP(hipMemcpyAsync(host.data(), v ? vc_[layer] : kc_[layer], host.size() * 2, hipMemcpyDeviceToHost, st_));
+  sync();
+  for (int h = 0; h < c.n_kv_heads; ++h)
+    for (int p = 0; p < pos_; ++p)
+      for (int d = 0; d < hd; ++d)
+        out[((size_t)h * pos_ + p) * hd + d] = __half2float(host[((size_t)h * ctx_ + p) * hd + d]);
+}
+
+}  // namespace iek

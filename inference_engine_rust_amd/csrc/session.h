@@ -1,0 +1,67 @@
+// Device-resident inference session: owns the fp16 KV cache, activation buffers, the HIP stream
+// and the captured decode-step graph. Mirrors InferenceSession (src/engine/session.rs:12-75).
+#pragma once
+#include <vector>
+
+#include "model.h"
+
+namespace iek {
+
+class Session {
+ public:
+  explicit Session(Model* m);
+  ~Session();
+
+  void reset();                                   // session.rs:40-42 (fresh KV caches)
+  void prefill(const uint32_t* ids, int n);        // session.rs:44-56 (prefill_forward)
+  void decode_token(uint32_t id);                  // session.rs:58-69 (decode_forward)
+  void logits_last_token(float* out, int n);       // session.rs:71-74 (final_logits_last_token)
+  uint32_t greedy_next_token();                    // generation.rs:10-16
+  // n x (greedy_next_token; decode_token), the loop of main.rs:100-116 / bench_metrics.rs:178-182,
+  // replayed as one captured decode-step graph. Returns the n chosen ids.
+  void generate_greedy(int n, uint32_t* out_ids, bool use_graph = true);
+
+  int kv_len() const { return pos_; }
+  int state_rows() const { return state_rows_; }
+  void copy_hidden(float* out, size_t cap, int* rows);
+  void copy_kv(int layer, bool v, float* out, size_t cap);  // [n_kv][pos][head_dim] -> f32
+  hipStream_t stream() const { return st_; }
+  Model* model() const { return m_; }
+
+ private:
+  void ensure_rows(int rows);
+  void layer_prefill(int li, int M);
+  void layer_decode(int li);
+  void decode_body();           // embed(d_tok) + every layer + pos++; no host sync
+  void logits_body();           // final norm + LM head (+ softcap) into logits_
+  void argmax_body(bool record);
+  void sync();
+  void check_state() const;
+
+  Model* m_;
+  hipStream_t st_ = nullptr;
+  int ctx_ = 0, H_ = 0;
+  void* kv_blob_ = nullptr;
+  std::vector<__half*> kc_, vc_;
+  // activations; prefill buffers hold rows_cap_ rows
+  int rows_cap_ = 0;
+  float *x_ = nullptr, *xn_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *att_ = nullptr;
+  float *g_ = nullptr, *u_ = nullptr, *act_ = nullptr, *tmp_ = nullptr;
+  float *xdec_ = nullptr, *xndec_ = nullptr, *qd_ = nullptr, *kd_ = nullptr, *vd_ = nullptr, *attd_ = nullptr;
+  float *actd_ = nullptr, *logits_ = nullptr, *part_ = nullptr, *tmpd_ = nullptr;
+  // device-side loop state
+  int* d_pos_ = nullptr;
+  int* d_step_ = nullptr;
+  int* d_flags_ = nullptr;
+  uint32_t* d_tok_ = nullptr;
+  uint32_t* d_ids_ = nullptr;  // prompt ids / generated ids
+  uint32_t* d_gen_ = nullptr;
+  unsigned long long* d_key_ = nullptr;
+  int pos_ = 0;
+  int state_rows_ = 0;  // rows of the last ForwardState (0 = none)
+  bool state_prefill_ = false;
+  hipGraphExec_t step_exec_ = nullptr;
+  hipGraph_t step_graph_ = nullptr;
+};
+
+}  // namespace iek

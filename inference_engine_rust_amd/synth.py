@@ -1,0 +1,152 @@
+"""Seeded synthetic GGUF models (ctypes over libiek_synth.so).
+
+The reference has no model writer and no model file is reachable offline; every model the
+engine, the oracle and the bench run is produced here, deterministically from a seed.
+Presets follow the configurations the benchmark is quoted on:
+
+* ``c0``  — tiny Mistral-architecture decoder (2 layers, d 512, 8/2 heads, FFN 1408).
+* ``c2``  — Mistral-7B-v0.1 architecture (32 layers, d 4096, 32/8 heads, FFN 14336).
+* ``c4``  — ``c2`` with an 8704-token context for long-context decode.
+
+Quant recipe ("Q4_K_M-style"): Q4_K for attention and FFN gate/up and the token embedding,
+Q6_K for FFN down and the output head, f32 norms. Weights are N(0, 0.02); norm weights are
+1 + N(0, 0.1) so that a kernel dropping the norm scale fails parity (a builder choice).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass, replace
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+SYNTH_LIB = os.path.join(_HERE, "libiek_synth.so")
+
+GGML_F32, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 8, 12, 14
+
+
+class _Spec(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char_p),
+        ("n_layers", ctypes.c_uint32),
+        ("hidden", ctypes.c_uint32),
+        ("n_heads", ctypes.c_uint32),
+        ("n_kv_heads", ctypes.c_uint32),
+        ("ffn", ctypes.c_uint32),
+        ("vocab", ctypes.c_uint32),
+        ("context_length", ctypes.c_uint32),
+        ("rope_theta", ctypes.c_float),
+        ("rms_eps", ctypes.c_float),
+        ("weight_std", ctypes.c_float),
+        ("norm_std", ctypes.c_float),
+        ("t_attn", ctypes.c_uint32),
+        ("t_ffn_gate_up", ctypes.c_uint32),
+        ("t_ffn_down", ctypes.c_uint32),
+        ("t_embd", ctypes.c_uint32),
+        ("t_output", ctypes.c_uint32),
+        ("tied_output", ctypes.c_uint32),
+    ]
+
+
+@dataclass(frozen=True)
+class LlamaSpec:
+    name: str
+    n_layers: int
+    hidden: int
+    n_heads: int
+    n_kv_heads: int
+    ffn: int
+    vocab: int
+    context_length: int
+    rope_theta: float = 10000.0
+    rms_eps: float = 1e-5
+    weight_std: float = 0.02
+    norm_std: float = 0.1
+    t_attn: int = GGML_Q4_K
+    t_ffn_gate_up: int = GGML_Q4_K
+    t_ffn_down: int = GGML_Q6_K
+    t_embd: int = GGML_Q4_K
+    t_output: int = GGML_Q6_K
+    tied_output: bool = False
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden // self.n_heads
+
+
+PRESETS = {
+    "c0": LlamaSpec("synthetic-mistral-tiny", 2, 512, 8, 2, 1408, 32000, 64),
+    "c2": LlamaSpec("synthetic-mistral-7b-v0.1", 32, 4096, 32, 8, 14336, 32000, 1024),
+    "c4": LlamaSpec("synthetic-mistral-7b-v0.1-long", 32, 4096, 32, 8, 14336, 32000, 8704),
+    # mid-size parity model: Mistral-7B widths, 2 layers, short context
+    "c2_l2": LlamaSpec("synthetic-mistral-7b-2layer", 2, 4096, 32, 8, 14336, 32000, 640),
+}
+
+
+def preset(name: str, **overrides) -> LlamaSpec:
+    return replace(PRESETS[name], **overrides)
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(SYNTH_LIB):
+            raise RuntimeError(f"{SYNTH_LIB} is missing: run __graft_entry__.build() first")
+        L = ctypes.CDLL(SYNTH_LIB)
+        L.iek_synth_write_llama.argtypes = [ctypes.c_char_p, ctypes.POINTER(_Spec), ctypes.c_uint64, ctypes.c_int]
+        L.iek_synth_write_llama.restype = ctypes.c_int
+        L.iek_synth_quantize.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        L.iek_synth_quantize.restype = ctypes.c_int
+        L.iek_synth_normal.argtypes = [ctypes.c_uint64, ctypes.c_char_p, ctypes.c_size_t, ctypes.c_size_t,
+                                       ctypes.c_float, ctypes.c_float, ctypes.c_void_p]
+        L.iek_synth_normal.restype = None
+        L.iek_synth_f32_to_f16.argtypes = [ctypes.c_float]
+        L.iek_synth_f32_to_f16.restype = ctypes.c_uint16
+        _lib = L
+    return _lib
+
+
+def write_llama(path: str, spec: LlamaSpec, seed: int = 0, threads: int | None = None) -> str:
+    """Write a Mistral/Llama-family GGUF for ``spec`` to ``path`` and return the path."""
+    s = _Spec(spec.name.encode(), spec.n_layers, spec.hidden, spec.n_heads, spec.n_kv_heads, spec.ffn,
+              spec.vocab, spec.context_length, spec.rope_theta, spec.rms_eps, spec.weight_std,
+              spec.norm_std, spec.t_attn, spec.t_ffn_gate_up, spec.t_ffn_down, spec.t_embd,
+              spec.t_output, 1 if spec.tied_output else 0)
+    if threads is None:
+        threads = min(16, os.cpu_count() or 1)
+    rc = lib().iek_synth_write_llama(path.encode(), ctypes.byref(s), seed, threads)
+    if rc != 0:
+        raise OSError(f"iek_synth_write_llama({path}) failed with code {rc}")
+    return path
+
+
+def normal(seed: int, name: str, n: int, mean: float = 0.0, std: float = 1.0, start: int = 0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib().iek_synth_normal(seed, name.encode(), start, n, mean, std, out.ctypes.data)
+    return out
+
+
+BLOCK = {GGML_Q4_K: (256, 144), GGML_Q6_K: (256, 210), GGML_Q8_0: (32, 34)}
+
+
+def quantize(ggml_type: int, x: np.ndarray) -> np.ndarray:
+    """Quantise a float array whose length is a multiple of the block size; returns raw bytes."""
+    be, bb = BLOCK[ggml_type]
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    if x.size % be:
+        raise ValueError(f"length {x.size} is not a multiple of {be}")
+    nb = x.size // be
+    out = np.empty(nb * bb, dtype=np.uint8)
+    if lib().iek_synth_quantize(ggml_type, x.ctypes.data, nb, out.ctypes.data) != 0:
+        raise ValueError(f"unsupported type {ggml_type}")
+    return out
+
+
+def prompt_ids(seed: int, n: int, vocab: int = 32000) -> np.ndarray:
+    """Uniform token ids in [3, vocab) from seed+1 (the benchmark's prompt recipe)."""
+    rng = np.random.default_rng(seed + 1)
+    return rng.integers(3, vocab, size=n, dtype=np.int64).astype(np.uint32)

@@ -1,0 +1,160 @@
+// TEST INFRASTRUCTURE ONLY — the CPU oracle.
+//
+// A C++ restatement of the reference's CPU token loop (AntoineKhoury/inference_engine_rust,
+// a Rust crate that cannot be built in this environment: no rustc/cargo, crates not vendored).
+// Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load liboracle.so,
+// and only as the checker / the timed CPU baseline. The product (libiek.so) never links it.
+//
+// Arithmetic rules followed everywhere: f32 ops in the reference's order, no FMA contraction
+// (-ffp-contract=off), f64 block dequant as the reference writes it, glibc libm for
+// expf/cosf/sinf/powf/tanhf/sqrtf (Rust std calls the platform libm on Linux).
+#pragma once
+#include <cstddef>
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace orc {
+
+// Error codes mirror the EngineError variants (src/error.rs:5-38).
+enum Err : int {
+  OK = 0, E_IO = 1, E_UTF8 = 2, E_GGUF = 3, E_TENSOR = 4, E_MATMUL = 5, E_MODEL = 6,
+  E_TOKENIZER = 7, E_KVCACHE = 8, E_SAMPLING = 9, E_OP = 10,
+};
+
+struct Error {
+  int code;
+  std::string msg;
+};
+
+// ---- GGUF values (src/model_loader/gguf_types.rs:4-36) ----
+enum GType : int {
+  G_U8 = 0, G_I8 = 1, G_U16 = 2, G_I16 = 3, G_U32 = 4, G_I32 = 5, G_F32 = 6, G_BOOL = 7,
+  G_STR = 8, G_ARR = 9, G_U64 = 10, G_I64 = 11, G_F64 = 12,
+};
+
+struct GVal {
+  int type = G_U8;
+  uint64_t u = 0;
+  int64_t i = 0;
+  double f = 0;
+  float f32 = 0;
+  bool b = false;
+  std::string s;
+  std::vector<GVal> arr;
+};
+
+// TensorType (src/core/tensor.rs:13-23)
+enum TType : int { T_F32 = 0, T_Q4K = 1, T_Q6K = 2, T_Q8_0 = 3 };
+
+struct Tensor {
+  int dtype = T_F32;
+  std::vector<uint8_t> buf;
+  std::vector<size_t> dims;
+  const float* f32() const { return reinterpret_cast<const float*>(buf.data()); }
+  size_t f32_len() const { return buf.size() / 4; }
+};
+
+struct TensorInfo {
+  std::string name;
+  std::vector<size_t> dims;
+  uint32_t type_id = 0;
+  uint64_t offset = 0;
+};
+
+struct GGUF {
+  uint32_t version = 0;
+  std::map<std::string, GVal> kv;
+  std::vector<TensorInfo> infos;
+  uint64_t data_offset = 0;
+  std::map<std::string, Tensor> tensors;
+  const GVal* meta(const std::string& k) const {
+    auto it = kv.find(k);
+    return it == kv.end() ? nullptr : &it->second;
+  }
+  const Tensor* get(const std::string& n) const {
+    auto it = tensors.find(n);
+    return it == tensors.end() ? nullptr : &it->second;
+  }
+};
+
+enum Family : int { MISTRAL_LLAMA = 0, GEMMA4 = 1 };
+
+struct LayerAttentionSpec {
+  long sliding_window = -1;  // -1 = None (full causal)
+  float rope_theta = 10000.f;
+  size_t rope_rotary_dim = 0;
+};
+
+struct LayerDims {
+  size_t q_dim, kv_dim, head_dim, ffn_dim;
+};
+
+struct ModelConfig {
+  int family = MISTRAL_LLAMA;
+  size_t context_length = 0, hidden_dim = 0, n_layers = 0, n_heads = 0, n_kv_heads = 0;
+  size_t head_dim = 0, ffn_dim = 0;
+  std::vector<LayerDims> layer_dims;
+  float rope_theta = 10000.f, rms_norm_eps = 0.f;
+  size_t vocab_size = 0;
+  bool unpack_llama_gguf_qk = false;
+  std::vector<LayerAttentionSpec> layer_attention;
+  float token_embedding_scale = 1.f;
+  size_t embedding_length_per_layer = 0;
+  float ple_combine_scale = 0.f, ple_model_proj_scale = 0.f;
+  std::vector<long> kv_borrow_from;  // -1 = None
+  bool has_softcap = false;
+  float softcap = 0.f;
+};
+
+struct LayerW {
+  const Tensor *attn_norm = nullptr, *ffn_norm = nullptr, *attn_post_norm = nullptr,
+               *ffn_post_norm = nullptr, *attn_q_norm = nullptr, *attn_k_norm = nullptr;
+  const Tensor *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr;
+  const Tensor *w_gate = nullptr, *w_up = nullptr, *w_down = nullptr;
+  const Tensor *ple_inp_gate = nullptr, *ple_proj = nullptr, *ple_post_norm = nullptr;
+  const Tensor *rope_freqs = nullptr, *layer_output_scale = nullptr;
+};
+
+struct ModelW {
+  const Tensor *token_embd = nullptr, *output_norm = nullptr, *lm_head = nullptr;
+  std::vector<LayerW> layers;
+  const Tensor *ple_token_embd = nullptr, *ple_model_proj = nullptr, *ple_proj_norm = nullptr;
+};
+
+struct Model {
+  GGUF gguf;
+  ModelConfig cfg;
+  ModelW w;
+  std::string emb_name;
+};
+
+struct KVCache {
+  std::vector<float> k, v;
+  size_t current_pos = 0, max_seq_len = 0, n_kv_heads = 0, head_dim = 0;
+};
+
+struct State {
+  size_t seq_len = 0, hidden_dim = 0;
+  std::vector<float> hidden;
+  std::vector<float> ple_packed;
+  size_t ple_n_layers = 0, ple_dim = 0;
+};
+
+// Execution mode. PARITY: vectorised/threaded but bit-identical per output element.
+// BASELINE: the reference's own Rayon decomposition (rows of a matmul when M*N*K >= 65536,
+// heads in attention), for timing.
+enum Mode : int { PARITY = 0, BASELINE = 1 };
+
+struct Session {
+  const Model* model = nullptr;
+  std::vector<KVCache> kv;
+  State state;
+  int mode = PARITY;
+  int threads = 1;
+  size_t layer_limit = 0;  // 0 = all layers; >0 runs only the first N blocks (CPU-baseline sampling)
+};
+
+}  // namespace orc

@@ -1,0 +1,279 @@
+"""Pins the CPU oracle (oracle/oracle.cpp) before it is trusted as the parity reference.
+
+Each check is either a known answer the reference's own unit tests hold (cited file:line), a
+closed form fixed by the mathematics, an exhaustive sweep, or a round trip against the
+independently written quantiser — chosen so that a dropped term, a swapped nibble/sub-block or a
+wrong index fails.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+from inference_engine_rust_amd import synth
+
+
+# ---- reference known answers -----------------------------------------------------------------
+
+def test_rope_dim2_known_answer():  # src/ops/rope.rs:63-68
+    v = O.rope([1.0, 2.0], 1.0, 1, 2, 2)
+    assert abs(v[0] + 1.1426396) < 1e-5 and abs(v[1] - 1.9220756) < 1e-5
+
+
+def test_rope_pairs_non_overlapping():  # rope.rs:70-77
+    v = O.rope([1.0, 0.0, 1.0, 0.0], 10000.0, 0, 4, 4)
+    np.testing.assert_allclose(v, [1.0, 0.0, 1.0, 0.0], atol=1e-5)
+
+
+def test_rope_freq_factor_changes_angle():  # rope.rs:79-88
+    a = O.rope([1.0, 0.0], 10000.0, 1, 2, 2)
+    b = O.rope([1.0, 0.0], 10000.0, 1, 2, 2, ff=[2.0])
+    assert abs(a[0] - b[0]) > 1e-3
+
+
+def test_rope_running_product_closed_form():
+    # pair k at position p rotates by p * base^(-2k/d); the f32 running product agrees to ~1e-4 rad
+    d, base, pos = 128, 10000.0, 4095
+    x = np.tile([1.0, 0.0], d // 2).astype(np.float32)
+    y = O.rope(x, base, pos, d, d)
+    ang = np.arctan2(y[1::2], y[0::2]).astype(np.float64)
+    want = np.array([pos * base ** (-2.0 * k / d) for k in range(d // 2)])
+    diff = np.angle(np.exp(1j * (ang - want)))
+    assert np.max(np.abs(diff)) < 2e-3
+
+
+def test_rope_errors():  # rope.rs:19-38
+    with pytest.raises(O.OracleError):
+        O.rope([1.0, 2.0], 1.0, 0, 2, 4)
+    with pytest.raises(O.OracleError):
+        O.rope([1.0, 2.0, 3.0], 1.0, 0, 3, 3)
+
+
+def test_softmax_known_answer():  # src/ops/softmax.rs:35-49
+    out = O.softmax([0.0, 1.0])
+    assert abs(out.sum() - 1) < 1e-5
+    assert abs(out[0] - 0.2689414) < 1e-5 and abs(out[1] - 0.7310586) < 1e-5
+
+
+def test_softmax_masked_and_empty():
+    out = O.softmax([-np.inf, 0.0, 0.0])
+    assert out[0] == 0.0 and abs(out[1] - 0.5) < 1e-7
+    with pytest.raises(O.OracleError):
+        O.softmax(np.zeros(0, np.float32))
+
+
+def test_swiglu_known_answer():  # src/ops/swiglu.rs:39-50
+    out = O.swiglu([0.0, 1.0], [1.0, 1.0])
+    assert abs(out[0]) < 1e-5 and abs(out[1] - 0.7310586) < 1e-3
+
+
+def test_swiglu_closed_form():
+    g = np.linspace(-30, 30, 1001).astype(np.float32)
+    u = np.linspace(2, -2, 1001).astype(np.float32)
+    want = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * u
+    np.testing.assert_allclose(O.swiglu(g, u), want, rtol=2e-6, atol=1e-30)
+
+
+def test_gelu_known_answers():  # src/ops/gelu.rs:25-40
+    for x, e in [(-1.0, -0.15880801), (0.0, 0.0), (1.0, 0.841192), (2.0, 1.9545977)]:
+        assert abs(O.gelu_tanh(x) - e) < 1e-6
+
+
+def test_rmsnorm_known_answer():  # src/ops/rmsnorm.rs:65-79
+    out = O.rmsnorm([0.5, 1.0, 1.5], [0.2, 0.3, 0.4], 1e-6)
+    np.testing.assert_allclose(out, [0.092582, 0.277746, 0.555492], atol=1e-3)
+
+
+def test_rmsnorm_no_scale_known_answer():  # rmsnorm.rs:56-63
+    out = O.rmsnorm_no_scale([3.0, 4.0], 1e-6)
+    rms = math.sqrt((9 + 16) / 2 + 1e-6)
+    assert abs(out[0] - 3 / rms) < 1e-5 and abs(out[1] - 4 / rms) < 1e-5
+
+
+def test_argmax_known_answers():  # src/engine/sampling.rs:87-97
+    assert O.argmax([0.0, 2.0, 1.0]) == 1
+    assert O.argmax(np.zeros(0, np.float32)) == -1
+    assert O.argmax([1.0, 3.0, 3.0, 2.0]) == 1  # first index wins ties
+    assert O.argmax([1.0, np.nan, 0.0]) == -2
+    assert O.argmax([1.0, np.inf, 0.0]) == -2
+
+
+def test_unpack_qk_known_answer():  # src/layers/attention.rs:678-687
+    out = O.unpack_qk_row([0, 2, 1, 3, 4, 6, 5, 7], 2, 4)
+    np.testing.assert_array_equal(out, np.arange(8, dtype=np.float32))
+
+
+def test_matmul_f32_known_answer():  # src/ops/matmul.rs:453-463
+    w = np.array([1, 2, 3, 4], np.float32)
+    out = O.matmul(O.T_F32, np.array([1, 2], np.float32), w, 2, 2)
+    np.testing.assert_allclose(out[0], [5.0, 11.0], atol=1e-5)
+
+
+@pytest.mark.parametrize("t,nbytes,k,n", [(O.T_Q4K, 144, 2, 2), (O.T_Q6K, 210, 1, 1), (O.T_Q8_0, 34, 1, 1)])
+def test_matmul_zero_block(t, nbytes, k, n):  # matmul.rs:465-497
+    a = np.arange(1, k + 1, dtype=np.float32)
+    out = O.matmul(t, a, np.zeros(nbytes, np.uint8), k, n)
+    assert np.all(np.abs(out) < 1e-5)
+
+
+def test_matmul_short_weight_buffer_errors():  # matmul.rs:166-173
+    with pytest.raises(O.OracleError) as e:
+        O.matmul(O.T_Q4K, np.ones(256, np.float32), np.zeros(143, np.uint8), 256, 1)
+    assert e.value.code == 5
+
+
+# ---- quant primitives: exhaustive / closed forms ---------------------------------------------
+
+def test_f16_to_f32_exhaustive():
+    bits = np.arange(65536, dtype=np.uint32)
+    got = np.array([O.f16_to_f32(int(b)) for b in bits[::1]], np.float32)
+    want = bits.astype(np.uint16).view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def _pack_scales(sc, m):
+    """ggml get_scale_min_k4 packing written from the encoder side."""
+    s = np.zeros(12, np.uint8)
+    for j in range(4):
+        s[j] = (sc[j] & 63) | ((sc[j + 4] >> 4) << 6)
+        s[j + 4] = (m[j] & 63) | ((m[j + 4] >> 4) << 6)
+        s[j + 8] = (sc[j + 4] & 15) | ((m[j + 4] & 15) << 4)
+    return s
+
+
+def test_extract_scale_min_k4_roundtrip_every_value():
+    rng = np.random.default_rng(0)
+    for j in range(8):
+        for v in range(64):
+            sc = rng.integers(0, 64, 8)
+            m = rng.integers(0, 64, 8)
+            sc[j] = v
+            m[j] = 63 - v
+            s = _pack_scales(sc, m)
+            for jj in range(8):
+                assert O.extract_scale_min_k4(jj, s) == (int(sc[jj]), int(m[jj]))
+
+
+def _q4k_block(d_bits, dmin_bits, sc, m, q):
+    b = np.zeros(144, np.uint8)
+    b[0:2] = np.array([d_bits], np.uint16).view(np.uint8)
+    b[2:4] = np.array([dmin_bits], np.uint16).view(np.uint8)
+    b[4:16] = _pack_scales(sc, m)
+    for g in range(4):
+        for l in range(32):
+            b[16 + 32 * g + l] = q[64 * g + l] | (q[64 * g + 32 + l] << 4)
+    return b
+
+
+def test_q4k_positional_known_answer():
+    # d = 1, dmin = 0.5: y[e] = sc[j]*q[e] - 0.5*m[j], j = e // 32 — every position distinct.
+    sc = np.arange(1, 9)
+    m = np.arange(8, 0, -1)
+    q = np.arange(256) % 16
+    blk = _q4k_block(0x3C00, 0x3800, sc, m, q)
+    got = O.dequantize(O.T_Q4K, blk, 1)
+    e = np.arange(256)
+    want = sc[e // 32] * q - 0.5 * m[e // 32]
+    want[q == 0] = -0.5 * m[e // 32][q == 0]
+    np.testing.assert_array_equal(got, want.astype(np.float32))
+
+
+def test_q4k_single_rounding_matches_f64():
+    rng = np.random.default_rng(1)
+    for _ in range(200):
+        d, dmin = rng.integers(0, 0x7C00, 2)
+        sc = rng.integers(0, 64, 8)
+        m = rng.integers(0, 64, 8)
+        q = rng.integers(0, 16, 256)
+        blk = _q4k_block(int(d), int(dmin), sc, m, q)
+        got = O.dequantize(O.T_Q4K, blk, 1)
+        dd = float(np.uint16(d).view(np.float16))
+        dm = float(np.uint16(dmin).view(np.float16))
+        e = np.arange(256)
+        want = (np.where(q == 0, 0.0, dd * sc[e // 32] * q) - dm * m[e // 32]).astype(np.float32)
+        np.testing.assert_array_equal(got, want)
+
+
+def test_q6k_positional_known_answer():
+    # d = 1; scale s[i] = i - 8 (int8, negative included); q + 32 = e % 64.
+    b = np.zeros(210, np.uint8)
+    qb = np.arange(256) % 64
+    for h in range(2):
+        for l in range(32):
+            q1, q2, q3, q4 = (qb[128 * h + l], qb[128 * h + 32 + l], qb[128 * h + 64 + l], qb[128 * h + 96 + l])
+            b[64 * h + l] = (q1 & 15) | ((q3 & 15) << 4)
+            b[64 * h + 32 + l] = (q2 & 15) | ((q4 & 15) << 4)
+            b[128 + 32 * h + l] = (q1 >> 4) | ((q2 >> 4) << 2) | ((q3 >> 4) << 4) | ((q4 >> 4) << 6)
+    s = (np.arange(16) - 8).astype(np.int8)
+    b[192:208] = s.view(np.uint8)
+    b[208:210] = np.array([0x3C00], np.uint16).view(np.uint8)
+    got = O.dequantize(O.T_Q6K, b, 1)
+    e = np.arange(256)
+    want = (s[e // 16].astype(np.float64) * (qb - 32)).astype(np.float32)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_q8_0_known_answer():
+    b = np.zeros(34, np.uint8)
+    b[0:2] = np.array([0x3800], np.uint16).view(np.uint8)  # d = 0.5
+    q = (np.arange(32) - 16).astype(np.int8)
+    b[2:] = q.view(np.uint8)
+    np.testing.assert_array_equal(O.dequantize(O.T_Q8_0, b, 1), (q * 0.5).astype(np.float32))
+
+
+@pytest.mark.parametrize("ggml,orc,be", [(12, O.T_Q4K, 256), (14, O.T_Q6K, 256), (8, O.T_Q8_0, 32)])
+def test_quantize_dequantize_roundtrip(ggml, orc, be):
+    x = synth.normal(3, "rt", be * 64, 0.0, 0.02)
+    blocks = synth.quantize(ggml, x)
+    y = O.dequantize(orc, blocks, 64)
+    err = np.abs(y - x).reshape(64, -1).max(axis=1)
+    scale = np.abs(x).reshape(64, -1).max(axis=1)
+    # Q4_K: 4-bit affine (<= ~1/15 of the range plus 6-bit scale error); Q6_K/Q8_0 finer.
+    bound = {12: 0.15, 14: 0.05, 8: 0.01}[ggml]
+    assert np.all(err <= bound * scale + 1e-7)
+
+
+# ---- matmul ------------------------------------------------------------------------------------
+
+def _dense(orc, blocks, k, n, be):
+    nb = (k * n + be - 1) // be
+    return O.dequantize(orc, blocks, nb)[: k * n].astype(np.float64)
+
+
+@pytest.mark.parametrize("ggml,orc,be,k,n,m", [
+    (12, O.T_Q4K, 256, 512, 96, 1), (12, O.T_Q4K, 256, 512, 96, 7),
+    (14, O.T_Q6K, 256, 1408, 40, 1), (14, O.T_Q6K, 256, 1408, 40, 9),  # K % 256 != 0: blocks straddle rows
+    (8, O.T_Q8_0, 32, 160, 33, 5)])
+def test_matmul_vs_f64_and_modes(ggml, orc, be, k, n, m):
+    nb = (k * n + be - 1) // be
+    wf = synth.normal(5, f"w{k}", nb * be, 0.0, 0.02)
+    blocks = synth.quantize(ggml, wf)
+    a = synth.normal(6, f"a{k}", m * k, 0.0, 1.0).reshape(m, k)
+    a[0, ::7] = 0.0
+    w = _dense(orc, blocks, k, n, be)
+    want = a.astype(np.float64) @ w.reshape(n, k).T
+    got = O.matmul(orc, a, blocks, k, n)
+    bound = 2 * k * np.finfo(np.float32).eps * (np.abs(a) @ np.abs(w.reshape(n, k)).T) + 1e-30
+    assert np.all(np.abs(got - want) <= bound)
+    base = O.matmul(orc, a, blocks, k, n, mode=O.BASELINE, threads=4)
+    assert np.array_equal(got.view(np.uint32), base.view(np.uint32))
+
+
+def test_matmul_sequential_order_bitwise():
+    # The oracle's blocked GEMM equals the plain sequential f32 loop bit for bit.
+    k, n, m = 256, 37, 6
+    wf = synth.normal(9, "seq", k * n, 0.0, 0.5)
+    a = synth.normal(10, "seqa", m * k, 0.0, 1.0).reshape(m, k)
+    got = O.matmul(O.T_F32, a, wf, k, n)
+    want = np.zeros((m, n), np.float32)
+    W = wf.reshape(n, k)
+    for i in range(m):
+        for j in range(n):
+            acc = np.float32(0)
+            for kk in range(k):
+                acc = np.float32(acc + np.float32(a[i, kk] * W[j, kk]))
+            want[i, j] = acc
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

@@ -1,0 +1,94 @@
+"""Model-level invariants of the CPU oracle on the seeded tiny Mistral-architecture model.
+
+* prefill [t0..tN] vs prefill [t0..tN-1] + decode tN         (tests/prefill_smoke.rs:99-144)
+* greedy decode loop == teacher-forced re-prefill argmax     (tests/gemma_decode_self_consistency.rs:219-320)
+* parity mode == baseline (reference Rayon decomposition) bit for bit
+* config resolution of the synthetic GGUF (model_config.rs:143-306)
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+from inference_engine_rust_amd import synth
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.fixture(scope="module")
+def c0(c0_path):
+    return O.Model(c0_path)
+
+
+def test_config_resolution(c0):
+    c = c0.cfg
+    assert (c.hidden_dim, c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim, c.ffn_dim, c.vocab_size) == (
+        512, 2, 8, 2, 64, 1408, 32000)
+    assert c.rope_theta == 10000.0 and abs(c.rms_norm_eps - 1e-5) < 1e-12
+    assert c.unpack_qk == 0  # general.name contains "mistral" (model_config.rs:209-224)
+    spec = c0.layer_spec(0)
+    assert spec["sliding_window"] == -1 and spec["rotary_dim"] == 64 and spec["kv_borrow"] == -1
+
+
+def test_prefill_vs_prefill_plus_decode(c0):
+    ids = synth.prompt_ids(0, 9)
+    a = O.Session(c0)
+    a.prefill(ids)
+    la = a.logits()
+    b = O.Session(c0)
+    b.prefill(ids[:-1])
+    b.decode(int(ids[-1]))
+    lb = b.logits()
+    assert np.max(np.abs(la - lb)) < 1e-3
+
+
+def test_decode_loop_matches_teacher_forcing(c0):
+    ids = list(synth.prompt_ids(0, 6))
+    s = O.Session(c0)
+    toks, _ = O.greedy_generate(s, ids, 5)
+    seq = list(ids)
+    for t in toks:
+        r = O.Session(c0)
+        r.prefill(seq)
+        assert O.argmax(r.logits()) == t
+        seq.append(t)
+
+
+def test_parity_mode_equals_baseline_mode(c0):
+    ids = synth.prompt_ids(0, 16)
+    p = O.Session(c0, O.PARITY)
+    b = O.Session(c0, O.BASELINE, 3)
+    tp, lp = O.greedy_generate(p, ids, 4, record_logits=True)
+    tb, lb = O.greedy_generate(b, ids, 4, record_logits=True)
+    assert tp == tb
+    for x, y in zip(lp, lb):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+
+
+def test_c0_golden_tokens(c0):
+    """Greedy tokens of the benchmark's tiny config, frozen when the oracle was pinned."""
+    with open(os.path.join(GOLDEN, "c0_seed0.json")) as f:
+        g = json.load(f)
+    s = O.Session(c0)
+    toks, logs = O.greedy_generate(s, np.array(g["prompt"], np.uint32), g["n_decode"], record_logits=True)
+    assert toks == g["tokens"]
+    np.testing.assert_allclose([float(l[t]) for l, t in zip(logs, toks)], g["top_logits"], rtol=1e-6)
+
+
+def test_errors(c0):
+    s = O.Session(c0)
+    with pytest.raises(O.OracleError) as e:
+        s.prefill(np.zeros(0, np.uint32))
+    assert e.value.code == 6
+    with pytest.raises(O.OracleError) as e:
+        s.prefill(np.array([32000], np.uint32))
+    assert e.value.code == 6
+    with pytest.raises(O.OracleError) as e:
+        s.prefill(np.arange(65, dtype=np.uint32))  # > context_length (64)
+    assert e.value.code == 6
+    s.prefill(np.arange(3, 67, dtype=np.uint32))  # exactly full
+    with pytest.raises(O.OracleError) as e:
+        s.decode(5)
+    assert e.value.code == 8  # KVCacheFull (attention.rs:55-59)
