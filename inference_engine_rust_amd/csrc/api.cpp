@@ -280,16 +280,17 @@ iek_status iek_argmax(const float* logits, size_t n, uint32_t* out_index, void* 
     unsigned long long* key = nullptr;
     IEK_HIP(hipMalloc(&key, 64));
     int* flag = reinterpret_cast<int*>(key + 1);
-    uint32_t* tok = reinterpret_cast<uint32_t*>(key + 2);
+    int* flags = reinterpret_cast<int*>(key + 2);
+    uint32_t* tok = reinterpret_cast<uint32_t*>(key + 3);
     uint32_t host[2] = {0, 0};
     int hflag = 0;
     try {
-      launch_fill_u64(key, 0ull, 3, st);
+      launch_fill_u64(key, 0ull, 4, st);
       launch_argmax(logits, (int)n, key, flag, nullptr, st);
-      launch_argmax_finish(key, tok, nullptr, nullptr, st);
+      launch_argmax_finish(key, flag, tok, nullptr, flags, nullptr, st);
       after_launch();
       IEK_HIP(hipMemcpyAsync(host, tok, 4, hipMemcpyDeviceToHost, st));
-      IEK_HIP(hipMemcpyAsync(&hflag, flag, 4, hipMemcpyDeviceToHost, st));
+      IEK_HIP(hipMemcpyAsync(&hflag, flags, 4, hipMemcpyDeviceToHost, st));
       IEK_HIP(hipStreamSynchronize(st));
     } catch (...) {
       (void)hipFree(key);

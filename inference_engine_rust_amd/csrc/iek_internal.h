@@ -55,16 +55,19 @@ void launch_residual_add(const float* a, const float* b, float* out, size_t n, h
 void launch_softmax(const float* in, float* out, int n, hipStream_t st);
 // Greedy argmax: atomicMax of packed (value, first-index) keys; non-finite logits set flags[*step].
 void launch_argmax(const float* logits, int n, unsigned long long* key_out, int* flags, const int* step, hipStream_t st);
-// tok[0] = argmax index; with a step counter also list[*step] = index and ++*step.
-void launch_argmax_finish(const unsigned long long* key, uint32_t* tok, uint32_t* list, int* step, hipStream_t st);
+// tok[0] = argmax index, flags[step] = *flag; with a step counter also list[*step] = index and
+// ++*step; then *key = 0 and *flag = 0.
+void launch_argmax_finish(unsigned long long* key, int* flag, uint32_t* tok, uint32_t* list, int* flags, int* step,
+                          hipStream_t st);
 void launch_softcap(float* z, int n, float cap, hipStream_t st);
 void launch_unpack_qk(const float* src, float* dst, int rows, int row_stride, int n_groups, int head_dim,
                       hipStream_t st);
 void launch_copy_f32(const float* src, float* dst, size_t n, hipStream_t st);
 void launch_fill_i32(int* p, int v, int n, hipStream_t st);
-void launch_attn_decode(const float* q, const __half* kc, const __half* vc, float* out, float* part, int n_heads,
-                        int n_kv, int head_dim, int ctx, const int* pos_dev, int window, float scale, int max_len,
-                        hipStream_t st);
+// `counters` holds n_kv zero-initialised ints; the kernel leaves them zero again.
+void launch_attn_decode(const float* q, const __half* kc, const __half* vc, float* out, float* part, int* counters,
+                        int n_heads, int n_kv, int head_dim, int ctx, const int* pos_dev, int window, float scale,
+                        int max_len, hipStream_t st);
 void launch_attn_prefill(const float* q, const float* k, const float* v, float* out, int M, int n_heads, int n_kv,
                          int head_dim, int window, float scale, hipStream_t st);
 void launch_fill_u64(unsigned long long* p, unsigned long long v, int n, hipStream_t st);

@@ -1,14 +1,13 @@
 // Attention over an fp16 KV cache laid out per layer as [n_kv][ctx][head_dim].
 //
-// Decode (src/layers/attention.rs:462-655): split-K flash-decode. One wave owns one KV head and
-// one 64-key slice; each lane scores one key for all G = n_heads/n_kv query heads of the GQA
-// group (K streamed once per group), then lanes switch to head dimensions to accumulate
-// p*V. Slices write (max, sum, o[]) partials; a combine pass merges them with the usual
-// rescaling. The number of slices is fixed by the cache capacity so the launch shape never
-// changes between captured decode steps; the live length is read from device memory.
+// Decode (src/layers/attention.rs:462-655): split-K flash-decode over 64-key slices, GQA groups
+// sharing one K/V stream; the slice count is fixed by the cache capacity so the launch shape
+// never changes between captured decode steps, and the live length is read from device memory.
 //
 // Prefill (attention.rs:175-422): causal attention over the f32 K/V of the prompt (the
 // reference attends to the layer's own k_data/v_data, not the cache).
+#include <type_traits>
+
 #include "common.cuh"
 #include "../iek_internal.h"
 
@@ -16,13 +15,18 @@ namespace iek {
 
 constexpr int SPLIT = 64;
 
+// One wave per (KV head, 64-key slice). Lane j scores key j0+j against the G query heads of the
+// group; the V rows of the slice are fetched in the same burst (lanes over head dims) so each
+// wave makes a single trip to HBM. Slices publish (max, sum, o[]) partials; the last wave of a
+// KV head (device-scope counter, reset by that wave) merges them into the attention output.
 template <int HD>
-__global__ __launch_bounds__(64) void attn_decode_partial_kernel(const float* __restrict__ q,
-                                                                 const __half* __restrict__ kc,
-                                                                 const __half* __restrict__ vc, float* __restrict__ part,
-                                                                 int n_heads, int n_kv, int ctx, const int* pos_dev,
-                                                                 int window, float scale, int nsplit) {
+__global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict__ q, const __half* __restrict__ kc,
+                                                         const __half* __restrict__ vc, float* __restrict__ part,
+                                                         float* __restrict__ out, int* __restrict__ counters,
+                                                         int n_heads, int n_kv, int ctx, const int* pos_dev,
+                                                         int window, float scale, int nsplit) {
   constexpr int DPL = HD / 64;  // head dims per lane in the PV phase
+  constexpr int KV4 = HD / 8;   // uint4 (8 halves) per key row
   const int kvh = blockIdx.x, sp = blockIdx.y, lane = threadIdx.x;
   const int G = n_heads / n_kv;
   const int total = *pos_dev + 1;
@@ -30,135 +34,155 @@ __global__ __launch_bounds__(64) void attn_decode_partial_kernel(const float* __
   const int j0 = max(sp * SPLIT, jmin), j1 = min(total, (sp + 1) * SPLIT);
   __shared__ float qs[8][HD];
   __shared__ float ps[8][SPLIT];
-  for (int i = lane; i < G * HD; i += 64) qs[i / HD][i % HD] = q[(size_t)(kvh * G + i / HD) * HD + i % HD];
-  __syncthreads();
-  float* prow = part + ((size_t)(kvh * G) * nsplit + sp) * (HD + 2);
-  if (j0 >= j1) {
-    for (int g = 0; g < G; ++g) {
-      float* pr = prow + (size_t)g * nsplit * (HD + 2);
-      if (lane == 0) {
-        pr[0] = -INFINITY;
-        pr[1] = 0.f;
-      }
-      for (int d = lane; d < HD; d += 64) pr[2 + d] = 0.f;
+  __shared__ int last;
+  const int nk = j1 - j0;
+  if (nk > 0) {
+    const int j = j0 + lane;
+    const bool valid = lane < nk;
+    uint4 kr[KV4];
+    if (valid) {
+      const uint4* kp = reinterpret_cast<const uint4*>(kc + ((size_t)kvh * ctx + j) * HD);
+#pragma unroll
+      for (int c = 0; c < KV4; ++c) kr[c] = kp[c];
     }
-    return;
-  }
-  const int j = j0 + lane;
-  const bool valid = j < j1;
-  float sc[8];
+    // lane owns head dims [DPL*lane, DPL*lane + DPL) of every V row of the slice
+    static_assert(DPL == 2 || DPL == 1 || DPL == 4, "head_dim");
+    using VT = typename std::conditional<DPL == 1, uint16_t, typename std::conditional<DPL == 2, uint32_t, uint2>::type>::type;
+    VT vraw[SPLIT];
+    {
+      const __half* vb = vc + ((size_t)kvh * ctx + j0) * HD + DPL * lane;
 #pragma unroll
-  for (int g = 0; g < 8; ++g) sc[g] = 0.f;
-  if (valid) {
-    const uint4* kp = reinterpret_cast<const uint4*>(kc + ((size_t)kvh * ctx + j) * HD);
-#pragma unroll 4
-    for (int c = 0; c < HD / 8; ++c) {
-      uint4 raw = kp[c];
-      const __half2* h2 = reinterpret_cast<const __half2*>(&raw);
-      float kf[8];
+      for (int jj = 0; jj < SPLIT; ++jj)
+        if (jj < nk) vraw[jj] = *reinterpret_cast<const VT*>(vb + (size_t)jj * HD);
+    }
+    for (int i = lane; i < G * HD; i += 64) qs[i / HD][i % HD] = q[(size_t)(kvh * G) * HD + i];
+    __syncthreads();
+    float sc[8];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        float2 f = __half22float2(h2[t]);
-        kf[2 * t] = f.x;
-        kf[2 * t + 1] = f.y;
-      }
+    for (int g = 0; g < 8; ++g) sc[g] = 0.f;
+    if (valid) {
 #pragma unroll
-      for (int g = 0; g < 8; ++g) {
-        if (g < G) {
+      for (int c = 0; c < KV4; ++c) {
+        const __half2* h2 = reinterpret_cast<const __half2*>(&kr[c]);
+        float kf[8];
 #pragma unroll
-          for (int t = 0; t < 8; ++t) sc[g] += qs[g][8 * c + t] * kf[t];
+        for (int t = 0; t < 4; ++t) {
+          const float2 f = __half22float2(h2[t]);
+          kf[2 * t] = f.x;
+          kf[2 * t + 1] = f.y;
+        }
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+          if (g < G) {
+            const float4 qa = *reinterpret_cast<const float4*>(&qs[g][8 * c]);
+            const float4 qb = *reinterpret_cast<const float4*>(&qs[g][8 * c + 4]);
+            sc[g] += qa.x * kf[0] + qa.y * kf[1] + qa.z * kf[2] + qa.w * kf[3] + qb.x * kf[4] + qb.y * kf[5] +
+                     qb.z * kf[6] + qb.w * kf[7];
+          }
         }
       }
     }
-  }
-#pragma unroll
-  for (int g = 0; g < 8; ++g) {
-    if (g >= G) break;
-    float s = valid ? sc[g] * scale : -INFINITY;
-    float m = wave_max(s);
-    float p = valid ? expf(s - m) : 0.f;
-    float l = wave_sum(p);
-    ps[g][lane] = p;
-    if (lane == 0) {
-      float* pr = prow + (size_t)g * nsplit * (HD + 2);
-      pr[0] = m;
-      pr[1] = l;
-    }
-  }
-  __syncthreads();
-  float o[8][DPL];
-#pragma unroll
-  for (int g = 0; g < 8; ++g)
-#pragma unroll
-    for (int t = 0; t < DPL; ++t) o[g][t] = 0.f;
-  const int nk = j1 - j0;
-  const __half* vbase = vc + ((size_t)kvh * ctx + j0) * HD;
-  for (int jj = 0; jj < nk; ++jj) {
-    float vf[DPL];
-#pragma unroll
-    for (int t = 0; t < DPL; ++t) vf[t] = __half2float(vbase[(size_t)jj * HD + lane + 64 * t]);
+    float mg[8], lg[8];
 #pragma unroll
     for (int g = 0; g < 8; ++g) {
       if (g < G) {
-        float p = ps[g][jj];
+        const float s = valid ? sc[g] * scale : -INFINITY;
+        mg[g] = wave_max(s);
+        const float p = valid ? expf(s - mg[g]) : 0.f;
+        lg[g] = wave_sum(p);
+        ps[g][lane] = p;
+      }
+    }
+    __syncthreads();
+    float o[8][DPL];
 #pragma unroll
-        for (int t = 0; t < DPL; ++t) o[g][t] += p * vf[t];
+    for (int g = 0; g < 8; ++g)
+#pragma unroll
+      for (int t = 0; t < DPL; ++t) o[g][t] = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < SPLIT; ++jj) {
+      if (jj < nk) {
+        float vf[DPL];
+        const __half* hv = reinterpret_cast<const __half*>(&vraw[jj]);
+#pragma unroll
+        for (int t = 0; t < DPL; ++t) vf[t] = __half2float(hv[t]);
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+          if (g < G) {
+            const float p = ps[g][jj];
+#pragma unroll
+            for (int t = 0; t < DPL; ++t) o[g][t] += p * vf[t];
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      if (g < G) {
+        float* pr = part + ((size_t)(kvh * G + g) * nsplit + sp) * (HD + 2);
+        if (lane == 0) {
+          pr[0] = mg[g];
+          pr[1] = lg[g];
+        }
+#pragma unroll
+        for (int t = 0; t < DPL; ++t) pr[2 + DPL * lane + t] = o[g][t];
       }
     }
   }
+  // publish, then let the last slice of this KV head merge
+  __threadfence();
+  if (lane == 0) {
+    const int prev = atomicAdd(&counters[kvh], 1);
+    last = prev == nsplit - 1;
+    if (last) counters[kvh] = 0;
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  const int nlive = (total + SPLIT - 1) / SPLIT;
+  const int s0 = jmin / SPLIT;
+  for (int g = 0; g < G; ++g) {
+    const float* pr = part + (size_t)(kvh * G + g) * nsplit * (HD + 2);
+    float M = -INFINITY;
+    for (int s = s0; s < nlive; ++s) M = fmaxf(M, __builtin_nontemporal_load(pr + (size_t)s * (HD + 2)));
+    float L = 0.f;
+    float acc[DPL];
 #pragma unroll
-  for (int g = 0; g < 8; ++g) {
-    if (g < G) {
-      float* pr = prow + (size_t)g * nsplit * (HD + 2);
+    for (int t = 0; t < DPL; ++t) acc[t] = 0.f;
+    for (int s = s0; s < nlive; ++s) {
+      const float* e = pr + (size_t)s * (HD + 2);
+      const float w = expf(__builtin_nontemporal_load(e) - M);
+      L += __builtin_nontemporal_load(e + 1) * w;
 #pragma unroll
-      for (int t = 0; t < DPL; ++t) pr[2 + lane + 64 * t] = o[g][t];
+      for (int t = 0; t < DPL; ++t) acc[t] += __builtin_nontemporal_load(e + 2 + DPL * lane + t) * w;
     }
+#pragma unroll
+    for (int t = 0; t < DPL; ++t) out[(size_t)(kvh * G + g) * HD + DPL * lane + t] = acc[t] / L;
   }
 }
 
-__global__ void attn_decode_combine_kernel(const float* part, float* out, int nsplit, int hd) {
-  const int h = blockIdx.x;
-  const float* pr = part + (size_t)h * nsplit * (hd + 2);
-  float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, pr[(size_t)s * (hd + 2)]);
-  float L = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    float m = pr[(size_t)s * (hd + 2)];
-    if (m != -INFINITY) L += pr[(size_t)s * (hd + 2) + 1] * expf(m - M);
-  }
-  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-    float acc = 0.f;
-    for (int s = 0; s < nsplit; ++s) {
-      float m = pr[(size_t)s * (hd + 2)];
-      if (m != -INFINITY) acc += pr[(size_t)s * (hd + 2) + 2 + d] * expf(m - M);
-    }
-    out[(size_t)h * hd + d] = acc / L;
-  }
-}
-
-void launch_attn_decode(const float* q, const __half* kc, const __half* vc, float* out, float* part, int n_heads,
-                        int n_kv, int head_dim, int ctx, const int* pos_dev, int window, float scale, int max_len,
-                        hipStream_t st) {
+void launch_attn_decode(const float* q, const __half* kc, const __half* vc, float* out, float* part, int* counters,
+                        int n_heads, int n_kv, int head_dim, int ctx, const int* pos_dev, int window, float scale,
+                        int max_len, hipStream_t st) {
   const int nsplit = (max_len + SPLIT - 1) / SPLIT;
   dim3 grid(n_kv, nsplit);
-  if (n_heads / n_kv > 8) fail(ST_OP, "attention: GQA group larger than 8 is not supported");
+  if (n_heads % n_kv != 0 || n_heads / n_kv > 8) fail(ST_OP, "attention: GQA group larger than 8 is not supported");
   switch (head_dim) {
     case 64:
-      hipLaunchKernelGGL(attn_decode_partial_kernel<64>, grid, dim3(64), 0, st, q, kc, vc, part, n_heads, n_kv, ctx,
-                         pos_dev, window, scale, nsplit);
+      hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(64), 0, st, q, kc, vc, part, out, counters, n_heads, n_kv,
+                         ctx, pos_dev, window, scale, nsplit);
       break;
     case 128:
-      hipLaunchKernelGGL(attn_decode_partial_kernel<128>, grid, dim3(64), 0, st, q, kc, vc, part, n_heads, n_kv, ctx,
-                         pos_dev, window, scale, nsplit);
+      hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(64), 0, st, q, kc, vc, part, out, counters, n_heads,
+                         n_kv, ctx, pos_dev, window, scale, nsplit);
       break;
     case 256:
-      hipLaunchKernelGGL(attn_decode_partial_kernel<256>, grid, dim3(64), 0, st, q, kc, vc, part, n_heads, n_kv, ctx,
-                         pos_dev, window, scale, nsplit);
+      hipLaunchKernelGGL(attn_decode_kernel<256>, grid, dim3(64), 0, st, q, kc, vc, part, out, counters, n_heads,
+                         n_kv, ctx, pos_dev, window, scale, nsplit);
       break;
     default:
       fail(ST_OP, "attention: head_dim must be 64, 128 or 256");
   }
-  hipLaunchKernelGGL(attn_decode_combine_kernel, dim3(n_heads), dim3(128), 0, st, part, out, nsplit, head_dim);
 }
 
 // Prefill: one wave per (head, 64-query tile); lane i owns query i. Keys/values are staged in

@@ -57,9 +57,9 @@ IEK_DEV void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2, float* s
 // f64-then-f32 result.
 IEK_DEV float q4k_value(float d, float dmin, float sc, float m, uint32_t q) {
 #pragma clang fp contract(off)
-  float ds = __fmul_rn(d, sc);
-  float dq = q == 0 ? 0.0f : __fmul_rn(ds, (float)q);
-  return __fsub_rn(dq, __fmul_rn(dmin, m));
+  float ds = d * sc;
+  float dq = q == 0 ? 0.0f : ds * (float)q;
+  return dq - dmin * m;
 }
 
 // Unaligned little-endian u16 from a byte pointer (Q6_K / Q8_0 blocks are only 2-byte aligned).
@@ -92,14 +92,14 @@ IEK_DEV float q6k_elem(const uint8_t* blk, int o) {
   uint32_t hb = (blk[128 + 32 * h + l] >> (2 * quarter)) & 3u;
   int q = (int)(nib | (hb << 4)) - 32;
   float s = (float)(int8_t)blk[192 + 8 * h + (l >> 4) + 2 * quarter];
-  float ds = __fmul_rn(d, s);
-  return q == 0 ? 0.0f : __fmul_rn(ds, (float)q);
+  float ds = d * s;
+  return q == 0 ? 0.0f : ds * (float)q;
 }
 
 // Single element of a Q8_0 block (quant_k_handler.rs:21-35).
 IEK_DEV float q80_elem(const uint8_t* blk, int o) {
   float d = half_bits_to_float(load_u16(blk));
-  return __fmul_rn(d, (float)(int8_t)blk[2 + o]);
+  return d * (float)(int8_t)blk[2 + o];
 }
 
 // Element at flat index `f` of a tensor stored as consecutive blocks of type `dt`.

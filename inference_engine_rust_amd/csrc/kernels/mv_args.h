@@ -1,0 +1,51 @@
+// Launch arguments of the decode matvec family (kernels/matvec.hip), shared with the host engine.
+#pragma once
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace iek {
+
+enum MvEpilogue : int {
+  EPI_STORE = 0,   // out[s][n] = dot
+  EPI_RESID = 1,   // out[0][n] = resid[n] + dot
+  EPI_SWIGLU = 2,  // w[0] = gate, w[1] = up: out[0][n] = silu(gate.x) * (up.x)
+  EPI_QKV = 3,     // segments q, k, v: RoPE on q and k pairs, q -> out[0], k/v -> fp16 KV cache at *pos
+  EPI_ARGMAX = 4,  // logits -> out[0] (optional soft cap), atomicMax of packed (value, first index)
+};
+
+struct MvArgs {
+  const uint8_t* w[3];
+  float* out[3];
+  int n[3];
+  int seg_start[4];
+  int nseg;
+  const float* x;       // input vector (raw residual stream when norm_w is set)
+  const float* norm_w;  // fused RMSNorm weight, or null
+  float eps;
+  int K;
+  int epi;
+  const float* resid;
+  // EPI_QKV
+  const float* rope_cs;  // [ctx][npairs][2] (cos, sin)
+  int npairs, head_dim, ctx;
+  const int* pos;
+  __half* kc;
+  __half* vc;
+  // EPI_ARGMAX
+  unsigned long long* amax_key;
+  int* amax_flag;
+  float softcap;  // <= 0: none
+  int* pos_inc;   // when set, one thread adds 1 after the launch's work is issued (end of a decode step)
+};
+
+__host__ __device__ inline int seg_of(const MvArgs& a, int row) {
+  int s = 0;
+  if (a.nseg > 1 && row >= a.seg_start[1]) s = 1;
+  if (a.nseg > 2 && row >= a.seg_start[2]) s = 2;
+  return s;
+}
+
+void launch_mv(int dt, MvArgs a, hipStream_t st);
+
+}  // namespace iek

@@ -29,7 +29,7 @@ __global__ void embed_kernel(int dt, const uint8_t* table, size_t hidden, const 
   const size_t base = (size_t)ids[r] * hidden;
   for (size_t h = threadIdx.x; h < hidden; h += blockDim.x) {
     float v = flat_elem(dt, table, base + h);
-    if (scale != 1.0f) v = __fmul_rn(v, scale);
+    if (scale != 1.0f) v = v * scale;
     out[(size_t)r * hidden + h] = v;
   }
 }
@@ -64,10 +64,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* in, const flo
   const float* x = in + (size_t)blockIdx.x * dim;
   float* y = out + (size_t)blockIdx.x * dim;
   float ss = 0.f;
-  for (int i = threadIdx.x; i < dim; i += blockDim.x) ss += __fmul_rn(x[i], x[i]);
+  for (int i = threadIdx.x; i < dim; i += blockDim.x) ss += x[i] * x[i];
   ss = block_sum256(ss, sh);
-  const float rms = __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)dim), eps));
-  for (int i = threadIdx.x; i < dim; i += blockDim.x) y[i] = __fdiv_rn(__fmul_rn(x[i], w[i]), rms);
+  const float rms = sqrtf(ss / (float)dim + eps);
+  for (int i = threadIdx.x; i < dim; i += blockDim.x) y[i] = (x[i] * w[i]) / rms;
 }
 
 void launch_rmsnorm(const float* in, const float* w, int rows, int dim, float eps, float* out, hipStream_t st) {
@@ -80,8 +80,8 @@ void launch_rmsnorm(const float* in, const float* w, int rows, int dim, float ep
 IEK_DEV void rotate(float* v, int p, float c, float s) {
 #pragma clang fp contract(off)
   float t0 = v[p], t1 = v[p + 1];
-  v[p] = __fsub_rn(__fmul_rn(t0, c), __fmul_rn(t1, s));
-  v[p + 1] = __fadd_rn(__fmul_rn(t0, s), __fmul_rn(t1, c));
+  v[p] = t0 * c - t1 * s;
+  v[p + 1] = t0 * s + t1 * c;
 }
 
 __global__ void rope_rows_kernel(float* v, int rows, int row_stride, int n_heads, int head_dim, int pos0,
@@ -153,12 +153,12 @@ __global__ void swiglu_kernel(const float* g, const float* u, float* out, size_t
   float x = g[i], s;
   if (x >= 0.0f) {
     float z = expf(-x);
-    s = __fdiv_rn(1.0f, __fadd_rn(1.0f, z));
+    s = 1.0f / (1.0f + z);
   } else {
     float z = expf(x);
-    s = __fdiv_rn(z, __fadd_rn(1.0f, z));
+    s = z / (1.0f + z);
   }
-  out[i] = __fmul_rn(__fmul_rn(x, s), u[i]);
+  out[i] = x * s * u[i];
 }
 
 void launch_swiglu(const float* g, const float* u, float* out, size_t n, hipStream_t st) {
@@ -170,14 +170,13 @@ void launch_swiglu(const float* g, const float* u, float* out, size_t n, hipStre
 IEK_DEV float gelu_tanh_dev(float x) {
 #pragma clang fp contract(off)
   const float k = 1.12837916709551257390f * 0.707106781186547524401f;
-  float x3 = __fmul_rn(__fmul_rn(x, x), x);
-  float inner = __fmul_rn(k, __fadd_rn(x, __fmul_rn(0.044715f, x3)));
-  return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanhf(inner)));
+  float x3 = x * x * x;
+  return 0.5f * x * (1.0f + tanhf(k * (x + 0.044715f * x3)));
 }
 
 __global__ void gelu_mul_kernel(const float* g, const float* u, float* out, size_t n) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) out[i] = __fmul_rn(gelu_tanh_dev(g[i]), u ? u[i] : 1.0f);
+  if (i < n) out[i] = u ? gelu_tanh_dev(g[i]) * u[i] : gelu_tanh_dev(g[i]);
 }
 
 void launch_gelu_mul(const float* g, const float* u, float* out, size_t n, hipStream_t st) {
@@ -187,7 +186,7 @@ void launch_gelu_mul(const float* g, const float* u, float* out, size_t n, hipSt
 
 __global__ void residual_add_kernel(const float* a, const float* b, float* out, size_t n) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) out[i] = __fadd_rn(a[i], b[i]);
+  if (i < n) out[i] = a[i] + b[i];
 }
 
 void launch_residual_add(const float* a, const float* b, float* out, size_t n, hipStream_t st) {
@@ -211,7 +210,7 @@ __global__ __launch_bounds__(256) void softmax_kernel(const float* in, float* ou
   float s = 0.f;
   for (int i = threadIdx.x; i < n; i += blockDim.x) s += expf(in[i] - mm);
   s = block_sum256(s, sh);
-  for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = __fdiv_rn(expf(in[i] - mm), s);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = expf(in[i] - mm) / s;
 }
 
 void launch_softmax(const float* in, float* out, int n, hipStream_t st) {
@@ -253,25 +252,32 @@ void launch_argmax(const float* logits, int n, unsigned long long* key_out, int*
 }
 
 // Publishes the chosen token: tok[0] feeds the next embedding gather; with a step counter the id
-// is also appended to the generated-token list and the counter advances.
-__global__ void argmax_finish_kernel(const unsigned long long* key, uint32_t* tok, uint32_t* list, int* step) {
+// and the non-finite flag are also appended to the per-step lists and the counter advances. The
+// packed key and the flag are reset for the next LM-head launch.
+__global__ void argmax_finish_kernel(unsigned long long* key, int* flag, uint32_t* tok, uint32_t* list, int* flags,
+                                     int* step) {
   uint32_t idx = 0xFFFFFFFFu - (uint32_t)(*key & 0xFFFFFFFFull);
   tok[0] = idx;
+  const int i = step ? *step : 0;
+  flags[i] = *flag;
   if (step) {
-    list[*step] = idx;
-    *step += 1;
+    list[i] = idx;
+    *step = i + 1;
   }
+  *key = 0ull;
+  *flag = 0;
 }
 
-void launch_argmax_finish(const unsigned long long* key, uint32_t* tok, uint32_t* list, int* step, hipStream_t st) {
-  hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(1), 0, st, key, tok, list, step);
+void launch_argmax_finish(unsigned long long* key, int* flag, uint32_t* tok, uint32_t* list, int* flags, int* step,
+                          hipStream_t st) {
+  hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(1), 0, st, key, flag, tok, list, flags, step);
 }
 
 // Final-logit soft cap z -> cap * tanh(z / cap) (src/engine/runtime.rs:110-114).
 __global__ void softcap_kernel(float* z, int n, float cap) {
 #pragma clang fp contract(off)
   int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) z[i] = __fmul_rn(cap, tanhf(__fdiv_rn(z[i], cap)));
+  if (i < n) z[i] = cap * tanhf(z[i] / cap);
 }
 void launch_softcap(float* z, int n, float cap, hipStream_t st) {
   hipLaunchKernelGGL(softcap_kernel, dim3((n + 255) / 256), dim3(256), 0, st, z, n, cap);

@@ -6,6 +6,8 @@
 //   final_logits_last_token                      src/engine/runtime.rs:76-116
 #include "session.h"
 
+#include "kernels/mv_args.h"
+
 #include <cmath>
 #include <cstring>
 
@@ -71,6 +73,11 @@ Session::Session(Model* m) : m_(m) {
   d_ids_ = dev_alloc<uint32_t>(ctx_);
   d_gen_ = dev_alloc<uint32_t>(ctx_ + 1);
   d_key_ = dev_alloc<unsigned long long>(1);
+  d_flag_ = dev_alloc<int>(1);
+  d_cnt_ = dev_alloc<int>(c.n_kv_heads);
+  launch_fill_u64(d_key_, 0ull, 1, st_);
+  launch_fill_i32(d_flag_, 0, 1, st_);
+  launch_fill_i32(d_cnt_, 0, c.n_kv_heads, st_);
   reset();
 }
 
@@ -82,7 +89,7 @@ Session::~Session() {
                   (void*)act_, (void*)tmp_, (void*)xdec_, (void*)xndec_, (void*)qd_, (void*)kd_, (void*)vd_,
                   (void*)attd_, (void*)actd_, (void*)logits_, (void*)part_, (void*)tmpd_, (void*)d_pos_,
                   (void*)d_step_, (void*)d_flags_, (void*)d_tok_, (void*)d_ids_, (void*)d_gen_, (void*)d_key_,
-                  kv_blob_})
+                  (void*)d_flag_, (void*)d_cnt_, kv_blob_})
     dev_free(p);
   if (st_) (void)hipStreamDestroy(st_);
 }
@@ -179,13 +186,95 @@ void Session::layer_prefill(int li, int M) {
   project(L.down, act_, M, S.ffn_dim, H_, x_, x_, st_);
 }
 
-void Session::layer_decode(int li) {
+// Decode layer, fused path: 5 launches (QKV+norm+RoPE+KV append, attention, O+residual,
+// gate/up+norm+SwiGLU, down+residual). Conditions: no Q/K un-permute, same K-quant dtype for
+// Q/K/V and for gate/up, K a multiple of 256.
+bool Session::fused_ok(int li) const {
+  const Config& c = m_->cfg;
+  const LayerTensors& L = m_->layers[li];
+  auto kq = [](int dt) { return dt == DT_Q4K || dt == DT_Q6K; };
+  return !c.unpack_qk && L.wq.dtype == L.wk.dtype && L.wq.dtype == L.wv.dtype && kq(L.wq.dtype) &&
+         L.gate.dtype == L.up.dtype && kq(L.gate.dtype) && H_ % 256 == 0 && c.layers[li].head_dim % 2 == 0;
+}
+
+void Session::layer_decode(int li, bool last) {
+  const Config& c = m_->cfg;
+  const LayerSpec& S = c.layers[li];
+  const LayerTensors& L = m_->layers[li];
+  const int hd = S.head_dim, qd = S.q_dim, kvd = S.kv_dim;
+  const float scale = 1.0f / sqrtf((float)hd);
+  if (!fused_ok(li)) {
+    layer_decode_unfused(li);
+    if (last) launch_add_int(d_pos_, 1, st_);
+    return;
+  }
+  const RopeTable& rt = m_->rope_tables[L.rope_table];
+  MvArgs a{};
+  a.nseg = 3;
+  a.w[0] = (const uint8_t*)L.wq.dev;
+  a.w[1] = (const uint8_t*)L.wk.dev;
+  a.w[2] = (const uint8_t*)L.wv.dev;
+  a.out[0] = qd_;
+  a.n[0] = qd;
+  a.n[1] = kvd;
+  a.n[2] = kvd;
+  a.x = xdec_;
+  a.norm_w = (const float*)L.attn_norm.dev;
+  a.eps = c.rms_eps;
+  a.K = H_;
+  a.epi = EPI_QKV;
+  a.rope_cs = rt.dev;
+  a.npairs = S.rotary_dim / 2;
+  a.head_dim = hd;
+  a.ctx = ctx_;
+  a.pos = d_pos_;
+  a.kc = kc_[li];
+  a.vc = vc_[li];
+  launch_mv(L.wq.dtype, a, st_);
+  launch_attn_decode(qd_, kc_[li], vc_[li], attd_, part_, d_cnt_, c.n_heads, c.n_kv_heads, hd, ctx_, d_pos_, S.window,
+                     scale, ctx_, st_);
+  MvArgs o{};
+  o.nseg = 1;
+  o.w[0] = (const uint8_t*)L.wo.dev;
+  o.out[0] = xdec_;
+  o.n[0] = H_;
+  o.x = attd_;
+  o.K = qd;
+  o.epi = EPI_RESID;
+  o.resid = xdec_;
+  launch_mv(L.wo.dtype, o, st_);
+  MvArgs f{};
+  f.nseg = 2;
+  f.w[0] = (const uint8_t*)L.gate.dev;
+  f.w[1] = (const uint8_t*)L.up.dev;
+  f.out[0] = actd_;
+  f.n[0] = S.ffn_dim;
+  f.n[1] = S.ffn_dim;
+  f.x = xdec_;
+  f.norm_w = (const float*)L.ffn_norm.dev;
+  f.eps = c.rms_eps;
+  f.K = H_;
+  f.epi = EPI_SWIGLU;
+  launch_mv(L.gate.dtype, f, st_);
+  MvArgs dn{};
+  dn.nseg = 1;
+  dn.w[0] = (const uint8_t*)L.down.dev;
+  dn.out[0] = xdec_;
+  dn.n[0] = H_;
+  dn.x = actd_;
+  dn.K = S.ffn_dim;
+  dn.epi = EPI_RESID;
+  dn.resid = xdec_;
+  dn.pos_inc = last ? d_pos_ : nullptr;
+  launch_mv(L.down.dtype, dn, st_);
+}
+
+void Session::layer_decode_unfused(int li) {
   const Config& c = m_->cfg;
   const LayerSpec& S = c.layers[li];
   const LayerTensors& L = m_->layers[li];
   const int hd = S.head_dim, qd = S.q_dim, kvd = S.kv_dim;
   launch_rmsnorm(xdec_, (const float*)L.attn_norm.dev, 1, H_, c.rms_eps, xndec_, st_);
-  // Q/K/V in one launch when they share a dtype (each wave's rows stay inside one weight).
   if (L.wq.dtype == L.wk.dtype && L.wq.dtype == L.wv.dtype) {
     MvSegDesc s[3] = {{L.wq.dev, qd_, nullptr, qd}, {L.wk.dev, kd_, nullptr, kvd}, {L.wv.dev, vd_, nullptr, kvd}};
     launch_matvec(L.wq.dtype, s, 3, xndec_, H_, 0, st_);
@@ -205,8 +294,8 @@ void Session::layer_decode(int li) {
   launch_rope_table(kd_, c.n_kv_heads, hd, S.rotary_dim / 2, rt.dev, d_pos_, st_);
   launch_kv_store(kd_, vd_, 1, kvd, kc_[li], vc_[li], c.n_kv_heads, hd, ctx_, d_pos_, 0, st_);
   const float scale = 1.0f / sqrtf((float)hd);
-  launch_attn_decode(qd_, kc_[li], vc_[li], attd_, part_, c.n_heads, c.n_kv_heads, hd, ctx_, d_pos_, S.window, scale,
-                     ctx_, st_);
+  launch_attn_decode(qd_, kc_[li], vc_[li], attd_, part_, d_cnt_, c.n_heads, c.n_kv_heads, hd, ctx_, d_pos_, S.window,
+                     scale, ctx_, st_);
   project(L.wo, attd_, 1, qd, H_, xdec_, xdec_, st_);
   launch_rmsnorm(xdec_, (const float*)L.ffn_norm.dev, 1, H_, c.rms_eps, xndec_, st_);
   if (L.gate.dtype == L.up.dtype) {
@@ -260,8 +349,7 @@ void Session::decode_body() {
   size_t vocab;
   size_t hid = embedding_hidden(m_->token_embd, &vocab);
   launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, d_tok_, 1, c.embed_scale, xdec_, st_);
-  for (int li = 0; li < c.n_layers; ++li) layer_decode(li);
-  launch_add_int(d_pos_, 1, st_);
+  for (int li = 0; li < c.n_layers; ++li) layer_decode(li, li == c.n_layers - 1);
 }
 
 void Session::decode_token(uint32_t id) {
@@ -282,32 +370,53 @@ void Session::check_state() const {
   if (state_rows_ == 0) fail(ST_MODEL, "final_logits_last_token: empty input");
 }
 
-void Session::logits_body() {
+// Final RMSNorm (last row) + LM head (+ soft cap). With `argmax`, the LM-head epilogue also folds
+// every logit into the packed greedy key (d_key_) and the non-finite flag (d_flag_).
+void Session::logits_body(bool argmax) {
   const Config& c = m_->cfg;
-  launch_rmsnorm(xdec_, (const float*)m_->output_norm.dev, 1, H_, c.rms_eps, xndec_, st_);
-  project(m_->lm_head, xndec_, 1, H_, c.vocab, logits_, nullptr, st_);
-  if (c.has_softcap) launch_softcap(logits_, c.vocab, c.softcap, st_);
+  MvArgs a{};
+  a.nseg = 1;
+  a.w[0] = (const uint8_t*)m_->lm_head.dev;
+  a.out[0] = logits_;
+  a.n[0] = c.vocab;
+  a.x = xdec_;
+  a.norm_w = (const float*)m_->output_norm.dev;
+  a.eps = c.rms_eps;
+  a.K = H_;
+  const DevTensor& w = m_->lm_head;
+  if (w.dims.size() != 2 || (int)w.dims[0] != H_ || (int)w.dims[1] != c.vocab)
+    fail(ST_MATMUL, "LM head dims do not match hidden_dim x vocab_size");
+  if (argmax) {
+    a.epi = EPI_ARGMAX;
+    a.amax_key = d_key_;
+    a.amax_flag = d_flag_;
+    a.softcap = c.has_softcap ? c.softcap : 0.f;
+    launch_mv(w.dtype, a, st_);
+  } else {
+    a.epi = EPI_STORE;
+    launch_mv(w.dtype, a, st_);
+    if (c.has_softcap) launch_softcap(logits_, c.vocab, c.softcap, st_);
+  }
 }
 
 void Session::logits_last_token(float* out, int n) {
   check_state();
   if (n < m_->cfg.vocab) fail(ST_OP, "logits buffer smaller than vocab_size");
-  logits_body();
+  logits_body(false);
   IEK_HIP(hipMemcpyAsync(out, logits_, (size_t)m_->cfg.vocab * 4, hipMemcpyDeviceToHost, st_));
   sync();
 }
 
+// LM head with the fused argmax, then one thread publishes the token (and resets the key/flag).
 void Session::argmax_body(bool record) {
-  launch_fill_u64(d_key_, 0ull, 1, st_);
-  launch_argmax(logits_, m_->cfg.vocab, d_key_, d_flags_, record ? d_step_ : nullptr, st_);
-  launch_argmax_finish(d_key_, d_tok_, d_gen_, record ? d_step_ : nullptr, st_);
+  logits_body(true);
+  launch_argmax_finish(d_key_, d_flag_, d_tok_, d_gen_, d_flags_, record ? d_step_ : nullptr, st_);
 }
 
 uint32_t Session::greedy_next_token() {
   check_state();
   if (m_->cfg.vocab == 0) fail(ST_SAMPLING, "logits slice is empty");
   launch_fill_i32(d_flags_, 0, 1, st_);
-  logits_body();
   argmax_body(false);
   uint32_t tok = 0;
   int flag = 0;
@@ -329,7 +438,6 @@ void Session::generate_greedy(int n, uint32_t* out_ids, bool use_graph) {
       sync();
       IEK_HIP(hipStreamBeginCapture(st_, hipStreamCaptureModeThreadLocal));
       try {
-        logits_body();
         argmax_body(true);
         decode_body();
       } catch (...) {
@@ -344,7 +452,6 @@ void Session::generate_greedy(int n, uint32_t* out_ids, bool use_graph) {
     for (int i = 0; i < n; ++i) IEK_HIP(hipGraphLaunch(step_exec_, st_));
   } else {
     for (int i = 0; i < n; ++i) {
-      logits_body();
       argmax_body(true);
       decode_body();
     }

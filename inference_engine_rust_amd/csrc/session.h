@@ -31,9 +31,11 @@ class Session {
  private:
   void ensure_rows(int rows);
   void layer_prefill(int li, int M);
-  void layer_decode(int li);
+  bool fused_ok(int li) const;
+  void layer_decode(int li, bool last);
+  void layer_decode_unfused(int li);
   void decode_body();           // embed(d_tok) + every layer + pos++; no host sync
-  void logits_body();           // final norm + LM head (+ softcap) into logits_
+  void logits_body(bool argmax);  // final norm + LM head (+ softcap) into logits_
   void argmax_body(bool record);
   void sync();
   void check_state() const;
@@ -57,6 +59,8 @@ class Session {
   uint32_t* d_ids_ = nullptr;  // prompt ids / generated ids
   uint32_t* d_gen_ = nullptr;
   unsigned long long* d_key_ = nullptr;
+  int* d_flag_ = nullptr;  // non-finite logit seen by the fused argmax
+  int* d_cnt_ = nullptr;   // per-KV-head slice counters of the decode attention
   int pos_ = 0;
   int state_rows_ = 0;  // rows of the last ForwardState (0 = none)
   bool state_prefill_ = false;
