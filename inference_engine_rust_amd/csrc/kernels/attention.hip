@@ -15,170 +15,231 @@ namespace iek {
 
 constexpr int SPLIT = 64;
 
-// One wave per (KV head, 64-key slice). Lane j scores key j0+j against the G query heads of the
-// group; the V rows of the slice are fetched in the same burst (lanes over head dims) so each
-// wave makes a single trip to HBM. Slices publish (max, sum, o[]) partials; the last wave of a
-// KV head (device-scope counter, reset by that wave) merges them into the attention output.
-template <int HD>
+// One wave per (KV head, 64-key slice). Lane j scores key j0+j against the G <= GM query heads of
+// the group; the V rows of the slice are fetched in the same burst as K (uint4 per lane, LPR lanes
+// per row) so each wave makes a single trip to HBM (two for head_dim 256, where holding both
+// would exceed the register file). Slices publish (max, sum, o[]) partials that a second launch
+// merges per query head (a cross-workgroup merge inside one launch would need device-scope
+// fences, which write back the L2 of every XCD).
+template <int HD, int GM>
 __global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict__ q, const __half* __restrict__ kc,
                                                          const __half* __restrict__ vc, float* __restrict__ part,
-                                                         float* __restrict__ out, int* __restrict__ counters,
                                                          int n_heads, int n_kv, int ctx, const int* pos_dev,
                                                          int window, float scale, int nsplit) {
-  constexpr int DPL = HD / 64;  // head dims per lane in the PV phase
-  constexpr int KV4 = HD / 8;   // uint4 (8 halves) per key row
+  constexpr int KV4 = HD / 8;      // uint4 (8 halves) per key row
+  constexpr int LPR = HD / 8;      // lanes per V row in the PV phase
+  constexpr int RPI = 64 / LPR;    // V rows covered by one load instruction of the wave
+  constexpr int NV = SPLIT / RPI;  // V loads per lane
+  constexpr bool TWO_TRIPS = HD > 128;
+  static_assert(HD == 64 || HD == 128 || HD == 256, "head_dim");
   const int kvh = blockIdx.x, sp = blockIdx.y, lane = threadIdx.x;
   const int G = n_heads / n_kv;
   const int total = *pos_dev + 1;
   const int jmin = (window > 0 && total > window) ? total - window : 0;
   const int j0 = max(sp * SPLIT, jmin), j1 = min(total, (sp + 1) * SPLIT);
-  __shared__ float qs[8][HD];
-  __shared__ float ps[8][SPLIT];
-  __shared__ int last;
+  __shared__ __align__(16) float qs[GM][HD];
+  __shared__ float ps[GM][SPLIT];
   const int nk = j1 - j0;
-  if (nk > 0) {
-    const int j = j0 + lane;
-    const bool valid = lane < nk;
-    uint4 kr[KV4];
-    if (valid) {
-      const uint4* kp = reinterpret_cast<const uint4*>(kc + ((size_t)kvh * ctx + j) * HD);
+  if (nk <= 0) return;
+  // Every load is issued unconditionally (indices clamped into the live slice) so the compiler
+  // keeps all of them in flight at once instead of waiting on each guarded load.
+  const bool valid = lane < nk;
+  const int j = j0 + min(lane, nk - 1);
+  const int vrow = lane / LPR, vcol = 8 * (lane % LPR);
+  const __half* vb = vc + ((size_t)kvh * ctx + j0) * HD + vcol;
+  uint4 kr[KV4];
+  uint4 vraw[NV];
+  {
+    const uint4* kp = reinterpret_cast<const uint4*>(kc + ((size_t)kvh * ctx + j) * HD);
 #pragma unroll
-      for (int c = 0; c < KV4; ++c) kr[c] = kp[c];
+    for (int c = 0; c < KV4; ++c) kr[c] = kp[c];
+  }
+  if constexpr (!TWO_TRIPS) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      vraw[i] = *reinterpret_cast<const uint4*>(vb + (size_t)min(vrow + RPI * i, nk - 1) * HD);
+  }
+  for (int i = lane; i < G * HD; i += 64) qs[i / HD][i % HD] = q[(size_t)(kvh * G) * HD + i];
+  __syncthreads();
+  float sc[GM];
+#pragma unroll
+  for (int g = 0; g < GM; ++g) sc[g] = 0.f;
+#pragma unroll
+  for (int c = 0; c < KV4; ++c) {
+    const __half2* h2 = reinterpret_cast<const __half2*>(&kr[c]);
+    float kf[8];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float2 f = __half22float2(h2[t]);
+      kf[2 * t] = f.x;
+      kf[2 * t + 1] = f.y;
     }
-    // lane owns head dims [DPL*lane, DPL*lane + DPL) of every V row of the slice
-    static_assert(DPL == 2 || DPL == 1 || DPL == 4, "head_dim");
-    using VT = typename std::conditional<DPL == 1, uint16_t, typename std::conditional<DPL == 2, uint32_t, uint2>::type>::type;
-    VT vraw[SPLIT];
-    {
-      const __half* vb = vc + ((size_t)kvh * ctx + j0) * HD + DPL * lane;
 #pragma unroll
-      for (int jj = 0; jj < SPLIT; ++jj)
-        if (jj < nk) vraw[jj] = *reinterpret_cast<const VT*>(vb + (size_t)jj * HD);
-    }
-    for (int i = lane; i < G * HD; i += 64) qs[i / HD][i % HD] = q[(size_t)(kvh * G) * HD + i];
-    __syncthreads();
-    float sc[8];
-#pragma unroll
-    for (int g = 0; g < 8; ++g) sc[g] = 0.f;
-    if (valid) {
-#pragma unroll
-      for (int c = 0; c < KV4; ++c) {
-        const __half2* h2 = reinterpret_cast<const __half2*>(&kr[c]);
-        float kf[8];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const float2 f = __half22float2(h2[t]);
-          kf[2 * t] = f.x;
-          kf[2 * t + 1] = f.y;
-        }
-#pragma unroll
-        for (int g = 0; g < 8; ++g) {
-          if (g < G) {
-            const float4 qa = *reinterpret_cast<const float4*>(&qs[g][8 * c]);
-            const float4 qb = *reinterpret_cast<const float4*>(&qs[g][8 * c + 4]);
-            sc[g] += qa.x * kf[0] + qa.y * kf[1] + qa.z * kf[2] + qa.w * kf[3] + qb.x * kf[4] + qb.y * kf[5] +
-                     qb.z * kf[6] + qb.w * kf[7];
-          }
-        }
-      }
-    }
-    float mg[8], lg[8];
-#pragma unroll
-    for (int g = 0; g < 8; ++g) {
+    for (int g = 0; g < GM; ++g) {
       if (g < G) {
-        const float s = valid ? sc[g] * scale : -INFINITY;
-        mg[g] = wave_max(s);
-        const float p = valid ? expf(s - mg[g]) : 0.f;
-        lg[g] = wave_sum(p);
-        ps[g][lane] = p;
-      }
-    }
-    __syncthreads();
-    float o[8][DPL];
-#pragma unroll
-    for (int g = 0; g < 8; ++g)
-#pragma unroll
-      for (int t = 0; t < DPL; ++t) o[g][t] = 0.f;
-#pragma unroll
-    for (int jj = 0; jj < SPLIT; ++jj) {
-      if (jj < nk) {
-        float vf[DPL];
-        const __half* hv = reinterpret_cast<const __half*>(&vraw[jj]);
-#pragma unroll
-        for (int t = 0; t < DPL; ++t) vf[t] = __half2float(hv[t]);
-#pragma unroll
-        for (int g = 0; g < 8; ++g) {
-          if (g < G) {
-            const float p = ps[g][jj];
-#pragma unroll
-            for (int t = 0; t < DPL; ++t) o[g][t] += p * vf[t];
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < 8; ++g) {
-      if (g < G) {
-        float* pr = part + ((size_t)(kvh * G + g) * nsplit + sp) * (HD + 2);
-        if (lane == 0) {
-          pr[0] = mg[g];
-          pr[1] = lg[g];
-        }
-#pragma unroll
-        for (int t = 0; t < DPL; ++t) pr[2 + DPL * lane + t] = o[g][t];
+        const float4 qa = *reinterpret_cast<const float4*>(&qs[g][8 * c]);
+        const float4 qb = *reinterpret_cast<const float4*>(&qs[g][8 * c + 4]);
+        sc[g] += qa.x * kf[0] + qa.y * kf[1] + qa.z * kf[2] + qa.w * kf[3] + qb.x * kf[4] + qb.y * kf[5] +
+                 qb.z * kf[6] + qb.w * kf[7];
       }
     }
   }
-  // publish, then let the last slice of this KV head merge
-  __threadfence();
-  if (lane == 0) {
-    const int prev = atomicAdd(&counters[kvh], 1);
-    last = prev == nsplit - 1;
-    if (last) counters[kvh] = 0;
+  if constexpr (TWO_TRIPS) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      vraw[i] = *reinterpret_cast<const uint4*>(vb + (size_t)min(vrow + RPI * i, nk - 1) * HD);
+  }
+  float mg[GM], lg[GM];
+#pragma unroll
+  for (int g = 0; g < GM; ++g) {
+    if (g < G) {
+      const float s = valid ? sc[g] * scale : -INFINITY;
+      mg[g] = wave_max(s);
+      const float p = valid ? expf(s - mg[g]) : 0.f;
+      lg[g] = wave_sum(p);
+      ps[g][lane] = p;
+    }
   }
   __syncthreads();
-  if (!last) return;
-  __threadfence();
-  const int nlive = (total + SPLIT - 1) / SPLIT;
-  const int s0 = jmin / SPLIT;
-  for (int g = 0; g < G; ++g) {
-    const float* pr = part + (size_t)(kvh * G + g) * nsplit * (HD + 2);
-    float M = -INFINITY;
-    for (int s = s0; s < nlive; ++s) M = fmaxf(M, __builtin_nontemporal_load(pr + (size_t)s * (HD + 2)));
-    float L = 0.f;
-    float acc[DPL];
+  float o[GM][8];
 #pragma unroll
-    for (int t = 0; t < DPL; ++t) acc[t] = 0.f;
-    for (int s = s0; s < nlive; ++s) {
-      const float* e = pr + (size_t)s * (HD + 2);
-      const float w = expf(__builtin_nontemporal_load(e) - M);
-      L += __builtin_nontemporal_load(e + 1) * w;
+  for (int g = 0; g < GM; ++g)
 #pragma unroll
-      for (int t = 0; t < DPL; ++t) acc[t] += __builtin_nontemporal_load(e + 2 + DPL * lane + t) * w;
+    for (int t = 0; t < 8; ++t) o[g][t] = 0.f;
+  // rows past the live slice carry p = 0 (ps holds p = 0 for invalid lanes)
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const __half2* h2 = reinterpret_cast<const __half2*>(&vraw[i]);
+    float vf[8];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float2 f = __half22float2(h2[t]);
+      vf[2 * t] = f.x;
+      vf[2 * t + 1] = f.y;
     }
 #pragma unroll
-    for (int t = 0; t < DPL; ++t) out[(size_t)(kvh * G + g) * HD + DPL * lane + t] = acc[t] / L;
+    for (int g = 0; g < GM; ++g) {
+      if (g < G) {
+        const float p = ps[g][vrow + RPI * i];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) o[g][t] += p * vf[t];
+      }
+    }
   }
+  // sum the RPI row subsets: lanes with equal lane % LPR hold the same head dims
+#pragma unroll
+  for (int g = 0; g < GM; ++g) {
+    if (g < G) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+#pragma unroll
+        for (int off = LPR; off < 64; off <<= 1) o[g][t] += __shfl_xor(o[g][t], off, 64);
+      }
+      float* pr = part + ((size_t)(kvh * G + g) * nsplit + sp) * (HD + 2);
+      if (lane == 0) {
+        pr[0] = mg[g];
+        pr[1] = lg[g];
+      }
+      if (lane < LPR) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) pr[2 + vcol + t] = o[g][t];
+      }
+    }
+  }
+}
+
+// Merge the live slices of one query head: (max, sum) of 64 slices at a time across lanes, then
+// each lane streams its head dims of every slice partial with the loads issued back to back.
+template <int HD>
+__global__ __launch_bounds__(64) void attn_decode_merge_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                                               int nsplit, const int* pos_dev, int window) {
+  constexpr int DPL = HD / 64;
+  const int h = blockIdx.x, lane = threadIdx.x;
+  const int total = *pos_dev + 1;
+  const int jmin = (window > 0 && total > window) ? total - window : 0;
+  const int nlive = (total + SPLIT - 1) / SPLIT;
+  const int s0 = jmin / SPLIT;
+  __shared__ float wsl[256];
+  const float* pr = part + (size_t)h * nsplit * (HD + 2);
+  float M = -INFINITY;
+  for (int s = s0 + lane; s < nlive; s += 64) M = fmaxf(M, pr[(size_t)s * (HD + 2)]);
+  M = wave_max(M);
+  float L = 0.f;
+  for (int s = s0 + lane; s < nlive; s += 64) {
+    const float w = expf(pr[(size_t)s * (HD + 2)] - M);
+    L += pr[(size_t)s * (HD + 2) + 1] * w;
+    if (s - s0 < 256) wsl[s - s0] = w;
+  }
+  L = wave_sum(L);
+  __syncthreads();
+  float acc[DPL];
+#pragma unroll
+  for (int t = 0; t < DPL; ++t) acc[t] = 0.f;
+  const int ns = min(nlive - s0, 256);
+  for (int s8 = 0; s8 < ns; s8 += 8) {
+    // clamped, unconditional loads: all eight slices' rows are in flight together
+    float v[8][DPL];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const size_t row = (size_t)(s0 + min(s8 + u, ns - 1)) * (HD + 2) + 2 + DPL * lane;
+#pragma unroll
+      for (int t = 0; t < DPL; ++t) v[u][t] = pr[row + t];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (s8 + u < ns) {
+        const float w = wsl[s8 + u];
+#pragma unroll
+        for (int t = 0; t < DPL; ++t) acc[t] += v[u][t] * w;
+      }
+    }
+  }
+  // slices beyond the 256 staged weights (contexts over 16K keys) use direct weights
+  for (int s = s0 + 256; s < nlive; ++s) {
+    const float w = expf(pr[(size_t)s * (HD + 2)] - M);
+#pragma unroll
+    for (int t = 0; t < DPL; ++t) acc[t] += pr[(size_t)s * (HD + 2) + 2 + DPL * lane + t] * w;
+  }
+#pragma unroll
+  for (int t = 0; t < DPL; ++t) out[(size_t)h * HD + DPL * lane + t] = acc[t] / L;
+}
+
+template <int HD, int GM>
+static void attn_decode_pair(dim3 grid, hipStream_t st, const float* q, const __half* kc, const __half* vc, float* out,
+                             float* part, int n_heads, int n_kv, int ctx, const int* pos_dev, int window, float scale,
+                             int nsplit) {
+  hipLaunchKernelGGL((attn_decode_kernel<HD, GM>), grid, dim3(64), 0, st, q, kc, vc, part, n_heads, n_kv, ctx, pos_dev,
+                     window, scale, nsplit);
+  hipLaunchKernelGGL(attn_decode_merge_kernel<HD>, dim3(n_heads), dim3(64), 0, st, part, out, nsplit, pos_dev, window);
+}
+
+template <int HD>
+static void attn_decode_hd(dim3 grid, hipStream_t st, const float* q, const __half* kc, const __half* vc, float* out,
+                           float* part, int n_heads, int n_kv, int ctx, const int* pos_dev, int window, float scale,
+                           int nsplit) {
+  if (n_heads / n_kv <= 4)
+    attn_decode_pair<HD, 4>(grid, st, q, kc, vc, out, part, n_heads, n_kv, ctx, pos_dev, window, scale, nsplit);
+  else
+    attn_decode_pair<HD, 8>(grid, st, q, kc, vc, out, part, n_heads, n_kv, ctx, pos_dev, window, scale, nsplit);
 }
 
 void launch_attn_decode(const float* q, const __half* kc, const __half* vc, float* out, float* part, int* counters,
                         int n_heads, int n_kv, int head_dim, int ctx, const int* pos_dev, int window, float scale,
                         int max_len, hipStream_t st) {
+  (void)counters;
   const int nsplit = (max_len + SPLIT - 1) / SPLIT;
   dim3 grid(n_kv, nsplit);
-  if (n_heads % n_kv != 0 || n_heads / n_kv > 8) fail(ST_OP, "attention: GQA group larger than 8 is not supported");
+  if (n_kv <= 0 || n_heads % n_kv != 0 || n_heads / n_kv > 8)
+    fail(ST_OP, "attention: GQA group must divide the heads and be at most 8");
   switch (head_dim) {
     case 64:
-      hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(64), 0, st, q, kc, vc, part, out, counters, n_heads, n_kv,
-                         ctx, pos_dev, window, scale, nsplit);
+      attn_decode_hd<64>(grid, st, q, kc, vc, out, part, n_heads, n_kv, ctx, pos_dev, window, scale, nsplit);
       break;
     case 128:
-      hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(64), 0, st, q, kc, vc, part, out, counters, n_heads,
-                         n_kv, ctx, pos_dev, window, scale, nsplit);
+      attn_decode_hd<128>(grid, st, q, kc, vc, out, part, n_heads, n_kv, ctx, pos_dev, window, scale, nsplit);
       break;
     case 256:
-      hipLaunchKernelGGL(attn_decode_kernel<256>, grid, dim3(64), 0, st, q, kc, vc, part, out, counters, n_heads,
-                         n_kv, ctx, pos_dev, window, scale, nsplit);
+      attn_decode_hd<256>(grid, st, q, kc, vc, out, part, n_heads, n_kv, ctx, pos_dev, window, scale, nsplit);
       break;
     default:
       fail(ST_OP, "attention: head_dim must be 64, 128 or 256");

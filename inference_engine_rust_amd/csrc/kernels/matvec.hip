@@ -11,6 +11,9 @@
 //  4. a wave butterfly leaves the R row sums in every lane; lanes 0..R-1 run the epilogue
 //     (store, residual add, SwiGLU pair, RoPE + fp16 KV append, or logits + argmax).
 // Weights are streamed exactly once per token as 16-byte coalesced loads; x never leaves LDS.
+#include <algorithm>
+#include <cstdlib>
+
 #include "common.cuh"
 #include "mv_args.h"
 
@@ -58,39 +61,112 @@ IEK_DEV float rms_of(float sum_sq, int dim, float eps) {
 #pragma clang fp contract(off)
   return sqrtf(sum_sq / (float)dim + eps);
 }
-IEK_DEV float norm_scale(float x, float w, float rms) {
+IEK_DEV float mul_rn(float x, float w) {
 #pragma clang fp contract(off)
-  return (x * w) / rms;
+  return x * w;
+}
+IEK_DEV float div_rn(float x, float y) {
+#pragma clang fp contract(off)
+  return x / y;
 }
 
 // ---- prologue: x (optionally RMS-normalised) into LDS ----------------------------------------
-IEK_DEV void stage_x(const MvArgs& a, float* xs) {
+// x (or x*w, accumulating sum(x^2)) is loaded in batches of 8 float4 per thread with all loads of a
+// batch in flight together; the normalised variant then divides the LDS copy by rms in place, i.e.
+// y = (x*w)/rms with the reference's two roundings. The epilogue's inputs (residual vector, this
+// position's RoPE cos/sin) are staged here too, so the main loop never waits on a global load.
+struct Lds {
+  float* x;     // K
+  float* res;   // N (EPI_RESID)
+  float* rope;  // 2*npairs (EPI_QKV)
+};
+
+IEK_DEV void stage(const MvArgs& a, const Lds& L, int pos) {
   const int K = a.K, tid = threadIdx.x;
+  const bool vec = (K & 3) == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
+                   (!a.norm_w || (reinterpret_cast<uintptr_t>(a.norm_w) & 15) == 0);
+  const int K4 = vec ? K >> 2 : 0;
+  const float4* x4 = reinterpret_cast<const float4*>(a.x);
+  const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
+  float4* s4 = reinterpret_cast<float4*>(L.x);
+  constexpr int B = 8;
+  float ss = 0.f;
+  for (int base = tid; base < K4; base += 256 * B) {
+    float4 v[B], w[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) v[b] = x4[min(base + 256 * b, K4 - 1)];
+    if (a.norm_w) {
+#pragma unroll
+      for (int b = 0; b < B; ++b) w[b] = w4[min(base + 256 * b, K4 - 1)];
+    }
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const int i = base + 256 * b;
+      if (i < K4) {
+        if (a.norm_w) {
+          ss += (v[b].x * v[b].x + v[b].y * v[b].y) + (v[b].z * v[b].z + v[b].w * v[b].w);
+          s4[i] = make_float4(mul_rn(v[b].x, w[b].x), mul_rn(v[b].y, w[b].y), mul_rn(v[b].z, w[b].z),
+                              mul_rn(v[b].w, w[b].w));
+        } else {
+          s4[i] = v[b];
+        }
+      }
+    }
+  }
+  for (int i = 4 * K4 + tid; i < K; i += 256) {
+    const float v = a.x[i];
+    if (a.norm_w) {
+      ss += v * v;
+      L.x[i] = mul_rn(v, a.norm_w[i]);
+    } else {
+      L.x[i] = v;
+    }
+  }
+  if (a.epi == EPI_RESID) {
+    const int N = a.n[0];
+    for (int i = tid; i < N; i += 256) L.res[i] = a.resid[i];
+  }
+  if (a.epi == EPI_QKV) {
+    for (int i = tid; i < 2 * a.npairs; i += 256) L.rope[i] = a.rope_cs[(size_t)pos * a.npairs * 2 + i];
+  }
   if (a.norm_w) {
     __shared__ float red[4];
-    float ss = 0.f;
-    for (int i = tid; i < K; i += 256) {
-      float v = a.x[i];
-      ss += v * v;
-    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, WAVE);
     if ((tid & 63) == 0) red[tid >> 6] = ss;
     __syncthreads();
-    float tot = (red[0] + red[1]) + (red[2] + red[3]);
-    const float rms = rms_of(tot, K, a.eps);
-    for (int i = tid; i < K; i += 256) xs[i] = norm_scale(a.x[i], a.norm_w[i], rms);
-  } else {
-    for (int i = tid; i < K; i += 256) xs[i] = a.x[i];
+    const float rms = rms_of((red[0] + red[1]) + (red[2] + red[3]), K, a.eps);
+    for (int i = tid; i < K; i += 256) L.x[i] = div_rn(L.x[i], rms);
   }
   __syncthreads();
+  // Clamped loads whose values went unused (lanes past K) are still counted as pending; retire
+  // them here, where nothing else is in flight, so the main loop's first wait is not a full drain.
+  __builtin_amdgcn_s_waitcnt(0);
 }
 
+IEK_DEV size_t lds_floats(const MvArgs& a) {
+  return (size_t)a.K + (a.epi == EPI_RESID ? (size_t)a.n[0] : 0) + (a.epi == EPI_QKV ? 2 * (size_t)a.npairs : 0);
+}
+
+IEK_DEV Lds lds_layout(const MvArgs& a, float* base) {
+  Lds L;
+  L.x = base;
+  L.res = base + a.K;
+  L.rope = base + a.K + (a.epi == EPI_RESID ? a.n[0] : 0);
+  return L;
+}
+
+// Segment fields picked with constant indices: a dynamic index into the by-value argument block
+// becomes a vector memory load, whose wait would also drain the in-flight weight prefetch.
+IEK_DEV const uint8_t* seg_w(const MvArgs& a, int s) { return s == 0 ? a.w[0] : (s == 1 ? a.w[1] : a.w[2]); }
+IEK_DEV float* seg_out(const MvArgs& a, int s) { return s == 0 ? a.out[0] : (s == 1 ? a.out[1] : a.out[2]); }
+IEK_DEV int seg_base(const MvArgs& a, int s) { return s == 0 ? a.seg_start[0] : (s == 1 ? a.seg_start[1] : a.seg_start[2]); }
+
 // ---- epilogue -----------------------------------------------------------------------------------
+// Reads only registers and LDS (pos was loaded at kernel start).
 template <int R>
-IEK_DEV void epilogue(const MvArgs& a, int s, int lr0, float (&acc)[R], const float* acc_up, int lane) {
-  // The position counter is read by earlier launches of the step only, never by this one.
-  if (a.pos_inc && blockIdx.x == 0 && threadIdx.x == 0) *a.pos_inc += 1;
+IEK_DEV void epilogue(const MvArgs& a, const Lds& L, int s, int lr0, float (&acc)[R], const float* acc_up, int lane,
+                      int pos) {
   if (a.epi == EPI_SWIGLU) {
     if (lane < R) {
       float g = acc[0], u = acc_up[0];
@@ -116,12 +192,7 @@ IEK_DEV void epilogue(const MvArgs& a, int s, int lr0, float (&acc)[R], const fl
       }
       const int hd = a.head_dim;
       const int d = n % hd;
-      const int pos = *a.pos;
-      if (s < 2 && d < 2 * a.npairs) {
-        const float* e = a.rope_cs + ((size_t)pos * a.npairs + (d >> 1)) * 2;
-        const float c = e[0], sn = e[1];
-        v = rope_rotate(v, partner, c, sn, (d & 1) == 0);
-      }
+      if (s < 2 && d < 2 * a.npairs) v = rope_rotate(v, partner, L.rope[d & ~1], L.rope[(d & ~1) + 1], (d & 1) == 0);
       if (s == 0) {
         a.out[0][n] = v;
       } else {
@@ -159,8 +230,8 @@ IEK_DEV void epilogue(const MvArgs& a, int s, int lr0, float (&acc)[R], const fl
     for (int r = 1; r < R; ++r)
       if (lane == r) v = acc[r];
     const int n = lr0 + lane;
-    if (a.epi == EPI_RESID) v = a.resid[n] + v;
-    a.out[s][n] = v;
+    if (a.epi == EPI_RESID) v = L.res[n] + v;
+    seg_out(a, s)[n] = v;
   }
 }
 
@@ -171,98 +242,51 @@ IEK_DEV void wave_reduce(float (&acc)[R]) {
 }
 
 // ---- Q4_K -----------------------------------------------------------------------------------
-// Chunk j (0..7) of a superblock = qs bytes [16j, 16j+16): 16 low nibbles of sub-block 2g and 16
-// high nibbles of sub-block 2g+1 (g = j/2), i.e. elements 64g+16h+t and 64g+32+16h+t, h = j&1.
-IEK_DEV float q4k_dot(uint4 hdr, uint4 qv, int j, const float4* xl4, const float4* xh4, float xsl, float xsh) {
-  const int g = j >> 1;
-  float d = half_bits_to_float(hdr.x), dmin = half_bits_to_float(hdr.x >> 16);
-  float sc0, m0, sc1, m1;
-  scale_min_k4(2 * g, hdr.y, hdr.z, hdr.w, &sc0, &m0);
-  scale_min_k4(2 * g + 1, hdr.y, hdr.z, hdr.w, &sc1, &m1);
-  const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
-  float sl = 0.f, sh = 0.f;
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const uint32_t lo = qw[t] & 0x0F0F0F0Fu, hi = (qw[t] >> 4) & 0x0F0F0F0Fu;
-    const float4 a = xl4[t], b = xh4[t];
-    sl += a.x * ubyte_f<0>(lo) + a.y * ubyte_f<1>(lo) + a.z * ubyte_f<2>(lo) + a.w * ubyte_f<3>(lo);
-    sh += b.x * ubyte_f<0>(hi) + b.y * ubyte_f<1>(hi) + b.z * ubyte_f<2>(hi) + b.w * ubyte_f<3>(hi);
-  }
-  return (d * sc0) * sl - (dmin * m0) * xsl + (d * sc1) * sh - (dmin * m1) * xsh;
+// Chunk g (0..3) of a superblock = qs bytes [32g, 32g+32): 32 low nibbles (sub-block 2g, elements
+// 64g+l) and 32 high nibbles (sub-block 2g+1, elements 64g+32+l). The nibbles go straight into
+// v_fma_mix_f32 as f16 operands: (w >> s) & 0x000F000F leaves two nibbles in the two halves of a
+// register, each the f16 subnormal q * 2^-24, which the instruction widens exactly; the 2^24 is
+// folded into the sub-block scale.
+IEK_DEV float h_lo(uint32_t w) { return __half2float(__ushort_as_half((unsigned short)(w & 0xFFFFu))); }
+IEK_DEV float h_hi(uint32_t w) { return __half2float(__ushort_as_half((unsigned short)(w >> 16))); }
+
+// sum over one qs dword (bytes l..l+3): lo nibbles against xl[0..3], hi nibbles against xh[0..3]
+IEK_DEV void q4_dword(uint32_t w, const float4 xl, const float4 xh, float& sl, float& sh) {
+  const uint32_t t0 = w & 0x000F000Fu, t1 = (w >> 4) & 0x000F000Fu;
+  const uint32_t t2 = (w >> 8) & 0x000F000Fu, t3 = (w >> 12) & 0x000F000Fu;
+  sl = fmaf(xl.x, h_lo(t0), sl);
+  sl = fmaf(xl.z, h_hi(t0), sl);
+  sh = fmaf(xh.x, h_lo(t1), sh);
+  sh = fmaf(xh.z, h_hi(t1), sh);
+  sl = fmaf(xl.y, h_lo(t2), sl);
+  sl = fmaf(xl.w, h_hi(t2), sl);
+  sh = fmaf(xh.y, h_lo(t3), sh);
+  sh = fmaf(xh.w, h_hi(t3), sh);
 }
 
-template <int R, bool DUAL>
-__global__ __launch_bounds__(256) void mv_q4k(MvArgs a) {
-  extern __shared__ float xs[];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int row0 = (blockIdx.x * 4 + wave) * R;
-  const int total = a.seg_start[a.nseg];
-  const bool active = row0 < total;
-  const int s = active ? seg_of(a, row0) : 0;
-  const int lr0 = row0 - a.seg_start[s];
-  const int K = a.K;
-  const size_t rb = (size_t)(K / QK_K) * Q4K_BYTES;
-  const int nchunk = (K / QK_K) * 8;
-  const uint8_t* W0 = a.w[s] + (size_t)lr0 * rb;
-  const uint8_t* W1 = DUAL ? a.w[1] + (size_t)lr0 * rb : nullptr;
-  constexpr int NR = DUAL ? 2 * R : R;
-  auto rowp = [&](int r) { return r < R ? W0 + (size_t)r * rb : W1 + (size_t)(r - R) * rb; };
+// get_scale_min_k4 for a per-lane sub-block index without branches (both forms are extracted and
+// selected), so every lane of the wave runs one path and every loaded header dword is consumed.
+IEK_DEV void scale_min_k4_sel(int j, uint32_t s0, uint32_t s1, uint32_t s2, float* sc, float* m) {
+  const int i = j & 3;
+  const uint32_t b0 = byte_of(s0, i), b1 = byte_of(s1, i), b2 = byte_of(s2, i);
+  const uint32_t sc_lo = b0 & 63u, m_lo = b1 & 63u;
+  const uint32_t sc_hi = (b2 & 0xFu) | ((b0 >> 6) << 4), m_hi = (b2 >> 4) | ((b1 >> 6) << 4);
+  *sc = (float)(j < 4 ? sc_lo : sc_hi);
+  *m = (float)(j < 4 ? m_lo : m_hi);
+}
 
-  uint4 hdr[NR], qv[NR];
-  int c = lane;
-  if (active && c < nchunk) {
+IEK_DEV float q4k_dot(uint4 hdr, uint4 q0, uint4 q1, int g, const float4* xl4, const float4* xh4, float xsl,
+                      float xsh) {
+  float d = half_bits_to_float(hdr.x), dmin = half_bits_to_float(hdr.x >> 16);
+  float sc0, m0, sc1, m1;
+  scale_min_k4_sel(2 * g, hdr.y, hdr.z, hdr.w, &sc0, &m0);
+  scale_min_k4_sel(2 * g + 1, hdr.y, hdr.z, hdr.w, &sc1, &m1);
+  const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+  float sl = 0.f, sh = 0.f;
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      const uint8_t* blk = rowp(r) + (size_t)(c >> 3) * Q4K_BYTES;
-      hdr[r] = *reinterpret_cast<const uint4*>(blk);
-      qv[r] = *reinterpret_cast<const uint4*>(blk + 16 + 16 * (c & 7));
-    }
-  }
-  stage_x(a, xs);
-  if (!active) return;
-
-  float acc[NR];
-#pragma unroll
-  for (int r = 0; r < NR; ++r) acc[r] = 0.f;
-  for (; c < nchunk; c += WAVE) {
-    const int cn = c + WAVE;
-    uint4 hdr_n[NR], qv_n[NR];
-    if (cn < nchunk) {
-#pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        const uint8_t* blk = rowp(r) + (size_t)(cn >> 3) * Q4K_BYTES;
-        hdr_n[r] = *reinterpret_cast<const uint4*>(blk);
-        qv_n[r] = *reinterpret_cast<const uint4*>(blk + 16 + 16 * (cn & 7));
-      }
-    }
-    const int b = c >> 3, j = c & 7;
-    const int e0 = b * QK_K + (j >> 1) * 64 + (j & 1) * 16;
-    const float4* xl4 = reinterpret_cast<const float4*>(xs + e0);
-    const float4* xh4 = reinterpret_cast<const float4*>(xs + e0 + 32);
-    float xsl = 0.f, xsh = 0.f;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const float4 u = xl4[t], v = xh4[t];
-      xsl += (u.x + u.y) + (u.z + u.w);
-      xsh += (v.x + v.y) + (v.z + v.w);
-    }
-#pragma unroll
-    for (int r = 0; r < NR; ++r) acc[r] += q4k_dot(hdr[r], qv[r], j, xl4, xh4, xsl, xsh);
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      hdr[r] = hdr_n[r];
-      qv[r] = qv_n[r];
-    }
-  }
-  float accg[R], accu[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    accg[r] = acc[r];
-    accu[r] = DUAL ? acc[R + r] : 0.f;
-  }
-  wave_reduce<R>(accg);
-  if (DUAL) wave_reduce<R>(accu);
-  epilogue<R>(a, s, lr0, accg, accu, lane);
+  for (int t = 0; t < 8; ++t) q4_dword(qw[t], xl4[t], xh4[t], sl, sh);
+  const float k24 = 16777216.0f;  // 2^24
+  return (d * sc0 * k24) * sl - (dmin * m0) * xsl + (d * sc1 * k24) * sh - (dmin * m1) * xsh;
 }
 
 // ---- Q6_K -----------------------------------------------------------------------------------
@@ -282,7 +306,7 @@ IEK_DEV void load_tri(const uint8_t* p, uint32_t (&o)[3], uint32_t* shift) {
   *shift = (uint32_t)(ap & 3u);
   o[0] = base[0];
   o[1] = base[1];
-  o[2] = *shift ? base[2] : 0u;
+  o[2] = base[*shift ? 2 : 1];  // always issued; with shift 0 the third dword is not used
 }
 
 IEK_DEV void q6_load(const uint8_t* blk, int h, int o8, Q6Raw& q) {
@@ -297,7 +321,7 @@ IEK_DEV void q6_load(const uint8_t* blk, int h, int o8, Q6Raw& q) {
   q.sh_s = (uint32_t)(ap & 3u);
   q.s[0] = base[0];
   q.s[1] = base[1];
-  q.s[2] = q.sh_s >= 2 ? base[2] : 0u;
+  q.s[2] = base[q.sh_s >= 2 ? 2 : 1];  // always issued; unused bytes are never extracted
   q.d = *reinterpret_cast<const uint16_t*>(blk + 208);
 }
 
@@ -311,6 +335,8 @@ IEK_DEV float q6k_dot(const Q6Raw& q, const float4* x4, const float (&xs4)[4]) {
   const float sc[4] = {(float)(int8_t)(S0 & 0xFF), (float)(int8_t)((S0 >> 16) & 0xFF), (float)(int8_t)(S1 & 0xFF),
                        (float)(int8_t)((S1 >> 16) & 0xFF)};
   const float d = half_bits_to_float(q.d);
+  // 6-bit values (q + 32) are assembled per byte, split into register halves and fed to
+  // v_fma_mix_f32 as exact f16 subnormals (value * 2^-24).
   float s[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
@@ -321,52 +347,72 @@ IEK_DEV float q6k_dot(const Q6Raw& q, const float4* x4, const float (&xs4)[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float4 xv = x4[2 * i + t];
-      s[i] += xv.x * ubyte_f<0>(qq[i]) + xv.y * ubyte_f<1>(qq[i]) + xv.z * ubyte_f<2>(qq[i]) +
-              xv.w * ubyte_f<3>(qq[i]);
+      const uint32_t e = qq[i] & 0x00FF00FFu, o = (qq[i] >> 8) & 0x00FF00FFu;
+      s[i] = fmaf(xv.x, h_lo(e), s[i]);
+      s[i] = fmaf(xv.z, h_hi(e), s[i]);
+      s[i] = fmaf(xv.y, h_lo(o), s[i]);
+      s[i] = fmaf(xv.w, h_hi(o), s[i]);
     }
   }
   float r = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) r += (d * sc[i]) * (s[i] - 32.0f * xs4[i]);
+  for (int i = 0; i < 4; ++i) r += (d * sc[i]) * (16777216.0f * s[i] - 32.0f * xs4[i]);
   return r;
 }
 
-template <int R, bool DUAL>
-__global__ __launch_bounds__(256) void mv_q6k(MvArgs a) {
-  extern __shared__ float xs[];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int row0 = (blockIdx.x * 4 + wave) * R;
-  const int total = a.seg_start[a.nseg];
-  const bool active = row0 < total;
-  const int s = active ? seg_of(a, row0) : 0;
-  const int lr0 = row0 - a.seg_start[s];
-  const int K = a.K;
-  const size_t rb = (size_t)(K / QK_K) * Q6K_BYTES;
-  const int nchunk = (K / QK_K) * 8;
-  const uint8_t* W0 = a.w[s] + (size_t)lr0 * rb;
-  const uint8_t* W1 = DUAL ? a.w[1] + (size_t)lr0 * rb : nullptr;
-  constexpr int NR = DUAL ? 2 * R : R;
-  auto rowp = [&](int r) { return r < R ? W0 + (size_t)r * rb : W1 + (size_t)(r - R) * rb; };
-
-  Q6Raw q[NR];
-  int c = lane;
-  if (active && c < nchunk) {
+// ---- streaming driver ------------------------------------------------------------------------
+// Wave w of workgroup b owns row groups (4b + w) + k * (4 * gridDim.x). It walks the flattened
+// (group, pass) sequence with two register buffers used alternately (no copies of in-flight data),
+// issuing the next step's weight loads before computing the current one. Loads are unconditional
+// with clamped addresses so the compiler can count them statically and keep them all in flight.
+struct Q4Tr {
+  static constexpr int CHUNKS = 4;  // 64-value chunks per superblock
+  static constexpr int BYTES = Q4K_BYTES;
+  template <int NR>
+  struct Buf {
+    uint4 hdr[NR], qa[NR], qb[NR];
+  };
+  template <int NR>
+  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c) {
 #pragma unroll
-    for (int r = 0; r < NR; ++r) q6_load(rowp(r) + (size_t)(c >> 3) * Q6K_BYTES, (c >> 2) & 1, c & 3, q[r]);
-  }
-  stage_x(a, xs);
-  if (!active) return;
-
-  float acc[NR];
-#pragma unroll
-  for (int r = 0; r < NR; ++r) acc[r] = 0.f;
-  for (; c < nchunk; c += WAVE) {
-    const int cn = c + WAVE;
-    Q6Raw qn[NR];
-    if (cn < nchunk) {
-#pragma unroll
-      for (int r = 0; r < NR; ++r) q6_load(rowp(r) + (size_t)(cn >> 3) * Q6K_BYTES, (cn >> 2) & 1, cn & 3, qn[r]);
+    for (int r = 0; r < NR; ++r) {
+      const uint8_t* blk = rows[r] + (size_t)(c >> 2) * Q4K_BYTES;
+      b.hdr[r] = *reinterpret_cast<const uint4*>(blk);
+      b.qa[r] = *reinterpret_cast<const uint4*>(blk + 16 + 32 * (c & 3));
+      b.qb[r] = *reinterpret_cast<const uint4*>(blk + 32 + 32 * (c & 3));
     }
+  }
+  template <int NR>
+  IEK_DEV static void compute(const Buf<NR>& b, int c, const float* xs, float (&acc)[NR]) {
+    const int e0 = (c >> 2) * QK_K + (c & 3) * 64;
+    float4 xl4[8], xh4[8];
+    float xsl = 0.f, xsh = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      xl4[t] = *reinterpret_cast<const float4*>(xs + e0 + 4 * t);
+      xh4[t] = *reinterpret_cast<const float4*>(xs + e0 + 32 + 4 * t);
+      xsl += (xl4[t].x + xl4[t].y) + (xl4[t].z + xl4[t].w);
+      xsh += (xh4[t].x + xh4[t].y) + (xh4[t].z + xh4[t].w);
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc[r] += q4k_dot(b.hdr[r], b.qa[r], b.qb[r], c & 3, xl4, xh4, xsl, xsh);
+  }
+};
+
+struct Q6Tr {
+  static constexpr int CHUNKS = 8;  // 32-value chunks per superblock
+  static constexpr int BYTES = Q6K_BYTES;
+  template <int NR>
+  struct Buf {
+    Q6Raw q[NR];
+  };
+  template <int NR>
+  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c) {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) q6_load(rows[r] + (size_t)(c >> 3) * Q6K_BYTES, (c >> 2) & 1, c & 3, b.q[r]);
+  }
+  template <int NR>
+  IEK_DEV static void compute(const Buf<NR>& b, int c, const float* xs, float (&acc)[NR]) {
     const int e0 = (c >> 3) * QK_K + 128 * ((c >> 2) & 1) + 8 * (c & 3);
     float4 x4[8];
     float xs4[4];
@@ -378,27 +424,115 @@ __global__ __launch_bounds__(256) void mv_q6k(MvArgs a) {
       xs4[i] = ((u.x + u.y) + (u.z + u.w)) + ((v.x + v.y) + (v.z + v.w));
     }
 #pragma unroll
-    for (int r = 0; r < NR; ++r) acc[r] += q6k_dot(q[r], x4, xs4);
-#pragma unroll
-    for (int r = 0; r < NR; ++r) q[r] = qn[r];
+    for (int r = 0; r < NR; ++r) acc[r] += q6k_dot(b.q[r], x4, xs4);
   }
-  float accg[R], accu[R];
+};
+
+template <class Tr, int R, bool DUAL>
+__global__ __launch_bounds__(256) void mv_stream(MvArgs a) {
+  extern __shared__ __align__(16) float lds[];
+  const Lds L = lds_layout(a, lds);
+  constexpr int NR = DUAL ? 2 * R : R;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int pos = a.epi == EPI_QKV ? __builtin_amdgcn_readfirstlane(*a.pos) : 0;
+  const int total = a.nseg == 1 ? a.seg_start[1] : (a.nseg == 2 ? a.seg_start[2] : a.seg_start[3]);
+  const int groups = total / R;
+  const int stride = gridDim.x * 4;
+  const int g0 = blockIdx.x * 4 + wave;
+  const size_t rb = (size_t)(a.K / QK_K) * Tr::BYTES;
+  const int nchunk = (a.K / QK_K) * Tr::CHUNKS;
+  const int npass = (nchunk + WAVE - 1) / WAVE;
+  // number of (group, pass) steps of this wave
+  const int my_groups = g0 < groups ? (groups - 1 - g0) / stride + 1 : 0;
+  const int steps = my_groups * npass;
+
+  auto rows_of = [&](int it, const uint8_t* (&rows)[NR], int& c) {
+    const int k = min(it, steps - 1);
+    const int g = g0 + (k / npass) * stride, p = k % npass;
+    c = min(lane + WAVE * p, nchunk - 1);
+    const int row0 = g * R;
+    const int s = DUAL ? 0 : seg_of(a, row0);
+    const int lr0 = row0 - seg_base(a, s);
+    const uint8_t* w0 = seg_w(a, s);
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    accg[r] = acc[r];
-    accu[r] = DUAL ? acc[R + r] : 0.f;
+    for (int r = 0; r < NR; ++r) rows[r] = r < R ? w0 + (size_t)(lr0 + r) * rb : a.w[1] + (size_t)(lr0 + r - R) * rb;
+  };
+  typename Tr::template Buf<NR> A, B;
+  float acc[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) acc[r] = 0.f;
+
+  auto finish = [&](int it) {
+    const int p = it % npass;
+    if (p != npass - 1) return;
+    const int g = g0 + (it / npass) * stride;
+    float accg[R], accu[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      accg[r] = acc[r];
+      accu[r] = DUAL ? acc[R + r] : 0.f;
+    }
+    wave_reduce<R>(accg);
+    if (DUAL) wave_reduce<R>(accu);
+    const int row0 = g * R;
+    const int s = DUAL ? 0 : seg_of(a, row0);
+    epilogue<R>(a, L, s, row0 - seg_base(a, s), accg, accu, lane, pos);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc[r] = 0.f;
+  };
+  auto step = [&](const typename Tr::template Buf<NR>& buf, int it) {
+    const int p = it % npass;
+    const int c = lane + WAVE * p;
+    float part[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) part[r] = 0.f;
+    Tr::template compute<NR>(buf, min(c, nchunk - 1), L.x, part);
+    // The empty asm pins the dot products as computed on every path: otherwise the compiler sinks
+    // them under the c < nchunk branch and a wave whose lanes all skip it leaves the buffer's loads
+    // unretired, which costs a full drain at the next reuse of those registers.
+#pragma unroll
+    for (int r = 0; r < NR; ++r) asm volatile("" : "+v"(part[r]));
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc[r] += c < nchunk ? part[r] : 0.f;
+    finish(it);
+  };
+
+  if (steps > 0) {
+    const uint8_t* rows[NR];
+    int c;
+    rows_of(0, rows, c);
+    Tr::template load<NR>(A, rows, c);
   }
-  wave_reduce<R>(accg);
-  if (DUAL) wave_reduce<R>(accu);
-  epilogue<R>(a, s, lr0, accg, accu, lane);
+  stage(a, L, pos);
+  for (int it = 0; it < steps; it += 2) {
+    {
+      const uint8_t* rows[NR];
+      int c;
+      rows_of(it + 1, rows, c);
+      Tr::template load<NR>(B, rows, c);
+    }
+    step(A, it);
+    if (it + 1 >= steps) break;
+    {
+      const uint8_t* rows[NR];
+      int c;
+      rows_of(it + 2, rows, c);
+      Tr::template load<NR>(A, rows, c);
+    }
+    step(B, it + 1);
+  }
+  if (a.pos_inc && blockIdx.x == 0 && threadIdx.x == 0) *a.pos_inc += 1;
 }
 
 // ---- generic path: any dtype, any K (blocks may straddle rows when K % block != 0) ----------
 __global__ __launch_bounds__(256) void mv_generic(MvArgs a, int dt) {
-  extern __shared__ float xs[];
+  extern __shared__ __align__(16) float lds[];
+  const Lds L = lds_layout(a, lds);
+  const float* xs = L.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row = blockIdx.x * 4 + wave;
-  stage_x(a, xs);
+  const int pos = a.epi == EPI_QKV ? *a.pos : 0;
+  stage(a, L, pos);
   const int total = a.seg_start[a.nseg];
   if (row >= total) return;
   const int s = seg_of(a, row);
@@ -414,10 +548,40 @@ __global__ __launch_bounds__(256) void mv_generic(MvArgs a, int dt) {
   }
   float acc[1] = {wave_sum(g)};
   float accu[1] = {dual ? wave_sum(u) : 0.f};
-  epilogue<1>(a, s, n, acc, accu, lane);
+  epilogue<1>(a, L, s, n, acc, accu, lane, pos);
+  if (a.pos_inc && blockIdx.x == 0 && threadIdx.x == 0) *a.pos_inc += 1;
 }
 
 // ---------------------------------------------------------------------------------------------
+static int num_cus() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+  }
+  return n;
+}
+
+// Persistent grid: exactly the workgroups that are resident at once (the occupancy the register
+// and LDS use allow, optionally capped by IEK_MV_PER_CU), so no second wave of workgroups forms a
+// tail; every wave then strides over the row groups.
+template <class Tr, bool DUAL>
+static void launch_stream(const MvArgs& a, int groups, size_t lds, hipStream_t st) {
+  static int cap = -1;
+  if (cap < 0) {
+    const char* e = getenv("IEK_MV_PER_CU");
+    cap = e ? std::max(1, atoi(e)) : 8;
+  }
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mv_stream<Tr, 2, DUAL>, 256, lds) != hipSuccess ||
+      per_cu <= 0)
+    per_cu = 1;
+  per_cu = std::min(per_cu, cap);
+  const int blocks = std::max(1, std::min((groups + 3) / 4, num_cus() * per_cu));
+  hipLaunchKernelGGL((mv_stream<Tr, 2, DUAL>), dim3(blocks), dim3(256), lds, st, a);
+}
+
 void launch_mv(int dt, MvArgs a, hipStream_t st) {
   int total = 0;
   for (int i = 0; i < a.nseg; ++i) {
@@ -434,27 +598,24 @@ void launch_mv(int dt, MvArgs a, hipStream_t st) {
   }
   bool fast = (dt == DT_Q4K || dt == DT_Q6K) && a.K % QK_K == 0 && (reinterpret_cast<uintptr_t>(a.x) % 16) == 0;
   for (int i = 0; i < (dual ? 2 : a.nseg); ++i) fast = fast && (reinterpret_cast<uintptr_t>(a.w[i]) % 16) == 0;
-  const size_t lds = (size_t)a.K * sizeof(float);
+  const size_t lds = ((size_t)a.K + (a.epi == EPI_RESID ? (size_t)a.n[0] : 0) +
+                      (a.epi == EPI_QKV ? 2 * (size_t)a.npairs : 0)) * sizeof(float);
   if (lds > 160 * 1024) fail(ST_OP, "matvec: K too large for the LDS-staged input");
   if (fast) {
-    int R = dual ? 2 : (total >= 16384 ? 4 : 2);
+    // Two rows per wave: more rows per wave spill the prefetch registers.
+    const int R = 2;
     bool ok = true;
-    for (int i = 0; i < a.nseg; ++i) ok = ok && a.n[i] % R == 0;
-    if (!ok) R = 2;
-    ok = true;
     for (int i = 0; i < a.nseg; ++i) ok = ok && a.n[i] % R == 0;
     if (!ok) fast = false;
     if (fast) {
-      const int blocks = (total + 4 * R - 1) / (4 * R);
-#define IEK_L(KER, RR, DD) hipLaunchKernelGGL((KER<RR, DD>), dim3(blocks), dim3(256), lds, st, a)
+      const int groups = total / R;
+#define IEK_L(TR, DD) launch_stream<TR, DD>(a, groups, lds, st)
       if (dt == DT_Q4K) {
-        if (dual) IEK_L(mv_q4k, 2, true);
-        else if (R == 4) IEK_L(mv_q4k, 4, false);
-        else IEK_L(mv_q4k, 2, false);
+        if (dual) IEK_L(Q4Tr, true);
+        else IEK_L(Q4Tr, false);
       } else {
-        if (dual) IEK_L(mv_q6k, 2, true);
-        else if (R == 4) IEK_L(mv_q6k, 4, false);
-        else IEK_L(mv_q6k, 2, false);
+        if (dual) IEK_L(Q6Tr, true);
+        else IEK_L(Q6Tr, false);
       }
 #undef IEK_L
       return;

@@ -167,3 +167,23 @@ def test_mistral_width_two_layers_parity(gpu, mid_path):
         s.decode_token(t)
         r.decode(t)
     assert worst < LOGIT_REL_L2, worst
+
+
+def test_qk_unpack_path_matches_oracle(gpu, c0_path, monkeypatch):
+    """INFERENCE_ENGINE_GGUF_QK_UNPACK=1 forces the Llama Q/K un-permute (model_config.rs:209-224)
+    on both sides; the device then runs its unfused decode path."""
+    monkeypatch.setenv("INFERENCE_ENGINE_GGUF_QK_UNPACK", "1")
+    m = E.LoadedModel.load(c0_path)
+    om = O.Model(c0_path)
+    assert m.config.unpack_llama_gguf_qk == 1 and om.cfg.unpack_qk == 1
+    prompt = synth.prompt_ids(5, 10)
+    s, r = E.InferenceSession(m), O.Session(om)
+    s.prefill(prompt)
+    r.prefill(prompt)
+    for step in range(6):
+        lg, lr = s.logits_last_token(), r.logits()
+        assert rel_l2(lg, lr) < LOGIT_REL_L2
+        t = O.argmax(lr)
+        assert E.greedy_next_token(s) == t, f"step {step}"
+        s.decode_token(t)
+        r.decode(t)
