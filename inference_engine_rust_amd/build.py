@@ -31,6 +31,7 @@ SOURCES = [
     "kernels/ops.hip",
     "kernels/attention.hip",
     "kernels/gemm.hip",
+    "kernels/gemm_mfma.hip",
     "model.cpp",
     "session.cpp",
     "api.cpp",

@@ -39,6 +39,11 @@ struct MvSegDesc {
 void launch_matvec(int dt, const MvSegDesc* segs, int nseg, const float* x, int K, int epi, hipStream_t st);
 void launch_gemm(int dt, const void* w, const float* a, int M, int K, int N, float* out, const float* resid,
                  hipStream_t st);
+// Matrix-core GEMM on activations pre-split into fp16 pairs (kernels/gemm_mfma.hip).
+void launch_split_f16(const float* x, size_t n, __half* hi, __half* lo, hipStream_t st);
+bool gemm_mfma_ok(int dt, const void* w, int K, int N);
+void launch_gemm_mfma(int dt, const void* w, const __half* xh, const __half* xl, int M, int K, int N, float* out,
+                      const float* resid, hipStream_t st);
 void launch_dequant(int dt, const void* blocks, size_t nblocks, float* out, hipStream_t st);
 void launch_embed(int dt, const void* table, size_t hidden, const uint32_t* ids, int n, float scale, float* out,
                   hipStream_t st);

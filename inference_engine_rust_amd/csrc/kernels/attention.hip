@@ -301,15 +301,186 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(const float* __restric
   }
 }
 
+// Prefill on the matrix cores (v_mfma_f32_16x16x32_f16): one 256-thread workgroup per (head,
+// 64-query tile), each wave owning 16 queries; 64-key blocks of K (row-major) and V (transposed)
+// are staged in LDS as fp16 (hi, lo) pairs, S = Q K^T and O += P V each take three MFMAs per step
+// (hi*hi + hi*lo + lo*hi, products exact in f32), and the softmax is the online form of the SIMT
+// kernel above (running max, rescaled sum).
+typedef _Float16 ah8_t __attribute__((ext_vector_type(8)));
+typedef float af4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t au4_t __attribute__((ext_vector_type(4)));
+
+IEK_DEV uint32_t apack2(_Float16 a, _Float16 b) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+IEK_DEV void asplit(float v, _Float16& h, _Float16& l) {
+#pragma clang fp contract(off)
+  h = (_Float16)v;
+  l = (_Float16)(v - (float)h);
+}
+
+IEK_DEV af4_t mma3(au4_t ah, au4_t al, au4_t bh, au4_t bl, af4_t c) {
+  const ah8_t a_h = __builtin_bit_cast(ah8_t, ah), a_l = __builtin_bit_cast(ah8_t, al);
+  const ah8_t b_h = __builtin_bit_cast(ah8_t, bh), b_l = __builtin_bit_cast(ah8_t, bl);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_h, b_h, c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_h, b_l, c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_l, b_h, c, 0, 0, 0);
+  return c;
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                                const float* __restrict__ v, float* __restrict__ out,
+                                                                int M, int n_heads, int n_kv, int window, float scale) {
+  constexpr int KB = 64;         // keys per block
+  constexpr int KS = HD / 32;    // MFMA K steps of S = Q K^T
+  constexpr int NS = HD / 16;    // 16-wide head-dim subtiles of O
+  constexpr int KROW = HD + 8;   // padded LDS rows (halves)
+  constexpr int VROW = KB + 8;
+  __shared__ __align__(16) _Float16 kh[KB][KROW];
+  __shared__ __align__(16) _Float16 kl[KB][KROW];
+  __shared__ __align__(16) _Float16 vth[HD][VROW];
+  __shared__ __align__(16) _Float16 vtl[HD][VROW];
+  __shared__ __align__(16) _Float16 ph[4][16][VROW];
+  __shared__ __align__(16) _Float16 pl[4][16][VROW];
+
+  const int h = blockIdx.x, qt = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = n_heads / n_kv, kvh = h / G;
+  const int qd = n_heads * HD, kvd = n_kv * HD;
+  const int q0 = qt * 64 + 16 * wave;
+  const int fr = lane & 15, fk = 8 * (lane >> 4);
+
+  // Q fragments (A operand): row q0 + fr, dims 32 s + fk .. +7, split into fp16 pairs
+  au4_t qah[KS], qal[KS];
+  {
+    const float* qrow = q + (size_t)min(q0 + fr, M - 1) * qd + h * HD;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const float4 a = *reinterpret_cast<const float4*>(qrow + 32 * s + fk);
+      const float4 b = *reinterpret_cast<const float4*>(qrow + 32 * s + fk + 4);
+      const float vv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      _Float16 hh[8], ll[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) asplit(vv[t], hh[t], ll[t]);
+      qah[s] = au4_t{apack2(hh[0], hh[1]), apack2(hh[2], hh[3]), apack2(hh[4], hh[5]), apack2(hh[6], hh[7])};
+      qal[s] = au4_t{apack2(ll[0], ll[1]), apack2(ll[2], ll[3]), apack2(ll[4], ll[5]), apack2(ll[6], ll[7])};
+    }
+  }
+  af4_t o[NS];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) o[j] = af4_t{0.f, 0.f, 0.f, 0.f};
+  float mrow[4], lrow[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    mrow[r] = -INFINITY;
+    lrow[r] = 0.f;
+  }
+  const int last_q = min(M - 1, qt * 64 + 63);
+  const int jmin_tile = window > 0 ? max(0, qt * 64 - (window - 1)) : 0;
+  for (int kb0 = (jmin_tile / KB) * KB; kb0 <= last_q; kb0 += KB) {
+    __syncthreads();  // the previous block's LDS reads are done
+    for (int e = tid; e < KB * HD / 4; e += 256) {
+      const int j = e / (HD / 4), d4 = 4 * (e % (HD / 4));
+      const size_t row = (size_t)min(kb0 + j, M - 1) * kvd + kvh * HD + d4;
+      const float4 kk = *reinterpret_cast<const float4*>(k + row);
+      const float4 vv = *reinterpret_cast<const float4*>(v + row);
+      const float kf[4] = {kk.x, kk.y, kk.z, kk.w}, vf[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        asplit(kf[t], kh[j][d4 + t], kl[j][d4 + t]);
+        asplit(vf[t], vth[d4 + t][j], vtl[d4 + t][j]);
+      }
+    }
+    __syncthreads();
+    if (kb0 > q0 + 15) continue;  // every query of this wave precedes the block
+    // S = Q K^T for the wave's 16 queries x 64 keys
+    af4_t sacc[4];
+#pragma unroll
+    for (int jn = 0; jn < 4; ++jn) {
+      sacc[jn] = af4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const au4_t bh = *reinterpret_cast<const au4_t*>(&kh[16 * jn + fr][32 * s + fk]);
+        const au4_t bl = *reinterpret_cast<const au4_t*>(&kl[16 * jn + fr][32 * s + fk]);
+        sacc[jn] = mma3(qah[s], qal[s], bh, bl, sacc[jn]);
+      }
+    }
+    // mask, scale, online softmax; lane holds rows 4 * (lane >> 4) + r, key column 16 jn + fr
+    float p[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = q0 + 4 * (lane >> 4) + r;
+      const int jlo = window > 0 ? max(0, i - (window - 1)) : 0;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int jn = 0; jn < 4; ++jn) {
+        const int j = kb0 + 16 * jn + fr;
+        const bool ok = j <= i && j >= jlo && j < M && i < M;
+        const float sv = sacc[jn][r] * scale;
+        p[jn][r] = ok ? sv : -INFINITY;
+        mx = fmaxf(mx, p[jn][r]);
+      }
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      const float mn = fmaxf(mrow[r], mx);
+      const float corr = mn == -INFINITY ? 1.f : expf(mrow[r] - mn);
+      float sum = 0.f;
+#pragma unroll
+      for (int jn = 0; jn < 4; ++jn) {
+        const float e = p[jn][r] == -INFINITY ? 0.f : expf(p[jn][r] - mn);
+        p[jn][r] = e;
+        sum += e;
+      }
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off, 64);
+      lrow[r] = lrow[r] * corr + sum;
+      mrow[r] = mn;
+#pragma unroll
+      for (int j = 0; j < NS; ++j) o[j][r] *= corr;
+    }
+    // P to LDS in A-operand order [query][key] (this wave's slice only)
+#pragma unroll
+    for (int jn = 0; jn < 4; ++jn)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) asplit(p[jn][r], ph[wave][4 * (lane >> 4) + r][16 * jn + fr], pl[wave][4 * (lane >> 4) + r][16 * jn + fr]);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // O += P V
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const au4_t pah = *reinterpret_cast<const au4_t*>(&ph[wave][fr][32 * ks + fk]);
+      const au4_t pal = *reinterpret_cast<const au4_t*>(&pl[wave][fr][32 * ks + fk]);
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        const au4_t bh = *reinterpret_cast<const au4_t*>(&vth[16 * j + fr][32 * ks + fk]);
+        const au4_t bl = *reinterpret_cast<const au4_t*>(&vtl[16 * j + fr][32 * ks + fk]);
+        o[j] = mma3(pah, pal, bh, bl, o[j]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int i = q0 + 4 * (lane >> 4) + r;
+    if (i < M) {
+#pragma unroll
+      for (int j = 0; j < NS; ++j) out[(size_t)i * qd + h * HD + 16 * j + fr] = o[j][r] / lrow[r];
+    }
+  }
+}
+
 void launch_attn_prefill(const float* q, const float* k, const float* v, float* out, int M, int n_heads, int n_kv,
                          int head_dim, int window, float scale, hipStream_t st) {
   dim3 grid(n_heads, (M + 63) / 64);
   switch (head_dim) {
     case 64:
-      hipLaunchKernelGGL(attn_prefill_kernel<64>, grid, dim3(64), 0, st, q, k, v, out, M, n_heads, n_kv, window, scale);
+      hipLaunchKernelGGL(attn_prefill_mfma_kernel<64>, grid, dim3(256), 0, st, q, k, v, out, M, n_heads, n_kv, window,
+                         scale);
       break;
     case 128:
-      hipLaunchKernelGGL(attn_prefill_kernel<128>, grid, dim3(64), 0, st, q, k, v, out, M, n_heads, n_kv, window,
+      hipLaunchKernelGGL(attn_prefill_mfma_kernel<128>, grid, dim3(256), 0, st, q, k, v, out, M, n_heads, n_kv, window,
                          scale);
       break;
     default:

@@ -59,6 +59,17 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(int dt, const uint8_t* _
 
 void launch_gemm(int dt, const void* w, const float* a, int M, int K, int N, float* out, const float* resid,
                  hipStream_t st) {
+  if (gemm_mfma_ok(dt, w, K, N) && (reinterpret_cast<uintptr_t>(a) & 15) == 0) {
+    // stream-ordered scratch for the fp16 activation pair
+    const size_t n = (size_t)M * K;
+    void* buf = nullptr;
+    check_hip(hipMallocAsync(&buf, n * 2 * sizeof(__half), st), "hipMallocAsync");
+    __half* xh = static_cast<__half*>(buf);
+    launch_split_f16(a, n, xh, xh + n, st);
+    launch_gemm_mfma(dt, w, xh, xh + n, M, K, N, out, resid, st);
+    check_hip(hipFreeAsync(buf, st), "hipFreeAsync");
+    return;
+  }
   dim3 grid((N + GBN - 1) / GBN, (M + GBM - 1) / GBM);
   hipLaunchKernelGGL(gemm_simt_kernel, grid, dim3(256), 0, st, dt, (const uint8_t*)w, a, M, K, N, out, resid);
 }

@@ -89,7 +89,7 @@ Session::~Session() {
                   (void*)act_, (void*)tmp_, (void*)xdec_, (void*)xndec_, (void*)qd_, (void*)kd_, (void*)vd_,
                   (void*)attd_, (void*)actd_, (void*)logits_, (void*)part_, (void*)tmpd_, (void*)d_pos_,
                   (void*)d_step_, (void*)d_flags_, (void*)d_tok_, (void*)d_ids_, (void*)d_gen_, (void*)d_key_,
-                  (void*)d_flag_, (void*)d_cnt_, kv_blob_})
+                  (void*)d_flag_, (void*)d_cnt_, (void*)xs_, kv_blob_})
     dev_free(p);
   if (st_) (void)hipStreamDestroy(st_);
 }
@@ -114,6 +114,8 @@ void Session::ensure_rows(int rows) {
     dev_free(*b);
     *b = nullptr;
   }
+  dev_free(xs_);
+  xs_ = nullptr;
   const Config& c = m_->cfg;
   int qmax = 0, kvmax = 0, fmax = 0;
   for (auto& L : c.layers) {
@@ -132,17 +134,22 @@ void Session::ensure_rows(int rows) {
   u_ = dev_alloc<float>(R * fmax);
   act_ = dev_alloc<float>(R * fmax);
   tmp_ = dev_alloc<float>(R * std::max(qmax, fmax));
+  // fp16 (hi, lo) pair of the widest GEMM input, for the matrix-core prefill projections
+  xs_ = dev_alloc<__half>(2 * R * std::max(std::max(H_, qmax), fmax));
   rows_cap_ = rows;
 }
 
-// One projection over `rows` activation rows: matvec for a single row, GEMM otherwise.
-static void project(const DevTensor& w, const float* a, int rows, int K, int N, float* out, const float* resid,
-                    hipStream_t st) {
+// One projection over `rows` activation rows: matvec for a single row, GEMM otherwise. `xs` is
+// the fp16 (hi, lo) split of `a` when the caller has made it (rows*K halves each), else null.
+static void project(const DevTensor& w, const float* a, const __half* xs, int rows, int K, int N, float* out,
+                    const float* resid, hipStream_t st) {
   if (w.dims.size() != 2 || (int)w.dims[0] != K || (int)w.dims[1] != N)
     fail(ST_MATMUL, "inner dim mismatch: weight dims do not match the activation width");
   if (rows == 1) {
     MvSegDesc s{w.dev, out, resid, N};
     launch_matvec(w.dtype, &s, 1, a, K, resid ? 1 : 0, st);
+  } else if (xs && gemm_mfma_ok(w.dtype, w.dev, K, N)) {
+    launch_gemm_mfma(w.dtype, w.dev, xs, xs + (size_t)rows * K, rows, K, N, out, resid, st);
   } else {
     launch_gemm(w.dtype, w.dev, a, rows, K, N, out, resid, st);
   }
@@ -156,10 +163,17 @@ void Session::layer_prefill(int li, int M) {
   const float eps = c.rms_eps;
   // attention sub-layer: pre-norm, projections, RoPE at prompt positions 0..M-1, KV append at the
   // cache's current length, causal attention within the prompt, O projection + residual.
+  // fp16 pair of a GEMM input (only when it has more than one row and a width the split takes)
+  auto split = [&](const float* a, int K) -> const __half* {
+    if (M < 2 || K % 32 != 0) return nullptr;
+    launch_split_f16(a, (size_t)M * K, xs_, xs_ + (size_t)M * K, st_);
+    return xs_;
+  };
   launch_rmsnorm(x_, (const float*)L.attn_norm.dev, M, H_, eps, xn_, st_);
-  project(L.wq, xn_, M, H_, qd, q_, nullptr, st_);
-  project(L.wk, xn_, M, H_, kvd, k_, nullptr, st_);
-  project(L.wv, xn_, M, H_, kvd, v_, nullptr, st_);
+  const __half* xs = split(xn_, H_);
+  project(L.wq, xn_, xs, M, H_, qd, q_, nullptr, st_);
+  project(L.wk, xn_, xs, M, H_, kvd, k_, nullptr, st_);
+  project(L.wv, xn_, xs, M, H_, kvd, v_, nullptr, st_);
   if (c.unpack_qk) {
     launch_unpack_qk(q_, tmp_, M, qd, c.n_heads, hd, st_);
     launch_copy_f32(tmp_, q_, (size_t)M * qd, st_);
@@ -172,18 +186,19 @@ void Session::layer_prefill(int li, int M) {
   launch_kv_store(k_, v_, M, kvd, kc_[li], vc_[li], c.n_kv_heads, hd, ctx_, nullptr, pos_, st_);
   const float scale = 1.0f / sqrtf((float)hd);
   launch_attn_prefill(q_, k_, v_, att_, M, c.n_heads, c.n_kv_heads, hd, S.window, scale, st_);
-  project(L.wo, att_, M, qd, H_, x_, x_, st_);
+  project(L.wo, att_, split(att_, qd), M, qd, H_, x_, x_, st_);
   // FFN sub-layer: pre-norm, gate/up, SwiGLU, down + residual.
   launch_rmsnorm(x_, (const float*)L.ffn_norm.dev, M, H_, eps, xn_, st_);
   if (M == 1 && L.gate.dtype == L.up.dtype) {
     MvSegDesc s[2] = {{L.gate.dev, act_, nullptr, S.ffn_dim}, {L.up.dev, nullptr, nullptr, S.ffn_dim}};
     launch_matvec(L.gate.dtype, s, 2, xn_, H_, 2, st_);
   } else {
-    project(L.gate, xn_, M, H_, S.ffn_dim, g_, nullptr, st_);
-    project(L.up, xn_, M, H_, S.ffn_dim, u_, nullptr, st_);
+    xs = split(xn_, H_);
+    project(L.gate, xn_, xs, M, H_, S.ffn_dim, g_, nullptr, st_);
+    project(L.up, xn_, xs, M, H_, S.ffn_dim, u_, nullptr, st_);
     launch_swiglu(g_, u_, act_, (size_t)M * S.ffn_dim, st_);
   }
-  project(L.down, act_, M, S.ffn_dim, H_, x_, x_, st_);
+  project(L.down, act_, split(act_, S.ffn_dim), M, S.ffn_dim, H_, x_, x_, st_);
 }
 
 // Decode layer, fused path: 5 launches (QKV+norm+RoPE+KV append, attention, O+residual,
@@ -279,9 +294,9 @@ void Session::layer_decode_unfused(int li) {
     MvSegDesc s[3] = {{L.wq.dev, qd_, nullptr, qd}, {L.wk.dev, kd_, nullptr, kvd}, {L.wv.dev, vd_, nullptr, kvd}};
     launch_matvec(L.wq.dtype, s, 3, xndec_, H_, 0, st_);
   } else {
-    project(L.wq, xndec_, 1, H_, qd, qd_, nullptr, st_);
-    project(L.wk, xndec_, 1, H_, kvd, kd_, nullptr, st_);
-    project(L.wv, xndec_, 1, H_, kvd, vd_, nullptr, st_);
+    project(L.wq, xndec_, nullptr, 1, H_, qd, qd_, nullptr, st_);
+    project(L.wk, xndec_, nullptr, 1, H_, kvd, kd_, nullptr, st_);
+    project(L.wv, xndec_, nullptr, 1, H_, kvd, vd_, nullptr, st_);
   }
   if (c.unpack_qk) {
     launch_unpack_qk(qd_, tmpd_, 1, qd, c.n_heads, hd, st_);
@@ -296,17 +311,17 @@ void Session::layer_decode_unfused(int li) {
   const float scale = 1.0f / sqrtf((float)hd);
   launch_attn_decode(qd_, kc_[li], vc_[li], attd_, part_, d_cnt_, c.n_heads, c.n_kv_heads, hd, ctx_, d_pos_, S.window,
                      scale, ctx_, st_);
-  project(L.wo, attd_, 1, qd, H_, xdec_, xdec_, st_);
+  project(L.wo, attd_, nullptr, 1, qd, H_, xdec_, xdec_, st_);
   launch_rmsnorm(xdec_, (const float*)L.ffn_norm.dev, 1, H_, c.rms_eps, xndec_, st_);
   if (L.gate.dtype == L.up.dtype) {
     MvSegDesc s[2] = {{L.gate.dev, actd_, nullptr, S.ffn_dim}, {L.up.dev, nullptr, nullptr, S.ffn_dim}};
     launch_matvec(L.gate.dtype, s, 2, xndec_, H_, 2, st_);
   } else {
-    project(L.gate, xndec_, 1, H_, S.ffn_dim, tmpd_, nullptr, st_);
-    project(L.up, xndec_, 1, H_, S.ffn_dim, actd_, nullptr, st_);
+    project(L.gate, xndec_, nullptr, 1, H_, S.ffn_dim, tmpd_, nullptr, st_);
+    project(L.up, xndec_, nullptr, 1, H_, S.ffn_dim, actd_, nullptr, st_);
     launch_swiglu(tmpd_, actd_, actd_, S.ffn_dim, st_);
   }
-  project(L.down, actd_, 1, S.ffn_dim, H_, xdec_, xdec_, st_);
+  project(L.down, actd_, nullptr, 1, S.ffn_dim, H_, xdec_, xdec_, st_);
 }
 
 static size_t embedding_hidden(const DevTensor& t, size_t* vocab) {

@@ -49,6 +49,7 @@ class Session {
   int rows_cap_ = 0;
   float *x_ = nullptr, *xn_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *att_ = nullptr;
   float *g_ = nullptr, *u_ = nullptr, *act_ = nullptr, *tmp_ = nullptr;
+  __half* xs_ = nullptr;  // fp16 (hi, lo) split of the current prefill GEMM input
   float *xdec_ = nullptr, *xndec_ = nullptr, *qd_ = nullptr, *kd_ = nullptr, *vd_ = nullptr, *attd_ = nullptr;
   float *actd_ = nullptr, *logits_ = nullptr, *part_ = nullptr, *tmpd_ = nullptr;
   // device-side loop state

@@ -105,7 +105,10 @@ def test_matvec_parity(gpu, dt, k, n):
 
 
 @pytest.mark.parametrize("dt,k,n,m", [(E.Q4K, 4096, 1024, 37), (E.Q6K, 1408, 512, 16), (E.Q6K, 14336, 256, 8),
-                                      (E.Q8_0, 1024, 96, 5), (E.F32, 256, 64, 70)])
+                                      (E.Q8_0, 1024, 96, 5), (E.F32, 256, 64, 70),
+                                      # matrix-core tiles: BM = 256 and 128, ragged M and N edges
+                                      (E.Q4K, 4096, 2048, 300), (E.Q4K, 512, 1408, 129), (E.Q6K, 4096, 320, 256),
+                                      (E.Q8_0, 2048, 200, 64), (E.F32, 1024, 136, 33)])
 def test_gemm_parity(gpu, dt, k, n, m):
     _check_matmul(dt, k, n, m)
 
