@@ -1510,6 +1510,19 @@ struct orc_cfg {
 
 int orc_model_load(const char* path, void** out) { ORC_TRY(*out = model_load(path)) }
 void orc_model_free(void* m) { delete (Model*)m; }
+// Raw bytes, dtype and ggml dims of a loaded tensor (for tests that recompose a layer by hand).
+int orc_model_tensor(void* mp, const char* name, const uint8_t** data, size_t* nbytes, int* dtype, uint64_t* ne0,
+                     uint64_t* ne1) {
+  ORC_TRY({
+    const Tensor* t = ((Model*)mp)->gguf.get(name);
+    if (!t) fail(E_MODEL, std::string("no tensor ") + name);
+    *data = t->buf.data();
+    *nbytes = t->buf.size();
+    *dtype = t->dtype;
+    *ne0 = t->dims.empty() ? 0 : t->dims[0];
+    *ne1 = t->dims.size() > 1 ? t->dims[1] : 1;
+  })
+}
 int orc_model_config(void* mp, orc_cfg* o) {
   ORC_TRY({
     const ModelConfig& c = ((Model*)mp)->cfg;

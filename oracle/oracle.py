@@ -65,6 +65,9 @@ def lib():
         L.orc_model_load.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)]
         L.orc_model_free.argtypes = [_f]
         L.orc_model_config.argtypes = [_f, ctypes.POINTER(Cfg)]
+        L.orc_model_tensor.argtypes = [_f, ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p),
+                                       ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_int),
+                                       ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]
         L.orc_model_layer_spec.argtypes = [_f, ctypes.c_size_t, ctypes.POINTER(ctypes.c_long),
                                            ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_uint64),
                                            ctypes.POINTER(ctypes.c_long), ctypes.POINTER(ctypes.c_uint64),
@@ -203,6 +206,15 @@ class Model:
                                           ctypes.byref(b), ctypes.byref(hd), ctypes.byref(fd)))
         return dict(sliding_window=w.value, rope_theta=t.value, rotary_dim=r.value, kv_borrow=b.value,
                     head_dim=hd.value, ffn_dim=fd.value)
+
+    def tensor(self, name: str):
+        """(dtype, raw bytes copy, ne0, ne1) of a loaded tensor."""
+        d, nb, dt, n0, n1 = (ctypes.c_void_p(), ctypes.c_size_t(), ctypes.c_int(), ctypes.c_uint64(),
+                             ctypes.c_uint64())
+        _check(lib().orc_model_tensor(self.h, name.encode(), ctypes.byref(d), ctypes.byref(nb), ctypes.byref(dt),
+                                      ctypes.byref(n0), ctypes.byref(n1)))
+        raw = np.ctypeslib.as_array((ctypes.c_uint8 * nb.value).from_address(d.value)).copy()
+        return dt.value, raw, n0.value, n1.value
 
     def __del__(self):
         if getattr(self, "h", None):

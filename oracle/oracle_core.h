@@ -8,6 +8,22 @@
 // Arithmetic rules followed everywhere: f32 ops in the reference's order, no FMA contraction
 // (-ffp-contract=off), f64 block dequant as the reference writes it, glibc libm for
 // expf/cosf/sinf/powf/tanhf/sqrtf (Rust std calls the platform libm on Linux).
+//
+// What pins each part (tests/test_oracle_known_answers.py, tests/test_oracle_model.py):
+//   f16_to_f32            exhaustive over all 65536 half patterns vs the IEEE closed form
+//   extract_scale_min_k4  every 6-bit (scale, min) value round-trips through the packing
+//   Q4_K / Q6_K / Q8_0    positional known answers (one nonzero field at a time), f64 single
+//                         rounding, quantise->dequantise round trip against the synthetic writer
+//   matmul                reference known answers (matmul.rs:453-497), float64 GEMM bound,
+//                         sequential-order bit test, parity mode == baseline mode bit for bit
+//   rmsnorm / rope / softmax / swiglu / gelu / argmax / unpack_qk
+//                         the reference's own inline known answers (file:line in each test) plus
+//                         closed forms (rope running product, swiglu two-branch sigmoid)
+//   attention + layer     layer 0 of the tiny model recomposed from the pinned ops around a
+//                         brute-force float64 causal GQA attention; prefill N+1 == prefill N +
+//                         decode; greedy loop == teacher-forced re-prefill
+// Parity unpinned: the Gemma-4 specific parts (per-layer embeddings, layer output scale, q/k/v
+// head norms, KV borrowing, GeGLU FFN wiring) have no known answer or closed-form check yet.
 #pragma once
 #include <cstddef>
 #include <cstdint>

@@ -92,3 +92,58 @@ def test_errors(c0):
     with pytest.raises(O.OracleError) as e:
         s.decode(5)
     assert e.value.code == 8  # KVCacheFull (attention.rs:55-59)
+
+
+def test_layer0_recomposed_with_brute_force_attention(c0):
+    """Pins the oracle's layer composition and attention (A13/A15/A18/A22/A24/A25) against an
+    independent recomposition: layer 0 of C0 rebuilt from the separately pinned ops (matmul,
+    rmsnorm, rope, swiglu) around a brute-force float64 causal GQA attention. A wrong GQA head
+    map, score scale, causal bound or residual wiring moves the result by O(1)."""
+    m = 16
+    prompt = synth.prompt_ids(0, m)
+    s = O.Session(c0)
+    s.set_layer_limit(1)
+    s.prefill(prompt)
+    want = s.hidden()
+    c = c0.cfg
+    H, nh, nkv, hd, F, eps = c.hidden_dim, c.n_heads, c.n_kv_heads, c.head_dim, c.ffn_dim, c.rms_norm_eps
+
+    def mat(name, a, k, n):
+        dt, raw, k0, n0 = c0.tensor(name)
+        assert (k0, n0) == (k, n)
+        return O.matmul(dt, a, raw, k, n)
+
+    def vec(name):
+        dt, raw, _, _ = c0.tensor(name)
+        assert dt == O.T_F32
+        return raw.view(np.float32)
+
+    dt, raw, _, _ = c0.tensor("token_embd.weight")
+    per_row = H // 256 * 144
+    x = np.stack([O.dequantize(dt, raw[t * per_row:(t + 1) * per_row], H // 256) for t in prompt])
+    xn = np.stack([O.rmsnorm(r, vec("blk.0.attn_norm.weight"), eps) for r in x])
+    q = mat("blk.0.attn_q.weight", xn, H, nh * hd)
+    k = mat("blk.0.attn_k.weight", xn, H, nkv * hd)
+    v = mat("blk.0.attn_v.weight", xn, H, nkv * hd)
+    for p in range(m):
+        q[p] = np.concatenate([O.rope(q[p, h * hd:(h + 1) * hd], 10000.0, p, hd, hd) for h in range(nh)])
+        k[p] = np.concatenate([O.rope(k[p, h * hd:(h + 1) * hd], 10000.0, p, hd, hd) for h in range(nkv)])
+    att = np.zeros((m, nh * hd), np.float64)
+    for h in range(nh):
+        kvh = h // (nh // nkv)
+        qh = q[:, h * hd:(h + 1) * hd].astype(np.float64)
+        kh = k[:, kvh * hd:(kvh + 1) * hd].astype(np.float64)
+        vh = v[:, kvh * hd:(kvh + 1) * hd].astype(np.float64)
+        sc = qh @ kh.T / np.sqrt(hd)
+        sc[np.triu_indices(m, 1)] = -np.inf
+        w = np.exp(sc - sc.max(axis=1, keepdims=True))
+        w /= w.sum(axis=1, keepdims=True)
+        att[:, h * hd:(h + 1) * hd] = w @ vh
+    x1 = x + mat("blk.0.attn_output.weight", att.astype(np.float32), nh * hd, H)
+    xn1 = np.stack([O.rmsnorm(r, vec("blk.0.ffn_norm.weight"), eps) for r in x1])
+    g = mat("blk.0.ffn_gate.weight", xn1, H, F)
+    u = mat("blk.0.ffn_up.weight", xn1, H, F)
+    act = np.stack([O.swiglu(g[i], u[i]) for i in range(m)])
+    got = x1 + mat("blk.0.ffn_down.weight", act, F, H)
+    rel = np.linalg.norm(got.astype(np.float64) - want) / np.linalg.norm(want.astype(np.float64))
+    assert rel < 1e-5, rel
