@@ -15,136 +15,107 @@ namespace iek {
 
 constexpr int SPLIT = 64;
 
-// One wave per (KV head, 64-key slice). Lane j scores key j0+j against the G <= GM query heads of
-// the group; the V rows of the slice are fetched in the same burst as K (uint4 per lane, LPR lanes
-// per row) so each wave makes a single trip to HBM (two for head_dim 256, where holding both
-// would exceed the register file). Slices publish (max, sum, o[]) partials that a second launch
-// merges per query head (a cross-workgroup merge inside one launch would need device-scope
-// fences, which write back the L2 of every XCD).
-template <int HD, int GM>
-__global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict__ q, const __half* __restrict__ kc,
-                                                         const __half* __restrict__ vc, float* __restrict__ part,
-                                                         int n_heads, int n_kv, int ctx, const int* pos_dev,
-                                                         int window, float scale, int nsplit) {
-  constexpr int KV4 = HD / 8;      // uint4 (8 halves) per key row
-  constexpr int LPR = HD / 8;      // lanes per V row in the PV phase
-  constexpr int RPI = 64 / LPR;    // V rows covered by one load instruction of the wave
-  constexpr int NV = SPLIT / RPI;  // V loads per lane
-  constexpr bool TWO_TRIPS = HD > 128;
+// One 256-thread workgroup per (KV head, 64-key slice): the four waves load the slice's K and V
+// rows (fp16) into LDS together in one burst of clamped, unconditional 16-byte loads, then wave w
+// takes query heads w and w+4 of the GQA group. Lane j scores key j against its head (K row from
+// LDS, q broadcast from LDS), the wave forms the slice softmax, and for P.V lane l owns head dims
+// [DPL*l, DPL*l + DPL). Slices publish (max, sum, o[]) partials that a second launch merges per
+// query head (a cross-workgroup merge inside one launch would need device-scope fences, which
+// write back the L2 of every XCD).
+template <int HD>
+__global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, const __half* __restrict__ kc,
+                                                          const __half* __restrict__ vc, float* __restrict__ part,
+                                                          int n_heads, int n_kv, int ctx, const int* pos_dev,
+                                                          int window, float scale, int nsplit) {
+  constexpr int DPL = HD / 64;        // head dims per lane in the PV phase
+  constexpr int KROW = HD + 8;        // padded K row (halves): 16-byte reads of different rows spread banks
+  constexpr int U4 = SPLIT * HD / 8;  // uint4 per K (or V) slice
   static_assert(HD == 64 || HD == 128 || HD == 256, "head_dim");
-  const int kvh = blockIdx.x, sp = blockIdx.y, lane = threadIdx.x;
+  const int kvh = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = n_heads / n_kv;
   const int total = *pos_dev + 1;
   const int jmin = (window > 0 && total > window) ? total - window : 0;
   const int j0 = max(sp * SPLIT, jmin), j1 = min(total, (sp + 1) * SPLIT);
-  __shared__ __align__(16) float qs[GM][HD];
-  __shared__ float ps[GM][SPLIT];
   const int nk = j1 - j0;
-  if (nk <= 0) return;
-  // Every load is issued unconditionally (indices clamped into the live slice) so the compiler
-  // keeps all of them in flight at once instead of waiting on each guarded load.
-  const bool valid = lane < nk;
-  const int j = j0 + min(lane, nk - 1);
-  const int vrow = lane / LPR, vcol = 8 * (lane % LPR);
-  const __half* vb = vc + ((size_t)kvh * ctx + j0) * HD + vcol;
-  uint4 kr[KV4];
-  uint4 vraw[NV];
+  if (nk <= 0) return;  // uniform across the workgroup
+  __shared__ __align__(16) __half ks[SPLIT][KROW];
+  __shared__ __align__(16) __half vs[SPLIT][HD];
+  __shared__ __align__(16) float qs[8][HD];
+  __shared__ float ps[4][SPLIT];
   {
-    const uint4* kp = reinterpret_cast<const uint4*>(kc + ((size_t)kvh * ctx + j) * HD);
+    const __half* kb = kc + ((size_t)kvh * ctx + j0) * HD;
+    const __half* vb = vc + ((size_t)kvh * ctx + j0) * HD;
+    uint4 kr[U4 / 256], vr[U4 / 256];
 #pragma unroll
-    for (int c = 0; c < KV4; ++c) kr[c] = kp[c];
-  }
-  if constexpr (!TWO_TRIPS) {
-#pragma unroll
-    for (int i = 0; i < NV; ++i)
-      vraw[i] = *reinterpret_cast<const uint4*>(vb + (size_t)min(vrow + RPI * i, nk - 1) * HD);
-  }
-  for (int i = lane; i < G * HD; i += 64) qs[i / HD][i % HD] = q[(size_t)(kvh * G) * HD + i];
-  __syncthreads();
-  float sc[GM];
-#pragma unroll
-  for (int g = 0; g < GM; ++g) sc[g] = 0.f;
-#pragma unroll
-  for (int c = 0; c < KV4; ++c) {
-    const __half2* h2 = reinterpret_cast<const __half2*>(&kr[c]);
-    float kf[8];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const float2 f = __half22float2(h2[t]);
-      kf[2 * t] = f.x;
-      kf[2 * t + 1] = f.y;
+    for (int u = 0; u < U4 / 256; ++u) {
+      const int i = tid + 256 * u, row = min(i / (HD / 8), nk - 1), c8 = i % (HD / 8);
+      kr[u] = *reinterpret_cast<const uint4*>(kb + (size_t)row * HD + 8 * c8);
+      vr[u] = *reinterpret_cast<const uint4*>(vb + (size_t)row * HD + 8 * c8);
     }
+    for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = q[(size_t)(kvh * G) * HD + i];
 #pragma unroll
-    for (int g = 0; g < GM; ++g) {
-      if (g < G) {
-        const float4 qa = *reinterpret_cast<const float4*>(&qs[g][8 * c]);
-        const float4 qb = *reinterpret_cast<const float4*>(&qs[g][8 * c + 4]);
-        sc[g] += qa.x * kf[0] + qa.y * kf[1] + qa.z * kf[2] + qa.w * kf[3] + qb.x * kf[4] + qb.y * kf[5] +
-                 qb.z * kf[6] + qb.w * kf[7];
-      }
-    }
-  }
-  if constexpr (TWO_TRIPS) {
-#pragma unroll
-    for (int i = 0; i < NV; ++i)
-      vraw[i] = *reinterpret_cast<const uint4*>(vb + (size_t)min(vrow + RPI * i, nk - 1) * HD);
-  }
-  float mg[GM], lg[GM];
-#pragma unroll
-  for (int g = 0; g < GM; ++g) {
-    if (g < G) {
-      const float s = valid ? sc[g] * scale : -INFINITY;
-      mg[g] = wave_max(s);
-      const float p = valid ? expf(s - mg[g]) : 0.f;
-      lg[g] = wave_sum(p);
-      ps[g][lane] = p;
+    for (int u = 0; u < U4 / 256; ++u) {
+      const int i = tid + 256 * u, row = i / (HD / 8), c8 = i % (HD / 8);
+      *reinterpret_cast<uint4*>(&ks[row][8 * c8]) = kr[u];
+      *reinterpret_cast<uint4*>(&vs[row][8 * c8]) = vr[u];
     }
   }
   __syncthreads();
-  float o[GM][8];
+  const bool valid = lane < nk;
+  for (int g = wave; g < G; g += 4) {
+    // scores: lane = key
+    float sc = 0.f;
 #pragma unroll
-  for (int g = 0; g < GM; ++g)
+    for (int c = 0; c < HD / 8; ++c) {
+      const uint4 kraw = *reinterpret_cast<const uint4*>(&ks[lane][8 * c]);
+      const __half2* h2 = reinterpret_cast<const __half2*>(&kraw);
+      const float4 qa = *reinterpret_cast<const float4*>(&qs[g][8 * c]);
+      const float4 qb = *reinterpret_cast<const float4*>(&qs[g][8 * c + 4]);
+      const float2 k0 = __half22float2(h2[0]), k1 = __half22float2(h2[1]), k2 = __half22float2(h2[2]),
+                   k3 = __half22float2(h2[3]);
+      sc += qa.x * k0.x + qa.y * k0.y + qa.z * k1.x + qa.w * k1.y + qb.x * k2.x + qb.y * k2.y + qb.z * k3.x +
+            qb.w * k3.y;
+    }
+    const float s = valid ? sc * scale : -INFINITY;
+    const float m = wave_max(s);
+    const float p = valid ? expf(s - m) : 0.f;
+    const float l = wave_sum(p);
+    ps[wave][lane] = p;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // P.V: lane owns dims DPL*lane .. +DPL-1; keys past the live slice carry p = 0
+    float o[DPL];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) o[g][t] = 0.f;
-  // rows past the live slice carry p = 0 (ps holds p = 0 for invalid lanes)
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const __half2* h2 = reinterpret_cast<const __half2*>(&vraw[i]);
-    float vf[8];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const float2 f = __half22float2(h2[t]);
-      vf[2 * t] = f.x;
-      vf[2 * t + 1] = f.y;
+    for (int t = 0; t < DPL; ++t) o[t] = 0.f;
+#pragma unroll 8
+    for (int j = 0; j < SPLIT; ++j) {
+      const float pj = ps[wave][j];
+      if constexpr (DPL == 1) {
+        o[0] += pj * __half2float(vs[j][lane]);
+      } else if constexpr (DPL == 2) {
+        const float2 v2 = __half22float2(*reinterpret_cast<const __half2*>(&vs[j][2 * lane]));
+        o[0] += pj * v2.x;
+        o[1] += pj * v2.y;
+      } else {
+        const uint2 raw = *reinterpret_cast<const uint2*>(&vs[j][4 * lane]);
+        const __half2* h2 = reinterpret_cast<const __half2*>(&raw);
+        const float2 a0 = __half22float2(h2[0]), a1 = __half22float2(h2[1]);
+        o[0] += pj * a0.x;
+        o[1] += pj * a0.y;
+        o[2] += pj * a1.x;
+        o[3] += pj * a1.y;
+      }
+    }
+    float* pr = part + ((size_t)(kvh * G + g) * nsplit + sp) * (HD + 2);
+    if (lane == 0) {
+      pr[0] = m;
+      pr[1] = l;
     }
 #pragma unroll
-    for (int g = 0; g < GM; ++g) {
-      if (g < G) {
-        const float p = ps[g][vrow + RPI * i];
-#pragma unroll
-        for (int t = 0; t < 8; ++t) o[g][t] += p * vf[t];
-      }
-    }
-  }
-  // sum the RPI row subsets: lanes with equal lane % LPR hold the same head dims
-#pragma unroll
-  for (int g = 0; g < GM; ++g) {
-    if (g < G) {
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-#pragma unroll
-        for (int off = LPR; off < 64; off <<= 1) o[g][t] += __shfl_xor(o[g][t], off, 64);
-      }
-      float* pr = part + ((size_t)(kvh * G + g) * nsplit + sp) * (HD + 2);
-      if (lane == 0) {
-        pr[0] = mg[g];
-        pr[1] = lg[g];
-      }
-      if (lane < LPR) {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) pr[2 + vcol + t] = o[g][t];
-      }
-    }
+    for (int t = 0; t < DPL; ++t) pr[2 + DPL * lane + t] = o[t];
+    __builtin_amdgcn_wave_barrier();  // ps[wave] is rewritten by the next head of this wave
   }
 }
 
@@ -204,23 +175,13 @@ __global__ __launch_bounds__(64) void attn_decode_merge_kernel(const float* __re
   for (int t = 0; t < DPL; ++t) out[(size_t)h * HD + DPL * lane + t] = acc[t] / L;
 }
 
-template <int HD, int GM>
-static void attn_decode_pair(dim3 grid, hipStream_t st, const float* q, const __half* kc, const __half* vc, float* out,
-                             float* part, int n_heads, int n_kv, int ctx, const int* pos_dev, int window, float scale,
-                             int nsplit) {
-  hipLaunchKernelGGL((attn_decode_kernel<HD, GM>), grid, dim3(64), 0, st, q, kc, vc, part, n_heads, n_kv, ctx, pos_dev,
-                     window, scale, nsplit);
-  hipLaunchKernelGGL(attn_decode_merge_kernel<HD>, dim3(n_heads), dim3(64), 0, st, part, out, nsplit, pos_dev, window);
-}
-
 template <int HD>
 static void attn_decode_hd(dim3 grid, hipStream_t st, const float* q, const __half* kc, const __half* vc, float* out,
                            float* part, int n_heads, int n_kv, int ctx, const int* pos_dev, int window, float scale,
                            int nsplit) {
-  if (n_heads / n_kv <= 4)
-    attn_decode_pair<HD, 4>(grid, st, q, kc, vc, out, part, n_heads, n_kv, ctx, pos_dev, window, scale, nsplit);
-  else
-    attn_decode_pair<HD, 8>(grid, st, q, kc, vc, out, part, n_heads, n_kv, ctx, pos_dev, window, scale, nsplit);
+  hipLaunchKernelGGL(attn_decode_kernel<HD>, grid, dim3(256), 0, st, q, kc, vc, part, n_heads, n_kv, ctx, pos_dev,
+                     window, scale, nsplit);
+  hipLaunchKernelGGL(attn_decode_merge_kernel<HD>, dim3(n_heads), dim3(64), 0, st, part, out, nsplit, pos_dev, window);
 }
 
 void launch_attn_decode(const float* q, const __half* kc, const __half* vc, float* out, float* part, int* counters,

@@ -76,9 +76,14 @@ IEK_DEV float div_rn(float x, float y) {
 // y = (x*w)/rms with the reference's two roundings. The epilogue's inputs (residual vector, this
 // position's RoPE cos/sin) are staged here too, so the main loop never waits on a global load.
 struct Lds {
-  float* x;     // K
-  float* res;   // N (EPI_RESID)
-  float* rope;  // 2*npairs (EPI_QKV)
+  float* x;      // K f32 (float staging)
+  float* res;    // N (EPI_RESID)
+  float* rope;   // 2*npairs (EPI_QKV)
+  // int8 staging: x ~= s_b * (256 * xh + xl) per 32-element block b
+  int8_t* xh;    // K
+  int8_t* xl;    // K
+  float* sb;     // K/32 block scales
+  int* sx;       // K/32 block sums of (256 * xh + xl)
 };
 
 IEK_DEV void stage(const MvArgs& a, const Lds& L, int pos) {
@@ -144,16 +149,133 @@ IEK_DEV void stage(const MvArgs& a, const Lds& L, int pos) {
   __builtin_amdgcn_s_waitcnt(0);
 }
 
-IEK_DEV size_t lds_floats(const MvArgs& a) {
-  return (size_t)a.K + (a.epi == EPI_RESID ? (size_t)a.n[0] : 0) + (a.epi == EPI_QKV ? 2 * (size_t)a.npairs : 0);
+// LDS bytes: x staging (f32: 4K; int8: 2K planes + 8 bytes per 32-block), then the residual
+// vector (EPI_RESID) and this position's RoPE (cos, sin) pairs (EPI_QKV).
+__host__ __device__ inline size_t lds_bytes(const MvArgs& a, bool i8) {
+  const size_t xb = i8 ? 2 * (size_t)a.K + 8 * (size_t)(a.K / 32) : 4 * (size_t)a.K;
+  return xb + (a.epi == EPI_RESID ? 4 * (size_t)a.n[0] : 0) + (a.epi == EPI_QKV ? 8 * (size_t)a.npairs : 0);
 }
 
-IEK_DEV Lds lds_layout(const MvArgs& a, float* base) {
+IEK_DEV Lds lds_layout(const MvArgs& a, float* base, bool i8) {
   Lds L;
-  L.x = base;
-  L.res = base + a.K;
-  L.rope = base + a.K + (a.epi == EPI_RESID ? a.n[0] : 0);
+  char* p = reinterpret_cast<char*>(base);
+  L.x = nullptr;
+  L.xh = L.xl = nullptr;
+  L.sb = nullptr;
+  L.sx = nullptr;
+  if (i8) {
+    L.xh = reinterpret_cast<int8_t*>(p);
+    L.xl = L.xh + a.K;
+    L.sb = reinterpret_cast<float*>(p + 2 * (size_t)a.K);
+    L.sx = reinterpret_cast<int*>(L.sb + a.K / 32);
+    p += 2 * (size_t)a.K + 8 * (size_t)(a.K / 32);
+  } else {
+    L.x = base;
+    p += 4 * (size_t)a.K;
+  }
+  L.res = reinterpret_cast<float*>(p);
+  L.rope = L.res + (a.epi == EPI_RESID ? a.n[0] : 0);
   return L;
+}
+
+// ---- int8 staging of x ------------------------------------------------------------------------
+// Each 32-element block b of y = x*w (or x) is stored as a 16-bit integer vector X with
+// y ~= s_b * X, s_b = amax_b / (32639 * rms) and |X| <= 32639, split as X = 256*xh + xl with
+// xh in [-127, 127] and xl in [-128, 127], so two v_dot4_i32_i8 per 4 weights give the exact
+// integer sum of q*X. The representation error is at most s_b/2 per element (~1.5e-5 of the
+// block's largest |y|); the RMS factor never touches the elements (it only enters s_b), so no
+// per-element division is needed. Threads own whole blocks (K <= 16384).
+constexpr float XQ_MAX = 32639.0f;
+
+IEK_DEV void quant_block(const float (&y)[32], float am, uint32_t (&h)[8], uint32_t (&l)[8], int& sum) {
+  const float inv = am > 0.f ? XQ_MAX / am : 0.f;
+  sum = 0;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    uint32_t hw = 0, lw = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      int X = __float2int_rn(y[4 * g + e] * inv);
+      X = max(-32639, min(32639, X));
+      const int hi = (X + 128) >> 8, lo = X - (hi << 8);
+      sum += X;
+      hw |= (uint32_t)(hi & 0xFF) << (8 * e);
+      lw |= (uint32_t)(lo & 0xFF) << (8 * e);
+    }
+    h[g] = hw;
+    l[g] = lw;
+  }
+}
+
+IEK_DEV void stage_i8(const MvArgs& a, const Lds& L, int pos) {
+  const int K = a.K, tid = threadIdx.x, nb = K >> 5;
+  float ss = 0.f;
+  float amax[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int b = tid + 256 * j;
+    const int bc = min(b, nb - 1);
+    const float4* x4 = reinterpret_cast<const float4*>(a.x) + (size_t)bc * 8;
+    float4 xv[8], wv[8] = {};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) xv[t] = x4[t];
+    if (a.norm_w) {
+      const float4* w4 = reinterpret_cast<const float4*>(a.norm_w) + (size_t)bc * 8;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) wv[t] = w4[t];
+    }
+    float y[32];
+    float am = 0.f, sq = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const float xs[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+      const float ws[4] = {wv[t].x, wv[t].y, wv[t].z, wv[t].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sq += xs[e] * xs[e];
+        y[4 * t + e] = a.norm_w ? mul_rn(xs[e], ws[e]) : xs[e];
+        am = fmaxf(am, fabsf(y[4 * t + e]));
+      }
+    }
+    uint32_t h[8], l[8];
+    int sum;
+    quant_block(y, am, h, l, sum);
+    amax[j] = am;
+    if (b < nb) {
+      ss += sq;
+      uint4* ph = reinterpret_cast<uint4*>(L.xh + 32 * b);
+      uint4* pl = reinterpret_cast<uint4*>(L.xl + 32 * b);
+      ph[0] = make_uint4(h[0], h[1], h[2], h[3]);
+      ph[1] = make_uint4(h[4], h[5], h[6], h[7]);
+      pl[0] = make_uint4(l[0], l[1], l[2], l[3]);
+      pl[1] = make_uint4(l[4], l[5], l[6], l[7]);
+      L.sx[b] = sum;
+    }
+    if (nb <= 256) break;
+  }
+  if (a.epi == EPI_RESID) {
+    const int N = a.n[0];
+    for (int i = tid; i < N; i += 256) L.res[i] = a.resid[i];
+  }
+  if (a.epi == EPI_QKV) {
+    for (int i = tid; i < 2 * a.npairs; i += 256) L.rope[i] = a.rope_cs[(size_t)pos * a.npairs * 2 + i];
+  }
+  float rms = 1.f;
+  if (a.norm_w) {
+    __shared__ float red[4];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, WAVE);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    rms = rms_of((red[0] + red[1]) + (red[2] + red[3]), K, a.eps);
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int b = tid + 256 * j;
+    if (b < nb) L.sb[b] = amax[j] / (XQ_MAX * rms);
+  }
+  __syncthreads();
+  __builtin_amdgcn_s_waitcnt(0);
 }
 
 // Segment fields picked with constant indices: a dynamic index into the by-value argument block
@@ -166,7 +288,7 @@ IEK_DEV int seg_base(const MvArgs& a, int s) { return s == 0 ? a.seg_start[0] : 
 // Reads only registers and LDS (pos was loaded at kernel start).
 template <int R>
 IEK_DEV void epilogue(const MvArgs& a, const Lds& L, int s, int lr0, float (&acc)[R], const float* acc_up, int lane,
-                      int pos) {
+                      int pos, unsigned long long& run_key) {
   if (a.epi == EPI_SWIGLU) {
     if (lane < R) {
       float g = acc[0], u = acc_up[0];
@@ -203,25 +325,19 @@ IEK_DEV void epilogue(const MvArgs& a, const Lds& L, int s, int lr0, float (&acc
     return;
   }
   if (a.epi == EPI_ARGMAX) {
+    // logits row n: store (soft-capped), fold its packed (value, first-index) key into the lane's
+    // running maximum; one atomic per workgroup at the end of the launch (argmax_flush)
     float v = acc[0];
 #pragma unroll
     for (int r = 1; r < R; ++r)
       if (lane == r) v = acc[r];
     if (a.softcap > 0.f) v = soft_cap(v, a.softcap);
-    unsigned long long key = 0;
-    bool bad = false;
     if (lane < R) {
       a.out[0][lr0 + lane] = v;
-      key = argmax_key_dev(v, (uint32_t)(lr0 + lane));
-      bad = !isfinite(v);
+      const unsigned long long key = argmax_key_dev(v, (uint32_t)(lr0 + lane));
+      run_key = key > run_key ? key : run_key;
+      if (!isfinite(v)) atomicOr(a.amax_flag, 1);
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      unsigned long long o = __shfl_xor(key, off, WAVE);
-      key = o > key ? o : key;
-    }
-    if (lane == 0) atomicMax(a.amax_key, key);
-    if (bad) atomicOr(a.amax_flag, 1);
     return;
   }
   if (lane < R) {
@@ -360,12 +476,33 @@ IEK_DEV float q6k_dot(const Q6Raw& q, const float4* x4, const float (&xs4)[4]) {
   return r;
 }
 
+// End of an EPI_ARGMAX launch: reduce the lanes' running keys over the workgroup and publish one
+// atomicMax (the key packs the value's order and the inverted index, so the maximum is the first
+// maximal index).
+IEK_DEV void argmax_flush(const MvArgs& a, unsigned long long run_key) {
+  __shared__ unsigned long long red_key[4];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned long long o = __shfl_xor(run_key, off, WAVE);
+    run_key = o > run_key ? o : run_key;
+  }
+  if ((threadIdx.x & 63) == 0) red_key[threadIdx.x >> 6] = run_key;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long k = red_key[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) k = red_key[w] > k ? red_key[w] : k;
+    if (k) atomicMax(a.amax_key, k);
+  }
+}
+
 // ---- streaming driver ------------------------------------------------------------------------
 // Wave w of workgroup b owns row groups (4b + w) + k * (4 * gridDim.x). It walks the flattened
 // (group, pass) sequence with two register buffers used alternately (no copies of in-flight data),
 // issuing the next step's weight loads before computing the current one. Loads are unconditional
 // with clamped addresses so the compiler can count them statically and keep them all in flight.
 struct Q4Tr {
+  static constexpr bool I8 = false;
   static constexpr int CHUNKS = 4;  // 64-value chunks per superblock
   static constexpr int BYTES = Q4K_BYTES;
   template <int NR>
@@ -383,7 +520,8 @@ struct Q4Tr {
     }
   }
   template <int NR>
-  IEK_DEV static void compute(const Buf<NR>& b, int c, const float* xs, float (&acc)[NR]) {
+  IEK_DEV static void compute(const Buf<NR>& b, int c, const Lds& L, float (&acc)[NR]) {
+    const float* xs = L.x;
     const int e0 = (c >> 2) * QK_K + (c & 3) * 64;
     float4 xl4[8], xh4[8];
     float xsl = 0.f, xsh = 0.f;
@@ -400,6 +538,7 @@ struct Q4Tr {
 };
 
 struct Q6Tr {
+  static constexpr bool I8 = false;
   static constexpr int CHUNKS = 8;  // 32-value chunks per superblock
   static constexpr int BYTES = Q6K_BYTES;
   template <int NR>
@@ -412,7 +551,8 @@ struct Q6Tr {
     for (int r = 0; r < NR; ++r) q6_load(rows[r] + (size_t)(c >> 3) * Q6K_BYTES, (c >> 2) & 1, c & 3, b.q[r]);
   }
   template <int NR>
-  IEK_DEV static void compute(const Buf<NR>& b, int c, const float* xs, float (&acc)[NR]) {
+  IEK_DEV static void compute(const Buf<NR>& b, int c, const Lds& L, float (&acc)[NR]) {
+    const float* xs = L.x;
     const int e0 = (c >> 3) * QK_K + 128 * ((c >> 2) & 1) + 8 * (c & 3);
     float4 x4[8];
     float xs4[4];
@@ -428,10 +568,61 @@ struct Q6Tr {
   }
 };
 
+// Q4_K against the int8-staged x: per 64-value chunk, the low nibbles (sub-block 2g) and high
+// nibbles (sub-block 2g+1) each give the exact integer S = sum q*X through v_dot4_i32_i8 on the
+// (xh, xl) planes; the row sum is then s_b * (d*sc*S - dmin*m*sum X) per sub-block, the same
+// algebra as the reference's sum over (d*sc*q - dmin*m) * x with x replaced by s_b*X.
+struct Q4I8Tr {
+  static constexpr bool I8 = true;
+  static constexpr int CHUNKS = 4;
+  static constexpr int BYTES = Q4K_BYTES;
+  template <int NR>
+  using Buf = Q4Tr::Buf<NR>;
+  template <int NR>
+  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c) {
+    Q4Tr::load<NR>(b, rows, c);
+  }
+  template <int NR>
+  IEK_DEV static void compute(const Buf<NR>& b, int c, const Lds& L, float (&acc)[NR]) {
+    const int e0 = (c >> 2) * QK_K + (c & 3) * 64, b0 = e0 >> 5;
+    const uint4* ph = reinterpret_cast<const uint4*>(L.xh + e0);
+    const uint4* pl = reinterpret_cast<const uint4*>(L.xl + e0);
+    const uint4 H0 = ph[0], H1 = ph[1], H2 = ph[2], H3 = ph[3];
+    const uint4 L0 = pl[0], L1 = pl[1], L2 = pl[2], L3 = pl[3];
+    const uint32_t xh[16] = {H0.x, H0.y, H0.z, H0.w, H1.x, H1.y, H1.z, H1.w,
+                             H2.x, H2.y, H2.z, H2.w, H3.x, H3.y, H3.z, H3.w};
+    const uint32_t xl[16] = {L0.x, L0.y, L0.z, L0.w, L1.x, L1.y, L1.z, L1.w,
+                             L2.x, L2.y, L2.z, L2.w, L3.x, L3.y, L3.z, L3.w};
+    const float2 sb = *reinterpret_cast<const float2*>(L.sb + b0);
+    const int2 sx = *reinterpret_cast<const int2*>(L.sx + b0);
+    const int g = c & 3;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const uint4 hdr = b.hdr[r];
+      const uint32_t qw[8] = {b.qa[r].x, b.qa[r].y, b.qa[r].z, b.qa[r].w, b.qb[r].x, b.qb[r].y, b.qb[r].z, b.qb[r].w};
+      int h0 = 0, l0 = 0, h1 = 0, l1 = 0;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int lo = (int)(qw[t] & 0x0F0F0F0Fu), hi = (int)((qw[t] >> 4) & 0x0F0F0F0Fu);
+        h0 = __builtin_amdgcn_sdot4(lo, (int)xh[t], h0, false);
+        l0 = __builtin_amdgcn_sdot4(lo, (int)xl[t], l0, false);
+        h1 = __builtin_amdgcn_sdot4(hi, (int)xh[8 + t], h1, false);
+        l1 = __builtin_amdgcn_sdot4(hi, (int)xl[8 + t], l1, false);
+      }
+      const float d = half_bits_to_float(hdr.x), dmin = half_bits_to_float(hdr.x >> 16);
+      float sc0, m0, sc1, m1;
+      scale_min_k4_sel(2 * g, hdr.y, hdr.z, hdr.w, &sc0, &m0);
+      scale_min_k4_sel(2 * g + 1, hdr.y, hdr.z, hdr.w, &sc1, &m1);
+      const float S0 = (float)(h0 * 256 + l0), S1 = (float)(h1 * 256 + l1);
+      acc[r] += sb.x * ((d * sc0) * S0 - (dmin * m0) * (float)sx.x) + sb.y * ((d * sc1) * S1 - (dmin * m1) * (float)sx.y);
+    }
+  }
+};
+
 template <class Tr, int R, bool DUAL>
 __global__ __launch_bounds__(256) void mv_stream(MvArgs a) {
   extern __shared__ __align__(16) float lds[];
-  const Lds L = lds_layout(a, lds);
+  const Lds L = lds_layout(a, lds, Tr::I8);
   constexpr int NR = DUAL ? 2 * R : R;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int pos = a.epi == EPI_QKV ? __builtin_amdgcn_readfirstlane(*a.pos) : 0;
@@ -458,6 +649,7 @@ __global__ __launch_bounds__(256) void mv_stream(MvArgs a) {
     for (int r = 0; r < NR; ++r) rows[r] = r < R ? w0 + (size_t)(lr0 + r) * rb : a.w[1] + (size_t)(lr0 + r - R) * rb;
   };
   typename Tr::template Buf<NR> A, B;
+  unsigned long long run_key = 0;
   float acc[NR];
 #pragma unroll
   for (int r = 0; r < NR; ++r) acc[r] = 0.f;
@@ -476,7 +668,7 @@ __global__ __launch_bounds__(256) void mv_stream(MvArgs a) {
     if (DUAL) wave_reduce<R>(accu);
     const int row0 = g * R;
     const int s = DUAL ? 0 : seg_of(a, row0);
-    epilogue<R>(a, L, s, row0 - seg_base(a, s), accg, accu, lane, pos);
+    epilogue<R>(a, L, s, row0 - seg_base(a, s), accg, accu, lane, pos, run_key);
 #pragma unroll
     for (int r = 0; r < NR; ++r) acc[r] = 0.f;
   };
@@ -486,7 +678,7 @@ __global__ __launch_bounds__(256) void mv_stream(MvArgs a) {
     float part[NR];
 #pragma unroll
     for (int r = 0; r < NR; ++r) part[r] = 0.f;
-    Tr::template compute<NR>(buf, min(c, nchunk - 1), L.x, part);
+    Tr::template compute<NR>(buf, min(c, nchunk - 1), L, part);
     // The empty asm pins the dot products as computed on every path: otherwise the compiler sinks
     // them under the c < nchunk branch and a wave whose lanes all skip it leaves the buffer's loads
     // unretired, which costs a full drain at the next reuse of those registers.
@@ -503,7 +695,10 @@ __global__ __launch_bounds__(256) void mv_stream(MvArgs a) {
     rows_of(0, rows, c);
     Tr::template load<NR>(A, rows, c);
   }
-  stage(a, L, pos);
+  if constexpr (Tr::I8)
+    stage_i8(a, L, pos);
+  else
+    stage(a, L, pos);
   for (int it = 0; it < steps; it += 2) {
     {
       const uint8_t* rows[NR];
@@ -521,34 +716,38 @@ __global__ __launch_bounds__(256) void mv_stream(MvArgs a) {
     }
     step(B, it + 1);
   }
+  if (a.epi == EPI_ARGMAX) argmax_flush(a, run_key);
   if (a.pos_inc && blockIdx.x == 0 && threadIdx.x == 0) *a.pos_inc += 1;
 }
 
 // ---- generic path: any dtype, any K (blocks may straddle rows when K % block != 0) ----------
 __global__ __launch_bounds__(256) void mv_generic(MvArgs a, int dt) {
   extern __shared__ __align__(16) float lds[];
-  const Lds L = lds_layout(a, lds);
+  const Lds L = lds_layout(a, lds, false);
   const float* xs = L.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row = blockIdx.x * 4 + wave;
   const int pos = a.epi == EPI_QKV ? *a.pos : 0;
   stage(a, L, pos);
   const int total = a.seg_start[a.nseg];
-  if (row >= total) return;
-  const int s = seg_of(a, row);
-  const int n = row - a.seg_start[s];
-  const bool dual = a.epi == EPI_SWIGLU;
-  const int K = a.K;
-  float g = 0.f, u = 0.f;
-  for (int k = lane; k < K; k += WAVE) {
-    const float xv = xs[k];
-    const size_t f = (size_t)k + (size_t)n * (size_t)K;
-    g += xv * flat_elem(dt, a.w[s], f);
-    if (dual) u += xv * flat_elem(dt, a.w[1], f);
+  unsigned long long run_key = 0;
+  if (row < total) {  // no early return: argmax_flush below has a workgroup barrier
+    const int s = seg_of(a, row);
+    const int n = row - a.seg_start[s];
+    const bool dual = a.epi == EPI_SWIGLU;
+    const int K = a.K;
+    float g = 0.f, u = 0.f;
+    for (int k = lane; k < K; k += WAVE) {
+      const float xv = xs[k];
+      const size_t f = (size_t)k + (size_t)n * (size_t)K;
+      g += xv * flat_elem(dt, a.w[s], f);
+      if (dual) u += xv * flat_elem(dt, a.w[1], f);
+    }
+    float acc[1] = {wave_sum(g)};
+    float accu[1] = {dual ? wave_sum(u) : 0.f};
+    epilogue<1>(a, L, s, n, acc, accu, lane, pos, run_key);
   }
-  float acc[1] = {wave_sum(g)};
-  float accu[1] = {dual ? wave_sum(u) : 0.f};
-  epilogue<1>(a, L, s, n, acc, accu, lane, pos);
+  if (a.epi == EPI_ARGMAX) argmax_flush(a, run_key);
   if (a.pos_inc && blockIdx.x == 0 && threadIdx.x == 0) *a.pos_inc += 1;
 }
 
@@ -598,8 +797,16 @@ void launch_mv(int dt, MvArgs a, hipStream_t st) {
   }
   bool fast = (dt == DT_Q4K || dt == DT_Q6K) && a.K % QK_K == 0 && (reinterpret_cast<uintptr_t>(a.x) % 16) == 0;
   for (int i = 0; i < (dual ? 2 : a.nseg); ++i) fast = fast && (reinterpret_cast<uintptr_t>(a.w[i]) % 16) == 0;
-  const size_t lds = ((size_t)a.K + (a.epi == EPI_RESID ? (size_t)a.n[0] : 0) +
-                      (a.epi == EPI_QKV ? 2 * (size_t)a.npairs : 0)) * sizeof(float);
+  // Q4_K takes the int8-staged x (v_dot4) path when x and the norm weight are 16-byte aligned and
+  // every 32-element block fits the two-blocks-per-thread staging; IEK_MV_F32=1 keeps the f32 path.
+  static int force_f32 = -1;
+  if (force_f32 < 0) {
+    const char* e = getenv("IEK_MV_F32");
+    force_f32 = (e && atoi(e) != 0) ? 1 : 0;
+  }
+  const bool i8 = fast && dt == DT_Q4K && !force_f32 && a.K <= 16384 &&
+                  (!a.norm_w || (reinterpret_cast<uintptr_t>(a.norm_w) % 16) == 0);
+  const size_t lds = lds_bytes(a, i8);
   if (lds > 160 * 1024) fail(ST_OP, "matvec: K too large for the LDS-staged input");
   if (fast) {
     // Two rows per wave: more rows per wave spill the prefetch registers.
@@ -610,7 +817,10 @@ void launch_mv(int dt, MvArgs a, hipStream_t st) {
     if (fast) {
       const int groups = total / R;
 #define IEK_L(TR, DD) launch_stream<TR, DD>(a, groups, lds, st)
-      if (dt == DT_Q4K) {
+      if (dt == DT_Q4K && i8) {
+        if (dual) IEK_L(Q4I8Tr, true);
+        else IEK_L(Q4I8Tr, false);
+      } else if (dt == DT_Q4K) {
         if (dual) IEK_L(Q4Tr, true);
         else IEK_L(Q4Tr, false);
       } else {
@@ -621,8 +831,10 @@ void launch_mv(int dt, MvArgs a, hipStream_t st) {
       return;
     }
   }
+  const size_t lds_f = lds_bytes(a, false);
+  if (lds_f > 160 * 1024) fail(ST_OP, "matvec: K too large for the LDS-staged input");
   if (a.epi == EPI_QKV) fail(ST_OP, "matvec: fused Q/K/V epilogue needs the aligned K-quant path");
-  hipLaunchKernelGGL(mv_generic, dim3((total + 3) / 4), dim3(256), lds, st, a, dt);
+  hipLaunchKernelGGL(mv_generic, dim3((total + 3) / 4), dim3(256), lds_f, st, a, dt);
 }
 
 void launch_matvec(int dt, const MvSegDesc* segs, int nseg, const float* x, int K, int epi, hipStream_t st) {

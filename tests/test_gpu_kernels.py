@@ -76,6 +76,9 @@ def _weights(dt, k, n, seed):
     return x[:nel].copy() if dt == E.F32 else synth.quantize(GGML[dt], x)
 
 
+XQ_MAX = 32639.0  # |X| bound of the int8-staged activation (matvec.hip, stage_i8)
+
+
 def _check_matmul(dt, k, n, m, seed=0):
     w = _weights(dt, k, n, seed)
     a = synth.normal(seed + 1, f"a{k}", m * k, 0.0, 1.0).reshape(m, k)
@@ -92,9 +95,18 @@ def _check_matmul(dt, k, n, m, seed=0):
     mag = np.abs(a).astype(np.float64) @ np.abs(wd).T
     err = np.abs(got.astype(np.float64) - want)
     # fp32 accumulation in a different order: |err| <= 2*K*eps*sum|a*w| (deterministic bound)
-    assert np.all(err <= 2 * k * np.finfo(np.float32).eps * mag + 1e-30), float(np.max(err / (mag + 1e-30)))
+    bound = 2 * k * np.finfo(np.float32).eps * mag + 1e-30
+    rel_bar = 1e-5
+    if dt == E.Q4K and m == 1 and k % 32 == 0:
+        # The decode matvec stages x as 16-bit integers per 32-element block (x ~= s_b * X with
+        # s_b = max|x_b| / 32639): each element is off by at most s_b / 2, so the dot is off by
+        # at most sum_i |w_i| s_b(i) / 2 on top of the reordering bound. Expected rel L2 ~2e-5.
+        sb = np.abs(a.astype(np.float64)).reshape(m, k // 32, 32).max(axis=2) / XQ_MAX
+        bound = bound + (np.repeat(sb, 32, axis=1) / 2) @ np.abs(wd).T
+        rel_bar = 6e-5
+    assert np.all(err <= bound), float(np.max(err / bound))
     rel = np.linalg.norm(got - want) / np.linalg.norm(want)
-    assert rel < 1e-5, rel
+    assert rel < rel_bar, rel
 
 
 @pytest.mark.parametrize("dt,k,n", [(E.Q4K, 4096, 4096), (E.Q4K, 4096, 1024), (E.Q4K, 4096, 14336),
