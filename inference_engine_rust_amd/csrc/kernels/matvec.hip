@@ -84,6 +84,7 @@ struct Lds {
   int8_t* xl;    // K
   float* sb;     // K/32 block scales
   int* sx;       // K/32 block sums of (256 * xh + xl)
+  uint8_t* wb;   // per-wave staging of raw weight bytes (coalesced-load traits only)
 };
 
 IEK_DEV void stage(const MvArgs& a, const Lds& L, int pos) {
@@ -151,13 +152,16 @@ IEK_DEV void stage(const MvArgs& a, const Lds& L, int pos) {
 
 // LDS bytes: x staging (f32: 4K; int8: 2K planes + 8 bytes per 32-block), then the residual
 // vector (EPI_RESID) and this position's RoPE (cos, sin) pairs (EPI_QKV).
-__host__ __device__ inline size_t lds_bytes(const MvArgs& a, bool i8) {
+__host__ __device__ inline size_t lds_bytes(const MvArgs& a, bool i8, size_t wbuf = 0) {
   const size_t xb = i8 ? 2 * (size_t)a.K + 8 * (size_t)(a.K / 32) : 4 * (size_t)a.K;
-  return xb + (a.epi == EPI_RESID ? 4 * (size_t)a.n[0] : 0) + (a.epi == EPI_QKV ? 8 * (size_t)a.npairs : 0);
+  return wbuf + xb + (a.epi == EPI_RESID ? 4 * (size_t)a.n[0] : 0) + (a.epi == EPI_QKV ? 8 * (size_t)a.npairs : 0);
 }
 
-IEK_DEV Lds lds_layout(const MvArgs& a, float* base, bool i8) {
+// [per-wave weight staging (wbuf bytes)][x staging][residual][RoPE]
+IEK_DEV Lds lds_layout(const MvArgs& a, float* base, bool i8, size_t wbuf = 0) {
   Lds L;
+  L.wb = reinterpret_cast<uint8_t*>(base);
+  base = reinterpret_cast<float*>(reinterpret_cast<char*>(base) + wbuf);
   char* p = reinterpret_cast<char*>(base);
   L.x = nullptr;
   L.xh = L.xl = nullptr;
@@ -207,59 +211,111 @@ IEK_DEV void quant_block(const float (&y)[32], float am, uint32_t (&h)[8], uint3
   }
 }
 
-IEK_DEV void stage_i8(const MvArgs& a, const Lds& L, int pos) {
+// The staging is split so its global loads can be issued before the first weight loads: the
+// memory counter retires in order, so x (an L2 hit) would otherwise wait behind the weight stream.
+// stage_i8_issue loads this thread's first 32-element block of x (and w), its share of the residual
+// vector and its RoPE pair into registers; stage_i8_finish consumes them.
+struct XPre {
+  float4 xv[8], wv[8];
+  float4 res[4];
+  float2 rope;
+};
+
+IEK_DEV bool res_vec(const MvArgs& a) {
+  return a.epi == EPI_RESID && (a.n[0] & 3) == 0 && a.n[0] <= 4096 && (reinterpret_cast<uintptr_t>(a.resid) & 15) == 0;
+}
+
+IEK_DEV void stage_i8_issue(const MvArgs& a, XPre& p, int pos) {
+  const int tid = threadIdx.x, nb = a.K >> 5, bc = min(tid, nb - 1);
+  const float4* x4 = reinterpret_cast<const float4*>(a.x) + (size_t)bc * 8;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) p.xv[t] = x4[t];
+  if (a.norm_w) {
+    const float4* w4 = reinterpret_cast<const float4*>(a.norm_w) + (size_t)bc * 8;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) p.wv[t] = w4[t];
+  } else {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) p.wv[t] = make_float4(1.f, 1.f, 1.f, 1.f);
+  }
+  if (res_vec(a)) {
+    const float4* r4 = reinterpret_cast<const float4*>(a.resid);
+    const int n4 = a.n[0] >> 2;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) p.res[u] = r4[min(tid + 256 * u, n4 - 1)];
+  }
+  if (a.epi == EPI_QKV)
+    p.rope = reinterpret_cast<const float2*>(a.rope_cs)[(size_t)pos * a.npairs + min(tid, a.npairs - 1)];
+}
+
+IEK_DEV void quant_store(const MvArgs& a, const Lds& L, int b, const float4 (&xv)[8], const float4 (&wv)[8], float& ss,
+                         float& amax) {
+  float y[32];
+  float am = 0.f, sq = 0.f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const float xs[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+    const float ws[4] = {wv[t].x, wv[t].y, wv[t].z, wv[t].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sq += xs[e] * xs[e];
+      y[4 * t + e] = a.norm_w ? mul_rn(xs[e], ws[e]) : xs[e];
+      am = fmaxf(am, fabsf(y[4 * t + e]));
+    }
+  }
+  uint32_t h[8], l[8];
+  int sum;
+  quant_block(y, am, h, l, sum);
+  amax = am;
+  if (b < (a.K >> 5)) {
+    ss += sq;
+    uint4* ph = reinterpret_cast<uint4*>(L.xh + 32 * b);
+    uint4* pl = reinterpret_cast<uint4*>(L.xl + 32 * b);
+    ph[0] = make_uint4(h[0], h[1], h[2], h[3]);
+    ph[1] = make_uint4(h[4], h[5], h[6], h[7]);
+    pl[0] = make_uint4(l[0], l[1], l[2], l[3]);
+    pl[1] = make_uint4(l[4], l[5], l[6], l[7]);
+    L.sx[b] = sum;
+  }
+}
+
+IEK_DEV void stage_i8_finish(const MvArgs& a, const Lds& L, int pos, const XPre& p) {
   const int K = a.K, tid = threadIdx.x, nb = K >> 5;
   float ss = 0.f;
-  float amax[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int b = tid + 256 * j;
-    const int bc = min(b, nb - 1);
+  float amax[2] = {0.f, 0.f};
+  quant_store(a, L, tid, p.xv, p.wv, ss, amax[0]);
+  if (nb > 256) {
+    // second block of this thread (K > 8192), loaded here
+    const int b = tid + 256, bc = min(b, nb - 1);
+    float4 xv[8], wv[8];
     const float4* x4 = reinterpret_cast<const float4*>(a.x) + (size_t)bc * 8;
-    float4 xv[8], wv[8] = {};
 #pragma unroll
     for (int t = 0; t < 8; ++t) xv[t] = x4[t];
     if (a.norm_w) {
       const float4* w4 = reinterpret_cast<const float4*>(a.norm_w) + (size_t)bc * 8;
 #pragma unroll
       for (int t = 0; t < 8; ++t) wv[t] = w4[t];
-    }
-    float y[32];
-    float am = 0.f, sq = 0.f;
+    } else {
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const float xs[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
-      const float ws[4] = {wv[t].x, wv[t].y, wv[t].z, wv[t].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        sq += xs[e] * xs[e];
-        y[4 * t + e] = a.norm_w ? mul_rn(xs[e], ws[e]) : xs[e];
-        am = fmaxf(am, fabsf(y[4 * t + e]));
-      }
+      for (int t = 0; t < 8; ++t) wv[t] = make_float4(1.f, 1.f, 1.f, 1.f);
     }
-    uint32_t h[8], l[8];
-    int sum;
-    quant_block(y, am, h, l, sum);
-    amax[j] = am;
-    if (b < nb) {
-      ss += sq;
-      uint4* ph = reinterpret_cast<uint4*>(L.xh + 32 * b);
-      uint4* pl = reinterpret_cast<uint4*>(L.xl + 32 * b);
-      ph[0] = make_uint4(h[0], h[1], h[2], h[3]);
-      ph[1] = make_uint4(h[4], h[5], h[6], h[7]);
-      pl[0] = make_uint4(l[0], l[1], l[2], l[3]);
-      pl[1] = make_uint4(l[4], l[5], l[6], l[7]);
-      L.sx[b] = sum;
-    }
-    if (nb <= 256) break;
+    quant_store(a, L, b, xv, wv, ss, amax[1]);
   }
   if (a.epi == EPI_RESID) {
     const int N = a.n[0];
-    for (int i = tid; i < N; i += 256) L.res[i] = a.resid[i];
+    if (res_vec(a)) {
+      float4* d4 = reinterpret_cast<float4*>(L.res);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (tid + 256 * u < (N >> 2)) d4[tid + 256 * u] = p.res[u];
+    } else {
+      for (int i = tid; i < N; i += 256) L.res[i] = a.resid[i];
+    }
   }
-  if (a.epi == EPI_QKV) {
-    for (int i = tid; i < 2 * a.npairs; i += 256) L.rope[i] = a.rope_cs[(size_t)pos * a.npairs * 2 + i];
-  }
+  if (a.epi == EPI_QKV && tid < a.npairs) reinterpret_cast<float2*>(L.rope)[tid] = p.rope;
+  if (a.epi == EPI_QKV)
+    for (int i = 256 + tid; i < a.npairs; i += 256)
+      reinterpret_cast<float2*>(L.rope)[i] = reinterpret_cast<const float2*>(a.rope_cs)[(size_t)pos * a.npairs + i];
   float rms = 1.f;
   if (a.norm_w) {
     __shared__ float red[4];
@@ -275,8 +331,8 @@ IEK_DEV void stage_i8(const MvArgs& a, const Lds& L, int pos) {
     if (b < nb) L.sb[b] = amax[j] / (XQ_MAX * rms);
   }
   __syncthreads();
-  __builtin_amdgcn_s_waitcnt(0);
 }
+
 
 // Segment fields picked with constant indices: a dynamic index into the by-value argument block
 // becomes a vector memory load, whose wait would also drain the in-flight weight prefetch.
@@ -503,6 +559,7 @@ IEK_DEV void argmax_flush(const MvArgs& a, unsigned long long run_key) {
 // with clamped addresses so the compiler can count them statically and keep them all in flight.
 struct Q4Tr {
   static constexpr bool I8 = false;
+  static constexpr bool WB = false;
   static constexpr int CHUNKS = 4;  // 64-value chunks per superblock
   static constexpr int BYTES = Q4K_BYTES;
   template <int NR>
@@ -539,6 +596,7 @@ struct Q4Tr {
 
 struct Q6Tr {
   static constexpr bool I8 = false;
+  static constexpr bool WB = false;
   static constexpr int CHUNKS = 8;  // 32-value chunks per superblock
   static constexpr int BYTES = Q6K_BYTES;
   template <int NR>
@@ -574,6 +632,7 @@ struct Q6Tr {
 // algebra as the reference's sum over (d*sc*q - dmin*m) * x with x replaced by s_b*X.
 struct Q4I8Tr {
   static constexpr bool I8 = true;
+  static constexpr bool WB = false;
   static constexpr int CHUNKS = 4;
   static constexpr int BYTES = Q4K_BYTES;
   template <int NR>
@@ -619,12 +678,15 @@ struct Q4I8Tr {
   }
 };
 
+constexpr int Q6_ROW_SLOT = 2048;  // LDS bytes per staged row for traits that stage raw weight bytes
+
 template <class Tr, int R, bool DUAL>
 __global__ __launch_bounds__(256) void mv_stream(MvArgs a) {
   extern __shared__ __align__(16) float lds[];
-  const Lds L = lds_layout(a, lds, Tr::I8);
   constexpr int NR = DUAL ? 2 * R : R;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  Lds L = lds_layout(a, lds, Tr::I8, Tr::WB ? 4 * NR * Q6_ROW_SLOT : 0);
+  L.wb += wave * NR * Q6_ROW_SLOT;
   const int pos = a.epi == EPI_QKV ? __builtin_amdgcn_readfirstlane(*a.pos) : 0;
   const int total = a.nseg == 1 ? a.seg_start[1] : (a.nseg == 2 ? a.seg_start[2] : a.seg_start[3]);
   const int groups = total / R;
@@ -689,6 +751,10 @@ __global__ __launch_bounds__(256) void mv_stream(MvArgs a) {
     finish(it);
   };
 
+  // x / residual / RoPE loads go out first, then the first weight buffer, so the staging work
+  // overlaps the weight fetch instead of queueing behind it.
+  XPre xp;
+  if constexpr (Tr::I8) stage_i8_issue(a, xp, pos);
   if (steps > 0) {
     const uint8_t* rows[NR];
     int c;
@@ -696,11 +762,11 @@ __global__ __launch_bounds__(256) void mv_stream(MvArgs a) {
     Tr::template load<NR>(A, rows, c);
   }
   if constexpr (Tr::I8)
-    stage_i8(a, L, pos);
+    stage_i8_finish(a, L, pos, xp);
   else
     stage(a, L, pos);
   for (int it = 0; it < steps; it += 2) {
-    {
+    if (it + 1 < steps) {
       const uint8_t* rows[NR];
       int c;
       rows_of(it + 1, rows, c);
@@ -708,7 +774,7 @@ __global__ __launch_bounds__(256) void mv_stream(MvArgs a) {
     }
     step(A, it);
     if (it + 1 >= steps) break;
-    {
+    if (it + 2 < steps) {
       const uint8_t* rows[NR];
       int c;
       rows_of(it + 2, rows, c);
@@ -766,12 +832,15 @@ static int num_cus() {
 // and LDS use allow, optionally capped by IEK_MV_PER_CU), so no second wave of workgroups forms a
 // tail; every wave then strides over the row groups.
 template <class Tr, bool DUAL>
-static void launch_stream(const MvArgs& a, int groups, size_t lds, hipStream_t st) {
+static void launch_stream(const MvArgs& a, int groups, hipStream_t st) {
   static int cap = -1;
   if (cap < 0) {
     const char* e = getenv("IEK_MV_PER_CU");
-    cap = e ? std::max(1, atoi(e)) : 8;
+    cap = e ? std::max(1, atoi(e)) : 2;
   }
+  constexpr int NR = DUAL ? 4 : 2;
+  const size_t lds = lds_bytes(a, Tr::I8, Tr::WB ? 4 * NR * Q6_ROW_SLOT : 0);
+  if (lds > 160 * 1024) fail(ST_OP, "matvec: K too large for the LDS-staged input");
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mv_stream<Tr, 2, DUAL>, 256, lds) != hipSuccess ||
       per_cu <= 0)
@@ -804,10 +873,8 @@ void launch_mv(int dt, MvArgs a, hipStream_t st) {
     const char* e = getenv("IEK_MV_F32");
     force_f32 = (e && atoi(e) != 0) ? 1 : 0;
   }
-  const bool i8 = fast && dt == DT_Q4K && !force_f32 && a.K <= 16384 &&
+  const bool i8 = fast && !force_f32 && a.K <= 16384 &&
                   (!a.norm_w || (reinterpret_cast<uintptr_t>(a.norm_w) % 16) == 0);
-  const size_t lds = lds_bytes(a, i8);
-  if (lds > 160 * 1024) fail(ST_OP, "matvec: K too large for the LDS-staged input");
   if (fast) {
     // Two rows per wave: more rows per wave spill the prefetch registers.
     const int R = 2;
@@ -816,7 +883,7 @@ void launch_mv(int dt, MvArgs a, hipStream_t st) {
     if (!ok) fast = false;
     if (fast) {
       const int groups = total / R;
-#define IEK_L(TR, DD) launch_stream<TR, DD>(a, groups, lds, st)
+#define IEK_L(TR, DD) launch_stream<TR, DD>(a, groups, st)
       if (dt == DT_Q4K && i8) {
         if (dual) IEK_L(Q4I8Tr, true);
         else IEK_L(Q4I8Tr, false);
