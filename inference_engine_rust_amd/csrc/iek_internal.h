@@ -16,7 +16,14 @@ enum Status : int {
 };
 
 // dtype ids follow the reference's TensorType (src/core/tensor.rs:13-23).
-enum DType : int { DT_F32 = 0, DT_Q4K = 1, DT_Q6K = 2, DT_Q8_0 = 3 };
+enum DType : int { DT_F32 = 0, DT_Q4K = 1, DT_Q6K = 2, DT_Q8_0 = 3,
+                   // internal only: Q6_K bytes regrouped per row for 16-byte lane loads (see
+                   // kernels/matvec.hip, Q6RTr); never crosses the C ABI
+                   DT_Q6K_R = 4 };
+// Row bytes of the regrouped Q6_K layout: nsb superblocks of [4 x 48 B lane chunks] followed by
+// nsb x 16 scale bytes and nsb x 2 d bytes, padded to 16.
+__host__ __device__ inline size_t q6r_row_bytes(size_t nsb) { return nsb * 208 + ((2 * nsb + 15) / 16) * 16; }
+void launch_repack_q6k(const void* src, int K, int N, void* dst, hipStream_t st);
 
 struct Error {
   int code;

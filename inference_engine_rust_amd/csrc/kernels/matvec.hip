@@ -562,12 +562,13 @@ struct Q4Tr {
   static constexpr bool WB = false;
   static constexpr int CHUNKS = 4;  // 64-value chunks per superblock
   static constexpr int BYTES = Q4K_BYTES;
+  IEK_DEV static size_t row_bytes(int nsb) { return (size_t)nsb * BYTES; }
   template <int NR>
   struct Buf {
     uint4 hdr[NR], qa[NR], qb[NR];
   };
   template <int NR>
-  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c) {
+  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c, int nsb) {
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
       const uint8_t* blk = rows[r] + (size_t)(c >> 2) * Q4K_BYTES;
@@ -599,12 +600,13 @@ struct Q6Tr {
   static constexpr bool WB = false;
   static constexpr int CHUNKS = 8;  // 32-value chunks per superblock
   static constexpr int BYTES = Q6K_BYTES;
+  IEK_DEV static size_t row_bytes(int nsb) { return (size_t)nsb * BYTES; }
   template <int NR>
   struct Buf {
     Q6Raw q[NR];
   };
   template <int NR>
-  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c) {
+  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c, int nsb) {
 #pragma unroll
     for (int r = 0; r < NR; ++r) q6_load(rows[r] + (size_t)(c >> 3) * Q6K_BYTES, (c >> 2) & 1, c & 3, b.q[r]);
   }
@@ -635,11 +637,12 @@ struct Q4I8Tr {
   static constexpr bool WB = false;
   static constexpr int CHUNKS = 4;
   static constexpr int BYTES = Q4K_BYTES;
+  IEK_DEV static size_t row_bytes(int nsb) { return (size_t)nsb * BYTES; }
   template <int NR>
   using Buf = Q4Tr::Buf<NR>;
   template <int NR>
-  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c) {
-    Q4Tr::load<NR>(b, rows, c);
+  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c, int nsb) {
+    Q4Tr::load<NR>(b, rows, c, nsb);
   }
   template <int NR>
   IEK_DEV static void compute(const Buf<NR>& b, int c, const Lds& L, float (&acc)[NR]) {
@@ -680,6 +683,174 @@ struct Q4I8Tr {
 
 constexpr int Q6_ROW_SLOT = 2048;  // LDS bytes per staged row for traits that stage raw weight bytes
 
+// Q6_K against the int8-staged x. The 6-bit values are assembled per byte as in q6k_dot, made
+// signed (q - 32) bytewise with (q + 0x60) ^ 0x80, and two v_dot4 per 4 weights give
+// S = sum (q - 32) * X exactly; each 8-weight run contributes s_b * (d * sc) * S.
+struct Q6I8Tr {
+  static constexpr bool I8 = true;
+  static constexpr bool WB = false;
+  static constexpr int CHUNKS = 8;
+  static constexpr int BYTES = Q6K_BYTES;
+  IEK_DEV static size_t row_bytes(int nsb) { return (size_t)nsb * BYTES; }
+  template <int NR>
+  using Buf = Q6Tr::Buf<NR>;
+  template <int NR>
+  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c, int nsb) {
+    Q6Tr::load<NR>(b, rows, c, nsb);
+  }
+  template <int NR>
+  IEK_DEV static void compute(const Buf<NR>& b, int c, const Lds& L, float (&acc)[NR]) {
+    const int e0 = (c >> 3) * QK_K + 128 * ((c >> 2) & 1) + 8 * (c & 3);
+    uint32_t xh[8], xl[8];
+    float sq[4];
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const uint2 vh = *reinterpret_cast<const uint2*>(L.xh + e0 + 32 * qd);
+      const uint2 vl = *reinterpret_cast<const uint2*>(L.xl + e0 + 32 * qd);
+      xh[2 * qd] = vh.x, xh[2 * qd + 1] = vh.y, xl[2 * qd] = vl.x, xl[2 * qd + 1] = vl.y;
+      sq[qd] = L.sb[(e0 + 32 * qd) >> 5];
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const Q6Raw& q = b.q[r];
+      const uint32_t sh_ql = q.sh_ql, sh_s = q.sh_s;
+      const uint32_t A[2] = {__builtin_amdgcn_alignbyte(q.a[1], q.a[0], sh_ql), __builtin_amdgcn_alignbyte(q.a[2], q.a[1], sh_ql)};
+      const uint32_t B[2] = {__builtin_amdgcn_alignbyte(q.b[1], q.b[0], sh_ql), __builtin_amdgcn_alignbyte(q.b[2], q.b[1], sh_ql)};
+      const uint32_t H[2] = {__builtin_amdgcn_alignbyte(q.h[1], q.h[0], sh_ql), __builtin_amdgcn_alignbyte(q.h[2], q.h[1], sh_ql)};
+      const uint32_t S0 = __builtin_amdgcn_alignbyte(q.s[1], q.s[0], sh_s), S1 = __builtin_amdgcn_alignbyte(q.s[2], q.s[1], sh_s);
+      const float sc[4] = {(float)(int8_t)(S0 & 0xFF), (float)(int8_t)((S0 >> 16) & 0xFF), (float)(int8_t)(S1 & 0xFF),
+                           (float)(int8_t)((S1 >> 16) & 0xFF)};
+      const float d = half_bits_to_float(q.d);
+      int hs[4] = {0, 0, 0, 0}, ls[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint32_t qq[4] = {(A[t] & 0x0F0F0F0Fu) | ((H[t] << 4) & 0x30303030u),
+                                (B[t] & 0x0F0F0F0Fu) | ((H[t] << 2) & 0x30303030u),
+                                ((A[t] >> 4) & 0x0F0F0F0Fu) | (H[t] & 0x30303030u),
+                                ((B[t] >> 4) & 0x0F0F0F0Fu) | ((H[t] >> 2) & 0x30303030u)};
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const int sgn = (int)((qq[qd] + 0x60606060u) ^ 0x80808080u);  // bytes q - 32 as int8
+          hs[qd] = __builtin_amdgcn_sdot4(sgn, (int)xh[2 * qd + t], hs[qd], false);
+          ls[qd] = __builtin_amdgcn_sdot4(sgn, (int)xl[2 * qd + t], ls[qd], false);
+        }
+      }
+      float sum = 0.f;
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) sum += sq[qd] * ((d * sc[qd]) * (float)(hs[qd] * 256 + ls[qd]));
+      acc[r] += sum;
+    }
+  }
+};
+
+// Q6_K in the regrouped per-row layout (DT_Q6K_R, built once at model load by
+// launch_repack_q6k): for superblock j of a row, lane chunk k = 2h + j16 holds the 16 ql bytes of
+// quarters 0/2, the 16 ql bytes of quarters 1/3 and the 16 qh bytes for weights l = 16*j16 ..
+// 16*j16+15 of half h (48 contiguous, 16-byte aligned bytes), its four sub-block scales as one
+// dword and the superblock's d. A lane's 64 weights are thus three coalesced 16-byte loads plus
+// two small ones, instead of thirteen dword loads per 32 weights from the 210-byte blocks. The
+// values are the same bytes, so the dequantised weights are unchanged.
+struct Q6RTr {
+  static constexpr bool I8 = true;
+  static constexpr bool WB = false;
+  static constexpr int CHUNKS = 4;
+  static constexpr int BYTES = 208;
+  IEK_DEV static size_t row_bytes(int nsb) { return q6r_row_bytes(nsb); }
+  template <int NR>
+  struct Buf {
+    uint4 qa[NR], qb[NR], qh[NR];
+    uint32_t sc[NR], d[NR];
+  };
+  template <int NR>
+  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c, int nsb) {
+    const int j = c >> 2, k = c & 3;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const uint8_t* m = rows[r] + (size_t)j * 192 + 48 * k;
+      b.qa[r] = *reinterpret_cast<const uint4*>(m);
+      b.qb[r] = *reinterpret_cast<const uint4*>(m + 16);
+      b.qh[r] = *reinterpret_cast<const uint4*>(m + 32);
+      b.sc[r] = *reinterpret_cast<const uint32_t*>(rows[r] + (size_t)nsb * 192 + 16 * j + 4 * k);
+      b.d[r] = *reinterpret_cast<const uint16_t*>(rows[r] + (size_t)nsb * 208 + 2 * j);
+    }
+  }
+  template <int NR>
+  IEK_DEV static void compute(const Buf<NR>& b, int c, const Lds& L, float (&acc)[NR]) {
+    const int j = c >> 2, k = c & 3, h = k >> 1, j16 = k & 1;
+    const int e0 = j * QK_K + 128 * h + 16 * j16;
+    uint4 XH[4], XL[4];
+    float sq[4];
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      XH[qd] = *reinterpret_cast<const uint4*>(L.xh + e0 + 32 * qd);
+      XL[qd] = *reinterpret_cast<const uint4*>(L.xl + e0 + 32 * qd);
+      sq[qd] = L.sb[(e0 >> 5) + qd];
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const uint32_t A[4] = {b.qa[r].x, b.qa[r].y, b.qa[r].z, b.qa[r].w};
+      const uint32_t B[4] = {b.qb[r].x, b.qb[r].y, b.qb[r].z, b.qb[r].w};
+      const uint32_t H[4] = {b.qh[r].x, b.qh[r].y, b.qh[r].z, b.qh[r].w};
+      int hs[4] = {0, 0, 0, 0}, ls[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t qq[4] = {(A[t] & 0x0F0F0F0Fu) | ((H[t] << 4) & 0x30303030u),
+                                (B[t] & 0x0F0F0F0Fu) | ((H[t] << 2) & 0x30303030u),
+                                ((A[t] >> 4) & 0x0F0F0F0Fu) | (H[t] & 0x30303030u),
+                                ((B[t] >> 4) & 0x0F0F0F0Fu) | ((H[t] >> 2) & 0x30303030u)};
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const uint32_t xhw = t == 0 ? XH[qd].x : t == 1 ? XH[qd].y : t == 2 ? XH[qd].z : XH[qd].w;
+          const uint32_t xlw = t == 0 ? XL[qd].x : t == 1 ? XL[qd].y : t == 2 ? XL[qd].z : XL[qd].w;
+          const int sgn = (int)((qq[qd] + 0x60606060u) ^ 0x80808080u);  // bytes q - 32 as int8
+          hs[qd] = __builtin_amdgcn_sdot4(sgn, (int)xhw, hs[qd], false);
+          ls[qd] = __builtin_amdgcn_sdot4(sgn, (int)xlw, ls[qd], false);
+        }
+      }
+      const float d = half_bits_to_float(b.d[r]);
+      float sum = 0.f;
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd)
+        sum += sq[qd] * ((d * (float)(int8_t)((b.sc[r] >> (8 * qd)) & 0xFF)) * (float)(hs[qd] * 256 + ls[qd]));
+      acc[r] += sum;
+    }
+  }
+};
+
+// One thread per (row, superblock, lane chunk): regroup a Q6_K tensor [K, N] (K % 256 == 0) into
+// the DT_Q6K_R layout above. Runs once at model load.
+__global__ void repack_q6k_kernel(const uint8_t* __restrict__ src, int nsb, int N, uint8_t* __restrict__ dst) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)N * nsb * 4) return;
+  const int k = (int)(i & 3), j = (int)((i >> 2) % nsb);
+  const size_t n = (i >> 2) / nsb;
+  const uint8_t* blk = src + (n * nsb + j) * Q6K_BYTES;
+  uint8_t* row = dst + n * q6r_row_bytes(nsb);
+  const int h = k >> 1, j16 = k & 1;
+  uint8_t* m = row + (size_t)j * 192 + 48 * k;
+  for (int t = 0; t < 16; ++t) {
+    m[t] = blk[64 * h + 16 * j16 + t];
+    m[16 + t] = blk[64 * h + 32 + 16 * j16 + t];
+    m[32 + t] = blk[128 + 32 * h + 16 * j16 + t];
+  }
+  uint8_t* sc = row + (size_t)nsb * 192 + 16 * j + 4 * k;
+  for (int qd = 0; qd < 4; ++qd) sc[qd] = blk[192 + 8 * h + j16 + 2 * qd];
+  if (k == 0) {
+    uint8_t* d = row + (size_t)nsb * 208 + 2 * j;
+    d[0] = blk[208];
+    d[1] = blk[209];
+  }
+}
+
+void launch_repack_q6k(const void* src, int K, int N, void* dst, hipStream_t st) {
+  if (K % QK_K != 0) fail(ST_OP, "repack_q6k: K must be a multiple of 256");
+  const int nsb = K / QK_K;
+  IEK_HIP(hipMemsetAsync(dst, 0, (size_t)N * q6r_row_bytes(nsb), st));
+  const size_t threads = (size_t)N * nsb * 4;
+  hipLaunchKernelGGL(repack_q6k_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                     (const uint8_t*)src, nsb, N, (uint8_t*)dst);
+}
+
 template <class Tr, int R, bool DUAL>
 __global__ __launch_bounds__(256) void mv_stream(MvArgs a) {
   extern __shared__ __align__(16) float lds[];
@@ -692,7 +863,8 @@ __global__ __launch_bounds__(256) void mv_stream(MvArgs a) {
   const int groups = total / R;
   const int stride = gridDim.x * 4;
   const int g0 = blockIdx.x * 4 + wave;
-  const size_t rb = (size_t)(a.K / QK_K) * Tr::BYTES;
+  const int nsb = a.K / QK_K;
+  const size_t rb = Tr::row_bytes(nsb);
   const int nchunk = (a.K / QK_K) * Tr::CHUNKS;
   const int npass = (nchunk + WAVE - 1) / WAVE;
   // number of (group, pass) steps of this wave
@@ -759,7 +931,7 @@ __global__ __launch_bounds__(256) void mv_stream(MvArgs a) {
     const uint8_t* rows[NR];
     int c;
     rows_of(0, rows, c);
-    Tr::template load<NR>(A, rows, c);
+    Tr::template load<NR>(A, rows, c, nsb);
   }
   if constexpr (Tr::I8)
     stage_i8_finish(a, L, pos, xp);
@@ -770,7 +942,7 @@ __global__ __launch_bounds__(256) void mv_stream(MvArgs a) {
       const uint8_t* rows[NR];
       int c;
       rows_of(it + 1, rows, c);
-      Tr::template load<NR>(B, rows, c);
+      Tr::template load<NR>(B, rows, c, nsb);
     }
     step(A, it);
     if (it + 1 >= steps) break;
@@ -778,7 +950,7 @@ __global__ __launch_bounds__(256) void mv_stream(MvArgs a) {
       const uint8_t* rows[NR];
       int c;
       rows_of(it + 2, rows, c);
-      Tr::template load<NR>(A, rows, c);
+      Tr::template load<NR>(A, rows, c, nsb);
     }
     step(B, it + 1);
   }
@@ -850,6 +1022,15 @@ static void launch_stream(const MvArgs& a, int groups, hipStream_t st) {
   hipLaunchKernelGGL((mv_stream<Tr, 2, DUAL>), dim3(blocks), dim3(256), lds, st, a);
 }
 
+bool mv_int8_staging() {
+  static int v = -1;
+  if (v < 0) {
+    const char* e = getenv("IEK_MV_F32");
+    v = (e && atoi(e) != 0) ? 0 : 1;
+  }
+  return v == 1;
+}
+
 void launch_mv(int dt, MvArgs a, hipStream_t st) {
   int total = 0;
   for (int i = 0; i < a.nseg; ++i) {
@@ -864,15 +1045,12 @@ void launch_mv(int dt, MvArgs a, hipStream_t st) {
     a.nseg = 1;
     total = a.n[0];
   }
-  bool fast = (dt == DT_Q4K || dt == DT_Q6K) && a.K % QK_K == 0 && (reinterpret_cast<uintptr_t>(a.x) % 16) == 0;
+  bool fast = (dt == DT_Q4K || dt == DT_Q6K || dt == DT_Q6K_R) && a.K % QK_K == 0 &&
+              (reinterpret_cast<uintptr_t>(a.x) % 16) == 0;
   for (int i = 0; i < (dual ? 2 : a.nseg); ++i) fast = fast && (reinterpret_cast<uintptr_t>(a.w[i]) % 16) == 0;
-  // Q4_K takes the int8-staged x (v_dot4) path when x and the norm weight are 16-byte aligned and
-  // every 32-element block fits the two-blocks-per-thread staging; IEK_MV_F32=1 keeps the f32 path.
-  static int force_f32 = -1;
-  if (force_f32 < 0) {
-    const char* e = getenv("IEK_MV_F32");
-    force_f32 = (e && atoi(e) != 0) ? 1 : 0;
-  }
+  // K-quants take the int8-staged x (v_dot4) path when x and the norm weight are 16-byte aligned
+  // and every 32-element block fits the two-blocks-per-thread staging; IEK_MV_F32=1 keeps f32.
+  const bool force_f32 = !mv_int8_staging();
   const bool i8 = fast && !force_f32 && a.K <= 16384 &&
                   (!a.norm_w || (reinterpret_cast<uintptr_t>(a.norm_w) % 16) == 0);
   if (fast) {
@@ -884,12 +1062,19 @@ void launch_mv(int dt, MvArgs a, hipStream_t st) {
     if (fast) {
       const int groups = total / R;
 #define IEK_L(TR, DD) launch_stream<TR, DD>(a, groups, st)
-      if (dt == DT_Q4K && i8) {
+      if (dt == DT_Q6K_R) {
+        if (!i8) fail(ST_OP, "matvec: the regrouped Q6_K layout needs the int8-staged path");
+        if (dual) IEK_L(Q6RTr, true);
+        else IEK_L(Q6RTr, false);
+      } else if (dt == DT_Q4K && i8) {
         if (dual) IEK_L(Q4I8Tr, true);
         else IEK_L(Q4I8Tr, false);
       } else if (dt == DT_Q4K) {
         if (dual) IEK_L(Q4Tr, true);
         else IEK_L(Q4Tr, false);
+      } else if (i8) {
+        if (dual) IEK_L(Q6I8Tr, true);
+        else IEK_L(Q6I8Tr, false);
       } else {
         if (dual) IEK_L(Q6Tr, true);
         else IEK_L(Q6Tr, false);
@@ -901,6 +1086,7 @@ void launch_mv(int dt, MvArgs a, hipStream_t st) {
   const size_t lds_f = lds_bytes(a, false);
   if (lds_f > 160 * 1024) fail(ST_OP, "matvec: K too large for the LDS-staged input");
   if (a.epi == EPI_QKV) fail(ST_OP, "matvec: fused Q/K/V epilogue needs the aligned K-quant path");
+  if (dt == DT_Q6K_R) fail(ST_OP, "matvec: the regrouped Q6_K layout needs K % 256 == 0 and aligned inputs");
   hipLaunchKernelGGL(mv_generic, dim3((total + 3) / 4), dim3(256), lds_f, st, a, dt);
 }
 

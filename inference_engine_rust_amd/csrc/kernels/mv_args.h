@@ -47,5 +47,7 @@ __host__ __device__ inline int seg_of(const MvArgs& a, int row) {
 }
 
 void launch_mv(int dt, MvArgs a, hipStream_t st);
+// Whether K-quant matvecs stage x as int8 planes (default; IEK_MV_F32=1 selects the f32 path).
+bool mv_int8_staging();
 
 }  // namespace iek

@@ -370,6 +370,7 @@ Model::~Model() {
   for (auto& t : rope_tables)
     if (t.dev) (void)hipFree(t.dev);
   if (blob) (void)hipFree(blob);
+  if (blob_r) (void)hipFree(blob_r);
 }
 
 Model* load_model(const std::string& path, int device) {
@@ -533,6 +534,33 @@ Model* load_model(const std::string& path, int device) {
     d.dev = (char*)m->blob + s.off;
     d.host_f32 = host_f32[slot_of[w.name]];
     m->by_name[w.name] = &d;
+  }
+
+  // Regrouped copies of the Q6_K matrices the decode matvec streams (ffn_down, LM head): same
+  // bytes, laid out for 16-byte lane loads (DT_Q6K_R). The native blocks stay in place for every
+  // other consumer.
+  {
+    std::vector<DevTensor*> q6;
+    for (auto& L : m->layers)
+      if (L.down.present() && L.down.dtype == DT_Q6K && L.down.dims.size() == 2 && L.down.dims[0] % 256 == 0)
+        q6.push_back(&L.down);
+    if (m->lm_head.present() && m->lm_head.dtype == DT_Q6K && m->lm_head.dims.size() == 2 &&
+        m->lm_head.dims[0] % 256 == 0)
+      q6.push_back(&m->lm_head);
+    size_t total_r = 0;
+    std::vector<size_t> off_r;
+    for (DevTensor* t : q6) {
+      off_r.push_back(total_r);
+      total_r += (q6r_row_bytes(t->dims[0] / 256) * t->dims[1] + 255) / 256 * 256;
+    }
+    if (total_r) {
+      IEK_HIP(hipMalloc(&m->blob_r, total_r));
+      for (size_t i = 0; i < q6.size(); ++i) {
+        q6[i]->dev_r = (char*)m->blob_r + off_r[i];
+        launch_repack_q6k(q6[i]->dev, (int)q6[i]->dims[0], (int)q6[i]->dims[1], q6[i]->dev_r, nullptr);
+      }
+      IEK_HIP(hipDeviceSynchronize());
+    }
   }
 
   // Shape checks the reference performs lazily (rmsnorm/matmul length checks).

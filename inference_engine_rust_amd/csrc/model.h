@@ -84,6 +84,7 @@ struct DevTensor {
   std::vector<size_t> dims;
   size_t bytes = 0;
   void* dev = nullptr;
+  void* dev_r = nullptr;        // Q6_K only: regrouped copy (DT_Q6K_R) for the decode matvec
   std::vector<float> host_f32;  // small F32 tensors also kept on the host (norms, scales)
   bool present() const { return dev != nullptr; }
 };
@@ -110,6 +111,7 @@ struct Model {
   std::string path;
   void* blob = nullptr;  // one HBM allocation for every weight
   size_t blob_bytes = 0;
+  void* blob_r = nullptr;  // regrouped copies of the Q6_K matvec weights (ffn_down, output)
   DevTensor token_embd, output_norm, lm_head;
   std::vector<LayerTensors> layers;
   DevTensor ple_token_embd, ple_model_proj, ple_proj_norm;

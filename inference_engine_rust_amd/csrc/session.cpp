@@ -139,6 +139,17 @@ void Session::ensure_rows(int rows) {
   rows_cap_ = rows;
 }
 
+// The weight copy the decode matvec streams: the regrouped Q6_K layout when the model built one
+// and the int8-staged path (which it requires) is active, else the native blocks.
+static const void* mv_weight(const DevTensor& t, int K, int* dt) {
+  if (t.dev_r && mv_int8_staging() && K <= 16384) {
+    *dt = DT_Q6K_R;
+    return t.dev_r;
+  }
+  *dt = t.dtype;
+  return t.dev;
+}
+
 // One projection over `rows` activation rows: matvec for a single row, GEMM otherwise. `xs` is
 // the fp16 (hi, lo) split of `a` when the caller has made it (rows*K halves each), else null.
 static void project(const DevTensor& w, const float* a, const __half* xs, int rows, int K, int N, float* out,
@@ -273,7 +284,8 @@ void Session::layer_decode(int li, bool last) {
   launch_mv(L.gate.dtype, f, st_);
   MvArgs dn{};
   dn.nseg = 1;
-  dn.w[0] = (const uint8_t*)L.down.dev;
+  int down_dt = L.down.dtype;
+  dn.w[0] = (const uint8_t*)mv_weight(L.down, S.ffn_dim, &down_dt);
   dn.out[0] = xdec_;
   dn.n[0] = H_;
   dn.x = actd_;
@@ -281,7 +293,7 @@ void Session::layer_decode(int li, bool last) {
   dn.epi = EPI_RESID;
   dn.resid = xdec_;
   dn.pos_inc = last ? d_pos_ : nullptr;
-  launch_mv(L.down.dtype, dn, st_);
+  launch_mv(down_dt, dn, st_);
 }
 
 void Session::layer_decode_unfused(int li) {
@@ -391,7 +403,8 @@ void Session::logits_body(bool argmax) {
   const Config& c = m_->cfg;
   MvArgs a{};
   a.nseg = 1;
-  a.w[0] = (const uint8_t*)m_->lm_head.dev;
+  int head_dt = m_->lm_head.dtype;
+  a.w[0] = (const uint8_t*)mv_weight(m_->lm_head, H_, &head_dt);
   a.out[0] = logits_;
   a.n[0] = c.vocab;
   a.x = xdec_;
@@ -406,10 +419,10 @@ void Session::logits_body(bool argmax) {
     a.amax_key = d_key_;
     a.amax_flag = d_flag_;
     a.softcap = c.has_softcap ? c.softcap : 0.f;
-    launch_mv(w.dtype, a, st_);
+    launch_mv(head_dt, a, st_);
   } else {
     a.epi = EPI_STORE;
-    launch_mv(w.dtype, a, st_);
+    launch_mv(head_dt, a, st_);
     if (c.has_softcap) launch_softcap(logits_, c.vocab, c.softcap, st_);
   }
 }
