@@ -19,12 +19,65 @@ constexpr int SPLIT = 64;
 // rows (fp16) into LDS together in one burst of clamped, unconditional 16-byte loads, then wave w
 // takes query heads w and w+4 of the GQA group. Lane j scores key j against its head (K row from
 // LDS, q broadcast from LDS), the wave forms the slice softmax, and for P.V lane l owns head dims
-// [DPL*l, DPL*l + DPL). Slices publish (max, sum, o[]) partials that a second launch merges per
-// query head (a cross-workgroup merge inside one launch would need device-scope fences, which
-// write back the L2 of every XCD).
+// [DPL*l, DPL*l + DPL). Slices publish (max, sum, o[]) partials; the last workgroup of each KV
+// head to finish merges its query heads (counted with an agent-scope acq_rel atomic per KV head).
+// Merge of the live slice partials of query head h by one wave: global (max, sum) over slices,
+// then each lane folds its head dims of every slice with the rescaled weights.
+template <int HD>
+IEK_DEV void merge_head(const float* __restrict__ part, float* __restrict__ out, int h, int nsplit, int s0, int nlive,
+                        float* wsl) {
+  constexpr int DPL = HD / 64;
+  const int lane = threadIdx.x & 63;
+  const float* pr = part + (size_t)h * nsplit * (HD + 2);
+  float M = -INFINITY;
+  for (int s = s0 + lane; s < nlive; s += 64) M = fmaxf(M, pr[(size_t)s * (HD + 2)]);
+  M = wave_max(M);
+  float L = 0.f;
+  for (int s = s0 + lane; s < nlive; s += 64) {
+    const float w = expf(pr[(size_t)s * (HD + 2)] - M);
+    L += pr[(size_t)s * (HD + 2) + 1] * w;
+    if (s - s0 < 256) wsl[s - s0] = w;
+  }
+  L = wave_sum(L);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float acc[DPL];
+#pragma unroll
+  for (int t = 0; t < DPL; ++t) acc[t] = 0.f;
+  const int ns = min(nlive - s0, 256);
+  for (int s8 = 0; s8 < ns; s8 += 8) {
+    // clamped, unconditional loads: all eight slices' rows are in flight together
+    float v[8][DPL];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const size_t row = (size_t)(s0 + min(s8 + u, ns - 1)) * (HD + 2) + 2 + DPL * lane;
+#pragma unroll
+      for (int t = 0; t < DPL; ++t) v[u][t] = pr[row + t];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (s8 + u < ns) {
+        const float w = wsl[s8 + u];
+#pragma unroll
+        for (int t = 0; t < DPL; ++t) acc[t] += v[u][t] * w;
+      }
+    }
+  }
+  // slices beyond the 256 staged weights (contexts over 16K keys) use direct weights
+  for (int s = s0 + 256; s < nlive; ++s) {
+    const float w = expf(pr[(size_t)s * (HD + 2)] - M);
+#pragma unroll
+    for (int t = 0; t < DPL; ++t) acc[t] += pr[(size_t)s * (HD + 2) + 2 + DPL * lane + t] * w;
+  }
+#pragma unroll
+  for (int t = 0; t < DPL; ++t) out[(size_t)h * HD + DPL * lane + t] = acc[t] / L;
+}
+
 template <int HD>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, const __half* __restrict__ kc,
                                                           const __half* __restrict__ vc, float* __restrict__ part,
+                                                          float* __restrict__ out, int* __restrict__ counters,
                                                           int n_heads, int n_kv, int ctx, const int* pos_dev,
                                                           int window, float scale, int nsplit) {
   constexpr int DPL = HD / 64;        // head dims per lane in the PV phase
@@ -117,90 +170,53 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
     for (int t = 0; t < DPL; ++t) pr[2 + DPL * lane + t] = o[t];
     __builtin_amdgcn_wave_barrier();  // ps[wave] is rewritten by the next head of this wave
   }
-}
-
-// Merge the live slices of one query head: (max, sum) of 64 slices at a time across lanes, then
-// each lane streams its head dims of every slice partial with the loads issued back to back.
-template <int HD>
-__global__ __launch_bounds__(64) void attn_decode_merge_kernel(const float* __restrict__ part, float* __restrict__ out,
-                                                               int nsplit, const int* pos_dev, int window) {
-  constexpr int DPL = HD / 64;
-  const int h = blockIdx.x, lane = threadIdx.x;
-  const int total = *pos_dev + 1;
-  const int jmin = (window > 0 && total > window) ? total - window : 0;
-  const int nlive = (total + SPLIT - 1) / SPLIT;
-  const int s0 = jmin / SPLIT;
-  __shared__ float wsl[256];
-  const float* pr = part + (size_t)h * nsplit * (HD + 2);
-  float M = -INFINITY;
-  for (int s = s0 + lane; s < nlive; s += 64) M = fmaxf(M, pr[(size_t)s * (HD + 2)]);
-  M = wave_max(M);
-  float L = 0.f;
-  for (int s = s0 + lane; s < nlive; s += 64) {
-    const float w = expf(pr[(size_t)s * (HD + 2)] - M);
-    L += pr[(size_t)s * (HD + 2) + 1] * w;
-    if (s - s0 < 256) wsl[s - s0] = w;
-  }
-  L = wave_sum(L);
+  // The last workgroup of this KV head to finish merges the group's heads. Release: the
+  // workgroup barrier orders every wave's partial stores before thread 0's agent-scope acq_rel
+  // add (which writes back this XCD's L2); the last arrival's acquire side invalidates its L2
+  // before the partials are read. The counter is reset for the next launch.
+  __shared__ int last;
   __syncthreads();
-  float acc[DPL];
-#pragma unroll
-  for (int t = 0; t < DPL; ++t) acc[t] = 0.f;
-  const int ns = min(nlive - s0, 256);
-  for (int s8 = 0; s8 < ns; s8 += 8) {
-    // clamped, unconditional loads: all eight slices' rows are in flight together
-    float v[8][DPL];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const size_t row = (size_t)(s0 + min(s8 + u, ns - 1)) * (HD + 2) + 2 + DPL * lane;
-#pragma unroll
-      for (int t = 0; t < DPL; ++t) v[u][t] = pr[row + t];
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      if (s8 + u < ns) {
-        const float w = wsl[s8 + u];
-#pragma unroll
-        for (int t = 0; t < DPL; ++t) acc[t] += v[u][t] * w;
-      }
-    }
+  if (tid == 0) {
+    const int s0 = jmin / SPLIT, nlive = (total + SPLIT - 1) / SPLIT;
+    const int old = __hip_atomic_fetch_add(&counters[kvh], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    last = old == nlive - s0 - 1;
+    if (last) __hip_atomic_store(&counters[kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  // slices beyond the 256 staged weights (contexts over 16K keys) use direct weights
-  for (int s = s0 + 256; s < nlive; ++s) {
-    const float w = expf(pr[(size_t)s * (HD + 2)] - M);
-#pragma unroll
-    for (int t = 0; t < DPL; ++t) acc[t] += pr[(size_t)s * (HD + 2) + 2 + DPL * lane + t] * w;
-  }
-#pragma unroll
-  for (int t = 0; t < DPL; ++t) out[(size_t)h * HD + DPL * lane + t] = acc[t] / L;
+  __syncthreads();
+  if (!last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  const int s0 = jmin / SPLIT, nlive = (total + SPLIT - 1) / SPLIT;
+  __shared__ float wsl[4][256];
+  for (int g = wave; g < G; g += 4) merge_head<HD>(part, out, kvh * G + g, nsplit, s0, nlive, wsl[wave]);
 }
 
 template <int HD>
 static void attn_decode_hd(dim3 grid, hipStream_t st, const float* q, const __half* kc, const __half* vc, float* out,
-                           float* part, int n_heads, int n_kv, int ctx, const int* pos_dev, int window, float scale,
-                           int nsplit) {
-  hipLaunchKernelGGL(attn_decode_kernel<HD>, grid, dim3(256), 0, st, q, kc, vc, part, n_heads, n_kv, ctx, pos_dev,
-                     window, scale, nsplit);
-  hipLaunchKernelGGL(attn_decode_merge_kernel<HD>, dim3(n_heads), dim3(64), 0, st, part, out, nsplit, pos_dev, window);
+                           float* part, int* counters, int n_heads, int n_kv, int ctx, const int* pos_dev, int window,
+                           float scale, int nsplit) {
+  hipLaunchKernelGGL(attn_decode_kernel<HD>, grid, dim3(256), 0, st, q, kc, vc, part, out, counters, n_heads, n_kv,
+                     ctx, pos_dev, window, scale, nsplit);
 }
 
 void launch_attn_decode(const float* q, const __half* kc, const __half* vc, float* out, float* part, int* counters,
                         int n_heads, int n_kv, int head_dim, int ctx, const int* pos_dev, int window, float scale,
                         int max_len, hipStream_t st) {
-  (void)counters;
   const int nsplit = (max_len + SPLIT - 1) / SPLIT;
   dim3 grid(n_kv, nsplit);
   if (n_kv <= 0 || n_heads % n_kv != 0 || n_heads / n_kv > 8)
     fail(ST_OP, "attention: GQA group must divide the heads and be at most 8");
   switch (head_dim) {
     case 64:
-      attn_decode_hd<64>(grid, st, q, kc, vc, out, part, n_heads, n_kv, ctx, pos_dev, window, scale, nsplit);
+      attn_decode_hd<64>(grid, st, q, kc, vc, out, part, counters, n_heads, n_kv, ctx, pos_dev, window, scale,
+                          nsplit);
       break;
     case 128:
-      attn_decode_hd<128>(grid, st, q, kc, vc, out, part, n_heads, n_kv, ctx, pos_dev, window, scale, nsplit);
+      attn_decode_hd<128>(grid, st, q, kc, vc, out, part, counters, n_heads, n_kv, ctx, pos_dev, window, scale,
+                          nsplit);
       break;
     case 256:
-      attn_decode_hd<256>(grid, st, q, kc, vc, out, part, n_heads, n_kv, ctx, pos_dev, window, scale, nsplit);
+      attn_decode_hd<256>(grid, st, q, kc, vc, out, part, counters, n_heads, n_kv, ctx, pos_dev, window, scale,
+                          nsplit);
       break;
     default:
       fail(ST_OP, "attention: head_dim must be 64, 128 or 256");

@@ -24,19 +24,22 @@ void launch_dequant(int dt, const void* blocks, size_t nblocks, float* out, hipS
 // Token-row gather (src/layers/embeddings.rs:95-210): element h of token t sits at flat index
 // t*hidden + h. `ids` lives in device memory so a captured decode step can read the token that
 // the previous step's argmax produced.
+// One thread per element: row r = blockIdx.x, elements blockIdx.y*256 + threadIdx.x (a single
+// decode row spreads over hidden/256 workgroups instead of looping in one).
 __global__ void embed_kernel(int dt, const uint8_t* table, size_t hidden, const uint32_t* ids, float scale, float* out) {
   const int r = blockIdx.x;
+  const size_t h = (size_t)blockIdx.y * 256 + threadIdx.x;
+  if (h >= hidden) return;
   const size_t base = (size_t)ids[r] * hidden;
-  for (size_t h = threadIdx.x; h < hidden; h += blockDim.x) {
-    float v = flat_elem(dt, table, base + h);
-    if (scale != 1.0f) v = v * scale;
-    out[(size_t)r * hidden + h] = v;
-  }
+  float v = flat_elem(dt, table, base + h);
+  if (scale != 1.0f) v = v * scale;
+  out[(size_t)r * hidden + h] = v;
 }
 
 void launch_embed(int dt, const void* table, size_t hidden, const uint32_t* ids, int n, float scale, float* out,
                   hipStream_t st) {
-  hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, st, dt, (const uint8_t*)table, hidden, ids, scale, out);
+  hipLaunchKernelGGL(embed_kernel, dim3(n, (unsigned)((hidden + 255) / 256)), dim3(256), 0, st, dt,
+                     (const uint8_t*)table, hidden, ids, scale, out);
 }
 
 // Block-wide sum for 256-thread blocks.
