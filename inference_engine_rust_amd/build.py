@@ -32,6 +32,7 @@ SOURCES = [
     "kernels/attention.hip",
     "kernels/gemm.hip",
     "kernels/gemm_mfma.hip",
+    "kernels/gemm_q.hip",
     "model.cpp",
     "session.cpp",
     "api.cpp",

@@ -49,6 +49,17 @@ void launch_gemm(int dt, const void* w, const float* a, int M, int K, int N, flo
 // Matrix-core GEMM on activations pre-split into fp16 pairs (kernels/gemm_mfma.hip).
 void launch_split_f16(const float* x, size_t n, __half* hi, __half* lo, hipStream_t st);
 bool gemm_mfma_ok(int dt, const void* w, int K, int N);
+// Matrix-core GEMM for K-quant / Q8_0 weights with block scales applied outside the fp16 operands
+// (kernels/gemm_q.hip); up to three weight matrices sharing the activation in one launch.
+struct GemmQSeg {
+  const void* w;
+  float* out;
+  int n;
+};
+bool gemm_q_ok(int dt, const void* w, int K);
+void launch_block_sums(const float* a, int M, int K, float* xs, hipStream_t st);
+void launch_gemm_q(int dt, const GemmQSeg* segs, int nseg, const __half* xh, const __half* xl, const float* xs, int M,
+                   int K, const float* resid, hipStream_t st);
 void launch_gemm_mfma(int dt, const void* w, const __half* xh, const __half* xl, int M, int K, int N, float* out,
                       const float* resid, hipStream_t st);
 void launch_dequant(int dt, const void* blocks, size_t nblocks, float* out, hipStream_t st);

@@ -59,6 +59,20 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(int dt, const uint8_t* _
 
 void launch_gemm(int dt, const void* w, const float* a, int M, int K, int N, float* out, const float* resid,
                  hipStream_t st) {
+  if (gemm_q_ok(dt, w, K) && (reinterpret_cast<uintptr_t>(a) & 15) == 0) {
+    // scale-factored K-quant GEMM: stream-ordered scratch for the fp16 pair and the per-32 sums
+    const size_t n = (size_t)M * K;
+    void* buf = nullptr;
+    check_hip(hipMallocAsync(&buf, n * 2 * sizeof(__half) + (n / 32 + 64) * sizeof(float), st), "hipMallocAsync");
+    __half* xh = static_cast<__half*>(buf);
+    float* xs = reinterpret_cast<float*>(xh + 2 * n);
+    launch_split_f16(a, n, xh, xh + n, st);
+    launch_block_sums(a, M, K, xs, st);
+    GemmQSeg seg{w, out, N};
+    launch_gemm_q(dt, &seg, 1, xh, xh + n, xs, M, K, resid, st);
+    check_hip(hipFreeAsync(buf, st), "hipFreeAsync");
+    return;
+  }
   if (gemm_mfma_ok(dt, w, K, N) && (reinterpret_cast<uintptr_t>(a) & 15) == 0) {
     // stream-ordered scratch for the fp16 activation pair
     const size_t n = (size_t)M * K;

@@ -89,7 +89,7 @@ Session::~Session() {
                   (void*)act_, (void*)tmp_, (void*)xdec_, (void*)xndec_, (void*)qd_, (void*)kd_, (void*)vd_,
                   (void*)attd_, (void*)actd_, (void*)logits_, (void*)part_, (void*)tmpd_, (void*)d_pos_,
                   (void*)d_step_, (void*)d_flags_, (void*)d_tok_, (void*)d_ids_, (void*)d_gen_, (void*)d_key_,
-                  (void*)d_flag_, (void*)d_cnt_, (void*)xs_, kv_blob_})
+                  (void*)d_flag_, (void*)d_cnt_, (void*)xs_, (void*)xsum_, kv_blob_})
     dev_free(p);
   if (st_) (void)hipStreamDestroy(st_);
 }
@@ -116,6 +116,8 @@ void Session::ensure_rows(int rows) {
   }
   dev_free(xs_);
   xs_ = nullptr;
+  dev_free(xsum_);
+  xsum_ = nullptr;
   const Config& c = m_->cfg;
   int qmax = 0, kvmax = 0, fmax = 0;
   for (auto& L : c.layers) {
@@ -136,6 +138,7 @@ void Session::ensure_rows(int rows) {
   tmp_ = dev_alloc<float>(R * std::max(qmax, fmax));
   // fp16 (hi, lo) pair of the widest GEMM input, for the matrix-core prefill projections
   xs_ = dev_alloc<__half>(2 * R * std::max(std::max(H_, qmax), fmax));
+  xsum_ = dev_alloc<float>(R * std::max(std::max(H_, qmax), fmax) / 32 + 1);
   rows_cap_ = rows;
 }
 
@@ -166,6 +169,31 @@ static void project(const DevTensor& w, const float* a, const __half* xs, int ro
   }
 }
 
+// Prefill projections through the scale-factored matrix-core GEMM when every weight qualifies:
+// `a` (M x K) must already be split into xs_ (fp16 pair) and summed per 32 into xsum_.
+// Returns false when the caller should fall back to per-matrix projections.
+bool Session::project_q(const DevTensor* const* ws, float* const* outs, int nseg, int M, int K, const float* resid) {
+  if (M < 2) return false;
+  int dt = -1;
+  GemmQSeg segs[3];
+  for (int i = 0; i < nseg; ++i) {
+    const DevTensor& w = *ws[i];
+    if (w.dims.size() != 2 || (int)w.dims[0] != K) return false;
+    int wdt = w.dtype;
+    const void* p = w.dev;
+    if (w.dev_r) {
+      wdt = DT_Q6K_R;
+      p = w.dev_r;
+    }
+    if (dt >= 0 && wdt != dt) return false;
+    dt = wdt;
+    if (!gemm_q_ok(dt, p, K)) return false;
+    segs[i] = GemmQSeg{p, outs[i], (int)w.dims[1]};
+  }
+  launch_gemm_q(dt, segs, nseg, xs_, xs_ + (size_t)M * K, xsum_, M, K, resid, st_);
+  return true;
+}
+
 void Session::layer_prefill(int li, int M) {
   const Config& c = m_->cfg;
   const LayerSpec& S = c.layers[li];
@@ -178,13 +206,20 @@ void Session::layer_prefill(int li, int M) {
   auto split = [&](const float* a, int K) -> const __half* {
     if (M < 2 || K % 32 != 0) return nullptr;
     launch_split_f16(a, (size_t)M * K, xs_, xs_ + (size_t)M * K, st_);
+    launch_block_sums(a, M, K, xsum_, st_);
     return xs_;
   };
   launch_rmsnorm(x_, (const float*)L.attn_norm.dev, M, H_, eps, xn_, st_);
   const __half* xs = split(xn_, H_);
-  project(L.wq, xn_, xs, M, H_, qd, q_, nullptr, st_);
-  project(L.wk, xn_, xs, M, H_, kvd, k_, nullptr, st_);
-  project(L.wv, xn_, xs, M, H_, kvd, v_, nullptr, st_);
+  {
+    const DevTensor* ws[3] = {&L.wq, &L.wk, &L.wv};
+    float* outs[3] = {q_, k_, v_};
+    if (!xs || !project_q(ws, outs, 3, M, H_, nullptr)) {
+      project(L.wq, xn_, xs, M, H_, qd, q_, nullptr, st_);
+      project(L.wk, xn_, xs, M, H_, kvd, k_, nullptr, st_);
+      project(L.wv, xn_, xs, M, H_, kvd, v_, nullptr, st_);
+    }
+  }
   if (c.unpack_qk) {
     launch_unpack_qk(q_, tmp_, M, qd, c.n_heads, hd, st_);
     launch_copy_f32(tmp_, q_, (size_t)M * qd, st_);
@@ -197,7 +232,12 @@ void Session::layer_prefill(int li, int M) {
   launch_kv_store(k_, v_, M, kvd, kc_[li], vc_[li], c.n_kv_heads, hd, ctx_, nullptr, pos_, st_);
   const float scale = 1.0f / sqrtf((float)hd);
   launch_attn_prefill(q_, k_, v_, att_, M, c.n_heads, c.n_kv_heads, hd, S.window, scale, st_);
-  project(L.wo, att_, split(att_, qd), M, qd, H_, x_, x_, st_);
+  {
+    const __half* xa = split(att_, qd);
+    const DevTensor* ws[1] = {&L.wo};
+    float* outs[1] = {x_};
+    if (!xa || !project_q(ws, outs, 1, M, qd, x_)) project(L.wo, att_, xa, M, qd, H_, x_, x_, st_);
+  }
   // FFN sub-layer: pre-norm, gate/up, SwiGLU, down + residual.
   launch_rmsnorm(x_, (const float*)L.ffn_norm.dev, M, H_, eps, xn_, st_);
   if (M == 1 && L.gate.dtype == L.up.dtype) {
@@ -205,11 +245,20 @@ void Session::layer_prefill(int li, int M) {
     launch_matvec(L.gate.dtype, s, 2, xn_, H_, 2, st_);
   } else {
     xs = split(xn_, H_);
-    project(L.gate, xn_, xs, M, H_, S.ffn_dim, g_, nullptr, st_);
-    project(L.up, xn_, xs, M, H_, S.ffn_dim, u_, nullptr, st_);
+    const DevTensor* ws[2] = {&L.gate, &L.up};
+    float* outs[2] = {g_, u_};
+    if (!xs || !project_q(ws, outs, 2, M, H_, nullptr)) {
+      project(L.gate, xn_, xs, M, H_, S.ffn_dim, g_, nullptr, st_);
+      project(L.up, xn_, xs, M, H_, S.ffn_dim, u_, nullptr, st_);
+    }
     launch_swiglu(g_, u_, act_, (size_t)M * S.ffn_dim, st_);
   }
-  project(L.down, act_, split(act_, S.ffn_dim), M, S.ffn_dim, H_, x_, x_, st_);
+  {
+    const __half* xa = split(act_, S.ffn_dim);
+    const DevTensor* ws[1] = {&L.down};
+    float* outs[1] = {x_};
+    if (!xa || !project_q(ws, outs, 1, M, S.ffn_dim, x_)) project(L.down, act_, xa, M, S.ffn_dim, H_, x_, x_, st_);
+  }
 }
 
 // Decode layer, fused path: 5 launches (QKV+norm+RoPE+KV append, attention, O+residual,

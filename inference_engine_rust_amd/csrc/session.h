@@ -31,6 +31,7 @@ class Session {
  private:
   void ensure_rows(int rows);
   void layer_prefill(int li, int M);
+  bool project_q(const DevTensor* const* ws, float* const* outs, int nseg, int M, int K, const float* resid);
   bool fused_ok(int li) const;
   void layer_decode(int li, bool last);
   void layer_decode_unfused(int li);
@@ -50,6 +51,7 @@ class Session {
   float *x_ = nullptr, *xn_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *att_ = nullptr;
   float *g_ = nullptr, *u_ = nullptr, *act_ = nullptr, *tmp_ = nullptr;
   __half* xs_ = nullptr;  // fp16 (hi, lo) split of the current prefill GEMM input
+  float* xsum_ = nullptr;  // its per-32 row sums (Q4_K min term)
   float *xdec_ = nullptr, *xndec_ = nullptr, *qd_ = nullptr, *kd_ = nullptr, *vd_ = nullptr, *attd_ = nullptr;
   float *actd_ = nullptr, *logits_ = nullptr, *part_ = nullptr, *tmpd_ = nullptr;
   // device-side loop state

@@ -79,6 +79,21 @@ def _weights(dt, k, n, seed):
 XQ_MAX = 32639.0  # |X| bound of the int8-staged activation (matvec.hip, stage_i8)
 
 
+def _q4k_dmin_m(w, k, n):
+    """|dmin * m| of every element of a Q4_K tensor [k, n] (ggml get_scale_min_k4 min values)."""
+    blocks = np.asarray(w, dtype=np.uint8).reshape(-1, 144)
+    dmin = blocks[:, 2:4].copy().view(np.float16).astype(np.float64).reshape(-1)
+    s = blocks[:, 4:16].astype(np.int64)
+    mins = np.empty((blocks.shape[0], 8), np.float64)
+    for j in range(8):
+        if j < 4:
+            mins[:, j] = s[:, j + 4] & 63
+        else:
+            mins[:, j] = (s[:, j + 4] >> 4) | ((s[:, j] >> 6) << 4)
+    per = np.abs(dmin[:, None] * mins)  # [blocks, 8 sub-blocks of 32]
+    return np.repeat(per, 32, axis=1).reshape(-1)[: k * n].reshape(n, k)
+
+
 def _check_matmul(dt, k, n, m, seed=0):
     w = _weights(dt, k, n, seed)
     a = synth.normal(seed + 1, f"a{k}", m * k, 0.0, 1.0).reshape(m, k)
@@ -93,6 +108,10 @@ def _check_matmul(dt, k, n, m, seed=0):
         be = E.BLOCK[dt][0]
         wd = O.dequantize(ORC[dt], w, (k * n + be - 1) // be)[: k * n].reshape(n, k).astype(np.float64)
     mag = np.abs(a).astype(np.float64) @ np.abs(wd).T
+    if dt == E.Q4K and m > 1 and k % 256 == 0:
+        # The prefill GEMM sums d*sum(a*sc*q) and dmin*m*sum(a) separately, so its reordering bound
+        # is over the magnitudes of both terms of w = d*sc*q - dmin*m.
+        mag = np.abs(a).astype(np.float64) @ (np.abs(wd) + 2 * _q4k_dmin_m(w, k, n)).T
     err = np.abs(got.astype(np.float64) - want)
     # fp32 accumulation in a different order: |err| <= 2*K*eps*sum|a*w| (deterministic bound)
     bound = 2 * k * np.finfo(np.float32).eps * mag + 1e-30
