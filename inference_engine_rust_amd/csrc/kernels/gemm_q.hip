@@ -13,10 +13,12 @@
 // three (+ a_hi*w'_lo). The superblock factor d (Q8_0: per 32) multiplies a per-superblock MFMA
 // accumulator into the output accumulator; Q4_K's min term uses the per-32 row sums of a.
 //
-// Tiling: BM x 64 outputs per 256-thread workgroup (BM = 64 or 128), four waves stacked along M;
+// Tiling: BM x BN outputs per 256-thread workgroup (64x64 .. 128x128), four waves stacked along M;
 // 32-wide K stages double-buffered in LDS (one barrier per stage) with the next stage's raw bytes
 // in flight in registers while the current stage's MFMAs run. Up to three weight matrices that
 // share the activation (Q/K/V) run as one launch; M tiles of one N tile share an XCD's L2.
+#include <cstdlib>
+
 #include "common.cuh"
 #include "../iek_internal.h"
 
@@ -43,7 +45,7 @@ typedef _Float16 qh8_t __attribute__((ext_vector_type(8)));
 typedef float qf4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t qu4_t __attribute__((ext_vector_type(4)));
 
-constexpr int QBK = 32, QBN = 64, QROW = 40;  // K per stage, N per tile, LDS row (halves, padded)
+constexpr int QBK = 32, QROW = 40;  // K per stage, LDS row (halves, padded)
 
 IEK_DEV uint32_t hpack(_Float16 a, _Float16 b) {
   return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
@@ -199,17 +201,18 @@ __global__ __launch_bounds__(256) void block_sums_kernel(const float* __restrict
   xs[i] = s;
 }
 
-template <int DT, int BM>
+template <int DT, int BM, int BN>
 __global__ __launch_bounds__(256) void gemm_q_kernel(GemmQArgs g) {
-  constexpr int WM = BM / 4, MT = WM / 16, NT = QBN / 16;
+  constexpr int WM = BM / 4, MT = WM / 16, NT = BN / 16;
+  constexpr int BR = BN / 64;  // weight rows staged per thread per stage
   constexpr int AU = BM * 4 / 256;  // uint4 per thread per plane per stage (BM rows x 4 uint4)
   constexpr bool LO = QDeq<DT>::LO;
   constexpr int PERIOD = QDeq<DT>::PERIOD;
   __shared__ __align__(16) _Float16 as_h[2][BM][QROW];
   __shared__ __align__(16) _Float16 as_l[2][BM][QROW];
-  __shared__ __align__(16) _Float16 bs_h[2][QBN][QROW];
-  __shared__ __align__(16) _Float16 bs_l[LO ? 2 : 1][QBN][QROW];
-  __shared__ float sd[2][QBN], sdm[2][QBN], sxs[2][BM];
+  __shared__ __align__(16) _Float16 bs_h[2][BN][QROW];
+  __shared__ __align__(16) _Float16 bs_l[LO ? 2 : 1][BN][QROW];
+  __shared__ float sd[2][BN], sdm[2][BN], sxs[2][BM];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int M = g.M, K = g.K, nk = K / QBK, nsb = K / QK_K;
@@ -225,43 +228,56 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmQArgs g) {
   float* out = s == 0 ? g.out[0] : (s == 1 ? g.out[1] : g.out[2]);
   const int N = s == 0 ? g.n[0] : (s == 1 ? g.n[1] : g.n[2]);
   const int ts = s == 0 ? 0 : (s == 1 ? g.tile_start[1] : g.tile_start[2]);
-  const int m0 = mt * BM, n0 = (ntile - ts) * QBN;
+  const int m0 = mt * BM, n0 = (ntile - ts) * BN;
   const size_t row_bytes = g.row_bytes;
 
   const int b_row = tid >> 2, b_run = tid & 3;
-  const int b_n = min(n0 + b_row, N - 1);
-  qu4_t arh[AU], arl[AU];
-  float axs = 0.f;
-  QDeq<DT> braw;
+  int b_n[BR];
+#pragma unroll
+  for (int r = 0; r < BR; ++r) b_n[r] = min(n0 + b_row + 64 * r, N - 1);
+  // D stages of raw operand bytes in flight: slot i of the register ring holds stage kt with
+  // kt % D == i; a slot is refilled with stage kt + D right after stage kt is moved to LDS.
+  constexpr int D = 4;
+  struct Slot {
+    qu4_t arh[AU], arl[AU];
+    float axs;
+    QDeq<DT> braw[BR];
+  };
+  Slot ring[D];
 
-  auto fetch = [&](int kt) {
+  auto fetch = [&](int kt, Slot& sl) {
     const int k0 = kt * QBK;
 #pragma unroll
     for (int u = 0; u < AU; ++u) {
       const int idx = tid + 256 * u, row = idx >> 2, c8 = idx & 3;
       const size_t off = (size_t)min(m0 + row, M - 1) * K + k0 + 8 * c8;
-      arh[u] = *reinterpret_cast<const qu4_t*>(g.xh + off);
-      arl[u] = *reinterpret_cast<const qu4_t*>(g.xl + off);
+      sl.arh[u] = *reinterpret_cast<const qu4_t*>(g.xh + off);
+      sl.arl[u] = *reinterpret_cast<const qu4_t*>(g.xl + off);
     }
-    if (DT == DT_Q4K && tid < BM) axs = g.xs[(size_t)min(m0 + tid, M - 1) * (K / 32) + kt];
-    braw.load(w, row_bytes, b_n, k0 + 8 * b_run, nsb);
+    if (DT == DT_Q4K && tid < BM) sl.axs = g.xs[(size_t)min(m0 + tid, M - 1) * (K / 32) + kt];
+#pragma unroll
+    for (int r = 0; r < BR; ++r) sl.braw[r].load(w, row_bytes, b_n[r], k0 + 8 * b_run, nsb);
   };
-  auto stage = [&](int kt, int buf) {
+  auto stage = [&](int kt, int buf, const Slot& sl) {
 #pragma unroll
     for (int u = 0; u < AU; ++u) {
       const int idx = tid + 256 * u, row = idx >> 2, c8 = idx & 3;
-      *reinterpret_cast<qu4_t*>(&as_h[buf][row][8 * c8]) = arh[u];
-      *reinterpret_cast<qu4_t*>(&as_l[buf][row][8 * c8]) = arl[u];
+      *reinterpret_cast<qu4_t*>(&as_h[buf][row][8 * c8]) = sl.arh[u];
+      *reinterpret_cast<qu4_t*>(&as_l[buf][row][8 * c8]) = sl.arl[u];
     }
-    if (DT == DT_Q4K && tid < BM) sxs[buf][tid] = axs;
-    uint4 hi, lo;
-    float d, dm;
-    braw.decode(kt * QBK + 8 * b_run, hi, lo, d, dm);
-    *reinterpret_cast<uint4*>(&bs_h[buf][b_row][8 * b_run]) = hi;
-    if constexpr (LO) *reinterpret_cast<uint4*>(&bs_l[LO ? buf : 0][b_row][8 * b_run]) = lo;
-    if (b_run == 0) {
-      sd[buf][b_row] = d;
-      sdm[buf][b_row] = dm;
+    if (DT == DT_Q4K && tid < BM) sxs[buf][tid] = sl.axs;
+#pragma unroll
+    for (int r = 0; r < BR; ++r) {
+      uint4 hi, lo;
+      float d, dm;
+      sl.braw[r].decode(kt * QBK + 8 * b_run, hi, lo, d, dm);
+      const int row = b_row + 64 * r;
+      *reinterpret_cast<uint4*>(&bs_h[buf][row][8 * b_run]) = hi;
+      if constexpr (LO) *reinterpret_cast<uint4*>(&bs_l[LO ? buf : 0][row][8 * b_run]) = lo;
+      if (b_run == 0) {
+        sd[buf][row] = d;
+        sdm[buf][row] = dm;
+      }
     }
   };
 
@@ -273,63 +289,81 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmQArgs g) {
       acc[i][j] = qf4_t{0.f, 0.f, 0.f, 0.f};
       part[i][j] = qf4_t{0.f, 0.f, 0.f, 0.f};
     }
-  fetch(0);
-  stage(0, 0);
+#pragma unroll
+  for (int i = 0; i < D; ++i) fetch(min(i, nk - 1), ring[i]);
+  stage(0, 0, ring[0]);
+  fetch(min(D, nk - 1), ring[0]);
   __syncthreads();
   const int fr = lane & 15, fk = 8 * (lane >> 4);
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) fetch(kt + 1);
-    qu4_t ah[MT], al[MT], bh[NT], bl[NT];
+  for (int kt0 = 0; kt0 < nk; kt0 += D) {
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      ah[i] = *reinterpret_cast<const qu4_t*>(&as_h[buf][wave * WM + 16 * i + fr][fk]);
-      al[i] = *reinterpret_cast<const qu4_t*>(&as_l[buf][wave * WM + 16 * i + fr][fk]);
-    }
+    for (int u = 0; u < D; ++u) {
+      const int kt = kt0 + u;
+      if (kt >= nk) break;
+      const int buf = kt & 1;
+      qu4_t ah[MT], al[MT], bh[NT], bl[NT];
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      bh[j] = *reinterpret_cast<const qu4_t*>(&bs_h[buf][16 * j + fr][fk]);
-      if constexpr (LO) bl[j] = *reinterpret_cast<const qu4_t*>(&bs_l[LO ? buf : 0][16 * j + fr][fk]);
-    }
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        const qh8_t a_h = __builtin_bit_cast(qh8_t, ah[i]), a_l = __builtin_bit_cast(qh8_t, al[i]);
-        const qh8_t b_h = __builtin_bit_cast(qh8_t, bh[j]);
-        part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_h, b_h, part[i][j], 0, 0, 0);
-        part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_l, b_h, part[i][j], 0, 0, 0);
-        if constexpr (LO) {
-          const qh8_t b_l = __builtin_bit_cast(qh8_t, bl[j]);
-          part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_h, b_l, part[i][j], 0, 0, 0);
-        }
+      for (int i = 0; i < MT; ++i) {
+        ah[i] = *reinterpret_cast<const qu4_t*>(&as_h[buf][wave * WM + 16 * i + fr][fk]);
+        al[i] = *reinterpret_cast<const qu4_t*>(&as_l[buf][wave * WM + 16 * i + fr][fk]);
       }
-    // Q4_K min term of this 32-block: acc[m][n] -= (dmin*m_b)[n] * sum_b a[m]
-    if constexpr (DT == DT_Q4K) {
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
-        const float dmn = sdm[buf][16 * j + fr];
+        bh[j] = *reinterpret_cast<const qu4_t*>(&bs_h[buf][16 * j + fr][fk]);
+        if constexpr (LO) bl[j] = *reinterpret_cast<const qu4_t*>(&bs_l[LO ? buf : 0][16 * j + fr][fk]);
+      }
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          const qh8_t a_h = __builtin_bit_cast(qh8_t, ah[i]), a_l = __builtin_bit_cast(qh8_t, al[i]);
+          const qh8_t b_h = __builtin_bit_cast(qh8_t, bh[j]);
+          part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_h, b_h, part[i][j], 0, 0, 0);
+          part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_l, b_h, part[i][j], 0, 0, 0);
+          if constexpr (LO) {
+            const qh8_t b_l = __builtin_bit_cast(qh8_t, bl[j]);
+            part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_h, b_l, part[i][j], 0, 0, 0);
+          }
+        }
+      // Q4_K min term of this 32-block: acc[m][n] -= (dmin*m_b)[n] * sum_b a[m]
+      if constexpr (DT == DT_Q4K) {
+        float xsv[MT][4];
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[i][j][r] -= dmn * sxs[buf][wave * WM + 16 * i + 4 * (lane >> 4) + r];
-      }
-    }
-    // end of a d block: fold d[n] * (its partial) into the output accumulator
-    if ((kt + 1) % PERIOD == 0) {
+          for (int r = 0; r < 4; ++r) xsv[i][r] = sxs[buf][wave * WM + 16 * i + 4 * (lane >> 4) + r];
 #pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        const float dn = sd[buf][16 * j + fr];
+        for (int j = 0; j < NT; ++j) {
+          const float dmn = sdm[buf][16 * j + fr];
 #pragma unroll
-        for (int i = 0; i < MT; ++i) {
+          for (int i = 0; i < MT; ++i)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[i][j][r] += dn * part[i][j][r];
-          part[i][j] = qf4_t{0.f, 0.f, 0.f, 0.f};
+            for (int r = 0; r < 4; ++r) acc[i][j][r] -= dmn * xsv[i][r];
         }
       }
+      // end of a d block: fold d[n] * (its partial) into the output accumulator
+      if ((kt + 1) % PERIOD == 0) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          const float dn = sd[buf][16 * j + fr];
+#pragma unroll
+          for (int i = 0; i < MT; ++i) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][j][r] += dn * part[i][j][r];
+            part[i][j] = qf4_t{0.f, 0.f, 0.f, 0.f};
+          }
+        }
+      }
+      {
+        // unconditional with clamped stage indices, so the number of loads in flight is the same
+        // on every path and each stage waits only for its own slot (the tail re-reads the last
+        // stage and stages it into the idle buffer)
+        Slot& sl = ring[(u + 1) % D];
+        stage(min(kt + 1, nk - 1), buf ^ 1, sl);
+        fetch(min(kt + 1 + D, nk - 1), sl);
+      }
+      __syncthreads();
     }
-    if (kt + 1 < nk) stage(kt + 1, buf ^ 1);
-    __syncthreads();
   }
 
   const float* resid = s == 0 ? g.resid : nullptr;
@@ -368,21 +402,38 @@ void launch_block_sums(const float* a, int M, int K, float* xs, hipStream_t st) 
   hipLaunchKernelGGL(block_sums_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, st, a, nb, xs);
 }
 
-template <int DT, int BM>
+template <int DT, int BM, int BN>
 static void gemm_q_launch(GemmQArgs g, hipStream_t st) {
+  int t = 0;
+  for (int i = 0; i < g.nseg; ++i) {
+    g.tile_start[i] = t;
+    t += (g.n[i] + BN - 1) / BN;
+  }
+  for (int i = g.nseg; i <= 3; ++i) g.tile_start[i] = t;
   const int mtiles = (g.M + BM - 1) / BM;
-  const int tiles = mtiles * g.tile_start[g.nseg];
+  const int tiles = mtiles * t;
   g.xcd_remap = tiles % 8 == 0 ? 1 : 0;
-  hipLaunchKernelGGL((gemm_q_kernel<DT, BM>), dim3(tiles), dim3(256), 0, st, g);
+  hipLaunchKernelGGL((gemm_q_kernel<DT, BM, BN>), dim3(tiles), dim3(256), 0, st, g);
 }
 
+// Tile shape: 64 x 64 by default (measured fastest at the Mistral-7B prefill shapes: the larger
+// tiles lose more to occupancy than they gain in operand reuse); IEK_GEMM_TILE overrides.
 template <int DT>
 static void gemm_q_dt(GemmQArgs g, hipStream_t st) {
-  // BM = 128 unless that leaves fewer than two workgroups per CU's worth of tiles
-  const int ntiles = g.tile_start[g.nseg];
-  const bool small = (size_t)((g.M + 127) / 128) * ntiles < 512;
-  if (small) gemm_q_launch<DT, 64>(g, st);
-  else gemm_q_launch<DT, 128>(g, st);
+  auto tiles = [&](int bm, int bn) {
+    size_t n = 0;
+    for (int i = 0; i < g.nseg; ++i) n += (g.n[i] + bn - 1) / bn;
+    return (size_t)((g.M + bm - 1) / bm) * n;
+  };
+  static int force = -2;
+  if (force == -2) {
+    const char* e = getenv("IEK_GEMM_TILE");  // 0: 64x64, 1: 64x128, 2: 128x128 (tuning)
+    force = e ? atoi(e) : -1;
+  }
+  (void)tiles;
+  if (force == 2) gemm_q_launch<DT, 128, 128>(g, st);
+  else if (force == 1) gemm_q_launch<DT, 64, 128>(g, st);
+  else gemm_q_launch<DT, 64, 64>(g, st);
 }
 
 void launch_gemm_q(int dt, const GemmQSeg* segs, int nseg, const __half* xh, const __half* xl, const float* xs, int M,
@@ -390,16 +441,12 @@ void launch_gemm_q(int dt, const GemmQSeg* segs, int nseg, const __half* xh, con
   if (nseg < 1 || nseg > 3 || M < 1) fail(ST_OP, "gemm_q: 1..3 segments and M >= 1");
   GemmQArgs g{};
   g.nseg = nseg;
-  int t = 0;
   for (int i = 0; i < nseg; ++i) {
     if (!gemm_q_ok(dt, segs[i].w, K) || segs[i].n < 1) fail(ST_OP, "gemm_q: unsupported weight type, alignment or shape");
     g.w[i] = (const uint8_t*)segs[i].w;
     g.out[i] = segs[i].out;
     g.n[i] = segs[i].n;
-    g.tile_start[i] = t;
-    t += (segs[i].n + QBN - 1) / QBN;
   }
-  for (int i = nseg; i <= 3; ++i) g.tile_start[i] = t;
   g.M = M;
   g.K = K;
   g.xh = xh;
