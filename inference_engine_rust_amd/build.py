@@ -22,7 +22,8 @@ SYNTH_LIB = os.path.join(PKG, "libiek_synth.so")
 ARCH = os.environ.get("IEK_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
-# Packed-FP32 VALU ops are disabled for all device code ("Build flags").
+# Packed-FP32 VALU ops are disabled for all device code: some of their forms have given wrong
+# results, without an error, on the MI355X machines this is tested on.
 HIP_FLAGS = ["-std=c++17", "-O3", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
              "-packed-fp32-ops", "-Wall", "-Wno-unused-function", "-Wno-unused-result"]
 
@@ -33,6 +34,7 @@ SOURCES = [
     "kernels/gemm.hip",
     "kernels/gemm_mfma.hip",
     "kernels/gemm_q.hip",
+    "kernels/gemma.hip",
     "model.cpp",
     "session.cpp",
     "api.cpp",

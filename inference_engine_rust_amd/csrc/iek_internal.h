@@ -19,11 +19,16 @@ enum Status : int {
 enum DType : int { DT_F32 = 0, DT_Q4K = 1, DT_Q6K = 2, DT_Q8_0 = 3,
                    // internal only: Q6_K bytes regrouped per row for 16-byte lane loads (see
                    // kernels/matvec.hip, Q6RTr); never crosses the C ABI
-                   DT_Q6K_R = 4 };
+                   DT_Q6K_R = 4,
+                   // internal only: Q8_0 quants and scales split into per-row runs (Q8RTr)
+                   DT_Q8_0_R = 5 };
 // Row bytes of the regrouped Q6_K layout: nsb superblocks of [4 x 48 B lane chunks] followed by
 // nsb x 16 scale bytes and nsb x 2 d bytes, padded to 16.
 __host__ __device__ inline size_t q6r_row_bytes(size_t nsb) { return nsb * 208 + ((2 * nsb + 15) / 16) * 16; }
 void launch_repack_q6k(const void* src, int K, int N, void* dst, hipStream_t st);
+// Row bytes of the regrouped Q8_0 layout: nb x 32 quant bytes, then nb x 2 scale bytes padded to 16.
+__host__ __device__ inline size_t q8r_row_bytes(size_t nb) { return nb * 32 + ((2 * nb + 15) / 16) * 16; }
+void launch_repack_q80(const void* src, int K, int N, void* dst, hipStream_t st);
 
 struct Error {
   int code;
@@ -88,11 +93,24 @@ void launch_unpack_qk(const float* src, float* dst, int rows, int row_stride, in
 void launch_copy_f32(const float* src, float* dst, size_t n, hipStream_t st);
 void launch_fill_i32(int* p, int v, int n, hipStream_t st);
 // `counters` holds n_kv zero-initialised ints; the kernel leaves them zero again.
-void launch_attn_decode(const float* q, const __half* kc, const __half* vc, float* out, float* part, int* counters,
-                        int n_heads, int n_kv, int head_dim, int ctx, const int* pos_dev, int window, float scale,
-                        int max_len, hipStream_t st);
+// The cache is fp16, or f32 when kv_f32 (Gemma-4 sessions).
+void launch_attn_decode(const float* q, const void* kc, const void* vc, bool kv_f32, float* out, float* part,
+                        int* counters, int n_heads, int n_kv, int head_dim, int ctx, const int* pos_dev, int window,
+                        float scale, int max_len, hipStream_t st);
 void launch_attn_prefill(const float* q, const float* k, const float* v, float* out, int M, int n_heads, int n_kv,
                          int head_dim, int window, float scale, hipStream_t st);
+// Gemma-4 pieces (kernels/gemma.hip).
+void launch_head_prep(float* q, float* k, float* v, int rows, int q_stride, int kv_stride, int nq, int nkv, int hd,
+                      const float* qn, const float* kn, float eps, bool vnorm, const float* cs, int npairs,
+                      const int* pos_dev, int rope0, int kv0, void* kc, void* vc, bool kv_f32, int ctx,
+                      hipStream_t st);
+void launch_rmsnorm_add(float* x, const float* t, const float* w, int rows, int dim, float eps, bool has_scale,
+                        float scale, hipStream_t st);
+void launch_ple_pack(const float* proj, const float* tok, const float* norm_w, int rows, int n_layers, int pd,
+                     float eps, float proj_scale, float sqrt_pd, float combine, float* out, hipStream_t st);
+void launch_ple_gate(float* go, const float* packed, int rows, int pd, int n_layers, int layer, hipStream_t st);
+void launch_kv_load(const void* kc, const void* vc, bool kv_f32, int rows, int n_kv, int hd, int ctx, float* k,
+                    float* v, hipStream_t st);
 void launch_fill_u64(unsigned long long* p, unsigned long long v, int n, hipStream_t st);
 void launch_set_int(int* p, int v, hipStream_t st);
 void launch_add_int(int* p, int v, hipStream_t st);

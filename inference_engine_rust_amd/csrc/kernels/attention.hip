@@ -74,6 +74,28 @@ IEK_DEV void merge_head(const float* __restrict__ part, float* __restrict__ out,
   for (int t = 0; t < DPL; ++t) out[(size_t)h * HD + DPL * lane + t] = acc[t] / L;
 }
 
+// The last workgroup of a KV head to finish merges the group's heads. Release: the workgroup
+// barrier orders every wave's partial stores before thread 0's agent-scope acq_rel add (which
+// writes back this XCD's L2); the last arrival's acquire side invalidates its L2 before the
+// partials are read. The counter is reset for the next launch.
+template <int HD>
+IEK_DEV void merge_if_last(const float* __restrict__ part, float* __restrict__ out, int* __restrict__ counters,
+                           int kvh, int G, int nsplit, int jmin, int total, int wave) {
+  __shared__ int last;
+  __shared__ float wsl[4][256];
+  __syncthreads();
+  const int s0 = jmin / SPLIT, nlive = (total + SPLIT - 1) / SPLIT;
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(&counters[kvh], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    last = old == nlive - s0 - 1;
+    if (last) __hip_atomic_store(&counters[kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  for (int g = wave; g < G; g += 4) merge_head<HD>(part, out, kvh * G + g, nsplit, s0, nlive, wsl[wave]);
+}
+
 template <int HD>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, const __half* __restrict__ kc,
                                                           const __half* __restrict__ vc, float* __restrict__ part,
@@ -83,7 +105,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
   constexpr int DPL = HD / 64;        // head dims per lane in the PV phase
   constexpr int KROW = HD + 8;        // padded K row (halves): 16-byte reads of different rows spread banks
   constexpr int U4 = SPLIT * HD / 8;  // uint4 per K (or V) slice
-  static_assert(HD == 64 || HD == 128 || HD == 256, "head_dim");
+  // V is staged in LDS up to head_dim 256; at 512 the K slice, q and V would not fit together, so
+  // the P.V phase reads V rows straight from memory (each row one coalesced 1 KB wave load).
+  constexpr bool VL = HD <= 256;
+  static_assert(HD == 64 || HD == 128 || HD == 256 || HD == 512, "head_dim");
   const int kvh = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = n_heads / n_kv;
@@ -93,25 +118,25 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
   const int nk = j1 - j0;
   if (nk <= 0) return;  // uniform across the workgroup
   __shared__ __align__(16) __half ks[SPLIT][KROW];
-  __shared__ __align__(16) __half vs[SPLIT][HD];
+  __shared__ __align__(16) __half vs[VL ? SPLIT : 1][VL ? HD : 8];
   __shared__ __align__(16) float qs[8][HD];
   __shared__ float ps[4][SPLIT];
+  const __half* vb = vc + ((size_t)kvh * ctx + j0) * HD;
   {
     const __half* kb = kc + ((size_t)kvh * ctx + j0) * HD;
-    const __half* vb = vc + ((size_t)kvh * ctx + j0) * HD;
-    uint4 kr[U4 / 256], vr[U4 / 256];
+    uint4 kr[U4 / 256], vr[VL ? U4 / 256 : 1];
 #pragma unroll
     for (int u = 0; u < U4 / 256; ++u) {
       const int i = tid + 256 * u, row = min(i / (HD / 8), nk - 1), c8 = i % (HD / 8);
       kr[u] = *reinterpret_cast<const uint4*>(kb + (size_t)row * HD + 8 * c8);
-      vr[u] = *reinterpret_cast<const uint4*>(vb + (size_t)row * HD + 8 * c8);
+      if constexpr (VL) vr[u] = *reinterpret_cast<const uint4*>(vb + (size_t)row * HD + 8 * c8);
     }
     for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = q[(size_t)(kvh * G) * HD + i];
 #pragma unroll
     for (int u = 0; u < U4 / 256; ++u) {
       const int i = tid + 256 * u, row = i / (HD / 8), c8 = i % (HD / 8);
       *reinterpret_cast<uint4*>(&ks[row][8 * c8]) = kr[u];
-      *reinterpret_cast<uint4*>(&vs[row][8 * c8]) = vr[u];
+      if constexpr (VL) *reinterpret_cast<uint4*>(&vs[row][8 * c8]) = vr[u];
     }
   }
   __syncthreads();
@@ -151,7 +176,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
         const float2 v2 = __half22float2(*reinterpret_cast<const __half2*>(&vs[j][2 * lane]));
         o[0] += pj * v2.x;
         o[1] += pj * v2.y;
-      } else {
+      } else if constexpr (DPL == 4) {
         const uint2 raw = *reinterpret_cast<const uint2*>(&vs[j][4 * lane]);
         const __half2* h2 = reinterpret_cast<const __half2*>(&raw);
         const float2 a0 = __half22float2(h2[0]), a1 = __half22float2(h2[1]);
@@ -159,6 +184,16 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
         o[1] += pj * a0.y;
         o[2] += pj * a1.x;
         o[3] += pj * a1.y;
+      } else {
+        // rows past the live slice have p = 0; their address is clamped into the slice
+        const uint4 raw = *reinterpret_cast<const uint4*>(vb + (size_t)min(j, nk - 1) * HD + 8 * lane);
+        const __half2* h2 = reinterpret_cast<const __half2*>(&raw);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float2 a = __half22float2(h2[t]);
+          o[2 * t] += pj * a.x;
+          o[2 * t + 1] += pj * a.y;
+        }
       }
     }
     float* pr = part + ((size_t)(kvh * G + g) * nsplit + sp) * (HD + 2);
@@ -170,119 +205,133 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
     for (int t = 0; t < DPL; ++t) pr[2 + DPL * lane + t] = o[t];
     __builtin_amdgcn_wave_barrier();  // ps[wave] is rewritten by the next head of this wave
   }
-  // The last workgroup of this KV head to finish merges the group's heads. Release: the
-  // workgroup barrier orders every wave's partial stores before thread 0's agent-scope acq_rel
-  // add (which writes back this XCD's L2); the last arrival's acquire side invalidates its L2
-  // before the partials are read. The counter is reset for the next launch.
-  __shared__ int last;
+  merge_if_last<HD>(part, out, counters, kvh, G, nsplit, jmin, total, wave);
+}
+
+// f32 KV cache variant (Gemma-4 sessions keep the reference's f32 cache: with q/k head norms
+// and a score scale of 1 the softmax is sharp enough that fp16 keys/values move the logits by
+// ~1e-2). Same grid, partials and merge as above. Score phase: lane = key; wave w sums head dims
+// [w HD/4, (w+1) HD/4) of every head of the group for its key, reading the key row straight from
+// memory, and the four partial sums meet in LDS. P.V: lane l owns head dims [DPL l, DPL l + DPL)
+// and reads V rows straight from memory (one coalesced row per key).
+template <int HD>
+__global__ __launch_bounds__(256) void attn_decode_f32_kernel(const float* __restrict__ q, const float* __restrict__ kc,
+                                                              const float* __restrict__ vc, float* __restrict__ part,
+                                                              float* __restrict__ out, int* __restrict__ counters,
+                                                              int n_heads, int n_kv, int ctx, const int* pos_dev,
+                                                              int window, float scale, int nsplit) {
+  constexpr int DPL = HD / 64;
+  constexpr int DQ = HD / 4;
+  const int kvh = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = n_heads / n_kv;
+  const int total = *pos_dev + 1;
+  const int jmin = (window > 0 && total > window) ? total - window : 0;
+  const int j0 = max(sp * SPLIT, jmin), j1 = min(total, (sp + 1) * SPLIT);
+  const int nk = j1 - j0;
+  if (nk <= 0) return;  // uniform across the workgroup
+  __shared__ __align__(16) float qs[8][HD];
+  __shared__ float sc[4][8][SPLIT];
+  __shared__ float ps[8][SPLIT];
+  for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = q[(size_t)(kvh * G) * HD + i];
   __syncthreads();
-  if (tid == 0) {
-    const int s0 = jmin / SPLIT, nlive = (total + SPLIT - 1) / SPLIT;
-    const int old = __hip_atomic_fetch_add(&counters[kvh], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    last = old == nlive - s0 - 1;
-    if (last) __hip_atomic_store(&counters[kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const float* kb = kc + ((size_t)kvh * ctx + j0) * HD;
+  const float* vb = vc + ((size_t)kvh * ctx + j0) * HD;
+  {
+    const float* krow = kb + (size_t)min(lane, nk - 1) * HD + wave * DQ;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int d = 0; d < DQ; d += 4) {
+      const float4 k4 = *reinterpret_cast<const float4*>(krow + d);
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        if (g < G) {
+          const float4 q4 = *reinterpret_cast<const float4*>(&qs[g][wave * DQ + d]);
+          acc[g] += q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < 8; ++g)
+      if (g < G) sc[wave][g][lane] = acc[g];
   }
   __syncthreads();
-  if (!last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  const int s0 = jmin / SPLIT, nlive = (total + SPLIT - 1) / SPLIT;
-  __shared__ float wsl[4][256];
-  for (int g = wave; g < G; g += 4) merge_head<HD>(part, out, kvh * G + g, nsplit, s0, nlive, wsl[wave]);
+  const bool valid = lane < nk;
+  for (int g = wave; g < G; g += 4) {
+    const float s = valid ? ((sc[0][g][lane] + sc[1][g][lane]) + (sc[2][g][lane] + sc[3][g][lane])) * scale
+                          : -INFINITY;
+    const float m = wave_max(s);
+    const float p = valid ? expf(s - m) : 0.f;
+    const float l = wave_sum(p);
+    ps[g][lane] = p;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float o[DPL];
+#pragma unroll
+    for (int t = 0; t < DPL; ++t) o[t] = 0.f;
+    for (int j = 0; j < nk; ++j) {
+      const float pj = ps[g][j];
+      const float* vr = vb + (size_t)j * HD + DPL * lane;
+#pragma unroll
+      for (int t = 0; t < DPL; ++t) o[t] += pj * vr[t];
+    }
+    float* pr = part + ((size_t)(kvh * G + g) * nsplit + sp) * (HD + 2);
+    if (lane == 0) {
+      pr[0] = m;
+      pr[1] = l;
+    }
+#pragma unroll
+    for (int t = 0; t < DPL; ++t) pr[2 + DPL * lane + t] = o[t];
+  }
+  merge_if_last<HD>(part, out, counters, kvh, G, nsplit, jmin, total, wave);
 }
 
 template <int HD>
-static void attn_decode_hd(dim3 grid, hipStream_t st, const float* q, const __half* kc, const __half* vc, float* out,
-                           float* part, int* counters, int n_heads, int n_kv, int ctx, const int* pos_dev, int window,
-                           float scale, int nsplit) {
-  hipLaunchKernelGGL(attn_decode_kernel<HD>, grid, dim3(256), 0, st, q, kc, vc, part, out, counters, n_heads, n_kv,
-                     ctx, pos_dev, window, scale, nsplit);
+static void attn_decode_hd(dim3 grid, hipStream_t st, const float* q, const void* kc, const void* vc, bool kv_f32,
+                           float* out, float* part, int* counters, int n_heads, int n_kv, int ctx, const int* pos_dev,
+                           int window, float scale, int nsplit) {
+  if (kv_f32)
+    hipLaunchKernelGGL(attn_decode_f32_kernel<HD>, grid, dim3(256), 0, st, q, (const float*)kc, (const float*)vc, part,
+                       out, counters, n_heads, n_kv, ctx, pos_dev, window, scale, nsplit);
+  else
+    hipLaunchKernelGGL(attn_decode_kernel<HD>, grid, dim3(256), 0, st, q, (const __half*)kc, (const __half*)vc, part,
+                       out, counters, n_heads, n_kv, ctx, pos_dev, window, scale, nsplit);
 }
 
-void launch_attn_decode(const float* q, const __half* kc, const __half* vc, float* out, float* part, int* counters,
-                        int n_heads, int n_kv, int head_dim, int ctx, const int* pos_dev, int window, float scale,
-                        int max_len, hipStream_t st) {
+void launch_attn_decode(const float* q, const void* kc, const void* vc, bool kv_f32, float* out, float* part,
+                        int* counters, int n_heads, int n_kv, int head_dim, int ctx, const int* pos_dev, int window,
+                        float scale, int max_len, hipStream_t st) {
   const int nsplit = (max_len + SPLIT - 1) / SPLIT;
   dim3 grid(n_kv, nsplit);
   if (n_kv <= 0 || n_heads % n_kv != 0 || n_heads / n_kv > 8)
     fail(ST_OP, "attention: GQA group must divide the heads and be at most 8");
   switch (head_dim) {
+#define IEK_AD(HD)                                                                                               \
+  attn_decode_hd<HD>(grid, st, q, kc, vc, kv_f32, out, part, counters, n_heads, n_kv, ctx, pos_dev, window, scale, \
+                     nsplit)
     case 64:
-      attn_decode_hd<64>(grid, st, q, kc, vc, out, part, counters, n_heads, n_kv, ctx, pos_dev, window, scale,
-                          nsplit);
+      IEK_AD(64);
       break;
     case 128:
-      attn_decode_hd<128>(grid, st, q, kc, vc, out, part, counters, n_heads, n_kv, ctx, pos_dev, window, scale,
-                          nsplit);
+      IEK_AD(128);
       break;
     case 256:
-      attn_decode_hd<256>(grid, st, q, kc, vc, out, part, counters, n_heads, n_kv, ctx, pos_dev, window, scale,
-                          nsplit);
+      IEK_AD(256);
       break;
+    case 512:
+      IEK_AD(512);
+      break;
+#undef IEK_AD
     default:
-      fail(ST_OP, "attention: head_dim must be 64, 128 or 256");
-  }
-}
-
-// Prefill: one wave per (head, 64-query tile); lane i owns query i. Keys/values are staged in
-// LDS 32 at a time; online softmax per query.
-template <int HD>
-__global__ __launch_bounds__(64) void attn_prefill_kernel(const float* __restrict__ q, const float* __restrict__ k,
-                                                          const float* __restrict__ v, float* __restrict__ out, int M,
-                                                          int n_heads, int n_kv, int window, float scale) {
-  constexpr int KT = 32;
-  const int h = blockIdx.x, qt = blockIdx.y, lane = threadIdx.x;
-  const int G = n_heads / n_kv, kvh = h / G;
-  const int qd = n_heads * HD, kvd = n_kv * HD;
-  const int i = qt * 64 + lane;
-  const bool valid = i < M;
-  __shared__ float ks[KT][HD];
-  __shared__ float vs[KT][HD];
-  float qr[HD], o[HD];
-#pragma unroll
-  for (int d = 0; d < HD; ++d) {
-    qr[d] = valid ? q[(size_t)i * qd + h * HD + d] : 0.f;
-    o[d] = 0.f;
-  }
-  float m = -INFINITY, l = 0.f;
-  const int last_q = min(M - 1, qt * 64 + 63);
-  const int jmin_tile = window > 0 ? max(0, qt * 64 - (window - 1)) : 0;
-  for (int jt = (jmin_tile / KT) * KT; jt <= last_q; jt += KT) {
-    __syncthreads();
-    for (int e = lane; e < KT * HD; e += 64) {
-      int jj = jt + e / HD, d = e % HD;
-      ks[e / HD][d] = jj < M ? k[(size_t)jj * kvd + kvh * HD + d] : 0.f;
-      vs[e / HD][d] = jj < M ? v[(size_t)jj * kvd + kvh * HD + d] : 0.f;
-    }
-    __syncthreads();
-    if (!valid) continue;
-    const int jmin = window > 0 ? max(0, i - (window - 1)) : 0;
-    for (int t = 0; t < KT; ++t) {
-      const int j = jt + t;
-      if (j > i || j < jmin) continue;
-      float s = 0.f;
-#pragma unroll
-      for (int d = 0; d < HD; ++d) s += qr[d] * ks[t][d];
-      s *= scale;
-      const float mn = fmaxf(m, s);
-      const float corr = expf(m - mn);
-      const float p = expf(s - mn);
-      l = l * corr + p;
-#pragma unroll
-      for (int d = 0; d < HD; ++d) o[d] = o[d] * corr + p * vs[t][d];
-      m = mn;
-    }
-  }
-  if (valid) {
-#pragma unroll
-    for (int d = 0; d < HD; ++d) out[(size_t)i * qd + h * HD + d] = o[d] / l;
+      fail(ST_OP, "attention: head_dim must be 64, 128, 256 or 512");
   }
 }
 
 // Prefill on the matrix cores (v_mfma_f32_16x16x32_f16): one 256-thread workgroup per (head,
 // 64-query tile), each wave owning 16 queries; 64-key blocks of K (row-major) and V (transposed)
 // are staged in LDS as fp16 (hi, lo) pairs, S = Q K^T and O += P V each take three MFMAs per step
-// (hi*hi + hi*lo + lo*hi, products exact in f32), and the softmax is the online form of the SIMT
-// kernel above (running max, rescaled sum).
+// (hi*hi + hi*lo + lo*hi, products exact in f32), and the softmax is the online form (running max
+// per query row, sum rescaled whenever the max grows).
 typedef _Float16 ah8_t __attribute__((ext_vector_type(8)));
 typedef float af4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t au4_t __attribute__((ext_vector_type(4)));
@@ -306,11 +355,13 @@ IEK_DEV af4_t mma3(au4_t ah, au4_t al, au4_t bh, au4_t bl, af4_t c) {
   return c;
 }
 
-template <int HD>
+// KB keys per block: 64 up to head_dim 128; 32 at 256 and 512, where the (hi, lo) K block, the
+// transposed V block and the P tiles must still fit the 160 KB of LDS.
+template <int HD, int KB>
 __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                                 const float* __restrict__ v, float* __restrict__ out,
                                                                 int M, int n_heads, int n_kv, int window, float scale) {
-  constexpr int KB = 64;         // keys per block
+  constexpr int JN = KB / 16;    // 16-key column tiles of S
   constexpr int KS = HD / 32;    // MFMA K steps of S = Q K^T
   constexpr int NS = HD / 16;    // 16-wide head-dim subtiles of O
   constexpr int KROW = HD + 8;   // padded LDS rows (halves)
@@ -372,10 +423,10 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float* __r
     }
     __syncthreads();
     if (kb0 > q0 + 15) continue;  // every query of this wave precedes the block
-    // S = Q K^T for the wave's 16 queries x 64 keys
-    af4_t sacc[4];
+    // S = Q K^T for the wave's 16 queries x KB keys
+    af4_t sacc[JN];
 #pragma unroll
-    for (int jn = 0; jn < 4; ++jn) {
+    for (int jn = 0; jn < JN; ++jn) {
       sacc[jn] = af4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
@@ -385,14 +436,14 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float* __r
       }
     }
     // mask, scale, online softmax; lane holds rows 4 * (lane >> 4) + r, key column 16 jn + fr
-    float p[4][4];
+    float p[JN][4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = q0 + 4 * (lane >> 4) + r;
       const int jlo = window > 0 ? max(0, i - (window - 1)) : 0;
       float mx = -INFINITY;
 #pragma unroll
-      for (int jn = 0; jn < 4; ++jn) {
+      for (int jn = 0; jn < JN; ++jn) {
         const int j = kb0 + 16 * jn + fr;
         const bool ok = j <= i && j >= jlo && j < M && i < M;
         const float sv = sacc[jn][r] * scale;
@@ -405,7 +456,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float* __r
       const float corr = mn == -INFINITY ? 1.f : expf(mrow[r] - mn);
       float sum = 0.f;
 #pragma unroll
-      for (int jn = 0; jn < 4; ++jn) {
+      for (int jn = 0; jn < JN; ++jn) {
         const float e = p[jn][r] == -INFINITY ? 0.f : expf(p[jn][r] - mn);
         p[jn][r] = e;
         sum += e;
@@ -419,7 +470,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float* __r
     }
     // P to LDS in A-operand order [query][key] (this wave's slice only)
 #pragma unroll
-    for (int jn = 0; jn < 4; ++jn)
+    for (int jn = 0; jn < JN; ++jn)
 #pragma unroll
       for (int r = 0; r < 4; ++r) asplit(p[jn][r], ph[wave][4 * (lane >> 4) + r][16 * jn + fr], pl[wave][4 * (lane >> 4) + r][16 * jn + fr]);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -427,7 +478,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float* __r
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // O += P V
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < KB / 32; ++ks) {
       const au4_t pah = *reinterpret_cast<const au4_t*>(&ph[wave][fr][32 * ks + fk]);
       const au4_t pal = *reinterpret_cast<const au4_t*>(&pl[wave][fr][32 * ks + fk]);
 #pragma unroll
@@ -452,16 +503,24 @@ void launch_attn_prefill(const float* q, const float* k, const float* v, float* 
                          int head_dim, int window, float scale, hipStream_t st) {
   dim3 grid(n_heads, (M + 63) / 64);
   switch (head_dim) {
+#define IEK_AP(HD, KB)                                                                                          \
+  hipLaunchKernelGGL((attn_prefill_mfma_kernel<HD, KB>), grid, dim3(256), 0, st, q, k, v, out, M, n_heads, n_kv, \
+                     window, scale)
     case 64:
-      hipLaunchKernelGGL(attn_prefill_mfma_kernel<64>, grid, dim3(256), 0, st, q, k, v, out, M, n_heads, n_kv, window,
-                         scale);
+      IEK_AP(64, 64);
       break;
     case 128:
-      hipLaunchKernelGGL(attn_prefill_mfma_kernel<128>, grid, dim3(256), 0, st, q, k, v, out, M, n_heads, n_kv, window,
-                         scale);
+      IEK_AP(128, 64);
       break;
+    case 256:
+      IEK_AP(256, 32);
+      break;
+    case 512:
+      IEK_AP(512, 32);
+      break;
+#undef IEK_AP
     default:
-      fail(ST_OP, "prefill attention: head_dim must be 64 or 128");
+      fail(ST_OP, "prefill attention: head_dim must be 64, 128, 256 or 512");
   }
 }
 

@@ -36,6 +36,15 @@ IEK_DEV float wave_max(float v) {
   return v;
 }
 
+// gelu_tanh (src/ops/gelu.rs:5-11): 0.5 x (1 + tanh(k (x + 0.044715 x^3))) with
+// k = FRAC_2_SQRT_PI * FRAC_1_SQRT_2 rounded to f32, each step rounded separately.
+IEK_DEV float gelu_tanh_dev(float x) {
+#pragma clang fp contract(off)
+  const float k = 1.12837916709551257390f * 0.707106781186547524401f;
+  float x3 = x * x * x;
+  return 0.5f * x * (1.0f + tanhf(k * (x + 0.044715f * x3)));
+}
+
 IEK_DEV uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xFFu; }
 
 // get_scale_min_k4 over the 12 packed scale bytes held as three dwords

@@ -345,7 +345,7 @@ IEK_DEV int seg_base(const MvArgs& a, int s) { return s == 0 ? a.seg_start[0] : 
 template <int R>
 IEK_DEV void epilogue(const MvArgs& a, const Lds& L, int s, int lr0, float (&acc)[R], const float* acc_up, int lane,
                       int pos, unsigned long long& run_key) {
-  if (a.epi == EPI_SWIGLU) {
+  if (a.epi == EPI_SWIGLU || a.epi == EPI_GEGLU) {
     if (lane < R) {
       float g = acc[0], u = acc_up[0];
 #pragma unroll
@@ -354,7 +354,7 @@ IEK_DEV void epilogue(const MvArgs& a, const Lds& L, int s, int lr0, float (&acc
           g = acc[r];
           u = acc_up[r];
         }
-      a.out[0][lr0 + lane] = silu_mul(g, u);
+      a.out[0][lr0 + lane] = a.epi == EPI_GEGLU ? gelu_tanh_dev(g) * u : silu_mul(g, u);
     }
     return;
   }
@@ -851,6 +851,81 @@ void launch_repack_q6k(const void* src, int K, int N, void* dst, hipStream_t st)
                      (const uint8_t*)src, nsb, N, (uint8_t*)dst);
 }
 
+// Q8_0 in a regrouped per-row layout (DT_Q8_0_R, built once at model load by launch_repack_q80):
+// a row's nb = K/32 blocks keep their 32 int8 quants as nb contiguous 32-byte runs, followed by
+// the nb f16 scales (padded to 16 bytes), so one lane's block is two 16-byte loads and one short
+// load instead of 34 bytes at 2-byte alignment. The bytes are the native ones, rearranged.
+// x stays f32 here (the Gemma-4 models that use Q8_0 have a score scale of 1 on normalised q/k,
+// which turns the int8 staging's 2^-16 activation rounding into ~1e-3 of logit error): each quant
+// byte is read as the unsigned q + 128 (v_cvt_f32_ubyte after flipping the sign bits), and the
+// offset comes back as one term per block, d * (sum x*(q+128) - 128 * sum x).
+struct Q8RTr {
+  static constexpr bool I8 = false;
+  static constexpr bool WB = false;
+  static constexpr int CHUNKS = 8;  // 32-value blocks per 256
+  static constexpr int BYTES = 34;
+  IEK_DEV static size_t row_bytes(int nsb) { return q8r_row_bytes((size_t)nsb * 8); }
+  template <int NR>
+  struct Buf {
+    uint4 qa[NR], qb[NR];
+    uint32_t d[NR];
+  };
+  template <int NR>
+  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c, int nsb) {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const uint8_t* m = rows[r] + (size_t)c * 32;
+      b.qa[r] = *reinterpret_cast<const uint4*>(m);
+      b.qb[r] = *reinterpret_cast<const uint4*>(m + 16);
+      b.d[r] = *reinterpret_cast<const uint16_t*>(rows[r] + (size_t)nsb * 256 + 2 * c);
+    }
+  }
+  template <int NR>
+  IEK_DEV static void compute(const Buf<NR>& b, int c, const Lds& L, float (&acc)[NR]) {
+    const float4* x4 = reinterpret_cast<const float4*>(L.x + 32 * c);
+    float4 xv[8];
+    float xsum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      xv[t] = x4[t];
+      xsum += (xv[t].x + xv[t].y) + (xv[t].z + xv[t].w);
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const uint32_t q[8] = {b.qa[r].x, b.qa[r].y, b.qa[r].z, b.qa[r].w, b.qb[r].x, b.qb[r].y, b.qb[r].z, b.qb[r].w};
+      float s = 0.f;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const uint32_t u = q[t] ^ 0x80808080u;  // bytes q + 128
+        s += xv[t].x * ubyte_f<0>(u) + xv[t].y * ubyte_f<1>(u) + xv[t].z * ubyte_f<2>(u) + xv[t].w * ubyte_f<3>(u);
+      }
+      acc[r] += half_bits_to_float(b.d[r]) * (s - 128.f * xsum);
+    }
+  }
+};
+
+// One thread per (row, block): regroup a Q8_0 tensor [K, N] (K % 32 == 0) into DT_Q8_0_R.
+__global__ void repack_q80_kernel(const uint8_t* __restrict__ src, int nb, int N, uint8_t* __restrict__ dst) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)N * nb) return;
+  const int b = (int)(i % nb);
+  const size_t n = i / nb;
+  const uint8_t* blk = src + i * Q8_0_BYTES;
+  uint8_t* row = dst + n * q8r_row_bytes(nb);
+  for (int t = 0; t < 32; ++t) row[32 * b + t] = blk[2 + t];
+  row[(size_t)32 * nb + 2 * b] = blk[0];
+  row[(size_t)32 * nb + 2 * b + 1] = blk[1];
+}
+
+void launch_repack_q80(const void* src, int K, int N, void* dst, hipStream_t st) {
+  if (K % Q8_0_ELEMS != 0) fail(ST_OP, "repack_q80: K must be a multiple of 32");
+  const int nb = K / Q8_0_ELEMS;
+  IEK_HIP(hipMemsetAsync(dst, 0, (size_t)N * q8r_row_bytes(nb), st));
+  const size_t threads = (size_t)N * nb;
+  hipLaunchKernelGGL(repack_q80_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                     (const uint8_t*)src, nb, N, (uint8_t*)dst);
+}
+
 template <class Tr, int R, bool DUAL>
 __global__ __launch_bounds__(256) void mv_stream(MvArgs a) {
   extern __shared__ __align__(16) float lds[];
@@ -972,7 +1047,7 @@ __global__ __launch_bounds__(256) void mv_generic(MvArgs a, int dt) {
   if (row < total) {  // no early return: argmax_flush below has a workgroup barrier
     const int s = seg_of(a, row);
     const int n = row - a.seg_start[s];
-    const bool dual = a.epi == EPI_SWIGLU;
+    const bool dual = a.epi == EPI_SWIGLU || a.epi == EPI_GEGLU;
     const int K = a.K;
     float g = 0.f, u = 0.f;
     for (int k = lane; k < K; k += WAVE) {
@@ -1038,14 +1113,14 @@ void launch_mv(int dt, MvArgs a, hipStream_t st) {
     total += a.n[i];
   }
   a.seg_start[a.nseg] = total;
-  const bool dual = a.epi == EPI_SWIGLU;
+  const bool dual = a.epi == EPI_SWIGLU || a.epi == EPI_GEGLU;
   if (dual) {
     // the row space is the gate rows; the up weight rides along as w[1]
     a.seg_start[1] = a.n[0];
     a.nseg = 1;
     total = a.n[0];
   }
-  bool fast = (dt == DT_Q4K || dt == DT_Q6K || dt == DT_Q6K_R) && a.K % QK_K == 0 &&
+  bool fast = (dt == DT_Q4K || dt == DT_Q6K || dt == DT_Q6K_R || dt == DT_Q8_0_R) && a.K % QK_K == 0 &&
               (reinterpret_cast<uintptr_t>(a.x) % 16) == 0;
   for (int i = 0; i < (dual ? 2 : a.nseg); ++i) fast = fast && (reinterpret_cast<uintptr_t>(a.w[i]) % 16) == 0;
   // K-quants take the int8-staged x (v_dot4) path when x and the norm weight are 16-byte aligned
@@ -1066,6 +1141,9 @@ void launch_mv(int dt, MvArgs a, hipStream_t st) {
         if (!i8) fail(ST_OP, "matvec: the regrouped Q6_K layout needs the int8-staged path");
         if (dual) IEK_L(Q6RTr, true);
         else IEK_L(Q6RTr, false);
+      } else if (dt == DT_Q8_0_R) {
+        if (dual) IEK_L(Q8RTr, true);
+        else IEK_L(Q8RTr, false);
       } else if (dt == DT_Q4K && i8) {
         if (dual) IEK_L(Q4I8Tr, true);
         else IEK_L(Q4I8Tr, false);
@@ -1086,7 +1164,8 @@ void launch_mv(int dt, MvArgs a, hipStream_t st) {
   const size_t lds_f = lds_bytes(a, false);
   if (lds_f > 160 * 1024) fail(ST_OP, "matvec: K too large for the LDS-staged input");
   if (a.epi == EPI_QKV) fail(ST_OP, "matvec: fused Q/K/V epilogue needs the aligned K-quant path");
-  if (dt == DT_Q6K_R) fail(ST_OP, "matvec: the regrouped Q6_K layout needs K % 256 == 0 and aligned inputs");
+  if (dt == DT_Q6K_R || dt == DT_Q8_0_R)
+    fail(ST_OP, "matvec: a regrouped weight layout needs K % 256 == 0 and aligned inputs");
   hipLaunchKernelGGL(mv_generic, dim3((total + 3) / 4), dim3(256), lds_f, st, a, dt);
 }
 

@@ -169,13 +169,7 @@ void launch_swiglu(const float* g, const float* u, float* out, size_t n, hipStre
   hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, u, out, n);
 }
 
-// gelu_tanh(g) * u (src/ops/gelu.rs:5-11, src/layers/ffn.rs:49-53).
-IEK_DEV float gelu_tanh_dev(float x) {
-#pragma clang fp contract(off)
-  const float k = 1.12837916709551257390f * 0.707106781186547524401f;
-  float x3 = x * x * x;
-  return 0.5f * x * (1.0f + tanhf(k * (x + 0.044715f * x3)));
-}
+// gelu_tanh(g) * u (src/layers/ffn.rs:49-53); gelu_tanh_dev is in common.cuh.
 
 __global__ void gelu_mul_kernel(const float* g, const float* u, float* out, size_t n) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;

@@ -536,28 +536,44 @@ Model* load_model(const std::string& path, int device) {
     m->by_name[w.name] = &d;
   }
 
-  // Regrouped copies of the Q6_K matrices the decode matvec streams (ffn_down, LM head): same
-  // bytes, laid out for 16-byte lane loads (DT_Q6K_R). The native blocks stay in place for every
-  // other consumer.
+  // Regrouped copies of the matrices the decode matvec streams, laid out for 16-byte lane loads:
+  // Q6_K ffn_down and LM head (DT_Q6K_R), and every Q8_0 projection and a Q8_0 LM head
+  // (DT_Q8_0_R). Same bytes, rearranged; the native blocks stay in place for every other consumer
+  // (prefill GEMM, embedding lookups, op-level entry points).
   {
-    std::vector<DevTensor*> q6;
-    for (auto& L : m->layers)
-      if (L.down.present() && L.down.dtype == DT_Q6K && L.down.dims.size() == 2 && L.down.dims[0] % 256 == 0)
-        q6.push_back(&L.down);
-    if (m->lm_head.present() && m->lm_head.dtype == DT_Q6K && m->lm_head.dims.size() == 2 &&
-        m->lm_head.dims[0] % 256 == 0)
-      q6.push_back(&m->lm_head);
+    std::vector<DevTensor*> rg;
+    auto consider = [&](DevTensor& t) {
+      if (!t.present() || t.dims.size() != 2 || t.dims[0] % 256 != 0) return;
+      if (t.dtype != DT_Q6K && t.dtype != DT_Q8_0) return;
+      for (DevTensor* o : rg)
+        if (o == &t) return;
+      rg.push_back(&t);
+    };
+    for (auto& L : m->layers) {
+      if (L.down.dtype == DT_Q6K) consider(L.down);
+      for (DevTensor* t : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down, &L.ple_gate, &L.ple_proj})
+        if (t->dtype == DT_Q8_0) consider(*t);
+    }
+    consider(m->lm_head);
     size_t total_r = 0;
     std::vector<size_t> off_r;
-    for (DevTensor* t : q6) {
+    for (DevTensor* t : rg) {
       off_r.push_back(total_r);
-      total_r += (q6r_row_bytes(t->dims[0] / 256) * t->dims[1] + 255) / 256 * 256;
+      const size_t rb = t->dtype == DT_Q6K ? q6r_row_bytes(t->dims[0] / 256) : q8r_row_bytes(t->dims[0] / 32);
+      total_r += (rb * t->dims[1] + 255) / 256 * 256;
     }
     if (total_r) {
       IEK_HIP(hipMalloc(&m->blob_r, total_r));
-      for (size_t i = 0; i < q6.size(); ++i) {
-        q6[i]->dev_r = (char*)m->blob_r + off_r[i];
-        launch_repack_q6k(q6[i]->dev, (int)q6[i]->dims[0], (int)q6[i]->dims[1], q6[i]->dev_r, nullptr);
+      for (size_t i = 0; i < rg.size(); ++i) {
+        DevTensor* t = rg[i];
+        t->dev_r = (char*)m->blob_r + off_r[i];
+        if (t->dtype == DT_Q6K) {
+          t->dtype_r = DT_Q6K_R;
+          launch_repack_q6k(t->dev, (int)t->dims[0], (int)t->dims[1], t->dev_r, nullptr);
+        } else {
+          t->dtype_r = DT_Q8_0_R;
+          launch_repack_q80(t->dev, (int)t->dims[0], (int)t->dims[1], t->dev_r, nullptr);
+        }
       }
       IEK_HIP(hipDeviceSynchronize());
     }

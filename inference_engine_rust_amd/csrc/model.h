@@ -84,7 +84,8 @@ struct DevTensor {
   std::vector<size_t> dims;
   size_t bytes = 0;
   void* dev = nullptr;
-  void* dev_r = nullptr;        // Q6_K only: regrouped copy (DT_Q6K_R) for the decode matvec
+  void* dev_r = nullptr;        // regrouped copy for the decode matvec (Q6_K, Q8_0), or null
+  int dtype_r = -1;             // its layout: DT_Q6K_R or DT_Q8_0_R
   std::vector<float> host_f32;  // small F32 tensors also kept on the host (norms, scales)
   bool present() const { return dev != nullptr; }
 };
@@ -111,7 +112,7 @@ struct Model {
   std::string path;
   void* blob = nullptr;  // one HBM allocation for every weight
   size_t blob_bytes = 0;
-  void* blob_r = nullptr;  // regrouped copies of the Q6_K matvec weights (ffn_down, output)
+  void* blob_r = nullptr;  // regrouped copies of the matvec weights (Q6_K ffn_down/output, Q8_0 matrices)
   DevTensor token_embd, output_norm, lm_head;
   std::vector<LayerTensors> layers;
   DevTensor ple_token_embd, ple_model_proj, ple_proj_norm;

@@ -4,6 +4,8 @@
 //   prefill_attention_layer / decode_attention   src/layers/attention.rs:175-655
 //   mistral_prefill_ffn_with_norm / prefill_ffn  src/layers/ffn.rs:16-117
 //   final_logits_last_token                      src/engine/runtime.rs:76-116
+//   Gemma-4: head norms, post-norms, GeGLU, PLE  attention.rs:277-308,424-455; ffn.rs:120-278;
+//                                                src/layers/gemma4_ple.rs:27-109; embed.rs:53-149
 #include "session.h"
 
 #include "kernels/mv_args.h"
@@ -30,20 +32,34 @@ void dev_free(void* p) {
 
 Session::Session(Model* m) : m_(m) {
   const Config& c = m->cfg;
-  if (c.family != FAM_MISTRAL_LLAMA)
-    fail(ST_MODEL, "device session: the Gemma 4 family is not supported by the device engine yet");
+  gemma_ = c.family == FAM_GEMMA4;
   IEK_HIP(hipSetDevice(m->device));
   IEK_HIP(hipStreamCreateWithFlags(&st_, hipStreamNonBlocking));
   ctx_ = c.context_length;
   H_ = c.hidden;
   // KV cache (fp16): per layer K and V as [n_kv][ctx][head_dim] (kv_caches_for_config,
   // attention.rs:129-135, sizes every cache to context_length).
+  // A layer that borrows another layer's KV (Gemma-4 shared-KV layers, model_config.rs:332-372)
+  // never appends to its own cache; it gets none and aliases its source's.
+  // Gemma-4 keeps the reference's f32 cache: its attention has q/k head norms and a score scale of
+  // 1, and fp16 keys/values there move the logits by ~1e-2 relative.
+  kv_f32_ = gemma_;
+  const size_t esz = kv_f32_ ? 4 : 2;
   size_t total = 0;
-  for (auto& L : c.layers) total += 2 * (size_t)c.n_kv_heads * ctx_ * L.head_dim;
-  IEK_HIP(hipMalloc(&kv_blob_, std::max<size_t>(total * sizeof(__half), 16)));
-  __half* p = static_cast<__half*>(kv_blob_);
-  for (auto& L : c.layers) {
-    size_t per = (size_t)c.n_kv_heads * ctx_ * L.head_dim;
+  for (auto& L : c.layers)
+    if (L.kv_borrow < 0) total += 2 * (size_t)c.n_kv_heads * ctx_ * L.head_dim;
+  IEK_HIP(hipMalloc(&kv_blob_, std::max<size_t>(total * esz, 16)));
+  char* p = static_cast<char*>(kv_blob_);
+  for (int li = 0; li < c.n_layers; ++li) {
+    const LayerSpec& L = c.layers[li];
+    if (L.kv_borrow >= 0) {
+      if (L.kv_borrow >= li || c.layers[L.kv_borrow].head_dim != L.head_dim)
+        fail(ST_MODEL, "borrow source KV shape mismatch");
+      kc_.push_back(kc_[L.kv_borrow]);
+      vc_.push_back(vc_[L.kv_borrow]);
+      continue;
+    }
+    size_t per = (size_t)c.n_kv_heads * ctx_ * L.head_dim * esz;
     kc_.push_back(p);
     vc_.push_back(p + per);
     p += 2 * per;
@@ -75,6 +91,12 @@ Session::Session(Model* m) : m_(m) {
   d_key_ = dev_alloc<unsigned long long>(1);
   d_flag_ = dev_alloc<int>(1);
   d_cnt_ = dev_alloc<int>(c.n_kv_heads);
+  if (gemma_ && c.ple_dim > 0) {
+    const size_t pack = (size_t)c.n_layers * c.ple_dim;
+    ple_tokd_ = dev_alloc<float>(pack);
+    ple_projd_ = dev_alloc<float>(pack);
+    ple_packd_ = dev_alloc<float>(pack);
+  }
   launch_fill_u64(d_key_, 0ull, 1, st_);
   launch_fill_i32(d_flag_, 0, 1, st_);
   launch_fill_i32(d_cnt_, 0, c.n_kv_heads, st_);
@@ -89,7 +111,8 @@ Session::~Session() {
                   (void*)act_, (void*)tmp_, (void*)xdec_, (void*)xndec_, (void*)qd_, (void*)kd_, (void*)vd_,
                   (void*)attd_, (void*)actd_, (void*)logits_, (void*)part_, (void*)tmpd_, (void*)d_pos_,
                   (void*)d_step_, (void*)d_flags_, (void*)d_tok_, (void*)d_ids_, (void*)d_gen_, (void*)d_key_,
-                  (void*)d_flag_, (void*)d_cnt_, (void*)xs_, (void*)xsum_, kv_blob_})
+                  (void*)d_flag_, (void*)d_cnt_, (void*)xs_, (void*)xsum_, kv_blob_, (void*)ple_tok_,
+                  (void*)ple_proj_, (void*)ple_pack_, (void*)ple_tokd_, (void*)ple_projd_, (void*)ple_packd_})
     dev_free(p);
   if (st_) (void)hipStreamDestroy(st_);
 }
@@ -110,7 +133,7 @@ void Session::reset() {
 void Session::ensure_rows(int rows) {
   if (rows <= rows_cap_) return;
   sync();
-  for (float** b : {&x_, &xn_, &q_, &k_, &v_, &att_, &g_, &u_, &act_, &tmp_}) {
+  for (float** b : {&x_, &xn_, &q_, &k_, &v_, &att_, &g_, &u_, &act_, &tmp_, &ple_tok_, &ple_proj_, &ple_pack_}) {
     dev_free(*b);
     *b = nullptr;
   }
@@ -139,14 +162,20 @@ void Session::ensure_rows(int rows) {
   // fp16 (hi, lo) pair of the widest GEMM input, for the matrix-core prefill projections
   xs_ = dev_alloc<__half>(2 * R * std::max(std::max(H_, qmax), fmax));
   xsum_ = dev_alloc<float>(R * std::max(std::max(H_, qmax), fmax) / 32 + 1);
+  if (gemma_ && c.ple_dim > 0) {
+    const size_t pack = (size_t)c.n_layers * c.ple_dim;
+    ple_tok_ = dev_alloc<float>(R * pack);
+    ple_proj_ = dev_alloc<float>(R * pack);
+    ple_pack_ = dev_alloc<float>(R * pack);
+  }
   rows_cap_ = rows;
 }
 
-// The weight copy the decode matvec streams: the regrouped Q6_K layout when the model built one
-// and the int8-staged path (which it requires) is active, else the native blocks.
+// The weight copy the decode matvec streams: the regrouped layout when the model built one (the
+// Q6_K one only with the int8-staged path, which it requires), else the native blocks.
 static const void* mv_weight(const DevTensor& t, int K, int* dt) {
-  if (t.dev_r && mv_int8_staging() && K <= 16384) {
-    *dt = DT_Q6K_R;
+  if (t.dev_r && K <= 16384 && (t.dtype_r != DT_Q6K_R || mv_int8_staging())) {
+    *dt = t.dtype_r;
     return t.dev_r;
   }
   *dt = t.dtype;
@@ -181,7 +210,7 @@ bool Session::project_q(const DevTensor* const* ws, float* const* outs, int nseg
     if (w.dims.size() != 2 || (int)w.dims[0] != K) return false;
     int wdt = w.dtype;
     const void* p = w.dev;
-    if (w.dev_r) {
+    if (w.dev_r && w.dtype_r == DT_Q6K_R) {
       wdt = DT_Q6K_R;
       p = w.dev_r;
     }
@@ -229,7 +258,7 @@ void Session::layer_prefill(int li, int M) {
   const RopeTable& rt = m_->rope_tables[L.rope_table];
   launch_rope_rows(q_, M, qd, c.n_heads, hd, 0, rt.dev, S.rotary_dim / 2, st_);
   launch_rope_rows(k_, M, kvd, c.n_kv_heads, hd, 0, rt.dev, S.rotary_dim / 2, st_);
-  launch_kv_store(k_, v_, M, kvd, kc_[li], vc_[li], c.n_kv_heads, hd, ctx_, nullptr, pos_, st_);
+  launch_kv_store(k_, v_, M, kvd, (__half*)kc_[li], (__half*)vc_[li], c.n_kv_heads, hd, ctx_, nullptr, pos_, st_);
   const float scale = 1.0f / sqrtf((float)hd);
   launch_attn_prefill(q_, k_, v_, att_, M, c.n_heads, c.n_kv_heads, hd, S.window, scale, st_);
   {
@@ -303,10 +332,10 @@ void Session::layer_decode(int li, bool last) {
   a.head_dim = hd;
   a.ctx = ctx_;
   a.pos = d_pos_;
-  a.kc = kc_[li];
-  a.vc = vc_[li];
+  a.kc = (__half*)kc_[li];
+  a.vc = (__half*)vc_[li];
   launch_mv(L.wq.dtype, a, st_);
-  launch_attn_decode(qd_, kc_[li], vc_[li], attd_, part_, d_cnt_, c.n_heads, c.n_kv_heads, hd, ctx_, d_pos_, S.window,
+  launch_attn_decode(qd_, kc_[li], vc_[li], kv_f32_, attd_, part_, d_cnt_, c.n_heads, c.n_kv_heads, hd, ctx_, d_pos_, S.window,
                      scale, ctx_, st_);
   MvArgs o{};
   o.nseg = 1;
@@ -368,9 +397,9 @@ void Session::layer_decode_unfused(int li) {
   const RopeTable& rt = m_->rope_tables[L.rope_table];
   launch_rope_table(qd_, c.n_heads, hd, S.rotary_dim / 2, rt.dev, d_pos_, st_);
   launch_rope_table(kd_, c.n_kv_heads, hd, S.rotary_dim / 2, rt.dev, d_pos_, st_);
-  launch_kv_store(kd_, vd_, 1, kvd, kc_[li], vc_[li], c.n_kv_heads, hd, ctx_, d_pos_, 0, st_);
+  launch_kv_store(kd_, vd_, 1, kvd, (__half*)kc_[li], (__half*)vc_[li], c.n_kv_heads, hd, ctx_, d_pos_, 0, st_);
   const float scale = 1.0f / sqrtf((float)hd);
-  launch_attn_decode(qd_, kc_[li], vc_[li], attd_, part_, d_cnt_, c.n_heads, c.n_kv_heads, hd, ctx_, d_pos_, S.window,
+  launch_attn_decode(qd_, kc_[li], vc_[li], kv_f32_, attd_, part_, d_cnt_, c.n_heads, c.n_kv_heads, hd, ctx_, d_pos_, S.window,
                      scale, ctx_, st_);
   project(L.wo, attd_, nullptr, 1, qd, H_, xdec_, xdec_, st_);
   launch_rmsnorm(xdec_, (const float*)L.ffn_norm.dev, 1, H_, c.rms_eps, xndec_, st_);
@@ -383,6 +412,220 @@ void Session::layer_decode_unfused(int li) {
     launch_swiglu(tmpd_, actd_, actd_, S.ffn_dim, st_);
   }
   project(L.down, actd_, nullptr, 1, S.ffn_dim, H_, xdec_, xdec_, st_);
+}
+
+// ---- Gemma-4 family ---------------------------------------------------------------------------
+
+// fp16 (hi, lo) pair and per-32 sums of a GEMM input, when it has more than one row and a width
+// the split takes; null otherwise.
+const __half* Session::split_rows(const float* a, int M, int K) {
+  if (M < 2 || K % 32 != 0) return nullptr;
+  launch_split_f16(a, (size_t)M * K, xs_, xs_ + (size_t)M * K, st_);
+  launch_block_sums(a, M, K, xsum_, st_);
+  return xs_;
+}
+
+// Per-layer embedding inputs for n token rows (compute_packed_per_layer_inputs,
+// gemma4_ple.rs:27-109): model projection of the scaled embeddings `x`, per-layer RMSNorm, plus
+// the per-layer token rows scaled by sqrt(pd), times 1/sqrt(2).
+void Session::embed_ple(const uint32_t* d_ids, int n, const float* x, const __half* xs, float* tok, float* proj,
+                        float* pack) {
+  const Config& c = m_->cfg;
+  if (c.ple_dim <= 0) return;
+  const int packn = c.n_layers * c.ple_dim;
+  size_t vocab;
+  const DevTensor& te = m_->ple_token_embd;
+  if (te.dims.size() != 2) fail(ST_TENSOR, "expected 2D embedding tensor");
+  const size_t row = std::min(te.dims[0], te.dims[1]);
+  vocab = std::max(te.dims[0], te.dims[1]);
+  (void)vocab;
+  if ((int)row != packn) fail(ST_MODEL, "per_layer_token_embd row width != n_layers*ple_dim");
+  if (m_->ple_proj_norm.host_f32.size() != (size_t)c.ple_dim)
+    fail(ST_MODEL, "per_layer_proj_norm len != ple_dim");
+  launch_embed(te.dtype, te.dev, row, d_ids, n, 1.0f, tok, st_);
+  project(m_->ple_model_proj, x, xs, n, H_, packn, proj, nullptr, st_);
+  launch_ple_pack(proj, tok, (const float*)m_->ple_proj_norm.dev, n, c.n_layers, c.ple_dim, c.rms_eps,
+                  c.ple_proj_scale, sqrtf((float)c.ple_dim), c.ple_combine_scale, pack, st_);
+}
+
+// prefill_layer_block for Gemma-4 (block.rs:12-47): attention with q/k head norms, v norm,
+// optional KV borrowing and sliding window, scale 1 (attention.rs:175-422), post-attention norm +
+// residual; GeGLU FFN with post-FFN norm + residual (ffn.rs:120-167); PLE tail (ffn.rs:170-240)
+// and the layer output scale (ffn.rs:242-278), folded into the last residual update.
+void Session::layer_prefill_gemma(int li, int M) {
+  const Config& c = m_->cfg;
+  const LayerSpec& S = c.layers[li];
+  const LayerTensors& L = m_->layers[li];
+  const int hd = S.head_dim, qd = S.q_dim, kvd = S.kv_dim;
+  const float eps = c.rms_eps;
+  const bool borrow = S.kv_borrow >= 0;
+  if (borrow && pos_ != 0) fail(ST_MODEL, "prefill attention: borrow source cache len mismatch");
+  if (!L.attn_post_norm.present()) fail(ST_MODEL, "Gemma 4: missing post_attention_norm");
+  if (!L.ffn_post_norm.present()) fail(ST_MODEL, "Gemma 4: missing post_ffw_norm");
+  launch_rmsnorm(x_, (const float*)L.attn_norm.dev, M, H_, eps, xn_, st_);
+  const __half* xs = split_rows(xn_, M, H_);
+  {
+    const DevTensor* ws[3] = {&L.wq, &L.wk, &L.wv};
+    float* outs[3] = {q_, k_, v_};
+    if (!xs || !project_q(ws, outs, borrow ? 1 : 3, M, H_, nullptr)) {
+      project(L.wq, xn_, xs, M, H_, qd, q_, nullptr, st_);
+      if (!borrow) {
+        project(L.wk, xn_, xs, M, H_, kvd, k_, nullptr, st_);
+        project(L.wv, xn_, xs, M, H_, kvd, v_, nullptr, st_);
+      }
+    }
+  }
+  const RopeTable& rt = m_->rope_tables[L.rope_table];
+  launch_head_prep(q_, k_, v_, M, qd, kvd, c.n_heads, borrow ? 0 : c.n_kv_heads, hd,
+                   L.q_norm.present() ? (const float*)L.q_norm.dev : nullptr,
+                   L.k_norm.present() ? (const float*)L.k_norm.dev : nullptr, eps, true, rt.dev, S.rotary_dim / 2,
+                   nullptr, 0, pos_, borrow ? nullptr : kc_[li], borrow ? nullptr : vc_[li], kv_f32_, ctx_, st_);
+  if (borrow) launch_kv_load(kc_[li], vc_[li], kv_f32_, M, c.n_kv_heads, hd, ctx_, k_, v_, st_);
+  launch_attn_prefill(q_, k_, v_, att_, M, c.n_heads, c.n_kv_heads, hd, S.window, 1.0f, st_);
+  {
+    const __half* xa = split_rows(att_, M, qd);
+    const DevTensor* ws[1] = {&L.wo};
+    float* outs[1] = {tmp_};
+    if (!xa || !project_q(ws, outs, 1, M, qd, nullptr)) project(L.wo, att_, xa, M, qd, H_, tmp_, nullptr, st_);
+  }
+  launch_rmsnorm_add(x_, tmp_, (const float*)L.attn_post_norm.dev, M, H_, eps, false, 1.f, st_);
+  launch_rmsnorm(x_, (const float*)L.ffn_norm.dev, M, H_, eps, xn_, st_);
+  xs = split_rows(xn_, M, H_);
+  {
+    const DevTensor* ws[2] = {&L.gate, &L.up};
+    float* outs[2] = {g_, u_};
+    if (!xs || !project_q(ws, outs, 2, M, H_, nullptr)) {
+      project(L.gate, xn_, xs, M, H_, S.ffn_dim, g_, nullptr, st_);
+      project(L.up, xn_, xs, M, H_, S.ffn_dim, u_, nullptr, st_);
+    }
+  }
+  launch_gelu_mul(g_, u_, act_, (size_t)M * S.ffn_dim, st_);
+  {
+    const __half* xa = split_rows(act_, M, S.ffn_dim);
+    const DevTensor* ws[1] = {&L.down};
+    float* outs[1] = {tmp_};
+    if (!xa || !project_q(ws, outs, 1, M, S.ffn_dim, nullptr))
+      project(L.down, act_, xa, M, S.ffn_dim, H_, tmp_, nullptr, st_);
+  }
+  const bool ple = c.ple_dim > 0;
+  launch_rmsnorm_add(x_, tmp_, (const float*)L.ffn_post_norm.dev, M, H_, eps, !ple && L.has_out_scale,
+                     L.out_scale_value, st_);
+  if (ple) {
+    const int pd = c.ple_dim;
+    if (!L.ple_gate.present() || !L.ple_proj.present() || !L.ple_post_norm.present())
+      fail(ST_MODEL, "PLE: missing inp_gate / proj / post_norm");
+    xs = split_rows(x_, M, H_);
+    project(L.ple_gate, x_, xs, M, H_, pd, g_, nullptr, st_);
+    launch_ple_gate(g_, ple_pack_, M, pd, c.n_layers, li, st_);
+    const __half* xg = split_rows(g_, M, pd);
+    project(L.ple_proj, g_, xg, M, pd, H_, tmp_, nullptr, st_);
+    launch_rmsnorm_add(x_, tmp_, (const float*)L.ple_post_norm.dev, M, H_, eps, L.has_out_scale, L.out_scale_value,
+                       st_);
+  }
+}
+
+// One decode-step matvec over up to three weights sharing x (optionally RMS-normalised on the
+// way in). Uses the regrouped copies when every weight has one of the same layout.
+static void mv_multi(const DevTensor* const* ws, float* const* outs, int nseg, const float* x, int K,
+                     const float* norm_w, float eps, int epi, hipStream_t st) {
+  int dt0 = -1;
+  const void* wp[3];
+  bool same = true;
+  for (int i = 0; i < nseg; ++i) {
+    const DevTensor& w = *ws[i];
+    if (w.dims.size() != 2 || (int)w.dims[0] != K)
+      fail(ST_MATMUL, "inner dim mismatch: weight dims do not match the activation width");
+    int dt;
+    wp[i] = mv_weight(w, K, &dt);
+    if (dt0 >= 0 && dt != dt0) same = false;
+    dt0 = dt;
+  }
+  if (!same) {  // mixed layouts: native blocks, one launch per weight
+    for (int i = 0; i < nseg; ++i) {
+      const DevTensor* one[1] = {ws[i]};
+      DevTensor native = *ws[i];
+      native.dev_r = nullptr;
+      one[0] = &native;
+      float* o[1] = {outs[i]};
+      mv_multi(one, o, 1, x, K, norm_w, eps, epi, st);
+    }
+    return;
+  }
+  MvArgs a{};
+  a.nseg = nseg;
+  for (int i = 0; i < nseg; ++i) {
+    a.w[i] = (const uint8_t*)wp[i];
+    a.out[i] = outs[i];
+    a.n[i] = (int)ws[i]->dims[1];
+  }
+  a.x = x;
+  a.norm_w = norm_w;
+  a.eps = eps;
+  a.K = K;
+  a.epi = epi;
+  launch_mv(dt0, a, st);
+}
+
+// decode_layer_block for Gemma-4 (block.rs:50-89), same sub-steps as layer_prefill_gemma for one
+// token at the device position (*d_pos_).
+void Session::layer_decode_gemma(int li) {
+  const Config& c = m_->cfg;
+  const LayerSpec& S = c.layers[li];
+  const LayerTensors& L = m_->layers[li];
+  const int hd = S.head_dim, qd = S.q_dim, kvd = S.kv_dim;
+  const float eps = c.rms_eps;
+  const bool borrow = S.kv_borrow >= 0;
+  if (!L.attn_post_norm.present()) fail(ST_MODEL, "Gemma 4: missing post_attention_norm");
+  if (!L.ffn_post_norm.present()) fail(ST_MODEL, "Gemma 4: missing post_ffw_norm");
+  {
+    const DevTensor* ws[3] = {&L.wq, &L.wk, &L.wv};
+    float* outs[3] = {qd_, kd_, vd_};
+    mv_multi(ws, outs, borrow ? 1 : 3, xdec_, H_, (const float*)L.attn_norm.dev, eps, EPI_STORE, st_);
+  }
+  const RopeTable& rt = m_->rope_tables[L.rope_table];
+  launch_head_prep(qd_, kd_, vd_, 1, qd, kvd, c.n_heads, borrow ? 0 : c.n_kv_heads, hd,
+                   L.q_norm.present() ? (const float*)L.q_norm.dev : nullptr,
+                   L.k_norm.present() ? (const float*)L.k_norm.dev : nullptr, eps, true, rt.dev, S.rotary_dim / 2,
+                   d_pos_, 0, 0, borrow ? nullptr : kc_[li], borrow ? nullptr : vc_[li], kv_f32_, ctx_, st_);
+  launch_attn_decode(qd_, kc_[li], vc_[li], kv_f32_, attd_, part_, d_cnt_, c.n_heads, c.n_kv_heads, hd, ctx_, d_pos_, S.window,
+                     1.0f, ctx_, st_);
+  {
+    const DevTensor* ws[1] = {&L.wo};
+    float* outs[1] = {tmpd_};
+    mv_multi(ws, outs, 1, attd_, qd, nullptr, eps, EPI_STORE, st_);
+  }
+  launch_rmsnorm_add(xdec_, tmpd_, (const float*)L.attn_post_norm.dev, 1, H_, eps, false, 1.f, st_);
+  {
+    const DevTensor* ws[2] = {&L.gate, &L.up};
+    float* outs[2] = {actd_, nullptr};
+    mv_multi(ws, outs, 2, xdec_, H_, (const float*)L.ffn_norm.dev, eps, EPI_GEGLU, st_);
+  }
+  {
+    const DevTensor* ws[1] = {&L.down};
+    float* outs[1] = {tmpd_};
+    mv_multi(ws, outs, 1, actd_, S.ffn_dim, nullptr, eps, EPI_STORE, st_);
+  }
+  const bool ple = c.ple_dim > 0;
+  launch_rmsnorm_add(xdec_, tmpd_, (const float*)L.ffn_post_norm.dev, 1, H_, eps, !ple && L.has_out_scale,
+                     L.out_scale_value, st_);
+  if (ple) {
+    const int pd = c.ple_dim;
+    if (!L.ple_gate.present() || !L.ple_proj.present() || !L.ple_post_norm.present())
+      fail(ST_MODEL, "PLE: missing inp_gate / proj / post_norm");
+    {
+      const DevTensor* ws[1] = {&L.ple_gate};
+      float* outs[1] = {actd_};
+      mv_multi(ws, outs, 1, xdec_, H_, nullptr, eps, EPI_STORE, st_);
+    }
+    launch_ple_gate(actd_, ple_packd_, 1, pd, c.n_layers, li, st_);
+    {
+      const DevTensor* ws[1] = {&L.ple_proj};
+      float* outs[1] = {tmpd_};
+      mv_multi(ws, outs, 1, actd_, pd, nullptr, eps, EPI_STORE, st_);
+    }
+    launch_rmsnorm_add(xdec_, tmpd_, (const float*)L.ple_post_norm.dev, 1, H_, eps, L.has_out_scale,
+                       L.out_scale_value, st_);
+  }
 }
 
 static size_t embedding_hidden(const DevTensor& t, size_t* vocab) {
@@ -411,7 +654,12 @@ void Session::prefill(const uint32_t* ids, int n) {
   ensure_rows(n);
   IEK_HIP(hipMemcpyAsync(d_ids_, ids, (size_t)n * 4, hipMemcpyHostToDevice, st_));
   launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, d_ids_, n, c.embed_scale, x_, st_);
-  for (int li = 0; li < c.n_layers; ++li) layer_prefill(li, n);
+  if (gemma_) {
+    embed_ple(d_ids_, n, x_, split_rows(x_, n, H_), ple_tok_, ple_proj_, ple_pack_);
+    for (int li = 0; li < c.n_layers; ++li) layer_prefill_gemma(li, n);
+  } else {
+    for (int li = 0; li < c.n_layers; ++li) layer_prefill(li, n);
+  }
   launch_copy_f32(x_ + (size_t)(n - 1) * H_, xdec_, H_, st_);
   pos_ += n;
   launch_set_int(d_pos_, pos_, st_);
@@ -425,7 +673,13 @@ void Session::decode_body() {
   size_t vocab;
   size_t hid = embedding_hidden(m_->token_embd, &vocab);
   launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, d_tok_, 1, c.embed_scale, xdec_, st_);
-  for (int li = 0; li < c.n_layers; ++li) layer_decode(li, li == c.n_layers - 1);
+  if (gemma_) {
+    embed_ple(d_tok_, 1, xdec_, nullptr, ple_tokd_, ple_projd_, ple_packd_);
+    for (int li = 0; li < c.n_layers; ++li) layer_decode_gemma(li);
+    launch_add_int(d_pos_, 1, st_);
+  } else {
+    for (int li = 0; li < c.n_layers; ++li) layer_decode(li, li == c.n_layers - 1);
+  }
 }
 
 void Session::decode_token(uint32_t id) {
@@ -559,13 +813,18 @@ void Session::copy_kv(int layer, bool v, float* out, size_t cap) {
   const int hd = c.layers[layer].head_dim;
   size_t n = (size_t)c.n_kv_heads * pos_ * hd;
   if (cap < n) fail(ST_OP, "kv buffer too small");
-  std::vector<__half> host((size_t)c.n_kv_heads * ctx_ * hd);
-  IEK_HIP(hipMemcpyAsync(host.data(), v ? vc_[layer] : kc_[layer], host.size() * 2, hipMemcpyDeviceToHost, st_));
+  const size_t cells = (size_t)c.n_kv_heads * ctx_ * hd;
+  std::vector<uint8_t> host(cells * (kv_f32_ ? 4 : 2));
+  IEK_HIP(hipMemcpyAsync(host.data(), v ? vc_[layer] : kc_[layer], host.size(), hipMemcpyDeviceToHost, st_));
   sync();
+  const __half* h16 = reinterpret_cast<const __half*>(host.data());
+  const float* h32 = reinterpret_cast<const float*>(host.data());
   for (int h = 0; h < c.n_kv_heads; ++h)
     for (int p = 0; p < pos_; ++p)
-      for (int d = 0; d < hd; ++d)
-        out[((size_t)h * pos_ + p) * hd + d] = __half2float(host[((size_t)h * ctx_ + p) * hd + d]);
+      for (int d = 0; d < hd; ++d) {
+        const size_t src = ((size_t)h * ctx_ + p) * hd + d;
+        out[((size_t)h * pos_ + p) * hd + d] = kv_f32_ ? h32[src] : __half2float(h16[src]);
+      }
 }
 
 }  // namespace iek

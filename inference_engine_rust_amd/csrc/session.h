@@ -35,6 +35,11 @@ class Session {
   bool fused_ok(int li) const;
   void layer_decode(int li, bool last);
   void layer_decode_unfused(int li);
+  // Gemma-4 family (attention.rs / ffn.rs Gemma branches, gemma4_ple.rs)
+  const __half* split_rows(const float* a, int M, int K);
+  void embed_ple(const uint32_t* d_ids, int n, const float* x, const __half* xs, float* tok, float* proj, float* pack);
+  void layer_prefill_gemma(int li, int M);
+  void layer_decode_gemma(int li);
   void decode_body();           // embed(d_tok) + every layer + pos++; no host sync
   void logits_body(bool argmax);  // final norm + LM head (+ softcap) into logits_
   void argmax_body(bool record);
@@ -45,7 +50,9 @@ class Session {
   hipStream_t st_ = nullptr;
   int ctx_ = 0, H_ = 0;
   void* kv_blob_ = nullptr;
-  std::vector<__half*> kc_, vc_;
+  // per-layer K/V caches [n_kv][ctx][head_dim]: fp16, or f32 when kv_f32_ (Gemma-4)
+  std::vector<void*> kc_, vc_;
+  bool kv_f32_ = false;
   // activations; prefill buffers hold rows_cap_ rows
   int rows_cap_ = 0;
   float *x_ = nullptr, *xn_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *att_ = nullptr;
@@ -54,6 +61,10 @@ class Session {
   float* xsum_ = nullptr;  // its per-32 row sums (Q4_K min term)
   float *xdec_ = nullptr, *xndec_ = nullptr, *qd_ = nullptr, *kd_ = nullptr, *vd_ = nullptr, *attd_ = nullptr;
   float *actd_ = nullptr, *logits_ = nullptr, *part_ = nullptr, *tmpd_ = nullptr;
+  // per-layer embeddings (Gemma-4): token rows, model projection and packed inputs, [rows][L*pd]
+  float *ple_tok_ = nullptr, *ple_proj_ = nullptr, *ple_pack_ = nullptr;
+  float *ple_tokd_ = nullptr, *ple_projd_ = nullptr, *ple_packd_ = nullptr;
+  bool gemma_ = false;
   // device-side loop state
   int* d_pos_ = nullptr;
   int* d_step_ = nullptr;

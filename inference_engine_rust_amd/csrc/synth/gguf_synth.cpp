@@ -200,12 +200,13 @@ void quantize_q8_0(const float* x, uint8_t* b) {
   for (int l = 0; l < 32; ++l) b[2 + l] = (uint8_t)(int8_t)(d > 0 ? std::min(127, std::max(-127, nearest(x[l] / d))) : 0);
 }
 
-enum { T_F32 = 0, T_Q8_0 = 8, T_Q4K = 12, T_Q6K = 14 };
+enum { T_F32 = 0, T_Q8_0 = 8, T_Q4K = 12, T_Q6K = 14, T_BF16 = 30 };
 
 size_t block_elems(int t) { return t == T_Q8_0 ? 32 : 256; }
 size_t block_bytes(int t) { return t == T_Q4K ? 144 : t == T_Q6K ? 210 : 34; }
 size_t tensor_bytes(int t, size_t n) {
   if (t == T_F32) return n * 4;
+  if (t == T_BF16) return n * 2;
   return (n + block_elems(t) - 1) / block_elems(t) * block_bytes(t);
 }
 
@@ -233,6 +234,19 @@ std::vector<uint8_t> make_tensor(uint64_t seed, const std::string& name, int typ
     std::vector<float> v(nelem);
     parallel_chunks(nelem, threads, [&](size_t a, size_t e) { gen_normal(key, a, e - a, mean, stdv, v.data() + a); });
     memcpy(out.data(), v.data(), nelem * 4);
+    return out;
+  }
+  if (type == T_BF16) {  // round to nearest even on the upper 16 bits
+    parallel_chunks(nelem, threads, [&](size_t a, size_t e) {
+      std::vector<float> v(e - a);
+      gen_normal(key, a, e - a, mean, stdv, v.data());
+      for (size_t i = a; i < e; ++i) {
+        uint32_t x;
+        memcpy(&x, &v[i - a], 4);
+        uint16_t h = (uint16_t)((x + 0x7FFFu + ((x >> 16) & 1u)) >> 16);
+        memcpy(out.data() + 2 * i, &h, 2);
+      }
+    });
     return out;
   }
   size_t be = block_elems(type), bb = block_bytes(type), nb = (nelem + be - 1) / be;
@@ -296,56 +310,8 @@ KV kv_bool_arr(const std::string& k, const std::vector<bool>& v) {
   return x;
 }
 
-}  // namespace
-
-extern "C" {
-
-// Model spec for the generator. Types are ggml ids (0 F32, 8 Q8_0, 12 Q4_K, 14 Q6_K).
-struct iek_synth_spec {
-  const char* name;         // general.name ("...mistral..." keeps Q/K un-permute off)
-  uint32_t n_layers, hidden, n_heads, n_kv_heads, ffn, vocab, context_length;
-  float rope_theta, rms_eps, weight_std, norm_std;
-  uint32_t t_attn, t_ffn_gate_up, t_ffn_down, t_embd, t_output;
-  uint32_t tied_output;     // 1: no output.weight (LM head reuses token_embd)
-};
-
-// Writes a Mistral/Llama-family GGUF. Returns 0 on success, nonzero on I/O failure.
-int iek_synth_write_llama(const char* path, const iek_synth_spec* sp, uint64_t seed, int threads) {
-  const iek_synth_spec& s = *sp;
-  uint32_t hd = s.hidden / s.n_heads;
-  std::vector<KV> kvs = {
-      kv_str("general.architecture", "llama"),
-      kv_str("general.name", s.name),
-      kv_u32("general.alignment", 32),
-      kv_u32("llama.context_length", s.context_length),
-      kv_u32("llama.embedding_length", s.hidden),
-      kv_u32("llama.block_count", s.n_layers),
-      kv_u32("llama.attention.head_count", s.n_heads),
-      kv_u32("llama.attention.head_count_kv", s.n_kv_heads),
-      kv_u32("llama.feed_forward_length", s.ffn),
-      kv_f32("llama.attention.layer_norm_rms_epsilon", s.rms_eps),
-      kv_u32("llama.vocab_size", s.vocab),
-      kv_f32("llama.rope.theta", s.rope_theta),
-      kv_u32("llama.rope.dimension_count", hd),
-  };
-  std::vector<TI> tis;
-  float ws = s.weight_std, ns = s.norm_std;
-  tis.push_back({"token_embd.weight", {s.hidden, s.vocab}, s.t_embd, 0.f, ws});
-  for (uint32_t l = 0; l < s.n_layers; ++l) {
-    std::string p = "blk." + std::to_string(l) + ".";
-    tis.push_back({p + "attn_norm.weight", {s.hidden}, T_F32, 1.f, ns});
-    tis.push_back({p + "attn_q.weight", {s.hidden, s.n_heads * hd}, s.t_attn, 0.f, ws});
-    tis.push_back({p + "attn_k.weight", {s.hidden, s.n_kv_heads * hd}, s.t_attn, 0.f, ws});
-    tis.push_back({p + "attn_v.weight", {s.hidden, s.n_kv_heads * hd}, s.t_attn, 0.f, ws});
-    tis.push_back({p + "attn_output.weight", {s.n_heads * hd, s.hidden}, s.t_attn, 0.f, ws});
-    tis.push_back({p + "ffn_norm.weight", {s.hidden}, T_F32, 1.f, ns});
-    tis.push_back({p + "ffn_gate.weight", {s.hidden, s.ffn}, s.t_ffn_gate_up, 0.f, ws});
-    tis.push_back({p + "ffn_up.weight", {s.hidden, s.ffn}, s.t_ffn_gate_up, 0.f, ws});
-    tis.push_back({p + "ffn_down.weight", {s.ffn, s.hidden}, s.t_ffn_down, 0.f, ws});
-  }
-  tis.push_back({"output_norm.weight", {s.hidden}, T_F32, 1.f, ns});
-  if (!s.tied_output) tis.push_back({"output.weight", {s.hidden, s.vocab}, s.t_output, 0.f, ws});
-
+// Header + tensor data for `tis` (offsets aligned to 32 like general.alignment).
+int write_gguf(const char* path, const std::vector<KV>& kvs, const std::vector<TI>& tis, uint64_t seed, int threads) {
   std::vector<uint8_t> head;
   head.insert(head.end(), {'G', 'G', 'U', 'F'});
   put<uint32_t>(head, 3);
@@ -396,6 +362,143 @@ int iek_synth_write_llama(const char* path, const iek_synth_spec* sp, uint64_t s
   }
   if (fclose(f) != 0) return 3;
   return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+// Model spec for the generator. Types are ggml ids (0 F32, 8 Q8_0, 12 Q4_K, 14 Q6_K).
+struct iek_synth_spec {
+  const char* name;         // general.name ("...mistral..." keeps Q/K un-permute off)
+  uint32_t n_layers, hidden, n_heads, n_kv_heads, ffn, vocab, context_length;
+  float rope_theta, rms_eps, weight_std, norm_std;
+  uint32_t t_attn, t_ffn_gate_up, t_ffn_down, t_embd, t_output;
+  uint32_t tied_output;     // 1: no output.weight (LM head reuses token_embd)
+};
+
+// Writes a Mistral/Llama-family GGUF. Returns 0 on success, nonzero on I/O failure.
+int iek_synth_write_llama(const char* path, const iek_synth_spec* sp, uint64_t seed, int threads) {
+  const iek_synth_spec& s = *sp;
+  uint32_t hd = s.hidden / s.n_heads;
+  std::vector<KV> kvs = {
+      kv_str("general.architecture", "llama"),
+      kv_str("general.name", s.name),
+      kv_u32("general.alignment", 32),
+      kv_u32("llama.context_length", s.context_length),
+      kv_u32("llama.embedding_length", s.hidden),
+      kv_u32("llama.block_count", s.n_layers),
+      kv_u32("llama.attention.head_count", s.n_heads),
+      kv_u32("llama.attention.head_count_kv", s.n_kv_heads),
+      kv_u32("llama.feed_forward_length", s.ffn),
+      kv_f32("llama.attention.layer_norm_rms_epsilon", s.rms_eps),
+      kv_u32("llama.vocab_size", s.vocab),
+      kv_f32("llama.rope.theta", s.rope_theta),
+      kv_u32("llama.rope.dimension_count", hd),
+  };
+  std::vector<TI> tis;
+  float ws = s.weight_std, ns = s.norm_std;
+  tis.push_back({"token_embd.weight", {s.hidden, s.vocab}, s.t_embd, 0.f, ws});
+  for (uint32_t l = 0; l < s.n_layers; ++l) {
+    std::string p = "blk." + std::to_string(l) + ".";
+    tis.push_back({p + "attn_norm.weight", {s.hidden}, T_F32, 1.f, ns});
+    tis.push_back({p + "attn_q.weight", {s.hidden, s.n_heads * hd}, s.t_attn, 0.f, ws});
+    tis.push_back({p + "attn_k.weight", {s.hidden, s.n_kv_heads * hd}, s.t_attn, 0.f, ws});
+    tis.push_back({p + "attn_v.weight", {s.hidden, s.n_kv_heads * hd}, s.t_attn, 0.f, ws});
+    tis.push_back({p + "attn_output.weight", {s.n_heads * hd, s.hidden}, s.t_attn, 0.f, ws});
+    tis.push_back({p + "ffn_norm.weight", {s.hidden}, T_F32, 1.f, ns});
+    tis.push_back({p + "ffn_gate.weight", {s.hidden, s.ffn}, s.t_ffn_gate_up, 0.f, ws});
+    tis.push_back({p + "ffn_up.weight", {s.hidden, s.ffn}, s.t_ffn_gate_up, 0.f, ws});
+    tis.push_back({p + "ffn_down.weight", {s.ffn, s.hidden}, s.t_ffn_down, 0.f, ws});
+  }
+  tis.push_back({"output_norm.weight", {s.hidden}, T_F32, 1.f, ns});
+  if (!s.tied_output) tis.push_back({"output.weight", {s.hidden, s.vocab}, s.t_output, 0.f, ws});
+  return write_gguf(path, kvs, tis, seed, threads);
+}
+
+// Gemma-4-architecture spec. Layer i is a sliding-window layer unless (i % global_every) ==
+// global_every - 1; sliding layers use head_dim_swa, global layers head_dim_global (per-layer
+// dims are read back from the Q/K weight shapes, model_config.rs:374-444). The last
+// shared_kv_layers layers borrow K/V from an earlier layer of the same kind (model_config.rs:332-372).
+struct iek_synth_gemma_spec {
+  const char* name;
+  uint32_t n_layers, hidden, n_heads, n_kv_heads, head_dim_swa, head_dim_global, ffn, vocab, context_length;
+  uint32_t ple_dim, sliding_window, global_every, shared_kv_layers, rot_swa, rot_global;
+  float theta_swa, theta_global, rms_eps, weight_std, norm_std, softcap;
+  uint32_t t_weights;       // projections (ggml type)
+  uint32_t t_embd;          // token_embd (also the tied LM head)
+  uint32_t t_ple_embd;      // per_layer_token_embd
+  uint32_t t_ple_proj;      // per_layer_model_proj (F32 or BF16)
+  uint32_t rope_freqs;      // 1: global layers carry rope_freqs (factors in [1, 2))
+  uint32_t q8_layer_scale;  // 1: odd layers store layer_output_scale as one Q8_0 block
+};
+
+int iek_synth_write_gemma4(const char* path, const iek_synth_gemma_spec* sp, uint64_t seed, int threads) {
+  const iek_synth_gemma_spec& s = *sp;
+  const uint32_t ge = s.global_every ? s.global_every : 1;
+  std::vector<bool> swa(s.n_layers);
+  for (uint32_t i = 0; i < s.n_layers; ++i) swa[i] = (i % ge) != ge - 1;
+  std::vector<KV> kvs = {
+      kv_str("general.architecture", "gemma4"),
+      kv_str("general.name", s.name),
+      kv_u32("general.alignment", 32),
+      kv_u32("gemma4.context_length", s.context_length),
+      kv_u32("gemma4.embedding_length", s.hidden),
+      kv_u32("gemma4.block_count", s.n_layers),
+      kv_u32("gemma4.attention.head_count", s.n_heads),
+      kv_u32("gemma4.attention.head_count_kv", s.n_kv_heads),
+      kv_u32("gemma4.feed_forward_length", s.ffn),
+      kv_f32("gemma4.attention.layer_norm_rms_epsilon", s.rms_eps),
+      kv_u32("gemma4.vocab_size", s.vocab),
+      kv_f32("gemma4.rope.freq_base", s.theta_global),
+      kv_f32("gemma4.rope.freq_base_swa", s.theta_swa),
+      kv_u32("gemma4.rope.dimension_count", s.rot_global),
+      kv_u32("gemma4.rope.dimension_count_swa", s.rot_swa),
+      kv_u32("gemma4.attention.sliding_window", s.sliding_window),
+      kv_bool_arr("gemma4.attention.sliding_window_pattern", swa),
+      kv_u32("gemma4.attention.shared_kv_layers", s.shared_kv_layers),
+      kv_u32("gemma4.embedding_length_per_layer_input", s.ple_dim),
+      kv_f32("gemma4.final_logit_softcapping", s.softcap),
+  };
+  std::vector<TI> tis;
+  const float ws = s.weight_std, ns = s.norm_std;
+  const uint32_t pack = s.n_layers * s.ple_dim;
+  tis.push_back({"token_embd.weight", {s.hidden, s.vocab}, s.t_embd, 0.f, ws});
+  if (s.ple_dim) {
+    tis.push_back({"per_layer_token_embd.weight", {pack, s.vocab}, s.t_ple_embd, 0.f, ws});
+    tis.push_back({"per_layer_model_proj.weight", {s.hidden, pack}, s.t_ple_proj, 0.f, ws});
+    tis.push_back({"per_layer_proj_norm.weight", {s.ple_dim}, T_F32, 1.f, ns});
+  }
+  for (uint32_t l = 0; l < s.n_layers; ++l) {
+    const std::string p = "blk." + std::to_string(l) + ".";
+    const uint32_t hd = swa[l] ? s.head_dim_swa : s.head_dim_global;
+    const uint32_t qd = s.n_heads * hd, kvd = s.n_kv_heads * hd;
+    tis.push_back({p + "attn_norm.weight", {s.hidden}, T_F32, 1.f, ns});
+    tis.push_back({p + "attn_q.weight", {s.hidden, qd}, s.t_weights, 0.f, ws});
+    tis.push_back({p + "attn_k.weight", {s.hidden, kvd}, s.t_weights, 0.f, ws});
+    tis.push_back({p + "attn_v.weight", {s.hidden, kvd}, s.t_weights, 0.f, ws});
+    tis.push_back({p + "attn_q_norm.weight", {hd}, T_F32, 1.f, ns});
+    tis.push_back({p + "attn_k_norm.weight", {hd}, T_F32, 1.f, ns});
+    tis.push_back({p + "attn_output.weight", {qd, s.hidden}, s.t_weights, 0.f, ws});
+    tis.push_back({p + "post_attention_norm.weight", {s.hidden}, T_F32, 1.f, ns});
+    tis.push_back({p + "ffn_norm.weight", {s.hidden}, T_F32, 1.f, ns});
+    tis.push_back({p + "ffn_gate.weight", {s.hidden, s.ffn}, s.t_weights, 0.f, ws});
+    tis.push_back({p + "ffn_up.weight", {s.hidden, s.ffn}, s.t_weights, 0.f, ws});
+    tis.push_back({p + "ffn_down.weight", {s.ffn, s.hidden}, s.t_weights, 0.f, ws});
+    tis.push_back({p + "post_ffw_norm.weight", {s.hidden}, T_F32, 1.f, ns});
+    if (s.ple_dim) {
+      tis.push_back({p + "inp_gate.weight", {s.hidden, s.ple_dim}, s.t_weights, 0.f, ws});
+      tis.push_back({p + "proj.weight", {s.ple_dim, s.hidden}, s.t_weights, 0.f, ws});
+      tis.push_back({p + "post_norm.weight", {s.hidden}, T_F32, 1.f, ns});
+    }
+    if (s.rope_freqs && !swa[l]) tis.push_back({p + "rope_freqs.weight", {s.rot_global / 2}, T_F32, 1.5f, 0.25f});
+    if (s.q8_layer_scale && (l & 1))
+      tis.push_back({p + "layer_output_scale.weight", {32}, T_Q8_0, 1.f, 0.05f});
+    else
+      tis.push_back({p + "layer_output_scale.weight", {1}, T_F32, 1.f, 0.05f});
+  }
+  tis.push_back({"output_norm.weight", {s.hidden}, T_F32, 1.f, ns});
+  return write_gguf(path, kvs, tis, seed, threads);
 }
 
 // Quantise `nblocks` blocks of float input (type 8/12/14) — used by tests to build weights.

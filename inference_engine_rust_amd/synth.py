@@ -7,6 +7,11 @@ Presets follow the configurations the benchmark is quoted on:
 * ``c0``  — tiny Mistral-architecture decoder (2 layers, d 512, 8/2 heads, FFN 1408).
 * ``c2``  — Mistral-7B-v0.1 architecture (32 layers, d 4096, 32/8 heads, FFN 14336).
 * ``c4``  — ``c2`` with an 8704-token context for long-context decode.
+* ``c3``  — Gemma-4-E2B-style decoder (35 layers, d 1536, 8/1 heads, head dim 256 on sliding
+  layers and 512 on global ones, FFN 6144, per-layer embeddings of 256, vocab 262144), Q8_0.
+* ``g0``  — a tiny Gemma-4-architecture model with every Gemma feature switched on (sliding
+  window smaller than the prompt, KV borrowing, partial rotary with freq factors, both
+  layer-scale encodings) for parity tests.
 
 Quant recipe ("Q4_K_M-style"): Q4_K for attention and FFN gate/up and the token embedding,
 Q6_K for FFN down and the output head, f32 norms. Weights are N(0, 0.02); norm weights are
@@ -23,7 +28,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 SYNTH_LIB = os.path.join(_HERE, "libiek_synth.so")
 
-GGML_F32, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 8, 12, 14
+GGML_F32, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K, GGML_BF16 = 0, 8, 12, 14, 30
 
 
 class _Spec(ctypes.Structure):
@@ -84,7 +89,67 @@ PRESETS = {
 }
 
 
-def preset(name: str, **overrides) -> LlamaSpec:
+class _GemmaSpec(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p)] + [
+        (f, ctypes.c_uint32) for f in (
+            "n_layers", "hidden", "n_heads", "n_kv_heads", "head_dim_swa", "head_dim_global", "ffn", "vocab",
+            "context_length", "ple_dim", "sliding_window", "global_every", "shared_kv_layers", "rot_swa",
+            "rot_global")
+    ] + [(f, ctypes.c_float) for f in ("theta_swa", "theta_global", "rms_eps", "weight_std", "norm_std", "softcap")] + [
+        (f, ctypes.c_uint32) for f in ("t_weights", "t_embd", "t_ple_embd", "t_ple_proj", "rope_freqs",
+                                       "q8_layer_scale")
+    ]
+
+
+@dataclass(frozen=True)
+class GemmaSpec:
+    """Gemma-4-architecture model. The reference does not pin Gemma-4-E2B's dimensions; these are
+    the builder's choice (recorded with the benchmark). Layer i is global when
+    i % global_every == global_every - 1, otherwise sliding-window."""
+    name: str
+    n_layers: int
+    hidden: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim_swa: int
+    head_dim_global: int
+    ffn: int
+    vocab: int
+    context_length: int
+    ple_dim: int
+    sliding_window: int
+    global_every: int
+    shared_kv_layers: int
+    rot_swa: int
+    rot_global: int
+    theta_swa: float = 10000.0
+    theta_global: float = 1000000.0
+    rms_eps: float = 1e-6
+    weight_std: float = 0.02
+    norm_std: float = 0.1
+    softcap: float = 30.0
+    t_weights: int = GGML_Q8_0
+    t_embd: int = GGML_Q8_0
+    t_ple_embd: int = GGML_Q8_0
+    t_ple_proj: int = GGML_BF16
+    rope_freqs: bool = True
+    q8_layer_scale: bool = True
+
+    def is_swa(self, layer: int) -> bool:
+        return layer % self.global_every != self.global_every - 1
+
+    def head_dim(self, layer: int) -> int:
+        return self.head_dim_swa if self.is_swa(layer) else self.head_dim_global
+
+
+PRESETS.update({
+    "c3": GemmaSpec("synthetic-gemma-4-e2b", 35, 1536, 8, 1, 256, 512, 6144, 262144, 512, 256, 512, 5, 20,
+                    256, 128, rope_freqs=False, q8_layer_scale=False),
+    "g0": GemmaSpec("synthetic-gemma-4-tiny", 6, 256, 4, 1, 64, 128, 512, 8192, 96, 32, 16, 3, 2, 64, 32),
+})
+
+
+def preset(name: str, **overrides):
     return replace(PRESETS[name], **overrides)
 
 
@@ -99,6 +164,9 @@ def lib() -> ctypes.CDLL:
         L = ctypes.CDLL(SYNTH_LIB)
         L.iek_synth_write_llama.argtypes = [ctypes.c_char_p, ctypes.POINTER(_Spec), ctypes.c_uint64, ctypes.c_int]
         L.iek_synth_write_llama.restype = ctypes.c_int
+        L.iek_synth_write_gemma4.argtypes = [ctypes.c_char_p, ctypes.POINTER(_GemmaSpec), ctypes.c_uint64,
+                                             ctypes.c_int]
+        L.iek_synth_write_gemma4.restype = ctypes.c_int
         L.iek_synth_quantize.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         L.iek_synth_quantize.restype = ctypes.c_int
         L.iek_synth_normal.argtypes = [ctypes.c_uint64, ctypes.c_char_p, ctypes.c_size_t, ctypes.c_size_t,
@@ -122,6 +190,26 @@ def write_llama(path: str, spec: LlamaSpec, seed: int = 0, threads: int | None =
     if rc != 0:
         raise OSError(f"iek_synth_write_llama({path}) failed with code {rc}")
     return path
+
+
+def write_gemma4(path: str, spec: GemmaSpec, seed: int = 0, threads: int | None = None) -> str:
+    """Write a Gemma-4-architecture GGUF for ``spec`` to ``path`` and return the path."""
+    vals = [spec.name.encode()] + [getattr(spec, f) for f, _ in _GemmaSpec._fields_[1:]]
+    vals = [int(v) if isinstance(v, bool) else v for v in vals]
+    s = _GemmaSpec(*vals)
+    if threads is None:
+        threads = min(16, os.cpu_count() or 1)
+    rc = lib().iek_synth_write_gemma4(path.encode(), ctypes.byref(s), seed, threads)
+    if rc != 0:
+        raise OSError(f"iek_synth_write_gemma4({path}) failed with code {rc}")
+    return path
+
+
+def write_model(path: str, spec, seed: int = 0, threads: int | None = None) -> str:
+    """Write ``spec`` (a LlamaSpec or GemmaSpec) as GGUF."""
+    if isinstance(spec, GemmaSpec):
+        return write_gemma4(path, spec, seed, threads)
+    return write_llama(path, spec, seed, threads)
 
 
 def normal(seed: int, name: str, n: int, mean: float = 0.0, std: float = 1.0, start: int = 0) -> np.ndarray:
