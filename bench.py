@@ -22,18 +22,66 @@ METRIC = "decode tok/s + 512-tok prefill TTFT ms, Mistral-7B Q4_K_M, 1×MI355X, 
 HBM_PEAK_GBS = 8000.0
 
 
-def weight_bytes_per_token(model, cfg):
-    """Native block bytes streamed per decode token: every layer weight, output norm, LM head and
-    one embedding row (the algorithmic denominator of the decode roofline)."""
+def weight_bytes_per_token(model, cfg, specs):
+    """Bytes of weights streamed per decode token, as resident in HBM (native GGUF blocks; BF16
+    widened to F32 at load as the reference does): every layer weight the step reads, the output
+    norm and LM head, and one row of each embedding table (the algorithmic denominator of the
+    decode roofline). Layers that borrow another layer's KV read no K/V projection."""
+    gemma = int(cfg.family) == 1
     total = 0
     for li in range(cfg.n_layers):
-        for t in ["attn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "ffn_norm", "ffn_gate", "ffn_up",
-                  "ffn_down"]:
+        names = ["attn_norm", "attn_q", "attn_output", "ffn_norm", "ffn_gate", "ffn_up", "ffn_down"]
+        if specs[li]["kv_borrow"] < 0:
+            names += ["attn_k", "attn_v"]
+        if gemma:
+            names += ["attn_q_norm", "attn_k_norm", "post_attention_norm", "post_ffw_norm", "layer_output_scale"]
+            if cfg.embedding_length_per_layer:
+                names += ["inp_gate", "proj", "post_norm"]
+        for t in names:
             total += model.tensor(f"blk.{li}.{t}.weight")["bytes"]
-    total += model.tensor("output_norm.weight")["bytes"] + model.tensor("output.weight")["bytes"]
+    total += model.tensor("output_norm.weight")["bytes"]
     emb = model.tensor("token_embd.weight")
-    total += emb["bytes"] // emb["ne1"]
+    head = "token_embd.weight" if gemma else "output.weight"  # the synthetic Gemma models tie the head
+    total += model.tensor(head)["bytes"] + emb["bytes"] // emb["ne1"]
+    if gemma and cfg.embedding_length_per_layer:
+        pe = model.tensor("per_layer_token_embd.weight")
+        total += pe["bytes"] // pe["ne1"] + model.tensor("per_layer_model_proj.weight")["bytes"]
+        total += model.tensor("per_layer_proj_norm.weight")["bytes"]
     return total
+
+
+def kv_bytes_per_token(cfg, specs, ctx_len):
+    """KV bytes one decode step reads (keys/values visible to each layer at context length
+    ctx_len, borrowed caches included) and writes (one row per layer that owns a cache)."""
+    esz = 4 if int(cfg.family) == 1 else 2  # Gemma-4 sessions keep an f32 cache
+    rd = wr = 0
+    for sp in specs:
+        row = 2 * cfg.n_kv_heads * sp["head_dim"] * esz
+        keys = ctx_len if sp["sliding_window"] <= 0 else min(ctx_len, sp["sliding_window"])
+        rd += row * keys
+        if sp["kv_borrow"] < 0:
+            wr += row
+    return rd + wr
+
+
+def prefill_flops(cfg, specs, prompt):
+    """2 * params * tokens for every projection the prompt runs, plus causal (windowed) attention
+    4 * head_dim * visible keys per head, plus the last row's LM head."""
+    H = cfg.hidden_dim
+    lin = 0
+    attn = 0.0
+    for sp in specs:
+        qd = cfg.n_heads * sp["head_dim"]
+        kvd = cfg.n_kv_heads * sp["head_dim"]
+        lin += H * qd * 2 + (H * kvd * 2 if sp["kv_borrow"] < 0 else 0) + 3 * H * sp["ffn_dim"]
+        lin += 2 * H * int(cfg.embedding_length_per_layer)
+        w = sp["sliding_window"]
+        vis = sum(min(p + 1, w) if w > 0 else p + 1 for p in range(prompt))
+        attn += 4.0 * sp["head_dim"] * vis * cfg.n_heads
+    lin_flops = 2.0 * lin * prompt
+    if int(cfg.embedding_length_per_layer):
+        lin_flops += 2.0 * H * cfg.n_layers * cfg.embedding_length_per_layer * prompt
+    return lin_flops + attn + 2.0 * H * cfg.vocab_size
 
 
 def kernel_roofline(E, model, cfg, reps):
@@ -126,7 +174,7 @@ def main():
         path = os.path.join(d, f"iek_{args.config}_seed0.gguf")
         if not os.path.exists(path):
             t0 = time.perf_counter()
-            synth.write_llama(path, spec, seed=0)
+            synth.write_model(path, spec, seed=0)
             print(f"[bench] wrote {path} in {time.perf_counter() - t0:.1f}s", file=sys.stderr, flush=True)
     t0 = time.perf_counter()
     model = E.LoadedModel.load(path, device=0)
@@ -165,15 +213,20 @@ def main():
     print(f"[bench] decode {args.steps} tokens in {elapsed * 1e3:.1f} ms ({tok_s:.1f} tok/s)", file=sys.stderr,
           flush=True)
 
-    wbytes = weight_bytes_per_token(model, cfg)
-    kv_per_key = 2 * cfg.n_layers * cfg.n_kv_heads * cfg.head_dim * 2  # fp16 K + V
-    avg_keys = args.prompt + args.warmup + (args.steps + 1) / 2.0
-    step_bytes = wbytes + kv_per_key * (avg_keys + 1)
+    specs = [model.layer_spec(li) for li in range(cfg.n_layers)]
+    gemma = int(cfg.family) == 1
+    wbytes = weight_bytes_per_token(model, cfg, specs)
+    # the timed steps see context lengths prompt + warmup + 1 ... prompt + warmup + steps
+    c0 = args.prompt + args.warmup
+    kv_avg = sum(kv_bytes_per_token(cfg, specs, c0 + i + 1) for i in range(args.steps)) / args.steps
+    step_bytes = wbytes + kv_avg
     step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    roof = kernel_roofline(E, model, cfg, args.kernel_reps)
-    print(f"[bench] dominant kernel {roof['achieved']} GB/s ({roof['avg_launch_us']} us/launch)", file=sys.stderr,
-          flush=True)
+    roof = None
+    if not gemma:
+        roof = kernel_roofline(E, model, cfg, args.kernel_reps)
+        print(f"[bench] dominant kernel {roof['achieved']} GB/s ({roof['avg_launch_us']} us/launch)",
+              file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -182,20 +235,27 @@ def main():
         cpu = cpu_baseline(path, args.cpu_layers)
         print(f"[bench] cpu baseline {cpu['value']} tok/s", file=sys.stderr, flush=True)
 
-    lin_params = cfg.n_layers * (cfg.hidden_dim * (cfg.n_heads * cfg.head_dim) * 2 +
-                                 cfg.hidden_dim * (cfg.n_kv_heads * cfg.head_dim) * 2 +
-                                 3 * cfg.hidden_dim * cfg.ffn_dim)
-    attn_flops = 4 * cfg.head_dim * (args.prompt * (args.prompt + 1) / 2) * cfg.n_heads * cfg.n_layers
-    flops_prefill = 2.0 * lin_params * args.prompt + attn_flops + 2.0 * cfg.hidden_dim * cfg.vocab_size
+    flops_prefill = prefill_flops(cfg, specs, args.prompt)
+    if gemma:
+        arch = (f"Gemma-4-E2B-style architecture ({cfg.n_layers} layers, d {cfg.hidden_dim}, "
+                f"{cfg.n_heads}/{cfg.n_kv_heads} heads, head dim {specs[0]['head_dim']} sliding / "
+                f"{max(sp['head_dim'] for sp in specs)} global, FFN {cfg.ffn_dim}, per-layer embeddings "
+                f"{cfg.embedding_length_per_layer}, vocab {cfg.vocab_size}), Q8_0 GGUF")
+        data = "synthetic (seeded random-init N(0,0.02) weights quantised Q8_0, uniform random prompt ids)"
+        kv = "f32 KV cache"
+    else:
+        arch = (f"Mistral-7B-v0.1 architecture ({cfg.n_layers} layers, d {cfg.hidden_dim}, "
+                f"{cfg.n_heads}/{cfg.n_kv_heads} heads, FFN {cfg.ffn_dim}, vocab {cfg.vocab_size}), "
+                f"Q4_K_M-style GGUF")
+        data = "synthetic (seeded random-init N(0,0.02) weights quantised Q4_K/Q6_K, uniform random prompt ids)"
+        kv = "fp16 KV cache"
     out = {
         "metric": METRIC, "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32",
-        "data": "synthetic (seeded random-init N(0,0.02) weights quantised Q4_K/Q6_K, uniform random prompt ids)",
-        "config": {"workload": f"{args.config}: Mistral-7B-v0.1 architecture ({cfg.n_layers} layers, d "
-                               f"{cfg.hidden_dim}, {cfg.n_heads}/{cfg.n_kv_heads} heads, FFN {cfg.ffn_dim}, vocab "
-                               f"{cfg.vocab_size}), Q4_K_M-style GGUF, {args.prompt}-token prompt prefill then "
-                               f"greedy decode at batch 1, fp16 KV cache",
+        "data": data,
+        "config": {"workload": f"{args.config}: {arch}, {args.prompt}-token prompt prefill then greedy decode "
+                               f"at batch 1, {kv}",
                    "prompt_tokens": args.prompt, "decode_tokens": args.steps, "seed": 0},
         "ttft_ms": round(ttft_ms, 3),
         "prefill_tok_s": round(args.prompt / (ttft_ms * 1e-3), 1),
