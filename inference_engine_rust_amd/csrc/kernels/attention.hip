@@ -238,15 +238,22 @@ __global__ __launch_bounds__(256) void attn_decode_f32_kernel(const float* __res
   const float* kb = kc + ((size_t)kvh * ctx + j0) * HD;
   const float* vb = vc + ((size_t)kvh * ctx + j0) * HD;
   {
+    // the key row's slice in 8-float4 batches, all loads of a batch in flight together
     const float* krow = kb + (size_t)min(lane, nk - 1) * HD + wave * DQ;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int d = 0; d < DQ; d += 4) {
-      const float4 k4 = *reinterpret_cast<const float4*>(krow + d);
+    constexpr int NB = DQ >= 32 ? 8 : DQ / 4;  // float4 per batch
+    for (int d0 = 0; d0 < DQ; d0 += 4 * NB) {
+      float4 k4[NB];
 #pragma unroll
-      for (int g = 0; g < 8; ++g) {
-        if (g < G) {
-          const float4 q4 = *reinterpret_cast<const float4*>(&qs[g][wave * DQ + d]);
-          acc[g] += q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
+      for (int u = 0; u < NB; ++u) k4[u] = *reinterpret_cast<const float4*>(krow + d0 + 4 * u);
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+          if (g < G) {
+            const float4 q4 = *reinterpret_cast<const float4*>(&qs[g][wave * DQ + d0 + 4 * u]);
+            acc[g] += q4.x * k4[u].x + q4.y * k4[u].y + q4.z * k4[u].z + q4.w * k4[u].w;
+          }
         }
       }
     }
@@ -269,11 +276,35 @@ __global__ __launch_bounds__(256) void attn_decode_f32_kernel(const float* __res
     float o[DPL];
 #pragma unroll
     for (int t = 0; t < DPL; ++t) o[t] = 0.f;
-    for (int j = 0; j < nk; ++j) {
-      const float pj = ps[g][j];
-      const float* vr = vb + (size_t)j * HD + DPL * lane;
+    // 8 V rows in flight per batch; rows past the live slice have p = 0 and a clamped address
+    for (int j0 = 0; j0 < SPLIT; j0 += 8) {
+      float vr[8][DPL];
 #pragma unroll
-      for (int t = 0; t < DPL; ++t) o[t] += pj * vr[t];
+      for (int u = 0; u < 8; ++u) {
+        const float* src = vb + (size_t)min(j0 + u, nk - 1) * HD + DPL * lane;
+        if constexpr (DPL == 1) {
+          vr[u][0] = src[0];
+        } else if constexpr (DPL == 2) {
+          const float2 t2 = *reinterpret_cast<const float2*>(src);
+          vr[u][0] = t2.x;
+          vr[u][1] = t2.y;
+        } else {
+#pragma unroll
+          for (int t = 0; t < DPL; t += 4) {
+            const float4 t4 = *reinterpret_cast<const float4*>(src + t);
+            vr[u][t] = t4.x;
+            vr[u][t + 1] = t4.y;
+            vr[u][t + 2] = t4.z;
+            vr[u][t + 3] = t4.w;
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float pj = ps[g][j0 + u];
+#pragma unroll
+        for (int t = 0; t < DPL; ++t) o[t] += pj * vr[u][t];
+      }
     }
     float* pr = part + ((size_t)(kvh * G + g) * nsplit + sp) * (HD + 2);
     if (lane == 0) {
