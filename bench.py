@@ -84,6 +84,41 @@ def prefill_flops(cfg, specs, prompt):
     return lin_flops + attn + 2.0 * H * cfg.vocab_size
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "c2_matvec_traffic.json")
+
+
+def measured_traffic(algo_bytes):
+    """HBM bytes per launch of the roofline kernel from the committed rocprofv3 --pmc counts
+    (FETCH_SIZE and WRITE_SIZE, one run each, of `bench.py --probe traffic`), each scaled by
+    what the same counter reads for a plain copy kernel of known size in that run."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("algorithmic_bytes") != algo_bytes:
+        return None
+    return int(round(t["fetch_bytes"] + t["write_bytes"]))
+
+
+def probe_traffic(E, model, cfg, reps):
+    """Launches only what the --pmc runs count: one plain copy of COPY_BYTES (torch's copy
+    kernel), then `reps` roofline-kernel launches rotating over the gate/up tensors."""
+    import torch
+
+    n = COPY_BYTES // 4
+    a = torch.ones(n, device="cuda", dtype=torch.float32)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    kernel_roofline(E, model, cfg, reps)
+    torch.cuda.synchronize()
+
+
+COPY_BYTES = 256 << 20
+
+
 def kernel_roofline(E, model, cfg, reps):
     """Average duration of the decode matvec on the FFN gate/up weights (Q4_K, 14336x4096, the
     largest weight class), launched on torch's current stream between HIP events and rotating over
@@ -111,7 +146,8 @@ def kernel_roofline(E, model, cfg, reps):
     algo = ts[0]["bytes"] + 4 * (K + N)
     gbs = algo / (avg_ms * 1e-3) / 1e9
     return {"kernel": "mv_stream<Q4I8Tr,2,false> (decode matvec, Q4_K 14336x4096)", "bound": "hbm", "achieved": round(gbs, 1),
-            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic(algo),
             "algorithmic_bytes_per_launch": algo, "avg_launch_us": round(avg_ms * 1e3, 3), "launches": reps}
 
 
@@ -154,6 +190,8 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=256)
     ap.add_argument("--cpu-layers", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--probe", choices=["traffic"], default=None,
+                    help="traffic: run only a plain copy and the roofline kernel (for rocprofv3 --pmc)")
     ap.add_argument("--model", default=None, help="existing GGUF (default: generate the synthetic config)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -180,6 +218,11 @@ def main():
     model = E.LoadedModel.load(path, device=0)
     print(f"[bench] model load + HBM upload {time.perf_counter() - t0:.1f}s", file=sys.stderr, flush=True)
     cfg = model.config
+    if args.probe == "traffic":
+        probe_traffic(E, model, cfg, args.kernel_reps)
+        print(f"[bench] traffic probe done: 1 copy of {COPY_BYTES} B, {args.kernel_reps} roofline-kernel launches",
+              file=sys.stderr, flush=True)
+        return
     if args.prompt + args.warmup + args.steps > cfg.context_length:
         sys.exit(f"prompt + warmup + steps exceeds context_length {cfg.context_length}")
     prompt = synth.prompt_ids(0, args.prompt, int(cfg.vocab_size))
