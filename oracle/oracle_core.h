@@ -22,8 +22,12 @@
 //   attention + layer     layer 0 of the tiny model recomposed from the pinned ops around a
 //                         brute-force float64 causal GQA attention; prefill N+1 == prefill N +
 //                         decode; greedy loop == teacher-forced re-prefill
-// Parity unpinned: the Gemma-4 specific parts (per-layer embeddings, layer output scale, q/k/v
-// head norms, KV borrowing, GeGLU FFN wiring) have no known answer or closed-form check yet.
+//   Gemma-4 parts         (tests/test_oracle_gemma.py) the whole tiny Gemma-4 model recomposed from
+//                         the pinned ops around a brute-force float64 windowed attention (per-layer
+//                         embeddings, q/k head norms, v norm, post-norms, GeGLU, KV borrowing,
+//                         layer output scale in both encodings, tied head, soft cap); prefill N+1
+//                         == prefill N + decode past the window; greedy == teacher forcing; config
+//                         resolution of the Gemma-4 metadata; exact BF16 widening
 #pragma once
 #include <cstddef>
 #include <cstdint>
