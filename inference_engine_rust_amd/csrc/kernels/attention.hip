@@ -8,93 +8,9 @@
 // reference attends to the layer's own k_data/v_data, not the cache).
 #include <type_traits>
 
-#include "common.cuh"
-#include "../iek_internal.h"
+#include "attn_core.cuh"
 
 namespace iek {
-
-constexpr int SPLIT = 64;
-
-// One 256-thread workgroup per (KV head, 64-key slice): the four waves load the slice's K and V
-// rows (fp16) into LDS together in one burst of clamped, unconditional 16-byte loads, then wave w
-// takes query heads w and w+4 of the GQA group. Lane j scores key j against its head (K row from
-// LDS, q broadcast from LDS), the wave forms the slice softmax, and for P.V lane l owns head dims
-// [DPL*l, DPL*l + DPL). Slices publish (max, sum, o[]) partials; the last workgroup of each KV
-// head to finish merges its query heads (counted with an agent-scope acq_rel atomic per KV head).
-// Merge of the live slice partials of query head h by one wave: global (max, sum) over slices,
-// then each lane folds its head dims of every slice with the rescaled weights.
-template <int HD>
-IEK_DEV void merge_head(const float* __restrict__ part, float* __restrict__ out, int h, int nsplit, int s0, int nlive,
-                        float* wsl) {
-  constexpr int DPL = HD / 64;
-  const int lane = threadIdx.x & 63;
-  const float* pr = part + (size_t)h * nsplit * (HD + 2);
-  float M = -INFINITY;
-  for (int s = s0 + lane; s < nlive; s += 64) M = fmaxf(M, pr[(size_t)s * (HD + 2)]);
-  M = wave_max(M);
-  float L = 0.f;
-  for (int s = s0 + lane; s < nlive; s += 64) {
-    const float w = expf(pr[(size_t)s * (HD + 2)] - M);
-    L += pr[(size_t)s * (HD + 2) + 1] * w;
-    if (s - s0 < 256) wsl[s - s0] = w;
-  }
-  L = wave_sum(L);
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  float acc[DPL];
-#pragma unroll
-  for (int t = 0; t < DPL; ++t) acc[t] = 0.f;
-  const int ns = min(nlive - s0, 256);
-  for (int s8 = 0; s8 < ns; s8 += 8) {
-    // clamped, unconditional loads: all eight slices' rows are in flight together
-    float v[8][DPL];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const size_t row = (size_t)(s0 + min(s8 + u, ns - 1)) * (HD + 2) + 2 + DPL * lane;
-#pragma unroll
-      for (int t = 0; t < DPL; ++t) v[u][t] = pr[row + t];
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      if (s8 + u < ns) {
-        const float w = wsl[s8 + u];
-#pragma unroll
-        for (int t = 0; t < DPL; ++t) acc[t] += v[u][t] * w;
-      }
-    }
-  }
-  // slices beyond the 256 staged weights (contexts over 16K keys) use direct weights
-  for (int s = s0 + 256; s < nlive; ++s) {
-    const float w = expf(pr[(size_t)s * (HD + 2)] - M);
-#pragma unroll
-    for (int t = 0; t < DPL; ++t) acc[t] += pr[(size_t)s * (HD + 2) + 2 + DPL * lane + t] * w;
-  }
-#pragma unroll
-  for (int t = 0; t < DPL; ++t) out[(size_t)h * HD + DPL * lane + t] = acc[t] / L;
-}
-
-// The last workgroup of a KV head to finish merges the group's heads. Release: the workgroup
-// barrier orders every wave's partial stores before thread 0's agent-scope acq_rel add (which
-// writes back this XCD's L2); the last arrival's acquire side invalidates its L2 before the
-// partials are read. The counter is reset for the next launch.
-template <int HD>
-IEK_DEV void merge_if_last(const float* __restrict__ part, float* __restrict__ out, int* __restrict__ counters,
-                           int kvh, int G, int nsplit, int jmin, int total, int wave) {
-  __shared__ int last;
-  __shared__ float wsl[4][256];
-  __syncthreads();
-  const int s0 = jmin / SPLIT, nlive = (total + SPLIT - 1) / SPLIT;
-  if (threadIdx.x == 0) {
-    const int old = __hip_atomic_fetch_add(&counters[kvh], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    last = old == nlive - s0 - 1;
-    if (last) __hip_atomic_store(&counters[kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  for (int g = wave; g < G; g += 4) merge_head<HD>(part, out, kvh * G + g, nsplit, s0, nlive, wsl[wave]);
-}
 
 template <int HD>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, const __half* __restrict__ kc,
@@ -102,110 +18,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
                                                           float* __restrict__ out, int* __restrict__ counters,
                                                           int n_heads, int n_kv, int ctx, const int* pos_dev,
                                                           int window, float scale, int nsplit) {
-  constexpr int DPL = HD / 64;        // head dims per lane in the PV phase
-  constexpr int KROW = HD + 8;        // padded K row (halves): 16-byte reads of different rows spread banks
-  constexpr int U4 = SPLIT * HD / 8;  // uint4 per K (or V) slice
-  // V is staged in LDS up to head_dim 256; at 512 the K slice, q and V would not fit together, so
-  // the P.V phase reads V rows straight from memory (each row one coalesced 1 KB wave load).
-  constexpr bool VL = HD <= 256;
-  static_assert(HD == 64 || HD == 128 || HD == 256 || HD == 512, "head_dim");
-  const int kvh = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int G = n_heads / n_kv;
-  const int total = *pos_dev + 1;
-  const int jmin = (window > 0 && total > window) ? total - window : 0;
-  const int j0 = max(sp * SPLIT, jmin), j1 = min(total, (sp + 1) * SPLIT);
-  const int nk = j1 - j0;
-  if (nk <= 0) return;  // uniform across the workgroup
-  __shared__ __align__(16) __half ks[SPLIT][KROW];
-  __shared__ __align__(16) __half vs[VL ? SPLIT : 1][VL ? HD : 8];
-  __shared__ __align__(16) float qs[8][HD];
-  __shared__ float ps[4][SPLIT];
-  const __half* vb = vc + ((size_t)kvh * ctx + j0) * HD;
-  {
-    const __half* kb = kc + ((size_t)kvh * ctx + j0) * HD;
-    uint4 kr[U4 / 256], vr[VL ? U4 / 256 : 1];
-#pragma unroll
-    for (int u = 0; u < U4 / 256; ++u) {
-      const int i = tid + 256 * u, row = min(i / (HD / 8), nk - 1), c8 = i % (HD / 8);
-      kr[u] = *reinterpret_cast<const uint4*>(kb + (size_t)row * HD + 8 * c8);
-      if constexpr (VL) vr[u] = *reinterpret_cast<const uint4*>(vb + (size_t)row * HD + 8 * c8);
-    }
-    for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = q[(size_t)(kvh * G) * HD + i];
-#pragma unroll
-    for (int u = 0; u < U4 / 256; ++u) {
-      const int i = tid + 256 * u, row = i / (HD / 8), c8 = i % (HD / 8);
-      *reinterpret_cast<uint4*>(&ks[row][8 * c8]) = kr[u];
-      if constexpr (VL) *reinterpret_cast<uint4*>(&vs[row][8 * c8]) = vr[u];
-    }
-  }
-  __syncthreads();
-  const bool valid = lane < nk;
-  for (int g = wave; g < G; g += 4) {
-    // scores: lane = key
-    float sc = 0.f;
-#pragma unroll
-    for (int c = 0; c < HD / 8; ++c) {
-      const uint4 kraw = *reinterpret_cast<const uint4*>(&ks[lane][8 * c]);
-      const __half2* h2 = reinterpret_cast<const __half2*>(&kraw);
-      const float4 qa = *reinterpret_cast<const float4*>(&qs[g][8 * c]);
-      const float4 qb = *reinterpret_cast<const float4*>(&qs[g][8 * c + 4]);
-      const float2 k0 = __half22float2(h2[0]), k1 = __half22float2(h2[1]), k2 = __half22float2(h2[2]),
-                   k3 = __half22float2(h2[3]);
-      sc += qa.x * k0.x + qa.y * k0.y + qa.z * k1.x + qa.w * k1.y + qb.x * k2.x + qb.y * k2.y + qb.z * k3.x +
-            qb.w * k3.y;
-    }
-    const float s = valid ? sc * scale : -INFINITY;
-    const float m = wave_max(s);
-    const float p = valid ? expf(s - m) : 0.f;
-    const float l = wave_sum(p);
-    ps[wave][lane] = p;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // P.V: lane owns dims DPL*lane .. +DPL-1; keys past the live slice carry p = 0
-    float o[DPL];
-#pragma unroll
-    for (int t = 0; t < DPL; ++t) o[t] = 0.f;
-#pragma unroll 8
-    for (int j = 0; j < SPLIT; ++j) {
-      const float pj = ps[wave][j];
-      if constexpr (DPL == 1) {
-        o[0] += pj * __half2float(vs[j][lane]);
-      } else if constexpr (DPL == 2) {
-        const float2 v2 = __half22float2(*reinterpret_cast<const __half2*>(&vs[j][2 * lane]));
-        o[0] += pj * v2.x;
-        o[1] += pj * v2.y;
-      } else if constexpr (DPL == 4) {
-        const uint2 raw = *reinterpret_cast<const uint2*>(&vs[j][4 * lane]);
-        const __half2* h2 = reinterpret_cast<const __half2*>(&raw);
-        const float2 a0 = __half22float2(h2[0]), a1 = __half22float2(h2[1]);
-        o[0] += pj * a0.x;
-        o[1] += pj * a0.y;
-        o[2] += pj * a1.x;
-        o[3] += pj * a1.y;
-      } else {
-        // rows past the live slice have p = 0; their address is clamped into the slice
-        const uint4 raw = *reinterpret_cast<const uint4*>(vb + (size_t)min(j, nk - 1) * HD + 8 * lane);
-        const __half2* h2 = reinterpret_cast<const __half2*>(&raw);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const float2 a = __half22float2(h2[t]);
-          o[2 * t] += pj * a.x;
-          o[2 * t + 1] += pj * a.y;
-        }
-      }
-    }
-    float* pr = part + ((size_t)(kvh * G + g) * nsplit + sp) * (HD + 2);
-    if (lane == 0) {
-      pr[0] = m;
-      pr[1] = l;
-    }
-#pragma unroll
-    for (int t = 0; t < DPL; ++t) pr[2 + DPL * lane + t] = o[t];
-    __builtin_amdgcn_wave_barrier();  // ps[wave] is rewritten by the next head of this wave
-  }
-  merge_if_last<HD>(part, out, counters, kvh, G, nsplit, jmin, total, wave);
+  __shared__ __align__(16) char smem[AttnSmem<HD>::BYTES];
+  attn_slice_f16<HD>(q, kc, vc, part, out, counters, n_heads, n_kv, ctx, *pos_dev + 1, window, scale, nsplit,
+                     blockIdx.x, blockIdx.y, smem);
 }
 
 // f32 KV cache variant (Gemma-4 sessions keep the reference's f32 cache: with q/k head norms
@@ -238,22 +53,16 @@ __global__ __launch_bounds__(256) void attn_decode_f32_kernel(const float* __res
   const float* kb = kc + ((size_t)kvh * ctx + j0) * HD;
   const float* vb = vc + ((size_t)kvh * ctx + j0) * HD;
   {
-    // the key row's slice in 8-float4 batches, all loads of a batch in flight together
     const float* krow = kb + (size_t)min(lane, nk - 1) * HD + wave * DQ;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    constexpr int NB = DQ >= 32 ? 8 : DQ / 4;  // float4 per batch
-    for (int d0 = 0; d0 < DQ; d0 += 4 * NB) {
-      float4 k4[NB];
+#pragma unroll 2
+    for (int d = 0; d < DQ; d += 4) {
+      const float4 k4 = *reinterpret_cast<const float4*>(krow + d);
 #pragma unroll
-      for (int u = 0; u < NB; ++u) k4[u] = *reinterpret_cast<const float4*>(krow + d0 + 4 * u);
-#pragma unroll
-      for (int u = 0; u < NB; ++u) {
-#pragma unroll
-        for (int g = 0; g < 8; ++g) {
-          if (g < G) {
-            const float4 q4 = *reinterpret_cast<const float4*>(&qs[g][wave * DQ + d0 + 4 * u]);
-            acc[g] += q4.x * k4[u].x + q4.y * k4[u].y + q4.z * k4[u].z + q4.w * k4[u].w;
-          }
+      for (int g = 0; g < 8; ++g) {
+        if (g < G) {
+          const float4 q4 = *reinterpret_cast<const float4*>(&qs[g][wave * DQ + d]);
+          acc[g] += q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
         }
       }
     }
@@ -277,10 +86,12 @@ __global__ __launch_bounds__(256) void attn_decode_f32_kernel(const float* __res
 #pragma unroll
     for (int t = 0; t < DPL; ++t) o[t] = 0.f;
     // 8 V rows in flight per batch; rows past the live slice have p = 0 and a clamped address
-    for (int j0 = 0; j0 < SPLIT; j0 += 8) {
-      float vr[8][DPL];
+    constexpr int NV = DPL >= 8 ? 4 : 8;  // V rows per batch
+#pragma unroll 1
+    for (int j0 = 0; j0 < SPLIT; j0 += NV) {
+      float vr[NV][DPL];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < NV; ++u) {
         const float* src = vb + (size_t)min(j0 + u, nk - 1) * HD + DPL * lane;
         if constexpr (DPL == 1) {
           vr[u][0] = src[0];
@@ -300,7 +111,7 @@ __global__ __launch_bounds__(256) void attn_decode_f32_kernel(const float* __res
         }
       }
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < NV; ++u) {
         const float pj = ps[g][j0 + u];
 #pragma unroll
         for (int t = 0; t < DPL; ++t) o[t] += pj * vr[u][t];
@@ -314,7 +125,9 @@ __global__ __launch_bounds__(256) void attn_decode_f32_kernel(const float* __res
 #pragma unroll
     for (int t = 0; t < DPL; ++t) pr[2 + DPL * lane + t] = o[t];
   }
-  merge_if_last<HD>(part, out, counters, kvh, G, nsplit, jmin, total, wave);
+  __shared__ int last;
+  __shared__ float wsl[4 * 256];
+  merge_if_last<HD>(part, out, counters, kvh, G, nsplit, jmin, total, wave, &last, wsl);
 }
 
 template <int HD>

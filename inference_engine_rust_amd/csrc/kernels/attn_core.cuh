@@ -1,0 +1,239 @@
+// Decode attention device code over a per-layer KV cache [n_kv][ctx][head_dim], shared by the
+// per-launch kernels (attention.hip) and the persistent decode step (decode_step.hip).
+// src/layers/attention.rs:462-655 (decode_attention_layer): split-K flash-decode over 64-key
+// slices, GQA groups sharing one K/V stream, (max, sum, o[]) partials merged per query head.
+#pragma once
+#include "common.cuh"
+#include "../iek_internal.h"
+
+namespace iek {
+
+constexpr int SPLIT = 64;
+
+// One 256-thread workgroup per (KV head, 64-key slice): the four waves load the slice's K and V
+// rows (fp16) into LDS together in one burst of clamped, unconditional 16-byte loads, then wave w
+// takes query heads w and w+4 of the GQA group. Lane j scores key j against its head (K row from
+// LDS, q broadcast from LDS), the wave forms the slice softmax, and for P.V lane l owns head dims
+// [DPL*l, DPL*l + DPL). Slices publish (max, sum, o[]) partials; the last workgroup of each KV
+// head to finish merges its query heads (counted with an agent-scope acq_rel atomic per KV head).
+// Merge of the live slice partials of query head h by one wave: global (max, sum) over slices,
+// then each lane folds its head dims of every slice with the rescaled weights.
+template <int HD, bool COH = false>
+IEK_DEV void merge_head(const float* __restrict__ part, float* __restrict__ out, int h, int nsplit, int s0, int nlive,
+                        float* wsl) {
+  constexpr int DPL = HD / 64;
+  const int lane = threadIdx.x & 63;
+  const float* pr = part + (size_t)h * nsplit * (HD + 2);
+  float M = -INFINITY;
+  for (int s = s0 + lane; s < nlive; s += 64) M = fmaxf(M, ld_f<COH>(pr + (size_t)s * (HD + 2)));
+  M = wave_max(M);
+  float L = 0.f;
+  for (int s = s0 + lane; s < nlive; s += 64) {
+    const float w = expf(ld_f<COH>(pr + (size_t)s * (HD + 2)) - M);
+    L += ld_f<COH>(pr + (size_t)s * (HD + 2) + 1) * w;
+    if (s - s0 < 256) wsl[s - s0] = w;
+  }
+  L = wave_sum(L);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float acc[DPL];
+#pragma unroll
+  for (int t = 0; t < DPL; ++t) acc[t] = 0.f;
+  const int ns = min(nlive - s0, 256);
+  for (int s8 = 0; s8 < ns; s8 += 8) {
+    // clamped, unconditional loads: all eight slices' rows are in flight together
+    float v[8][DPL];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const size_t row = (size_t)(s0 + min(s8 + u, ns - 1)) * (HD + 2) + 2 + DPL * lane;
+#pragma unroll
+      for (int t = 0; t < DPL; ++t) v[u][t] = ld_f<COH>(pr + row + t);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (s8 + u < ns) {
+        const float w = wsl[s8 + u];
+#pragma unroll
+        for (int t = 0; t < DPL; ++t) acc[t] += v[u][t] * w;
+      }
+    }
+  }
+  // slices beyond the 256 staged weights (contexts over 16K keys) use direct weights
+  for (int s = s0 + 256; s < nlive; ++s) {
+    const float w = expf(ld_f<COH>(pr + (size_t)s * (HD + 2)) - M);
+#pragma unroll
+    for (int t = 0; t < DPL; ++t) acc[t] += ld_f<COH>(pr + (size_t)s * (HD + 2) + 2 + DPL * lane + t) * w;
+  }
+#pragma unroll
+  for (int t = 0; t < DPL; ++t) st_f<COH>(out + (size_t)h * HD + DPL * lane + t, acc[t] / L);
+}
+
+// The last workgroup of a KV head to finish merges the group's heads. Release: the workgroup
+// barrier orders every wave's partial stores before thread 0's agent-scope acq_rel add (which
+// writes back this XCD's L2); the last arrival's acquire side invalidates its L2 before the
+// partials are read. The counter is reset for the next launch.
+template <int HD, bool COH = false>
+IEK_DEV void merge_if_last(const float* __restrict__ part, float* __restrict__ out, int* __restrict__ counters,
+                           int kvh, int G, int nsplit, int jmin, int total, int wave, int* last_s, float* wsl) {
+  int& last = *last_s;
+  // every wave's partial stores complete before thread 0's release (the workgroup barrier alone
+  // does not wait for global stores on this target)
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  const int s0 = jmin / SPLIT, nlive = (total + SPLIT - 1) / SPLIT;
+  if (threadIdx.x == 0) {
+    // COH: the partials went out with coherent stores and were waited for above, so a relaxed
+    // count (no L2 write-back / invalidate) orders them
+    const int old = COH ? __hip_atomic_fetch_add(&counters[kvh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                        : __hip_atomic_fetch_add(&counters[kvh], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    last = old == nlive - s0 - 1;
+    if (last) __hip_atomic_store(&counters[kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last) return;
+  if (!COH) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  for (int g = wave; g < G; g += 4) merge_head<HD, COH>(part, out, kvh * G + g, nsplit, s0, nlive, wsl + 256 * wave);
+}
+
+// LDS of one slice item: K rows (padded), V rows (HD <= 256), the group's q, the wave's
+// probabilities, the merge weights and the last-arrival flag.
+template <int HD>
+struct AttnSmem {
+  static constexpr int KROW = HD + 8;
+  static constexpr bool VL = HD <= 256;
+  static constexpr size_t KS = (size_t)SPLIT * KROW * 2, VS = VL ? (size_t)SPLIT * HD * 2 : 16,
+                          QS = 8 * (size_t)HD * 4, PS = 4 * SPLIT * 4, WS = 4 * 256 * 4;
+  static constexpr size_t BYTES = KS + VS + QS + PS + WS + 16;
+  __half* ks;
+  __half* vs;
+  float* qs;
+  float* ps;
+  float* wsl;
+  int* last;
+  IEK_DEV explicit AttnSmem(char* base) {
+    ks = reinterpret_cast<__half*>(base);
+    vs = reinterpret_cast<__half*>(base + KS);
+    qs = reinterpret_cast<float*>(base + KS + VS);
+    ps = reinterpret_cast<float*>(base + KS + VS + QS);
+    wsl = reinterpret_cast<float*>(base + KS + VS + QS + PS);
+    last = reinterpret_cast<int*>(base + KS + VS + QS + PS + WS);
+  }
+};
+
+// One (KV head, 64-key slice) item of the fp16-cache decode attention, by one 256-thread
+// workgroup; `total` = keys in the cache including this step's. Items past the live range return
+// at once (uniformly).
+template <int HD, bool COH = false>
+IEK_DEV void attn_slice_f16(const float* __restrict__ q, const __half* __restrict__ kc, const __half* __restrict__ vc,
+                            float* __restrict__ part, float* __restrict__ out, int* __restrict__ counters,
+                            int n_heads, int n_kv, int ctx, int total, int window, float scale, int nsplit, int kvh,
+                            int sp, char* smem) {
+  constexpr int DPL = HD / 64;        // head dims per lane in the PV phase
+  constexpr int KROW = HD + 8;        // padded K row (halves): 16-byte reads of different rows spread banks
+  constexpr int U4 = SPLIT * HD / 8;  // uint4 per K (or V) slice
+  // V is staged in LDS up to head_dim 256; at 512 the K slice, q and V would not fit together, so
+  // the P.V phase reads V rows straight from memory (each row one coalesced 1 KB wave load).
+  constexpr bool VL = HD <= 256;
+  static_assert(HD == 64 || HD == 128 || HD == 256 || HD == 512, "head_dim");
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = n_heads / n_kv;
+  const int jmin = (window > 0 && total > window) ? total - window : 0;
+  const int j0 = max(sp * SPLIT, jmin), j1 = min(total, (sp + 1) * SPLIT);
+  const int nk = j1 - j0;
+  if (nk <= 0) return;  // uniform across the workgroup
+  const AttnSmem<HD> S(smem);
+  auto ks = reinterpret_cast<__half(*)[KROW]>(S.ks);
+  auto vs = reinterpret_cast<__half(*)[VL ? HD : 8]>(S.vs);
+  auto qs = reinterpret_cast<float(*)[HD]>(S.qs);
+  auto ps = reinterpret_cast<float(*)[SPLIT]>(S.ps);
+  const __half* vb = vc + ((size_t)kvh * ctx + j0) * HD;
+  {
+    const __half* kb = kc + ((size_t)kvh * ctx + j0) * HD;
+    uint4 kr[U4 / 256], vr[VL ? U4 / 256 : 1];
+#pragma unroll
+    for (int u = 0; u < U4 / 256; ++u) {
+      const int i = tid + 256 * u, row = min(i / (HD / 8), nk - 1), c8 = i % (HD / 8);
+      kr[u] = *reinterpret_cast<const uint4*>(kb + (size_t)row * HD + 8 * c8);
+      if constexpr (VL) vr[u] = *reinterpret_cast<const uint4*>(vb + (size_t)row * HD + 8 * c8);
+    }
+    for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = ld_f<COH>(q + (size_t)(kvh * G) * HD + i);
+#pragma unroll
+    for (int u = 0; u < U4 / 256; ++u) {
+      const int i = tid + 256 * u, row = i / (HD / 8), c8 = i % (HD / 8);
+      *reinterpret_cast<uint4*>(&ks[row][8 * c8]) = kr[u];
+      if constexpr (VL) *reinterpret_cast<uint4*>(&vs[row][8 * c8]) = vr[u];
+    }
+  }
+  __syncthreads();
+  const bool valid = lane < nk;
+  for (int g = wave; g < G; g += 4) {
+    // scores: lane = key
+    float sc = 0.f;
+#pragma unroll
+    for (int c = 0; c < HD / 8; ++c) {
+      const uint4 kraw = *reinterpret_cast<const uint4*>(&ks[lane][8 * c]);
+      const __half2* h2 = reinterpret_cast<const __half2*>(&kraw);
+      const float4 qa = *reinterpret_cast<const float4*>(&qs[g][8 * c]);
+      const float4 qb = *reinterpret_cast<const float4*>(&qs[g][8 * c + 4]);
+      const float2 k0 = __half22float2(h2[0]), k1 = __half22float2(h2[1]), k2 = __half22float2(h2[2]),
+                   k3 = __half22float2(h2[3]);
+      sc += qa.x * k0.x + qa.y * k0.y + qa.z * k1.x + qa.w * k1.y + qb.x * k2.x + qb.y * k2.y + qb.z * k3.x +
+            qb.w * k3.y;
+    }
+    const float s = valid ? sc * scale : -INFINITY;
+    const float m = wave_max(s);
+    const float p = valid ? expf(s - m) : 0.f;
+    const float l = wave_sum(p);
+    ps[wave][lane] = p;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // P.V: lane owns dims DPL*lane .. +DPL-1; keys past the live slice carry p = 0
+    float o[DPL];
+#pragma unroll
+    for (int t = 0; t < DPL; ++t) o[t] = 0.f;
+#pragma unroll 8
+    for (int j = 0; j < SPLIT; ++j) {
+      const float pj = ps[wave][j];
+      if constexpr (DPL == 1) {
+        o[0] += pj * __half2float(vs[j][lane]);
+      } else if constexpr (DPL == 2) {
+        const float2 v2 = __half22float2(*reinterpret_cast<const __half2*>(&vs[j][2 * lane]));
+        o[0] += pj * v2.x;
+        o[1] += pj * v2.y;
+      } else if constexpr (DPL == 4) {
+        const uint2 raw = *reinterpret_cast<const uint2*>(&vs[j][4 * lane]);
+        const __half2* h2 = reinterpret_cast<const __half2*>(&raw);
+        const float2 a0 = __half22float2(h2[0]), a1 = __half22float2(h2[1]);
+        o[0] += pj * a0.x;
+        o[1] += pj * a0.y;
+        o[2] += pj * a1.x;
+        o[3] += pj * a1.y;
+      } else {
+        // rows past the live slice have p = 0; their address is clamped into the slice
+        const uint4 raw = *reinterpret_cast<const uint4*>(vb + (size_t)min(j, nk - 1) * HD + 8 * lane);
+        const __half2* h2 = reinterpret_cast<const __half2*>(&raw);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float2 a = __half22float2(h2[t]);
+          o[2 * t] += pj * a.x;
+          o[2 * t + 1] += pj * a.y;
+        }
+      }
+    }
+    float* pr = part + ((size_t)(kvh * G + g) * nsplit + sp) * (HD + 2);
+    if (lane == 0) {
+      st_f<COH>(pr, m);
+      st_f<COH>(pr + 1, l);
+    }
+#pragma unroll
+    for (int t = 0; t < DPL; ++t) st_f<COH>(pr + 2 + DPL * lane + t, o[t]);
+    __builtin_amdgcn_wave_barrier();  // ps[wave] is rewritten by the next head of this wave
+  }
+  merge_if_last<HD, COH>(part, out, counters, kvh, G, nsplit, jmin, total, wave, S.last, S.wsl);
+}
+
+
+}  // namespace iek

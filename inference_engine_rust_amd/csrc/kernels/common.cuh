@@ -36,6 +36,44 @@ IEK_DEV float wave_max(float v) {
   return v;
 }
 
+// Loads and stores coherent across the XCDs' L2 caches without cache maintenance (agent-scope
+// relaxed atomics: sc1 accesses). Used, under a COH template flag, for data that one workgroup
+// writes and another reads within the same launch (the persistent decode step); the per-launch
+// kernels keep plain accesses (kernel boundaries order their data).
+IEK_DEV float ld_coh(const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+IEK_DEV float4 ld_coh4(const float4* p) {
+  const unsigned long long* q = reinterpret_cast<const unsigned long long*>(p);
+  const unsigned long long a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float4(__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)), __uint_as_float((uint32_t)b),
+                     __uint_as_float((uint32_t)(b >> 32)));
+}
+IEK_DEV void st_coh(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+IEK_DEV void st_coh_h(__half* p, __half v) {
+  __hip_atomic_store(reinterpret_cast<unsigned short*>(p), __half_as_ushort(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+template <bool COH>
+IEK_DEV float ld_f(const float* p) {
+  if constexpr (COH) return ld_coh(p);
+  else return *p;
+}
+template <bool COH>
+IEK_DEV float4 ld_f4(const float4* p) {
+  if constexpr (COH) return ld_coh4(p);
+  else return *p;
+}
+template <bool COH>
+IEK_DEV void st_f(float* p, float v) {
+  if constexpr (COH) st_coh(p, v);
+  else *p = v;
+}
+template <bool COH>
+IEK_DEV void st_h(__half* p, __half v) {
+  if constexpr (COH) st_coh_h(p, v);
+  else *p = v;
+}
+
 // gelu_tanh (src/ops/gelu.rs:5-11): 0.5 x (1 + tanh(k (x + 0.044715 x^3))) with
 // k = FRAC_2_SQRT_PI * FRAC_1_SQRT_2 rounded to f32, each step rounded separately.
 IEK_DEV float gelu_tanh_dev(float x) {

@@ -1,0 +1,1015 @@
+// Decode matvec (M = 1) device code, shared by the per-launch kernels (matvec.hip) and the
+// persistent decode step (decode_step.hip).
+//
+// Decode matvec (M = 1): y[n] = sum_k x[k] * W(k, n) over weights kept in their native GGUF
+// block layout (ggml order: element (k, n) at flat k + n*K, src/ops/matmul.rs:1-3).
+//
+// CDNA4 mapping. A 256-thread workgroup owns 4*R consecutive output rows (R per wave):
+//  1. every lane issues the loads of its first quant chunk for all R rows;
+//  2. while they fly, the workgroup stages x in LDS once, optionally fused with RMSNorm
+//     (rms over the whole vector, y = (x*w)/rms as in src/ops/rmsnorm.rs:25-50);
+//  3. lane l walks chunks c = l, l+64, ... of its rows with the next chunk's loads in flight,
+//     dequantising in registers; per-sub-block scales are applied once per chunk:
+//        sum_k x_k (d*sc*q_k - dmin*m) = (d*sc) * sum x_k q_k - (dmin*m) * sum x_k;
+//  4. a wave butterfly leaves the R row sums in every lane; lanes 0..R-1 run the epilogue
+//     (store, residual add, SwiGLU pair, RoPE + fp16 KV append, or logits + argmax).
+// Weights are streamed exactly once per token as 16-byte coalesced loads; x never leaves LDS.
+#pragma once
+#include <algorithm>
+#include <cstdlib>
+
+#include "common.cuh"
+#include "mv_args.h"
+
+namespace iek {
+
+// (g * sigmoid(g)) * u, the reference's two-branch sigmoid (src/ops/swiglu.rs:3-36).
+IEK_DEV float silu_mul(float g, float u) {
+#pragma clang fp contract(off)
+  float s;
+  if (g >= 0.0f) {
+    float z = expf(-g);
+    s = 1.0f / (1.0f + z);
+  } else {
+    float z = expf(g);
+    s = z / (1.0f + z);
+  }
+  return g * s * u;
+}
+
+// RoPE on one element of an adjacent pair (t0, t1) (src/ops/rope.rs:52-56), unfused f32 steps.
+IEK_DEV float rope_rotate(float v, float partner, float c, float s, bool even) {
+#pragma clang fp contract(off)
+  return even ? v * c - partner * s : partner * s + v * c;
+}
+
+// cap * tanh(z / cap) (src/engine/runtime.rs:110-114).
+IEK_DEV float soft_cap(float z, float cap) {
+#pragma clang fp contract(off)
+  return cap * tanhf(z / cap);
+}
+
+template <int I>
+IEK_DEV float ubyte_f(uint32_t w) {
+  return (float)((w >> (8 * I)) & 0xFFu);
+}
+
+IEK_DEV unsigned long long argmax_key_dev(float v, uint32_t idx) {
+  uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
+}
+
+// rms = sqrt(sum/dim + eps) and y = (x*w)/rms, each step rounded like src/ops/rmsnorm.rs:44-47.
+IEK_DEV float rms_of(float sum_sq, int dim, float eps) {
+#pragma clang fp contract(off)
+  return sqrtf(sum_sq / (float)dim + eps);
+}
+IEK_DEV float mul_rn(float x, float w) {
+#pragma clang fp contract(off)
+  return x * w;
+}
+IEK_DEV float div_rn(float x, float y) {
+#pragma clang fp contract(off)
+  return x / y;
+}
+
+// ---- prologue: x (optionally RMS-normalised) into LDS ----------------------------------------
+// x (or x*w, accumulating sum(x^2)) is loaded in batches of 8 float4 per thread with all loads of a
+// batch in flight together; the normalised variant then divides the LDS copy by rms in place, i.e.
+// y = (x*w)/rms with the reference's two roundings. The epilogue's inputs (residual vector, this
+// position's RoPE cos/sin) are staged here too, so the main loop never waits on a global load.
+struct Lds {
+  float* x;      // K f32 (float staging)
+  float* res;    // N (EPI_RESID)
+  float* rope;   // 2*npairs (EPI_QKV)
+  // int8 staging: x ~= s_b * (256 * xh + xl) per 32-element block b
+  int8_t* xh;    // K
+  int8_t* xl;    // K
+  float* sb;     // K/32 block scales
+  int* sx;       // K/32 block sums of (256 * xh + xl)
+  uint8_t* wb;   // per-wave staging of raw weight bytes (coalesced-load traits only)
+};
+
+IEK_DEV void stage(const MvArgs& a, const Lds& L, int pos) {
+  const int K = a.K, tid = threadIdx.x;
+  const bool vec = (K & 3) == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
+                   (!a.norm_w || (reinterpret_cast<uintptr_t>(a.norm_w) & 15) == 0);
+  const int K4 = vec ? K >> 2 : 0;
+  const float4* x4 = reinterpret_cast<const float4*>(a.x);
+  const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
+  float4* s4 = reinterpret_cast<float4*>(L.x);
+  constexpr int B = 8;
+  float ss = 0.f;
+  for (int base = tid; base < K4; base += 256 * B) {
+    float4 v[B], w[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) v[b] = x4[min(base + 256 * b, K4 - 1)];
+    if (a.norm_w) {
+#pragma unroll
+      for (int b = 0; b < B; ++b) w[b] = w4[min(base + 256 * b, K4 - 1)];
+    }
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const int i = base + 256 * b;
+      if (i < K4) {
+        if (a.norm_w) {
+          ss += (v[b].x * v[b].x + v[b].y * v[b].y) + (v[b].z * v[b].z + v[b].w * v[b].w);
+          s4[i] = make_float4(mul_rn(v[b].x, w[b].x), mul_rn(v[b].y, w[b].y), mul_rn(v[b].z, w[b].z),
+                              mul_rn(v[b].w, w[b].w));
+        } else {
+          s4[i] = v[b];
+        }
+      }
+    }
+  }
+  for (int i = 4 * K4 + tid; i < K; i += 256) {
+    const float v = a.x[i];
+    if (a.norm_w) {
+      ss += v * v;
+      L.x[i] = mul_rn(v, a.norm_w[i]);
+    } else {
+      L.x[i] = v;
+    }
+  }
+  if (a.epi == EPI_RESID) {
+    const int N = a.n[0];
+    for (int i = tid; i < N; i += 256) L.res[i] = a.resid[i];
+  }
+  if (a.epi == EPI_QKV) {
+    for (int i = tid; i < 2 * a.npairs; i += 256) L.rope[i] = a.rope_cs[(size_t)pos * a.npairs * 2 + i];
+  }
+  if (a.norm_w) {
+    __shared__ float red[4];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, WAVE);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    const float rms = rms_of((red[0] + red[1]) + (red[2] + red[3]), K, a.eps);
+    for (int i = tid; i < K; i += 256) L.x[i] = div_rn(L.x[i], rms);
+  }
+  __syncthreads();
+  // Clamped loads whose values went unused (lanes past K) are still counted as pending; retire
+  // them here, where nothing else is in flight, so the main loop's first wait is not a full drain.
+  __builtin_amdgcn_s_waitcnt(0);
+}
+
+// LDS bytes: x staging (f32: 4K; int8: 2K planes + 8 bytes per 32-block), then the residual
+// vector (EPI_RESID) and this position's RoPE (cos, sin) pairs (EPI_QKV).
+__host__ __device__ inline size_t lds_bytes(const MvArgs& a, bool i8, size_t wbuf = 0) {
+  const size_t xb = i8 ? 2 * (size_t)a.K + 8 * (size_t)(a.K / 32) : 4 * (size_t)a.K;
+  return wbuf + xb + (a.epi == EPI_RESID ? 4 * (size_t)a.n[0] : 0) + (a.epi == EPI_QKV ? 8 * (size_t)a.npairs : 0);
+}
+
+// [per-wave weight staging (wbuf bytes)][x staging][residual][RoPE]
+IEK_DEV Lds lds_layout(const MvArgs& a, float* base, bool i8, size_t wbuf = 0) {
+  Lds L;
+  L.wb = reinterpret_cast<uint8_t*>(base);
+  base = reinterpret_cast<float*>(reinterpret_cast<char*>(base) + wbuf);
+  char* p = reinterpret_cast<char*>(base);
+  L.x = nullptr;
+  L.xh = L.xl = nullptr;
+  L.sb = nullptr;
+  L.sx = nullptr;
+  if (i8) {
+    L.xh = reinterpret_cast<int8_t*>(p);
+    L.xl = L.xh + a.K;
+    L.sb = reinterpret_cast<float*>(p + 2 * (size_t)a.K);
+    L.sx = reinterpret_cast<int*>(L.sb + a.K / 32);
+    p += 2 * (size_t)a.K + 8 * (size_t)(a.K / 32);
+  } else {
+    L.x = base;
+    p += 4 * (size_t)a.K;
+  }
+  L.res = reinterpret_cast<float*>(p);
+  L.rope = L.res + (a.epi == EPI_RESID ? a.n[0] : 0);
+  return L;
+}
+
+// ---- int8 staging of x ------------------------------------------------------------------------
+// Each 32-element block b of y = x*w (or x) is stored as a 16-bit integer vector X with
+// y ~= s_b * X, s_b = amax_b / (32639 * rms) and |X| <= 32639, split as X = 256*xh + xl with
+// xh in [-127, 127] and xl in [-128, 127], so two v_dot4_i32_i8 per 4 weights give the exact
+// integer sum of q*X. The representation error is at most s_b/2 per element (~1.5e-5 of the
+// block's largest |y|); the RMS factor never touches the elements (it only enters s_b), so no
+// per-element division is needed. Threads own whole blocks (K <= 16384).
+constexpr float XQ_MAX = 32639.0f;
+
+IEK_DEV void quant_block(const float (&y)[32], float am, uint32_t (&h)[8], uint32_t (&l)[8], int& sum) {
+  const float inv = am > 0.f ? XQ_MAX / am : 0.f;
+  sum = 0;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    uint32_t hw = 0, lw = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      int X = __float2int_rn(y[4 * g + e] * inv);
+      X = max(-32639, min(32639, X));
+      const int hi = (X + 128) >> 8, lo = X - (hi << 8);
+      sum += X;
+      hw |= (uint32_t)(hi & 0xFF) << (8 * e);
+      lw |= (uint32_t)(lo & 0xFF) << (8 * e);
+    }
+    h[g] = hw;
+    l[g] = lw;
+  }
+}
+
+// The staging is split so its global loads can be issued before the first weight loads: the
+// memory counter retires in order, so x (an L2 hit) would otherwise wait behind the weight stream.
+// stage_i8_issue loads this thread's first 32-element block of x (and w), its share of the residual
+// vector and its RoPE pair into registers; stage_i8_finish consumes them.
+struct XPre {
+  float4 xv[8], wv[8];
+  float4 res[4];
+  float2 rope;
+};
+
+IEK_DEV bool res_vec(const MvArgs& a) {
+  return a.epi == EPI_RESID && (a.n[0] & 3) == 0 && a.n[0] <= 4096 && (reinterpret_cast<uintptr_t>(a.resid) & 15) == 0;
+}
+
+template <bool COH = false>
+IEK_DEV void stage_i8_issue(const MvArgs& a, XPre& p, int pos) {
+  const int tid = threadIdx.x, nb = a.K >> 5, bc = min(tid, nb - 1);
+  const float4* x4 = reinterpret_cast<const float4*>(a.x) + (size_t)bc * 8;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) p.xv[t] = ld_f4<COH>(x4 + t);
+  if (a.norm_w) {
+    const float4* w4 = reinterpret_cast<const float4*>(a.norm_w) + (size_t)bc * 8;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) p.wv[t] = w4[t];
+  } else {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) p.wv[t] = make_float4(1.f, 1.f, 1.f, 1.f);
+  }
+  if (res_vec(a)) {
+    const float4* r4 = reinterpret_cast<const float4*>(a.resid);
+    const int n4 = a.n[0] >> 2;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) p.res[u] = ld_f4<COH>(r4 + min(tid + 256 * u, n4 - 1));
+  }
+  if (a.epi == EPI_QKV)
+    p.rope = reinterpret_cast<const float2*>(a.rope_cs)[(size_t)pos * a.npairs + min(tid, a.npairs - 1)];
+}
+
+IEK_DEV void quant_store(const MvArgs& a, const Lds& L, int b, const float4 (&xv)[8], const float4 (&wv)[8], float& ss,
+                         float& amax) {
+  float y[32];
+  float am = 0.f, sq = 0.f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const float xs[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+    const float ws[4] = {wv[t].x, wv[t].y, wv[t].z, wv[t].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sq += xs[e] * xs[e];
+      y[4 * t + e] = a.norm_w ? mul_rn(xs[e], ws[e]) : xs[e];
+      am = fmaxf(am, fabsf(y[4 * t + e]));
+    }
+  }
+  uint32_t h[8], l[8];
+  int sum;
+  quant_block(y, am, h, l, sum);
+  amax = am;
+  if (b < (a.K >> 5)) {
+    ss += sq;
+    uint4* ph = reinterpret_cast<uint4*>(L.xh + 32 * b);
+    uint4* pl = reinterpret_cast<uint4*>(L.xl + 32 * b);
+    ph[0] = make_uint4(h[0], h[1], h[2], h[3]);
+    ph[1] = make_uint4(h[4], h[5], h[6], h[7]);
+    pl[0] = make_uint4(l[0], l[1], l[2], l[3]);
+    pl[1] = make_uint4(l[4], l[5], l[6], l[7]);
+    L.sx[b] = sum;
+  }
+}
+
+template <bool COH = false>
+IEK_DEV void stage_i8_finish(const MvArgs& a, const Lds& L, int pos, const XPre& p) {
+  const int K = a.K, tid = threadIdx.x, nb = K >> 5;
+  float ss = 0.f;
+  float amax[2] = {0.f, 0.f};
+  quant_store(a, L, tid, p.xv, p.wv, ss, amax[0]);
+  if (nb > 256) {
+    // second block of this thread (K > 8192), loaded here
+    const int b = tid + 256, bc = min(b, nb - 1);
+    float4 xv[8], wv[8];
+    const float4* x4 = reinterpret_cast<const float4*>(a.x) + (size_t)bc * 8;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) xv[t] = ld_f4<COH>(x4 + t);
+    if (a.norm_w) {
+      const float4* w4 = reinterpret_cast<const float4*>(a.norm_w) + (size_t)bc * 8;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) wv[t] = w4[t];
+    } else {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) wv[t] = make_float4(1.f, 1.f, 1.f, 1.f);
+    }
+    quant_store(a, L, b, xv, wv, ss, amax[1]);
+  }
+  if (a.epi == EPI_RESID) {
+    const int N = a.n[0];
+    if (res_vec(a)) {
+      float4* d4 = reinterpret_cast<float4*>(L.res);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (tid + 256 * u < (N >> 2)) d4[tid + 256 * u] = p.res[u];
+    } else {
+      for (int i = tid; i < N; i += 256) L.res[i] = ld_f<COH>(a.resid + i);
+    }
+  }
+  if (a.epi == EPI_QKV && tid < a.npairs) reinterpret_cast<float2*>(L.rope)[tid] = p.rope;
+  if (a.epi == EPI_QKV)
+    for (int i = 256 + tid; i < a.npairs; i += 256)
+      reinterpret_cast<float2*>(L.rope)[i] = reinterpret_cast<const float2*>(a.rope_cs)[(size_t)pos * a.npairs + i];
+  float rms = 1.f;
+  if (a.norm_w) {
+    __shared__ float red[4];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, WAVE);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    rms = rms_of((red[0] + red[1]) + (red[2] + red[3]), K, a.eps);
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int b = tid + 256 * j;
+    if (b < nb) L.sb[b] = amax[j] / (XQ_MAX * rms);
+  }
+  __syncthreads();
+}
+
+
+// Segment fields picked with constant indices: a dynamic index into the by-value argument block
+// becomes a vector memory load, whose wait would also drain the in-flight weight prefetch.
+IEK_DEV const uint8_t* seg_w(const MvArgs& a, int s) { return s == 0 ? a.w[0] : (s == 1 ? a.w[1] : a.w[2]); }
+IEK_DEV float* seg_out(const MvArgs& a, int s) { return s == 0 ? a.out[0] : (s == 1 ? a.out[1] : a.out[2]); }
+IEK_DEV int seg_base(const MvArgs& a, int s) { return s == 0 ? a.seg_start[0] : (s == 1 ? a.seg_start[1] : a.seg_start[2]); }
+
+// ---- epilogue -----------------------------------------------------------------------------------
+// Reads only registers and LDS (pos was loaded at kernel start).
+template <int R, bool COH = false>
+IEK_DEV void epilogue(const MvArgs& a, const Lds& L, int s, int lr0, float (&acc)[R], const float* acc_up, int lane,
+                      int pos, unsigned long long& run_key) {
+  if (a.epi == EPI_SWIGLU || a.epi == EPI_GEGLU) {
+    if (lane < R) {
+      float g = acc[0], u = acc_up[0];
+#pragma unroll
+      for (int r = 1; r < R; ++r)
+        if (lane == r) {
+          g = acc[r];
+          u = acc_up[r];
+        }
+      st_f<COH>(a.out[0] + lr0 + lane, a.epi == EPI_GEGLU ? gelu_tanh_dev(g) * u : silu_mul(g, u));
+    }
+    return;
+  }
+  if (a.epi == EPI_QKV) {
+    // Rows come in RoPE pairs (2k, 2k+1) of one head (R is even and rows start even).
+    if (lane < R) {
+      const int n = lr0 + lane;
+      float v = acc[0], partner = acc[0];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (lane == r) v = acc[r];
+        if ((lane ^ 1) == r) partner = acc[r];
+      }
+      const int hd = a.head_dim;
+      const int d = n % hd;
+      if (s < 2 && d < 2 * a.npairs) v = rope_rotate(v, partner, L.rope[d & ~1], L.rope[(d & ~1) + 1], (d & 1) == 0);
+      if (s == 0) {
+        st_f<COH>(a.out[0] + n, v);
+      } else {
+        const size_t dst = ((size_t)(n / hd) * a.ctx + pos) * hd + d;
+        st_h<COH>((s == 1 ? a.kc : a.vc) + dst, __float2half_rn(v));
+      }
+    }
+    return;
+  }
+  if (a.epi == EPI_ARGMAX) {
+    // logits row n: store (soft-capped), fold its packed (value, first-index) key into the lane's
+    // running maximum; one atomic per workgroup at the end of the launch (argmax_flush)
+    float v = acc[0];
+#pragma unroll
+    for (int r = 1; r < R; ++r)
+      if (lane == r) v = acc[r];
+    if (a.softcap > 0.f) v = soft_cap(v, a.softcap);
+    if (lane < R) {
+      a.out[0][lr0 + lane] = v;
+      const unsigned long long key = argmax_key_dev(v, (uint32_t)(lr0 + lane));
+      run_key = key > run_key ? key : run_key;
+      if (!isfinite(v)) atomicOr(a.amax_flag, 1);
+    }
+    return;
+  }
+  if (lane < R) {
+    float v = acc[0];
+#pragma unroll
+    for (int r = 1; r < R; ++r)
+      if (lane == r) v = acc[r];
+    const int n = lr0 + lane;
+    if (a.epi == EPI_RESID) v = L.res[n] + v;
+    st_f<COH>(seg_out(a, s) + n, v);
+  }
+}
+
+template <int R>
+IEK_DEV void wave_reduce(float (&acc)[R]) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+}
+
+// ---- Q4_K -----------------------------------------------------------------------------------
+// Chunk g (0..3) of a superblock = qs bytes [32g, 32g+32): 32 low nibbles (sub-block 2g, elements
+// 64g+l) and 32 high nibbles (sub-block 2g+1, elements 64g+32+l). The nibbles go straight into
+// v_fma_mix_f32 as f16 operands: (w >> s) & 0x000F000F leaves two nibbles in the two halves of a
+// register, each the f16 subnormal q * 2^-24, which the instruction widens exactly; the 2^24 is
+// folded into the sub-block scale.
+IEK_DEV float h_lo(uint32_t w) { return __half2float(__ushort_as_half((unsigned short)(w & 0xFFFFu))); }
+IEK_DEV float h_hi(uint32_t w) { return __half2float(__ushort_as_half((unsigned short)(w >> 16))); }
+
+// sum over one qs dword (bytes l..l+3): lo nibbles against xl[0..3], hi nibbles against xh[0..3]
+IEK_DEV void q4_dword(uint32_t w, const float4 xl, const float4 xh, float& sl, float& sh) {
+  const uint32_t t0 = w & 0x000F000Fu, t1 = (w >> 4) & 0x000F000Fu;
+  const uint32_t t2 = (w >> 8) & 0x000F000Fu, t3 = (w >> 12) & 0x000F000Fu;
+  sl = fmaf(xl.x, h_lo(t0), sl);
+  sl = fmaf(xl.z, h_hi(t0), sl);
+  sh = fmaf(xh.x, h_lo(t1), sh);
+  sh = fmaf(xh.z, h_hi(t1), sh);
+  sl = fmaf(xl.y, h_lo(t2), sl);
+  sl = fmaf(xl.w, h_hi(t2), sl);
+  sh = fmaf(xh.y, h_lo(t3), sh);
+  sh = fmaf(xh.w, h_hi(t3), sh);
+}
+
+// get_scale_min_k4 for a per-lane sub-block index without branches (both forms are extracted and
+// selected), so every lane of the wave runs one path and every loaded header dword is consumed.
+IEK_DEV void scale_min_k4_sel(int j, uint32_t s0, uint32_t s1, uint32_t s2, float* sc, float* m) {
+  const int i = j & 3;
+  const uint32_t b0 = byte_of(s0, i), b1 = byte_of(s1, i), b2 = byte_of(s2, i);
+  const uint32_t sc_lo = b0 & 63u, m_lo = b1 & 63u;
+  const uint32_t sc_hi = (b2 & 0xFu) | ((b0 >> 6) << 4), m_hi = (b2 >> 4) | ((b1 >> 6) << 4);
+  *sc = (float)(j < 4 ? sc_lo : sc_hi);
+  *m = (float)(j < 4 ? m_lo : m_hi);
+}
+
+IEK_DEV float q4k_dot(uint4 hdr, uint4 q0, uint4 q1, int g, const float4* xl4, const float4* xh4, float xsl,
+                      float xsh) {
+  float d = half_bits_to_float(hdr.x), dmin = half_bits_to_float(hdr.x >> 16);
+  float sc0, m0, sc1, m1;
+  scale_min_k4_sel(2 * g, hdr.y, hdr.z, hdr.w, &sc0, &m0);
+  scale_min_k4_sel(2 * g + 1, hdr.y, hdr.z, hdr.w, &sc1, &m1);
+  const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+  float sl = 0.f, sh = 0.f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) q4_dword(qw[t], xl4[t], xh4[t], sl, sh);
+  const float k24 = 16777216.0f;  // 2^24
+  return (d * sc0 * k24) * sl - (dmin * m0) * xsl + (d * sc1 * k24) * sh - (dmin * m1) * xsh;
+}
+
+// ---- Q6_K -----------------------------------------------------------------------------------
+// Chunk (h, o8): l = 8*o8..8*o8+7 of half h, all four quarters (32 values). The 210-byte
+// superblocks are only 2-byte aligned, so 8-byte fields are read as aligned dword triples and
+// re-sliced with v_alignbyte.
+struct Q6Raw {
+  uint32_t a[3], b[3], h[3], s[3];
+  uint32_t d, sh_ql, sh_s;
+};
+
+// Three dwords from the aligned address at or below p (the third only when the 8-byte field
+// crosses into it), so reads never leave the superblock.
+IEK_DEV void load_tri(const uint8_t* p, uint32_t (&o)[3], uint32_t* shift) {
+  const uintptr_t ap = reinterpret_cast<uintptr_t>(p);
+  const uint32_t* base = reinterpret_cast<const uint32_t*>(ap & ~uintptr_t(3));
+  *shift = (uint32_t)(ap & 3u);
+  o[0] = base[0];
+  o[1] = base[1];
+  o[2] = base[*shift ? 2 : 1];  // always issued; with shift 0 the third dword is not used
+}
+
+IEK_DEV void q6_load(const uint8_t* blk, int h, int o8, Q6Raw& q) {
+  uint32_t sh;
+  load_tri(blk + 64 * h + 8 * o8, q.a, &q.sh_ql);
+  load_tri(blk + 64 * h + 32 + 8 * o8, q.b, &sh);
+  load_tri(blk + 128 + 32 * h + 8 * o8, q.h, &sh);
+  // scale window: bytes 192 + 8h + o8/2 + {0, 2, 4, 6}; a 7-byte span needs the third dword only
+  // when the window starts at offset 2 or 3 of its dword.
+  const uintptr_t ap = reinterpret_cast<uintptr_t>(blk + 192 + 8 * h + (o8 >> 1));
+  const uint32_t* base = reinterpret_cast<const uint32_t*>(ap & ~uintptr_t(3));
+  q.sh_s = (uint32_t)(ap & 3u);
+  q.s[0] = base[0];
+  q.s[1] = base[1];
+  q.s[2] = base[q.sh_s >= 2 ? 2 : 1];  // always issued; unused bytes are never extracted
+  q.d = *reinterpret_cast<const uint16_t*>(blk + 208);
+}
+
+IEK_DEV float q6k_dot(const Q6Raw& q, const float4* x4, const float (&xs4)[4]) {
+  const uint32_t sh_ql = q.sh_ql, sh_s = q.sh_s;
+  const uint32_t A[2] = {__builtin_amdgcn_alignbyte(q.a[1], q.a[0], sh_ql), __builtin_amdgcn_alignbyte(q.a[2], q.a[1], sh_ql)};
+  const uint32_t B[2] = {__builtin_amdgcn_alignbyte(q.b[1], q.b[0], sh_ql), __builtin_amdgcn_alignbyte(q.b[2], q.b[1], sh_ql)};
+  const uint32_t H[2] = {__builtin_amdgcn_alignbyte(q.h[1], q.h[0], sh_ql), __builtin_amdgcn_alignbyte(q.h[2], q.h[1], sh_ql)};
+  const uint32_t S0 = __builtin_amdgcn_alignbyte(q.s[1], q.s[0], sh_s), S1 = __builtin_amdgcn_alignbyte(q.s[2], q.s[1], sh_s);
+  // scales for the four quarters sit at window bytes 0, 2, 4, 6
+  const float sc[4] = {(float)(int8_t)(S0 & 0xFF), (float)(int8_t)((S0 >> 16) & 0xFF), (float)(int8_t)(S1 & 0xFF),
+                       (float)(int8_t)((S1 >> 16) & 0xFF)};
+  const float d = half_bits_to_float(q.d);
+  // 6-bit values (q + 32) are assembled per byte, split into register halves and fed to
+  // v_fma_mix_f32 as exact f16 subnormals (value * 2^-24).
+  float s[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const uint32_t qq[4] = {(A[t] & 0x0F0F0F0Fu) | ((H[t] << 4) & 0x30303030u),
+                            (B[t] & 0x0F0F0F0Fu) | ((H[t] << 2) & 0x30303030u),
+                            ((A[t] >> 4) & 0x0F0F0F0Fu) | (H[t] & 0x30303030u),
+                            ((B[t] >> 4) & 0x0F0F0F0Fu) | ((H[t] >> 2) & 0x30303030u)};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 xv = x4[2 * i + t];
+      const uint32_t e = qq[i] & 0x00FF00FFu, o = (qq[i] >> 8) & 0x00FF00FFu;
+      s[i] = fmaf(xv.x, h_lo(e), s[i]);
+      s[i] = fmaf(xv.z, h_hi(e), s[i]);
+      s[i] = fmaf(xv.y, h_lo(o), s[i]);
+      s[i] = fmaf(xv.w, h_hi(o), s[i]);
+    }
+  }
+  float r = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r += (d * sc[i]) * (16777216.0f * s[i] - 32.0f * xs4[i]);
+  return r;
+}
+
+// End of an EPI_ARGMAX launch: reduce the lanes' running keys over the workgroup and publish one
+// atomicMax (the key packs the value's order and the inverted index, so the maximum is the first
+// maximal index).
+IEK_DEV void argmax_flush(const MvArgs& a, unsigned long long run_key) {
+  __shared__ unsigned long long red_key[4];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned long long o = __shfl_xor(run_key, off, WAVE);
+    run_key = o > run_key ? o : run_key;
+  }
+  if ((threadIdx.x & 63) == 0) red_key[threadIdx.x >> 6] = run_key;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long k = red_key[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) k = red_key[w] > k ? red_key[w] : k;
+    if (k) atomicMax(a.amax_key, k);
+  }
+}
+
+// ---- streaming driver ------------------------------------------------------------------------
+// Wave w of workgroup b owns row groups (4b + w) + k * (4 * gridDim.x). It walks the flattened
+// (group, pass) sequence with two register buffers used alternately (no copies of in-flight data),
+// issuing the next step's weight loads before computing the current one. Loads are unconditional
+// with clamped addresses so the compiler can count them statically and keep them all in flight.
+struct Q4Tr {
+  static constexpr bool I8 = false;
+  static constexpr bool WB = false;
+  static constexpr int CHUNKS = 4;  // 64-value chunks per superblock
+  static constexpr int BYTES = Q4K_BYTES;
+  IEK_DEV static size_t row_bytes(int nsb) { return (size_t)nsb * BYTES; }
+  template <int NR>
+  struct Buf {
+    uint4 hdr[NR], qa[NR], qb[NR];
+  };
+  template <int NR>
+  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c, int nsb) {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const uint8_t* blk = rows[r] + (size_t)(c >> 2) * Q4K_BYTES;
+      b.hdr[r] = *reinterpret_cast<const uint4*>(blk);
+      b.qa[r] = *reinterpret_cast<const uint4*>(blk + 16 + 32 * (c & 3));
+      b.qb[r] = *reinterpret_cast<const uint4*>(blk + 32 + 32 * (c & 3));
+    }
+  }
+  template <int NR>
+  IEK_DEV static void compute(const Buf<NR>& b, int c, const Lds& L, float (&acc)[NR]) {
+    const float* xs = L.x;
+    const int e0 = (c >> 2) * QK_K + (c & 3) * 64;
+    float4 xl4[8], xh4[8];
+    float xsl = 0.f, xsh = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      xl4[t] = *reinterpret_cast<const float4*>(xs + e0 + 4 * t);
+      xh4[t] = *reinterpret_cast<const float4*>(xs + e0 + 32 + 4 * t);
+      xsl += (xl4[t].x + xl4[t].y) + (xl4[t].z + xl4[t].w);
+      xsh += (xh4[t].x + xh4[t].y) + (xh4[t].z + xh4[t].w);
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc[r] += q4k_dot(b.hdr[r], b.qa[r], b.qb[r], c & 3, xl4, xh4, xsl, xsh);
+  }
+};
+
+struct Q6Tr {
+  static constexpr bool I8 = false;
+  static constexpr bool WB = false;
+  static constexpr int CHUNKS = 8;  // 32-value chunks per superblock
+  static constexpr int BYTES = Q6K_BYTES;
+  IEK_DEV static size_t row_bytes(int nsb) { return (size_t)nsb * BYTES; }
+  template <int NR>
+  struct Buf {
+    Q6Raw q[NR];
+  };
+  template <int NR>
+  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c, int nsb) {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) q6_load(rows[r] + (size_t)(c >> 3) * Q6K_BYTES, (c >> 2) & 1, c & 3, b.q[r]);
+  }
+  template <int NR>
+  IEK_DEV static void compute(const Buf<NR>& b, int c, const Lds& L, float (&acc)[NR]) {
+    const float* xs = L.x;
+    const int e0 = (c >> 3) * QK_K + 128 * ((c >> 2) & 1) + 8 * (c & 3);
+    float4 x4[8];
+    float xs4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x4[2 * i] = *reinterpret_cast<const float4*>(xs + e0 + 32 * i);
+      x4[2 * i + 1] = *reinterpret_cast<const float4*>(xs + e0 + 32 * i + 4);
+      const float4 u = x4[2 * i], v = x4[2 * i + 1];
+      xs4[i] = ((u.x + u.y) + (u.z + u.w)) + ((v.x + v.y) + (v.z + v.w));
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc[r] += q6k_dot(b.q[r], x4, xs4);
+  }
+};
+
+// Q4_K against the int8-staged x: per 64-value chunk, the low nibbles (sub-block 2g) and high
+// nibbles (sub-block 2g+1) each give the exact integer S = sum q*X through v_dot4_i32_i8 on the
+// (xh, xl) planes; the row sum is then s_b * (d*sc*S - dmin*m*sum X) per sub-block, the same
+// algebra as the reference's sum over (d*sc*q - dmin*m) * x with x replaced by s_b*X.
+struct Q4I8Tr {
+  static constexpr bool I8 = true;
+  static constexpr bool WB = false;
+  static constexpr int CHUNKS = 4;
+  static constexpr int BYTES = Q4K_BYTES;
+  IEK_DEV static size_t row_bytes(int nsb) { return (size_t)nsb * BYTES; }
+  template <int NR>
+  using Buf = Q4Tr::Buf<NR>;
+  template <int NR>
+  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c, int nsb) {
+    Q4Tr::load<NR>(b, rows, c, nsb);
+  }
+  template <int NR>
+  IEK_DEV static void compute(const Buf<NR>& b, int c, const Lds& L, float (&acc)[NR]) {
+    const int e0 = (c >> 2) * QK_K + (c & 3) * 64, b0 = e0 >> 5;
+    const uint4* ph = reinterpret_cast<const uint4*>(L.xh + e0);
+    const uint4* pl = reinterpret_cast<const uint4*>(L.xl + e0);
+    const uint4 H0 = ph[0], H1 = ph[1], H2 = ph[2], H3 = ph[3];
+    const uint4 L0 = pl[0], L1 = pl[1], L2 = pl[2], L3 = pl[3];
+    const uint32_t xh[16] = {H0.x, H0.y, H0.z, H0.w, H1.x, H1.y, H1.z, H1.w,
+                             H2.x, H2.y, H2.z, H2.w, H3.x, H3.y, H3.z, H3.w};
+    const uint32_t xl[16] = {L0.x, L0.y, L0.z, L0.w, L1.x, L1.y, L1.z, L1.w,
+                             L2.x, L2.y, L2.z, L2.w, L3.x, L3.y, L3.z, L3.w};
+    const float2 sb = *reinterpret_cast<const float2*>(L.sb + b0);
+    const int2 sx = *reinterpret_cast<const int2*>(L.sx + b0);
+    const int g = c & 3;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const uint4 hdr = b.hdr[r];
+      const uint32_t qw[8] = {b.qa[r].x, b.qa[r].y, b.qa[r].z, b.qa[r].w, b.qb[r].x, b.qb[r].y, b.qb[r].z, b.qb[r].w};
+      int h0 = 0, l0 = 0, h1 = 0, l1 = 0;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int lo = (int)(qw[t] & 0x0F0F0F0Fu), hi = (int)((qw[t] >> 4) & 0x0F0F0F0Fu);
+        h0 = __builtin_amdgcn_sdot4(lo, (int)xh[t], h0, false);
+        l0 = __builtin_amdgcn_sdot4(lo, (int)xl[t], l0, false);
+        h1 = __builtin_amdgcn_sdot4(hi, (int)xh[8 + t], h1, false);
+        l1 = __builtin_amdgcn_sdot4(hi, (int)xl[8 + t], l1, false);
+      }
+      const float d = half_bits_to_float(hdr.x), dmin = half_bits_to_float(hdr.x >> 16);
+      float sc0, m0, sc1, m1;
+      scale_min_k4_sel(2 * g, hdr.y, hdr.z, hdr.w, &sc0, &m0);
+      scale_min_k4_sel(2 * g + 1, hdr.y, hdr.z, hdr.w, &sc1, &m1);
+      const float S0 = (float)(h0 * 256 + l0), S1 = (float)(h1 * 256 + l1);
+      acc[r] += sb.x * ((d * sc0) * S0 - (dmin * m0) * (float)sx.x) + sb.y * ((d * sc1) * S1 - (dmin * m1) * (float)sx.y);
+    }
+  }
+};
+
+constexpr int Q6_ROW_SLOT = 2048;  // LDS bytes per staged row for traits that stage raw weight bytes
+
+// Q6_K against the int8-staged x. The 6-bit values are assembled per byte as in q6k_dot, made
+// signed (q - 32) bytewise with (q + 0x60) ^ 0x80, and two v_dot4 per 4 weights give
+// S = sum (q - 32) * X exactly; each 8-weight run contributes s_b * (d * sc) * S.
+struct Q6I8Tr {
+  static constexpr bool I8 = true;
+  static constexpr bool WB = false;
+  static constexpr int CHUNKS = 8;
+  static constexpr int BYTES = Q6K_BYTES;
+  IEK_DEV static size_t row_bytes(int nsb) { return (size_t)nsb * BYTES; }
+  template <int NR>
+  using Buf = Q6Tr::Buf<NR>;
+  template <int NR>
+  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c, int nsb) {
+    Q6Tr::load<NR>(b, rows, c, nsb);
+  }
+  template <int NR>
+  IEK_DEV static void compute(const Buf<NR>& b, int c, const Lds& L, float (&acc)[NR]) {
+    const int e0 = (c >> 3) * QK_K + 128 * ((c >> 2) & 1) + 8 * (c & 3);
+    uint32_t xh[8], xl[8];
+    float sq[4];
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const uint2 vh = *reinterpret_cast<const uint2*>(L.xh + e0 + 32 * qd);
+      const uint2 vl = *reinterpret_cast<const uint2*>(L.xl + e0 + 32 * qd);
+      xh[2 * qd] = vh.x, xh[2 * qd + 1] = vh.y, xl[2 * qd] = vl.x, xl[2 * qd + 1] = vl.y;
+      sq[qd] = L.sb[(e0 + 32 * qd) >> 5];
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const Q6Raw& q = b.q[r];
+      const uint32_t sh_ql = q.sh_ql, sh_s = q.sh_s;
+      const uint32_t A[2] = {__builtin_amdgcn_alignbyte(q.a[1], q.a[0], sh_ql), __builtin_amdgcn_alignbyte(q.a[2], q.a[1], sh_ql)};
+      const uint32_t B[2] = {__builtin_amdgcn_alignbyte(q.b[1], q.b[0], sh_ql), __builtin_amdgcn_alignbyte(q.b[2], q.b[1], sh_ql)};
+      const uint32_t H[2] = {__builtin_amdgcn_alignbyte(q.h[1], q.h[0], sh_ql), __builtin_amdgcn_alignbyte(q.h[2], q.h[1], sh_ql)};
+      const uint32_t S0 = __builtin_amdgcn_alignbyte(q.s[1], q.s[0], sh_s), S1 = __builtin_amdgcn_alignbyte(q.s[2], q.s[1], sh_s);
+      const float sc[4] = {(float)(int8_t)(S0 & 0xFF), (float)(int8_t)((S0 >> 16) & 0xFF), (float)(int8_t)(S1 & 0xFF),
+                           (float)(int8_t)((S1 >> 16) & 0xFF)};
+      const float d = half_bits_to_float(q.d);
+      int hs[4] = {0, 0, 0, 0}, ls[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint32_t qq[4] = {(A[t] & 0x0F0F0F0Fu) | ((H[t] << 4) & 0x30303030u),
+                                (B[t] & 0x0F0F0F0Fu) | ((H[t] << 2) & 0x30303030u),
+                                ((A[t] >> 4) & 0x0F0F0F0Fu) | (H[t] & 0x30303030u),
+                                ((B[t] >> 4) & 0x0F0F0F0Fu) | ((H[t] >> 2) & 0x30303030u)};
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const int sgn = (int)((qq[qd] + 0x60606060u) ^ 0x80808080u);  // bytes q - 32 as int8
+          hs[qd] = __builtin_amdgcn_sdot4(sgn, (int)xh[2 * qd + t], hs[qd], false);
+          ls[qd] = __builtin_amdgcn_sdot4(sgn, (int)xl[2 * qd + t], ls[qd], false);
+        }
+      }
+      float sum = 0.f;
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) sum += sq[qd] * ((d * sc[qd]) * (float)(hs[qd] * 256 + ls[qd]));
+      acc[r] += sum;
+    }
+  }
+};
+
+// Q6_K in the regrouped per-row layout (DT_Q6K_R, built once at model load by
+// launch_repack_q6k): for superblock j of a row, lane chunk k = 2h + j16 holds the 16 ql bytes of
+// quarters 0/2, the 16 ql bytes of quarters 1/3 and the 16 qh bytes for weights l = 16*j16 ..
+// 16*j16+15 of half h (48 contiguous, 16-byte aligned bytes), its four sub-block scales as one
+// dword and the superblock's d. A lane's 64 weights are thus three coalesced 16-byte loads plus
+// two small ones, instead of thirteen dword loads per 32 weights from the 210-byte blocks. The
+// values are the same bytes, so the dequantised weights are unchanged.
+struct Q6RTr {
+  static constexpr bool I8 = true;
+  static constexpr bool WB = false;
+  static constexpr int CHUNKS = 4;
+  static constexpr int BYTES = 208;
+  IEK_DEV static size_t row_bytes(int nsb) { return q6r_row_bytes(nsb); }
+  template <int NR>
+  struct Buf {
+    uint4 qa[NR], qb[NR], qh[NR];
+    uint32_t sc[NR], d[NR];
+  };
+  template <int NR>
+  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c, int nsb) {
+    const int j = c >> 2, k = c & 3;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const uint8_t* m = rows[r] + (size_t)j * 192 + 48 * k;
+      b.qa[r] = *reinterpret_cast<const uint4*>(m);
+      b.qb[r] = *reinterpret_cast<const uint4*>(m + 16);
+      b.qh[r] = *reinterpret_cast<const uint4*>(m + 32);
+      b.sc[r] = *reinterpret_cast<const uint32_t*>(rows[r] + (size_t)nsb * 192 + 16 * j + 4 * k);
+      b.d[r] = *reinterpret_cast<const uint16_t*>(rows[r] + (size_t)nsb * 208 + 2 * j);
+    }
+  }
+  template <int NR>
+  IEK_DEV static void compute(const Buf<NR>& b, int c, const Lds& L, float (&acc)[NR]) {
+    const int j = c >> 2, k = c & 3, h = k >> 1, j16 = k & 1;
+    const int e0 = j * QK_K + 128 * h + 16 * j16;
+    uint4 XH[4], XL[4];
+    float sq[4];
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      XH[qd] = *reinterpret_cast<const uint4*>(L.xh + e0 + 32 * qd);
+      XL[qd] = *reinterpret_cast<const uint4*>(L.xl + e0 + 32 * qd);
+      sq[qd] = L.sb[(e0 >> 5) + qd];
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const uint32_t A[4] = {b.qa[r].x, b.qa[r].y, b.qa[r].z, b.qa[r].w};
+      const uint32_t B[4] = {b.qb[r].x, b.qb[r].y, b.qb[r].z, b.qb[r].w};
+      const uint32_t H[4] = {b.qh[r].x, b.qh[r].y, b.qh[r].z, b.qh[r].w};
+      int hs[4] = {0, 0, 0, 0}, ls[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t qq[4] = {(A[t] & 0x0F0F0F0Fu) | ((H[t] << 4) & 0x30303030u),
+                                (B[t] & 0x0F0F0F0Fu) | ((H[t] << 2) & 0x30303030u),
+                                ((A[t] >> 4) & 0x0F0F0F0Fu) | (H[t] & 0x30303030u),
+                                ((B[t] >> 4) & 0x0F0F0F0Fu) | ((H[t] >> 2) & 0x30303030u)};
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const uint32_t xhw = t == 0 ? XH[qd].x : t == 1 ? XH[qd].y : t == 2 ? XH[qd].z : XH[qd].w;
+          const uint32_t xlw = t == 0 ? XL[qd].x : t == 1 ? XL[qd].y : t == 2 ? XL[qd].z : XL[qd].w;
+          const int sgn = (int)((qq[qd] + 0x60606060u) ^ 0x80808080u);  // bytes q - 32 as int8
+          hs[qd] = __builtin_amdgcn_sdot4(sgn, (int)xhw, hs[qd], false);
+          ls[qd] = __builtin_amdgcn_sdot4(sgn, (int)xlw, ls[qd], false);
+        }
+      }
+      const float d = half_bits_to_float(b.d[r]);
+      float sum = 0.f;
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd)
+        sum += sq[qd] * ((d * (float)(int8_t)((b.sc[r] >> (8 * qd)) & 0xFF)) * (float)(hs[qd] * 256 + ls[qd]));
+      acc[r] += sum;
+    }
+  }
+};
+
+// Q8_0 in a regrouped per-row layout (DT_Q8_0_R, built once at model load by launch_repack_q80):
+// a row's nb = K/32 blocks keep their 32 int8 quants as nb contiguous 32-byte runs, followed by
+// the nb f16 scales (padded to 16 bytes), so one lane's block is two 16-byte loads and one short
+// load instead of 34 bytes at 2-byte alignment. The bytes are the native ones, rearranged.
+// x stays f32 here (the Gemma-4 models that use Q8_0 have a score scale of 1 on normalised q/k,
+// which turns the int8 staging's 2^-16 activation rounding into ~1e-3 of logit error): each quant
+// byte is read as the unsigned q + 128 (v_cvt_f32_ubyte after flipping the sign bits), and the
+// offset comes back as one term per block, d * (sum x*(q+128) - 128 * sum x).
+struct Q8RTr {
+  static constexpr bool I8 = false;
+  static constexpr bool WB = false;
+  static constexpr int CHUNKS = 8;  // 32-value blocks per 256
+  static constexpr int BYTES = 34;
+  IEK_DEV static size_t row_bytes(int nsb) { return q8r_row_bytes((size_t)nsb * 8); }
+  template <int NR>
+  struct Buf {
+    uint4 qa[NR], qb[NR];
+    uint32_t d[NR];
+  };
+  template <int NR>
+  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c, int nsb) {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const uint8_t* m = rows[r] + (size_t)c * 32;
+      b.qa[r] = *reinterpret_cast<const uint4*>(m);
+      b.qb[r] = *reinterpret_cast<const uint4*>(m + 16);
+      b.d[r] = *reinterpret_cast<const uint16_t*>(rows[r] + (size_t)nsb * 256 + 2 * c);
+    }
+  }
+  template <int NR>
+  IEK_DEV static void compute(const Buf<NR>& b, int c, const Lds& L, float (&acc)[NR]) {
+    const float4* x4 = reinterpret_cast<const float4*>(L.x + 32 * c);
+    float4 xv[8];
+    float xsum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      xv[t] = x4[t];
+      xsum += (xv[t].x + xv[t].y) + (xv[t].z + xv[t].w);
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const uint32_t q[8] = {b.qa[r].x, b.qa[r].y, b.qa[r].z, b.qa[r].w, b.qb[r].x, b.qb[r].y, b.qb[r].z, b.qb[r].w};
+      float s = 0.f;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const uint32_t u = q[t] ^ 0x80808080u;  // bytes q + 128
+        s += xv[t].x * ubyte_f<0>(u) + xv[t].y * ubyte_f<1>(u) + xv[t].z * ubyte_f<2>(u) + xv[t].w * ubyte_f<3>(u);
+      }
+      acc[r] += half_bits_to_float(b.d[r]) * (s - 128.f * xsum);
+    }
+  }
+};
+
+// Geometry of one streaming pass over a launch's rows: wave w of workgroup b owns row groups
+// (4b + w) + k * (4 * gridDim.x) and walks its flattened (group, K pass) steps.
+template <class Tr, int R, bool DUAL>
+struct MvGeom {
+  static constexpr int NR = DUAL ? 2 * R : R;
+  int lane, g0, stride, groups, nsb, nchunk, npass, steps;
+  size_t rb;
+  IEK_DEV MvGeom(const MvArgs& a) {
+    lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int total = a.nseg == 1 ? a.seg_start[1] : (a.nseg == 2 ? a.seg_start[2] : a.seg_start[3]);
+    groups = total / R;
+    stride = gridDim.x * 4;
+    g0 = blockIdx.x * 4 + wave;
+    nsb = a.K / QK_K;
+    rb = Tr::row_bytes(nsb);
+    nchunk = (a.K / QK_K) * Tr::CHUNKS;
+    npass = (nchunk + WAVE - 1) / WAVE;
+    const int my_groups = g0 < groups ? (groups - 1 - g0) / stride + 1 : 0;
+    steps = my_groups * npass;
+  }
+  // Row pointers and chunk of step `it` (clamped into the wave's range so every load is valid).
+  IEK_DEV void rows_of(const MvArgs& a, int it, const uint8_t* (&rows)[NR], int& c) const {
+    const int k = min(it, steps - 1);
+    const int g = g0 + (k / npass) * stride, p = k % npass;
+    c = min(lane + WAVE * p, nchunk - 1);
+    const int row0 = g * R;
+    const int s = DUAL ? 0 : seg_of(a, row0);
+    const int lr0 = row0 - seg_base(a, s);
+    const uint8_t* w0 = seg_w(a, s);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) rows[r] = r < R ? w0 + (size_t)lr0 * rb + (size_t)r * rb : a.w[1] + (size_t)(lr0 + r - R) * rb;
+  }
+};
+
+// Issues the loads of a launch's first step into `A` (used to start a phase's weight stream
+// before the data it depends on is ready).
+template <class Tr, int R, bool DUAL>
+IEK_DEV void mv_prefetch(const MvArgs& a, typename Tr::template Buf<DUAL ? 2 * R : R>& A) {
+  constexpr int NR = DUAL ? 2 * R : R;
+  const MvGeom<Tr, R, DUAL> G(a);
+  if (G.steps > 0) {
+    const uint8_t* rows[NR];
+    int c;
+    G.rows_of(a, 0, rows, c);
+    Tr::template load<NR>(A, rows, c, G.nsb);
+  }
+}
+
+// The streaming matvec of one launch's rows. With `prefetched`, buffer A already holds (or has in
+// flight) the first step, issued by mv_prefetch with the same arguments.
+template <class Tr, int R, bool DUAL, bool COH = false>
+IEK_DEV void mv_body(const MvArgs& a, float* lds, int pos, typename Tr::template Buf<DUAL ? 2 * R : R>& A,
+                     bool prefetched) {
+  static_assert(!COH || Tr::I8, "coherent staging is implemented for the int8-staged traits");
+  constexpr int NR = DUAL ? 2 * R : R;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  Lds L = lds_layout(a, lds, Tr::I8, Tr::WB ? 4 * NR * Q6_ROW_SLOT : 0);
+  L.wb += wave * NR * Q6_ROW_SLOT;
+  const MvGeom<Tr, R, DUAL> G(a);
+  const int npass = G.npass, nchunk = G.nchunk, steps = G.steps;
+  typename Tr::template Buf<NR> B;
+  unsigned long long run_key = 0;
+  float acc[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) acc[r] = 0.f;
+
+  auto finish = [&](int it) {
+    const int p = it % npass;
+    if (p != npass - 1) return;
+    const int g = G.g0 + (it / npass) * G.stride;
+    float accg[R], accu[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      accg[r] = acc[r];
+      accu[r] = DUAL ? acc[R + r] : 0.f;
+    }
+    wave_reduce<R>(accg);
+    if (DUAL) wave_reduce<R>(accu);
+    const int row0 = g * R;
+    const int s = DUAL ? 0 : seg_of(a, row0);
+    epilogue<R, COH>(a, L, s, row0 - seg_base(a, s), accg, accu, lane, pos, run_key);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc[r] = 0.f;
+  };
+  auto step = [&](const typename Tr::template Buf<NR>& buf, int it) {
+    const int p = it % npass;
+    const int c = lane + WAVE * p;
+    float part[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) part[r] = 0.f;
+    Tr::template compute<NR>(buf, min(c, nchunk - 1), L, part);
+    // The empty asm pins the dot products as computed on every path: otherwise the compiler sinks
+    // them under the c < nchunk branch and a wave whose lanes all skip it leaves the buffer's loads
+    // unretired, which costs a full drain at the next reuse of those registers.
+#pragma unroll
+    for (int r = 0; r < NR; ++r) asm volatile("" : "+v"(part[r]));
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc[r] += c < nchunk ? part[r] : 0.f;
+    finish(it);
+  };
+
+  // x / residual / RoPE loads go out first, then the first weight buffer, so the staging work
+  // overlaps the weight fetch instead of queueing behind it.
+  XPre xp;
+  if constexpr (Tr::I8) stage_i8_issue<COH>(a, xp, pos);
+  if (!prefetched && steps > 0) {
+    const uint8_t* rows[NR];
+    int c;
+    G.rows_of(a, 0, rows, c);
+    Tr::template load<NR>(A, rows, c, G.nsb);
+  }
+  if constexpr (Tr::I8)
+    stage_i8_finish<COH>(a, L, pos, xp);
+  else
+    stage(a, L, pos);
+  for (int it = 0; it < steps; it += 2) {
+    if (it + 1 < steps) {
+      const uint8_t* rows[NR];
+      int c;
+      G.rows_of(a, it + 1, rows, c);
+      Tr::template load<NR>(B, rows, c, G.nsb);
+    }
+    step(A, it);
+    if (it + 1 >= steps) break;
+    if (it + 2 < steps) {
+      const uint8_t* rows[NR];
+      int c;
+      G.rows_of(a, it + 2, rows, c);
+      Tr::template load<NR>(A, rows, c, G.nsb);
+    }
+    step(B, it + 1);
+  }
+  if (a.epi == EPI_ARGMAX) argmax_flush(a, run_key);
+}
+
+}  // namespace iek

@@ -100,10 +100,17 @@ Session::Session(Model* m) : m_(m) {
   launch_fill_u64(d_key_, 0ull, 1, st_);
   launch_fill_i32(d_flag_, 0, 1, st_);
   launch_fill_i32(d_cnt_, 0, c.n_kv_heads, st_);
+  d_bar_ = dev_alloc<unsigned>(step_bar_words());
+  d_err_ = dev_alloc<int>(1);
+  launch_fill_i32((int*)d_bar_, 0, step_bar_words(), st_);
+  launch_fill_i32(d_err_, 0, 1, st_);
+  prepare_step();
   reset();
 }
 
 Session::~Session() {
+  if (st_) (void)hipStreamSynchronize(st_);
+  dump_step_trace();
   if (step_exec_) (void)hipGraphExecDestroy(step_exec_);
   if (step_graph_) (void)hipGraphDestroy(step_graph_);
   if (st_) (void)hipStreamSynchronize(st_);
@@ -112,7 +119,8 @@ Session::~Session() {
                   (void*)attd_, (void*)actd_, (void*)logits_, (void*)part_, (void*)tmpd_, (void*)d_pos_,
                   (void*)d_step_, (void*)d_flags_, (void*)d_tok_, (void*)d_ids_, (void*)d_gen_, (void*)d_key_,
                   (void*)d_flag_, (void*)d_cnt_, (void*)xs_, (void*)xsum_, kv_blob_, (void*)ple_tok_,
-                  (void*)ple_proj_, (void*)ple_pack_, (void*)ple_tokd_, (void*)ple_projd_, (void*)ple_packd_})
+                  (void*)ple_proj_, (void*)ple_pack_, (void*)ple_tokd_, (void*)ple_projd_, (void*)ple_packd_,
+                  (void*)d_bar_, (void*)d_err_, step_layers_, (void*)d_trace_})
     dev_free(p);
   if (st_) (void)hipStreamDestroy(st_);
 }
@@ -301,19 +309,16 @@ bool Session::fused_ok(int li) const {
          L.gate.dtype == L.up.dtype && kq(L.gate.dtype) && H_ % 256 == 0 && c.layers[li].head_dim % 2 == 0;
 }
 
-void Session::layer_decode(int li, bool last) {
+// Launch arguments of the fused decode path's four matvecs of layer li (QKV with RMSNorm, RoPE and
+// the KV append; O + residual; gate/up with RMSNorm and SwiGLU; down + residual) and their
+// weight layouts.
+void Session::decode_args(int li, MvArgs& a, MvArgs& o, MvArgs& f, MvArgs& dn, int* dts) {
   const Config& c = m_->cfg;
   const LayerSpec& S = c.layers[li];
   const LayerTensors& L = m_->layers[li];
   const int hd = S.head_dim, qd = S.q_dim, kvd = S.kv_dim;
-  const float scale = 1.0f / sqrtf((float)hd);
-  if (!fused_ok(li)) {
-    layer_decode_unfused(li);
-    if (last) launch_add_int(d_pos_, 1, st_);
-    return;
-  }
   const RopeTable& rt = m_->rope_tables[L.rope_table];
-  MvArgs a{};
+  a = MvArgs{};
   a.nseg = 3;
   a.w[0] = (const uint8_t*)L.wq.dev;
   a.w[1] = (const uint8_t*)L.wk.dev;
@@ -334,10 +339,8 @@ void Session::layer_decode(int li, bool last) {
   a.pos = d_pos_;
   a.kc = (__half*)kc_[li];
   a.vc = (__half*)vc_[li];
-  launch_mv(L.wq.dtype, a, st_);
-  launch_attn_decode(qd_, kc_[li], vc_[li], kv_f32_, attd_, part_, d_cnt_, c.n_heads, c.n_kv_heads, hd, ctx_, d_pos_, S.window,
-                     scale, ctx_, st_);
-  MvArgs o{};
+  dts[0] = L.wq.dtype;
+  o = MvArgs{};
   o.nseg = 1;
   o.w[0] = (const uint8_t*)L.wo.dev;
   o.out[0] = xdec_;
@@ -346,8 +349,8 @@ void Session::layer_decode(int li, bool last) {
   o.K = qd;
   o.epi = EPI_RESID;
   o.resid = xdec_;
-  launch_mv(L.wo.dtype, o, st_);
-  MvArgs f{};
+  dts[1] = L.wo.dtype;
+  f = MvArgs{};
   f.nseg = 2;
   f.w[0] = (const uint8_t*)L.gate.dev;
   f.w[1] = (const uint8_t*)L.up.dev;
@@ -359,8 +362,8 @@ void Session::layer_decode(int li, bool last) {
   f.eps = c.rms_eps;
   f.K = H_;
   f.epi = EPI_SWIGLU;
-  launch_mv(L.gate.dtype, f, st_);
-  MvArgs dn{};
+  dts[2] = L.gate.dtype;
+  dn = MvArgs{};
   dn.nseg = 1;
   int down_dt = L.down.dtype;
   dn.w[0] = (const uint8_t*)mv_weight(L.down, S.ffn_dim, &down_dt);
@@ -370,8 +373,82 @@ void Session::layer_decode(int li, bool last) {
   dn.K = S.ffn_dim;
   dn.epi = EPI_RESID;
   dn.resid = xdec_;
+  dts[3] = down_dt;
+}
+
+void Session::layer_decode(int li, bool last) {
+  const Config& c = m_->cfg;
+  const LayerSpec& S = c.layers[li];
+  const int hd = S.head_dim;
+  const float scale = 1.0f / sqrtf((float)hd);
+  if (!fused_ok(li)) {
+    layer_decode_unfused(li);
+    if (last) launch_add_int(d_pos_, 1, st_);
+    return;
+  }
+  MvArgs a, o, f, dn;
+  int dts[4];
+  decode_args(li, a, o, f, dn, dts);
+  launch_mv(dts[0], a, st_);
+  launch_attn_decode(qd_, kc_[li], vc_[li], kv_f32_, attd_, part_, d_cnt_, c.n_heads, c.n_kv_heads, hd, ctx_, d_pos_,
+                     S.window, scale, ctx_, st_);
+  launch_mv(dts[1], o, st_);
+  launch_mv(dts[2], f, st_);
   dn.pos_inc = last ? d_pos_ : nullptr;
-  launch_mv(down_dt, dn, st_);
+  launch_mv(dts[3], dn, st_);
+}
+
+// IEK_DECODE_STEP=1 selects the persistent decode step (every layer of a token in one launch) when
+// every layer takes the fused path with the int8-staged matvec traits it is built for (Q4_K Q/K/V,
+// O, gate/up and the regrouped Q6_K down), one head dim of 64 or 128 and no sliding window. It is
+// not the default: its grid barriers and coherent activation traffic cost more than the kernel
+// boundaries they replace (2.84 ms against 2.01 ms per C2 token, measured with IEK_STEP_TRACE).
+void Session::prepare_step() {
+  const Config& c = m_->cfg;
+  const char* e = getenv("IEK_DECODE_STEP");
+  if (!e || atoi(e) != 1) return;
+  if (gemma_ || c.n_layers <= 0) return;
+  const int hd = c.layers[0].head_dim;
+  if (hd != 64 && hd != 128) return;
+  if (c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads != 0 || c.n_heads / c.n_kv_heads > 8) return;
+  std::vector<uint8_t> host((size_t)c.n_layers * step_layer_bytes());
+  size_t lds = 0;
+  for (int li = 0; li < c.n_layers; ++li) {
+    const LayerSpec& S = c.layers[li];
+    if (!fused_ok(li) || S.head_dim != hd || S.window > 0 || S.kv_borrow >= 0) return;
+    MvArgs ph[4];
+    int dts[4];
+    decode_args(li, ph[0], ph[1], ph[2], ph[3], dts);
+    const int want[4] = {DT_Q4K, DT_Q4K, DT_Q4K, DT_Q6K_R};
+    for (int i = 0; i < 4; ++i) {
+      mv_finalize(ph[i]);
+      if (dts[i] != want[i] || !mv_stream_i8_ok(dts[i], ph[i])) return;
+      lds = std::max(lds, mv_lds_bytes_i8(ph[i]));
+    }
+    step_layer_pack(host.data() + (size_t)li * step_layer_bytes(), ph[0], ph[1], ph[2], ph[3],
+                    (const __half*)kc_[li], (const __half*)vc_[li], qd_, attd_, S.window);
+  }
+  IEK_HIP(hipMalloc(&step_layers_, host.size()));
+  IEK_HIP(hipMemcpy(step_layers_, host.data(), host.size(), hipMemcpyHostToDevice));
+  step_lds_ = lds;
+  // IEK_STEP_TRACE=1: record workgroup 0's clock at every phase boundary of the last step and print
+  // the per-phase durations when the session ends (a profiling aid; the step does the same work)
+  const char* t = getenv("IEK_STEP_TRACE");
+  if (t && atoi(t) != 0) d_trace_ = dev_alloc<unsigned long long>(16 * (size_t)c.n_layers + 4);
+}
+
+void Session::dump_step_trace() {
+  if (!d_trace_) return;
+  const int nl = m_->cfg.n_layers, n = 1 + 10 * nl;
+  std::vector<unsigned long long> h(n);
+  if (hipMemcpy(h.data(), d_trace_, n * 8, hipMemcpyDeviceToHost) != hipSuccess) return;
+  const char* names[10] = {"qkv", "bar1", "attn", "bar2", "o", "bar3", "gateup", "bar4", "down", "bar5"};
+  double sum[10] = {0};
+  for (int l = 0; l < nl; ++l)
+    for (int k = 0; k < 10; ++k) sum[k] += (double)(h[1 + 10 * l + k] - h[10 * l + k]) * 0.01;  // 100 MHz
+  fprintf(stderr, "[step trace] per-layer average us:");
+  for (int k = 0; k < 10; ++k) fprintf(stderr, " %s %.2f", names[k], sum[k] / nl);
+  fprintf(stderr, " | step %.1f us\n", (double)(h[n - 1] - h[0]) * 0.01);
 }
 
 void Session::layer_decode_unfused(int li) {
@@ -677,8 +754,27 @@ void Session::decode_body() {
     embed_ple(d_tok_, 1, xdec_, nullptr, ple_tokd_, ple_projd_, ple_packd_);
     for (int li = 0; li < c.n_layers; ++li) layer_decode_gemma(li);
     launch_add_int(d_pos_, 1, st_);
+  } else if (step_layers_) {
+    launch_decode_step(step_layers_, c.n_layers, c.n_heads, c.n_kv_heads, c.layers[0].head_dim, ctx_,
+                       1.0f / sqrtf((float)c.layers[0].head_dim), part_, d_cnt_, d_pos_, d_pos_, d_bar_, d_err_,
+                       step_lds_, d_trace_, st_);
   } else {
     for (int li = 0; li < c.n_layers; ++li) layer_decode(li, li == c.n_layers - 1);
+  }
+}
+
+// A grid-barrier timeout in the persistent decode step leaves its flag set; the session reports
+// it as a device error (its state is then undefined, as after any failed step).
+void Session::check_step_error() {
+  if (!step_layers_) return;
+  int err = 0;
+  IEK_HIP(hipMemcpyAsync(&err, d_err_, 4, hipMemcpyDeviceToHost, st_));
+  sync();
+  if (err) {
+    launch_fill_i32((int*)d_bar_, 0, step_bar_words(), st_);
+    launch_fill_i32(d_err_, 0, 1, st_);
+    sync();
+    fail(ST_DEVICE, "decode step: a grid barrier wait timed out");
   }
 }
 
@@ -694,6 +790,7 @@ void Session::decode_token(uint32_t id) {
   state_rows_ = 1;
   state_prefill_ = false;
   sync();
+  check_step_error();
 }
 
 void Session::check_state() const {
@@ -794,6 +891,7 @@ void Session::generate_greedy(int n, uint32_t* out_ids, bool use_graph) {
   pos_ += n;
   state_rows_ = 1;
   state_prefill_ = false;
+  check_step_error();
   for (int i = 0; i < n; ++i)
     if (flags[i]) fail(ST_SAMPLING, "invalid logits for argmax (empty or non-finite) at step " + std::to_string(i));
 }

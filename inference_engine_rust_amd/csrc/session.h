@@ -4,6 +4,7 @@
 #include <vector>
 
 #include "model.h"
+#include "kernels/mv_args.h"
 
 namespace iek {
 
@@ -33,6 +34,10 @@ class Session {
   void layer_prefill(int li, int M);
   bool project_q(const DevTensor* const* ws, float* const* outs, int nseg, int M, int K, const float* resid);
   bool fused_ok(int li) const;
+  void decode_args(int li, MvArgs& qkv, MvArgs& o, MvArgs& gate_up, MvArgs& down, int* dts);
+  void prepare_step();
+  void check_step_error();
+  void dump_step_trace();
   void layer_decode(int li, bool last);
   void layer_decode_unfused(int li);
   // Gemma-4 family (attention.rs / ffn.rs Gemma branches, gemma4_ple.rs)
@@ -65,6 +70,13 @@ class Session {
   float *ple_tok_ = nullptr, *ple_proj_ = nullptr, *ple_pack_ = nullptr;
   float *ple_tokd_ = nullptr, *ple_projd_ = nullptr, *ple_packd_ = nullptr;
   bool gemma_ = false;
+  // persistent decode step: device array of per-layer launch arguments (null: per-launch path),
+  // its LDS size, the grid-barrier counters and the barrier timeout flag
+  void* step_layers_ = nullptr;
+  size_t step_lds_ = 0;
+  unsigned* d_bar_ = nullptr;
+  int* d_err_ = nullptr;
+  unsigned long long* d_trace_ = nullptr;
   // device-side loop state
   int* d_pos_ = nullptr;
   int* d_step_ = nullptr;
