@@ -17,10 +17,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
                                                           const __half* __restrict__ vc, float* __restrict__ part,
                                                           float* __restrict__ out, int* __restrict__ counters,
                                                           int n_heads, int n_kv, int ctx, const int* pos_dev,
-                                                          int window, float scale, int nsplit) {
+                                                          int window, float scale, int nsplit, int spc) {
   __shared__ __align__(16) char smem[AttnSmem<HD>::BYTES];
-  attn_slice_f16<HD>(q, kc, vc, part, out, counters, n_heads, n_kv, ctx, *pos_dev + 1, window, scale, nsplit,
-                     blockIdx.x, blockIdx.y, smem);
+  attn_chunk_f16<HD>(q, kc, vc, part, out, counters, n_heads, n_kv, ctx, *pos_dev + 1, window, scale, nsplit,
+                     blockIdx.x, blockIdx.y, spc, smem);
 }
 
 // f32 KV cache variant (Gemma-4 sessions keep the reference's f32 cache: with q/k head norms
@@ -127,19 +127,24 @@ __global__ __launch_bounds__(256) void attn_decode_f32_kernel(const float* __res
   }
   __shared__ int last;
   __shared__ float wsl[4 * 256];
-  merge_if_last<HD>(part, out, counters, kvh, G, nsplit, jmin, total, wave, &last, wsl);
+  merge_if_last<HD>(part, out, counters, kvh, G, nsplit, jmin / SPLIT, (total + SPLIT - 1) / SPLIT, wave, &last, wsl);
 }
 
 template <int HD>
 static void attn_decode_hd(dim3 grid, hipStream_t st, const float* q, const void* kc, const void* vc, bool kv_f32,
                            float* out, float* part, int* counters, int n_heads, int n_kv, int ctx, const int* pos_dev,
                            int window, float scale, int nsplit) {
-  if (kv_f32)
+  if (kv_f32) {
     hipLaunchKernelGGL(attn_decode_f32_kernel<HD>, grid, dim3(256), 0, st, q, (const float*)kc, (const float*)vc, part,
                        out, counters, n_heads, n_kv, ctx, pos_dev, window, scale, nsplit);
-  else
-    hipLaunchKernelGGL(attn_decode_kernel<HD>, grid, dim3(256), 0, st, q, (const __half*)kc, (const __half*)vc, part,
-                       out, counters, n_heads, n_kv, ctx, pos_dev, window, scale, nsplit);
+  } else {
+    // fp16 cache: chunks of spc slices; one partial slot per chunk
+    const int spc = attn_slices_per_chunk(nsplit * SPLIT);
+    const int nchunk = (nsplit + spc - 1) / spc;
+    hipLaunchKernelGGL(attn_decode_kernel<HD>, dim3(grid.x, nchunk), dim3(256), 0, st, q, (const __half*)kc,
+                       (const __half*)vc, part, out, counters, n_heads, n_kv, ctx, pos_dev, window, scale, nchunk,
+                       spc);
+  }
 }
 
 void launch_attn_decode(const float* q, const void* kc, const void* vc, bool kv_f32, float* out, float* part,

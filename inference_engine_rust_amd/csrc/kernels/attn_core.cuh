@@ -73,15 +73,15 @@ IEK_DEV void merge_head(const float* __restrict__ part, float* __restrict__ out,
 // barrier orders every wave's partial stores before thread 0's agent-scope acq_rel add (which
 // writes back this XCD's L2); the last arrival's acquire side invalidates its L2 before the
 // partials are read. The counter is reset for the next launch.
+// s0 .. nlive-1 are the live partial slots of the KV head.
 template <int HD, bool COH = false>
 IEK_DEV void merge_if_last(const float* __restrict__ part, float* __restrict__ out, int* __restrict__ counters,
-                           int kvh, int G, int nsplit, int jmin, int total, int wave, int* last_s, float* wsl) {
+                           int kvh, int G, int nsplit, int s0, int nlive, int wave, int* last_s, float* wsl) {
   int& last = *last_s;
   // every wave's partial stores complete before thread 0's release (the workgroup barrier alone
   // does not wait for global stores on this target)
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  const int s0 = jmin / SPLIT, nlive = (total + SPLIT - 1) / SPLIT;
   if (threadIdx.x == 0) {
     // COH: the partials went out with coherent stores and were waited for above, so a relaxed
     // count (no L2 write-back / invalidate) orders them
@@ -121,14 +121,20 @@ struct AttnSmem {
   }
 };
 
-// One (KV head, 64-key slice) item of the fp16-cache decode attention, by one 256-thread
-// workgroup; `total` = keys in the cache including this step's. Items past the live range return
-// at once (uniformly).
+// One (KV head, chunk) item of the fp16-cache decode attention, by one 256-thread workgroup: the
+// chunk is `spc` consecutive 64-key slices. Each slice's K and V rows are loaded in one burst of
+// clamped, unconditional 16-byte loads and staged in LDS (V read straight from memory at head dim
+// 512); the loads of slice i+1 are in flight while slice i is computed. Wave w takes query heads
+// w and w+4 of the GQA group: lane = key for the scores, lane = head dims [DPL*l, DPL*l + DPL)
+// for P.V, with a running (max, sum, o) across the chunk's slices. The chunk publishes its
+// (max, sum, o[]) partial in slot `cp`; the last chunk of the KV head to finish merges the
+// group's heads. `total` = keys in the cache including this step's; chunks past the live range
+// return at once (uniformly).
 template <int HD, bool COH = false>
-IEK_DEV void attn_slice_f16(const float* __restrict__ q, const __half* __restrict__ kc, const __half* __restrict__ vc,
+IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restrict__ kc, const __half* __restrict__ vc,
                             float* __restrict__ part, float* __restrict__ out, int* __restrict__ counters,
-                            int n_heads, int n_kv, int ctx, int total, int window, float scale, int nsplit, int kvh,
-                            int sp, char* smem) {
+                            int n_heads, int n_kv, int ctx, int total, int window, float scale, int nslot, int kvh,
+                            int cp, int spc, char* smem) {
   constexpr int DPL = HD / 64;        // head dims per lane in the PV phase
   constexpr int KROW = HD + 8;        // padded K row (halves): 16-byte reads of different rows spread banks
   constexpr int U4 = SPLIT * HD / 8;  // uint4 per K (or V) slice
@@ -140,100 +146,134 @@ IEK_DEV void attn_slice_f16(const float* __restrict__ q, const __half* __restric
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = n_heads / n_kv;
   const int jmin = (window > 0 && total > window) ? total - window : 0;
-  const int j0 = max(sp * SPLIT, jmin), j1 = min(total, (sp + 1) * SPLIT);
-  const int nk = j1 - j0;
-  if (nk <= 0) return;  // uniform across the workgroup
+  const int CK = SPLIT * spc;
+  const int c0 = max(cp * CK, jmin), c1 = min(total, (cp + 1) * CK);
+  if (c1 <= c0) return;  // uniform across the workgroup
+  const int sb0 = c0 / SPLIT, sb1 = (c1 + SPLIT - 1) / SPLIT;
   const AttnSmem<HD> S(smem);
   auto ks = reinterpret_cast<__half(*)[KROW]>(S.ks);
   auto vs = reinterpret_cast<__half(*)[VL ? HD : 8]>(S.vs);
   auto qs = reinterpret_cast<float(*)[HD]>(S.qs);
   auto ps = reinterpret_cast<float(*)[SPLIT]>(S.ps);
-  const __half* vb = vc + ((size_t)kvh * ctx + j0) * HD;
-  {
-    const __half* kb = kc + ((size_t)kvh * ctx + j0) * HD;
-    uint4 kr[U4 / 256], vr[VL ? U4 / 256 : 1];
+  const __half* kh = kc + (size_t)kvh * ctx * HD;
+  const __half* vh = vc + (size_t)kvh * ctx * HD;
+  // native vectors (a HIP uint4 array captured by the lambda would not be promoted to registers)
+  typedef uint32_t kv4_t __attribute__((ext_vector_type(4)));
+  kv4_t kr[U4 / 256], vr[VL ? U4 / 256 : 1];
+  auto issue = [&](int sb) {
+    const int j0 = max(sb * SPLIT, c0), nk = min((sb + 1) * SPLIT, c1) - j0;
 #pragma unroll
     for (int u = 0; u < U4 / 256; ++u) {
-      const int i = tid + 256 * u, row = min(i / (HD / 8), nk - 1), c8 = i % (HD / 8);
-      kr[u] = *reinterpret_cast<const uint4*>(kb + (size_t)row * HD + 8 * c8);
-      if constexpr (VL) vr[u] = *reinterpret_cast<const uint4*>(vb + (size_t)row * HD + 8 * c8);
+      const int i = tid + 256 * u, row = j0 + min(i / (HD / 8), nk - 1), c8 = i % (HD / 8);
+      kr[u] = *reinterpret_cast<const kv4_t*>(kh + (size_t)row * HD + 8 * c8);
+      if constexpr (VL) vr[u] = *reinterpret_cast<const kv4_t*>(vh + (size_t)row * HD + 8 * c8);
     }
-    for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = ld_f<COH>(q + (size_t)(kvh * G) * HD + i);
+  };
+  issue(sb0);
+  for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = ld_f<COH>(q + (size_t)(kvh * G) * HD + i);
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f}, o_run[2][DPL];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) o_run[t][d] = 0.f;
+  for (int sb = sb0; sb < sb1; ++sb) {
+    const int j0 = max(sb * SPLIT, c0), nk = min((sb + 1) * SPLIT, c1) - j0;
+    __syncthreads();  // the previous slice's LDS reads are done
 #pragma unroll
     for (int u = 0; u < U4 / 256; ++u) {
       const int i = tid + 256 * u, row = i / (HD / 8), c8 = i % (HD / 8);
-      *reinterpret_cast<uint4*>(&ks[row][8 * c8]) = kr[u];
-      if constexpr (VL) *reinterpret_cast<uint4*>(&vs[row][8 * c8]) = vr[u];
+      *reinterpret_cast<kv4_t*>(&ks[row][8 * c8]) = kr[u];
+      if constexpr (VL) *reinterpret_cast<kv4_t*>(&vs[row][8 * c8]) = vr[u];
     }
-  }
-  __syncthreads();
-  const bool valid = lane < nk;
-  for (int g = wave; g < G; g += 4) {
-    // scores: lane = key
-    float sc = 0.f;
+    __syncthreads();
+    if (sb + 1 < sb1) issue(sb + 1);
+    const __half* vb = vh + (size_t)j0 * HD;
+    const bool valid = lane < nk;
 #pragma unroll
-    for (int c = 0; c < HD / 8; ++c) {
-      const uint4 kraw = *reinterpret_cast<const uint4*>(&ks[lane][8 * c]);
-      const __half2* h2 = reinterpret_cast<const __half2*>(&kraw);
-      const float4 qa = *reinterpret_cast<const float4*>(&qs[g][8 * c]);
-      const float4 qb = *reinterpret_cast<const float4*>(&qs[g][8 * c + 4]);
-      const float2 k0 = __half22float2(h2[0]), k1 = __half22float2(h2[1]), k2 = __half22float2(h2[2]),
-                   k3 = __half22float2(h2[3]);
-      sc += qa.x * k0.x + qa.y * k0.y + qa.z * k1.x + qa.w * k1.y + qb.x * k2.x + qb.y * k2.y + qb.z * k3.x +
-            qb.w * k3.y;
-    }
-    const float s = valid ? sc * scale : -INFINITY;
-    const float m = wave_max(s);
-    const float p = valid ? expf(s - m) : 0.f;
-    const float l = wave_sum(p);
-    ps[wave][lane] = p;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // P.V: lane owns dims DPL*lane .. +DPL-1; keys past the live slice carry p = 0
-    float o[DPL];
+    for (int t = 0; t < 2; ++t) {
+      const int g = wave + 4 * t;
+      if (g >= G) break;
+      // scores: lane = key
+      float sc = 0.f;
 #pragma unroll
-    for (int t = 0; t < DPL; ++t) o[t] = 0.f;
+      for (int c = 0; c < HD / 8; ++c) {
+        const uint4 kraw = *reinterpret_cast<const uint4*>(&ks[lane][8 * c]);
+        const __half2* h2 = reinterpret_cast<const __half2*>(&kraw);
+        const float4 qa = *reinterpret_cast<const float4*>(&qs[g][8 * c]);
+        const float4 qb = *reinterpret_cast<const float4*>(&qs[g][8 * c + 4]);
+        const float2 k0 = __half22float2(h2[0]), k1 = __half22float2(h2[1]), k2 = __half22float2(h2[2]),
+                     k3 = __half22float2(h2[3]);
+        sc += qa.x * k0.x + qa.y * k0.y + qa.z * k1.x + qa.w * k1.y + qb.x * k2.x + qb.y * k2.y + qb.z * k3.x +
+              qb.w * k3.y;
+      }
+      const float s = valid ? sc * scale : -INFINITY;
+      const float m_new = fmaxf(m_run[t], wave_max(s));
+      const float corr = m_run[t] == -INFINITY ? 1.f : expf(m_run[t] - m_new);
+      const float p = valid ? expf(s - m_new) : 0.f;
+      l_run[t] = l_run[t] * corr + wave_sum(p);
+      m_run[t] = m_new;
+      ps[wave][lane] = p;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // P.V: lane owns dims DPL*lane .. +DPL-1; keys past the live slice carry p = 0
+      float o[DPL];
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) o[d] = o_run[t][d] * corr;
 #pragma unroll 8
-    for (int j = 0; j < SPLIT; ++j) {
-      const float pj = ps[wave][j];
-      if constexpr (DPL == 1) {
-        o[0] += pj * __half2float(vs[j][lane]);
-      } else if constexpr (DPL == 2) {
-        const float2 v2 = __half22float2(*reinterpret_cast<const __half2*>(&vs[j][2 * lane]));
-        o[0] += pj * v2.x;
-        o[1] += pj * v2.y;
-      } else if constexpr (DPL == 4) {
-        const uint2 raw = *reinterpret_cast<const uint2*>(&vs[j][4 * lane]);
-        const __half2* h2 = reinterpret_cast<const __half2*>(&raw);
-        const float2 a0 = __half22float2(h2[0]), a1 = __half22float2(h2[1]);
-        o[0] += pj * a0.x;
-        o[1] += pj * a0.y;
-        o[2] += pj * a1.x;
-        o[3] += pj * a1.y;
-      } else {
-        // rows past the live slice have p = 0; their address is clamped into the slice
-        const uint4 raw = *reinterpret_cast<const uint4*>(vb + (size_t)min(j, nk - 1) * HD + 8 * lane);
-        const __half2* h2 = reinterpret_cast<const __half2*>(&raw);
+      for (int j = 0; j < SPLIT; ++j) {
+        const float pj = ps[wave][j];
+        if constexpr (DPL == 1) {
+          o[0] += pj * __half2float(vs[j][lane]);
+        } else if constexpr (DPL == 2) {
+          const float2 v2 = __half22float2(*reinterpret_cast<const __half2*>(&vs[j][2 * lane]));
+          o[0] += pj * v2.x;
+          o[1] += pj * v2.y;
+        } else if constexpr (DPL == 4) {
+          const uint2 raw = *reinterpret_cast<const uint2*>(&vs[j][4 * lane]);
+          const __half2* h2 = reinterpret_cast<const __half2*>(&raw);
+          const float2 a0 = __half22float2(h2[0]), a1 = __half22float2(h2[1]);
+          o[0] += pj * a0.x;
+          o[1] += pj * a0.y;
+          o[2] += pj * a1.x;
+          o[3] += pj * a1.y;
+        } else {
+          // rows past the live slice have p = 0; their address is clamped into the slice
+          const uint4 raw = *reinterpret_cast<const uint4*>(vb + (size_t)min(j, nk - 1) * HD + 8 * lane);
+          const __half2* h2 = reinterpret_cast<const __half2*>(&raw);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const float2 a = __half22float2(h2[t]);
-          o[2 * t] += pj * a.x;
-          o[2 * t + 1] += pj * a.y;
+          for (int d = 0; d < 4; ++d) {
+            const float2 a = __half22float2(h2[d]);
+            o[2 * d] += pj * a.x;
+            o[2 * d + 1] += pj * a.y;
+          }
         }
       }
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) o_run[t][d] = o[d];
+      __builtin_amdgcn_wave_barrier();  // ps[wave] is rewritten by the next head or slice
     }
-    float* pr = part + ((size_t)(kvh * G + g) * nsplit + sp) * (HD + 2);
+  }
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int g = wave + 4 * t;
+    if (g >= G) break;
+    float* pr = part + ((size_t)(kvh * G + g) * nslot + cp) * (HD + 2);
     if (lane == 0) {
-      st_f<COH>(pr, m);
-      st_f<COH>(pr + 1, l);
+      st_f<COH>(pr, m_run[t]);
+      st_f<COH>(pr + 1, l_run[t]);
     }
 #pragma unroll
-    for (int t = 0; t < DPL; ++t) st_f<COH>(pr + 2 + DPL * lane + t, o[t]);
-    __builtin_amdgcn_wave_barrier();  // ps[wave] is rewritten by the next head of this wave
+    for (int d = 0; d < DPL; ++d) st_f<COH>(pr + 2 + DPL * lane + d, o_run[t][d]);
   }
-  merge_if_last<HD, COH>(part, out, counters, kvh, G, nsplit, jmin, total, wave, S.last, S.wsl);
+  merge_if_last<HD, COH>(part, out, counters, kvh, G, nslot, jmin / CK, (total + CK - 1) / CK, wave, S.last, S.wsl);
 }
 
+// Slices per chunk for a cache of `max_len` keys: one up to 2 K keys, then enough that a KV head
+// has at most ~32 chunks (fewer workgroups, and fewer partials for the merge).
+__host__ __device__ inline int attn_slices_per_chunk(int max_len) {
+  const int nsl = (max_len + SPLIT - 1) / SPLIT;
+  return nsl <= 32 ? 1 : (nsl + 31) / 32;
+}
 
 }  // namespace iek

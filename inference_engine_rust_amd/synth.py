@@ -86,6 +86,8 @@ PRESETS = {
     "c4": LlamaSpec("synthetic-mistral-7b-v0.1-long", 32, 4096, 32, 8, 14336, 32000, 8704),
     # mid-size parity model: Mistral-7B widths, 2 layers, short context
     "c2_l2": LlamaSpec("synthetic-mistral-7b-2layer", 2, 4096, 32, 8, 14336, 32000, 640),
+    # c0 with a 4096-token context: long-context decode attention (multi-slice chunks) at parity size
+    "c0_long": LlamaSpec("synthetic-mistral-tiny-long", 2, 512, 8, 2, 1408, 32000, 4096),
 }
 
 

@@ -214,3 +214,23 @@ def test_persistent_decode_step_matches_per_launch_path(gpu, mid_path, monkeypat
     for layer in (0, 1):
         np.testing.assert_array_equal(a.kv(layer, False), b.kv(layer, False))
         np.testing.assert_array_equal(a.kv(layer, True), b.kv(layer, True))
+
+
+def test_long_context_decode_matches_oracle(gpu, model_dir):
+    """A 4096-token cache makes the decode attention process several 64-key slices per workgroup
+    (running softmax across slices, fewer partials to merge); 2300 prompt tokens then 4 greedy
+    steps against the oracle."""
+    p = str(model_dir / "c0_long.gguf")
+    synth.write_llama(p, synth.preset("c0_long"), seed=0)
+    m, om = E.LoadedModel.load(p), O.Model(p)
+    prompt = synth.prompt_ids(7, 2300)
+    s, r = E.InferenceSession(m), O.Session(om)
+    s.prefill(prompt)
+    r.prefill(prompt)
+    for step in range(4):
+        lg, lr = s.logits_last_token(), r.logits()
+        assert rel_l2(lg, lr) < LOGIT_REL_L2, (step, rel_l2(lg, lr))
+        t = O.argmax(lr)
+        assert E.greedy_next_token(s) == t, f"step {step}"
+        s.decode_token(t)
+        r.decode(t)
