@@ -105,7 +105,7 @@ void launch_head_prep(float* q, float* k, float* v, int rows, int q_stride, int 
                       const int* pos_dev, int rope0, int kv0, void* kc, void* vc, bool kv_f32, int ctx,
                       hipStream_t st);
 void launch_rmsnorm_add(float* x, const float* t, const float* w, int rows, int dim, float eps, bool has_scale,
-                        float scale, hipStream_t st);
+                        float scale, hipStream_t st, float* y = nullptr);
 void launch_ple_pack(const float* proj, const float* tok, const float* norm_w, int rows, int n_layers, int pd,
                      float eps, float proj_scale, float sqrt_pd, float combine, float* out, hipStream_t st);
 void launch_ple_gate(float* go, const float* packed, int rows, int pd, int n_layers, int layer, hipStream_t st);

@@ -6,6 +6,7 @@
 //
 // Prefill (attention.rs:175-422): causal attention over the f32 K/V of the prompt (the
 // reference attends to the layer's own k_data/v_data, not the cache).
+#include <cstdlib>
 #include <type_traits>
 
 #include "attn_core.cuh"
@@ -25,18 +26,21 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
 
 // f32 KV cache variant (Gemma-4 sessions keep the reference's f32 cache: with q/k head norms
 // and a score scale of 1 the softmax is sharp enough that fp16 keys/values move the logits by
-// ~1e-2). Same grid, partials and merge as above. Score phase: lane = key; wave w sums head dims
-// [w HD/4, (w+1) HD/4) of every head of the group for its key, reading the key row straight from
-// memory, and the four partial sums meet in LDS. P.V: lane l owns head dims [DPL l, DPL l + DPL)
-// and reads V rows straight from memory (one coalesced row per key).
+// ~1e-2). Same grid, partials and merge as the fp16 kernel. The slice's K rows, then its V rows,
+// are staged through one LDS buffer in pieces of up to 256 head dims with cooperative 16-byte
+// loads (every load of a piece in flight at once); lane = key for the scores (two query heads
+// per wave), then for P.V each lane owns DPP consecutive dims of the piece.
 template <int HD>
 __global__ __launch_bounds__(256) void attn_decode_f32_kernel(const float* __restrict__ q, const float* __restrict__ kc,
                                                               const float* __restrict__ vc, float* __restrict__ part,
                                                               float* __restrict__ out, int* __restrict__ counters,
                                                               int n_heads, int n_kv, int ctx, const int* pos_dev,
                                                               int window, float scale, int nsplit) {
-  constexpr int DPL = HD / 64;
-  constexpr int DQ = HD / 4;
+  constexpr int PD = HD < 256 ? HD : 256;  // dims per staged piece
+  constexpr int NP = HD / PD;
+  constexpr int ROW = PD + 4;               // padded LDS row (floats)
+  constexpr int DPP = PD / 64;              // dims per lane per piece in P.V
+  constexpr int F4 = SPLIT * PD / 4 / 256;  // float4 per thread per piece
   const int kvh = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = n_heads / n_kv;
@@ -46,84 +50,96 @@ __global__ __launch_bounds__(256) void attn_decode_f32_kernel(const float* __res
   const int nk = j1 - j0;
   if (nk <= 0) return;  // uniform across the workgroup
   __shared__ __align__(16) float qs[8][HD];
-  __shared__ float sc[4][8][SPLIT];
+  __shared__ __align__(16) float kv[SPLIT][ROW];
   __shared__ float ps[8][SPLIT];
-  for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = q[(size_t)(kvh * G) * HD + i];
-  __syncthreads();
   const float* kb = kc + ((size_t)kvh * ctx + j0) * HD;
   const float* vb = vc + ((size_t)kvh * ctx + j0) * HD;
-  {
-    const float* krow = kb + (size_t)min(lane, nk - 1) * HD + wave * DQ;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll 2
-    for (int d = 0; d < DQ; d += 4) {
-      const float4 k4 = *reinterpret_cast<const float4*>(krow + d);
+  // cooperative piece load: element e of the piece is row e / (PD/4), float4 column e % (PD/4)
+  typedef float pf4_t __attribute__((ext_vector_type(4)));  // native vectors stay in registers
+  auto stage_piece = [&](const float* base, int p) {
+    pf4_t r[F4];
 #pragma unroll
-      for (int g = 0; g < 8; ++g) {
-        if (g < G) {
-          const float4 q4 = *reinterpret_cast<const float4*>(&qs[g][wave * DQ + d]);
-          acc[g] += q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
+    for (int u = 0; u < F4; ++u) {
+      const int e = tid + 256 * u, row = min(e / (PD / 4), nk - 1), c4 = e % (PD / 4);
+      r[u] = *reinterpret_cast<const pf4_t*>(base + (size_t)row * HD + p * PD + 4 * c4);
+    }
+    __syncthreads();  // the previous piece's readers are done
+#pragma unroll
+    for (int u = 0; u < F4; ++u) {
+      const int e = tid + 256 * u, row = e / (PD / 4), c4 = e % (PD / 4);
+      *reinterpret_cast<pf4_t*>(&kv[row][4 * c4]) = r[u];
+    }
+    __syncthreads();
+  };
+  for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = q[(size_t)(kvh * G) * HD + i];
+  float sc[2] = {0.f, 0.f};
+  for (int p = 0; p < NP; ++p) {
+    stage_piece(kb, p);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int g = wave + 4 * t;
+      if (g < G) {
+        float acc = 0.f;
+#pragma unroll 8
+        for (int d = 0; d < PD; d += 4) {
+          const float4 k4 = *reinterpret_cast<const float4*>(&kv[lane][d]);
+          const float4 q4 = *reinterpret_cast<const float4*>(&qs[g][p * PD + d]);
+          acc += q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
         }
+        sc[t] += acc;
       }
     }
-#pragma unroll
-    for (int g = 0; g < 8; ++g)
-      if (g < G) sc[wave][g][lane] = acc[g];
   }
-  __syncthreads();
   const bool valid = lane < nk;
-  for (int g = wave; g < G; g += 4) {
-    const float s = valid ? ((sc[0][g][lane] + sc[1][g][lane]) + (sc[2][g][lane] + sc[3][g][lane])) * scale
-                          : -INFINITY;
-    const float m = wave_max(s);
-    const float p = valid ? expf(s - m) : 0.f;
-    const float l = wave_sum(p);
-    ps[g][lane] = p;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    float o[DPL];
+  float m[2], l[2];
 #pragma unroll
-    for (int t = 0; t < DPL; ++t) o[t] = 0.f;
-    // 8 V rows in flight per batch; rows past the live slice have p = 0 and a clamped address
-    constexpr int NV = DPL >= 8 ? 4 : 8;  // V rows per batch
-#pragma unroll 1
-    for (int j0 = 0; j0 < SPLIT; j0 += NV) {
-      float vr[NV][DPL];
+  for (int t = 0; t < 2; ++t) {
+    const int g = wave + 4 * t;
+    if (g < G) {
+      const float s = valid ? sc[t] * scale : -INFINITY;
+      m[t] = wave_max(s);
+      const float pr = valid ? expf(s - m[t]) : 0.f;
+      l[t] = wave_sum(pr);
+      ps[g][lane] = pr;
+    }
+  }
+  float o[2][NP][DPP];
 #pragma unroll
-      for (int u = 0; u < NV; ++u) {
-        const float* src = vb + (size_t)min(j0 + u, nk - 1) * HD + DPL * lane;
-        if constexpr (DPL == 1) {
-          vr[u][0] = src[0];
-        } else if constexpr (DPL == 2) {
-          const float2 t2 = *reinterpret_cast<const float2*>(src);
-          vr[u][0] = t2.x;
-          vr[u][1] = t2.y;
-        } else {
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int t = 0; t < DPL; t += 4) {
-            const float4 t4 = *reinterpret_cast<const float4*>(src + t);
-            vr[u][t] = t4.x;
-            vr[u][t + 1] = t4.y;
-            vr[u][t + 2] = t4.z;
-            vr[u][t + 3] = t4.w;
-          }
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int e = 0; e < DPP; ++e) o[t][p][e] = 0.f;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    stage_piece(vb, p);  // its first barrier also publishes ps
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int g = wave + 4 * t;
+      if (g < G) {
+#pragma unroll 8
+        for (int j = 0; j < SPLIT; ++j) {
+          const float pj = ps[g][j];
+#pragma unroll
+          for (int e = 0; e < DPP; ++e) o[t][p][e] += pj * kv[j][DPP * lane + e];
         }
       }
+    }
+  }
 #pragma unroll
-      for (int u = 0; u < NV; ++u) {
-        const float pj = ps[g][j0 + u];
-#pragma unroll
-        for (int t = 0; t < DPL; ++t) o[t] += pj * vr[u][t];
+  for (int t = 0; t < 2; ++t) {
+    const int g = wave + 4 * t;
+    if (g < G) {
+      float* pr = part + ((size_t)(kvh * G + g) * nsplit + sp) * (HD + 2);
+      if (lane == 0) {
+        pr[0] = m[t];
+        pr[1] = l[t];
       }
-    }
-    float* pr = part + ((size_t)(kvh * G + g) * nsplit + sp) * (HD + 2);
-    if (lane == 0) {
-      pr[0] = m;
-      pr[1] = l;
-    }
 #pragma unroll
-    for (int t = 0; t < DPL; ++t) pr[2 + DPL * lane + t] = o[t];
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int e = 0; e < DPP; ++e) pr[2 + p * PD + DPP * lane + e] = o[t][p][e];
+    }
   }
   __shared__ int last;
   __shared__ float wsl[4 * 256];
@@ -139,7 +155,12 @@ static void attn_decode_hd(dim3 grid, hipStream_t st, const float* q, const void
                        out, counters, n_heads, n_kv, ctx, pos_dev, window, scale, nsplit);
   } else {
     // fp16 cache: chunks of spc slices; one partial slot per chunk
-    const int spc = attn_slices_per_chunk(nsplit * SPLIT);
+    static int target = -1;
+    if (target < 0) {
+      const char* e = getenv("IEK_ATTN_CHUNKS");
+      target = e ? std::max(1, atoi(e)) : 32;
+    }
+    const int spc = attn_slices_per_chunk(nsplit * SPLIT, target);
     const int nchunk = (nsplit + spc - 1) / spc;
     hipLaunchKernelGGL(attn_decode_kernel<HD>, dim3(grid.x, nchunk), dim3(256), 0, st, q, (const __half*)kc,
                        (const __half*)vc, part, out, counters, n_heads, n_kv, ctx, pos_dev, window, scale, nchunk,

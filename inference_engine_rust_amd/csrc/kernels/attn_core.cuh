@@ -269,11 +269,12 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
   merge_if_last<HD, COH>(part, out, counters, kvh, G, nslot, jmin / CK, (total + CK - 1) / CK, wave, S.last, S.wsl);
 }
 
-// Slices per chunk for a cache of `max_len` keys: one up to 2 K keys, then enough that a KV head
-// has at most ~32 chunks (fewer workgroups, and fewer partials for the merge).
-__host__ __device__ inline int attn_slices_per_chunk(int max_len) {
+// Slices per chunk for a cache of `max_len` keys: one up to `target` slices per KV head, then
+// enough that a KV head has at most ~`target` chunks (fewer workgroups, and fewer partials for
+// the merge).
+__host__ __device__ inline int attn_slices_per_chunk(int max_len, int target = 32) {
   const int nsl = (max_len + SPLIT - 1) / SPLIT;
-  return nsl <= 32 ? 1 : (nsl + 31) / 32;
+  return nsl <= target ? 1 : (nsl + target - 1) / target;
 }
 
 }  // namespace iek

@@ -217,12 +217,25 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmQArgs g) {
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int M = g.M, K = g.K, nk = K / QBK, nsb = K / QK_K;
   const int mtiles = (M + BM - 1) / BM;
-  int tile = blockIdx.x;
-  if (g.xcd_remap) {
-    const int per = gridDim.x / 8;
-    tile = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  // Workgroup b runs on XCD b % 8. xcd_remap 2 (mtiles % 8 == 0): XCD x takes the M tiles
+  // m % 8 == x and every N tile, so its activation rows stay resident in its L2 while the
+  // weights stream (each XCD reads the weights once; the activation is read once per XCD instead
+  // of once per N tile). xcd_remap 1: XCD x takes a contiguous run of tiles (all M tiles of its
+  // N tiles share the weight tile in L2).
+  int mt, ntile;
+  if (g.xcd_remap == 2) {
+    const int x = blockIdx.x % 8, j = blockIdx.x / 8, mpx = mtiles / 8;
+    mt = x + 8 * (j % mpx);
+    ntile = j / mpx;
+  } else {
+    int tile = blockIdx.x;
+    if (g.xcd_remap == 1) {
+      const int per = gridDim.x / 8;
+      tile = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    }
+    mt = tile % mtiles;
+    ntile = tile / mtiles;
   }
-  const int mt = tile % mtiles, ntile = tile / mtiles;
   const int s = ntile < g.tile_start[1] ? 0 : (ntile < g.tile_start[2] ? 1 : 2);
   const uint8_t* w = s == 0 ? g.w[0] : (s == 1 ? g.w[1] : g.w[2]);
   float* out = s == 0 ? g.out[0] : (s == 1 ? g.out[1] : g.out[2]);
@@ -412,7 +425,12 @@ static void gemm_q_launch(GemmQArgs g, hipStream_t st) {
   for (int i = g.nseg; i <= 3; ++i) g.tile_start[i] = t;
   const int mtiles = (g.M + BM - 1) / BM;
   const int tiles = mtiles * t;
-  g.xcd_remap = tiles % 8 == 0 ? 1 : 0;
+  static int mode = -1;
+  if (mode < 0) {
+    const char* e = getenv("IEK_GEMM_XCD");  // 1: N-tile runs per XCD (tuning)
+    mode = e ? atoi(e) : 2;
+  }
+  g.xcd_remap = (mode == 2 && mtiles % 8 == 0) ? 2 : (tiles % 8 == 0 ? 1 : 0);
   hipLaunchKernelGGL((gemm_q_kernel<DT, BM, BN>), dim3(tiles), dim3(256), 0, st, g);
 }
 

@@ -120,15 +120,17 @@ void launch_head_prep(float* q, float* k, float* v, int rows, int q_stride, int 
 #undef IEK_HP
 }
 
-// x[r] = (x[r] + (t[r] * w) / rms(t[r])) * scale, one 256-thread workgroup per row; scale == 1
-// skips the multiply (the reference applies no scale when the layer has none).
-__global__ __launch_bounds__(256) void rmsnorm_add_kernel(float* __restrict__ x, const float* __restrict__ t,
+// y[r] = (x[r] + (t[r] * w) / rms(t[r])) * scale (y = x when no output is given), one 256-thread
+// workgroup per row; has_scale false skips the multiply (the reference applies no scale when the
+// layer has none).
+__global__ __launch_bounds__(256) void rmsnorm_add_kernel(const float* x, const float* __restrict__ t,
                                                           const float* __restrict__ w, int dim, float eps,
-                                                          float scale, int has_scale) {
+                                                          float scale, int has_scale, float* y) {
 #pragma clang fp contract(off)
   __shared__ float sh[4];
   const float* tr = t + (size_t)blockIdx.x * dim;
-  float* xr = x + (size_t)blockIdx.x * dim;
+  const float* xr = x + (size_t)blockIdx.x * dim;
+  float* yr = y + (size_t)blockIdx.x * dim;
   float ss = 0.f;
   for (int i = threadIdx.x; i < dim; i += 256) ss += tr[i] * tr[i];
   ss = wave_sum(ss);
@@ -137,16 +139,17 @@ __global__ __launch_bounds__(256) void rmsnorm_add_kernel(float* __restrict__ x,
   ss = (sh[0] + sh[1]) + (sh[2] + sh[3]);
   const float rms = rms_value(ss, dim, eps);
   for (int i = threadIdx.x; i < dim; i += 256) {
-    float y = xr[i] + (tr[i] * w[i]) / rms;
-    if (has_scale) y = y * scale;
-    xr[i] = y;
+    float v = xr[i] + (tr[i] * w[i]) / rms;
+    if (has_scale) v = v * scale;
+    yr[i] = v;
   }
 }
 
 void launch_rmsnorm_add(float* x, const float* t, const float* w, int rows, int dim, float eps, bool has_scale,
-                        float scale, hipStream_t st) {
+                        float scale, hipStream_t st, float* y) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL(rmsnorm_add_kernel, dim3(rows), dim3(256), 0, st, x, t, w, dim, eps, scale, has_scale ? 1 : 0);
+  hipLaunchKernelGGL(rmsnorm_add_kernel, dim3(rows), dim3(256), 0, st, x, t, w, dim, eps, scale, has_scale ? 1 : 0,
+                     y ? y : x);
 }
 
 // PLE packing (gemma4_ple.rs:27-109) for one (row, layer) per workgroup:

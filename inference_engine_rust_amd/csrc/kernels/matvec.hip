@@ -188,7 +188,7 @@ void launch_mv(int dt, MvArgs a, hipStream_t st) {
   // K-quants take the int8-staged x (v_dot4) path when x and the norm weight are 16-byte aligned
   // and every 32-element block fits the two-blocks-per-thread staging; IEK_MV_F32=1 keeps f32.
   const bool force_f32 = !mv_int8_staging();
-  const bool i8 = fast && !force_f32 && a.K <= 16384 &&
+  const bool i8 = fast && !force_f32 && a.K <= 16384 && !a.pre_t &&
                   (!a.norm_w || (reinterpret_cast<uintptr_t>(a.norm_w) % 16) == 0);
   if (fast) {
     // Two rows per wave: more rows per wave spill the prefetch registers.

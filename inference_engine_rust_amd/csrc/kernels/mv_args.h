@@ -13,6 +13,7 @@ enum MvEpilogue : int {
   EPI_QKV = 3,     // segments q, k, v: RoPE on q and k pairs, q -> out[0], k/v -> fp16 KV cache at *pos
   EPI_ARGMAX = 4,  // logits -> out[0] (optional soft cap), atomicMax of packed (value, first index)
   EPI_GEGLU = 5,   // w[0] = gate, w[1] = up: out[0][n] = gelu_tanh(gate.x) * (up.x)
+  EPI_GELU_MUL = 6,  // out[0][n] = gelu_tanh(dot) * mulv[n]
 };
 
 struct MvArgs {
@@ -38,6 +39,17 @@ struct MvArgs {
   int* amax_flag;
   float softcap;  // <= 0: none
   int* pos_inc;   // when set, one thread adds 1 after the launch's work is issued (end of a decode step)
+  // EPI_GELU_MUL
+  const float* mulv;
+  // Optional residual update ahead of the staging (f32-staged traits and the generic path):
+  //   y = (x + (pre_t * pre_w) / rms(pre_t)) [* pre_scale]
+  // the launch then uses y as its input x (RMS-normalised again when norm_w is set), and workgroup
+  // 0 writes y to pre_out (a buffer other than x and pre_t).
+  const float* pre_t;
+  const float* pre_w;
+  float* pre_out;
+  float pre_scale;
+  int pre_has_scale;
 };
 
 __host__ __device__ inline int seg_of(const MvArgs& a, int row) {

@@ -91,7 +91,55 @@ struct Lds {
   uint8_t* wb;   // per-wave staging of raw weight bytes (coalesced-load traits only)
 };
 
+// Block-wide sum for the 256-thread matvec workgroups.
+IEK_DEV float block_sum_mv(float v, float* red) {
+  v = wave_sum(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// Staging with the residual update in front (a.pre_t set; f32 staging): y = x + rmsnorm(pre_t,
+// pre_w) [* pre_scale] with the reference's roundings (rmsnorm.rs:44-47, residual_add.rs:3-12,
+// ffn.rs:242-278), then the launch's own RMSNorm of y when norm_w is set. Workgroup 0 stores y.
+IEK_DEV void stage_pre(const MvArgs& a, const Lds& L, int pos) {
+  __shared__ float red[4];
+  const int K = a.K, tid = threadIdx.x;
+  float st = 0.f;
+  for (int i = tid; i < K; i += 256) {
+    const float t = a.pre_t[i];
+    st += t * t;
+  }
+  const float rms_t = rms_of(block_sum_mv(st, red), K, a.eps);
+  float sy = 0.f;
+  for (int i = tid; i < K; i += 256) {
+    float y = a.x[i] + div_rn(mul_rn(a.pre_t[i], a.pre_w[i]), rms_t);
+    if (a.pre_has_scale) y = mul_rn(y, a.pre_scale);
+    if (blockIdx.x == 0) a.pre_out[i] = y;
+    sy += y * y;
+    L.x[i] = a.norm_w ? mul_rn(y, a.norm_w[i]) : y;
+  }
+  if (a.norm_w) {
+    const float rms = rms_of(block_sum_mv(sy, red), K, a.eps);
+    for (int i = tid; i < K; i += 256) L.x[i] = div_rn(L.x[i], rms);
+  }
+  if (a.epi == EPI_RESID) {
+    const int N = a.n[0];
+    for (int i = tid; i < N; i += 256) L.res[i] = a.resid[i];
+  }
+  if (a.epi == EPI_QKV) {
+    for (int i = tid; i < 2 * a.npairs; i += 256) L.rope[i] = a.rope_cs[(size_t)pos * a.npairs * 2 + i];
+  }
+  __syncthreads();
+  __builtin_amdgcn_s_waitcnt(0);
+}
+
 IEK_DEV void stage(const MvArgs& a, const Lds& L, int pos) {
+  if (a.pre_t) {
+    stage_pre(a, L, pos);
+    return;
+  }
   const int K = a.K, tid = threadIdx.x;
   const bool vec = (K & 3) == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
                    (!a.norm_w || (reinterpret_cast<uintptr_t>(a.norm_w) & 15) == 0);
@@ -409,6 +457,7 @@ IEK_DEV void epilogue(const MvArgs& a, const Lds& L, int s, int lr0, float (&acc
       if (lane == r) v = acc[r];
     const int n = lr0 + lane;
     if (a.epi == EPI_RESID) v = L.res[n] + v;
+    if (a.epi == EPI_GELU_MUL) v = gelu_tanh_dev(v) * a.mulv[n];
     st_f<COH>(seg_out(a, s) + n, v);
   }
 }

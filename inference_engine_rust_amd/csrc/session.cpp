@@ -72,6 +72,7 @@ Session::Session(Model* m) : m_(m) {
     hdmax = std::max(hdmax, L.head_dim);
   }
   xdec_ = dev_alloc<float>(H_);
+  xdec2_ = dev_alloc<float>(H_);
   xndec_ = dev_alloc<float>(std::max(H_, qmax));
   qd_ = dev_alloc<float>(qmax);
   kd_ = dev_alloc<float>(kvmax);
@@ -120,7 +121,7 @@ Session::~Session() {
                   (void*)d_step_, (void*)d_flags_, (void*)d_tok_, (void*)d_ids_, (void*)d_gen_, (void*)d_key_,
                   (void*)d_flag_, (void*)d_cnt_, (void*)xs_, (void*)xsum_, kv_blob_, (void*)ple_tok_,
                   (void*)ple_proj_, (void*)ple_pack_, (void*)ple_tokd_, (void*)ple_projd_, (void*)ple_packd_,
-                  (void*)d_bar_, (void*)d_err_, step_layers_, (void*)d_trace_})
+                  (void*)d_bar_, (void*)d_err_, step_layers_, (void*)d_trace_, (void*)xdec2_})
     dev_free(p);
   if (st_) (void)hipStreamDestroy(st_);
 }
@@ -604,7 +605,8 @@ void Session::layer_prefill_gemma(int li, int M) {
 // One decode-step matvec over up to three weights sharing x (optionally RMS-normalised on the
 // way in). Uses the regrouped copies when every weight has one of the same layout.
 static void mv_multi(const DevTensor* const* ws, float* const* outs, int nseg, const float* x, int K,
-                     const float* norm_w, float eps, int epi, hipStream_t st) {
+                     const float* norm_w, float eps, int epi, hipStream_t st, const ResidUpdate* pre = nullptr,
+                     float* pre_out = nullptr, const float* mulv = nullptr) {
   int dt0 = -1;
   const void* wp[3];
   bool same = true;
@@ -624,7 +626,7 @@ static void mv_multi(const DevTensor* const* ws, float* const* outs, int nseg, c
       native.dev_r = nullptr;
       one[0] = &native;
       float* o[1] = {outs[i]};
-      mv_multi(one, o, 1, x, K, norm_w, eps, epi, st);
+      mv_multi(one, o, 1, x, K, norm_w, eps, epi, st, pre, pre_out, mulv);
     }
     return;
   }
@@ -640,12 +642,24 @@ static void mv_multi(const DevTensor* const* ws, float* const* outs, int nseg, c
   a.eps = eps;
   a.K = K;
   a.epi = epi;
+  a.mulv = mulv;
+  if (pre && pre->t) {
+    a.pre_t = pre->t;
+    a.pre_w = pre->w;
+    a.pre_out = pre_out;
+    a.pre_scale = pre->scale;
+    a.pre_has_scale = pre->has_scale ? 1 : 0;
+  }
   launch_mv(dt0, a, st);
 }
 
 // decode_layer_block for Gemma-4 (block.rs:50-89), same sub-steps as layer_prefill_gemma for one
-// token at the device position (*d_pos_).
-void Session::layer_decode_gemma(int li) {
+// token at the device position (*d_pos_). Each post-norm residual update
+//   x <- (x + rmsnorm(t, w)) [* layer scale]
+// is carried into the staging of the next matvec that reads x (`pend` -> the launch's pre-op),
+// which writes the updated x to the other of the two residual buffers; `xr` tracks which one holds
+// the current residual.
+void Session::layer_decode_gemma(int li, float*& xr, ResidUpdate& pend) {
   const Config& c = m_->cfg;
   const LayerSpec& S = c.layers[li];
   const LayerTensors& L = m_->layers[li];
@@ -654,28 +668,41 @@ void Session::layer_decode_gemma(int li) {
   const bool borrow = S.kv_borrow >= 0;
   if (!L.attn_post_norm.present()) fail(ST_MODEL, "Gemma 4: missing post_attention_norm");
   if (!L.ffn_post_norm.present()) fail(ST_MODEL, "Gemma 4: missing post_ffw_norm");
+  auto other = [&]() { return xr == xdec_ ? xdec2_ : xdec_; };
+  // matvec over the current residual, applying the pending update first (then it is current)
+  auto mv_x = [&](const DevTensor* const* ws, float* const* outs, int nseg, const float* norm_w, int epi,
+                  const float* mulv) {
+    if (pend.t) {
+      float* nx = other();
+      mv_multi(ws, outs, nseg, xr, H_, norm_w, eps, epi, st_, &pend, nx, mulv);
+      xr = nx;
+      pend = ResidUpdate{};
+    } else {
+      mv_multi(ws, outs, nseg, xr, H_, norm_w, eps, epi, st_, nullptr, nullptr, mulv);
+    }
+  };
   {
     const DevTensor* ws[3] = {&L.wq, &L.wk, &L.wv};
     float* outs[3] = {qd_, kd_, vd_};
-    mv_multi(ws, outs, borrow ? 1 : 3, xdec_, H_, (const float*)L.attn_norm.dev, eps, EPI_STORE, st_);
+    mv_x(ws, outs, borrow ? 1 : 3, (const float*)L.attn_norm.dev, EPI_STORE, nullptr);
   }
   const RopeTable& rt = m_->rope_tables[L.rope_table];
   launch_head_prep(qd_, kd_, vd_, 1, qd, kvd, c.n_heads, borrow ? 0 : c.n_kv_heads, hd,
                    L.q_norm.present() ? (const float*)L.q_norm.dev : nullptr,
                    L.k_norm.present() ? (const float*)L.k_norm.dev : nullptr, eps, true, rt.dev, S.rotary_dim / 2,
                    d_pos_, 0, 0, borrow ? nullptr : kc_[li], borrow ? nullptr : vc_[li], kv_f32_, ctx_, st_);
-  launch_attn_decode(qd_, kc_[li], vc_[li], kv_f32_, attd_, part_, d_cnt_, c.n_heads, c.n_kv_heads, hd, ctx_, d_pos_, S.window,
-                     1.0f, ctx_, st_);
+  launch_attn_decode(qd_, kc_[li], vc_[li], kv_f32_, attd_, part_, d_cnt_, c.n_heads, c.n_kv_heads, hd, ctx_, d_pos_,
+                     S.window, 1.0f, ctx_, st_);
   {
     const DevTensor* ws[1] = {&L.wo};
     float* outs[1] = {tmpd_};
     mv_multi(ws, outs, 1, attd_, qd, nullptr, eps, EPI_STORE, st_);
   }
-  launch_rmsnorm_add(xdec_, tmpd_, (const float*)L.attn_post_norm.dev, 1, H_, eps, false, 1.f, st_);
+  pend = ResidUpdate{tmpd_, (const float*)L.attn_post_norm.dev, false, 1.f};
   {
     const DevTensor* ws[2] = {&L.gate, &L.up};
     float* outs[2] = {actd_, nullptr};
-    mv_multi(ws, outs, 2, xdec_, H_, (const float*)L.ffn_norm.dev, eps, EPI_GEGLU, st_);
+    mv_x(ws, outs, 2, (const float*)L.ffn_norm.dev, EPI_GEGLU, nullptr);
   }
   {
     const DevTensor* ws[1] = {&L.down};
@@ -683,25 +710,23 @@ void Session::layer_decode_gemma(int li) {
     mv_multi(ws, outs, 1, actd_, S.ffn_dim, nullptr, eps, EPI_STORE, st_);
   }
   const bool ple = c.ple_dim > 0;
-  launch_rmsnorm_add(xdec_, tmpd_, (const float*)L.ffn_post_norm.dev, 1, H_, eps, !ple && L.has_out_scale,
-                     L.out_scale_value, st_);
+  pend = ResidUpdate{tmpd_, (const float*)L.ffn_post_norm.dev, !ple && L.has_out_scale, L.out_scale_value};
   if (ple) {
     const int pd = c.ple_dim;
     if (!L.ple_gate.present() || !L.ple_proj.present() || !L.ple_post_norm.present())
       fail(ST_MODEL, "PLE: missing inp_gate / proj / post_norm");
     {
+      // gelu_tanh(x . inp_gate) * this layer's per-layer input (ffn.rs:196-205) in the epilogue
       const DevTensor* ws[1] = {&L.ple_gate};
       float* outs[1] = {actd_};
-      mv_multi(ws, outs, 1, xdec_, H_, nullptr, eps, EPI_STORE, st_);
+      mv_x(ws, outs, 1, nullptr, EPI_GELU_MUL, ple_packd_ + (size_t)li * pd);
     }
-    launch_ple_gate(actd_, ple_packd_, 1, pd, c.n_layers, li, st_);
     {
       const DevTensor* ws[1] = {&L.ple_proj};
       float* outs[1] = {tmpd_};
       mv_multi(ws, outs, 1, actd_, pd, nullptr, eps, EPI_STORE, st_);
     }
-    launch_rmsnorm_add(xdec_, tmpd_, (const float*)L.ple_post_norm.dev, 1, H_, eps, L.has_out_scale,
-                       L.out_scale_value, st_);
+    pend = ResidUpdate{tmpd_, (const float*)L.ple_post_norm.dev, L.has_out_scale, L.out_scale_value};
   }
 }
 
@@ -752,7 +777,12 @@ void Session::decode_body() {
   launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, d_tok_, 1, c.embed_scale, xdec_, st_);
   if (gemma_) {
     embed_ple(d_tok_, 1, xdec_, nullptr, ple_tokd_, ple_projd_, ple_packd_);
-    for (int li = 0; li < c.n_layers; ++li) layer_decode_gemma(li);
+    float* xr = xdec_;
+    ResidUpdate pend{};
+    for (int li = 0; li < c.n_layers; ++li) layer_decode_gemma(li, xr, pend);
+    // the last layer's update lands in xdec_, where the LM head and the next step read the state
+    if (pend.t) launch_rmsnorm_add(xr, pend.t, pend.w, 1, H_, c.rms_eps, pend.has_scale, pend.scale, st_, xdec_);
+    else if (xr != xdec_) launch_copy_f32(xr, xdec_, H_, st_);
     launch_add_int(d_pos_, 1, st_);
   } else if (step_layers_) {
     launch_decode_step(step_layers_, c.n_layers, c.n_heads, c.n_kv_heads, c.layers[0].head_dim, ctx_,

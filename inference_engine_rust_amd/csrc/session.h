@@ -8,6 +8,15 @@
 
 namespace iek {
 
+// A pending residual update x <- (x + rmsnorm(t, w)) [* scale] (Gemma-4 post-norms and layer
+// output scale), applied by the staging of the next matvec that reads x.
+struct ResidUpdate {
+  const float* t = nullptr;
+  const float* w = nullptr;
+  bool has_scale = false;
+  float scale = 1.f;
+};
+
 class Session {
  public:
   explicit Session(Model* m);
@@ -44,7 +53,7 @@ class Session {
   const __half* split_rows(const float* a, int M, int K);
   void embed_ple(const uint32_t* d_ids, int n, const float* x, const __half* xs, float* tok, float* proj, float* pack);
   void layer_prefill_gemma(int li, int M);
-  void layer_decode_gemma(int li);
+  void layer_decode_gemma(int li, float*& xr, ResidUpdate& pend);
   void decode_body();           // embed(d_tok) + every layer + pos++; no host sync
   void logits_body(bool argmax);  // final norm + LM head (+ softcap) into logits_
   void argmax_body(bool record);
@@ -64,7 +73,7 @@ class Session {
   float *g_ = nullptr, *u_ = nullptr, *act_ = nullptr, *tmp_ = nullptr;
   __half* xs_ = nullptr;  // fp16 (hi, lo) split of the current prefill GEMM input
   float* xsum_ = nullptr;  // its per-32 row sums (Q4_K min term)
-  float *xdec_ = nullptr, *xndec_ = nullptr, *qd_ = nullptr, *kd_ = nullptr, *vd_ = nullptr, *attd_ = nullptr;
+  float *xdec_ = nullptr, *xdec2_ = nullptr, *xndec_ = nullptr, *qd_ = nullptr, *kd_ = nullptr, *vd_ = nullptr, *attd_ = nullptr;
   float *actd_ = nullptr, *logits_ = nullptr, *part_ = nullptr, *tmpd_ = nullptr;
   // per-layer embeddings (Gemma-4): token rows, model projection and packed inputs, [rows][L*pd]
   float *ple_tok_ = nullptr, *ple_proj_ = nullptr, *ple_pack_ = nullptr;
