@@ -56,36 +56,6 @@ IEK_DEV uint32_t hpack(_Float16 a, _Float16 b) {
 template <int DT>
 struct QDeq;
 
-template <>
-struct QDeq<DT_Q4K> {
-  static constexpr int PERIOD = 8;  // stages per d block
-  static constexpr bool LO = false;
-  uint4 hdr;
-  uint2 qs;
-  IEK_DEV void load(const uint8_t* w, size_t row_bytes, int n, int k0, int nsb) {
-    const uint8_t* blk = w + (size_t)n * row_bytes + (size_t)(k0 >> 8) * Q4K_BYTES;
-    const int e = k0 & 255, g = e >> 6, l0 = e & 31;
-    hdr = *reinterpret_cast<const uint4*>(blk);
-    qs = *reinterpret_cast<const uint2*>(blk + 16 + 32 * g + l0);
-  }
-  IEK_DEV void decode(int k0, uint4& hi, uint4& lo, float& d, float& dm) const {
-#pragma clang fp contract(off)
-    const int e = k0 & 255, sb = e >> 5, nib = sb & 1;
-    d = half_bits_to_float(hdr.x);
-    const float dmin = half_bits_to_float(hdr.x >> 16);
-    float sc, m;
-    scale_min_k4(sb, hdr.y, hdr.z, hdr.w, &sc, &m);
-    dm = dmin * m;
-    const uint32_t isc = (uint32_t)sc;
-    _Float16 h[8];
-    const uint32_t w2[2] = {qs.x, qs.y};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) h[i] = (_Float16)(int)(((w2[i >> 2] >> (8 * (i & 3) + 4 * nib)) & 0xFu) * isc);
-    hi = make_uint4(hpack(h[0], h[1]), hpack(h[2], h[3]), hpack(h[4], h[5]), hpack(h[6], h[7]));
-    lo = make_uint4(0, 0, 0, 0);
-  }
-};
-
 // Q6_K weights from the regrouped per-row layout (DT_Q6K_R: lane chunks of [ql 0/2 | ql 1/3 | qh]
 // 16 bytes each, then per-chunk scale dwords, then d per superblock; see matvec.hip).
 template <>
@@ -104,10 +74,9 @@ struct QDeq<DT_Q6K_R> {
     sc = *reinterpret_cast<const uint32_t*>(row + (size_t)nsb * 192 + 16 * j + 4 * kc);
     d16 = *reinterpret_cast<const uint16_t*>(row + (size_t)nsb * 208 + 2 * j);
   }
-  IEK_DEV void decode(int k0, uint4& hi, uint4& lo, float& d, float& dm) const {
+  IEK_DEV void decode(int k0, uint4& hi, uint4& lo, float& d) const {
     const int qd = ((k0 & 255) & 127) >> 5;
     d = half_bits_to_float(d16);
-    dm = 0.f;
     const int isc = (int)(int8_t)((sc >> (8 * qd)) & 0xFF);
     const uint32_t lw[2] = {ql.x, ql.y}, hw[2] = {qh.x, qh.y};
     _Float16 h[8], l[8];
@@ -145,10 +114,9 @@ struct QDeq<DT_Q6K> {
     sd = ((si & 1) ? (uint32_t)(s2 >> 8) : (uint32_t)(s2 & 0xFF)) |
          ((uint32_t)*reinterpret_cast<const uint16_t*>(blk + 208) << 16);
   }
-  IEK_DEV void decode(int k0, uint4& hi, uint4& lo, float& d, float& dm) const {
+  IEK_DEV void decode(int k0, uint4& hi, uint4& lo, float& d) const {
     const int quarter = ((k0 & 255) & 127) >> 5;
     d = half_bits_to_float(sd >> 16);
-    dm = 0.f;
     const int isc = (int)(int8_t)(sd & 0xFF);
     _Float16 h[8], l[8];
 #pragma unroll
@@ -176,9 +144,8 @@ struct QDeq<DT_Q8_0> {
     for (int i = 0; i < 4; ++i) q[i] = p[i];
     d16 = *reinterpret_cast<const uint16_t*>(blk);
   }
-  IEK_DEV void decode(int, uint4& hi, uint4& lo, float& d, float& dm) const {
+  IEK_DEV void decode(int, uint4& hi, uint4& lo, float& d) const {
     d = half_bits_to_float(d16);
-    dm = 0.f;
     _Float16 h[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) h[i] = (_Float16)(int)(int8_t)((q[i >> 1] >> (8 * (i & 1))) & 0xFFu);
@@ -187,8 +154,11 @@ struct QDeq<DT_Q8_0> {
   }
 };
 
-// Per-32 row sums of the activation (Q4_K's min term): xs[m * (K/32) + b] = sum of a[m, 32b..].
-__global__ __launch_bounds__(256) void block_sums_kernel(const float* __restrict__ a, size_t nb, float* __restrict__ xs) {
+// Per-32 row sums of the activation (Q4_K's min term), summed in f32 and stored as an fp16 pair
+// over two planes of nb halves: hi[m * (K/32) + b] + lo[...] = sum of a[m, 32b .. 32b+31].
+__global__ __launch_bounds__(256) void block_sums_kernel(const float* __restrict__ a, size_t nb,
+                                                         _Float16* __restrict__ hi, _Float16* __restrict__ lo) {
+#pragma clang fp contract(off)
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= nb) return;
   const float4* p = reinterpret_cast<const float4*>(a + 32 * i);
@@ -198,7 +168,9 @@ __global__ __launch_bounds__(256) void block_sums_kernel(const float* __restrict
     const float4 v = p[t];
     s += (v.x + v.y) + (v.z + v.w);
   }
-  xs[i] = s;
+  const _Float16 h = (_Float16)s;
+  hi[i] = h;
+  lo[i] = (_Float16)(s - (float)h);
 }
 
 template <int DT, int BM, int BN>
@@ -212,7 +184,7 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmQArgs g) {
   __shared__ __align__(16) _Float16 as_l[2][BM][QROW];
   __shared__ __align__(16) _Float16 bs_h[2][BN][QROW];
   __shared__ __align__(16) _Float16 bs_l[LO ? 2 : 1][BN][QROW];
-  __shared__ float sd[2][BN], sdm[2][BN], sxs[2][BM];
+  __shared__ float sd[2][BN];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int M = g.M, K = g.K, nk = K / QBK, nsb = K / QK_K;
@@ -253,7 +225,6 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmQArgs g) {
   constexpr int D = 4;
   struct Slot {
     qu4_t arh[AU], arl[AU];
-    float axs;
     QDeq<DT> braw[BR];
   };
   Slot ring[D];
@@ -267,7 +238,6 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmQArgs g) {
       sl.arh[u] = *reinterpret_cast<const qu4_t*>(g.xh + off);
       sl.arl[u] = *reinterpret_cast<const qu4_t*>(g.xl + off);
     }
-    if (DT == DT_Q4K && tid < BM) sl.axs = g.xs[(size_t)min(m0 + tid, M - 1) * (K / 32) + kt];
 #pragma unroll
     for (int r = 0; r < BR; ++r) sl.braw[r].load(w, row_bytes, b_n[r], k0 + 8 * b_run, nsb);
   };
@@ -278,19 +248,15 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmQArgs g) {
       *reinterpret_cast<qu4_t*>(&as_h[buf][row][8 * c8]) = sl.arh[u];
       *reinterpret_cast<qu4_t*>(&as_l[buf][row][8 * c8]) = sl.arl[u];
     }
-    if (DT == DT_Q4K && tid < BM) sxs[buf][tid] = sl.axs;
 #pragma unroll
     for (int r = 0; r < BR; ++r) {
       uint4 hi, lo;
-      float d, dm;
-      sl.braw[r].decode(kt * QBK + 8 * b_run, hi, lo, d, dm);
+      float d;
+      sl.braw[r].decode(kt * QBK + 8 * b_run, hi, lo, d);
       const int row = b_row + 64 * r;
       *reinterpret_cast<uint4*>(&bs_h[buf][row][8 * b_run]) = hi;
       if constexpr (LO) *reinterpret_cast<uint4*>(&bs_l[LO ? buf : 0][row][8 * b_run]) = lo;
-      if (b_run == 0) {
-        sd[buf][row] = d;
-        sdm[buf][row] = dm;
-      }
+      if (b_run == 0) sd[buf][row] = d;
     }
   };
 
@@ -338,22 +304,6 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmQArgs g) {
             part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_h, b_l, part[i][j], 0, 0, 0);
           }
         }
-      // Q4_K min term of this 32-block: acc[m][n] -= (dmin*m_b)[n] * sum_b a[m]
-      if constexpr (DT == DT_Q4K) {
-        float xsv[MT][4];
-#pragma unroll
-        for (int i = 0; i < MT; ++i)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) xsv[i][r] = sxs[buf][wave * WM + 16 * i + 4 * (lane >> 4) + r];
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-          const float dmn = sdm[buf][16 * j + fr];
-#pragma unroll
-          for (int i = 0; i < MT; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[i][j][r] -= dmn * xsv[i][r];
-        }
-      }
       // end of a d block: fold d[n] * (its partial) into the output accumulator
       if ((kt + 1) % PERIOD == 0) {
 #pragma unroll
@@ -397,6 +347,266 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmQArgs g) {
     }
 }
 
+// ---- Q4_K: 64 x 64 wave tiles, weights dequantised straight into MFMA operand registers -------
+//
+// A workgroup of four waves owns a BM x BN output tile (waves WGM x WGN, each 64 x 64 = 4 x 4
+// MFMA tiles). K advances in 64-wide stages (one Q4_K sub-block pair). The activation pair is
+// staged through LDS (double-buffered, XOR-swizzled 16-byte chunks); each wave decodes the weights
+// of its own 64 columns into registers: lane (column n, k group g) holds k = 8g .. 8g+7 of the
+// stage's two sub-blocks, built as exact fp16 integers w' = sc * q from the nibbles by a byte
+// permute under the exponent byte 0x64 (1024 + q) and one packed fp16 FMA (1024 + q) * sc -
+// 1024 * sc, which is exact because the result sc * q <= 945 is. An MFMA output column is the
+// lane's own weight column, so the superblock factors d and dmin apply per lane. The min term
+// -dmin * sum_b m_b * sum(a over sub-block b) runs on the matrix cores once per superblock: the
+// per-32 activation sums (fp16 pair) against the eight 6-bit mins.
+typedef _Float16 qh2_t __attribute__((ext_vector_type(2)));
+
+IEK_DEV uint32_t pk_fma16(uint32_t a, uint32_t b, uint32_t c) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(qh2_t, a), __builtin_bit_cast(qh2_t, b),
+                                                                __builtin_bit_cast(qh2_t, c)));
+}
+// (1024 + byte) as fp16 in each half: bytes of x picked by the selector's bytes 0 and 2.
+IEK_DEV uint32_t mag16(uint32_t x, uint32_t sel) { return __builtin_amdgcn_perm(0x64646464u, x, sel); }
+constexpr uint32_t SEL01 = 0x04010400u, SEL23 = 0x04030402u;
+constexpr uint32_t H2_M1024 = 0xE400E400u;  // (-1024, -1024)
+constexpr uint32_t H2_ONE = 0x3C003C00u;    // (1, 1)
+
+// {sc, sc} and {-1024 sc, -1024 sc} for the 6-bit scale in byte `i` of `scs`.
+IEK_DEV void q4k_scale2(uint32_t scs, uint32_t i, uint32_t& s2, uint32_t& c2) {
+  s2 = pk_fma16(mag16(scs, 0x04000400u | i | (i << 16)), H2_ONE, H2_M1024);
+  c2 = pk_fma16(s2, H2_M1024, 0u);
+}
+
+// B operand of sub-block 2P + H (H = 0: low nibbles, 1: high nibbles) for one 16-column tile.
+template <int P, int H>
+IEK_DEV qu4_t q4k_b(const uint4& hdr, uint2 q) {
+  const uint32_t scs = P < 2 ? (hdr.y & 0x3F3F3F3Fu) : ((hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u));
+  uint32_t sc, c;
+  q4k_scale2(scs, 2 * (P & 1) + H, sc, c);
+  const uint32_t x = (q.x >> (4 * H)) & 0x0F0F0F0Fu, y = (q.y >> (4 * H)) & 0x0F0F0F0Fu;
+  return qu4_t{pk_fma16(mag16(x, SEL01), sc, c), pk_fma16(mag16(x, SEL23), sc, c), pk_fma16(mag16(y, SEL01), sc, c),
+               pk_fma16(mag16(y, SEL23), sc, c)};
+}
+
+// The eight 6-bit mins of a superblock as fp16 (k groups 0 and 1; zero for groups 2 and 3).
+IEK_DEV qu4_t q4k_mins(const uint4& hdr, bool live) {
+  const uint32_t m03 = hdr.z & 0x3F3F3F3Fu;
+  const uint32_t m47 = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
+  qu4_t r{pk_fma16(mag16(m03, SEL01), H2_ONE, H2_M1024), pk_fma16(mag16(m03, SEL23), H2_ONE, H2_M1024),
+          pk_fma16(mag16(m47, SEL01), H2_ONE, H2_M1024), pk_fma16(mag16(m47, SEL23), H2_ONE, H2_M1024)};
+  return live ? r : qu4_t{0u, 0u, 0u, 0u};
+}
+
+IEK_DEV qf4_t mfma16(qu4_t a, qu4_t b, qf4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(qh8_t, a), __builtin_bit_cast(qh8_t, b), c, 0, 0, 0);
+}
+
+// Buffer resource over `bytes` bytes at `p` (raw, unswizzled; word 3 as gfx9 data loads expect).
+IEK_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+IEK_DEV qu4_t ld_b128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+IEK_DEV uint2 ld_b64(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+}
+
+template <int WGM, int WGN>
+__global__ __launch_bounds__(256) void gemm_q4k_kernel(GemmQArgs g) {
+  constexpr int BM = 64 * WGM, BN = 64 * WGN;
+  constexpr int PL = BM * 8;        // 16-byte chunks per plane per stage (BM rows x 64 halves)
+  constexpr int AR = PL / 256;      // chunk rows per thread per plane per stage
+  constexpr int DB = 4;             // stages of raw weight bytes in flight (the activation: one)
+  __shared__ __align__(16) qu4_t As[2][2 * PL];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int M = g.M, K = g.K, nst = K / 64, kb = K / 32, nsb = K / QK_K;
+  const int mtiles = (M + BM - 1) / BM;
+  int tile = blockIdx.x;
+  if (g.xcd_remap == 1) {
+    const int per = gridDim.x / 8;
+    tile = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  }
+  const int mt = tile % mtiles, ntile = tile / mtiles;
+  const int s = ntile < g.tile_start[1] ? 0 : (ntile < g.tile_start[2] ? 1 : 2);
+  const uint8_t* w = s == 0 ? g.w[0] : (s == 1 ? g.w[1] : g.w[2]);
+  float* out = s == 0 ? g.out[0] : (s == 1 ? g.out[1] : g.out[2]);
+  const int N = s == 0 ? g.n[0] : (s == 1 ? g.n[1] : g.n[2]);
+  const int ts = s == 0 ? 0 : (s == 1 ? g.tile_start[1] : g.tile_start[2]);
+  const int m0 = mt * BM, n0 = (ntile - ts) * BN;
+  const int lr = lane & 15, lg = lane >> 4;
+
+  // Operand streams as buffer loads: one descriptor per array, 32-bit per-lane offsets, the
+  // stage's advance in the scalar offset.
+  const __amdgpu_buffer_rsrc_t rw = buf_rsrc(w, (uint32_t)(g.row_bytes * (size_t)N));
+  const __amdgpu_buffer_rsrc_t rxh = buf_rsrc(g.xh, (uint32_t)((size_t)M * K * 2));
+  const __amdgpu_buffer_rsrc_t rxl = buf_rsrc(g.xl, (uint32_t)((size_t)M * K * 2));
+  const __amdgpu_buffer_rsrc_t rxs = buf_rsrc(g.xs, (uint32_t)((size_t)M * kb * 4));
+  uint32_t vb[4];  // weight row of the lane's column in each 16-column tile
+#pragma unroll
+  for (int j = 0; j < 4; ++j) vb[j] = (uint32_t)((size_t)min(n0 + 64 * wn + 16 * j + lr, N - 1) * g.row_bytes);
+  const uint32_t vq = 16 + 8 * lg;  // the lane's 8 bytes within a 32-byte nibble pair
+  uint32_t va[AR];                  // activation rows staged by this thread (both planes)
+#pragma unroll
+  for (int u = 0; u < AR; ++u) va[u] = (uint32_t)(min(m0 + (tid >> 3) + 32 * u, M - 1) * K + 8 * (tid & 7)) * 2u;
+  uint32_t vx[4];  // per-32 sums: k group 0 reads the hi plane, 1 the lo plane
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    vx[i] = (uint32_t)(min(m0 + 64 * wm + 16 * i + lr, M - 1) * kb + ((lg & 1) ? M * kb : 0)) * 2u;
+
+  struct ASlot {
+    qu4_t a[2 * AR];
+  };
+  struct BSlot {
+    uint2 q[4];
+  };
+  ASlot ra;
+  BSlot rb[DB];
+  uint4 hdr[4], hdrn[4];  // headers of the current and the next superblock
+  qu4_t xsv[4];
+
+  auto fetch_a = [&](int kt, ASlot& sl) {
+#pragma unroll
+    for (int u = 0; u < AR; ++u) {
+      sl.a[u] = ld_b128(rxh, va[u], 128u * kt);
+      sl.a[AR + u] = ld_b128(rxl, va[u], 128u * kt);
+    }
+  };
+  auto store_a = [&](int buf, const ASlot& sl) {
+    const int c = tid & 7;
+#pragma unroll
+    for (int u = 0; u < AR; ++u) {
+      const int row = (tid >> 3) + 32 * u;
+      As[buf][row * 8 + (c ^ (row & 7))] = sl.a[u];
+      As[buf][PL + row * 8 + (c ^ (row & 7))] = sl.a[AR + u];
+    }
+  };
+  auto fetch_b = [&](int kt, BSlot& sl) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sl.q[j] = ld_b64(rw, vb[j] + vq, (uint32_t)((kt >> 2) * Q4K_BYTES + 32 * (kt & 3)));
+  };
+  auto fetch_hdr = [&](int sb, uint4 (&h)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) h[j] = __builtin_bit_cast(uint4, ld_b128(rw, vb[j], (uint32_t)(sb * Q4K_BYTES)));
+  };
+  auto fetch_xs = [&](int sb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xsv[i] = ld_b128(rxs, vx[i], 16u * sb);
+  };
+
+  qf4_t acc[4][4], part[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[i][j] = qf4_t{0.f, 0.f, 0.f, 0.f};
+      part[i][j] = qf4_t{0.f, 0.f, 0.f, 0.f};
+    }
+
+  // prologue: A(0) in LDS, A(1) and B(0) .. B(3) in flight. The loads leave in the order the
+  // loop's last stage issues them (an activation stage, then a weight stage), so the wait counts
+  // at the loop head are the same on entry and on the back edge.
+  fetch_hdr(0, hdr);
+#pragma unroll
+  for (int i = 0; i < DB - 1; ++i) fetch_b(min(i, nst - 1), rb[i]);
+  fetch_a(0, ra);
+  store_a(0, ra);
+  __builtin_amdgcn_sched_barrier(0);
+  fetch_a(min(1, nst - 1), ra);
+  __builtin_amdgcn_sched_barrier(0);
+  fetch_b(min(DB - 1, nst - 1), rb[DB - 1]);
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();
+
+  for (int sb = 0; sb < nsb; ++sb) {
+    const int kt0 = 4 * sb;
+    const uint4 (&hd)[4] = hdr;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int kt = kt0 + p, buf = p & 1;
+      // A(kt+1) into the other LDS buffer (last read before the previous barrier), then refill
+      // (scheduling fences keep every fetch where it is written: the compiler would otherwise sink
+      // loads next to their use and expose their latency)
+      store_a(buf ^ 1, ra);
+      __builtin_amdgcn_sched_barrier(0);
+      fetch_a(min(kt + 2, nst - 1), ra);
+      // the next superblock's header goes out ahead of this stage's weight refill, so waiting
+      // for it at the superblock end never waits for a younger load
+      if (p == 0) fetch_hdr(min(sb + 1, nsb - 1), hdrn);
+      if (p == 2) fetch_xs(sb);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        qu4_t b[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint2 q = rb[p].q[j];
+          if (p == 0) b[j] = h == 0 ? q4k_b<0, 0>(hd[j], q) : q4k_b<0, 1>(hd[j], q);
+          if (p == 1) b[j] = h == 0 ? q4k_b<1, 0>(hd[j], q) : q4k_b<1, 1>(hd[j], q);
+          if (p == 2) b[j] = h == 0 ? q4k_b<2, 0>(hd[j], q) : q4k_b<2, 1>(hd[j], q);
+          if (p == 3) b[j] = h == 0 ? q4k_b<3, 0>(hd[j], q) : q4k_b<3, 1>(hd[j], q);
+        }
+        if (h == 1) {
+          __builtin_amdgcn_sched_barrier(0);
+          fetch_b(min(kt + DB, nst - 1), rb[p]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        qu4_t ah[4], al[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = 64 * wm + 16 * i + lr, ch = row * 8 + ((4 * h + lg) ^ (row & 7));
+          ah[i] = As[buf][ch];
+          al[i] = As[buf][PL + ch];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            part[i][j] = mfma16(ah[i], b[j], (p == 0 && h == 0) ? qf4_t{0.f, 0.f, 0.f, 0.f} : part[i][j]);
+            part[i][j] = mfma16(al[i], b[j], part[i][j]);
+          }
+      }
+      if (p == 3) {
+        // superblock end: acc += d * part - dmin * (sum_b m_b * xs_b); the mins are zero in k
+        // groups 2 and 3, so those lanes' activation sums drop out
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float d = half_bits_to_float(hd[j].x), dmin = half_bits_to_float(hd[j].x >> 16);
+          const qu4_t mb = q4k_mins(hd[j], lg < 2);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const qf4_t mp = mfma16(xsv[i], mb, qf4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][j][r] = (acc[i][j][r] + d * part[i][j][r]) - dmin * mp[r];
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) hdr[j] = hdrn[j];
+      }
+      __syncthreads();
+    }
+  }
+
+  const float* resid = s == 0 ? g.resid : nullptr;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + 64 * wn + 16 * j + lr;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + 64 * wm + 16 * i + 4 * lg + r;
+        if (m < M && n < N) {
+          float v = acc[i][j][r];
+          if (resid) v = resid[(size_t)m * N + n] + v;
+          out[(size_t)m * N + n] = v;
+        }
+      }
+    }
+}
+
 }  // namespace
 
 bool gemm_q_ok(int dt, const void* w, int K) {
@@ -412,7 +622,8 @@ bool gemm_q_ok(int dt, const void* w, int K) {
 void launch_block_sums(const float* a, int M, int K, float* xs, hipStream_t st) {
   if (K % 32 != 0) fail(ST_OP, "block_sums: K must be a multiple of 32");
   const size_t nb = (size_t)M * (K / 32);
-  hipLaunchKernelGGL(block_sums_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, st, a, nb, xs);
+  _Float16* h = reinterpret_cast<_Float16*>(xs);
+  hipLaunchKernelGGL(block_sums_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, st, a, nb, h, h + nb);
 }
 
 template <int DT, int BM, int BN>
@@ -432,6 +643,31 @@ static void gemm_q_launch(GemmQArgs g, hipStream_t st) {
   }
   g.xcd_remap = (mode == 2 && mtiles % 8 == 0) ? 2 : (tiles % 8 == 0 ? 1 : 0);
   hipLaunchKernelGGL((gemm_q_kernel<DT, BM, BN>), dim3(tiles), dim3(256), 0, st, g);
+}
+
+template <int WGM, int WGN>
+static void gemm_q4k_launch(GemmQArgs g, hipStream_t st) {
+  constexpr int BM = 64 * WGM, BN = 64 * WGN;
+  int t = 0;
+  for (int i = 0; i < g.nseg; ++i) {
+    g.tile_start[i] = t;
+    t += (g.n[i] + BN - 1) / BN;
+  }
+  for (int i = g.nseg; i <= 3; ++i) g.tile_start[i] = t;
+  const int tiles = ((g.M + BM - 1) / BM) * t;
+  g.xcd_remap = tiles % 8 == 0 ? 1 : 0;
+  hipLaunchKernelGGL((gemm_q4k_kernel<WGM, WGN>), dim3(tiles), dim3(256), 0, st, g);
+}
+
+// Q4_K tile: 128 x 128 (2 x 2 waves) by default; IEK_GEMM_Q4_TILE=1 selects 64 x 256 (tuning).
+static void gemm_q4k(GemmQArgs g, hipStream_t st) {
+  static int force = -2;
+  if (force == -2) {
+    const char* e = getenv("IEK_GEMM_Q4_TILE");
+    force = e ? atoi(e) : 0;
+  }
+  if (force == 1) gemm_q4k_launch<1, 4>(g, st);
+  else gemm_q4k_launch<2, 2>(g, st);
 }
 
 // Tile shape: 64 x 64 by default (measured fastest at the Mistral-7B prefill shapes: the larger
@@ -480,7 +716,7 @@ void launch_gemm_q(int dt, const GemmQSeg* segs, int nseg, const __half* xh, con
   }
   if (dt == DT_Q4K && !xs) fail(ST_OP, "gemm_q: Q4_K needs the per-32 activation sums");
   switch (dt) {
-    case DT_Q4K: gemm_q_dt<DT_Q4K>(g, st); break;
+    case DT_Q4K: gemm_q4k(g, st); break;
     case DT_Q6K: gemm_q_dt<DT_Q6K>(g, st); break;
     case DT_Q6K_R: gemm_q_dt<DT_Q6K_R>(g, st); break;
     default: gemm_q_dt<DT_Q8_0>(g, st); break;
