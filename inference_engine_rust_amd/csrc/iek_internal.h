@@ -62,9 +62,12 @@ struct GemmQSeg {
   int n;
 };
 bool gemm_q_ok(int dt, const void* w, int K);
+int num_cus();  // compute units of the current device
 void launch_block_sums(const float* a, int M, int K, float* xs, hipStream_t st);
+// kpart: optional M x N f32 scratch; with it a one-segment K-quant GEMM whose tiles would fill at
+// most half the CUs splits K in two and adds the second half's partial sums in a second pass.
 void launch_gemm_q(int dt, const GemmQSeg* segs, int nseg, const __half* xh, const __half* xl, const float* xs, int M,
-                   int K, const float* resid, hipStream_t st);
+                   int K, const float* resid, hipStream_t st, float* kpart = nullptr);
 void launch_gemm_mfma(int dt, const void* w, const __half* xh, const __half* xl, int M, int K, int N, float* out,
                       const float* resid, hipStream_t st);
 void launch_dequant(int dt, const void* blocks, size_t nblocks, float* out, hipStream_t st);

@@ -60,16 +60,31 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(int dt, const uint8_t* _
 void launch_gemm(int dt, const void* w, const float* a, int M, int K, int N, float* out, const float* resid,
                  hipStream_t st) {
   if (gemm_q_ok(dt, w, K) && (reinterpret_cast<uintptr_t>(a) & 15) == 0) {
-    // scale-factored K-quant GEMM: stream-ordered scratch for the fp16 pair and the per-32 sums
+    // scale-factored K-quant GEMM: stream-ordered scratch for the fp16 pair and the per-32 sums;
+    // Q6_K is first regrouped (the layout the model path keeps beside the native tensor), which
+    // the wave-tiled matrix-core kernel reads
     const size_t n = (size_t)M * K;
+    const bool q6r = dt == DT_Q6K && K % QK_K == 0;
+    const size_t wr = q6r ? (size_t)N * q6r_row_bytes((size_t)K / QK_K) : 0;
+    const size_t xbytes = (n * 2 * sizeof(__half) + (n / 32 + 64) * sizeof(float) + 255) / 256 * 256;
+    const size_t pbytes = ((size_t)M * N * sizeof(float) + 255) / 256 * 256;  // split-K partial
     void* buf = nullptr;
-    check_hip(hipMallocAsync(&buf, n * 2 * sizeof(__half) + (n / 32 + 64) * sizeof(float), st), "hipMallocAsync");
+    check_hip(hipMallocAsync(&buf, xbytes + pbytes + wr, st), "hipMallocAsync");
     __half* xh = static_cast<__half*>(buf);
     float* xs = reinterpret_cast<float*>(xh + 2 * n);
     launch_split_f16(a, n, xh, xh + n, st);
     launch_block_sums(a, M, K, xs, st);
-    GemmQSeg seg{w, out, N};
-    launch_gemm_q(dt, &seg, 1, xh, xh + n, xs, M, K, resid, st);
+    const void* wq = w;
+    int wdt = dt;
+    if (q6r) {
+      void* r = static_cast<char*>(buf) + xbytes + pbytes;
+      launch_repack_q6k(w, K, N, r, st);
+      wq = r;
+      wdt = DT_Q6K_R;
+    }
+    GemmQSeg seg{wq, out, N};
+    launch_gemm_q(wdt, &seg, 1, xh, xh + n, xs, M, K, resid, st,
+                  reinterpret_cast<float*>(static_cast<char*>(buf) + xbytes));
     check_hip(hipFreeAsync(buf, st), "hipFreeAsync");
     return;
   }

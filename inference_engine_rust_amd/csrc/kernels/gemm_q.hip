@@ -37,6 +37,10 @@ struct GemmQArgs {
   const float* xs;
   const float* resid;  // segment 0 only
   int xcd_remap;
+  // split-K (wave-tiled kernel, one segment): the second half of the superblocks writes its
+  // partial sums to kpart [M, N], which a follow-up pass adds to out
+  int ksplit;
+  float* kpart;
 };
 
 namespace {
@@ -55,43 +59,6 @@ IEK_DEV uint32_t hpack(_Float16 a, _Float16 b) {
 // their decode into the integer w' (as fp16, exact), the stage's column scale and Q4_K's dmin*m.
 template <int DT>
 struct QDeq;
-
-// Q6_K weights from the regrouped per-row layout (DT_Q6K_R: lane chunks of [ql 0/2 | ql 1/3 | qh]
-// 16 bytes each, then per-chunk scale dwords, then d per superblock; see matvec.hip).
-template <>
-struct QDeq<DT_Q6K_R> {
-  static constexpr int PERIOD = 8;
-  static constexpr bool LO = true;
-  uint2 ql, qh;
-  uint32_t sc, d16;
-  IEK_DEV void load(const uint8_t* w, size_t row_bytes, int n, int k0, int nsb) {
-    const uint8_t* row = w + (size_t)n * row_bytes;
-    const int j = k0 >> 8, e = k0 & 255, h = e >> 7, r = e & 127, qd = r >> 5, l = r & 31;
-    const int kc = 2 * h + (l >> 4), i0 = l & 15;
-    const uint8_t* m = row + (size_t)j * 192 + 48 * kc;
-    ql = *reinterpret_cast<const uint2*>(m + ((qd & 1) ? 16 : 0) + i0);
-    qh = *reinterpret_cast<const uint2*>(m + 32 + i0);
-    sc = *reinterpret_cast<const uint32_t*>(row + (size_t)nsb * 192 + 16 * j + 4 * kc);
-    d16 = *reinterpret_cast<const uint16_t*>(row + (size_t)nsb * 208 + 2 * j);
-  }
-  IEK_DEV void decode(int k0, uint4& hi, uint4& lo, float& d) const {
-    const int qd = ((k0 & 255) & 127) >> 5;
-    d = half_bits_to_float(d16);
-    const int isc = (int)(int8_t)((sc >> (8 * qd)) & 0xFF);
-    const uint32_t lw[2] = {ql.x, ql.y}, hw[2] = {qh.x, qh.y};
-    _Float16 h[8], l[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t lb = (lw[i >> 2] >> (8 * (i & 3))) & 0xFFu, hb = (hw[i >> 2] >> (8 * (i & 3))) & 0xFFu;
-      const uint32_t nib = qd < 2 ? (lb & 0xFu) : (lb >> 4);
-      const int wq = ((int)(nib | (((hb >> (2 * qd)) & 3u) << 4)) - 32) * isc;
-      h[i] = (_Float16)wq;
-      l[i] = (_Float16)(wq - (int)h[i]);
-    }
-    hi = make_uint4(hpack(h[0], h[1]), hpack(h[2], h[3]), hpack(h[4], h[5]), hpack(h[6], h[7]));
-    lo = make_uint4(hpack(l[0], l[1]), hpack(l[2], l[3]), hpack(l[4], l[5]), hpack(l[6], l[7]));
-  }
-};
 
 // Q6_K from the native 210-byte blocks (2-byte aligned: u16 loads).
 template <>
@@ -347,7 +314,7 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(GemmQArgs g) {
     }
 }
 
-// ---- Q4_K: 64 x 64 wave tiles, weights dequantised straight into MFMA operand registers -------
+// ---- K-quants: 64 x 64 wave tiles, weights dequantised straight into MFMA operand registers ----
 //
 // A workgroup of four waves owns a BM x BN output tile (waves WGM x WGN, each 64 x 64 = 4 x 4
 // MFMA tiles). K advances in 64-wide stages (one Q4_K sub-block pair). The activation pair is
@@ -412,22 +379,140 @@ IEK_DEV uint2 ld_b64(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
 }
 
-template <int WGM, int WGN>
-__global__ __launch_bounds__(256) void gemm_q4k_kernel(GemmQArgs g) {
+IEK_DEV uint32_t ld_b32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+IEK_DEV uint32_t ld_b16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
+
+// Weight formats of the wave-tiled kernel. Each provides the raw bytes of one 64-wide stage for
+// the lane's four columns (`Raw`), the per-superblock factors (`Hdr`), and the B operands of
+// half-step (P, H): hi, plus lo when the integer weight w' does not fit fp16 (LO).
+struct Q4KB {
+  static constexpr bool LO = false, MINS = true;
+  struct Raw {
+    uint2 q[4];
+  };
+  struct Hdr {
+    uint4 h[4];
+  };
+  IEK_DEV static void fetch(__amdgpu_buffer_rsrc_t r, const uint32_t (&vb)[4], int lg, int kt, Raw& o) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o.q[j] = ld_b64(r, vb[j] + 16 + 8 * lg, (uint32_t)((kt >> 2) * Q4K_BYTES + 32 * (kt & 3)));
+  }
+  IEK_DEV static void fetch_hdr(__amdgpu_buffer_rsrc_t r, const uint32_t (&vb)[4], int, int sb, int, Hdr& o) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o.h[j] = __builtin_bit_cast(uint4, ld_b128(r, vb[j], (uint32_t)(sb * Q4K_BYTES)));
+  }
+  template <int P, int H>
+  IEK_DEV static void deq(const Hdr& hd, const Raw& q, qu4_t (&bh)[4], qu4_t (&)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bh[j] = q4k_b<P, H>(hd.h[j], q.q[j]);
+  }
+  IEK_DEV static float d(const Hdr& hd, int j) { return half_bits_to_float(hd.h[j].x); }
+  IEK_DEV static float dmin(const Hdr& hd, int j) { return half_bits_to_float(hd.h[j].x >> 16); }
+  IEK_DEV static qu4_t mins(const Hdr& hd, int j, bool live) { return q4k_mins(hd.h[j], live); }
+};
+
+// Q6_K from the regrouped rows (DT_Q6K_R: per superblock four 48-byte lane chunks [ql of quarters
+// 0/2 | ql of quarters 1/3 | qh], then per-chunk scale dwords, then d). Stage P covers half
+// P >> 1 and quarters 2(P & 1) + H; lane group g reads chunk 2(P >> 1) + (g >> 1), bytes 8(g & 1).
+// w' = sc * (q - 32) reaches 4096, so it is an fp16 pair: hi = fp16(w'), lo = w' - hi (|lo| <= 1).
+struct Q6RB {
+  static constexpr bool LO = true, MINS = false;
+  struct Raw {
+    uint2 l0[4], l1[4], h[4];
+  };
+  struct Hdr {
+    uint32_t sc[2][4], d[4];
+  };
+  IEK_DEV static void fetch(__amdgpu_buffer_rsrc_t r, const uint32_t (&vb)[4], int lg, int kt, Raw& o) {
+    const uint32_t so = (uint32_t)((kt >> 2) * 192 + 48 * 2 * ((kt & 3) >> 1));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t v = vb[j] + 48 * (lg >> 1) + 8 * (lg & 1);
+      o.l0[j] = ld_b64(r, v, so);
+      o.l1[j] = ld_b64(r, v + 16, so);
+      o.h[j] = ld_b64(r, v + 32, so);
+    }
+  }
+  IEK_DEV static void fetch_hdr(__amdgpu_buffer_rsrc_t r, const uint32_t (&vb)[4], int lg, int sb, int nsb, Hdr& o) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t v = vb[j] + (uint32_t)nsb * 192 + 4 * (lg >> 1);
+      o.sc[0][j] = ld_b32(r, v, 16u * sb);
+      o.sc[1][j] = ld_b32(r, v + 8, 16u * sb);
+      o.d[j] = ld_b16(r, vb[j] + (uint32_t)nsb * 208, 2u * sb);
+    }
+  }
+  template <int P, int H>
+  IEK_DEV static void deq(const Hdr& hd, const Raw& q, qu4_t (&bh)[4], qu4_t (&bl)[4]) {
+    constexpr int qd = 2 * (P & 1) + H;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // {sc, sc} from the signed scale byte: (sc + 128) under the exponent byte, minus 1152
+      const uint32_t scb = hd.sc[P >> 1][j] ^ 0x80808080u;
+      const qh2_t s2 = __builtin_bit_cast(qh2_t, mag16(scb, 0x04000400u | qd | (qd << 16))) - qh2_t{1152.0f16, 1152.0f16};
+      const uint2 l = H ? q.l1[j] : q.l0[j], hb = q.h[j];
+      const uint32_t qx = ((l.x >> (4 * (P & 1))) & 0x0F0F0F0Fu) | (((hb.x >> (2 * qd)) << 4) & 0x30303030u);
+      const uint32_t qy = ((l.y >> (4 * (P & 1))) & 0x0F0F0F0Fu) | (((hb.y >> (2 * qd)) << 4) & 0x30303030u);
+      const uint32_t v[4] = {mag16(qx, SEL01), mag16(qx, SEL23), mag16(qy, SEL01), mag16(qy, SEL23)};
+      uint32_t hi[4], lo[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const qh2_t qm = __builtin_bit_cast(qh2_t, v[t]) - qh2_t{1056.0f16, 1056.0f16};  // q - 32, exact
+        const qh2_t h = qm * s2;
+        hi[t] = __builtin_bit_cast(uint32_t, h);
+        lo[t] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(qm, s2, -h));  // exact remainder
+      }
+      bh[j] = qu4_t{hi[0], hi[1], hi[2], hi[3]};
+      bl[j] = qu4_t{lo[0], lo[1], lo[2], lo[3]};
+    }
+  }
+  IEK_DEV static float d(const Hdr& hd, int j) { return half_bits_to_float(hd.d[j]); }
+  IEK_DEV static float dmin(const Hdr&, int) { return 0.f; }
+  IEK_DEV static qu4_t mins(const Hdr&, int, bool) { return qu4_t{0u, 0u, 0u, 0u}; }
+};
+
+template <class T>
+IEK_DEV void kq_deq(int p, int h, const typename T::Hdr& hd, const typename T::Raw& q, qu4_t (&bh)[4], qu4_t (&bl)[4]) {
+  switch (2 * p + h) {
+    case 0: T::template deq<0, 0>(hd, q, bh, bl); break;
+    case 1: T::template deq<0, 1>(hd, q, bh, bl); break;
+    case 2: T::template deq<1, 0>(hd, q, bh, bl); break;
+    case 3: T::template deq<1, 1>(hd, q, bh, bl); break;
+    case 4: T::template deq<2, 0>(hd, q, bh, bl); break;
+    case 5: T::template deq<2, 1>(hd, q, bh, bl); break;
+    case 6: T::template deq<3, 0>(hd, q, bh, bl); break;
+    default: T::template deq<3, 1>(hd, q, bh, bl); break;
+  }
+}
+
+template <class T, int WGM, int WGN, int DA>
+__global__ __launch_bounds__(256) void gemm_kq_kernel(GemmQArgs g) {
   constexpr int BM = 64 * WGM, BN = 64 * WGN;
   constexpr int PL = BM * 8;        // 16-byte chunks per plane per stage (BM rows x 64 halves)
   constexpr int AR = PL / 256;      // chunk rows per thread per plane per stage
-  constexpr int DB = 4;             // stages of raw weight bytes in flight (the activation: one)
+  constexpr int DB = 2;             // stages of raw weight bytes in flight and (DA) of activation
+                                    // stages; both divide the 4 stages of a superblock, so ring
+                                    // slots are static
+  static_assert(4 % DA == 0 && 4 % DB == 0, "ring slots are indexed by stage within the superblock");
   __shared__ __align__(16) qu4_t As[2][2 * PL];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WGN, wn = wave % WGN;
-  const int M = g.M, K = g.K, nst = K / 64, kb = K / 32, nsb = K / QK_K;
+  const int M = g.M, K = g.K, kb = K / 32, nsb = K / QK_K;
   const int mtiles = (M + BM - 1) / BM;
-  int tile = blockIdx.x;
+  // split-K: workgroups [ks * per_split, (ks + 1) * per_split) take superblocks [sb_lo, sb_hi)
+  const int per_split = gridDim.x / g.ksplit, ks = blockIdx.x / per_split;
+  const int sb_lo = ks == 0 ? 0 : nsb / 2, sb_hi = (g.ksplit == 1 || ks == 1) ? nsb : nsb / 2;
+  const int kt_last = 4 * sb_hi - 1;
+  int tile = blockIdx.x - ks * per_split;
   if (g.xcd_remap == 1) {
-    const int per = gridDim.x / 8;
-    tile = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    const int per = per_split / 8;
+    tile = (tile % 8) * per + tile / 8;
   }
   const int mt = tile % mtiles, ntile = tile / mtiles;
   const int s = ntile < g.tile_start[1] ? 0 : (ntile < g.tile_start[2] ? 1 : 2);
@@ -443,12 +528,11 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(GemmQArgs g) {
   const __amdgpu_buffer_rsrc_t rw = buf_rsrc(w, (uint32_t)(g.row_bytes * (size_t)N));
   const __amdgpu_buffer_rsrc_t rxh = buf_rsrc(g.xh, (uint32_t)((size_t)M * K * 2));
   const __amdgpu_buffer_rsrc_t rxl = buf_rsrc(g.xl, (uint32_t)((size_t)M * K * 2));
-  const __amdgpu_buffer_rsrc_t rxs = buf_rsrc(g.xs, (uint32_t)((size_t)M * kb * 4));
+  const __amdgpu_buffer_rsrc_t rxs = buf_rsrc(g.xs, T::MINS ? (uint32_t)((size_t)M * kb * 4) : 0u);
   uint32_t vb[4];  // weight row of the lane's column in each 16-column tile
 #pragma unroll
   for (int j = 0; j < 4; ++j) vb[j] = (uint32_t)((size_t)min(n0 + 64 * wn + 16 * j + lr, N - 1) * g.row_bytes);
-  const uint32_t vq = 16 + 8 * lg;  // the lane's 8 bytes within a 32-byte nibble pair
-  uint32_t va[AR];                  // activation rows staged by this thread (both planes)
+  uint32_t va[AR];  // activation rows staged by this thread (both planes)
 #pragma unroll
   for (int u = 0; u < AR; ++u) va[u] = (uint32_t)(min(m0 + (tid >> 3) + 32 * u, M - 1) * K + 8 * (tid & 7)) * 2u;
   uint32_t vx[4];  // per-32 sums: k group 0 reads the hi plane, 1 the lo plane
@@ -459,12 +543,9 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(GemmQArgs g) {
   struct ASlot {
     qu4_t a[2 * AR];
   };
-  struct BSlot {
-    uint2 q[4];
-  };
-  ASlot ra;
-  BSlot rb[DB];
-  uint4 hdr[4], hdrn[4];  // headers of the current and the next superblock
+  ASlot ra[DA];
+  typename T::Raw rb[DB];
+  typename T::Hdr hdr, hdrn;  // factors of the current and the next superblock
   qu4_t xsv[4];
 
   auto fetch_a = [&](int kt, ASlot& sl) {
@@ -483,14 +564,6 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(GemmQArgs g) {
       As[buf][PL + row * 8 + (c ^ (row & 7))] = sl.a[AR + u];
     }
   };
-  auto fetch_b = [&](int kt, BSlot& sl) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) sl.q[j] = ld_b64(rw, vb[j] + vq, (uint32_t)((kt >> 2) * Q4K_BYTES + 32 * (kt & 3)));
-  };
-  auto fetch_hdr = [&](int sb, uint4 (&h)[4]) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) h[j] = __builtin_bit_cast(uint4, ld_b128(rw, vb[j], (uint32_t)(sb * Q4K_BYTES)));
-  };
   auto fetch_xs = [&](int sb) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) xsv[i] = ld_b128(rxs, vx[i], 16u * sb);
@@ -505,91 +578,97 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(GemmQArgs g) {
       part[i][j] = qf4_t{0.f, 0.f, 0.f, 0.f};
     }
 
-  // prologue: A(0) in LDS, A(1) and B(0) .. B(3) in flight. The loads leave in the order the
-  // loop's last stage issues them (an activation stage, then a weight stage), so the wait counts
-  // at the loop head are the same on entry and on the back edge.
-  fetch_hdr(0, hdr);
+  // prologue: A(0) in LDS, A(1) .. A(DA) and B(0) .. B(DB-1) in flight. The loads leave in the
+  // order the loop's last stage issues them (an activation stage, then a weight stage), so the
+  // wait counts at the loop head are the same on entry and on the back edge.
+  const int kt_lo = 4 * sb_lo;
+  T::fetch_hdr(rw, vb, lg, sb_lo, nsb, hdr);
 #pragma unroll
-  for (int i = 0; i < DB - 1; ++i) fetch_b(min(i, nst - 1), rb[i]);
-  fetch_a(0, ra);
-  store_a(0, ra);
+  for (int i = 0; i < DB - 1; ++i) T::fetch(rw, vb, lg, min(kt_lo + i, kt_last), rb[i]);
+  fetch_a(kt_lo, ra[0]);
+  store_a(0, ra[0]);
   __builtin_amdgcn_sched_barrier(0);
-  fetch_a(min(1, nst - 1), ra);
+#pragma unroll
+  for (int i = 1; i <= DA; ++i) fetch_a(min(kt_lo + i, kt_last), ra[i % DA]);
   __builtin_amdgcn_sched_barrier(0);
-  fetch_b(min(DB - 1, nst - 1), rb[DB - 1]);
+  T::fetch(rw, vb, lg, min(kt_lo + DB - 1, kt_last), rb[DB - 1]);
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
 
-  for (int sb = 0; sb < nsb; ++sb) {
+  for (int sb = sb_lo; sb < sb_hi; ++sb) {
     const int kt0 = 4 * sb;
-    const uint4 (&hd)[4] = hdr;
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
       const int kt = kt0 + p, buf = p & 1;
       // A(kt+1) into the other LDS buffer (last read before the previous barrier), then refill
       // (scheduling fences keep every fetch where it is written: the compiler would otherwise sink
       // loads next to their use and expose their latency)
-      store_a(buf ^ 1, ra);
+      store_a(buf ^ 1, ra[(p + 1) % DA]);
       __builtin_amdgcn_sched_barrier(0);
-      fetch_a(min(kt + 2, nst - 1), ra);
-      // the next superblock's header goes out ahead of this stage's weight refill, so waiting
-      // for it at the superblock end never waits for a younger load
-      if (p == 0) fetch_hdr(min(sb + 1, nsb - 1), hdrn);
-      if (p == 2) fetch_xs(sb);
+      fetch_a(min(kt + 1 + DA, kt_last), ra[(p + 1) % DA]);
+      // the next superblock's factors go out ahead of this stage's weight refill, so waiting
+      // for them at the superblock end never waits for a younger load
+      if (p == 0) T::fetch_hdr(rw, vb, lg, min(sb + 1, sb_hi - 1), nsb, hdrn);
+      if (T::MINS && p == 2) fetch_xs(sb);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        qu4_t b[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint2 q = rb[p].q[j];
-          if (p == 0) b[j] = h == 0 ? q4k_b<0, 0>(hd[j], q) : q4k_b<0, 1>(hd[j], q);
-          if (p == 1) b[j] = h == 0 ? q4k_b<1, 0>(hd[j], q) : q4k_b<1, 1>(hd[j], q);
-          if (p == 2) b[j] = h == 0 ? q4k_b<2, 0>(hd[j], q) : q4k_b<2, 1>(hd[j], q);
-          if (p == 3) b[j] = h == 0 ? q4k_b<3, 0>(hd[j], q) : q4k_b<3, 1>(hd[j], q);
-        }
+        qu4_t bh[4], bl[4];
+        kq_deq<T>(p, h, hdr, rb[p % DB], bh, bl);
         if (h == 1) {
           __builtin_amdgcn_sched_barrier(0);
-          fetch_b(min(kt + DB, nst - 1), rb[p]);
+          T::fetch(rw, vb, lg, min(kt + DB, kt_last), rb[p % DB]);
           __builtin_amdgcn_sched_barrier(0);
         }
-        qu4_t ah[4], al[4];
+        // activation operands one m-tile ahead of the MFMAs that use them
+        qu4_t ah[2], al[2];
+        auto rd = [&](int i, qu4_t& x, qu4_t& y) {
+          const int row = 64 * wm + 16 * i + lr, ch = row * 8 + ((4 * h + lg) ^ (row & 7));
+          x = As[buf][ch];
+          y = As[buf][PL + ch];
+        };
+        rd(0, ah[0], al[0]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int row = 64 * wm + 16 * i + lr, ch = row * 8 + ((4 * h + lg) ^ (row & 7));
-          ah[i] = As[buf][ch];
-          al[i] = As[buf][PL + ch];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
+          if (i < 3) rd(i + 1, ah[(i + 1) & 1], al[(i + 1) & 1]);
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            part[i][j] = mfma16(ah[i], b[j], (p == 0 && h == 0) ? qf4_t{0.f, 0.f, 0.f, 0.f} : part[i][j]);
-            part[i][j] = mfma16(al[i], b[j], part[i][j]);
-          }
-      }
-      if (p == 3) {
-        // superblock end: acc += d * part - dmin * (sum_b m_b * xs_b); the mins are zero in k
-        // groups 2 and 3, so those lanes' activation sums drop out
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float d = half_bits_to_float(hd[j].x), dmin = half_bits_to_float(hd[j].x >> 16);
-          const qu4_t mb = q4k_mins(hd[j], lg < 2);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const qf4_t mp = mfma16(xsv[i], mb, qf4_t{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[i][j][r] = (acc[i][j][r] + d * part[i][j][r]) - dmin * mp[r];
+            part[i][j] = mfma16(ah[i & 1], bh[j], (p == 0 && h == 0) ? qf4_t{0.f, 0.f, 0.f, 0.f} : part[i][j]);
+            part[i][j] = mfma16(al[i & 1], bh[j], part[i][j]);
+            if constexpr (T::LO) part[i][j] = mfma16(ah[i & 1], bl[j], part[i][j]);
           }
         }
+      }
+      if (p == 3) {
+        // superblock end: acc += d * part (- dmin * sum_b m_b * xs_b for Q4_K; the mins are zero
+        // in k groups 2 and 3, so those lanes' activation sums drop out)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) hdr[j] = hdrn[j];
+        for (int j = 0; j < 4; ++j) {
+          const float d = T::d(hdr, j);
+          if constexpr (T::MINS) {
+            const float dmin = T::dmin(hdr, j);
+            const qu4_t mb = T::mins(hdr, j, lg < 2);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const qf4_t mp = mfma16(xsv[i], mb, qf4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc[i][j][r] = (acc[i][j][r] + d * part[i][j][r]) - dmin * mp[r];
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc[i][j][r] += d * part[i][j][r];
+          }
+        }
+        hdr = hdrn;
       }
       __syncthreads();
     }
   }
 
-  const float* resid = s == 0 ? g.resid : nullptr;
+  const float* resid = s == 0 && ks == 0 ? g.resid : nullptr;
+  float* dst = ks == 0 ? out : g.kpart;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -601,10 +680,24 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(GemmQArgs g) {
         if (m < M && n < N) {
           float v = acc[i][j][r];
           if (resid) v = resid[(size_t)m * N + n] + v;
-          out[(size_t)m * N + n] = v;
+          dst[(size_t)m * N + n] = v;
         }
       }
     }
+}
+
+// out[i] += part[i]: the split-K reduction (after the first half wrote resid + its sum).
+__global__ __launch_bounds__(256) void add_part_kernel(float* __restrict__ out, const float* __restrict__ part,
+                                                      size_t n4) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+    float4 o = reinterpret_cast<float4*>(out)[i];
+    const float4 q = reinterpret_cast<const float4*>(part)[i];
+    o.x += q.x;
+    o.y += q.y;
+    o.z += q.z;
+    o.w += q.w;
+    reinterpret_cast<float4*>(out)[i] = o;
+  }
 }
 
 }  // namespace
@@ -645,8 +738,8 @@ static void gemm_q_launch(GemmQArgs g, hipStream_t st) {
   hipLaunchKernelGGL((gemm_q_kernel<DT, BM, BN>), dim3(tiles), dim3(256), 0, st, g);
 }
 
-template <int WGM, int WGN>
-static void gemm_q4k_launch(GemmQArgs g, hipStream_t st) {
+template <class T, int WGM, int WGN, int DA>
+static void gemm_kq_launch(GemmQArgs g, hipStream_t st) {
   constexpr int BM = 64 * WGM, BN = 64 * WGN;
   int t = 0;
   for (int i = 0; i < g.nseg; ++i) {
@@ -656,18 +749,36 @@ static void gemm_q4k_launch(GemmQArgs g, hipStream_t st) {
   for (int i = g.nseg; i <= 3; ++i) g.tile_start[i] = t;
   const int tiles = ((g.M + BM - 1) / BM) * t;
   g.xcd_remap = tiles % 8 == 0 ? 1 : 0;
-  hipLaunchKernelGGL((gemm_q4k_kernel<WGM, WGN>), dim3(tiles), dim3(256), 0, st, g);
+  // split K in two when one workgroup per tile would leave most CUs idle (the M x N of the O and
+  // down projections at a 512-token prompt fill half the chip)
+  const size_t mn = (size_t)g.M * g.n[0];
+  g.ksplit = (g.kpart && g.nseg == 1 && 2 * tiles <= num_cus() && g.K / QK_K >= 2 && mn % 4 == 0) ? 2 : 1;
+  hipLaunchKernelGGL((gemm_kq_kernel<T, WGM, WGN, DA>), dim3(tiles * g.ksplit), dim3(256), 0, st, g);
+  if (g.ksplit == 2) {
+    const int blocks = (int)std::min<size_t>((mn / 4 + 255) / 256, 2048);
+    hipLaunchKernelGGL(add_part_kernel, dim3(blocks), dim3(256), 0, st, g.out[0], g.kpart, mn / 4);
+  }
 }
 
-// Q4_K tile: 128 x 128 (2 x 2 waves) by default; IEK_GEMM_Q4_TILE=1 selects 64 x 256 (tuning).
-static void gemm_q4k(GemmQArgs g, hipStream_t st) {
+// K-quant tile: 64 x 256 (1 x 4 waves; each wave streams its own 64 weight columns, the
+// activation tile is shared) with one activation stage in flight: measured 15% faster than
+// 128 x 128 at the Mistral-7B prefill shapes, and deeper activation prefetch gained nothing.
+// IEK_GEMM_KQ_TILE selects the others (tuning): 1: 128 x 128, 2: 128 x 128 with two stages,
+// 3 / 4: 64 x 256 with two / four stages.
+template <class T>
+static void gemm_kq(GemmQArgs g, hipStream_t st) {
   static int force = -2;
   if (force == -2) {
-    const char* e = getenv("IEK_GEMM_Q4_TILE");
+    const char* e = getenv("IEK_GEMM_KQ_TILE");
     force = e ? atoi(e) : 0;
   }
-  if (force == 1) gemm_q4k_launch<1, 4>(g, st);
-  else gemm_q4k_launch<2, 2>(g, st);
+  switch (force) {
+    case 1: gemm_kq_launch<T, 2, 2, 1>(g, st); break;
+    case 2: gemm_kq_launch<T, 2, 2, 2>(g, st); break;
+    case 3: gemm_kq_launch<T, 1, 4, 2>(g, st); break;
+    case 4: gemm_kq_launch<T, 1, 4, 4>(g, st); break;
+    default: gemm_kq_launch<T, 1, 4, 1>(g, st); break;
+  }
 }
 
 // Tile shape: 64 x 64 by default (measured fastest at the Mistral-7B prefill shapes: the larger
@@ -691,7 +802,7 @@ static void gemm_q_dt(GemmQArgs g, hipStream_t st) {
 }
 
 void launch_gemm_q(int dt, const GemmQSeg* segs, int nseg, const __half* xh, const __half* xl, const float* xs, int M,
-                   int K, const float* resid, hipStream_t st) {
+                   int K, const float* resid, hipStream_t st, float* kpart) {
   if (nseg < 1 || nseg > 3 || M < 1) fail(ST_OP, "gemm_q: 1..3 segments and M >= 1");
   GemmQArgs g{};
   g.nseg = nseg;
@@ -707,6 +818,8 @@ void launch_gemm_q(int dt, const GemmQSeg* segs, int nseg, const __half* xh, con
   g.xl = xl;
   g.xs = xs;
   g.resid = resid;
+  g.kpart = kpart;
+  g.ksplit = 1;
   const size_t nsb = (size_t)(K / QK_K);
   switch (dt) {
     case DT_Q4K: g.row_bytes = nsb * Q4K_BYTES; break;
@@ -716,9 +829,9 @@ void launch_gemm_q(int dt, const GemmQSeg* segs, int nseg, const __half* xh, con
   }
   if (dt == DT_Q4K && !xs) fail(ST_OP, "gemm_q: Q4_K needs the per-32 activation sums");
   switch (dt) {
-    case DT_Q4K: gemm_q4k(g, st); break;
+    case DT_Q4K: gemm_kq<Q4KB>(g, st); break;
     case DT_Q6K: gemm_q_dt<DT_Q6K>(g, st); break;
-    case DT_Q6K_R: gemm_q_dt<DT_Q6K_R>(g, st); break;
+    case DT_Q6K_R: gemm_kq<Q6RB>(g, st); break;
     default: gemm_q_dt<DT_Q8_0>(g, st); break;
   }
 }

@@ -106,7 +106,7 @@ __global__ __launch_bounds__(256) void mv_generic(MvArgs a, int dt) {
 }
 
 // ---------------------------------------------------------------------------------------------
-static int num_cus() {
+int num_cus() {
   static int n = 0;
   if (n == 0) {
     int dev = 0;

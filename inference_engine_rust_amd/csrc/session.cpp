@@ -168,6 +168,7 @@ void Session::ensure_rows(int rows) {
   u_ = dev_alloc<float>(R * fmax);
   act_ = dev_alloc<float>(R * fmax);
   tmp_ = dev_alloc<float>(R * std::max(qmax, fmax));
+  kpart_ok_ = std::max(qmax, fmax) >= H_;  // tmp_ holds a split-K partial of a [rows, hidden] output
   // fp16 (hi, lo) pair of the widest GEMM input, for the matrix-core prefill projections
   xs_ = dev_alloc<__half>(2 * R * std::max(std::max(H_, qmax), fmax));
   xsum_ = dev_alloc<float>(R * std::max(std::max(H_, qmax), fmax) / 32 + 1);
@@ -210,7 +211,8 @@ static void project(const DevTensor& w, const float* a, const __half* xs, int ro
 // Prefill projections through the scale-factored matrix-core GEMM when every weight qualifies:
 // `a` (M x K) must already be split into xs_ (fp16 pair) and summed per 32 into xsum_.
 // Returns false when the caller should fall back to per-matrix projections.
-bool Session::project_q(const DevTensor* const* ws, float* const* outs, int nseg, int M, int K, const float* resid) {
+bool Session::project_q(const DevTensor* const* ws, float* const* outs, int nseg, int M, int K, const float* resid,
+                        float* kpart) {
   if (M < 2) return false;
   int dt = -1;
   GemmQSeg segs[3];
@@ -228,7 +230,7 @@ bool Session::project_q(const DevTensor* const* ws, float* const* outs, int nseg
     if (!gemm_q_ok(dt, p, K)) return false;
     segs[i] = GemmQSeg{p, outs[i], (int)w.dims[1]};
   }
-  launch_gemm_q(dt, segs, nseg, xs_, xs_ + (size_t)M * K, xsum_, M, K, resid, st_);
+  launch_gemm_q(dt, segs, nseg, xs_, xs_ + (size_t)M * K, xsum_, M, K, resid, st_, kpart);
   return true;
 }
 
@@ -274,7 +276,8 @@ void Session::layer_prefill(int li, int M) {
     const __half* xa = split(att_, qd);
     const DevTensor* ws[1] = {&L.wo};
     float* outs[1] = {x_};
-    if (!xa || !project_q(ws, outs, 1, M, qd, x_)) project(L.wo, att_, xa, M, qd, H_, x_, x_, st_);
+    if (!xa || !project_q(ws, outs, 1, M, qd, x_, kpart_ok_ ? tmp_ : nullptr))
+      project(L.wo, att_, xa, M, qd, H_, x_, x_, st_);
   }
   // FFN sub-layer: pre-norm, gate/up, SwiGLU, down + residual.
   launch_rmsnorm(x_, (const float*)L.ffn_norm.dev, M, H_, eps, xn_, st_);
@@ -295,7 +298,8 @@ void Session::layer_prefill(int li, int M) {
     const __half* xa = split(act_, S.ffn_dim);
     const DevTensor* ws[1] = {&L.down};
     float* outs[1] = {x_};
-    if (!xa || !project_q(ws, outs, 1, M, S.ffn_dim, x_)) project(L.down, act_, xa, M, S.ffn_dim, H_, x_, x_, st_);
+    if (!xa || !project_q(ws, outs, 1, M, S.ffn_dim, x_, kpart_ok_ ? tmp_ : nullptr))
+      project(L.down, act_, xa, M, S.ffn_dim, H_, x_, x_, st_);
   }
 }
 

@@ -41,7 +41,8 @@ class Session {
  private:
   void ensure_rows(int rows);
   void layer_prefill(int li, int M);
-  bool project_q(const DevTensor* const* ws, float* const* outs, int nseg, int M, int K, const float* resid);
+  bool project_q(const DevTensor* const* ws, float* const* outs, int nseg, int M, int K, const float* resid,
+                 float* kpart = nullptr);
   bool fused_ok(int li) const;
   void decode_args(int li, MvArgs& qkv, MvArgs& o, MvArgs& gate_up, MvArgs& down, int* dts);
   void prepare_step();
@@ -71,6 +72,7 @@ class Session {
   int rows_cap_ = 0;
   float *x_ = nullptr, *xn_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *att_ = nullptr;
   float *g_ = nullptr, *u_ = nullptr, *act_ = nullptr, *tmp_ = nullptr;
+  bool kpart_ok_ = false;  // tmp_ can hold a [rows, hidden] split-K partial
   __half* xs_ = nullptr;  // fp16 (hi, lo) split of the current prefill GEMM input
   float* xsum_ = nullptr;  // its per-32 row sums (Q4_K min term)
   float *xdec_ = nullptr, *xdec2_ = nullptr, *xndec_ = nullptr, *qd_ = nullptr, *kd_ = nullptr, *vd_ = nullptr, *attd_ = nullptr;
