@@ -74,6 +74,15 @@ void launch_dequant(int dt, const void* blocks, size_t nblocks, float* out, hipS
 void launch_embed(int dt, const void* table, size_t hidden, const uint32_t* ids, int n, float scale, float* out,
                   hipStream_t st);
 void launch_rmsnorm(const float* in, const float* w, int rows, int dim, float eps, float* out, hipStream_t st);
+// Producers that also emit a prefill GEMM input: fp16 (hi, lo) planes of their [rows, dim] output
+// and its per-32 sums as an fp16 pair (two planes of rows * dim / 32 halves at `sums`), as
+// launch_split_f16 + launch_block_sums would (dim % 32 == 0, 16-byte aligned rows). A null `out`
+// skips the f32 output.
+void launch_rmsnorm_split(const float* in, const float* w, int rows, int dim, float eps, float* out, __half* hi,
+                          __half* lo, float* sums, hipStream_t st);
+void launch_split_sums(const float* a, int rows, int K, __half* hi, __half* lo, float* sums, hipStream_t st);
+void launch_swiglu_split(const float* g, const float* u, float* out, int rows, int K, __half* hi, __half* lo,
+                         float* sums, hipStream_t st);
 void launch_rope_rows(float* v, int rows, int row_stride, int n_heads, int head_dim, int pos0, const float* cs,
                       int half_pairs, hipStream_t st);
 void launch_rope_table(float* v, int n_heads, int head_dim, int npairs, const float* cs, const int* pos_dev,

@@ -78,6 +78,116 @@ void launch_rmsnorm(const float* in, const float* w, int rows, int dim, float ep
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, st, in, w, dim, eps, out);
 }
 
+// ---- GEMM inputs: fp16 pair planes and per-32 sums emitted by the producing kernel -----------
+// Eight consecutive values v = a[8i .. 8i+7] of a [rows, K] input (K % 32 == 0): hi = fp16(v),
+// lo = fp16(v - hi), and the per-32 sum of the block they belong to, summed in the order the
+// stand-alone per-32 sum pass uses (eight float4 partials (x + y) + (z + w), left to right) and
+// stored as an fp16 pair. The four consecutive lanes of one block exchange their partials by
+// shuffles, so every lane of the wave calls this (`live` masks the stores).
+IEK_DEV void emit_split8(const float (&v)[8], size_t i, bool live, uint4* __restrict__ hi, uint4* __restrict__ lo,
+                         _Float16* __restrict__ sh, _Float16* __restrict__ sl) {
+#pragma clang fp contract(off)
+  _Float16 h[8], l[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    h[k] = (_Float16)v[k];
+    l[k] = (_Float16)(v[k] - (float)h[k]);
+  }
+  auto pk = [](_Float16 a, _Float16 b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  };
+  if (live) {
+    hi[i] = make_uint4(pk(h[0], h[1]), pk(h[2], h[3]), pk(h[4], h[5]), pk(h[6], h[7]));
+    lo[i] = make_uint4(pk(l[0], l[1]), pk(l[2], l[3]), pk(l[4], l[5]), pk(l[6], l[7]));
+  }
+  const float pa = (v[0] + v[1]) + (v[2] + v[3]), pb = (v[4] + v[5]) + (v[6] + v[7]);
+  const int lane = threadIdx.x & 63, base = lane & ~3;
+  float p[8];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    p[2 * q] = __shfl(pa, base + q, 64);
+    p[2 * q + 1] = __shfl(pb, base + q, 64);
+  }
+  if (live && (lane & 3) == 0) {
+    float sum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) sum += p[t];
+    const _Float16 s16 = (_Float16)sum;
+    sh[i / 4] = s16;
+    sl[i / 4] = (_Float16)(sum - (float)s16);
+  }
+}
+
+// rmsnorm (as rmsnorm_kernel) that also emits the GEMM input planes of its output (the f32 output
+// itself only when `out` is set).
+__global__ __launch_bounds__(256) void rmsnorm_split_kernel(const float* in, const float* w, int dim, float eps,
+                                                            float* out, uint4* hi, uint4* lo, _Float16* sh,
+                                                            _Float16* sl) {
+#pragma clang fp contract(off)
+  __shared__ float red[8];
+  const float* x = in + (size_t)blockIdx.x * dim;
+  float* y = out + (size_t)blockIdx.x * dim;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < dim; i += blockDim.x) ss += x[i] * x[i];
+  ss = block_sum256(ss, red);
+  const float rms = sqrtf(ss / (float)dim + eps);
+  const int n8 = dim / 8;
+  for (int i0 = 0; i0 < n8; i0 += 256) {
+    const int e = i0 + threadIdx.x;
+    const bool live = e < n8;
+    float v[8];
+    const int c = live ? e : 0;
+    const float4 xa = reinterpret_cast<const float4*>(x)[2 * c], xb = reinterpret_cast<const float4*>(x)[2 * c + 1];
+    const float4 wa = reinterpret_cast<const float4*>(w)[2 * c], wb = reinterpret_cast<const float4*>(w)[2 * c + 1];
+    v[0] = (xa.x * wa.x) / rms;
+    v[1] = (xa.y * wa.y) / rms;
+    v[2] = (xa.z * wa.z) / rms;
+    v[3] = (xa.w * wa.w) / rms;
+    v[4] = (xb.x * wb.x) / rms;
+    v[5] = (xb.y * wb.y) / rms;
+    v[6] = (xb.z * wb.z) / rms;
+    v[7] = (xb.w * wb.w) / rms;
+    if (live && out) {
+      reinterpret_cast<float4*>(y)[2 * c] = make_float4(v[0], v[1], v[2], v[3]);
+      reinterpret_cast<float4*>(y)[2 * c + 1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    emit_split8(v, (size_t)blockIdx.x * n8 + c, live, hi, lo, sh, sl);
+  }
+}
+
+void launch_rmsnorm_split(const float* in, const float* w, int rows, int dim, float eps, float* out, __half* hi,
+                          __half* lo, float* sums, hipStream_t st) {
+  if (rows <= 0) return;
+  if (dim % 32 != 0 || (reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out)) % 16)
+    fail(ST_OP, "rmsnorm_split: dim % 32 and 16-byte aligned rows");
+  _Float16* s = reinterpret_cast<_Float16*>(sums);
+  const size_t nb = (size_t)rows * (dim / 32);
+  hipLaunchKernelGGL(rmsnorm_split_kernel, dim3(rows), dim3(256), 0, st, in, w, dim, eps, out, (uint4*)hi, (uint4*)lo,
+                     s, s + nb);
+}
+
+// fp16 pair planes and per-32 sums of an existing [rows, K] input in one pass.
+__global__ __launch_bounds__(256) void split_sums_kernel(const float* __restrict__ a, size_t n8, uint4* hi, uint4* lo,
+                                                         _Float16* sh, _Float16* sl) {
+  for (size_t i0 = (size_t)blockIdx.x * 256; i0 < n8; i0 += (size_t)gridDim.x * 256) {
+    const size_t i = i0 + threadIdx.x;
+    const bool live = i < n8;
+    const size_t c = live ? i : 0;
+    const float4 xa = reinterpret_cast<const float4*>(a)[2 * c], xb = reinterpret_cast<const float4*>(a)[2 * c + 1];
+    const float v[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    emit_split8(v, c, live, hi, lo, sh, sl);
+  }
+}
+
+void launch_split_sums(const float* a, int rows, int K, __half* hi, __half* lo, float* sums, hipStream_t st) {
+  if (rows <= 0) return;
+  if (K % 32 != 0 || reinterpret_cast<uintptr_t>(a) % 16) fail(ST_OP, "split_sums: K % 32 and 16-byte aligned input");
+  const size_t n8 = (size_t)rows * (K / 8), nb = n8 / 4;
+  _Float16* s = reinterpret_cast<_Float16*>(sums);
+  const int blocks = (int)std::min<size_t>((n8 + 255) / 256, 4096);
+  hipLaunchKernelGGL(split_sums_kernel, dim3(blocks), dim3(256), 0, st, a, n8, (uint4*)hi, (uint4*)lo, s, s + nb);
+}
+
 // RoPE on adjacent pairs (src/ops/rope.rs:11-59). `cs` holds (cos, sin) per (position, pair),
 // built on the host with the reference's f32 running-product angles and libm cosf/sinf.
 IEK_DEV void rotate(float* v, int p, float c, float s) {
@@ -167,6 +277,54 @@ __global__ void swiglu_kernel(const float* g, const float* u, float* out, size_t
 void launch_swiglu(const float* g, const float* u, float* out, size_t n, hipStream_t st) {
   if (n == 0) return;
   hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, u, out, n);
+}
+
+// swiglu (as swiglu_kernel) over a [rows, K] input that also emits the GEMM input planes (the f32
+// output itself only when `out` is set).
+__global__ __launch_bounds__(256) void swiglu_split_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                           float* __restrict__ out, size_t n8, uint4* hi, uint4* lo,
+                                                           _Float16* sh, _Float16* sl) {
+#pragma clang fp contract(off)
+  for (size_t i0 = (size_t)blockIdx.x * 256; i0 < n8; i0 += (size_t)gridDim.x * 256) {
+    const size_t i = i0 + threadIdx.x;
+    const bool live = i < n8;
+    const size_t c = live ? i : 0;
+    const float4 ga = reinterpret_cast<const float4*>(g)[2 * c], gb = reinterpret_cast<const float4*>(g)[2 * c + 1];
+    const float4 ua = reinterpret_cast<const float4*>(u)[2 * c], ub = reinterpret_cast<const float4*>(u)[2 * c + 1];
+    const float gx[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+    const float ux[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float x = gx[k];
+      float sg;
+      if (x >= 0.0f) {
+        const float z = expf(-x);
+        sg = 1.0f / (1.0f + z);
+      } else {
+        const float z = expf(x);
+        sg = z / (1.0f + z);
+      }
+      v[k] = x * sg * ux[k];
+    }
+    if (live && out) {
+      reinterpret_cast<float4*>(out)[2 * c] = make_float4(v[0], v[1], v[2], v[3]);
+      reinterpret_cast<float4*>(out)[2 * c + 1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    emit_split8(v, c, live, hi, lo, sh, sl);
+  }
+}
+
+void launch_swiglu_split(const float* g, const float* u, float* out, int rows, int K, __half* hi, __half* lo,
+                         float* sums, hipStream_t st) {
+  if (rows <= 0) return;
+  if (K % 32 != 0 || (reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(u) | reinterpret_cast<uintptr_t>(out)) % 16)
+    fail(ST_OP, "swiglu_split: K % 32 and 16-byte aligned inputs");
+  const size_t n8 = (size_t)rows * (K / 8), nb = n8 / 4;
+  _Float16* s = reinterpret_cast<_Float16*>(sums);
+  const int blocks = (int)std::min<size_t>((n8 + 255) / 256, 4096);
+  hipLaunchKernelGGL(swiglu_split_kernel, dim3(blocks), dim3(256), 0, st, g, u, out, n8, (uint4*)hi, (uint4*)lo, s,
+                     s + nb);
 }
 
 // gelu_tanh(g) * u (src/layers/ffn.rs:49-53); gelu_tanh_dev is in common.cuh.

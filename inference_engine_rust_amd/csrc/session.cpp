@@ -211,6 +211,25 @@ static void project(const DevTensor& w, const float* a, const __half* xs, int ro
 // Prefill projections through the scale-factored matrix-core GEMM when every weight qualifies:
 // `a` (M x K) must already be split into xs_ (fp16 pair) and summed per 32 into xsum_.
 // Returns false when the caller should fall back to per-matrix projections.
+// Whether project_q takes these weights (the checks it makes before launching).
+bool Session::quant_ready(const DevTensor* const* ws, int nseg, int M, int K) const {
+  if (M < 2) return false;
+  int dt = -1;
+  for (int i = 0; i < nseg; ++i) {
+    const DevTensor& w = *ws[i];
+    if (w.dims.size() != 2 || (int)w.dims[0] != K) return false;
+    int wdt = w.dtype;
+    const void* p = w.dev;
+    if (w.dev_r && w.dtype_r == DT_Q6K_R) {
+      wdt = DT_Q6K_R;
+      p = w.dev_r;
+    }
+    if ((dt >= 0 && wdt != dt) || !gemm_q_ok(wdt, p, K)) return false;
+    dt = wdt;
+  }
+  return true;
+}
+
 bool Session::project_q(const DevTensor* const* ws, float* const* outs, int nseg, int M, int K, const float* resid,
                         float* kpart) {
   if (M < 2) return false;
@@ -242,15 +261,26 @@ void Session::layer_prefill(int li, int M) {
   const float eps = c.rms_eps;
   // attention sub-layer: pre-norm, projections, RoPE at prompt positions 0..M-1, KV append at the
   // cache's current length, causal attention within the prompt, O projection + residual.
-  // fp16 pair of a GEMM input (only when it has more than one row and a width the split takes)
+  // fp16 pair (and per-32 sums) of a GEMM input, only when it has more than one row and a width
+  // the split takes; the pre-norms and SwiGLU emit them as they write their output
+  const bool wide = M >= 2;
   auto split = [&](const float* a, int K) -> const __half* {
-    if (M < 2 || K % 32 != 0) return nullptr;
-    launch_split_f16(a, (size_t)M * K, xs_, xs_ + (size_t)M * K, st_);
-    launch_block_sums(a, M, K, xsum_, st_);
+    if (!wide || K % 32 != 0) return nullptr;
+    launch_split_sums(a, M, K, xs_, xs_ + (size_t)M * K, xsum_, st_);
     return xs_;
   };
-  launch_rmsnorm(x_, (const float*)L.attn_norm.dev, M, H_, eps, xn_, st_);
-  const __half* xs = split(xn_, H_);
+  // (the f32 output is written only when a consumer may fall back to it)
+  auto norm_split = [&](const DevTensor& w, bool need_f32) -> const __half* {
+    if (!wide || H_ % 32 != 0) {
+      launch_rmsnorm(x_, (const float*)w.dev, M, H_, eps, xn_, st_);
+      return nullptr;
+    }
+    launch_rmsnorm_split(x_, (const float*)w.dev, M, H_, eps, need_f32 ? xn_ : nullptr, xs_, xs_ + (size_t)M * H_,
+                         xsum_, st_);
+    return xs_;
+  };
+  const DevTensor* wqkv[3] = {&L.wq, &L.wk, &L.wv};
+  const __half* xs = norm_split(L.attn_norm, !quant_ready(wqkv, 3, M, H_));
   {
     const DevTensor* ws[3] = {&L.wq, &L.wk, &L.wv};
     float* outs[3] = {q_, k_, v_};
@@ -280,22 +310,29 @@ void Session::layer_prefill(int li, int M) {
       project(L.wo, att_, xa, M, qd, H_, x_, x_, st_);
   }
   // FFN sub-layer: pre-norm, gate/up, SwiGLU, down + residual.
-  launch_rmsnorm(x_, (const float*)L.ffn_norm.dev, M, H_, eps, xn_, st_);
+  const DevTensor* wgu[2] = {&L.gate, &L.up};
+  xs = norm_split(L.ffn_norm, M == 1 || !quant_ready(wgu, 2, M, H_));
+  const __half* xa = nullptr;
   if (M == 1 && L.gate.dtype == L.up.dtype) {
     MvSegDesc s[2] = {{L.gate.dev, act_, nullptr, S.ffn_dim}, {L.up.dev, nullptr, nullptr, S.ffn_dim}};
     launch_matvec(L.gate.dtype, s, 2, xn_, H_, 2, st_);
   } else {
-    xs = split(xn_, H_);
     const DevTensor* ws[2] = {&L.gate, &L.up};
     float* outs[2] = {g_, u_};
     if (!xs || !project_q(ws, outs, 2, M, H_, nullptr)) {
       project(L.gate, xn_, xs, M, H_, S.ffn_dim, g_, nullptr, st_);
       project(L.up, xn_, xs, M, H_, S.ffn_dim, u_, nullptr, st_);
     }
-    launch_swiglu(g_, u_, act_, (size_t)M * S.ffn_dim, st_);
+    if (wide && S.ffn_dim % 32 == 0) {
+      const DevTensor* wd[1] = {&L.down};
+      launch_swiglu_split(g_, u_, quant_ready(wd, 1, M, S.ffn_dim) ? nullptr : act_, M, S.ffn_dim, xs_,
+                          xs_ + (size_t)M * S.ffn_dim, xsum_, st_);
+      xa = xs_;
+    } else {
+      launch_swiglu(g_, u_, act_, (size_t)M * S.ffn_dim, st_);
+    }
   }
   {
-    const __half* xa = split(act_, S.ffn_dim);
     const DevTensor* ws[1] = {&L.down};
     float* outs[1] = {x_};
     if (!xa || !project_q(ws, outs, 1, M, S.ffn_dim, x_, kpart_ok_ ? tmp_ : nullptr))
@@ -502,8 +539,7 @@ void Session::layer_decode_unfused(int li) {
 // the split takes; null otherwise.
 const __half* Session::split_rows(const float* a, int M, int K) {
   if (M < 2 || K % 32 != 0) return nullptr;
-  launch_split_f16(a, (size_t)M * K, xs_, xs_ + (size_t)M * K, st_);
-  launch_block_sums(a, M, K, xsum_, st_);
+  launch_split_sums(a, M, K, xs_, xs_ + (size_t)M * K, xsum_, st_);
   return xs_;
 }
 

@@ -43,6 +43,7 @@ class Session {
   void layer_prefill(int li, int M);
   bool project_q(const DevTensor* const* ws, float* const* outs, int nseg, int M, int K, const float* resid,
                  float* kpart = nullptr);
+  bool quant_ready(const DevTensor* const* ws, int nseg, int M, int K) const;
   bool fused_ok(int li) const;
   void decode_args(int li, MvArgs& qkv, MvArgs& o, MvArgs& gate_up, MvArgs& down, int* dts);
   void prepare_step();
