@@ -490,11 +490,15 @@ IEK_DEV void kq_deq(int p, int h, const typename T::Hdr& hd, const typename T::R
   }
 }
 
-template <class T, int WGM, int WGN, int DA>
-__global__ __launch_bounds__(256) void gemm_kq_kernel(GemmQArgs g) {
-  constexpr int BM = 64 * WGM, BN = 64 * WGN;
+// TM: 16-row MFMA tiles per wave along M (a wave owns 16 TM x 64); WGM x WGN waves.
+template <class T, int WGM, int WGN, int DA, int TM>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_kq_kernel(GemmQArgs g) {
+  constexpr int NT = 64 * WGM * WGN;  // threads
+  constexpr int WR = 16 * TM;         // rows per wave
+  constexpr int BM = WR * WGM, BN = 64 * WGN;
   constexpr int PL = BM * 8;        // 16-byte chunks per plane per stage (BM rows x 64 halves)
-  constexpr int AR = PL / 256;      // chunk rows per thread per plane per stage
+  constexpr int AR = PL / NT;       // chunk rows per thread per plane per stage
+  static_assert(AR >= 1 && PL % NT == 0, "activation tile must divide over the threads");
   constexpr int DB = 2;             // stages of raw weight bytes in flight and (DA) of activation
                                     // stages; both divide the 4 stages of a superblock, so ring
                                     // slots are static
@@ -534,11 +538,12 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(GemmQArgs g) {
   for (int j = 0; j < 4; ++j) vb[j] = (uint32_t)((size_t)min(n0 + 64 * wn + 16 * j + lr, N - 1) * g.row_bytes);
   uint32_t va[AR];  // activation rows staged by this thread (both planes)
 #pragma unroll
-  for (int u = 0; u < AR; ++u) va[u] = (uint32_t)(min(m0 + (tid >> 3) + 32 * u, M - 1) * K + 8 * (tid & 7)) * 2u;
-  uint32_t vx[4];  // per-32 sums: k group 0 reads the hi plane, 1 the lo plane
+  for (int u = 0; u < AR; ++u)
+    va[u] = (uint32_t)(min(m0 + (tid >> 3) + (NT / 8) * u, M - 1) * K + 8 * (tid & 7)) * 2u;
+  uint32_t vx[TM];  // per-32 sums: k group 0 reads the hi plane, 1 the lo plane
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    vx[i] = (uint32_t)(min(m0 + 64 * wm + 16 * i + lr, M - 1) * kb + ((lg & 1) ? M * kb : 0)) * 2u;
+  for (int i = 0; i < TM; ++i)
+    vx[i] = (uint32_t)(min(m0 + WR * wm + 16 * i + lr, M - 1) * kb + ((lg & 1) ? M * kb : 0)) * 2u;
 
   struct ASlot {
     qu4_t a[2 * AR];
@@ -546,7 +551,7 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(GemmQArgs g) {
   ASlot ra[DA];
   typename T::Raw rb[DB];
   typename T::Hdr hdr, hdrn;  // factors of the current and the next superblock
-  qu4_t xsv[4];
+  qu4_t xsv[TM];
 
   auto fetch_a = [&](int kt, ASlot& sl) {
 #pragma unroll
@@ -559,19 +564,19 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(GemmQArgs g) {
     const int c = tid & 7;
 #pragma unroll
     for (int u = 0; u < AR; ++u) {
-      const int row = (tid >> 3) + 32 * u;
+      const int row = (tid >> 3) + (NT / 8) * u;
       As[buf][row * 8 + (c ^ (row & 7))] = sl.a[u];
       As[buf][PL + row * 8 + (c ^ (row & 7))] = sl.a[AR + u];
     }
   };
   auto fetch_xs = [&](int sb) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xsv[i] = ld_b128(rxs, vx[i], 16u * sb);
+    for (int i = 0; i < TM; ++i) xsv[i] = ld_b128(rxs, vx[i], 16u * sb);
   };
 
-  qf4_t acc[4][4], part[4][4];
+  qf4_t acc[TM][4], part[TM][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       acc[i][j] = qf4_t{0.f, 0.f, 0.f, 0.f};
@@ -623,14 +628,14 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(GemmQArgs g) {
         // activation operands one m-tile ahead of the MFMAs that use them
         qu4_t ah[2], al[2];
         auto rd = [&](int i, qu4_t& x, qu4_t& y) {
-          const int row = 64 * wm + 16 * i + lr, ch = row * 8 + ((4 * h + lg) ^ (row & 7));
+          const int row = WR * wm + 16 * i + lr, ch = row * 8 + ((4 * h + lg) ^ (row & 7));
           x = As[buf][ch];
           y = As[buf][PL + ch];
         };
         rd(0, ah[0], al[0]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (i < 3) rd(i + 1, ah[(i + 1) & 1], al[(i + 1) & 1]);
+        for (int i = 0; i < TM; ++i) {
+          if (i < TM - 1) rd(i + 1, ah[(i + 1) & 1], al[(i + 1) & 1]);
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             part[i][j] = mfma16(ah[i & 1], bh[j], (p == 0 && h == 0) ? qf4_t{0.f, 0.f, 0.f, 0.f} : part[i][j]);
@@ -649,14 +654,14 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(GemmQArgs g) {
             const float dmin = T::dmin(hdr, j);
             const qu4_t mb = T::mins(hdr, j, lg < 2);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < TM; ++i) {
               const qf4_t mp = mfma16(xsv[i], mb, qf4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
               for (int r = 0; r < 4; ++r) acc[i][j][r] = (acc[i][j][r] + d * part[i][j][r]) - dmin * mp[r];
             }
           } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
               for (int r = 0; r < 4; ++r) acc[i][j][r] += d * part[i][j][r];
           }
@@ -670,13 +675,13 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(GemmQArgs g) {
   const float* resid = s == 0 && ks == 0 ? g.resid : nullptr;
   float* dst = ks == 0 ? out : g.kpart;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int n = n0 + 64 * wn + 16 * j + lr;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = m0 + 64 * wm + 16 * i + 4 * lg + r;
+        const int m = m0 + WR * wm + 16 * i + 4 * lg + r;
         if (m < M && n < N) {
           float v = acc[i][j][r];
           if (resid) v = resid[(size_t)m * N + n] + v;
@@ -738,9 +743,9 @@ static void gemm_q_launch(GemmQArgs g, hipStream_t st) {
   hipLaunchKernelGGL((gemm_q_kernel<DT, BM, BN>), dim3(tiles), dim3(256), 0, st, g);
 }
 
-template <class T, int WGM, int WGN, int DA>
+template <class T, int WGM, int WGN, int DA, int TM = 4>
 static void gemm_kq_launch(GemmQArgs g, hipStream_t st) {
-  constexpr int BM = 64 * WGM, BN = 64 * WGN;
+  constexpr int BM = 16 * TM * WGM, BN = 64 * WGN;
   int t = 0;
   for (int i = 0; i < g.nseg; ++i) {
     g.tile_start[i] = t;
@@ -753,7 +758,7 @@ static void gemm_kq_launch(GemmQArgs g, hipStream_t st) {
   // down projections at a 512-token prompt fill half the chip)
   const size_t mn = (size_t)g.M * g.n[0];
   g.ksplit = (g.kpart && g.nseg == 1 && 2 * tiles <= num_cus() && g.K / QK_K >= 2 && mn % 4 == 0) ? 2 : 1;
-  hipLaunchKernelGGL((gemm_kq_kernel<T, WGM, WGN, DA>), dim3(tiles * g.ksplit), dim3(256), 0, st, g);
+  hipLaunchKernelGGL((gemm_kq_kernel<T, WGM, WGN, DA, TM>), dim3(tiles * g.ksplit), dim3(64 * WGM * WGN), 0, st, g);
   if (g.ksplit == 2) {
     const int blocks = (int)std::min<size_t>((mn / 4 + 255) / 256, 2048);
     hipLaunchKernelGGL(add_part_kernel, dim3(blocks), dim3(256), 0, st, g.out[0], g.kpart, mn / 4);
@@ -764,7 +769,8 @@ static void gemm_kq_launch(GemmQArgs g, hipStream_t st) {
 // activation tile is shared) with one activation stage in flight: measured 15% faster than
 // 128 x 128 at the Mistral-7B prefill shapes, and deeper activation prefetch gained nothing.
 // IEK_GEMM_KQ_TILE selects the others (tuning): 1: 128 x 128, 2: 128 x 128 with two stages,
-// 3 / 4: 64 x 256 with two / four stages.
+// 3 / 4: 64 x 256 with two / four stages, 5 / 6: eight waves of 32 x 64 (two waves per SIMD; the
+// weight decode per MFMA doubles, measured 25% slower).
 template <class T>
 static void gemm_kq(GemmQArgs g, hipStream_t st) {
   static int force = -2;
@@ -777,6 +783,8 @@ static void gemm_kq(GemmQArgs g, hipStream_t st) {
     case 2: gemm_kq_launch<T, 2, 2, 2>(g, st); break;
     case 3: gemm_kq_launch<T, 1, 4, 2>(g, st); break;
     case 4: gemm_kq_launch<T, 1, 4, 4>(g, st); break;
+    case 5: gemm_kq_launch<T, 2, 4, 1, 2>(g, st); break;  // 32 x 64 wave tiles, eight waves
+    case 6: gemm_kq_launch<T, 4, 2, 1, 2>(g, st); break;
     default: gemm_kq_launch<T, 1, 4, 1>(g, st); break;
   }
 }
