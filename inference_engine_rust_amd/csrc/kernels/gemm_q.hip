@@ -491,8 +491,11 @@ IEK_DEV void kq_deq(int p, int h, const typename T::Hdr& hd, const typename T::R
 }
 
 // TM: 16-row MFMA tiles per wave along M (a wave owns 16 TM x 64); WGM x WGN waves.
-template <class T, int WGM, int WGN, int DA, int TM>
-__global__ __launch_bounds__(64 * WGM * WGN) void gemm_kq_kernel(GemmQArgs g) {
+// OCC: waves per SIMD the register allocation must allow (2 caps each wave at 256 registers).
+// FS: apply d per stage (each tile's stage sum is a short MFMA chain folded into the running sum
+// straight away) instead of per superblock (a second full set of partial accumulators).
+template <class T, int WGM, int WGN, int DA, int TM, int OCC = 1, bool FS = false>
+__global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kq_kernel(GemmQArgs g) {
   constexpr int NT = 64 * WGM * WGN;  // threads
   constexpr int WR = 16 * TM;         // rows per wave
   constexpr int BM = WR * WGM, BN = 64 * WGN;
@@ -616,6 +619,63 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kq_kernel(GemmQArgs g) {
       if (p == 0) T::fetch_hdr(rw, vb, lg, min(sb + 1, sb_hi - 1), nsb, hdrn);
       if (T::MINS && p == 2) fetch_xs(sb);
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (FS) {
+        qu4_t bh[2][4], bl[2][4];
+        kq_deq<T>(p, 0, hdr, rb[p % DB], bh[0], bl[0]);
+        kq_deq<T>(p, 1, hdr, rb[p % DB], bh[1], bl[1]);
+        __builtin_amdgcn_sched_barrier(0);
+        T::fetch(rw, vb, lg, min(kt + DB, kt_last), rb[p % DB]);
+        __builtin_amdgcn_sched_barrier(0);
+        float dj[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dj[j] = T::d(hdr, j);
+        // activation operands of both k-halves, one m-tile ahead of the MFMAs that use them
+        qu4_t a4[2][4];
+        auto rd4 = [&](int i, qu4_t (&x)[4]) {
+          const int row = WR * wm + 16 * i + lr;
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const int ch = row * 8 + ((4 * hh + lg) ^ (row & 7));
+            x[2 * hh] = As[buf][ch];
+            x[2 * hh + 1] = As[buf][PL + ch];
+          }
+        };
+        rd4(0, a4[0]);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          if (i < TM - 1) rd4(i + 1, a4[(i + 1) & 1]);
+          const qu4_t(&x)[4] = a4[i & 1];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            qf4_t t = mfma16(x[0], bh[0][j], qf4_t{0.f, 0.f, 0.f, 0.f});
+            t = mfma16(x[1], bh[0][j], t);
+            if constexpr (T::LO) t = mfma16(x[0], bl[0][j], t);
+            t = mfma16(x[2], bh[1][j], t);
+            t = mfma16(x[3], bh[1][j], t);
+            if constexpr (T::LO) t = mfma16(x[2], bl[1][j], t);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][j][r] += dj[j] * t[r];
+          }
+        }
+        if (p == 3) {
+          if constexpr (T::MINS) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float dmin = T::dmin(hdr, j);
+              const qu4_t mb = T::mins(hdr, j, lg < 2);
+#pragma unroll
+              for (int i = 0; i < TM; ++i) {
+                const qf4_t mp = mfma16(xsv[i], mb, qf4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[i][j][r] -= dmin * mp[r];
+              }
+            }
+          }
+          hdr = hdrn;
+        }
+        __syncthreads();
+        continue;
+      }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         qu4_t bh[4], bl[4];
@@ -743,7 +803,7 @@ static void gemm_q_launch(GemmQArgs g, hipStream_t st) {
   hipLaunchKernelGGL((gemm_q_kernel<DT, BM, BN>), dim3(tiles), dim3(256), 0, st, g);
 }
 
-template <class T, int WGM, int WGN, int DA, int TM = 4>
+template <class T, int WGM, int WGN, int DA, int TM = 4, int OCC = 1, bool FS = false>
 static void gemm_kq_launch(GemmQArgs g, hipStream_t st) {
   constexpr int BM = 16 * TM * WGM, BN = 64 * WGN;
   int t = 0;
@@ -758,7 +818,8 @@ static void gemm_kq_launch(GemmQArgs g, hipStream_t st) {
   // down projections at a 512-token prompt fill half the chip)
   const size_t mn = (size_t)g.M * g.n[0];
   g.ksplit = (g.kpart && g.nseg == 1 && 2 * tiles <= num_cus() && g.K / QK_K >= 2 && mn % 4 == 0) ? 2 : 1;
-  hipLaunchKernelGGL((gemm_kq_kernel<T, WGM, WGN, DA, TM>), dim3(tiles * g.ksplit), dim3(64 * WGM * WGN), 0, st, g);
+  hipLaunchKernelGGL((gemm_kq_kernel<T, WGM, WGN, DA, TM, OCC, FS>), dim3(tiles * g.ksplit), dim3(64 * WGM * WGN),
+                     0, st, g);
   if (g.ksplit == 2) {
     const int blocks = (int)std::min<size_t>((mn / 4 + 255) / 256, 2048);
     hipLaunchKernelGGL(add_part_kernel, dim3(blocks), dim3(256), 0, st, g.out[0], g.kpart, mn / 4);
@@ -768,23 +829,42 @@ static void gemm_kq_launch(GemmQArgs g, hipStream_t st) {
 // K-quant tile: 64 x 256 (1 x 4 waves; each wave streams its own 64 weight columns, the
 // activation tile is shared) with one activation stage in flight: measured 15% faster than
 // 128 x 128 at the Mistral-7B prefill shapes, and deeper activation prefetch gained nothing.
-// IEK_GEMM_KQ_TILE selects the others (tuning): 1: 128 x 128, 2: 128 x 128 with two stages,
-// 3 / 4: 64 x 256 with two / four stages, 5 / 6: eight waves of 32 x 64 (two waves per SIMD; the
-// weight decode per MFMA doubles, measured 25% slower).
+// Q4_K GEMMs with at least two tiles per CU (gate/up at a 512-token prompt: 896 tiles) apply d per
+// stage, which frees the superblock partials so two waves share each SIMD: 7% faster there, but
+// slower on grids that then pack two workgroups on some CUs and none on others. Q6_K's fp16
+// weight pairs do not fit two waves per SIMD. IEK_GEMM_KQ_TILE forces a shape (tuning): 0: the
+// default 64 x 256, 1: 128 x 128, 2: 128 x 128 with two activation stages, 3 / 4: 64 x 256 with
+// two / four, 5 / 6: eight waves of 32 x 64 (25% slower), 7 / 8: d per stage at one / two waves
+// per SIMD.
 template <class T>
 static void gemm_kq(GemmQArgs g, hipStream_t st) {
   static int force = -2;
   if (force == -2) {
     const char* e = getenv("IEK_GEMM_KQ_TILE");
-    force = e ? atoi(e) : 0;
+    force = e ? atoi(e) : -1;
+  }
+  if (force < 0) {
+    size_t nt = 0;
+    for (int i = 0; i < g.nseg; ++i) nt += (g.n[i] + 255) / 256;
+    const size_t tiles = nt * (size_t)((g.M + 63) / 64);
+    if constexpr (T::MINS) {
+      if (tiles >= 2 * (size_t)num_cus()) {
+        gemm_kq_launch<T, 1, 4, 1, 4, 2, true>(g, st);
+        return;
+      }
+    }
+    gemm_kq_launch<T, 1, 4, 1>(g, st);
+    return;
   }
   switch (force) {
     case 1: gemm_kq_launch<T, 2, 2, 1>(g, st); break;
     case 2: gemm_kq_launch<T, 2, 2, 2>(g, st); break;
     case 3: gemm_kq_launch<T, 1, 4, 2>(g, st); break;
     case 4: gemm_kq_launch<T, 1, 4, 4>(g, st); break;
-    case 5: gemm_kq_launch<T, 2, 4, 1, 2>(g, st); break;  // 32 x 64 wave tiles, eight waves
+    case 5: gemm_kq_launch<T, 2, 4, 1, 2>(g, st); break;
     case 6: gemm_kq_launch<T, 4, 2, 1, 2>(g, st); break;
+    case 7: gemm_kq_launch<T, 1, 4, 1, 4, 1, true>(g, st); break;
+    case 8: gemm_kq_launch<T, 1, 4, 1, 4, 2, true>(g, st); break;
     default: gemm_kq_launch<T, 1, 4, 1>(g, st); break;
   }
 }
