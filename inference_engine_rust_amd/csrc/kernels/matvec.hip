@@ -68,6 +68,11 @@ __global__ __launch_bounds__(256) void mv_stream(MvArgs args) {
   extern __shared__ __align__(16) float lds[];
   (void)args;
   const MvArgs& a = *(const MvArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+  // Every argument the prologue branches on or addresses with, loaded in one batch: read lazily,
+  // each branch would wait for its own scalar load before issuing the next.
+  asm volatile("" ::"s"(a.epi), "s"(a.nseg), "s"(a.K), "s"(a.seg_start[1]), "s"(a.seg_start[2]),
+               "s"(a.seg_start[3]), "s"(a.n[0]), "s"(a.x), "s"(a.norm_w), "s"(a.resid), "s"(a.w[0]), "s"(a.w[1]),
+               "s"(a.w[2]), "s"(a.pos), "s"(a.rope_cs), "s"(a.npairs), "s"(gridDim.x));
   const int pos = a.epi == EPI_QKV ? __builtin_amdgcn_readfirstlane(*a.pos) : 0;
   typename Tr::template Buf<DUAL ? 2 * R : R> A;
   mv_body<Tr, R, DUAL>(a, lds, pos, A, false);
