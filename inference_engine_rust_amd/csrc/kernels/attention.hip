@@ -20,6 +20,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
                                                           int n_heads, int n_kv, int ctx, const int* pos_dev,
                                                           int window, float scale, int nsplit, int spc) {
   __shared__ __align__(16) char smem[AttnSmem<HD>::BYTES];
+  // all arguments in one batch of scalar loads, ahead of the position they depend on
+  asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(part), "s"(out), "s"(counters), "s"(n_heads), "s"(n_kv), "s"(ctx),
+               "s"(pos_dev), "s"(window), "s"(scale), "s"(nsplit), "s"(spc));
   attn_chunk_f16<HD>(q, kc, vc, part, out, counters, n_heads, n_kv, ctx, *pos_dev + 1, window, scale, nsplit,
                      blockIdx.x, blockIdx.y, spc, smem);
 }
@@ -38,6 +41,9 @@ __global__ __launch_bounds__(256) void attn_decode_f32_kernel(const float* __res
                                                               int window, float scale, int nsplit) {
   constexpr int PD = HD < 256 ? HD : 256;  // dims per staged piece
   constexpr int NP = HD / PD;
+  // all arguments in one batch of scalar loads, ahead of the position they depend on
+  asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(part), "s"(out), "s"(counters), "s"(n_heads), "s"(n_kv), "s"(ctx),
+               "s"(pos_dev), "s"(window), "s"(scale), "s"(nsplit));
   constexpr int ROW = PD + 4;               // padded LDS row (floats)
   constexpr int DPP = PD / 64;              // dims per lane per piece in P.V
   constexpr int F4 = SPLIT * PD / 4 / 256;  // float4 per thread per piece
