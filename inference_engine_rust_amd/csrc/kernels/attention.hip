@@ -47,9 +47,13 @@ __global__ __launch_bounds__(256) void attn_decode_f32_kernel(const float* __res
   constexpr int ROW = PD + 4;               // padded LDS row (floats)
   constexpr int DPP = PD / 64;              // dims per lane per piece in P.V
   constexpr int F4 = SPLIT * PD / 4 / 256;  // float4 per thread per piece
-  const int kvh = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = n_heads / n_kv;
+  // query heads split over HG workgroups per (KV head, slice) when the group has 8: each
+  // workgroup stages the slice and runs one head per wave
+  const int HG = G == 8 ? 2 : 1, GH = G / HG;
+  const int kvh = blockIdx.x / HG, hg = blockIdx.x % HG, gb = hg * GH;
+  const int sp = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int total = *pos_dev + 1;
   const int jmin = (window > 0 && total > window) ? total - window : 0;
   const int j0 = max(sp * SPLIT, jmin), j1 = min(total, (sp + 1) * SPLIT);
@@ -77,14 +81,14 @@ __global__ __launch_bounds__(256) void attn_decode_f32_kernel(const float* __res
     }
     __syncthreads();
   };
-  for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = q[(size_t)(kvh * G) * HD + i];
+  for (int i = tid; i < GH * HD; i += 256) qs[i / HD][i % HD] = q[(size_t)(kvh * G + gb) * HD + i];
   float sc[2] = {0.f, 0.f};
   for (int p = 0; p < NP; ++p) {
     stage_piece(kb, p);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int g = wave + 4 * t;
-      if (g < G) {
+      if (g < GH) {
         float acc = 0.f;
 #pragma unroll 8
         for (int d = 0; d < PD; d += 4) {
@@ -101,7 +105,7 @@ __global__ __launch_bounds__(256) void attn_decode_f32_kernel(const float* __res
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int g = wave + 4 * t;
-    if (g < G) {
+    if (g < GH) {
       const float s = valid ? sc[t] * scale : -INFINITY;
       m[t] = wave_max(s);
       const float pr = valid ? expf(s - m[t]) : 0.f;
@@ -122,7 +126,7 @@ __global__ __launch_bounds__(256) void attn_decode_f32_kernel(const float* __res
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int g = wave + 4 * t;
-      if (g < G) {
+      if (g < GH) {
 #pragma unroll 8
         for (int j = 0; j < SPLIT; ++j) {
           const float pj = ps[g][j];
@@ -135,8 +139,8 @@ __global__ __launch_bounds__(256) void attn_decode_f32_kernel(const float* __res
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int g = wave + 4 * t;
-    if (g < G) {
-      float* pr = part + ((size_t)(kvh * G + g) * nsplit + sp) * (HD + 2);
+    if (g < GH) {
+      float* pr = part + ((size_t)(kvh * G + gb + g) * nsplit + sp) * (HD + 2);
       if (lane == 0) {
         pr[0] = m[t];
         pr[1] = l[t];
@@ -149,7 +153,8 @@ __global__ __launch_bounds__(256) void attn_decode_f32_kernel(const float* __res
   }
   __shared__ int last;
   __shared__ float wsl[4 * 256];
-  merge_if_last<HD>(part, out, counters, kvh, G, nsplit, jmin / SPLIT, (total + SPLIT - 1) / SPLIT, wave, &last, wsl);
+  merge_if_last<HD>(part, out, counters, kvh, G, nsplit, jmin / SPLIT, (total + SPLIT - 1) / SPLIT, wave, &last, wsl,
+                    gb, GH, kvh * HG + hg);
 }
 
 template <int HD>
@@ -157,8 +162,10 @@ static void attn_decode_hd(dim3 grid, hipStream_t st, const float* q, const void
                            float* out, float* part, int* counters, int n_heads, int n_kv, int ctx, const int* pos_dev,
                            int window, float scale, int nsplit) {
   if (kv_f32) {
-    hipLaunchKernelGGL(attn_decode_f32_kernel<HD>, grid, dim3(256), 0, st, q, (const float*)kc, (const float*)vc, part,
-                       out, counters, n_heads, n_kv, ctx, pos_dev, window, scale, nsplit);
+    const int hgroups = n_heads / n_kv == 8 ? 2 : 1;  // the kernel's query-head split
+    hipLaunchKernelGGL(attn_decode_f32_kernel<HD>, dim3(grid.x * hgroups, grid.y), dim3(256), 0, st, q,
+                       (const float*)kc, (const float*)vc, part, out, counters, n_heads, n_kv, ctx, pos_dev, window,
+                       scale, nsplit);
   } else {
     // fp16 cache: chunks of spc slices; one partial slot per chunk
     static int target = -1;

@@ -75,8 +75,13 @@ IEK_DEV void merge_head(const float* __restrict__ part, float* __restrict__ out,
 // partials are read. The counter is reset for the next launch.
 // s0 .. nlive-1 are the live partial slots of the KV head.
 template <int HD, bool COH = false>
+// The last workgroup to arrive on counters[cidx] merges query heads [gb, gb + gn) of KV head kvh
+// (G query heads per KV head).
 IEK_DEV void merge_if_last(const float* __restrict__ part, float* __restrict__ out, int* __restrict__ counters,
-                           int kvh, int G, int nsplit, int s0, int nlive, int wave, int* last_s, float* wsl) {
+                           int kvh, int G, int nsplit, int s0, int nlive, int wave, int* last_s, float* wsl,
+                           int gb = 0, int gn = -1, int cidx = -1) {
+  if (gn < 0) gn = G;
+  if (cidx < 0) cidx = kvh;
   int& last = *last_s;
   // every wave's partial stores complete before thread 0's release (the workgroup barrier alone
   // does not wait for global stores on this target)
@@ -85,15 +90,16 @@ IEK_DEV void merge_if_last(const float* __restrict__ part, float* __restrict__ o
   if (threadIdx.x == 0) {
     // COH: the partials went out with coherent stores and were waited for above, so a relaxed
     // count (no L2 write-back / invalidate) orders them
-    const int old = COH ? __hip_atomic_fetch_add(&counters[kvh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                        : __hip_atomic_fetch_add(&counters[kvh], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const int old = COH ? __hip_atomic_fetch_add(&counters[cidx], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                        : __hip_atomic_fetch_add(&counters[cidx], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     last = old == nlive - s0 - 1;
-    if (last) __hip_atomic_store(&counters[kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (last) __hip_atomic_store(&counters[cidx], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!last) return;
   if (!COH) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  for (int g = wave; g < G; g += 4) merge_head<HD, COH>(part, out, kvh * G + g, nsplit, s0, nlive, wsl + 256 * wave);
+  for (int g = gb + wave; g < gb + gn; g += 4)
+    merge_head<HD, COH>(part, out, kvh * G + g, nsplit, s0, nlive, wsl + 256 * wave);
 }
 
 // LDS of one slice item: K rows (padded), V rows (HD <= 256), the group's q, the wave's

@@ -91,7 +91,7 @@ Session::Session(Model* m) : m_(m) {
   d_gen_ = dev_alloc<uint32_t>(ctx_ + 1);
   d_key_ = dev_alloc<unsigned long long>(1);
   d_flag_ = dev_alloc<int>(1);
-  d_cnt_ = dev_alloc<int>(c.n_kv_heads);
+  d_cnt_ = dev_alloc<int>(2 * c.n_kv_heads);  // per (KV head, query-head group) arrival counters
   if (gemma_ && c.ple_dim > 0) {
     const size_t pack = (size_t)c.n_layers * c.ple_dim;
     ple_tokd_ = dev_alloc<float>(pack);
@@ -100,7 +100,7 @@ Session::Session(Model* m) : m_(m) {
   }
   launch_fill_u64(d_key_, 0ull, 1, st_);
   launch_fill_i32(d_flag_, 0, 1, st_);
-  launch_fill_i32(d_cnt_, 0, c.n_kv_heads, st_);
+  launch_fill_i32(d_cnt_, 0, 2 * c.n_kv_heads, st_);
   d_bar_ = dev_alloc<unsigned>(step_bar_words());
   d_err_ = dev_alloc<int>(1);
   launch_fill_i32((int*)d_bar_, 0, step_bar_words(), st_);

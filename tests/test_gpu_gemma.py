@@ -108,6 +108,29 @@ def test_gemma_greedy_tokens_and_logits(g0_gpu, g0_orc):
             np.testing.assert_allclose(kg, kr, rtol=1e-4, atol=2e-4)
 
 
+def test_gemma_decode_eight_query_heads_per_kv_head(gpu, model_dir):
+    """A GQA group of 8 (as in the Gemma-4-E2B shape): the f32-cache decode attention splits the
+    group's query heads over two workgroups per slice, each with its own merge."""
+    spec = synth.preset("g0", n_heads=8)
+    p = str(model_dir / "g0_h8.gguf")
+    synth.write_gemma4(p, spec, seed=4)
+    m, om = E.LoadedModel.load(p), O.Model(p)
+    assert m.config.n_heads // m.config.n_kv_heads == 8
+    prompt = synth.prompt_ids(4, 9, spec.vocab)
+    s, r = E.InferenceSession(m), O.Session(om)
+    s.prefill(prompt)
+    r.prefill(prompt)
+    worst = 0.0
+    for step in range(12):  # past the window (16) into the second window
+        lg, lr = s.logits_last_token(), r.logits()
+        worst = max(worst, rel_l2(lg, lr))
+        t = E.greedy_next_token(s)
+        assert t == O.argmax(lr), f"step {step}"
+        s.decode_token(t)
+        r.decode(t)
+    assert worst < LOGIT_REL_L2, worst
+
+
 def test_gemma_graph_generate_matches_stepwise(g0_gpu):
     prompt = synth.prompt_ids(2, 9, SPEC.vocab)
     a = E.InferenceSession(g0_gpu)
