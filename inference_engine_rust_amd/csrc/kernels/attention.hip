@@ -173,7 +173,7 @@ static void attn_decode_hd(dim3 grid, hipStream_t st, const float* q, const void
       const char* e = getenv("IEK_ATTN_CHUNKS");
       target = e ? std::max(1, atoi(e)) : 32;
     }
-    const int spc = attn_slices_per_chunk(nsplit * SPLIT, target);
+    const int spc = attn_slices_per_chunk(nsplit * SPLIT, window, target);
     const int nchunk = (nsplit + spc - 1) / spc;
     hipLaunchKernelGGL(attn_decode_kernel<HD>, dim3(grid.x, nchunk), dim3(256), 0, st, q, (const __half*)kc,
                        (const __half*)vc, part, out, counters, n_heads, n_kv, ctx, pos_dev, window, scale, nchunk,

@@ -17,21 +17,44 @@ constexpr int SPLIT = 64;
 // [DPL*l, DPL*l + DPL). Slices publish (max, sum, o[]) partials; the last workgroup of each KV
 // head to finish merges its query heads (counted with an agent-scope acq_rel atomic per KV head).
 // Merge of the live slice partials of query head h by one wave: global (max, sum) over slices,
-// then each lane folds its head dims of every slice with the rescaled weights.
+// then each lane folds its head dims of every slice with the rescaled weights. One round trip
+// fetches lane s's (max, sum) pair together with the first batch of o rows; further batches
+// follow only for more than B live slots.
 template <int HD, bool COH = false>
 IEK_DEV void merge_head(const float* __restrict__ part, float* __restrict__ out, int h, int nsplit, int s0, int nlive,
                         float* wsl) {
   constexpr int DPL = HD / 64;
+  constexpr int B = DPL >= 8 ? 4 : 32 / DPL;  // o rows per batch (32 floats per lane in flight)
   const int lane = threadIdx.x & 63;
-  const float* pr = part + (size_t)h * nsplit * (HD + 2);
-  float M = -INFINITY;
-  for (int s = s0 + lane; s < nlive; s += 64) M = fmaxf(M, ld_f<COH>(pr + (size_t)s * (HD + 2)));
+  const int ns = min(nlive - s0, 256);
+  const float* pr = part + ((size_t)h * nsplit + s0) * (HD + 2);
+  const int sl = min(lane, ns - 1);
+  const float m_l = ld_f<COH>(pr + (size_t)sl * (HD + 2));
+  const float l_l = ld_f<COH>(pr + (size_t)sl * (HD + 2) + 1);
+  float v[B][DPL];
+  auto load_rows = [&](int b0) {
+    // clamped, unconditional loads: the batch's rows are in flight together
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const size_t row = (size_t)min(b0 + u, ns - 1) * (HD + 2) + 2 + DPL * lane;
+#pragma unroll
+      for (int t = 0; t < DPL; ++t) v[u][t] = ld_f<COH>(pr + row + t);
+    }
+  };
+  load_rows(0);
+  float M = lane < ns ? m_l : -INFINITY;
+  for (int s = 64 + lane; s < ns; s += 64) M = fmaxf(M, ld_f<COH>(pr + (size_t)s * (HD + 2)));
   M = wave_max(M);
   float L = 0.f;
-  for (int s = s0 + lane; s < nlive; s += 64) {
+  if (lane < ns) {
+    const float w = expf(m_l - M);
+    L = l_l * w;
+    wsl[lane] = w;
+  }
+  for (int s = 64 + lane; s < ns; s += 64) {
     const float w = expf(ld_f<COH>(pr + (size_t)s * (HD + 2)) - M);
     L += ld_f<COH>(pr + (size_t)s * (HD + 2) + 1) * w;
-    if (s - s0 < 256) wsl[s - s0] = w;
+    wsl[s] = w;
   }
   L = wave_sum(L);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -40,27 +63,19 @@ IEK_DEV void merge_head(const float* __restrict__ part, float* __restrict__ out,
   float acc[DPL];
 #pragma unroll
   for (int t = 0; t < DPL; ++t) acc[t] = 0.f;
-  const int ns = min(nlive - s0, 256);
-  for (int s8 = 0; s8 < ns; s8 += 8) {
-    // clamped, unconditional loads: all eight slices' rows are in flight together
-    float v[8][DPL];
+  for (int b0 = 0; b0 < ns; b0 += B) {
+    if (b0 > 0) load_rows(b0);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const size_t row = (size_t)(s0 + min(s8 + u, ns - 1)) * (HD + 2) + 2 + DPL * lane;
-#pragma unroll
-      for (int t = 0; t < DPL; ++t) v[u][t] = ld_f<COH>(pr + row + t);
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      if (s8 + u < ns) {
-        const float w = wsl[s8 + u];
+    for (int u = 0; u < B; ++u) {
+      if (b0 + u < ns) {
+        const float w = wsl[b0 + u];
 #pragma unroll
         for (int t = 0; t < DPL; ++t) acc[t] += v[u][t] * w;
       }
     }
   }
   // slices beyond the 256 staged weights (contexts over 16K keys) use direct weights
-  for (int s = s0 + 256; s < nlive; ++s) {
+  for (int s = 256; s < nlive - s0; ++s) {
     const float w = expf(ld_f<COH>(pr + (size_t)s * (HD + 2)) - M);
 #pragma unroll
     for (int t = 0; t < DPL; ++t) acc[t] += ld_f<COH>(pr + (size_t)s * (HD + 2) + 2 + DPL * lane + t) * w;
@@ -278,8 +293,10 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
 // Slices per chunk for a cache of `max_len` keys: one up to `target` slices per KV head, then
 // enough that a KV head has at most ~`target` chunks (fewer workgroups, and fewer partials for
 // the merge).
-__host__ __device__ inline int attn_slices_per_chunk(int max_len, int target = 32) {
-  const int nsl = (max_len + SPLIT - 1) / SPLIT;
+__host__ __device__ inline int attn_slices_per_chunk(int max_len, int window = 0, int target = 32) {
+  int nsl = (max_len + SPLIT - 1) / SPLIT;
+  // a window keeps only ~window / SPLIT + 1 slices live: size the chunks for those
+  if (window > 0) nsl = min(nsl, (window + SPLIT - 1) / SPLIT + 1);
   return nsl <= target ? 1 : (nsl + target - 1) / target;
 }
 

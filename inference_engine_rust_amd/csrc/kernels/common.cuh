@@ -24,16 +24,48 @@ IEK_DEV float half_bits_to_float(uint32_t bits16) {
   return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xFFFFu)));
 }
 
+// Cross-lane steps on DPP (register-to-register, no LDS round trip). update_dpp returns `old` in
+// the rows the row mask leaves out.
+template <int CTRL, int ROW_MASK = 0xF>
+IEK_DEV float dpp_f(float old, float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, v),
+                                                               CTRL, ROW_MASK, 0xF, false));
+}
+constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1, 0, 3, 2]
+constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2, 3, 0, 1]
+constexpr int DPP_HALF_MIRROR = 0x141;  // lane i <- 7 - i within each 8
+constexpr int DPP_MIRROR = 0x140;       // lane i <- 15 - i within each 16
+constexpr int DPP_BCAST15 = 0x142;      // lane 15 of row r -> row r + 1
+constexpr int DPP_BCAST31 = 0x143;      // lane 31 -> rows 2 and 3
+
+// Sum / max over each 16-lane row, the result in every lane of the row.
+IEK_DEV float row16_sum(float v) {
+  v += dpp_f<DPP_XOR1>(0.f, v);
+  v += dpp_f<DPP_XOR2>(0.f, v);
+  v += dpp_f<DPP_HALF_MIRROR>(0.f, v);
+  return v + dpp_f<DPP_MIRROR>(0.f, v);
+}
+IEK_DEV float row16_max(float v) {
+  v = fmaxf(v, dpp_f<DPP_XOR1>(-INFINITY, v));
+  v = fmaxf(v, dpp_f<DPP_XOR2>(-INFINITY, v));
+  v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(-INFINITY, v));
+  return fmaxf(v, dpp_f<DPP_MIRROR>(-INFINITY, v));
+}
+
+// Sum / max over the wave, the result in every lane: the 16-lane rows, then rows 0+1 into row 1
+// and (0+1)+(2+3) into row 3, whose last lane is broadcast.
 IEK_DEV float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, WAVE);
-  return v;
+  v = row16_sum(v);
+  v += dpp_f<DPP_BCAST15, 0xA>(0.f, v);
+  v += dpp_f<DPP_BCAST31, 0xC>(0.f, v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 IEK_DEV float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, WAVE));
-  return v;
+  v = row16_max(v);
+  v = fmaxf(v, dpp_f<DPP_BCAST15, 0xA>(-INFINITY, v));
+  v = fmaxf(v, dpp_f<DPP_BCAST31, 0xC>(-INFINITY, v));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 // Loads and stores coherent across the XCDs' L2 caches without cache maintenance (agent-scope

@@ -63,7 +63,7 @@ void launch_repack_q80(const void* src, int K, int N, void* dst, hipStream_t st)
 
 // The body reads the arguments in place from the kernarg segment (a reference to the by-value
 // parameter would make a private copy, and the segment-selecting reads would keep it in scratch).
-template <class Tr, int R, bool DUAL>
+template <class Tr, int R, bool DUAL, bool X2, bool MULTI>
 __global__ __launch_bounds__(256) void mv_stream(MvArgs args) {
   extern __shared__ __align__(16) float lds[];
   (void)args;
@@ -73,9 +73,11 @@ __global__ __launch_bounds__(256) void mv_stream(MvArgs args) {
   asm volatile("" ::"s"(a.epi), "s"(a.nseg), "s"(a.K), "s"(a.seg_start[1]), "s"(a.seg_start[2]),
                "s"(a.seg_start[3]), "s"(a.n[0]), "s"(a.x), "s"(a.norm_w), "s"(a.resid), "s"(a.w[0]), "s"(a.w[1]),
                "s"(a.w[2]), "s"(a.pos), "s"(a.rope_cs), "s"(a.npairs), "s"(gridDim.x));
-  const int pos = a.epi == EPI_QKV ? __builtin_amdgcn_readfirstlane(*a.pos) : 0;
+  // a scalar load: its wait is on the scalar counter, not behind vector loads
+  typedef __attribute__((address_space(4))) const int* ConstInt;
+  const int pos = a.epi == EPI_QKV ? *(ConstInt)a.pos : 0;
   typename Tr::template Buf<DUAL ? 2 * R : R> A;
-  mv_body<Tr, R, DUAL>(a, lds, pos, A, false);
+  mv_body<Tr, R, DUAL, false, X2, MULTI>(a, lds, pos, A, false);
   if (a.pos_inc && blockIdx.x == 0 && threadIdx.x == 0) *a.pos_inc += 1;
 }
 
@@ -123,9 +125,10 @@ int num_cus() {
 
 // Persistent grid: exactly the workgroups that are resident at once (the occupancy the register
 // and LDS use allow, optionally capped by IEK_MV_PER_CU), so no second wave of workgroups forms a
-// tail; every wave then strides over the row groups.
-template <class Tr, bool DUAL>
-static void launch_stream(const MvArgs& a, int groups, hipStream_t st) {
+// tail; every wave then strides over the row groups. The kernel variant follows the grid: MULTI
+// when some wave has more than one step, X2 when each staging thread owns two 32-element blocks.
+template <class Tr, bool DUAL, bool X2>
+static void launch_stream_x(const MvArgs& a, int groups, hipStream_t st) {
   static int cap = -1;
   if (cap < 0) {
     const char* e = getenv("IEK_MV_PER_CU");
@@ -135,12 +138,30 @@ static void launch_stream(const MvArgs& a, int groups, hipStream_t st) {
   const size_t lds = lds_bytes(a, Tr::I8, Tr::WB ? 4 * NR * Q6_ROW_SLOT : 0);
   if (lds > 160 * 1024) fail(ST_OP, "matvec: K too large for the LDS-staged input");
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mv_stream<Tr, 2, DUAL>, 256, lds) != hipSuccess ||
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mv_stream<Tr, 2, DUAL, X2, true>, 256, lds) !=
+          hipSuccess ||
       per_cu <= 0)
     per_cu = 1;
   per_cu = std::min(per_cu, cap);
   const int blocks = std::max(1, std::min((groups + 3) / 4, num_cus() * per_cu));
-  hipLaunchKernelGGL((mv_stream<Tr, 2, DUAL>), dim3(blocks), dim3(256), lds, st, a);
+  const int waves = 4 * blocks;
+  const int nchunk = (a.K / QK_K) * Tr::CHUNKS, npass = (nchunk + WAVE - 1) / WAVE;
+  const int max_steps = ((groups + waves - 1) / waves) * npass;
+  if (max_steps > 1)
+    hipLaunchKernelGGL((mv_stream<Tr, 2, DUAL, X2, true>), dim3(blocks), dim3(256), lds, st, a);
+  else
+    hipLaunchKernelGGL((mv_stream<Tr, 2, DUAL, X2, false>), dim3(blocks), dim3(256), lds, st, a);
+}
+
+template <class Tr, bool DUAL>
+static void launch_stream(const MvArgs& a, int groups, hipStream_t st) {
+  if constexpr (Tr::I8 && !DUAL) {
+    if (a.K / 32 > 256) {
+      launch_stream_x<Tr, DUAL, true>(a, groups, st);
+      return;
+    }
+  }
+  launch_stream_x<Tr, DUAL, false>(a, groups, st);
 }
 
 bool mv_int8_staging() {

@@ -265,33 +265,43 @@ IEK_DEV void quant_block(const float (&y)[32], float am, uint32_t (&h)[8], uint3
 
 // The staging is split so its global loads can be issued before the first weight loads: the
 // memory counter retires in order, so x (an L2 hit) would otherwise wait behind the weight stream.
-// stage_i8_issue loads this thread's first 32-element block of x (and w), its share of the residual
-// vector and its RoPE pair into registers; stage_i8_finish consumes them.
+// stage_i8_issue loads this thread's 32-element block(s) of x (and w), its share of the residual
+// vector, its RoPE pair and the wave's epilogue residuals into registers; stage_i8_finish consumes
+// them. Every load whose issue depends on a runtime condition goes out before the unconditional
+// x block, and the weight loads follow that block: the compiler counts the loads in flight only
+// along paths with the same loads, so a wait for x then leaves the weight loads in flight instead
+// of draining them.
 struct XPre {
   float4 xv[8], wv[8];
+  float4 xv2[8], wv2[8];  // second block (K > 8192, X2 kernels)
   float4 res[4];
   float2 rope;
+  float ev;  // residual of this lane's row (lane < R) when the epilogue reads it from a register
 };
 
 IEK_DEV bool res_vec(const MvArgs& a) {
   return a.epi == EPI_RESID && (a.n[0] & 3) == 0 && a.n[0] <= 4096 && (reinterpret_cast<uintptr_t>(a.resid) & 15) == 0;
 }
 
-template <bool COH = false>
-IEK_DEV void stage_i8_issue(const MvArgs& a, XPre& p, int pos) {
-  const int tid = threadIdx.x, nb = a.K >> 5, bc = min(tid, nb - 1);
-  const float4* x4 = reinterpret_cast<const float4*>(a.x) + (size_t)bc * 8;
-#pragma unroll
-  for (int t = 0; t < 8; ++t) p.xv[t] = ld_f4<COH>(x4 + t);
+// ev_idx >= 0: this lane's epilogue residual index (EPI_RESID with at most one row group per
+// wave); otherwise the residual vector is staged in LDS. With X2 the thread's second block
+// (tid + 256, K > 8192) is loaded here too.
+template <bool COH = false, bool X2 = false>
+IEK_DEV void stage_i8_issue(const MvArgs& a, XPre& p, int pos, int ev_idx) {
+  const int tid = threadIdx.x, nb = a.K >> 5, bc = min(tid, nb - 1), bc2 = min(tid + 256, nb - 1);
   if (a.norm_w) {
     const float4* w4 = reinterpret_cast<const float4*>(a.norm_w) + (size_t)bc * 8;
 #pragma unroll
     for (int t = 0; t < 8; ++t) p.wv[t] = w4[t];
-  } else {
+    if constexpr (X2) {
+      const float4* w42 = reinterpret_cast<const float4*>(a.norm_w) + (size_t)bc2 * 8;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) p.wv[t] = make_float4(1.f, 1.f, 1.f, 1.f);
-  }
-  if (res_vec(a)) {
+      for (int t = 0; t < 8; ++t) p.wv2[t] = w42[t];
+    }
+  }  // without a norm weight, quant_store never reads wv
+  if (ev_idx >= 0) {
+    p.ev = ld_f<COH>((a.epi == EPI_GELU_MUL ? a.mulv : a.resid) + ev_idx);
+  } else if (res_vec(a)) {
     const float4* r4 = reinterpret_cast<const float4*>(a.resid);
     const int n4 = a.n[0] >> 2;
 #pragma unroll
@@ -299,6 +309,14 @@ IEK_DEV void stage_i8_issue(const MvArgs& a, XPre& p, int pos) {
   }
   if (a.epi == EPI_QKV)
     p.rope = reinterpret_cast<const float2*>(a.rope_cs)[(size_t)pos * a.npairs + min(tid, a.npairs - 1)];
+  if constexpr (X2) {
+    const float4* x42 = reinterpret_cast<const float4*>(a.x) + (size_t)bc2 * 8;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) p.xv2[t] = ld_f4<COH>(x42 + t);
+  }
+  const float4* x4 = reinterpret_cast<const float4*>(a.x) + (size_t)bc * 8;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) p.xv[t] = ld_f4<COH>(x4 + t);
 }
 
 IEK_DEV void quant_store(const MvArgs& a, const Lds& L, int b, const float4 (&xv)[8], const float4 (&wv)[8], float& ss,
@@ -332,13 +350,27 @@ IEK_DEV void quant_store(const MvArgs& a, const Lds& L, int b, const float4 (&xv
   }
 }
 
-template <bool COH = false>
-IEK_DEV void stage_i8_finish(const MvArgs& a, const Lds& L, int pos, const XPre& p) {
+template <bool COH = false, bool X2 = false>
+IEK_DEV void stage_i8_finish(const MvArgs& a, const Lds& L, int pos, XPre& p, bool res_lds) {
   const int K = a.K, tid = threadIdx.x, nb = K >> 5;
+  // The empty asm statements make x (and w) appear defined here, so no arithmetic on them is
+  // hoisted above the weight loads issued between stage_i8_issue and this point.
+  auto pin = [](float4& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); };
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    pin(p.xv[t]);
+    if (a.norm_w) pin(p.wv[t]);
+    if constexpr (X2) {
+      pin(p.xv2[t]);
+      if (a.norm_w) pin(p.wv2[t]);
+    }
+  }
   float ss = 0.f;
   float amax[2] = {0.f, 0.f};
   quant_store(a, L, tid, p.xv, p.wv, ss, amax[0]);
-  if (nb > 256) {
+  if constexpr (X2) {
+    quant_store(a, L, tid + 256, p.xv2, p.wv2, ss, amax[1]);
+  } else if (nb > 256) {
     // second block of this thread (K > 8192), loaded here
     const int b = tid + 256, bc = min(b, nb - 1);
     float4 xv[8], wv[8];
@@ -355,7 +387,7 @@ IEK_DEV void stage_i8_finish(const MvArgs& a, const Lds& L, int pos, const XPre&
     }
     quant_store(a, L, b, xv, wv, ss, amax[1]);
   }
-  if (a.epi == EPI_RESID) {
+  if (a.epi == EPI_RESID && res_lds) {
     const int N = a.n[0];
     if (res_vec(a)) {
       float4* d4 = reinterpret_cast<float4*>(L.res);
@@ -395,10 +427,11 @@ IEK_DEV float* seg_out(const MvArgs& a, int s) { return s == 0 ? a.out[0] : (s =
 IEK_DEV int seg_base(const MvArgs& a, int s) { return s == 0 ? a.seg_start[0] : (s == 1 ? a.seg_start[1] : a.seg_start[2]); }
 
 // ---- epilogue -----------------------------------------------------------------------------------
-// Reads only registers and LDS (pos was loaded at kernel start).
+// Reads only registers and LDS (pos was loaded at kernel start); with ev_reg, lane r < R holds the
+// residual (EPI_RESID) or multiplier (EPI_GELU_MUL) of row lr0 + r in ev.
 template <int R, bool COH = false>
 IEK_DEV void epilogue(const MvArgs& a, const Lds& L, int s, int lr0, float (&acc)[R], const float* acc_up, int lane,
-                      int pos, unsigned long long& run_key) {
+                      int pos, unsigned long long& run_key, float ev = 0.f, bool ev_reg = false) {
   if (a.epi == EPI_SWIGLU || a.epi == EPI_GEGLU) {
     if (lane < R) {
       float g = acc[0], u = acc_up[0];
@@ -456,8 +489,8 @@ IEK_DEV void epilogue(const MvArgs& a, const Lds& L, int s, int lr0, float (&acc
     for (int r = 1; r < R; ++r)
       if (lane == r) v = acc[r];
     const int n = lr0 + lane;
-    if (a.epi == EPI_RESID) v = L.res[n] + v;
-    if (a.epi == EPI_GELU_MUL) v = gelu_tanh_dev(v) * a.mulv[n];
+    if (a.epi == EPI_RESID) v = (ev_reg ? ev : L.res[n]) + v;
+    if (a.epi == EPI_GELU_MUL) v = gelu_tanh_dev(v) * (ev_reg ? ev : a.mulv[n]);
     st_f<COH>(seg_out(a, s) + n, v);
   }
 }
@@ -946,10 +979,11 @@ struct MvGeom {
     const int my_groups = g0 < groups ? (groups - 1 - g0) / stride + 1 : 0;
     steps = my_groups * npass;
   }
-  // Row pointers and chunk of step `it` (clamped into the wave's range so every load is valid).
+  // Row pointers and chunk of step `it`, clamped into the wave's steps and the launch's row groups
+  // so every load is valid (a wave without steps reads the last group).
   IEK_DEV void rows_of(const MvArgs& a, int it, const uint8_t* (&rows)[NR], int& c) const {
-    const int k = min(it, steps - 1);
-    const int g = g0 + (k / npass) * stride, p = k % npass;
+    const int k = max(0, min(it, steps - 1));
+    const int g = min(g0 + (k / npass) * stride, groups - 1), p = k % npass;
     c = min(lane + WAVE * p, nchunk - 1);
     const int row0 = g * R;
     const int s = DUAL ? 0 : seg_of(a, row0);
@@ -976,10 +1010,19 @@ IEK_DEV void mv_prefetch(const MvArgs& a, typename Tr::template Buf<DUAL ? 2 * R
 
 // The streaming matvec of one launch's rows. With `prefetched`, buffer A already holds (or has in
 // flight) the first step, issued by mv_prefetch with the same arguments.
-template <class Tr, int R, bool DUAL, bool COH = false>
+//
+// Load order and waits. The compiler waits for a load by counting the memory operations issued
+// after it, which it can only do along paths that issued the same ones; a load issued on some
+// paths only makes every later wait conservative (a full drain of the weight stream). So: the
+// conditional staging loads go first, then x, then the weight buffers, and in the stream the
+// other buffer is always in flight while one is computed. MULTI (the host's choice, when some
+// wave has more than one step) keeps two buffers in flight from the start; single-step launches
+// carry only one.
+template <class Tr, int R, bool DUAL, bool COH = false, bool X2 = false, bool MULTI = true>
 IEK_DEV void mv_body(const MvArgs& a, float* lds, int pos, typename Tr::template Buf<DUAL ? 2 * R : R>& A,
                      bool prefetched) {
   static_assert(!COH || Tr::I8, "coherent staging is implemented for the int8-staged traits");
+  static_assert(!X2 || Tr::I8, "two-block staging is implemented for the int8-staged traits");
   constexpr int NR = DUAL ? 2 * R : R;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   Lds L = lds_layout(a, lds, Tr::I8, Tr::WB ? 4 * NR * Q6_ROW_SLOT : 0);
@@ -991,6 +1034,16 @@ IEK_DEV void mv_body(const MvArgs& a, float* lds, int pos, typename Tr::template
   float acc[NR];
 #pragma unroll
   for (int r = 0; r < NR; ++r) acc[r] = 0.f;
+  // the epilogue's residual / multiplier in a register when every wave has at most one row group
+  const bool ev_reg = Tr::I8 && (a.epi == EPI_RESID || a.epi == EPI_GELU_MUL) && G.groups <= G.stride;
+  int ev_idx = -1;
+  if (ev_reg) {
+    const int row0 = min(G.g0, G.groups - 1) * R;
+    const int s0 = seg_of(a, row0);
+    ev_idx = max(0, min(row0 - seg_base(a, s0) + min(lane, R - 1), a.n[0] - 1));
+  }
+  XPre xp;
+  xp.ev = 0.f;
 
   auto finish = [&](int it) {
     const int p = it % npass;
@@ -1006,7 +1059,7 @@ IEK_DEV void mv_body(const MvArgs& a, float* lds, int pos, typename Tr::template
     if (DUAL) wave_reduce<R>(accu);
     const int row0 = g * R;
     const int s = DUAL ? 0 : seg_of(a, row0);
-    epilogue<R, COH>(a, L, s, row0 - seg_base(a, s), accg, accu, lane, pos, run_key);
+    epilogue<R, COH>(a, L, s, row0 - seg_base(a, s), accg, accu, lane, pos, run_key, xp.ev, ev_reg);
 #pragma unroll
     for (int r = 0; r < NR; ++r) acc[r] = 0.f;
   };
@@ -1026,37 +1079,41 @@ IEK_DEV void mv_body(const MvArgs& a, float* lds, int pos, typename Tr::template
     for (int r = 0; r < NR; ++r) acc[r] += c < nchunk ? part[r] : 0.f;
     finish(it);
   };
-
-  // x / residual / RoPE loads go out first, then the first weight buffer, so the staging work
-  // overlaps the weight fetch instead of queueing behind it.
-  XPre xp;
-  if constexpr (Tr::I8) stage_i8_issue<COH>(a, xp, pos);
-  if (!prefetched && steps > 0) {
+  auto load = [&](typename Tr::template Buf<NR>& buf, int it) {
     const uint8_t* rows[NR];
     int c;
-    G.rows_of(a, 0, rows, c);
-    Tr::template load<NR>(A, rows, c, G.nsb);
-  }
+    G.rows_of(a, it, rows, c);
+    Tr::template load<NR>(buf, rows, c, G.nsb);
+  };
+
+  // x / residual / RoPE loads go out first, then the weight buffers, so the staging work overlaps
+  // the weight fetch instead of queueing behind it.
+  if constexpr (Tr::I8) stage_i8_issue<COH, X2>(a, xp, pos, ev_idx);
+  if (!prefetched) load(A, 0);
+  if constexpr (MULTI) load(B, 1);
+  // keep the staging arithmetic below the weight loads: scheduled among them, its first use of x
+  // would hold the remaining weight loads back until x has arrived
+  __builtin_amdgcn_sched_barrier(0);
   if constexpr (Tr::I8)
-    stage_i8_finish<COH>(a, L, pos, xp);
+    stage_i8_finish<COH, X2>(a, L, pos, xp, !ev_reg);
   else
     stage(a, L, pos);
-  for (int it = 0; it < steps; it += 2) {
-    if (it + 1 < steps) {
-      const uint8_t* rows[NR];
-      int c;
-      G.rows_of(a, it + 1, rows, c);
-      Tr::template load<NR>(B, rows, c, G.nsb);
+  if (steps > 0) {
+    if constexpr (MULTI) {
+      // Each buffer's refill is issued right after it was computed, unconditionally (the last one
+      // re-reads the wave's final step and is never waited for), so every path into a step has
+      // the same loads in flight behind it.
+      for (int it = 0;; it += 2) {
+        step(A, it);
+        if (it + 1 >= steps) break;
+        load(A, it + 2);
+        step(B, it + 1);
+        if (it + 2 >= steps) break;
+        load(B, it + 3);
+      }
+    } else {
+      step(A, 0);
     }
-    step(A, it);
-    if (it + 1 >= steps) break;
-    if (it + 2 < steps) {
-      const uint8_t* rows[NR];
-      int c;
-      G.rows_of(a, it + 2, rows, c);
-      Tr::template load<NR>(A, rows, c, G.nsb);
-    }
-    step(B, it + 1);
   }
   if (a.epi == EPI_ARGMAX) argmax_flush(a, run_key);
 }
