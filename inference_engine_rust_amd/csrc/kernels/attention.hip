@@ -333,8 +333,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float* __r
         p[jn][r] = ok ? sv : -INFINITY;
         mx = fmaxf(mx, p[jn][r]);
       }
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      mx = row16_max(mx);
       const float mn = fmaxf(mrow[r], mx);
       const float corr = mn == -INFINITY ? 1.f : expf(mrow[r] - mn);
       float sum = 0.f;
@@ -344,8 +343,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float* __r
         p[jn][r] = e;
         sum += e;
       }
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off, 64);
+      sum = row16_sum(sum);
       lrow[r] = lrow[r] * corr + sum;
       mrow[r] = mn;
 #pragma unroll

@@ -189,8 +189,7 @@ IEK_DEV void stage(const MvArgs& a, const Lds& L, int pos) {
   }
   if (a.norm_w) {
     __shared__ float red[4];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, WAVE);
+    ss = wave_sum(ss);
     if ((tid & 63) == 0) red[tid >> 6] = ss;
     __syncthreads();
     const float rms = rms_of((red[0] + red[1]) + (red[2] + red[3]), K, a.eps);
@@ -405,8 +404,7 @@ IEK_DEV void stage_i8_finish(const MvArgs& a, const Lds& L, int pos, XPre& p, bo
   float rms = 1.f;
   if (a.norm_w) {
     __shared__ float red[4];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, WAVE);
+    ss = wave_sum(ss);
     if ((tid & 63) == 0) red[tid >> 6] = ss;
     __syncthreads();
     rms = rms_of((red[0] + red[1]) + (red[2] + red[3]), K, a.eps);
