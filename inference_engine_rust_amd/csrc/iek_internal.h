@@ -109,8 +109,12 @@ void launch_fill_i32(int* p, int v, int n, hipStream_t st);
 void launch_attn_decode(const float* q, const void* kc, const void* vc, bool kv_f32, float* out, float* part,
                         int* counters, int n_heads, int n_kv, int head_dim, int ctx, const int* pos_dev, int window,
                         float scale, int max_len, hipStream_t st);
+// With a scratch buffer of attn_prefill_scratch_halves() halves (head_dim 64 or 128), each K/V block
+// is staged once for all the query heads of its KV head; otherwise one workgroup per query head.
+size_t attn_prefill_scratch_halves(int M, int n_kv, int head_dim);
 void launch_attn_prefill(const float* q, const float* k, const float* v, float* out, int M, int n_heads, int n_kv,
-                         int head_dim, int window, float scale, hipStream_t st);
+                         int head_dim, int window, float scale, hipStream_t st, void* scratch = nullptr,
+                         size_t scratch_halves = 0);
 // Gemma-4 pieces (kernels/gemma.hip).
 void launch_head_prep(float* q, float* k, float* v, int rows, int q_stride, int kv_stride, int nq, int nkv, int hd,
                       const float* qn, const float* kn, float eps, bool vnorm, const float* cs, int npairs,

@@ -380,8 +380,277 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float* __r
   }
 }
 
+// ---- prefill attention sharing each K/V block across the query heads of a KV head --------------
+// K and V (f32 rows [M][n_kv * HD]) are split once per layer into fp16 (hi, lo) planes laid out for
+// the MFMA B operands: K per KV head as [n_kv][M][HD], V transposed as [n_kv][HD][Mp] (Mp = M
+// rounded up to 64; the padding is zero). One 64 x 64 tile per workgroup, through LDS for V.
+__global__ __launch_bounds__(256) void kv_split_kernel(const float* __restrict__ k, const float* __restrict__ v, int M,
+                                                       int n_kv, int hd, int Mp, _Float16* __restrict__ kh,
+                                                       _Float16* __restrict__ kl, _Float16* __restrict__ vh,
+                                                       _Float16* __restrict__ vl) {
+  __shared__ float tile[64][65];
+  const int h = blockIdx.z, d0 = blockIdx.y * 64, p0 = blockIdx.x * 64, tid = threadIdx.x;
+  const size_t kvd = (size_t)n_kv * hd;
+#pragma unroll 4
+  for (int r = 0; r < 16; ++r) {
+    const int pl = (tid >> 6) + 4 * r, dl = tid & 63, p = p0 + pl, d = d0 + dl;
+    float vv = 0.f;
+    if (p < M && d < hd) {
+      const size_t src = (size_t)p * kvd + (size_t)h * hd + d;
+      vv = v[src];
+      _Float16 a, b;
+      asplit(k[src], a, b);
+      const size_t kd = ((size_t)h * M + p) * hd + d;
+      kh[kd] = a;
+      kl[kd] = b;
+    }
+    tile[pl][dl] = vv;
+  }
+  __syncthreads();
+#pragma unroll 4
+  for (int r = 0; r < 16; ++r) {
+    const int dl = (tid >> 6) + 4 * r, pl = tid & 63, d = d0 + dl, p = p0 + pl;
+    if (d < hd && p < Mp) {
+      _Float16 a, b;
+      asplit(tile[pl][dl], a, b);
+      const size_t vd = ((size_t)h * hd + d) * Mp + p;
+      vh[vd] = a;
+      vl[vd] = b;
+    }
+  }
+}
+
+// One 256-thread workgroup per (KV head, group of up to 4 query heads, query tile): wave w takes
+// query head w % G4 and query sub-tile w / G4 (G4 = min(G, 4)), TMQ 16-row MFMA tiles of it. Each
+// 64-key block of K and V^T is staged once in LDS (16-byte copies of the split planes, the next
+// block's loads in flight during the current block's MFMAs) and serves every query head of the
+// KV head. S = Q K^T and O += P V take three MFMAs per product (hi*hi + hi*lo + lo*hi, exact in
+// f32), with the online softmax of the per-head kernel above. The longest (latest) query tiles
+// are dispatched first.
+template <int HD, int TMQ>
+__global__ __launch_bounds__(256) void attn_prefill_gqa_kernel(const float* __restrict__ q,
+                                                               const _Float16* __restrict__ kh,
+                                                               const _Float16* __restrict__ kl,
+                                                               const _Float16* __restrict__ vh,
+                                                               const _Float16* __restrict__ vl, float* __restrict__ out,
+                                                               int M, int Mp, int n_heads, int n_kv, int window,
+                                                               float scale) {
+  constexpr int KB = 64;         // keys per block
+  constexpr int JN = KB / 16;    // 16-key column tiles of S
+  constexpr int KS = HD / 32;    // MFMA K steps of S
+  constexpr int NS = HD / 16;    // 16-wide head-dim tiles of O
+  constexpr int KROW = HD + 8;   // padded LDS rows (halves)
+  constexpr int VROW = KB + 8;
+  constexpr int QW = 16 * TMQ;   // queries per wave
+  constexpr int CPT = KB * HD / 8 / 256;  // 16-byte chunks per thread per plane of a K (or V^T) block
+  static_assert(CPT >= 1 && (KB * HD / 8) % 256 == 0, "block must divide over the threads");
+  __shared__ __align__(16) _Float16 ksh[KB][KROW];
+  __shared__ __align__(16) _Float16 ksl[KB][KROW];
+  __shared__ __align__(16) _Float16 vsh[HD][VROW];
+  __shared__ __align__(16) _Float16 vsl[HD][VROW];
+  __shared__ __align__(16) _Float16 ph[4][16][VROW];
+  __shared__ __align__(16) _Float16 pl[4][16][VROW];
+
+  const int G = n_heads / n_kv, G4 = min(G, 4), HG = (G + 3) / 4;
+  const int kvh = blockIdx.x / HG, hg = blockIdx.x % HG;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hl = wave % G4, qs = wave / G4, h = 4 * hg + hl;
+  const bool active = h < G && qs < 4 / G4;
+  const int QT = QW * (4 / G4);
+  const int qt = gridDim.y - 1 - blockIdx.y;  // latest tiles first
+  const int wq0 = qt * QT, wq1 = min(M - 1, wq0 + QT - 1);
+  const int q0 = wq0 + qs * QW;
+  const int hq = kvh * G + min(h, G - 1);
+  const int qd = n_heads * HD;
+  const int fr = lane & 15, fk = 8 * (lane >> 4);
+
+  // Q fragments (A operand) of the wave's TMQ row tiles, split into fp16 pairs
+  au4_t qah[TMQ][KS], qal[TMQ][KS];
+#pragma unroll
+  for (int i = 0; i < TMQ; ++i) {
+    const float* qrow = q + (size_t)min(q0 + 16 * i + fr, M - 1) * qd + (size_t)hq * HD;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const float4 a = *reinterpret_cast<const float4*>(qrow + 32 * s + fk);
+      const float4 b = *reinterpret_cast<const float4*>(qrow + 32 * s + fk + 4);
+      const float vv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      _Float16 hh[8], ll[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) asplit(vv[t], hh[t], ll[t]);
+      qah[i][s] = au4_t{apack2(hh[0], hh[1]), apack2(hh[2], hh[3]), apack2(hh[4], hh[5]), apack2(hh[6], hh[7])};
+      qal[i][s] = au4_t{apack2(ll[0], ll[1]), apack2(ll[2], ll[3]), apack2(ll[4], ll[5]), apack2(ll[6], ll[7])};
+    }
+  }
+  af4_t o[TMQ][NS];
+  float mrow[TMQ][4], lrow[TMQ][4];
+#pragma unroll
+  for (int i = 0; i < TMQ; ++i) {
+#pragma unroll
+    for (int j = 0; j < NS; ++j) o[i][j] = af4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      mrow[i][r] = -INFINITY;
+      lrow[i][r] = 0.f;
+    }
+  }
+
+  // staged block: K rows [key][dim] and V^T rows [dim][key], both planes
+  const _Float16* khp = kh + (size_t)kvh * M * HD;
+  const _Float16* klp = kl + (size_t)kvh * M * HD;
+  const _Float16* vhp = vh + (size_t)kvh * HD * Mp;
+  const _Float16* vlp = vl + (size_t)kvh * HD * Mp;
+  au4_t rk[2][CPT], rv[2][CPT];
+  auto fetch = [&](int kb0) {
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int e = tid + 256 * c;
+      const int j = e / (HD / 8), kc = e % (HD / 8);
+      const size_t ks = (size_t)min(kb0 + j, M - 1) * HD + 8 * kc;
+      rk[0][c] = *reinterpret_cast<const au4_t*>(khp + ks);
+      rk[1][c] = *reinterpret_cast<const au4_t*>(klp + ks);
+      const int d = e / (KB / 8), vc = e % (KB / 8);
+      const size_t vs = (size_t)d * Mp + kb0 + 8 * vc;
+      rv[0][c] = *reinterpret_cast<const au4_t*>(vhp + vs);
+      rv[1][c] = *reinterpret_cast<const au4_t*>(vlp + vs);
+    }
+  };
+  const int kb_start = window > 0 ? (max(0, wq0 - (window - 1)) / KB) * KB : 0;
+  fetch(kb_start);
+  for (int kb0 = kb_start; kb0 <= wq1; kb0 += KB) {
+    __syncthreads();  // the previous block's LDS reads are done
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int e = tid + 256 * c;
+      const int j = e / (HD / 8), kc = e % (HD / 8);
+      *reinterpret_cast<au4_t*>(&ksh[j][8 * kc]) = rk[0][c];
+      *reinterpret_cast<au4_t*>(&ksl[j][8 * kc]) = rk[1][c];
+      const int d = e / (KB / 8), vc = e % (KB / 8);
+      *reinterpret_cast<au4_t*>(&vsh[d][8 * vc]) = rv[0][c];
+      *reinterpret_cast<au4_t*>(&vsl[d][8 * vc]) = rv[1][c];
+    }
+    __syncthreads();
+    if (kb0 + KB <= wq1) fetch(kb0 + KB);
+    // the wave's queries all precede the block, or the block is older than all their windows
+    if (!active || kb0 > q0 + QW - 1 || (window > 0 && kb0 + KB - 1 < q0 - (window - 1))) continue;
+#pragma unroll
+    for (int i = 0; i < TMQ; ++i) {
+      const int qi0 = q0 + 16 * i;
+      if (kb0 > qi0 + 15) continue;  // uniform: this row tile precedes the block
+      af4_t sacc[JN];
+#pragma unroll
+      for (int jn = 0; jn < JN; ++jn) {
+        sacc[jn] = af4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const au4_t bh = *reinterpret_cast<const au4_t*>(&ksh[16 * jn + fr][32 * s + fk]);
+          const au4_t bl = *reinterpret_cast<const au4_t*>(&ksl[16 * jn + fr][32 * s + fk]);
+          sacc[jn] = mma3(qah[i][s], qal[i][s], bh, bl, sacc[jn]);
+        }
+      }
+      float p[JN][4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int qi = qi0 + 4 * (lane >> 4) + r;
+        const int jlo = window > 0 ? max(0, qi - (window - 1)) : 0;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int jn = 0; jn < JN; ++jn) {
+          const int j = kb0 + 16 * jn + fr;
+          const bool ok = j <= qi && j >= jlo && j < M && qi < M;
+          const float sv = sacc[jn][r] * scale;
+          p[jn][r] = ok ? sv : -INFINITY;
+          mx = fmaxf(mx, p[jn][r]);
+        }
+        mx = row16_max(mx);
+        const float mn = fmaxf(mrow[i][r], mx);
+        const float corr = mn == -INFINITY ? 1.f : expf(mrow[i][r] - mn);
+        float sum = 0.f;
+#pragma unroll
+        for (int jn = 0; jn < JN; ++jn) {
+          const float e = p[jn][r] == -INFINITY ? 0.f : expf(p[jn][r] - mn);
+          p[jn][r] = e;
+          sum += e;
+        }
+        sum = row16_sum(sum);
+        lrow[i][r] = lrow[i][r] * corr + sum;
+        mrow[i][r] = mn;
+#pragma unroll
+        for (int j = 0; j < NS; ++j) o[i][j][r] *= corr;
+      }
+      // P to LDS in A-operand order [query][key] (this wave's 16 rows)
+#pragma unroll
+      for (int jn = 0; jn < JN; ++jn)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          asplit(p[jn][r], ph[wave][4 * (lane >> 4) + r][16 * jn + fr], pl[wave][4 * (lane >> 4) + r][16 * jn + fr]);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int ks = 0; ks < KB / 32; ++ks) {
+        const au4_t pah = *reinterpret_cast<const au4_t*>(&ph[wave][fr][32 * ks + fk]);
+        const au4_t pal = *reinterpret_cast<const au4_t*>(&pl[wave][fr][32 * ks + fk]);
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+          const au4_t bh = *reinterpret_cast<const au4_t*>(&vsh[16 * j + fr][32 * ks + fk]);
+          const au4_t bl = *reinterpret_cast<const au4_t*>(&vsl[16 * j + fr][32 * ks + fk]);
+          o[i][j] = mma3(pah, pal, bh, bl, o[i][j]);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();  // ph / pl are rewritten by the next row tile
+    }
+  }
+  if (!active) return;
+#pragma unroll
+  for (int i = 0; i < TMQ; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int qi = q0 + 16 * i + 4 * (lane >> 4) + r;
+      if (qi < M) {
+#pragma unroll
+        for (int j = 0; j < NS; ++j) out[(size_t)qi * qd + (size_t)hq * HD + 16 * j + fr] = o[i][j][r] / lrow[i][r];
+      }
+    }
+}
+
+// Scratch halves the shared-K/V path needs: four planes of n_kv * HD * Mp.
+size_t attn_prefill_scratch_halves(int M, int n_kv, int head_dim) {
+  const size_t Mp = (size_t)((M + 63) / 64) * 64;
+  return 4 * (size_t)n_kv * head_dim * Mp;
+}
+
 void launch_attn_prefill(const float* q, const float* k, const float* v, float* out, int M, int n_heads, int n_kv,
-                         int head_dim, int window, float scale, hipStream_t st) {
+                         int head_dim, int window, float scale, hipStream_t st, void* scratch, size_t scratch_halves) {
+  const int G = n_heads / n_kv;
+  if (scratch && (head_dim == 64 || head_dim == 128) && G >= 1 && n_heads % n_kv == 0 &&
+      scratch_halves >= attn_prefill_scratch_halves(M, n_kv, head_dim)) {
+    const int Mp = ((M + 63) / 64) * 64;
+    const size_t plane = (size_t)n_kv * head_dim * Mp;
+    _Float16* s16 = static_cast<_Float16*>(scratch);
+    _Float16 *kh = s16, *kl = s16 + plane, *vh = s16 + 2 * plane, *vl = s16 + 3 * plane;
+    hipLaunchKernelGGL(kv_split_kernel, dim3(Mp / 64, (head_dim + 63) / 64, n_kv), dim3(256), 0, st, k, v, M, n_kv,
+                       head_dim, Mp, kh, kl, vh, vl);
+    const int G4 = std::min(G, 4), HG = (G + 3) / 4;
+    if (head_dim == 128) {
+      // two row tiles per wave once the grid fills the machine twice over, one below that
+      const int qt2 = 32 * (4 / G4);
+      if ((size_t)n_kv * HG * ((M + qt2 - 1) / qt2) >= 2 * (size_t)num_cus()) {
+        hipLaunchKernelGGL((attn_prefill_gqa_kernel<128, 2>), dim3(n_kv * HG, (M + qt2 - 1) / qt2), dim3(256), 0, st,
+                           q, kh, kl, vh, vl, out, M, Mp, n_heads, n_kv, window, scale);
+      } else {
+        const int qt1 = 16 * (4 / G4);
+        hipLaunchKernelGGL((attn_prefill_gqa_kernel<128, 1>), dim3(n_kv * HG, (M + qt1 - 1) / qt1), dim3(256), 0, st,
+                           q, kh, kl, vh, vl, out, M, Mp, n_heads, n_kv, window, scale);
+      }
+    } else {
+      constexpr int TMQ = 4;
+      const int QT = 16 * TMQ * (4 / G4);
+      hipLaunchKernelGGL((attn_prefill_gqa_kernel<64, TMQ>), dim3(n_kv * HG, (M + QT - 1) / QT), dim3(256), 0, st, q,
+                         kh, kl, vh, vl, out, M, Mp, n_heads, n_kv, window, scale);
+    }
+    return;
+  }
   dim3 grid(n_heads, (M + 63) / 64);
   switch (head_dim) {
 #define IEK_AP(HD, KB)                                                                                          \

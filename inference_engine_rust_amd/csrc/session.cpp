@@ -170,7 +170,8 @@ void Session::ensure_rows(int rows) {
   tmp_ = dev_alloc<float>(R * std::max(qmax, fmax));
   kpart_ok_ = std::max(qmax, fmax) >= H_;  // tmp_ holds a split-K partial of a [rows, hidden] output
   // fp16 (hi, lo) pair of the widest GEMM input, for the matrix-core prefill projections
-  xs_ = dev_alloc<__half>(2 * R * std::max(std::max(H_, qmax), fmax));
+  xs_halves_ = 2 * R * std::max(std::max(H_, qmax), fmax);
+  xs_ = dev_alloc<__half>(xs_halves_);
   xsum_ = dev_alloc<float>(R * std::max(std::max(H_, qmax), fmax) / 32 + 1);
   if (gemma_ && c.ple_dim > 0) {
     const size_t pack = (size_t)c.n_layers * c.ple_dim;
@@ -301,7 +302,9 @@ void Session::layer_prefill(int li, int M) {
   launch_rope_rows(k_, M, kvd, c.n_kv_heads, hd, 0, rt.dev, S.rotary_dim / 2, st_);
   launch_kv_store(k_, v_, M, kvd, (__half*)kc_[li], (__half*)vc_[li], c.n_kv_heads, hd, ctx_, nullptr, pos_, st_);
   const float scale = 1.0f / sqrtf((float)hd);
-  launch_attn_prefill(q_, k_, v_, att_, M, c.n_heads, c.n_kv_heads, hd, S.window, scale, st_);
+  // xs_ (the GEMM input pair, consumed by the Q/K/V projection above) is free until the O
+  // projection's split: the shared-K/V attention stages its fp16 K / V planes there
+  launch_attn_prefill(q_, k_, v_, att_, M, c.n_heads, c.n_kv_heads, hd, S.window, scale, st_, xs_, xs_halves());
   {
     const __half* xa = split(att_, qd);
     const DevTensor* ws[1] = {&L.wo};

@@ -75,6 +75,8 @@ class Session {
   float *g_ = nullptr, *u_ = nullptr, *act_ = nullptr, *tmp_ = nullptr;
   bool kpart_ok_ = false;  // tmp_ can hold a [rows, hidden] split-K partial
   __half* xs_ = nullptr;  // fp16 (hi, lo) split of the current prefill GEMM input
+  size_t xs_halves_ = 0;
+  size_t xs_halves() const { return xs_halves_; }
   float* xsum_ = nullptr;  // its per-32 row sums (Q4_K min term)
   float *xdec_ = nullptr, *xdec2_ = nullptr, *xndec_ = nullptr, *qd_ = nullptr, *kd_ = nullptr, *vd_ = nullptr, *attd_ = nullptr;
   float *actd_ = nullptr, *logits_ = nullptr, *part_ = nullptr, *tmpd_ = nullptr;
