@@ -63,8 +63,8 @@ void launch_repack_q80(const void* src, int K, int N, void* dst, hipStream_t st)
 
 // The body reads the arguments in place from the kernarg segment (a reference to the by-value
 // parameter would make a private copy, and the segment-selecting reads would keep it in scratch).
-template <class Tr, int R, bool DUAL, bool X2, bool MULTI>
-__global__ __launch_bounds__(256) void mv_stream(MvArgs args) {
+template <class Tr, int R, bool DUAL, bool X2, bool MULTI, int NT>
+__global__ __launch_bounds__(NT) void mv_stream(MvArgs args) {
   extern __shared__ __align__(16) float lds[];
   (void)args;
   const MvArgs& a = *(const MvArgs*)__builtin_amdgcn_kernarg_segment_ptr();
@@ -77,7 +77,7 @@ __global__ __launch_bounds__(256) void mv_stream(MvArgs args) {
   typedef __attribute__((address_space(4))) const int* ConstInt;
   const int pos = a.epi == EPI_QKV ? *(ConstInt)a.pos : 0;
   typename Tr::template Buf<DUAL ? 2 * R : R> A;
-  mv_body<Tr, R, DUAL, false, X2, MULTI>(a, lds, pos, A, false);
+  mv_body<Tr, R, DUAL, false, X2, MULTI, NT>(a, lds, pos, A, false);
   if (a.pos_inc && blockIdx.x == 0 && threadIdx.x == 0) *a.pos_inc += 1;
 }
 
@@ -127,41 +127,58 @@ int num_cus() {
 // and LDS use allow, optionally capped by IEK_MV_PER_CU), so no second wave of workgroups forms a
 // tail; every wave then strides over the row groups. The kernel variant follows the grid: MULTI
 // when some wave has more than one step, X2 when each staging thread owns two 32-element blocks.
-template <class Tr, bool DUAL, bool X2>
+template <class Tr, bool DUAL, bool X2, int NT>
 static void launch_stream_x(const MvArgs& a, int groups, hipStream_t st) {
+  constexpr int NW = NT / 64;
   static int cap = -1;
   if (cap < 0) {
     const char* e = getenv("IEK_MV_PER_CU");
     cap = e ? std::max(1, atoi(e)) : 2;
   }
   constexpr int NR = DUAL ? 4 : 2;
-  const size_t lds = lds_bytes(a, Tr::I8, Tr::WB ? 4 * NR * Q6_ROW_SLOT : 0);
+  const size_t lds = lds_bytes(a, Tr::I8, Tr::WB ? NW * NR * Q6_ROW_SLOT : 0);
   if (lds > 160 * 1024) fail(ST_OP, "matvec: K too large for the LDS-staged input");
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mv_stream<Tr, 2, DUAL, X2, true>, 256, lds) !=
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mv_stream<Tr, 2, DUAL, X2, true, NT>, NT, lds) !=
           hipSuccess ||
       per_cu <= 0)
     per_cu = 1;
-  per_cu = std::min(per_cu, cap);
-  const int blocks = std::max(1, std::min((groups + 3) / 4, num_cus() * per_cu));
-  const int waves = 4 * blocks;
+  // the cap counts 256-thread workgroups' worth of waves per CU
+  per_cu = std::min(per_cu, std::max(1, cap * 256 / NT));
+  const int blocks = std::max(1, std::min((groups + NW - 1) / NW, num_cus() * per_cu));
+  const int waves = NW * blocks;
   const int nchunk = (a.K / QK_K) * Tr::CHUNKS, npass = (nchunk + WAVE - 1) / WAVE;
   const int max_steps = ((groups + waves - 1) / waves) * npass;
   if (max_steps > 1)
-    hipLaunchKernelGGL((mv_stream<Tr, 2, DUAL, X2, true>), dim3(blocks), dim3(256), lds, st, a);
+    hipLaunchKernelGGL((mv_stream<Tr, 2, DUAL, X2, true, NT>), dim3(blocks), dim3(NT), lds, st, a);
   else
-    hipLaunchKernelGGL((mv_stream<Tr, 2, DUAL, X2, false>), dim3(blocks), dim3(256), lds, st, a);
+    hipLaunchKernelGGL((mv_stream<Tr, 2, DUAL, X2, false, NT>), dim3(blocks), dim3(NT), lds, st, a);
 }
 
+// Workgroup size: 512 threads (one workgroup per CU, so x is staged once per CU instead of twice)
+// for the int8-staged traits when IEK_MV_NT=512 or, by default, for inputs of more than 4096
+// elements; 256 otherwise. With 256 threads, K > 8192 gives each staging thread two blocks (X2).
 template <class Tr, bool DUAL>
 static void launch_stream(const MvArgs& a, int groups, hipStream_t st) {
-  if constexpr (Tr::I8 && !DUAL) {
-    if (a.K / 32 > 256) {
-      launch_stream_x<Tr, DUAL, true>(a, groups, st);
+  static int nt_env = -1;
+  if (nt_env < 0) {
+    const char* e = getenv("IEK_MV_NT");
+    nt_env = e ? atoi(e) : 0;
+  }
+  if constexpr (Tr::I8) {
+    const bool wide = nt_env == 512 || (nt_env == 0 && a.K > 4096);
+    if (wide && a.K / 32 <= 512) {
+      launch_stream_x<Tr, DUAL, false, 512>(a, groups, st);
       return;
     }
+    if constexpr (!DUAL) {
+      if (a.K / 32 > 256) {
+        launch_stream_x<Tr, DUAL, true, 256>(a, groups, st);
+        return;
+      }
+    }
   }
-  launch_stream_x<Tr, DUAL, false>(a, groups, st);
+  launch_stream_x<Tr, DUAL, false, 256>(a, groups, st);
 }
 
 bool mv_int8_staging() {

@@ -285,9 +285,9 @@ IEK_DEV bool res_vec(const MvArgs& a) {
 // ev_idx >= 0: this lane's epilogue residual index (EPI_RESID with at most one row group per
 // wave); otherwise the residual vector is staged in LDS. With X2 the thread's second block
 // (tid + 256, K > 8192) is loaded here too.
-template <bool COH = false, bool X2 = false>
+template <bool COH = false, bool X2 = false, int NT = 256>
 IEK_DEV void stage_i8_issue(const MvArgs& a, XPre& p, int pos, int ev_idx) {
-  const int tid = threadIdx.x, nb = a.K >> 5, bc = min(tid, nb - 1), bc2 = min(tid + 256, nb - 1);
+  const int tid = threadIdx.x, nb = a.K >> 5, bc = min(tid, nb - 1), bc2 = min(tid + NT, nb - 1);
   if (a.norm_w) {
     const float4* w4 = reinterpret_cast<const float4*>(a.norm_w) + (size_t)bc * 8;
 #pragma unroll
@@ -304,7 +304,7 @@ IEK_DEV void stage_i8_issue(const MvArgs& a, XPre& p, int pos, int ev_idx) {
     const float4* r4 = reinterpret_cast<const float4*>(a.resid);
     const int n4 = a.n[0] >> 2;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) p.res[u] = ld_f4<COH>(r4 + min(tid + 256 * u, n4 - 1));
+    for (int u = 0; u < 1024 / NT; ++u) p.res[u] = ld_f4<COH>(r4 + min(tid + NT * u, n4 - 1));
   }
   if (a.epi == EPI_QKV)
     p.rope = reinterpret_cast<const float2*>(a.rope_cs)[(size_t)pos * a.npairs + min(tid, a.npairs - 1)];
@@ -349,7 +349,7 @@ IEK_DEV void quant_store(const MvArgs& a, const Lds& L, int b, const float4 (&xv
   }
 }
 
-template <bool COH = false, bool X2 = false>
+template <bool COH = false, bool X2 = false, int NT = 256>
 IEK_DEV void stage_i8_finish(const MvArgs& a, const Lds& L, int pos, XPre& p, bool res_lds) {
   const int K = a.K, tid = threadIdx.x, nb = K >> 5;
   // The empty asm statements make x (and w) appear defined here, so no arithmetic on them is
@@ -368,10 +368,10 @@ IEK_DEV void stage_i8_finish(const MvArgs& a, const Lds& L, int pos, XPre& p, bo
   float amax[2] = {0.f, 0.f};
   quant_store(a, L, tid, p.xv, p.wv, ss, amax[0]);
   if constexpr (X2) {
-    quant_store(a, L, tid + 256, p.xv2, p.wv2, ss, amax[1]);
-  } else if (nb > 256) {
+    quant_store(a, L, tid + NT, p.xv2, p.wv2, ss, amax[1]);
+  } else if (nb > NT) {
     // second block of this thread (K > 8192), loaded here
-    const int b = tid + 256, bc = min(b, nb - 1);
+    const int b = tid + NT, bc = min(b, nb - 1);
     float4 xv[8], wv[8];
     const float4* x4 = reinterpret_cast<const float4*>(a.x) + (size_t)bc * 8;
 #pragma unroll
@@ -391,27 +391,29 @@ IEK_DEV void stage_i8_finish(const MvArgs& a, const Lds& L, int pos, XPre& p, bo
     if (res_vec(a)) {
       float4* d4 = reinterpret_cast<float4*>(L.res);
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (tid + 256 * u < (N >> 2)) d4[tid + 256 * u] = p.res[u];
+      for (int u = 0; u < 1024 / NT; ++u)
+        if (tid + NT * u < (N >> 2)) d4[tid + NT * u] = p.res[u];
     } else {
-      for (int i = tid; i < N; i += 256) L.res[i] = ld_f<COH>(a.resid + i);
+      for (int i = tid; i < N; i += NT) L.res[i] = ld_f<COH>(a.resid + i);
     }
   }
   if (a.epi == EPI_QKV && tid < a.npairs) reinterpret_cast<float2*>(L.rope)[tid] = p.rope;
   if (a.epi == EPI_QKV)
-    for (int i = 256 + tid; i < a.npairs; i += 256)
+    for (int i = NT + tid; i < a.npairs; i += NT)
       reinterpret_cast<float2*>(L.rope)[i] = reinterpret_cast<const float2*>(a.rope_cs)[(size_t)pos * a.npairs + i];
   float rms = 1.f;
   if (a.norm_w) {
-    __shared__ float red[4];
+    __shared__ float red[NT / 64];
     ss = wave_sum(ss);
     if ((tid & 63) == 0) red[tid >> 6] = ss;
     __syncthreads();
-    rms = rms_of((red[0] + red[1]) + (red[2] + red[3]), K, a.eps);
+    float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    if constexpr (NT == 512) tot += (red[4] + red[5]) + (red[6] + red[7]);
+    rms = rms_of(tot, K, a.eps);
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int b = tid + 256 * j;
+    const int b = tid + NT * j;
     if (b < nb) L.sb[b] = amax[j] / (XQ_MAX * rms);
   }
   __syncthreads();
@@ -621,8 +623,9 @@ IEK_DEV float q6k_dot(const Q6Raw& q, const float4* x4, const float (&xs4)[4]) {
 // End of an EPI_ARGMAX launch: reduce the lanes' running keys over the workgroup and publish one
 // atomicMax (the key packs the value's order and the inverted index, so the maximum is the first
 // maximal index).
+template <int NT = 256>
 IEK_DEV void argmax_flush(const MvArgs& a, unsigned long long run_key) {
-  __shared__ unsigned long long red_key[4];
+  __shared__ unsigned long long red_key[NT / 64];
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
     const unsigned long long o = __shfl_xor(run_key, off, WAVE);
@@ -633,7 +636,7 @@ IEK_DEV void argmax_flush(const MvArgs& a, unsigned long long run_key) {
   if (threadIdx.x == 0) {
     unsigned long long k = red_key[0];
 #pragma unroll
-    for (int w = 1; w < 4; ++w) k = red_key[w] > k ? red_key[w] : k;
+    for (int w = 1; w < NT / 64; ++w) k = red_key[w] > k ? red_key[w] : k;
     if (k) atomicMax(a.amax_key, k);
   }
 }
@@ -958,7 +961,7 @@ struct Q8RTr {
 
 // Geometry of one streaming pass over a launch's rows: wave w of workgroup b owns row groups
 // (4b + w) + k * (4 * gridDim.x) and walks its flattened (group, K pass) steps.
-template <class Tr, int R, bool DUAL>
+template <class Tr, int R, bool DUAL, int NW = 4>
 struct MvGeom {
   static constexpr int NR = DUAL ? 2 * R : R;
   int lane, g0, stride, groups, nsb, nchunk, npass, steps;
@@ -968,8 +971,8 @@ struct MvGeom {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int total = a.nseg == 1 ? a.seg_start[1] : (a.nseg == 2 ? a.seg_start[2] : a.seg_start[3]);
     groups = total / R;
-    stride = gridDim.x * 4;
-    g0 = blockIdx.x * 4 + wave;
+    stride = gridDim.x * NW;
+    g0 = blockIdx.x * NW + wave;
     nsb = a.K / QK_K;
     rb = Tr::row_bytes(nsb);
     nchunk = (a.K / QK_K) * Tr::CHUNKS;
@@ -1016,16 +1019,18 @@ IEK_DEV void mv_prefetch(const MvArgs& a, typename Tr::template Buf<DUAL ? 2 * R
 // other buffer is always in flight while one is computed. MULTI (the host's choice, when some
 // wave has more than one step) keeps two buffers in flight from the start; single-step launches
 // carry only one.
-template <class Tr, int R, bool DUAL, bool COH = false, bool X2 = false, bool MULTI = true>
+template <class Tr, int R, bool DUAL, bool COH = false, bool X2 = false, bool MULTI = true, int NT = 256>
 IEK_DEV void mv_body(const MvArgs& a, float* lds, int pos, typename Tr::template Buf<DUAL ? 2 * R : R>& A,
                      bool prefetched) {
   static_assert(!COH || Tr::I8, "coherent staging is implemented for the int8-staged traits");
   static_assert(!X2 || Tr::I8, "two-block staging is implemented for the int8-staged traits");
+  static_assert(NT == 256 || (NT == 512 && Tr::I8), "512-thread workgroups are implemented for the int8-staged traits");
+  constexpr int NW = NT / 64;
   constexpr int NR = DUAL ? 2 * R : R;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   Lds L = lds_layout(a, lds, Tr::I8, Tr::WB ? 4 * NR * Q6_ROW_SLOT : 0);
   L.wb += wave * NR * Q6_ROW_SLOT;
-  const MvGeom<Tr, R, DUAL> G(a);
+  const MvGeom<Tr, R, DUAL, NW> G(a);
   const int npass = G.npass, nchunk = G.nchunk, steps = G.steps;
   typename Tr::template Buf<NR> B;
   unsigned long long run_key = 0;
@@ -1086,14 +1091,14 @@ IEK_DEV void mv_body(const MvArgs& a, float* lds, int pos, typename Tr::template
 
   // x / residual / RoPE loads go out first, then the weight buffers, so the staging work overlaps
   // the weight fetch instead of queueing behind it.
-  if constexpr (Tr::I8) stage_i8_issue<COH, X2>(a, xp, pos, ev_idx);
+  if constexpr (Tr::I8) stage_i8_issue<COH, X2, NT>(a, xp, pos, ev_idx);
   if (!prefetched) load(A, 0);
   if constexpr (MULTI) load(B, 1);
   // keep the staging arithmetic below the weight loads: scheduled among them, its first use of x
   // would hold the remaining weight loads back until x has arrived
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (Tr::I8)
-    stage_i8_finish<COH, X2>(a, L, pos, xp, !ev_reg);
+    stage_i8_finish<COH, X2, NT>(a, L, pos, xp, !ev_reg);
   else
     stage(a, L, pos);
   if (steps > 0) {
@@ -1113,7 +1118,7 @@ IEK_DEV void mv_body(const MvArgs& a, float* lds, int pos, typename Tr::template
       step(A, 0);
     }
   }
-  if (a.epi == EPI_ARGMAX) argmax_flush(a, run_key);
+  if (a.epi == EPI_ARGMAX) argmax_flush<NT>(a, run_key);
 }
 
 }  // namespace iek
