@@ -1,6 +1,8 @@
 // Decode matvec kernels and launchers: the streaming kernel (mv_stream), the generic fallback for
 // any dtype and K, and the one-time regrouping of Q6_K / Q8_0 weights. The device code they share
 // with the persistent decode step is in mv_core.cuh.
+#include <type_traits>
+
 #include "mv_core.cuh"
 
 namespace iek {
@@ -63,7 +65,7 @@ void launch_repack_q80(const void* src, int K, int N, void* dst, hipStream_t st)
 
 // The body reads the arguments in place from the kernarg segment (a reference to the by-value
 // parameter would make a private copy, and the segment-selecting reads would keep it in scratch).
-template <class Tr, int R, bool DUAL, bool X2, bool MULTI, int NT>
+template <class Tr, int R, bool DUAL, bool X2, bool MULTI, int NT, int XS = 0>
 __global__ __launch_bounds__(NT) void mv_stream(MvArgs args) {
   extern __shared__ __align__(16) float lds[];
   (void)args;
@@ -77,7 +79,7 @@ __global__ __launch_bounds__(NT) void mv_stream(MvArgs args) {
   typedef __attribute__((address_space(4))) const int* ConstInt;
   const int pos = a.epi == EPI_QKV ? *(ConstInt)a.pos : 0;
   typename Tr::template Buf<DUAL ? 2 * R : R> A;
-  mv_body<Tr, R, DUAL, false, X2, MULTI, NT>(a, lds, pos, A, false);
+  mv_body<Tr, R, DUAL, false, X2, MULTI, NT, XS>(a, lds, pos, A, false);
   if (a.pos_inc && blockIdx.x == 0 && threadIdx.x == 0) *a.pos_inc += 1;
 }
 
@@ -127,7 +129,7 @@ int num_cus() {
 // and LDS use allow, optionally capped by IEK_MV_PER_CU), so no second wave of workgroups forms a
 // tail; every wave then strides over the row groups. The kernel variant follows the grid: MULTI
 // when some wave has more than one step, X2 when each staging thread owns two 32-element blocks.
-template <class Tr, bool DUAL, bool X2, int NT>
+template <class Tr, bool DUAL, bool X2, int NT, int XS = 0>
 static void launch_stream_x(const MvArgs& a, int groups, hipStream_t st) {
   constexpr int NW = NT / 64;
   static int cap = -1;
@@ -139,7 +141,7 @@ static void launch_stream_x(const MvArgs& a, int groups, hipStream_t st) {
   const size_t lds = lds_bytes(a, Tr::I8, Tr::WB ? NW * NR * Q6_ROW_SLOT : 0);
   if (lds > 160 * 1024) fail(ST_OP, "matvec: K too large for the LDS-staged input");
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mv_stream<Tr, 2, DUAL, X2, true, NT>, NT, lds) !=
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mv_stream<Tr, 2, DUAL, X2, true, NT, XS>, NT, lds) !=
           hipSuccess ||
       per_cu <= 0)
     per_cu = 1;
@@ -150,9 +152,9 @@ static void launch_stream_x(const MvArgs& a, int groups, hipStream_t st) {
   const int nchunk = (a.K / QK_K) * Tr::CHUNKS, npass = (nchunk + WAVE - 1) / WAVE;
   const int max_steps = ((groups + waves - 1) / waves) * npass;
   if (max_steps > 1)
-    hipLaunchKernelGGL((mv_stream<Tr, 2, DUAL, X2, true, NT>), dim3(blocks), dim3(NT), lds, st, a);
+    hipLaunchKernelGGL((mv_stream<Tr, 2, DUAL, X2, true, NT, XS>), dim3(blocks), dim3(NT), lds, st, a);
   else
-    hipLaunchKernelGGL((mv_stream<Tr, 2, DUAL, X2, false, NT>), dim3(blocks), dim3(NT), lds, st, a);
+    hipLaunchKernelGGL((mv_stream<Tr, 2, DUAL, X2, false, NT, XS>), dim3(blocks), dim3(NT), lds, st, a);
 }
 
 // Workgroup size: 512 threads (one workgroup per CU, so x is staged once per CU instead of twice)
@@ -164,6 +166,20 @@ static void launch_stream(const MvArgs& a, int groups, hipStream_t st) {
   if (nt_env < 0) {
     const char* e = getenv("IEK_MV_NT");
     nt_env = e ? atoi(e) : 0;
+  }
+  if constexpr (std::is_same<Tr, Q8RTr>::value) {
+    // f32 staging issued ahead of the weight loads when x and its companions are float4-aligned
+    auto al = [](const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    if (a.K % 4 == 0 && al(a.x) && al(a.norm_w) && al(a.pre_t) && al(a.pre_w) && al(a.pre_out)) {
+      if (a.K <= 2048) {
+        launch_stream_x<Tr, DUAL, false, 256, 2>(a, groups, st);
+        return;
+      }
+      if (a.K <= 8192) {
+        launch_stream_x<Tr, DUAL, false, 256, 8>(a, groups, st);
+        return;
+      }
+    }
   }
   if constexpr (Tr::I8) {
     const bool wide = nt_env == 512 || (nt_env == 0 && a.K > 4096);

@@ -420,6 +420,138 @@ IEK_DEV void stage_i8_finish(const MvArgs& a, const Lds& L, int pos, XPre& p, bo
 }
 
 
+// ---- f32 staging split like the int8 one ------------------------------------------------------
+// Thread t owns the float4 slots t + 256 s (s < S, K <= 1024 S; the host picks S) of x, the norm
+// weight and the residual-update inputs (pre_t, pre_w). stage32_issue loads them (the conditional
+// ones first, x last, ahead of the weight loads); stage32_finish computes the staging with the
+// roundings of stage / stage_pre.
+template <int S>
+struct XPre32 {
+  float4 x[S], w[S], t[S], tw[S];
+  float4 res[4];
+  float2 rope;
+  float ev;
+};
+
+template <int S>
+IEK_DEV void stage32_issue(const MvArgs& a, XPre32<S>& p, int pos, int ev_idx) {
+  const int tid = threadIdx.x, K4 = a.K >> 2;
+  if (a.pre_t) {
+    const float4* t4 = reinterpret_cast<const float4*>(a.pre_t);
+    const float4* tw4 = reinterpret_cast<const float4*>(a.pre_w);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int i = min(tid + 256 * s, K4 - 1);
+      p.t[s] = t4[i];
+      p.tw[s] = tw4[i];
+    }
+  }
+  if (a.norm_w) {
+    const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
+#pragma unroll
+    for (int s = 0; s < S; ++s) p.w[s] = w4[min(tid + 256 * s, K4 - 1)];
+  }
+  if (ev_idx >= 0) {
+    p.ev = (a.epi == EPI_GELU_MUL ? a.mulv : a.resid)[ev_idx];
+  } else if (res_vec(a)) {
+    const float4* r4 = reinterpret_cast<const float4*>(a.resid);
+    const int n4 = a.n[0] >> 2;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) p.res[u] = r4[min(tid + 256 * u, n4 - 1)];
+  }
+  if (a.epi == EPI_QKV)
+    p.rope = reinterpret_cast<const float2*>(a.rope_cs)[(size_t)pos * a.npairs + min(tid, a.npairs - 1)];
+  const float4* x4 = reinterpret_cast<const float4*>(a.x);
+#pragma unroll
+  for (int s = 0; s < S; ++s) p.x[s] = x4[min(tid + 256 * s, K4 - 1)];
+}
+
+template <int S>
+IEK_DEV void stage32_finish(const MvArgs& a, const Lds& L, int pos, XPre32<S>& p, bool res_lds) {
+  __shared__ float red[4];
+  const int tid = threadIdx.x, K = a.K, K4 = K >> 2;
+  // the empty asm statements keep the arithmetic below the weight loads (as in stage_i8_finish;
+  // the memory clobber also keeps them from being hoisted among the loads)
+  auto pin = [](float4& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)::"memory"); };
+#pragma unroll
+  for (int s = 0; s < S; ++s) pin(p.x[s]);
+  float4* L4 = reinterpret_cast<float4*>(L.x);
+  float4 y[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) y[s] = p.x[s];
+  if (a.pre_t) {
+    // y = x + (t * w) / rms(t) [* scale], each step rounded as in stage_pre; workgroup 0 stores y
+    float st = 0.f;
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+      if (tid + 256 * s < K4) {
+        const float4 t = p.t[s];
+        st += t.x * t.x;
+        st += t.y * t.y;
+        st += t.z * t.z;
+        st += t.w * t.w;
+      }
+    const float rms_t = rms_of(block_sum_mv(st, red), K, a.eps);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int i = tid + 256 * s;
+      if (i < K4) {
+        const float4 x = p.x[s], t = p.t[s], w = p.tw[s];
+        float4 v = make_float4(x.x + div_rn(mul_rn(t.x, w.x), rms_t), x.y + div_rn(mul_rn(t.y, w.y), rms_t),
+                               x.z + div_rn(mul_rn(t.z, w.z), rms_t), x.w + div_rn(mul_rn(t.w, w.w), rms_t));
+        if (a.pre_has_scale)
+          v = make_float4(mul_rn(v.x, a.pre_scale), mul_rn(v.y, a.pre_scale), mul_rn(v.z, a.pre_scale),
+                          mul_rn(v.w, a.pre_scale));
+        if (blockIdx.x == 0) reinterpret_cast<float4*>(a.pre_out)[i] = v;
+        y[s] = v;
+      }
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int i = tid + 256 * s;
+    if (i < K4) {
+      const float4 v = y[s];
+      ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+      if (a.norm_w) {
+        const float4 w = p.w[s];
+        L4[i] = make_float4(mul_rn(v.x, w.x), mul_rn(v.y, w.y), mul_rn(v.z, w.z), mul_rn(v.w, w.w));
+      } else {
+        L4[i] = v;
+      }
+    }
+  }
+  if (a.epi == EPI_RESID && res_lds) {
+    const int N = a.n[0];
+    if (res_vec(a)) {
+      float4* d4 = reinterpret_cast<float4*>(L.res);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (tid + 256 * u < (N >> 2)) d4[tid + 256 * u] = p.res[u];
+    } else {
+      for (int i = tid; i < N; i += 256) L.res[i] = a.resid[i];
+    }
+  }
+  if (a.epi == EPI_QKV) {
+    if (tid < a.npairs) reinterpret_cast<float2*>(L.rope)[tid] = p.rope;
+    for (int i = 256 + tid; i < a.npairs; i += 256)
+      reinterpret_cast<float2*>(L.rope)[i] = reinterpret_cast<const float2*>(a.rope_cs)[(size_t)pos * a.npairs + i];
+  }
+  if (a.norm_w) {
+    const float rms = rms_of(block_sum_mv(ss, red), K, a.eps);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int i = tid + 256 * s;
+      if (i < K4) {
+        const float4 v = L4[i];
+        L4[i] = make_float4(div_rn(v.x, rms), div_rn(v.y, rms), div_rn(v.z, rms), div_rn(v.w, rms));
+      }
+    }
+  }
+  __syncthreads();
+}
+
 // Segment fields picked with constant indices: a dynamic index into the by-value argument block
 // becomes a vector memory load, whose wait would also drain the in-flight weight prefetch.
 IEK_DEV const uint8_t* seg_w(const MvArgs& a, int s) { return s == 0 ? a.w[0] : (s == 1 ? a.w[1] : a.w[2]); }
@@ -1019,12 +1151,13 @@ IEK_DEV void mv_prefetch(const MvArgs& a, typename Tr::template Buf<DUAL ? 2 * R
 // other buffer is always in flight while one is computed. MULTI (the host's choice, when some
 // wave has more than one step) keeps two buffers in flight from the start; single-step launches
 // carry only one.
-template <class Tr, int R, bool DUAL, bool COH = false, bool X2 = false, bool MULTI = true, int NT = 256>
+template <class Tr, int R, bool DUAL, bool COH = false, bool X2 = false, bool MULTI = true, int NT = 256, int XS = 0>
 IEK_DEV void mv_body(const MvArgs& a, float* lds, int pos, typename Tr::template Buf<DUAL ? 2 * R : R>& A,
                      bool prefetched) {
   static_assert(!COH || Tr::I8, "coherent staging is implemented for the int8-staged traits");
   static_assert(!X2 || Tr::I8, "two-block staging is implemented for the int8-staged traits");
   static_assert(NT == 256 || (NT == 512 && Tr::I8), "512-thread workgroups are implemented for the int8-staged traits");
+  static_assert(XS == 0 || (!Tr::I8 && NT == 256 && !COH), "split f32 staging: 256-thread f32 traits");
   constexpr int NW = NT / 64;
   constexpr int NR = DUAL ? 2 * R : R;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1038,7 +1171,7 @@ IEK_DEV void mv_body(const MvArgs& a, float* lds, int pos, typename Tr::template
 #pragma unroll
   for (int r = 0; r < NR; ++r) acc[r] = 0.f;
   // the epilogue's residual / multiplier in a register when every wave has at most one row group
-  const bool ev_reg = Tr::I8 && (a.epi == EPI_RESID || a.epi == EPI_GELU_MUL) && G.groups <= G.stride;
+  const bool ev_reg = (Tr::I8 || XS > 0) && (a.epi == EPI_RESID || a.epi == EPI_GELU_MUL) && G.groups <= G.stride;
   int ev_idx = -1;
   if (ev_reg) {
     const int row0 = min(G.g0, G.groups - 1) * R;
@@ -1047,6 +1180,7 @@ IEK_DEV void mv_body(const MvArgs& a, float* lds, int pos, typename Tr::template
   }
   XPre xp;
   xp.ev = 0.f;
+  XPre32<(XS > 0 ? XS : 1)> xq;
 
   auto finish = [&](int it) {
     const int p = it % npass;
@@ -1092,15 +1226,23 @@ IEK_DEV void mv_body(const MvArgs& a, float* lds, int pos, typename Tr::template
   // x / residual / RoPE loads go out first, then the weight buffers, so the staging work overlaps
   // the weight fetch instead of queueing behind it.
   if constexpr (Tr::I8) stage_i8_issue<COH, X2, NT>(a, xp, pos, ev_idx);
+  if constexpr (XS > 0) {
+    stage32_issue<XS>(a, xq, pos, ev_idx);
+    xp.ev = 0.f;
+  }
   if (!prefetched) load(A, 0);
   if constexpr (MULTI) load(B, 1);
   // keep the staging arithmetic below the weight loads: scheduled among them, its first use of x
   // would hold the remaining weight loads back until x has arrived
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (Tr::I8)
+  if constexpr (Tr::I8) {
     stage_i8_finish<COH, X2, NT>(a, L, pos, xp, !ev_reg);
-  else
+  } else if constexpr (XS > 0) {
+    stage32_finish<XS>(a, L, pos, xq, !ev_reg);
+    xp.ev = xq.ev;
+  } else {
     stage(a, L, pos);
+  }
   if (steps > 0) {
     if constexpr (MULTI) {
       // Each buffer's refill is issued right after it was computed, unconditionally (the last one
