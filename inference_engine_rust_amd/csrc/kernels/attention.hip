@@ -13,7 +13,7 @@
 
 namespace iek {
 
-template <int HD>
+template <int HD, bool EARLY>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, const __half* __restrict__ kc,
                                                           const __half* __restrict__ vc, float* __restrict__ part,
                                                           float* __restrict__ out, int* __restrict__ counters,
@@ -23,8 +23,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
   // all arguments in one batch of scalar loads, ahead of the position they depend on
   asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(part), "s"(out), "s"(counters), "s"(n_heads), "s"(n_kv), "s"(ctx),
                "s"(pos_dev), "s"(window), "s"(scale), "s"(nsplit), "s"(spc));
-  attn_chunk_f16<HD>(q, kc, vc, part, out, counters, n_heads, n_kv, ctx, *pos_dev + 1, window, scale, nsplit,
-                     blockIdx.x, blockIdx.y, spc, smem);
+  attn_chunk_f16<HD, false, EARLY>(q, kc, vc, part, out, counters, n_heads, n_kv, ctx, pos_dev, 0, window, scale, nsplit,
+                                   blockIdx.x, blockIdx.y, spc, smem);
 }
 
 // f32 KV cache variant (Gemma-4 sessions keep the reference's f32 cache: with q/k head norms
@@ -175,9 +175,15 @@ static void attn_decode_hd(dim3 grid, hipStream_t st, const float* q, const void
     }
     const int spc = attn_slices_per_chunk(nsplit * SPLIT, window, target);
     const int nchunk = (nsplit + spc - 1) / spc;
-    hipLaunchKernelGGL(attn_decode_kernel<HD>, dim3(grid.x, nchunk), dim3(256), 0, st, q, (const __half*)kc,
-                       (const __half*)vc, part, out, counters, n_heads, n_kv, ctx, pos_dev, window, scale, nchunk,
-                       spc);
+    // without a window the first slice's loads go out before the position is known
+    if (window <= 0)
+      hipLaunchKernelGGL((attn_decode_kernel<HD, true>), dim3(grid.x, nchunk), dim3(256), 0, st, q, (const __half*)kc,
+                         (const __half*)vc, part, out, counters, n_heads, n_kv, ctx, pos_dev, window, scale, nchunk,
+                         spc);
+    else
+      hipLaunchKernelGGL((attn_decode_kernel<HD, false>), dim3(grid.x, nchunk), dim3(256), 0, st, q,
+                         (const __half*)kc, (const __half*)vc, part, out, counters, n_heads, n_kv, ctx, pos_dev,
+                         window, scale, nchunk, spc);
   }
 }
 

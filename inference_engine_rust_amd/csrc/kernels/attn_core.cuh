@@ -151,11 +151,11 @@ struct AttnSmem {
 // (max, sum, o[]) partial in slot `cp`; the last chunk of the KV head to finish merges the
 // group's heads. `total` = keys in the cache including this step's; chunks past the live range
 // return at once (uniformly).
-template <int HD, bool COH = false>
+template <int HD, bool COH = false, bool EARLY = false>
 IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restrict__ kc, const __half* __restrict__ vc,
                             float* __restrict__ part, float* __restrict__ out, int* __restrict__ counters,
-                            int n_heads, int n_kv, int ctx, int total, int window, float scale, int nslot, int kvh,
-                            int cp, int spc, char* smem) {
+                            int n_heads, int n_kv, int ctx, const int* pos_dev, int total_in, int window, float scale,
+                            int nslot, int kvh, int cp, int spc, char* smem) {
   constexpr int DPL = HD / 64;        // head dims per lane in the PV phase
   constexpr int KROW = HD + 8;        // padded K row (halves): 16-byte reads of different rows spread banks
   constexpr int U4 = SPLIT * HD / 8;  // uint4 per K (or V) slice
@@ -166,11 +166,7 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = n_heads / n_kv;
-  const int jmin = (window > 0 && total > window) ? total - window : 0;
   const int CK = SPLIT * spc;
-  const int c0 = max(cp * CK, jmin), c1 = min(total, (cp + 1) * CK);
-  if (c1 <= c0) return;  // uniform across the workgroup
-  const int sb0 = c0 / SPLIT, sb1 = (c1 + SPLIT - 1) / SPLIT;
   const AttnSmem<HD> S(smem);
   auto ks = reinterpret_cast<__half(*)[KROW]>(S.ks);
   auto vs = reinterpret_cast<__half(*)[VL ? HD : 8]>(S.vs);
@@ -181,8 +177,8 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
   // native vectors (a HIP uint4 array captured by the lambda would not be promoted to registers)
   typedef uint32_t kv4_t __attribute__((ext_vector_type(4)));
   kv4_t kr[U4 / 256], vr[VL ? U4 / 256 : 1];
-  auto issue = [&](int sb) {
-    const int j0 = max(sb * SPLIT, c0), nk = min((sb + 1) * SPLIT, c1) - j0;
+  // rows [j0, j0 + nk) of the cache; rows past nk repeat row j0 + nk - 1
+  auto issue_rows = [&](int j0, int nk) {
 #pragma unroll
     for (int u = 0; u < U4 / 256; ++u) {
       const int i = tid + 256 * u, row = j0 + min(i / (HD / 8), nk - 1), c8 = i % (HD / 8);
@@ -190,8 +186,32 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
       if constexpr (VL) vr[u] = *reinterpret_cast<const kv4_t*>(vh + (size_t)row * HD + 8 * c8);
     }
   };
-  issue(sb0);
-  for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = ld_f<COH>(q + (size_t)(kvh * G) * HD + i);
+  // EARLY (no window): the chunk's first slice does not depend on the position, so its rows (all
+  // 64, within the cache; rows past the live keys are finite, the cache being zeroed at
+  // allocation, and get weight 0) go out with q before the position load returns.
+  // q first (a fixed number of clamped loads per thread, G <= 8), so the wait for it leaves the
+  // K / V loads in flight
+  constexpr int QU = (8 * HD + 255) / 256;
+  float qv[QU];
+#pragma unroll
+  for (int u = 0; u < QU; ++u) qv[u] = ld_f<COH>(q + (size_t)(kvh * G) * HD + min(tid + 256 * u, G * HD - 1));
+  if constexpr (EARLY) issue_rows(cp * CK, min(SPLIT, ctx - cp * CK));
+  typedef __attribute__((address_space(4))) const int* ConstInt;  // a scalar load
+  const int total = pos_dev ? *(ConstInt)pos_dev + 1 : total_in;
+  const int jmin = (window > 0 && total > window) ? total - window : 0;
+  const int c0 = max(cp * CK, jmin), c1 = min(total, (cp + 1) * CK);
+  if (c1 <= c0) return;  // uniform across the workgroup
+#pragma unroll
+  for (int u = 0; u < QU; ++u) {
+    const int i = tid + 256 * u;
+    if (i < G * HD) qs[i / HD][i % HD] = qv[u];
+  }
+  const int sb0 = c0 / SPLIT, sb1 = (c1 + SPLIT - 1) / SPLIT;
+  auto issue = [&](int sb) {
+    const int j0 = max(sb * SPLIT, c0);
+    issue_rows(j0, min((sb + 1) * SPLIT, c1) - j0);
+  };
+  if constexpr (!EARLY) issue(sb0);
   float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f}, o_run[2][DPL];
 #pragma unroll
   for (int t = 0; t < 2; ++t)

@@ -137,7 +137,7 @@ __global__ __launch_bounds__(256, 2) void decode_step_kernel(StepArgs args) {
     const int spc = attn_slices_per_chunk(S.nsplit * SPLIT, L.window), nchunk = (S.nsplit + spc - 1) / spc;
     const int items = S.n_kv * nchunk;
     for (int it = blockIdx.x; it < items; it += nwg) {
-      attn_chunk_f16<HD, true>(L.q, L.kc, L.vc, S.part, L.att, S.counters, S.n_heads, S.n_kv, S.ctx, pos + 1,
+      attn_chunk_f16<HD, true>(L.q, L.kc, L.vc, S.part, L.att, S.counters, S.n_heads, S.n_kv, S.ctx, nullptr, pos + 1,
                                L.window, S.scale, nchunk, it % S.n_kv, it / S.n_kv, spc, reinterpret_cast<char*>(lds));
       __syncthreads();
     }

@@ -49,6 +49,9 @@ Session::Session(Model* m) : m_(m) {
   for (auto& L : c.layers)
     if (L.kv_borrow < 0) total += 2 * (size_t)c.n_kv_heads * ctx_ * L.head_dim;
   IEK_HIP(hipMalloc(&kv_blob_, std::max<size_t>(total * esz, 16)));
+  // zeroed once: the decode attention may read cache rows past the live keys (weighted 0), which
+  // must hold finite values
+  IEK_HIP(hipMemset(kv_blob_, 0, std::max<size_t>(total * esz, 16)));
   char* p = static_cast<char*>(kv_blob_);
   for (int li = 0; li < c.n_layers; ++li) {
     const LayerSpec& L = c.layers[li];
