@@ -13,17 +13,17 @@
 
 namespace iek {
 
-template <int HD, bool EARLY>
-__global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, const __half* __restrict__ kc,
+template <int HD, bool EARLY, int SETS, bool COH>
+__global__ __launch_bounds__(256 * SETS) void attn_decode_kernel(const float* __restrict__ q, const __half* __restrict__ kc,
                                                           const __half* __restrict__ vc, float* __restrict__ part,
                                                           float* __restrict__ out, int* __restrict__ counters,
                                                           int n_heads, int n_kv, int ctx, const int* pos_dev,
                                                           int window, float scale, int nsplit, int spc) {
-  __shared__ __align__(16) char smem[AttnSmem<HD>::BYTES];
+  __shared__ __align__(16) char smem[AttnSmem<HD, SETS>::BYTES];
   // all arguments in one batch of scalar loads, ahead of the position they depend on
   asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(part), "s"(out), "s"(counters), "s"(n_heads), "s"(n_kv), "s"(ctx),
                "s"(pos_dev), "s"(window), "s"(scale), "s"(nsplit), "s"(spc));
-  attn_chunk_f16<HD, false, EARLY>(q, kc, vc, part, out, counters, n_heads, n_kv, ctx, pos_dev, 0, window, scale, nsplit,
+  attn_chunk_f16<HD, COH, EARLY, SETS>(q, kc, vc, part, out, counters, n_heads, n_kv, ctx, pos_dev, 0, window, scale, nsplit,
                                    blockIdx.x, blockIdx.y, spc, smem);
 }
 
@@ -175,15 +175,39 @@ static void attn_decode_hd(dim3 grid, hipStream_t st, const float* q, const void
     }
     const int spc = attn_slices_per_chunk(nsplit * SPLIT, window, target);
     const int nchunk = (nsplit + spc - 1) / spc;
+    // Chunks of several slices (long contexts) run two slice streams per workgroup (head dims up to
+    // 128: the doubled K / V buffers fit beside a second workgroup on the CU), and publish their
+    // partials with coherent stores and a relaxed count (no L2 write-back / invalidate around the
+    // arrival, measured faster there; one-slice chunks are faster with plain stores).
+    static int sets_env = -1;
+    if (sets_env < 0) {
+      const char* e = getenv("IEK_ATTN_SETS");
+      sets_env = e ? std::max(0, atoi(e)) : 0;
+    }
+    const bool two = HD <= 128 && (sets_env ? sets_env == 2 : spc >= 2);
+    static int coh = -2;
+    if (coh == -2) {
+      const char* e = getenv("IEK_ATTN_COH");
+      coh = e ? atoi(e) : -1;
+    }
+    const bool use_coh = coh < 0 ? two : coh != 0;
+    auto go = [&](auto kern, int nt) {
+      hipLaunchKernelGGL(kern, dim3(grid.x, nchunk), dim3(nt), 0, st, q, (const __half*)kc, (const __half*)vc, part,
+                         out, counters, n_heads, n_kv, ctx, pos_dev, window, scale, nchunk, spc);
+    };
     // without a window the first slice's loads go out before the position is known
-    if (window <= 0)
-      hipLaunchKernelGGL((attn_decode_kernel<HD, true>), dim3(grid.x, nchunk), dim3(256), 0, st, q, (const __half*)kc,
-                         (const __half*)vc, part, out, counters, n_heads, n_kv, ctx, pos_dev, window, scale, nchunk,
-                         spc);
-    else
-      hipLaunchKernelGGL((attn_decode_kernel<HD, false>), dim3(grid.x, nchunk), dim3(256), 0, st, q,
-                         (const __half*)kc, (const __half*)vc, part, out, counters, n_heads, n_kv, ctx, pos_dev,
-                         window, scale, nchunk, spc);
+    constexpr int S2 = HD <= 128 ? 2 : 1;
+    if (use_coh) {
+      if (window <= 0)
+        two ? go(attn_decode_kernel<HD, true, S2, true>, 512) : go(attn_decode_kernel<HD, true, 1, true>, 256);
+      else
+        two ? go(attn_decode_kernel<HD, false, S2, true>, 512) : go(attn_decode_kernel<HD, false, 1, true>, 256);
+    } else {
+      if (window <= 0)
+        two ? go(attn_decode_kernel<HD, true, S2, false>, 512) : go(attn_decode_kernel<HD, true, 1, false>, 256);
+      else
+        two ? go(attn_decode_kernel<HD, false, S2, false>, 512) : go(attn_decode_kernel<HD, false, 1, false>, 256);
+    }
   }
 }
 

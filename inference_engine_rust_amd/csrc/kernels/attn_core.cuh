@@ -18,13 +18,12 @@ constexpr int SPLIT = 64;
 // head to finish merges its query heads (counted with an agent-scope acq_rel atomic per KV head).
 // Merge of the live slice partials of query head h by one wave: global (max, sum) over slices,
 // then each lane folds its head dims of every slice with the rescaled weights. One round trip
-// fetches lane s's (max, sum) pair together with the first batch of o rows; further batches
+// fetches lane s's (max, sum) pair together with the first batch of B o rows; further batches
 // follow only for more than B live slots.
-template <int HD, bool COH = false>
+template <int HD, bool COH = false, int B = (HD >= 512 ? 4 : 2048 / HD)>
 IEK_DEV void merge_head(const float* __restrict__ part, float* __restrict__ out, int h, int nsplit, int s0, int nlive,
                         float* wsl) {
   constexpr int DPL = HD / 64;
-  constexpr int B = DPL >= 8 ? 4 : 32 / DPL;  // o rows per batch (32 floats per lane in flight)
   const int lane = threadIdx.x & 63;
   const int ns = min(nlive - s0, 256);
   const float* pr = part + ((size_t)h * nsplit + s0) * (HD + 2);
@@ -88,8 +87,9 @@ IEK_DEV void merge_head(const float* __restrict__ part, float* __restrict__ out,
 // barrier orders every wave's partial stores before thread 0's agent-scope acq_rel add (which
 // writes back this XCD's L2); the last arrival's acquire side invalidates its L2 before the
 // partials are read. The counter is reset for the next launch.
-// s0 .. nlive-1 are the live partial slots of the KV head.
-template <int HD, bool COH = false>
+// s0 .. nlive-1 are the live partial slots of the KV head. WIDE: up to twice the batch when that
+// fetches the live slots in one round trip (many-slot merges).
+template <int HD, bool COH = false, bool WIDE = false>
 // The last workgroup to arrive on counters[cidx] merges query heads [gb, gb + gn) of KV head kvh
 // (G query heads per KV head).
 IEK_DEV void merge_if_last(const float* __restrict__ part, float* __restrict__ out, int* __restrict__ counters,
@@ -113,18 +113,26 @@ IEK_DEV void merge_if_last(const float* __restrict__ part, float* __restrict__ o
   __syncthreads();
   if (!last) return;
   if (!COH) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  for (int g = gb + wave; g < gb + gn; g += 4)
-    merge_head<HD, COH>(part, out, kvh * G + g, nsplit, s0, nlive, wsl + 256 * wave);
+  constexpr int B1 = HD >= 512 ? 4 : 2048 / HD;  // 32 floats per lane
+  const bool wide = WIDE && nlive - s0 > B1 && nlive - s0 <= 2 * B1;
+  for (int g = gb + wave; g < gb + gn; g += 4) {
+    if (WIDE && wide)
+      merge_head<HD, COH, 2 * B1>(part, out, kvh * G + g, nsplit, s0, nlive, wsl + 256 * wave);
+    else
+      merge_head<HD, COH, B1>(part, out, kvh * G + g, nsplit, s0, nlive, wsl + 256 * wave);
+  }
 }
 
 // LDS of one slice item: K rows (padded), V rows (HD <= 256), the group's q, the wave's
-// probabilities, the merge weights and the last-arrival flag.
-template <int HD>
+// probabilities, the merge weights and the last-arrival flag; K, V and the probabilities once per
+// slice stream (SETS).
+template <int HD, int SETS = 1>
 struct AttnSmem {
   static constexpr int KROW = HD + 8;
   static constexpr bool VL = HD <= 256;
-  static constexpr size_t KS = (size_t)SPLIT * KROW * 2, VS = VL ? (size_t)SPLIT * HD * 2 : 16,
-                          QS = 8 * (size_t)HD * 4, PS = 4 * SPLIT * 4, WS = 4 * 256 * 4;
+  static constexpr size_t KS1 = (size_t)SPLIT * KROW * 2, VS1 = VL ? (size_t)SPLIT * HD * 2 : 16;
+  static constexpr size_t KS = SETS * KS1, VS = SETS * VS1, QS = 8 * (size_t)HD * 4, PS = 4 * SETS * SPLIT * 4,
+                          WS = 4 * 256 * 4;
   static constexpr size_t BYTES = KS + VS + QS + PS + WS + 16;
   __half* ks;
   __half* vs;
@@ -151,7 +159,10 @@ struct AttnSmem {
 // (max, sum, o[]) partial in slot `cp`; the last chunk of the KV head to finish merges the
 // group's heads. `total` = keys in the cache including this step's; chunks past the live range
 // return at once (uniformly).
-template <int HD, bool COH = false, bool EARLY = false>
+// SETS = 2 (a 512-thread workgroup): two slice streams, threads [256 s, 256 s + 256) taking the
+// chunk's slices s, s + 2, ... with their own LDS buffers and running (max, sum, o); stream 1
+// hands its state to stream 0 through LDS at the end, and stream 0 publishes the partial.
+template <int HD, bool COH = false, bool EARLY = false, int SETS = 1>
 IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restrict__ kc, const __half* __restrict__ vc,
                             float* __restrict__ part, float* __restrict__ out, int* __restrict__ counters,
                             int n_heads, int n_kv, int ctx, const int* pos_dev, int total_in, int window, float scale,
@@ -163,21 +174,24 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
   // the P.V phase reads V rows straight from memory (each row one coalesced 1 KB wave load).
   constexpr bool VL = HD <= 256;
   static_assert(HD == 64 || HD == 128 || HD == 256 || HD == 512, "head_dim");
-  const int tid = threadIdx.x, lane = tid & 63;
+  static_assert(SETS == 1 || SETS == 2, "slice streams");
+  const int tid = threadIdx.x & 255, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int set = SETS == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 8);
   const int G = n_heads / n_kv;
   const int CK = SPLIT * spc;
-  const AttnSmem<HD> S(smem);
-  auto ks = reinterpret_cast<__half(*)[KROW]>(S.ks);
-  auto vs = reinterpret_cast<__half(*)[VL ? HD : 8]>(S.vs);
+  const AttnSmem<HD, SETS> S(smem);
+  auto ks = reinterpret_cast<__half(*)[KROW]>(S.ks + (size_t)set * SPLIT * KROW);
+  auto vs = reinterpret_cast<__half(*)[VL ? HD : 8]>(S.vs + (VL ? (size_t)set * SPLIT * HD : 0));
   auto qs = reinterpret_cast<float(*)[HD]>(S.qs);
-  auto ps = reinterpret_cast<float(*)[SPLIT]>(S.ps);
+  auto ps = reinterpret_cast<float(*)[SPLIT]>(S.ps + (size_t)set * 4 * SPLIT);
   const __half* kh = kc + (size_t)kvh * ctx * HD;
   const __half* vh = vc + (size_t)kvh * ctx * HD;
   // native vectors (a HIP uint4 array captured by the lambda would not be promoted to registers)
   typedef uint32_t kv4_t __attribute__((ext_vector_type(4)));
   kv4_t kr[U4 / 256], vr[VL ? U4 / 256 : 1];
-  // rows [j0, j0 + nk) of the cache; rows past nk repeat row j0 + nk - 1
+  // rows [j0, j0 + nk) of the cache; rows past nk repeat row j0 + nk - 1 (nk <= 0: row j0 + nk - 1,
+  // within the cache for j0 + nk <= ctx)
   auto issue_rows = [&](int j0, int nk) {
 #pragma unroll
     for (int u = 0; u < U4 / 256; ++u) {
@@ -195,7 +209,7 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
   float qv[QU];
 #pragma unroll
   for (int u = 0; u < QU; ++u) qv[u] = ld_f<COH>(q + (size_t)(kvh * G) * HD + min(tid + 256 * u, G * HD - 1));
-  if constexpr (EARLY) issue_rows(cp * CK, min(SPLIT, ctx - cp * CK));
+  if constexpr (EARLY) issue_rows(cp * CK + SPLIT * set, min(SPLIT, ctx - cp * CK - SPLIT * set));
   typedef __attribute__((address_space(4))) const int* ConstInt;  // a scalar load
   const int total = pos_dev ? *(ConstInt)pos_dev + 1 : total_in;
   const int jmin = (window > 0 && total > window) ? total - window : 0;
@@ -211,13 +225,14 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
     const int j0 = max(sb * SPLIT, c0);
     issue_rows(j0, min((sb + 1) * SPLIT, c1) - j0);
   };
-  if constexpr (!EARLY) issue(sb0);
+  if constexpr (!EARLY) issue(sb0 + set);
   float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f}, o_run[2][DPL];
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int d = 0; d < DPL; ++d) o_run[t][d] = 0.f;
-  for (int sb = sb0; sb < sb1; ++sb) {
+  for (int pb = sb0; pb < sb1; pb += SETS) {
+    const int sb = pb + set;  // this stream's slice (none past sb1: the stream idles this round)
     const int j0 = max(sb * SPLIT, c0), nk = min((sb + 1) * SPLIT, c1) - j0;
     __syncthreads();  // the previous slice's LDS reads are done
 #pragma unroll
@@ -227,7 +242,8 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
       if constexpr (VL) *reinterpret_cast<kv4_t*>(&vs[row][8 * c8]) = vr[u];
     }
     __syncthreads();
-    if (sb + 1 < sb1) issue(sb + 1);
+    if (sb + SETS < sb1) issue(sb + SETS);
+    if (SETS > 1 && sb >= sb1) continue;
     const __half* vb = vh + (size_t)j0 * HD;
     const bool valid = lane < nk;
 #pragma unroll
@@ -295,10 +311,44 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
       __builtin_amdgcn_wave_barrier();  // ps[wave] is rewritten by the next head or slice
     }
   }
+  if constexpr (SETS == 2) {
+    // stream 1's (max, sum, o) per head into the free K buffer of stream 0, folded in by stream 0
+    float* hand = reinterpret_cast<float*>(S.ks);  // [4 waves][2 heads][HD + 2]
+    __syncthreads();
+    if (set == 1) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        if (wave + 4 * t >= G) break;
+        float* hp = hand + (size_t)(2 * wave + t) * (HD + 2);
+        if (lane == 0) {
+          hp[0] = m_run[t];
+          hp[1] = l_run[t];
+        }
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) hp[2 + DPL * lane + d] = o_run[t][d];
+      }
+    }
+    __syncthreads();
+    if (set == 0) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        if (wave + 4 * t >= G) break;
+        const float* hp = hand + (size_t)(2 * wave + t) * (HD + 2);
+        const float m1 = hp[0], l1 = hp[1];
+        // stream 0 always has a live key (c1 > c0), so m_new is finite
+        const float m_new = fmaxf(m_run[t], m1);
+        const float w0 = expf(m_run[t] - m_new), w1 = m1 == -INFINITY ? 0.f : expf(m1 - m_new);
+        l_run[t] = l_run[t] * w0 + l1 * w1;
+        m_run[t] = m_new;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) o_run[t][d] = o_run[t][d] * w0 + hp[2 + DPL * lane + d] * w1;
+      }
+    }
+  }
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int g = wave + 4 * t;
-    if (g >= G) break;
+    if (g >= G || set != 0) break;
     float* pr = part + ((size_t)(kvh * G + g) * nslot + cp) * (HD + 2);
     if (lane == 0) {
       st_f<COH>(pr, m_run[t]);
@@ -307,7 +357,9 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
 #pragma unroll
     for (int d = 0; d < DPL; ++d) st_f<COH>(pr + 2 + DPL * lane + d, o_run[t][d]);
   }
-  merge_if_last<HD, COH>(part, out, counters, kvh, G, nslot, jmin / CK, (total + CK - 1) / CK, wave, S.last, S.wsl);
+  // stream 1's waves pass a wave index past the group: they take part in the arrival only
+  merge_if_last<HD, COH, (SETS > 1)>(part, out, counters, kvh, G, nslot, jmin / CK, (total + CK - 1) / CK,
+                                      set ? 8 : wave, S.last, S.wsl);
 }
 
 // Slices per chunk for a cache of `max_len` keys: one up to `target` slices per KV head, then
