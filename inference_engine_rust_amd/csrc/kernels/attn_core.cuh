@@ -159,9 +159,10 @@ struct AttnSmem {
 // (max, sum, o[]) partial in slot `cp`; the last chunk of the KV head to finish merges the
 // group's heads. `total` = keys in the cache including this step's; chunks past the live range
 // return at once (uniformly).
-// SETS = 2 (a 512-thread workgroup): two slice streams, threads [256 s, 256 s + 256) taking the
-// chunk's slices s, s + 2, ... with their own LDS buffers and running (max, sum, o); stream 1
-// hands its state to stream 0 through LDS at the end, and stream 0 publishes the partial.
+// SETS = 2 (512 threads): two slice streams, threads [256 s, 256 s + 256) taking the
+// chunk's slices s, s + SETS, ... with their own LDS buffers and running (max, sum, o); streams
+// 1.. hand their state to stream 0 through LDS at the end, and stream 0 publishes the partial. A
+// chunk that is its KV head's only one (nslot = 1) writes the output itself (o / sum) instead.
 template <int HD, bool COH = false, bool EARLY = false, int SETS = 1>
 IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restrict__ kc, const __half* __restrict__ vc,
                             float* __restrict__ part, float* __restrict__ out, int* __restrict__ counters,
@@ -311,15 +312,15 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
       __builtin_amdgcn_wave_barrier();  // ps[wave] is rewritten by the next head or slice
     }
   }
-  if constexpr (SETS == 2) {
-    // stream 1's (max, sum, o) per head into the free K buffer of stream 0, folded in by stream 0
-    float* hand = reinterpret_cast<float*>(S.ks);  // [4 waves][2 heads][HD + 2]
+  if constexpr (SETS > 1) {
+    // streams 1..'s (max, sum, o) per head into the free K buffer of stream 0, folded in by stream 0
+    float* hand = reinterpret_cast<float*>(S.ks);  // [SETS - 1][4 waves][2 heads][HD + 2]
     __syncthreads();
-    if (set == 1) {
+    if (set > 0) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         if (wave + 4 * t >= G) break;
-        float* hp = hand + (size_t)(2 * wave + t) * (HD + 2);
+        float* hp = hand + (size_t)(8 * (set - 1) + 2 * wave + t) * (HD + 2);
         if (lane == 0) {
           hp[0] = m_run[t];
           hp[1] = l_run[t];
@@ -333,17 +334,32 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         if (wave + 4 * t >= G) break;
-        const float* hp = hand + (size_t)(2 * wave + t) * (HD + 2);
-        const float m1 = hp[0], l1 = hp[1];
-        // stream 0 always has a live key (c1 > c0), so m_new is finite
-        const float m_new = fmaxf(m_run[t], m1);
-        const float w0 = expf(m_run[t] - m_new), w1 = m1 == -INFINITY ? 0.f : expf(m1 - m_new);
-        l_run[t] = l_run[t] * w0 + l1 * w1;
-        m_run[t] = m_new;
+        for (int s1 = 1; s1 < SETS; ++s1) {
+          const float* hp = hand + (size_t)(8 * (s1 - 1) + 2 * wave + t) * (HD + 2);
+          const float m1 = hp[0], l1 = hp[1];
+          // stream 0 always has a live key (c1 > c0), so m_new is finite
+          const float m_new = fmaxf(m_run[t], m1);
+          const float w0 = expf(m_run[t] - m_new), w1 = m1 == -INFINITY ? 0.f : expf(m1 - m_new);
+          l_run[t] = l_run[t] * w0 + l1 * w1;
+          m_run[t] = m_new;
 #pragma unroll
-        for (int d = 0; d < DPL; ++d) o_run[t][d] = o_run[t][d] * w0 + hp[2 + DPL * lane + d] * w1;
+          for (int d = 0; d < DPL; ++d) o_run[t][d] = o_run[t][d] * w0 + hp[2 + DPL * lane + d] * w1;
+        }
       }
     }
+  }
+  if (nslot == 1) {
+    // the KV head's only chunk: the output directly, as the merge of one partial would give it
+    if (set == 0) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int g = wave + 4 * t;
+        if (g >= G) break;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) st_f<COH>(out + (size_t)(kvh * G + g) * HD + DPL * lane + d, o_run[t][d] / l_run[t]);
+      }
+    }
+    return;
   }
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
