@@ -145,7 +145,7 @@ def kernel_roofline(E, model, cfg, reps):
     avg_ms = ev0.elapsed_time(ev1) / reps
     algo = ts[0]["bytes"] + 4 * (K + N)
     gbs = algo / (avg_ms * 1e-3) / 1e9
-    return {"kernel": "mv_stream<Q4I8Tr,2,false,false,true> (decode matvec, Q4_K 14336x4096)", "bound": "hbm", "achieved": round(gbs, 1),
+    return {"kernel": "mv_stream<Q4Tr,2,false,true,256,4> (decode matvec, Q4_K 14336x4096, f32 activations)", "bound": "hbm", "achieved": round(gbs, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(algo),
             "algorithmic_bytes_per_launch": algo, "avg_launch_us": round(avg_ms * 1e3, 3), "launches": reps}

@@ -35,7 +35,6 @@ SOURCES = [
     "kernels/gemm_mfma.hip",
     "kernels/gemm_q.hip",
     "kernels/gemma.hip",
-    "kernels/decode_step.hip",
     "model.cpp",
     "session.cpp",
     "api.cpp",

@@ -155,8 +155,7 @@ iek_status iek_greedy_next_token(iek_session* s, uint32_t* out) { IEK_API_TRY(*o
 iek_status iek_session_generate_greedy(iek_session* s, size_t n, uint32_t* out) {
   IEK_API_TRY({
     if (n > (size_t)INT32_MAX) fail(ST_KVCACHE, "KVCache is Full");
-    const char* eg = getenv("IEK_NO_GRAPH");
-    s->s->generate_greedy((int)n, out, !(eg && eg[0] == '1'));
+    s->s->generate_greedy((int)n, out);
   })
 }
 

@@ -167,47 +167,24 @@ static void attn_decode_hd(dim3 grid, hipStream_t st, const float* q, const void
                        (const float*)kc, (const float*)vc, part, out, counters, n_heads, n_kv, ctx, pos_dev, window,
                        scale, nsplit);
   } else {
-    // fp16 cache: chunks of spc slices; one partial slot per chunk
-    static int target = -1;
-    if (target < 0) {
-      const char* e = getenv("IEK_ATTN_CHUNKS");
-      target = e ? std::max(1, atoi(e)) : 32;
-    }
-    const int spc = attn_slices_per_chunk(nsplit * SPLIT, window, target);
+    // fp16 cache: chunks of spc slices (about 32 chunks per KV head); one partial slot per chunk
+    const int spc = attn_slices_per_chunk(nsplit * SPLIT, window, 32);
     const int nchunk = (nsplit + spc - 1) / spc;
     // Chunks of several slices (long contexts) run two slice streams per workgroup (head dims up to
     // 128: the doubled K / V buffers fit beside a second workgroup on the CU), and publish their
     // partials with coherent stores and a relaxed count (no L2 write-back / invalidate around the
     // arrival, measured faster there; one-slice chunks are faster with plain stores).
-    static int sets_env = -1;
-    if (sets_env < 0) {
-      const char* e = getenv("IEK_ATTN_SETS");
-      sets_env = e ? std::max(0, atoi(e)) : 0;
-    }
-    const bool two = HD <= 128 && (sets_env ? sets_env == 2 : spc >= 2);
-    static int coh = -2;
-    if (coh == -2) {
-      const char* e = getenv("IEK_ATTN_COH");
-      coh = e ? atoi(e) : -1;
-    }
-    const bool use_coh = coh < 0 ? two : coh != 0;
+    const bool two = HD <= 128 && spc >= 2;
     auto go = [&](auto kern, int nt) {
       hipLaunchKernelGGL(kern, dim3(grid.x, nchunk), dim3(nt), 0, st, q, (const __half*)kc, (const __half*)vc, part,
                          out, counters, n_heads, n_kv, ctx, pos_dev, window, scale, nchunk, spc);
     };
     // without a window the first slice's loads go out before the position is known
     constexpr int S2 = HD <= 128 ? 2 : 1;
-    if (use_coh) {
-      if (window <= 0)
-        two ? go(attn_decode_kernel<HD, true, S2, true>, 512) : go(attn_decode_kernel<HD, true, 1, true>, 256);
-      else
-        two ? go(attn_decode_kernel<HD, false, S2, true>, 512) : go(attn_decode_kernel<HD, false, 1, true>, 256);
-    } else {
-      if (window <= 0)
-        two ? go(attn_decode_kernel<HD, true, S2, false>, 512) : go(attn_decode_kernel<HD, true, 1, false>, 256);
-      else
-        two ? go(attn_decode_kernel<HD, false, S2, false>, 512) : go(attn_decode_kernel<HD, false, 1, false>, 256);
-    }
+    if (window <= 0)
+      two ? go(attn_decode_kernel<HD, true, S2, true>, 512) : go(attn_decode_kernel<HD, true, 1, false>, 256);
+    else
+      two ? go(attn_decode_kernel<HD, false, S2, true>, 512) : go(attn_decode_kernel<HD, false, 1, false>, 256);
   }
 }
 

@@ -202,8 +202,8 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
     }
   };
   // EARLY (no window): the chunk's first slice does not depend on the position, so its rows (all
-  // 64, within the cache; rows past the live keys are finite, the cache being zeroed at
-  // allocation, and get weight 0) go out with q before the position load returns.
+  // 64, within the cache) go out with q before the position load returns; rows past the live keys
+  // get score -inf by a select and are skipped by P.V, so whatever they hold never reaches o.
   // q first (a fixed number of clamped loads per thread, G <= 8), so the wait for it leaves the
   // K / V loads in flight
   constexpr int QU = (8 * HD + 255) / 256;
@@ -274,12 +274,14 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      // P.V: lane owns dims DPL*lane .. +DPL-1; keys past the live slice carry p = 0
+      // P.V over the slice's live keys only: lane owns dims DPL*lane .. +DPL-1. Rows past them may
+      // hold anything (the cache is not cleared between conversations), so they are not read
+      // here, not even with weight 0 (0 * inf is NaN).
       float o[DPL];
 #pragma unroll
       for (int d = 0; d < DPL; ++d) o[d] = o_run[t][d] * corr;
 #pragma unroll 8
-      for (int j = 0; j < SPLIT; ++j) {
+      for (int j = 0; j < nk; ++j) {
         const float pj = ps[wave][j];
         if constexpr (DPL == 1) {
           o[0] += pj * __half2float(vs[j][lane]);

@@ -794,12 +794,7 @@ static void gemm_q_launch(GemmQArgs g, hipStream_t st) {
   for (int i = g.nseg; i <= 3; ++i) g.tile_start[i] = t;
   const int mtiles = (g.M + BM - 1) / BM;
   const int tiles = mtiles * t;
-  static int mode = -1;
-  if (mode < 0) {
-    const char* e = getenv("IEK_GEMM_XCD");  // 1: N-tile runs per XCD (tuning)
-    mode = e ? atoi(e) : 2;
-  }
-  g.xcd_remap = (mode == 2 && mtiles % 8 == 0) ? 2 : (tiles % 8 == 0 ? 1 : 0);
+  g.xcd_remap = mtiles % 8 == 0 ? 2 : (tiles % 8 == 0 ? 1 : 0);
   hipLaunchKernelGGL((gemm_q_kernel<DT, BM, BN>), dim3(tiles), dim3(256), 0, st, g);
 }
 
@@ -828,65 +823,30 @@ static void gemm_kq_launch(GemmQArgs g, hipStream_t st) {
 
 // K-quant tile: 64 x 256 (1 x 4 waves; each wave streams its own 64 weight columns, the
 // activation tile is shared) with one activation stage in flight: measured 15% faster than
-// 128 x 128 at the Mistral-7B prefill shapes, and deeper activation prefetch gained nothing.
-// Q4_K GEMMs with at least two tiles per CU (gate/up at a 512-token prompt: 896 tiles) apply d per
-// stage, which frees the superblock partials so two waves share each SIMD: 7% faster there, but
-// slower on grids that then pack two workgroups on some CUs and none on others. Q6_K's fp16
-// weight pairs do not fit two waves per SIMD. IEK_GEMM_KQ_TILE forces a shape (tuning): 0: the
-// default 64 x 256, 1: 128 x 128, 2: 128 x 128 with two activation stages, 3 / 4: 64 x 256 with
-// two / four, 5 / 6: eight waves of 32 x 64 (25% slower), 7 / 8: d per stage at one / two waves
-// per SIMD.
+// 128 x 128 at the Mistral-7B prefill shapes, and deeper activation prefetch (two or four stages)
+// or eight waves of 32 x 64 gained nothing. Q4_K GEMMs with at least two tiles per CU (gate/up at
+// a 512-token prompt: 896 tiles) apply d per stage, which frees the superblock partials so two
+// waves share each SIMD: 7% faster there, but slower on grids that then pack two workgroups on
+// some CUs and none on others. Q6_K's fp16 weight pairs do not fit two waves per SIMD.
 template <class T>
 static void gemm_kq(GemmQArgs g, hipStream_t st) {
-  static int force = -2;
-  if (force == -2) {
-    const char* e = getenv("IEK_GEMM_KQ_TILE");
-    force = e ? atoi(e) : -1;
-  }
-  if (force < 0) {
-    size_t nt = 0;
-    for (int i = 0; i < g.nseg; ++i) nt += (g.n[i] + 255) / 256;
-    const size_t tiles = nt * (size_t)((g.M + 63) / 64);
-    if constexpr (T::MINS) {
-      if (tiles >= 2 * (size_t)num_cus()) {
-        gemm_kq_launch<T, 1, 4, 1, 4, 2, true>(g, st);
-        return;
-      }
+  size_t nt = 0;
+  for (int i = 0; i < g.nseg; ++i) nt += (g.n[i] + 255) / 256;
+  const size_t tiles = nt * (size_t)((g.M + 63) / 64);
+  if constexpr (T::MINS) {
+    if (tiles >= 2 * (size_t)num_cus()) {
+      gemm_kq_launch<T, 1, 4, 1, 4, 2, true>(g, st);
+      return;
     }
-    gemm_kq_launch<T, 1, 4, 1>(g, st);
-    return;
   }
-  switch (force) {
-    case 1: gemm_kq_launch<T, 2, 2, 1>(g, st); break;
-    case 2: gemm_kq_launch<T, 2, 2, 2>(g, st); break;
-    case 3: gemm_kq_launch<T, 1, 4, 2>(g, st); break;
-    case 4: gemm_kq_launch<T, 1, 4, 4>(g, st); break;
-    case 5: gemm_kq_launch<T, 2, 4, 1, 2>(g, st); break;
-    case 6: gemm_kq_launch<T, 4, 2, 1, 2>(g, st); break;
-    case 7: gemm_kq_launch<T, 1, 4, 1, 4, 1, true>(g, st); break;
-    case 8: gemm_kq_launch<T, 1, 4, 1, 4, 2, true>(g, st); break;
-    default: gemm_kq_launch<T, 1, 4, 1>(g, st); break;
-  }
+  gemm_kq_launch<T, 1, 4, 1>(g, st);
 }
 
-// Tile shape: 64 x 64 by default (measured fastest at the Mistral-7B prefill shapes: the larger
-// tiles lose more to occupancy than they gain in operand reuse); IEK_GEMM_TILE overrides.
+// Tile shape 64 x 64 (measured fastest at the Mistral-7B prefill shapes: the larger tiles lose
+// more to occupancy than they gain in operand reuse).
 template <int DT>
 static void gemm_q_dt(GemmQArgs g, hipStream_t st) {
-  auto tiles = [&](int bm, int bn) {
-    size_t n = 0;
-    for (int i = 0; i < g.nseg; ++i) n += (g.n[i] + bn - 1) / bn;
-    return (size_t)((g.M + bm - 1) / bm) * n;
-  };
-  static int force = -2;
-  if (force == -2) {
-    const char* e = getenv("IEK_GEMM_TILE");  // 0: 64x64, 1: 64x128, 2: 128x128 (tuning)
-    force = e ? atoi(e) : -1;
-  }
-  (void)tiles;
-  if (force == 2) gemm_q_launch<DT, 128, 128>(g, st);
-  else if (force == 1) gemm_q_launch<DT, 64, 128>(g, st);
-  else gemm_q_launch<DT, 64, 64>(g, st);
+  gemm_q_launch<DT, 64, 64>(g, st);
 }
 
 void launch_gemm_q(int dt, const GemmQSeg* segs, int nseg, const __half* xh, const __half* xl, const float* xs, int M,

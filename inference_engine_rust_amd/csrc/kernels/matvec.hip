@@ -65,7 +65,7 @@ void launch_repack_q80(const void* src, int K, int N, void* dst, hipStream_t st)
 
 // The body reads the arguments in place from the kernarg segment (a reference to the by-value
 // parameter would make a private copy, and the segment-selecting reads would keep it in scratch).
-template <class Tr, int R, bool DUAL, bool X2, bool MULTI, int NT, int XS = 0>
+template <class Tr, int R, bool DUAL, bool MULTI, int NT, int XS = 0>
 __global__ __launch_bounds__(NT) void mv_stream(MvArgs args) {
   extern __shared__ __align__(16) float lds[];
   (void)args;
@@ -78,15 +78,14 @@ __global__ __launch_bounds__(NT) void mv_stream(MvArgs args) {
   // a scalar load: its wait is on the scalar counter, not behind vector loads
   typedef __attribute__((address_space(4))) const int* ConstInt;
   const int pos = a.epi == EPI_QKV ? *(ConstInt)a.pos : 0;
-  typename Tr::template Buf<DUAL ? 2 * R : R> A;
-  mv_body<Tr, R, DUAL, false, X2, MULTI, NT, XS>(a, lds, pos, A, false);
+  mv_body<Tr, R, DUAL, MULTI, NT, XS>(a, lds, pos);
   if (a.pos_inc && blockIdx.x == 0 && threadIdx.x == 0) *a.pos_inc += 1;
 }
 
 // ---- generic path: any dtype, any K (blocks may straddle rows when K % block != 0) ----------
 __global__ __launch_bounds__(256) void mv_generic(MvArgs a, int dt) {
   extern __shared__ __align__(16) float lds[];
-  const Lds L = lds_layout(a, lds, false);
+  const Lds L = lds_layout(a, lds);
   const float* xs = L.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row = blockIdx.x * 4 + wave;
@@ -125,85 +124,47 @@ int num_cus() {
   return n;
 }
 
-// Persistent grid: exactly the workgroups that are resident at once (the occupancy the register
-// and LDS use allow, optionally capped by IEK_MV_PER_CU), so no second wave of workgroups forms a
-// tail; every wave then strides over the row groups. The kernel variant follows the grid: MULTI
-// when some wave has more than one step, X2 when each staging thread owns two 32-element blocks.
-template <class Tr, bool DUAL, bool X2, int NT, int XS = 0>
+// Workgroups per CU of the streaming matvec (counted in 256-thread workgroups' worth of waves):
+// 3 measured best for the f32-staged traits at the C2 decode shapes (2: 430, 3: 445, 4: 445 tok/s).
+constexpr int kMvPerCu = 3;
+
+// Persistent grid: at most the workgroups that are resident at once, so no second wave of
+// workgroups forms a tail; every wave then strides over the row groups. MULTI when some wave has
+// more than one step.
+template <class Tr, bool DUAL, int NT, int XS = 0>
 static void launch_stream_x(const MvArgs& a, int groups, hipStream_t st) {
   constexpr int NW = NT / 64;
-  static int cap = -1;
-  if (cap < 0) {
-    const char* e = getenv("IEK_MV_PER_CU");
-    cap = e ? std::max(1, atoi(e)) : 2;
-  }
-  constexpr int NR = DUAL ? 4 : 2;
-  const size_t lds = lds_bytes(a, Tr::I8, Tr::WB ? NW * NR * Q6_ROW_SLOT : 0);
+  const size_t lds = lds_bytes(a);
   if (lds > 160 * 1024) fail(ST_OP, "matvec: K too large for the LDS-staged input");
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mv_stream<Tr, 2, DUAL, X2, true, NT, XS>, NT, lds) !=
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mv_stream<Tr, 2, DUAL, true, NT, XS>, NT, lds) !=
           hipSuccess ||
       per_cu <= 0)
     per_cu = 1;
-  // the cap counts 256-thread workgroups' worth of waves per CU
-  per_cu = std::min(per_cu, std::max(1, cap * 256 / NT));
+  per_cu = std::min(per_cu, std::max(1, kMvPerCu * 256 / NT));
   const int blocks = std::max(1, std::min((groups + NW - 1) / NW, num_cus() * per_cu));
   const int waves = NW * blocks;
   const int nchunk = (a.K / QK_K) * Tr::CHUNKS, npass = (nchunk + WAVE - 1) / WAVE;
   const int max_steps = ((groups + waves - 1) / waves) * npass;
   if (max_steps > 1)
-    hipLaunchKernelGGL((mv_stream<Tr, 2, DUAL, X2, true, NT, XS>), dim3(blocks), dim3(NT), lds, st, a);
+    hipLaunchKernelGGL((mv_stream<Tr, 2, DUAL, true, NT, XS>), dim3(blocks), dim3(NT), lds, st, a);
   else
-    hipLaunchKernelGGL((mv_stream<Tr, 2, DUAL, X2, false, NT, XS>), dim3(blocks), dim3(NT), lds, st, a);
+    hipLaunchKernelGGL((mv_stream<Tr, 2, DUAL, false, NT, XS>), dim3(blocks), dim3(NT), lds, st, a);
 }
 
-// Workgroup size: 512 threads (one workgroup per CU, so x is staged once per CU instead of twice)
-// for the int8-staged traits when IEK_MV_NT=512 or, by default, for inputs of more than 4096
-// elements; 256 otherwise. With 256 threads, K > 8192 gives each staging thread two blocks (X2).
+// x staging: split (issued ahead of the weight loads) when x and its companions are
+// float4-aligned, thread t owning float4 slots t + NT s of x for s < XS; 512-thread workgroups
+// (one per CU worth of waves, x staged once per CU) for inputs over 8192 elements.
 template <class Tr, bool DUAL>
 static void launch_stream(const MvArgs& a, int groups, hipStream_t st) {
-  static int nt_env = -1;
-  if (nt_env < 0) {
-    const char* e = getenv("IEK_MV_NT");
-    nt_env = e ? atoi(e) : 0;
+  auto al = [](const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (a.K % 4 == 0 && al(a.x) && al(a.norm_w) && al(a.pre_t) && al(a.pre_w) && al(a.pre_out)) {
+    if (a.K <= 2048) return launch_stream_x<Tr, DUAL, 256, 2>(a, groups, st);
+    if (a.K <= 4096) return launch_stream_x<Tr, DUAL, 256, 4>(a, groups, st);
+    if (a.K <= 8192) return launch_stream_x<Tr, DUAL, 256, 8>(a, groups, st);
+    if (a.K <= 16384) return launch_stream_x<Tr, DUAL, 512, 8>(a, groups, st);
   }
-  if constexpr (std::is_same<Tr, Q8RTr>::value) {
-    // f32 staging issued ahead of the weight loads when x and its companions are float4-aligned
-    auto al = [](const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-    if (a.K % 4 == 0 && al(a.x) && al(a.norm_w) && al(a.pre_t) && al(a.pre_w) && al(a.pre_out)) {
-      if (a.K <= 2048) {
-        launch_stream_x<Tr, DUAL, false, 256, 2>(a, groups, st);
-        return;
-      }
-      if (a.K <= 8192) {
-        launch_stream_x<Tr, DUAL, false, 256, 8>(a, groups, st);
-        return;
-      }
-    }
-  }
-  if constexpr (Tr::I8) {
-    const bool wide = nt_env == 512 || (nt_env == 0 && a.K > 4096);
-    if (wide && a.K / 32 <= 512) {
-      launch_stream_x<Tr, DUAL, false, 512>(a, groups, st);
-      return;
-    }
-    if constexpr (!DUAL) {
-      if (a.K / 32 > 256) {
-        launch_stream_x<Tr, DUAL, true, 256>(a, groups, st);
-        return;
-      }
-    }
-  }
-  launch_stream_x<Tr, DUAL, false, 256>(a, groups, st);
-}
-
-bool mv_int8_staging() {
-  static int v = -1;
-  if (v < 0) {
-    const char* e = getenv("IEK_MV_F32");
-    v = (e && atoi(e) != 0) ? 0 : 1;
-  }
-  return v == 1;
+  launch_stream_x<Tr, DUAL, 256>(a, groups, st);
 }
 
 // Segment starts of a launch's row space; a gate/up pair streams over the gate rows with the up
@@ -221,22 +182,6 @@ void mv_finalize(MvArgs& a) {
   }
 }
 
-// Whether a finalized launch runs on the int8-staged streaming path with the given trait (the
-// conditions launch_mv checks), i.e. whether the persistent decode step can run it as a phase.
-bool mv_stream_i8_ok(int dt, const MvArgs& a) {
-  const bool dual = a.epi == EPI_SWIGLU || a.epi == EPI_GEGLU;
-  if (!(dt == DT_Q4K || dt == DT_Q6K_R) || a.K % QK_K != 0 || a.K > 16384 || !mv_int8_staging()) return false;
-  if ((reinterpret_cast<uintptr_t>(a.x) % 16) != 0) return false;
-  if (a.norm_w && (reinterpret_cast<uintptr_t>(a.norm_w) % 16) != 0) return false;
-  for (int i = 0; i < (dual ? 2 : a.nseg); ++i)
-    if ((reinterpret_cast<uintptr_t>(a.w[i]) % 16) != 0) return false;
-  for (int i = 0; i < a.nseg; ++i)
-    if ((a.seg_start[i + 1] - a.seg_start[i]) % 2 != 0) return false;
-  return true;
-}
-
-size_t mv_lds_bytes_i8(const MvArgs& a) { return lds_bytes(a, true); }
-
 void launch_mv(int dt, MvArgs a, hipStream_t st) {
   mv_finalize(a);
   const bool dual = a.epi == EPI_SWIGLU || a.epi == EPI_GEGLU;
@@ -244,45 +189,20 @@ void launch_mv(int dt, MvArgs a, hipStream_t st) {
   bool fast = (dt == DT_Q4K || dt == DT_Q6K || dt == DT_Q6K_R || dt == DT_Q8_0_R) && a.K % QK_K == 0 &&
               (reinterpret_cast<uintptr_t>(a.x) % 16) == 0;
   for (int i = 0; i < (dual ? 2 : a.nseg); ++i) fast = fast && (reinterpret_cast<uintptr_t>(a.w[i]) % 16) == 0;
-  // K-quants take the int8-staged x (v_dot4) path when x and the norm weight are 16-byte aligned
-  // and every 32-element block fits the two-blocks-per-thread staging; IEK_MV_F32=1 keeps f32.
-  const bool force_f32 = !mv_int8_staging();
-  const bool i8 = fast && !force_f32 && a.K <= 16384 && !a.pre_t &&
-                  (!a.norm_w || (reinterpret_cast<uintptr_t>(a.norm_w) % 16) == 0);
+  // Two rows per wave: more rows per wave spill the prefetch registers.
+  const int R = 2;
+  for (int i = 0; i < a.nseg; ++i) fast = fast && a.n[i] % R == 0;
   if (fast) {
-    // Two rows per wave: more rows per wave spill the prefetch registers.
-    const int R = 2;
-    bool ok = true;
-    for (int i = 0; i < a.nseg; ++i) ok = ok && a.n[i] % R == 0;
-    if (!ok) fast = false;
-    if (fast) {
-      const int groups = total / R;
-#define IEK_L(TR, DD) launch_stream<TR, DD>(a, groups, st)
-      if (dt == DT_Q6K_R) {
-        if (!i8) fail(ST_OP, "matvec: the regrouped Q6_K layout needs the int8-staged path");
-        if (dual) IEK_L(Q6RTr, true);
-        else IEK_L(Q6RTr, false);
-      } else if (dt == DT_Q8_0_R) {
-        if (dual) IEK_L(Q8RTr, true);
-        else IEK_L(Q8RTr, false);
-      } else if (dt == DT_Q4K && i8) {
-        if (dual) IEK_L(Q4I8Tr, true);
-        else IEK_L(Q4I8Tr, false);
-      } else if (dt == DT_Q4K) {
-        if (dual) IEK_L(Q4Tr, true);
-        else IEK_L(Q4Tr, false);
-      } else if (i8) {
-        if (dual) IEK_L(Q6I8Tr, true);
-        else IEK_L(Q6I8Tr, false);
-      } else {
-        if (dual) IEK_L(Q6Tr, true);
-        else IEK_L(Q6Tr, false);
-      }
+    const int groups = total / R;
+#define IEK_L(TR) (dual ? launch_stream<TR, true>(a, groups, st) : launch_stream<TR, false>(a, groups, st))
+    if (dt == DT_Q6K_R) IEK_L(Q6RTr);
+    else if (dt == DT_Q8_0_R) IEK_L(Q8RTr);
+    else if (dt == DT_Q4K) IEK_L(Q4Tr);
+    else IEK_L(Q6Tr);
 #undef IEK_L
-      return;
-    }
+    return;
   }
-  const size_t lds_f = lds_bytes(a, false);
+  const size_t lds_f = lds_bytes(a);
   if (lds_f > 160 * 1024) fail(ST_OP, "matvec: K too large for the LDS-staged input");
   if (a.epi == EPI_QKV) fail(ST_OP, "matvec: fused Q/K/V epilogue needs the aligned K-quant path");
   if (dt == DT_Q6K_R || dt == DT_Q8_0_R)

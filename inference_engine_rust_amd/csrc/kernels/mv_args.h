@@ -60,20 +60,7 @@ __host__ __device__ inline int seg_of(const MvArgs& a, int row) {
 }
 
 void launch_mv(int dt, MvArgs a, hipStream_t st);
-// Host helpers for building launches ahead of time (the persistent decode step).
+// Segment starts of a launch's row space (launch_mv calls it; exposed for launch builders).
 void mv_finalize(MvArgs& a);
-bool mv_stream_i8_ok(int dt, const MvArgs& a);
-size_t mv_lds_bytes_i8(const MvArgs& a);
-// Persistent decode step (kernels/decode_step.hip): a device array of per-layer launch
-// arguments, packed on the host with step_layer_pack.
-size_t step_layer_bytes();
-int step_bar_words();
-void step_layer_pack(void* dst, const MvArgs& qkv, const MvArgs& o, const MvArgs& dual, const MvArgs& down,
-                     const __half* kc, const __half* vc, float* q, float* att, int window);
-void launch_decode_step(const void* layers, int n_layers, int n_heads, int n_kv, int head_dim, int ctx, float scale,
-                        float* part, int* counters, const int* pos, int* pos_inc, unsigned* bar, int* err,
-                        size_t lds_bytes, unsigned long long* trace, hipStream_t st);
-// Whether K-quant matvecs stage x as int8 planes (default; IEK_MV_F32=1 selects the f32 path).
-bool mv_int8_staging();
 
 }  // namespace iek

@@ -80,24 +80,21 @@ IEK_DEV float div_rn(float x, float y) {
 // y = (x*w)/rms with the reference's two roundings. The epilogue's inputs (residual vector, this
 // position's RoPE cos/sin) are staged here too, so the main loop never waits on a global load.
 struct Lds {
-  float* x;      // K f32 (float staging)
+  float* x;      // K f32
   float* res;    // N (EPI_RESID)
   float* rope;   // 2*npairs (EPI_QKV)
-  // int8 staging: x ~= s_b * (256 * xh + xl) per 32-element block b
-  int8_t* xh;    // K
-  int8_t* xl;    // K
-  float* sb;     // K/32 block scales
-  int* sx;       // K/32 block sums of (256 * xh + xl)
-  uint8_t* wb;   // per-wave staging of raw weight bytes (coalesced-load traits only)
 };
 
-// Block-wide sum for the 256-thread matvec workgroups.
+// Block-wide sum for the matvec workgroups (NT threads; red holds NT / 64 floats).
+template <int NT = 256>
 IEK_DEV float block_sum_mv(float v, float* red) {
   v = wave_sum(v);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
-  return (red[0] + red[1]) + (red[2] + red[3]);
+  float t = (red[0] + red[1]) + (red[2] + red[3]);
+  if constexpr (NT == 512) t += (red[4] + red[5]) + (red[6] + red[7]);
+  return t;
 }
 
 // Staging with the residual update in front (a.pre_t set; f32 staging): y = x + rmsnorm(pre_t,
@@ -201,230 +198,34 @@ IEK_DEV void stage(const MvArgs& a, const Lds& L, int pos) {
   __builtin_amdgcn_s_waitcnt(0);
 }
 
-// LDS bytes: x staging (f32: 4K; int8: 2K planes + 8 bytes per 32-block), then the residual
-// vector (EPI_RESID) and this position's RoPE (cos, sin) pairs (EPI_QKV).
-__host__ __device__ inline size_t lds_bytes(const MvArgs& a, bool i8, size_t wbuf = 0) {
-  const size_t xb = i8 ? 2 * (size_t)a.K + 8 * (size_t)(a.K / 32) : 4 * (size_t)a.K;
-  return wbuf + xb + (a.epi == EPI_RESID ? 4 * (size_t)a.n[0] : 0) + (a.epi == EPI_QKV ? 8 * (size_t)a.npairs : 0);
+// LDS bytes: x staging (4K), then the residual vector (EPI_RESID) and this position's RoPE
+// (cos, sin) pairs (EPI_QKV).
+__host__ __device__ inline size_t lds_bytes(const MvArgs& a) {
+  return 4 * (size_t)a.K + (a.epi == EPI_RESID ? 4 * (size_t)a.n[0] : 0) + (a.epi == EPI_QKV ? 8 * (size_t)a.npairs : 0);
 }
 
-// [per-wave weight staging (wbuf bytes)][x staging][residual][RoPE]
-IEK_DEV Lds lds_layout(const MvArgs& a, float* base, bool i8, size_t wbuf = 0) {
+// [x staging][residual][RoPE]
+IEK_DEV Lds lds_layout(const MvArgs& a, float* base) {
   Lds L;
-  L.wb = reinterpret_cast<uint8_t*>(base);
-  base = reinterpret_cast<float*>(reinterpret_cast<char*>(base) + wbuf);
-  char* p = reinterpret_cast<char*>(base);
-  L.x = nullptr;
-  L.xh = L.xl = nullptr;
-  L.sb = nullptr;
-  L.sx = nullptr;
-  if (i8) {
-    L.xh = reinterpret_cast<int8_t*>(p);
-    L.xl = L.xh + a.K;
-    L.sb = reinterpret_cast<float*>(p + 2 * (size_t)a.K);
-    L.sx = reinterpret_cast<int*>(L.sb + a.K / 32);
-    p += 2 * (size_t)a.K + 8 * (size_t)(a.K / 32);
-  } else {
-    L.x = base;
-    p += 4 * (size_t)a.K;
-  }
-  L.res = reinterpret_cast<float*>(p);
+  L.x = base;
+  L.res = base + a.K;
   L.rope = L.res + (a.epi == EPI_RESID ? a.n[0] : 0);
   return L;
 }
-
-// ---- int8 staging of x ------------------------------------------------------------------------
-// Each 32-element block b of y = x*w (or x) is stored as a 16-bit integer vector X with
-// y ~= s_b * X, s_b = amax_b / (32639 * rms) and |X| <= 32639, split as X = 256*xh + xl with
-// xh in [-127, 127] and xl in [-128, 127], so two v_dot4_i32_i8 per 4 weights give the exact
-// integer sum of q*X. The representation error is at most s_b/2 per element (~1.5e-5 of the
-// block's largest |y|); the RMS factor never touches the elements (it only enters s_b), so no
-// per-element division is needed. Threads own whole blocks (K <= 16384).
-constexpr float XQ_MAX = 32639.0f;
-
-IEK_DEV void quant_block(const float (&y)[32], float am, uint32_t (&h)[8], uint32_t (&l)[8], int& sum) {
-  const float inv = am > 0.f ? XQ_MAX / am : 0.f;
-  sum = 0;
-#pragma unroll
-  for (int g = 0; g < 8; ++g) {
-    uint32_t hw = 0, lw = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      int X = __float2int_rn(y[4 * g + e] * inv);
-      X = max(-32639, min(32639, X));
-      const int hi = (X + 128) >> 8, lo = X - (hi << 8);
-      sum += X;
-      hw |= (uint32_t)(hi & 0xFF) << (8 * e);
-      lw |= (uint32_t)(lo & 0xFF) << (8 * e);
-    }
-    h[g] = hw;
-    l[g] = lw;
-  }
-}
-
-// The staging is split so its global loads can be issued before the first weight loads: the
-// memory counter retires in order, so x (an L2 hit) would otherwise wait behind the weight stream.
-// stage_i8_issue loads this thread's 32-element block(s) of x (and w), its share of the residual
-// vector, its RoPE pair and the wave's epilogue residuals into registers; stage_i8_finish consumes
-// them. Every load whose issue depends on a runtime condition goes out before the unconditional
-// x block, and the weight loads follow that block: the compiler counts the loads in flight only
-// along paths with the same loads, so a wait for x then leaves the weight loads in flight instead
-// of draining them.
-struct XPre {
-  float4 xv[8], wv[8];
-  float4 xv2[8], wv2[8];  // second block (K > 8192, X2 kernels)
-  float4 res[4];
-  float2 rope;
-  float ev;  // residual of this lane's row (lane < R) when the epilogue reads it from a register
-};
 
 IEK_DEV bool res_vec(const MvArgs& a) {
   return a.epi == EPI_RESID && (a.n[0] & 3) == 0 && a.n[0] <= 4096 && (reinterpret_cast<uintptr_t>(a.resid) & 15) == 0;
 }
 
-// ev_idx >= 0: this lane's epilogue residual index (EPI_RESID with at most one row group per
-// wave); otherwise the residual vector is staged in LDS. With X2 the thread's second block
-// (tid + 256, K > 8192) is loaded here too.
-template <bool COH = false, bool X2 = false, int NT = 256>
-IEK_DEV void stage_i8_issue(const MvArgs& a, XPre& p, int pos, int ev_idx) {
-  const int tid = threadIdx.x, nb = a.K >> 5, bc = min(tid, nb - 1), bc2 = min(tid + NT, nb - 1);
-  if (a.norm_w) {
-    const float4* w4 = reinterpret_cast<const float4*>(a.norm_w) + (size_t)bc * 8;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) p.wv[t] = w4[t];
-    if constexpr (X2) {
-      const float4* w42 = reinterpret_cast<const float4*>(a.norm_w) + (size_t)bc2 * 8;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) p.wv2[t] = w42[t];
-    }
-  }  // without a norm weight, quant_store never reads wv
-  if (ev_idx >= 0) {
-    p.ev = ld_f<COH>((a.epi == EPI_GELU_MUL ? a.mulv : a.resid) + ev_idx);
-  } else if (res_vec(a)) {
-    const float4* r4 = reinterpret_cast<const float4*>(a.resid);
-    const int n4 = a.n[0] >> 2;
-#pragma unroll
-    for (int u = 0; u < 1024 / NT; ++u) p.res[u] = ld_f4<COH>(r4 + min(tid + NT * u, n4 - 1));
-  }
-  if (a.epi == EPI_QKV)
-    p.rope = reinterpret_cast<const float2*>(a.rope_cs)[(size_t)pos * a.npairs + min(tid, a.npairs - 1)];
-  if constexpr (X2) {
-    const float4* x42 = reinterpret_cast<const float4*>(a.x) + (size_t)bc2 * 8;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) p.xv2[t] = ld_f4<COH>(x42 + t);
-  }
-  const float4* x4 = reinterpret_cast<const float4*>(a.x) + (size_t)bc * 8;
-#pragma unroll
-  for (int t = 0; t < 8; ++t) p.xv[t] = ld_f4<COH>(x4 + t);
-}
-
-IEK_DEV void quant_store(const MvArgs& a, const Lds& L, int b, const float4 (&xv)[8], const float4 (&wv)[8], float& ss,
-                         float& amax) {
-  float y[32];
-  float am = 0.f, sq = 0.f;
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const float xs[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
-    const float ws[4] = {wv[t].x, wv[t].y, wv[t].z, wv[t].w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      sq += xs[e] * xs[e];
-      y[4 * t + e] = a.norm_w ? mul_rn(xs[e], ws[e]) : xs[e];
-      am = fmaxf(am, fabsf(y[4 * t + e]));
-    }
-  }
-  uint32_t h[8], l[8];
-  int sum;
-  quant_block(y, am, h, l, sum);
-  amax = am;
-  if (b < (a.K >> 5)) {
-    ss += sq;
-    uint4* ph = reinterpret_cast<uint4*>(L.xh + 32 * b);
-    uint4* pl = reinterpret_cast<uint4*>(L.xl + 32 * b);
-    ph[0] = make_uint4(h[0], h[1], h[2], h[3]);
-    ph[1] = make_uint4(h[4], h[5], h[6], h[7]);
-    pl[0] = make_uint4(l[0], l[1], l[2], l[3]);
-    pl[1] = make_uint4(l[4], l[5], l[6], l[7]);
-    L.sx[b] = sum;
-  }
-}
-
-template <bool COH = false, bool X2 = false, int NT = 256>
-IEK_DEV void stage_i8_finish(const MvArgs& a, const Lds& L, int pos, XPre& p, bool res_lds) {
-  const int K = a.K, tid = threadIdx.x, nb = K >> 5;
-  // The empty asm statements make x (and w) appear defined here, so no arithmetic on them is
-  // hoisted above the weight loads issued between stage_i8_issue and this point.
-  auto pin = [](float4& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); };
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    pin(p.xv[t]);
-    if (a.norm_w) pin(p.wv[t]);
-    if constexpr (X2) {
-      pin(p.xv2[t]);
-      if (a.norm_w) pin(p.wv2[t]);
-    }
-  }
-  float ss = 0.f;
-  float amax[2] = {0.f, 0.f};
-  quant_store(a, L, tid, p.xv, p.wv, ss, amax[0]);
-  if constexpr (X2) {
-    quant_store(a, L, tid + NT, p.xv2, p.wv2, ss, amax[1]);
-  } else if (nb > NT) {
-    // second block of this thread (K > 8192), loaded here
-    const int b = tid + NT, bc = min(b, nb - 1);
-    float4 xv[8], wv[8];
-    const float4* x4 = reinterpret_cast<const float4*>(a.x) + (size_t)bc * 8;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) xv[t] = ld_f4<COH>(x4 + t);
-    if (a.norm_w) {
-      const float4* w4 = reinterpret_cast<const float4*>(a.norm_w) + (size_t)bc * 8;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) wv[t] = w4[t];
-    } else {
-#pragma unroll
-      for (int t = 0; t < 8; ++t) wv[t] = make_float4(1.f, 1.f, 1.f, 1.f);
-    }
-    quant_store(a, L, b, xv, wv, ss, amax[1]);
-  }
-  if (a.epi == EPI_RESID && res_lds) {
-    const int N = a.n[0];
-    if (res_vec(a)) {
-      float4* d4 = reinterpret_cast<float4*>(L.res);
-#pragma unroll
-      for (int u = 0; u < 1024 / NT; ++u)
-        if (tid + NT * u < (N >> 2)) d4[tid + NT * u] = p.res[u];
-    } else {
-      for (int i = tid; i < N; i += NT) L.res[i] = ld_f<COH>(a.resid + i);
-    }
-  }
-  if (a.epi == EPI_QKV && tid < a.npairs) reinterpret_cast<float2*>(L.rope)[tid] = p.rope;
-  if (a.epi == EPI_QKV)
-    for (int i = NT + tid; i < a.npairs; i += NT)
-      reinterpret_cast<float2*>(L.rope)[i] = reinterpret_cast<const float2*>(a.rope_cs)[(size_t)pos * a.npairs + i];
-  float rms = 1.f;
-  if (a.norm_w) {
-    __shared__ float red[NT / 64];
-    ss = wave_sum(ss);
-    if ((tid & 63) == 0) red[tid >> 6] = ss;
-    __syncthreads();
-    float tot = (red[0] + red[1]) + (red[2] + red[3]);
-    if constexpr (NT == 512) tot += (red[4] + red[5]) + (red[6] + red[7]);
-    rms = rms_of(tot, K, a.eps);
-  }
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int b = tid + NT * j;
-    if (b < nb) L.sb[b] = amax[j] / (XQ_MAX * rms);
-  }
-  __syncthreads();
-}
-
-
-// ---- f32 staging split like the int8 one ------------------------------------------------------
-// Thread t owns the float4 slots t + 256 s (s < S, K <= 1024 S; the host picks S) of x, the norm
-// weight and the residual-update inputs (pre_t, pre_w). stage32_issue loads them (the conditional
-// ones first, x last, ahead of the weight loads); stage32_finish computes the staging with the
-// roundings of stage / stage_pre.
+// ---- x staging split in two ------------------------------------------------------------------
+// Thread t of an NT-thread workgroup owns the float4 slots t + NT s (s < S, K <= 4 NT S; the host
+// picks S) of x, the norm weight and the residual-update inputs (pre_t, pre_w). stage32_issue
+// loads them (the conditional ones first, x last, ahead of the weight loads); stage32_finish
+// computes the staging with the roundings of stage / stage_pre. The memory counter retires in
+// order, so x (an L2 hit) issued after the first weight loads would wait behind the weight stream;
+// every load whose issue depends on a runtime condition goes out before the unconditional x slots,
+// and the weight loads follow: the compiler counts the loads in flight only along paths with the
+// same loads, so a wait for x then leaves the weight loads in flight instead of draining them.
 template <int S>
 struct XPre32 {
   float4 x[S], w[S], t[S], tw[S];
@@ -433,7 +234,7 @@ struct XPre32 {
   float ev;
 };
 
-template <int S>
+template <int S, int NT = 256>
 IEK_DEV void stage32_issue(const MvArgs& a, XPre32<S>& p, int pos, int ev_idx) {
   const int tid = threadIdx.x, K4 = a.K >> 2;
   if (a.pre_t) {
@@ -441,7 +242,7 @@ IEK_DEV void stage32_issue(const MvArgs& a, XPre32<S>& p, int pos, int ev_idx) {
     const float4* tw4 = reinterpret_cast<const float4*>(a.pre_w);
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      const int i = min(tid + 256 * s, K4 - 1);
+      const int i = min(tid + NT * s, K4 - 1);
       p.t[s] = t4[i];
       p.tw[s] = tw4[i];
     }
@@ -449,7 +250,7 @@ IEK_DEV void stage32_issue(const MvArgs& a, XPre32<S>& p, int pos, int ev_idx) {
   if (a.norm_w) {
     const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
 #pragma unroll
-    for (int s = 0; s < S; ++s) p.w[s] = w4[min(tid + 256 * s, K4 - 1)];
+    for (int s = 0; s < S; ++s) p.w[s] = w4[min(tid + NT * s, K4 - 1)];
   }
   if (ev_idx >= 0) {
     p.ev = (a.epi == EPI_GELU_MUL ? a.mulv : a.resid)[ev_idx];
@@ -457,21 +258,21 @@ IEK_DEV void stage32_issue(const MvArgs& a, XPre32<S>& p, int pos, int ev_idx) {
     const float4* r4 = reinterpret_cast<const float4*>(a.resid);
     const int n4 = a.n[0] >> 2;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) p.res[u] = r4[min(tid + 256 * u, n4 - 1)];
+    for (int u = 0; u < 1024 / NT; ++u) p.res[u] = r4[min(tid + NT * u, n4 - 1)];
   }
   if (a.epi == EPI_QKV)
     p.rope = reinterpret_cast<const float2*>(a.rope_cs)[(size_t)pos * a.npairs + min(tid, a.npairs - 1)];
   const float4* x4 = reinterpret_cast<const float4*>(a.x);
 #pragma unroll
-  for (int s = 0; s < S; ++s) p.x[s] = x4[min(tid + 256 * s, K4 - 1)];
+  for (int s = 0; s < S; ++s) p.x[s] = x4[min(tid + NT * s, K4 - 1)];
 }
 
-template <int S>
+template <int S, int NT = 256>
 IEK_DEV void stage32_finish(const MvArgs& a, const Lds& L, int pos, XPre32<S>& p, bool res_lds) {
-  __shared__ float red[4];
+  __shared__ float red[NT / 64];
   const int tid = threadIdx.x, K = a.K, K4 = K >> 2;
-  // the empty asm statements keep the arithmetic below the weight loads (as in stage_i8_finish;
-  // the memory clobber also keeps them from being hoisted among the loads)
+  // the empty asm statements keep the arithmetic below the weight loads (the memory clobber also keeps them
+  // from being hoisted among the loads)
   auto pin = [](float4& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)::"memory"); };
 #pragma unroll
   for (int s = 0; s < S; ++s) pin(p.x[s]);
@@ -484,17 +285,17 @@ IEK_DEV void stage32_finish(const MvArgs& a, const Lds& L, int pos, XPre32<S>& p
     float st = 0.f;
 #pragma unroll
     for (int s = 0; s < S; ++s)
-      if (tid + 256 * s < K4) {
+      if (tid + NT * s < K4) {
         const float4 t = p.t[s];
         st += t.x * t.x;
         st += t.y * t.y;
         st += t.z * t.z;
         st += t.w * t.w;
       }
-    const float rms_t = rms_of(block_sum_mv(st, red), K, a.eps);
+    const float rms_t = rms_of(block_sum_mv<NT>(st, red), K, a.eps);
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      const int i = tid + 256 * s;
+      const int i = tid + NT * s;
       if (i < K4) {
         const float4 x = p.x[s], t = p.t[s], w = p.tw[s];
         float4 v = make_float4(x.x + div_rn(mul_rn(t.x, w.x), rms_t), x.y + div_rn(mul_rn(t.y, w.y), rms_t),
@@ -510,7 +311,7 @@ IEK_DEV void stage32_finish(const MvArgs& a, const Lds& L, int pos, XPre32<S>& p
   float ss = 0.f;
 #pragma unroll
   for (int s = 0; s < S; ++s) {
-    const int i = tid + 256 * s;
+    const int i = tid + NT * s;
     if (i < K4) {
       const float4 v = y[s];
       ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
@@ -527,22 +328,22 @@ IEK_DEV void stage32_finish(const MvArgs& a, const Lds& L, int pos, XPre32<S>& p
     if (res_vec(a)) {
       float4* d4 = reinterpret_cast<float4*>(L.res);
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (tid + 256 * u < (N >> 2)) d4[tid + 256 * u] = p.res[u];
+      for (int u = 0; u < 1024 / NT; ++u)
+        if (tid + NT * u < (N >> 2)) d4[tid + NT * u] = p.res[u];
     } else {
-      for (int i = tid; i < N; i += 256) L.res[i] = a.resid[i];
+      for (int i = tid; i < N; i += NT) L.res[i] = a.resid[i];
     }
   }
   if (a.epi == EPI_QKV) {
     if (tid < a.npairs) reinterpret_cast<float2*>(L.rope)[tid] = p.rope;
-    for (int i = 256 + tid; i < a.npairs; i += 256)
+    for (int i = NT + tid; i < a.npairs; i += NT)
       reinterpret_cast<float2*>(L.rope)[i] = reinterpret_cast<const float2*>(a.rope_cs)[(size_t)pos * a.npairs + i];
   }
   if (a.norm_w) {
-    const float rms = rms_of(block_sum_mv(ss, red), K, a.eps);
+    const float rms = rms_of(block_sum_mv<NT>(ss, red), K, a.eps);
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      const int i = tid + 256 * s;
+      const int i = tid + NT * s;
       if (i < K4) {
         const float4 v = L4[i];
         L4[i] = make_float4(div_rn(v.x, rms), div_rn(v.y, rms), div_rn(v.z, rms), div_rn(v.w, rms));
@@ -561,7 +362,7 @@ IEK_DEV int seg_base(const MvArgs& a, int s) { return s == 0 ? a.seg_start[0] : 
 // ---- epilogue -----------------------------------------------------------------------------------
 // Reads only registers and LDS (pos was loaded at kernel start); with ev_reg, lane r < R holds the
 // residual (EPI_RESID) or multiplier (EPI_GELU_MUL) of row lr0 + r in ev.
-template <int R, bool COH = false>
+template <int R>
 IEK_DEV void epilogue(const MvArgs& a, const Lds& L, int s, int lr0, float (&acc)[R], const float* acc_up, int lane,
                       int pos, unsigned long long& run_key, float ev = 0.f, bool ev_reg = false) {
   if (a.epi == EPI_SWIGLU || a.epi == EPI_GEGLU) {
@@ -573,7 +374,7 @@ IEK_DEV void epilogue(const MvArgs& a, const Lds& L, int s, int lr0, float (&acc
           g = acc[r];
           u = acc_up[r];
         }
-      st_f<COH>(a.out[0] + lr0 + lane, a.epi == EPI_GEGLU ? gelu_tanh_dev(g) * u : silu_mul(g, u));
+      st_f<false>(a.out[0] + lr0 + lane, a.epi == EPI_GEGLU ? gelu_tanh_dev(g) * u : silu_mul(g, u));
     }
     return;
   }
@@ -591,10 +392,10 @@ IEK_DEV void epilogue(const MvArgs& a, const Lds& L, int s, int lr0, float (&acc
       const int d = n % hd;
       if (s < 2 && d < 2 * a.npairs) v = rope_rotate(v, partner, L.rope[d & ~1], L.rope[(d & ~1) + 1], (d & 1) == 0);
       if (s == 0) {
-        st_f<COH>(a.out[0] + n, v);
+        st_f<false>(a.out[0] + n, v);
       } else {
         const size_t dst = ((size_t)(n / hd) * a.ctx + pos) * hd + d;
-        st_h<COH>((s == 1 ? a.kc : a.vc) + dst, __float2half_rn(v));
+        st_h<false>((s == 1 ? a.kc : a.vc) + dst, __float2half_rn(v));
       }
     }
     return;
@@ -623,7 +424,7 @@ IEK_DEV void epilogue(const MvArgs& a, const Lds& L, int s, int lr0, float (&acc
     const int n = lr0 + lane;
     if (a.epi == EPI_RESID) v = (ev_reg ? ev : L.res[n]) + v;
     if (a.epi == EPI_GELU_MUL) v = gelu_tanh_dev(v) * (ev_reg ? ev : a.mulv[n]);
-    st_f<COH>(seg_out(a, s) + n, v);
+    st_f<false>(seg_out(a, s) + n, v);
   }
 }
 
@@ -779,8 +580,6 @@ IEK_DEV void argmax_flush(const MvArgs& a, unsigned long long run_key) {
 // issuing the next step's weight loads before computing the current one. Loads are unconditional
 // with clamped addresses so the compiler can count them statically and keep them all in flight.
 struct Q4Tr {
-  static constexpr bool I8 = false;
-  static constexpr bool WB = false;
   static constexpr int CHUNKS = 4;  // 64-value chunks per superblock
   static constexpr int BYTES = Q4K_BYTES;
   IEK_DEV static size_t row_bytes(int nsb) { return (size_t)nsb * BYTES; }
@@ -817,8 +616,6 @@ struct Q4Tr {
 };
 
 struct Q6Tr {
-  static constexpr bool I8 = false;
-  static constexpr bool WB = false;
   static constexpr int CHUNKS = 8;  // 32-value chunks per superblock
   static constexpr int BYTES = Q6K_BYTES;
   IEK_DEV static size_t row_bytes(int nsb) { return (size_t)nsb * BYTES; }
@@ -849,121 +646,6 @@ struct Q6Tr {
   }
 };
 
-// Q4_K against the int8-staged x: per 64-value chunk, the low nibbles (sub-block 2g) and high
-// nibbles (sub-block 2g+1) each give the exact integer S = sum q*X through v_dot4_i32_i8 on the
-// (xh, xl) planes; the row sum is then s_b * (d*sc*S - dmin*m*sum X) per sub-block, the same
-// algebra as the reference's sum over (d*sc*q - dmin*m) * x with x replaced by s_b*X.
-struct Q4I8Tr {
-  static constexpr bool I8 = true;
-  static constexpr bool WB = false;
-  static constexpr int CHUNKS = 4;
-  static constexpr int BYTES = Q4K_BYTES;
-  IEK_DEV static size_t row_bytes(int nsb) { return (size_t)nsb * BYTES; }
-  template <int NR>
-  using Buf = Q4Tr::Buf<NR>;
-  template <int NR>
-  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c, int nsb) {
-    Q4Tr::load<NR>(b, rows, c, nsb);
-  }
-  template <int NR>
-  IEK_DEV static void compute(const Buf<NR>& b, int c, const Lds& L, float (&acc)[NR]) {
-    const int e0 = (c >> 2) * QK_K + (c & 3) * 64, b0 = e0 >> 5;
-    const uint4* ph = reinterpret_cast<const uint4*>(L.xh + e0);
-    const uint4* pl = reinterpret_cast<const uint4*>(L.xl + e0);
-    const uint4 H0 = ph[0], H1 = ph[1], H2 = ph[2], H3 = ph[3];
-    const uint4 L0 = pl[0], L1 = pl[1], L2 = pl[2], L3 = pl[3];
-    const uint32_t xh[16] = {H0.x, H0.y, H0.z, H0.w, H1.x, H1.y, H1.z, H1.w,
-                             H2.x, H2.y, H2.z, H2.w, H3.x, H3.y, H3.z, H3.w};
-    const uint32_t xl[16] = {L0.x, L0.y, L0.z, L0.w, L1.x, L1.y, L1.z, L1.w,
-                             L2.x, L2.y, L2.z, L2.w, L3.x, L3.y, L3.z, L3.w};
-    const float2 sb = *reinterpret_cast<const float2*>(L.sb + b0);
-    const int2 sx = *reinterpret_cast<const int2*>(L.sx + b0);
-    const int g = c & 3;
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      const uint4 hdr = b.hdr[r];
-      const uint32_t qw[8] = {b.qa[r].x, b.qa[r].y, b.qa[r].z, b.qa[r].w, b.qb[r].x, b.qb[r].y, b.qb[r].z, b.qb[r].w};
-      int h0 = 0, l0 = 0, h1 = 0, l1 = 0;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const int lo = (int)(qw[t] & 0x0F0F0F0Fu), hi = (int)((qw[t] >> 4) & 0x0F0F0F0Fu);
-        h0 = __builtin_amdgcn_sdot4(lo, (int)xh[t], h0, false);
-        l0 = __builtin_amdgcn_sdot4(lo, (int)xl[t], l0, false);
-        h1 = __builtin_amdgcn_sdot4(hi, (int)xh[8 + t], h1, false);
-        l1 = __builtin_amdgcn_sdot4(hi, (int)xl[8 + t], l1, false);
-      }
-      const float d = half_bits_to_float(hdr.x), dmin = half_bits_to_float(hdr.x >> 16);
-      float sc0, m0, sc1, m1;
-      scale_min_k4_sel(2 * g, hdr.y, hdr.z, hdr.w, &sc0, &m0);
-      scale_min_k4_sel(2 * g + 1, hdr.y, hdr.z, hdr.w, &sc1, &m1);
-      const float S0 = (float)(h0 * 256 + l0), S1 = (float)(h1 * 256 + l1);
-      acc[r] += sb.x * ((d * sc0) * S0 - (dmin * m0) * (float)sx.x) + sb.y * ((d * sc1) * S1 - (dmin * m1) * (float)sx.y);
-    }
-  }
-};
-
-constexpr int Q6_ROW_SLOT = 2048;  // LDS bytes per staged row for traits that stage raw weight bytes
-
-// Q6_K against the int8-staged x. The 6-bit values are assembled per byte as in q6k_dot, made
-// signed (q - 32) bytewise with (q + 0x60) ^ 0x80, and two v_dot4 per 4 weights give
-// S = sum (q - 32) * X exactly; each 8-weight run contributes s_b * (d * sc) * S.
-struct Q6I8Tr {
-  static constexpr bool I8 = true;
-  static constexpr bool WB = false;
-  static constexpr int CHUNKS = 8;
-  static constexpr int BYTES = Q6K_BYTES;
-  IEK_DEV static size_t row_bytes(int nsb) { return (size_t)nsb * BYTES; }
-  template <int NR>
-  using Buf = Q6Tr::Buf<NR>;
-  template <int NR>
-  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c, int nsb) {
-    Q6Tr::load<NR>(b, rows, c, nsb);
-  }
-  template <int NR>
-  IEK_DEV static void compute(const Buf<NR>& b, int c, const Lds& L, float (&acc)[NR]) {
-    const int e0 = (c >> 3) * QK_K + 128 * ((c >> 2) & 1) + 8 * (c & 3);
-    uint32_t xh[8], xl[8];
-    float sq[4];
-#pragma unroll
-    for (int qd = 0; qd < 4; ++qd) {
-      const uint2 vh = *reinterpret_cast<const uint2*>(L.xh + e0 + 32 * qd);
-      const uint2 vl = *reinterpret_cast<const uint2*>(L.xl + e0 + 32 * qd);
-      xh[2 * qd] = vh.x, xh[2 * qd + 1] = vh.y, xl[2 * qd] = vl.x, xl[2 * qd + 1] = vl.y;
-      sq[qd] = L.sb[(e0 + 32 * qd) >> 5];
-    }
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      const Q6Raw& q = b.q[r];
-      const uint32_t sh_ql = q.sh_ql, sh_s = q.sh_s;
-      const uint32_t A[2] = {__builtin_amdgcn_alignbyte(q.a[1], q.a[0], sh_ql), __builtin_amdgcn_alignbyte(q.a[2], q.a[1], sh_ql)};
-      const uint32_t B[2] = {__builtin_amdgcn_alignbyte(q.b[1], q.b[0], sh_ql), __builtin_amdgcn_alignbyte(q.b[2], q.b[1], sh_ql)};
-      const uint32_t H[2] = {__builtin_amdgcn_alignbyte(q.h[1], q.h[0], sh_ql), __builtin_amdgcn_alignbyte(q.h[2], q.h[1], sh_ql)};
-      const uint32_t S0 = __builtin_amdgcn_alignbyte(q.s[1], q.s[0], sh_s), S1 = __builtin_amdgcn_alignbyte(q.s[2], q.s[1], sh_s);
-      const float sc[4] = {(float)(int8_t)(S0 & 0xFF), (float)(int8_t)((S0 >> 16) & 0xFF), (float)(int8_t)(S1 & 0xFF),
-                           (float)(int8_t)((S1 >> 16) & 0xFF)};
-      const float d = half_bits_to_float(q.d);
-      int hs[4] = {0, 0, 0, 0}, ls[4] = {0, 0, 0, 0};
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const uint32_t qq[4] = {(A[t] & 0x0F0F0F0Fu) | ((H[t] << 4) & 0x30303030u),
-                                (B[t] & 0x0F0F0F0Fu) | ((H[t] << 2) & 0x30303030u),
-                                ((A[t] >> 4) & 0x0F0F0F0Fu) | (H[t] & 0x30303030u),
-                                ((B[t] >> 4) & 0x0F0F0F0Fu) | ((H[t] >> 2) & 0x30303030u)};
-#pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-          const int sgn = (int)((qq[qd] + 0x60606060u) ^ 0x80808080u);  // bytes q - 32 as int8
-          hs[qd] = __builtin_amdgcn_sdot4(sgn, (int)xh[2 * qd + t], hs[qd], false);
-          ls[qd] = __builtin_amdgcn_sdot4(sgn, (int)xl[2 * qd + t], ls[qd], false);
-        }
-      }
-      float sum = 0.f;
-#pragma unroll
-      for (int qd = 0; qd < 4; ++qd) sum += sq[qd] * ((d * sc[qd]) * (float)(hs[qd] * 256 + ls[qd]));
-      acc[r] += sum;
-    }
-  }
-};
-
 // Q6_K in the regrouped per-row layout (DT_Q6K_R, built once at model load by
 // launch_repack_q6k): for superblock j of a row, lane chunk k = 2h + j16 holds the 16 ql bytes of
 // quarters 0/2, the 16 ql bytes of quarters 1/3 and the 16 qh bytes for weights l = 16*j16 ..
@@ -971,12 +653,7 @@ struct Q6I8Tr {
 // dword and the superblock's d. A lane's 64 weights are thus three coalesced 16-byte loads plus
 // two small ones, instead of thirteen dword loads per 32 weights from the 210-byte blocks. The
 // values are the same bytes, so the dequantised weights are unchanged.
-struct Q6RTr {
-  static constexpr bool I8 = true;
-  static constexpr bool WB = false;
-  static constexpr int CHUNKS = 4;
-  static constexpr int BYTES = 208;
-  IEK_DEV static size_t row_bytes(int nsb) { return q6r_row_bytes(nsb); }
+struct Q6RLayout {
   template <int NR>
   struct Buf {
     uint4 qa[NR], qb[NR], qh[NR];
@@ -995,24 +672,47 @@ struct Q6RTr {
       b.d[r] = *reinterpret_cast<const uint16_t*>(rows[r] + (size_t)nsb * 208 + 2 * j);
     }
   }
+};
+
+// Q6_K in the regrouped per-row layout (DT_Q6K_R) against f32 x. Per lane chunk (64 weights of
+// one half: l = 16*j16 .. 16*j16+15 in each of the four quarters) the 6-bit values q + 32 are
+// assembled per byte, split into register halves and fed to v_fma_mix_f32 as exact f16 subnormals
+// (value * 2^-24), so each quarter's sum is S = sum x * (q + 32) in f32; the quarter then adds
+// (d * sc) * (2^24 * S - 32 * sum x), the reference's sum of x * (d * sc * q) reassociated.
+struct Q6RTr {
+  static constexpr int CHUNKS = 4;
+  static constexpr int BYTES = 208;
+  IEK_DEV static size_t row_bytes(int nsb) { return q6r_row_bytes(nsb); }
+  template <int NR>
+  using Buf = Q6RLayout::Buf<NR>;
+  template <int NR>
+  IEK_DEV static void load(Buf<NR>& b, const uint8_t* const (&rows)[NR], int c, int nsb) {
+    Q6RLayout::load<NR>(b, rows, c, nsb);
+  }
   template <int NR>
   IEK_DEV static void compute(const Buf<NR>& b, int c, const Lds& L, float (&acc)[NR]) {
     const int j = c >> 2, k = c & 3, h = k >> 1, j16 = k & 1;
     const int e0 = j * QK_K + 128 * h + 16 * j16;
-    uint4 XH[4], XL[4];
-    float sq[4];
+    // x of quarter qd, weights l = 16*j16 + 4t .. +3: X[qd][t]
+    float4 X[4][4];
+    float xs[4];
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd) {
-      XH[qd] = *reinterpret_cast<const uint4*>(L.xh + e0 + 32 * qd);
-      XL[qd] = *reinterpret_cast<const uint4*>(L.xl + e0 + 32 * qd);
-      sq[qd] = L.sb[(e0 >> 5) + qd];
+      const float4* p = reinterpret_cast<const float4*>(L.x + e0 + 32 * qd);
+      float s = 0.f;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        X[qd][t] = p[t];
+        s += (X[qd][t].x + X[qd][t].y) + (X[qd][t].z + X[qd][t].w);
+      }
+      xs[qd] = s;
     }
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
       const uint32_t A[4] = {b.qa[r].x, b.qa[r].y, b.qa[r].z, b.qa[r].w};
       const uint32_t B[4] = {b.qb[r].x, b.qb[r].y, b.qb[r].z, b.qb[r].w};
       const uint32_t H[4] = {b.qh[r].x, b.qh[r].y, b.qh[r].z, b.qh[r].w};
-      int hs[4] = {0, 0, 0, 0}, ls[4] = {0, 0, 0, 0};
+      float s[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const uint32_t qq[4] = {(A[t] & 0x0F0F0F0Fu) | ((H[t] << 4) & 0x30303030u),
@@ -1021,18 +721,19 @@ struct Q6RTr {
                                 ((B[t] >> 4) & 0x0F0F0F0Fu) | ((H[t] >> 2) & 0x30303030u)};
 #pragma unroll
         for (int qd = 0; qd < 4; ++qd) {
-          const uint32_t xhw = t == 0 ? XH[qd].x : t == 1 ? XH[qd].y : t == 2 ? XH[qd].z : XH[qd].w;
-          const uint32_t xlw = t == 0 ? XL[qd].x : t == 1 ? XL[qd].y : t == 2 ? XL[qd].z : XL[qd].w;
-          const int sgn = (int)((qq[qd] + 0x60606060u) ^ 0x80808080u);  // bytes q - 32 as int8
-          hs[qd] = __builtin_amdgcn_sdot4(sgn, (int)xhw, hs[qd], false);
-          ls[qd] = __builtin_amdgcn_sdot4(sgn, (int)xlw, ls[qd], false);
+          const float4 xv = X[qd][t];
+          const uint32_t e = qq[qd] & 0x00FF00FFu, o = (qq[qd] >> 8) & 0x00FF00FFu;
+          s[qd] = fmaf(xv.x, h_lo(e), s[qd]);
+          s[qd] = fmaf(xv.z, h_hi(e), s[qd]);
+          s[qd] = fmaf(xv.y, h_lo(o), s[qd]);
+          s[qd] = fmaf(xv.w, h_hi(o), s[qd]);
         }
       }
       const float d = half_bits_to_float(b.d[r]);
       float sum = 0.f;
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd)
-        sum += sq[qd] * ((d * (float)(int8_t)((b.sc[r] >> (8 * qd)) & 0xFF)) * (float)(hs[qd] * 256 + ls[qd]));
+        sum += (d * (float)(int8_t)((b.sc[r] >> (8 * qd)) & 0xFF)) * (16777216.0f * s[qd] - 32.0f * xs[qd]);
       acc[r] += sum;
     }
   }
@@ -1047,8 +748,6 @@ struct Q6RTr {
 // byte is read as the unsigned q + 128 (v_cvt_f32_ubyte after flipping the sign bits), and the
 // offset comes back as one term per block, d * (sum x*(q+128) - 128 * sum x).
 struct Q8RTr {
-  static constexpr bool I8 = false;
-  static constexpr bool WB = false;
   static constexpr int CHUNKS = 8;  // 32-value blocks per 256
   static constexpr int BYTES = 34;
   IEK_DEV static size_t row_bytes(int nsb) { return q8r_row_bytes((size_t)nsb * 8); }
@@ -1127,22 +826,7 @@ struct MvGeom {
   }
 };
 
-// Issues the loads of a launch's first step into `A` (used to start a phase's weight stream
-// before the data it depends on is ready).
-template <class Tr, int R, bool DUAL>
-IEK_DEV void mv_prefetch(const MvArgs& a, typename Tr::template Buf<DUAL ? 2 * R : R>& A) {
-  constexpr int NR = DUAL ? 2 * R : R;
-  const MvGeom<Tr, R, DUAL> G(a);
-  if (G.steps > 0) {
-    const uint8_t* rows[NR];
-    int c;
-    G.rows_of(a, 0, rows, c);
-    Tr::template load<NR>(A, rows, c, G.nsb);
-  }
-}
-
-// The streaming matvec of one launch's rows. With `prefetched`, buffer A already holds (or has in
-// flight) the first step, issued by mv_prefetch with the same arguments.
+// The streaming matvec of one launch's rows.
 //
 // Load order and waits. The compiler waits for a load by counting the memory operations issued
 // after it, which it can only do along paths that issued the same ones; a load issued on some
@@ -1150,37 +834,31 @@ IEK_DEV void mv_prefetch(const MvArgs& a, typename Tr::template Buf<DUAL ? 2 * R
 // conditional staging loads go first, then x, then the weight buffers, and in the stream the
 // other buffer is always in flight while one is computed. MULTI (the host's choice, when some
 // wave has more than one step) keeps two buffers in flight from the start; single-step launches
-// carry only one.
-template <class Tr, int R, bool DUAL, bool COH = false, bool X2 = false, bool MULTI = true, int NT = 256, int XS = 0>
-IEK_DEV void mv_body(const MvArgs& a, float* lds, int pos, typename Tr::template Buf<DUAL ? 2 * R : R>& A,
-                     bool prefetched) {
-  static_assert(!COH || Tr::I8, "coherent staging is implemented for the int8-staged traits");
-  static_assert(!X2 || Tr::I8, "two-block staging is implemented for the int8-staged traits");
-  static_assert(NT == 256 || (NT == 512 && Tr::I8), "512-thread workgroups are implemented for the int8-staged traits");
-  static_assert(XS == 0 || (!Tr::I8 && NT == 256 && !COH), "split f32 staging: 256-thread f32 traits");
+// carry only one. XS > 0 selects the split staging (x slots issued ahead of the weight loads).
+template <class Tr, int R, bool DUAL, bool MULTI = true, int NT = 256, int XS = 0>
+IEK_DEV void mv_body(const MvArgs& a, float* lds, int pos) {
+  static_assert(NT == 256 || (NT == 512 && XS > 0), "512-thread workgroups need the split staging");
   constexpr int NW = NT / 64;
   constexpr int NR = DUAL ? 2 * R : R;
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  Lds L = lds_layout(a, lds, Tr::I8, Tr::WB ? 4 * NR * Q6_ROW_SLOT : 0);
-  L.wb += wave * NR * Q6_ROW_SLOT;
+  const int lane = threadIdx.x & 63;
+  const Lds L = lds_layout(a, lds);
   const MvGeom<Tr, R, DUAL, NW> G(a);
   const int npass = G.npass, nchunk = G.nchunk, steps = G.steps;
-  typename Tr::template Buf<NR> B;
+  typename Tr::template Buf<NR> A, B;
   unsigned long long run_key = 0;
   float acc[NR];
 #pragma unroll
   for (int r = 0; r < NR; ++r) acc[r] = 0.f;
   // the epilogue's residual / multiplier in a register when every wave has at most one row group
-  const bool ev_reg = (Tr::I8 || XS > 0) && (a.epi == EPI_RESID || a.epi == EPI_GELU_MUL) && G.groups <= G.stride;
+  const bool ev_reg = XS > 0 && (a.epi == EPI_RESID || a.epi == EPI_GELU_MUL) && G.groups <= G.stride;
   int ev_idx = -1;
   if (ev_reg) {
     const int row0 = min(G.g0, G.groups - 1) * R;
     const int s0 = seg_of(a, row0);
     ev_idx = max(0, min(row0 - seg_base(a, s0) + min(lane, R - 1), a.n[0] - 1));
   }
-  XPre xp;
-  xp.ev = 0.f;
   XPre32<(XS > 0 ? XS : 1)> xq;
+  xq.ev = 0.f;
 
   auto finish = [&](int it) {
     const int p = it % npass;
@@ -1196,7 +874,7 @@ IEK_DEV void mv_body(const MvArgs& a, float* lds, int pos, typename Tr::template
     if (DUAL) wave_reduce<R>(accu);
     const int row0 = g * R;
     const int s = DUAL ? 0 : seg_of(a, row0);
-    epilogue<R, COH>(a, L, s, row0 - seg_base(a, s), accg, accu, lane, pos, run_key, xp.ev, ev_reg);
+    epilogue<R>(a, L, s, row0 - seg_base(a, s), accg, accu, lane, pos, run_key, xq.ev, ev_reg);
 #pragma unroll
     for (int r = 0; r < NR; ++r) acc[r] = 0.f;
   };
@@ -1225,24 +903,14 @@ IEK_DEV void mv_body(const MvArgs& a, float* lds, int pos, typename Tr::template
 
   // x / residual / RoPE loads go out first, then the weight buffers, so the staging work overlaps
   // the weight fetch instead of queueing behind it.
-  if constexpr (Tr::I8) stage_i8_issue<COH, X2, NT>(a, xp, pos, ev_idx);
-  if constexpr (XS > 0) {
-    stage32_issue<XS>(a, xq, pos, ev_idx);
-    xp.ev = 0.f;
-  }
-  if (!prefetched) load(A, 0);
+  if constexpr (XS > 0) stage32_issue<XS, NT>(a, xq, pos, ev_idx);
+  load(A, 0);
   if constexpr (MULTI) load(B, 1);
   // keep the staging arithmetic below the weight loads: scheduled among them, its first use of x
   // would hold the remaining weight loads back until x has arrived
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (Tr::I8) {
-    stage_i8_finish<COH, X2, NT>(a, L, pos, xp, !ev_reg);
-  } else if constexpr (XS > 0) {
-    stage32_finish<XS>(a, L, pos, xq, !ev_reg);
-    xp.ev = xq.ev;
-  } else {
-    stage(a, L, pos);
-  }
+  if constexpr (XS > 0) stage32_finish<XS, NT>(a, L, pos, xq, !ev_reg);
+  else stage(a, L, pos);
   if (steps > 0) {
     if constexpr (MULTI) {
       // Each buffer's refill is issued right after it was computed, unconditionally (the last one

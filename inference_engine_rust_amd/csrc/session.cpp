@@ -49,8 +49,7 @@ Session::Session(Model* m) : m_(m) {
   for (auto& L : c.layers)
     if (L.kv_borrow < 0) total += 2 * (size_t)c.n_kv_heads * ctx_ * L.head_dim;
   IEK_HIP(hipMalloc(&kv_blob_, std::max<size_t>(total * esz, 16)));
-  // zeroed once: the decode attention may read cache rows past the live keys (weighted 0), which
-  // must hold finite values
+  // zeroed once for determinism of copies; no kernel lets a row past the live keys reach a result
   IEK_HIP(hipMemset(kv_blob_, 0, std::max<size_t>(total * esz, 16)));
   char* p = static_cast<char*>(kv_blob_);
   for (int li = 0; li < c.n_layers; ++li) {
@@ -76,6 +75,7 @@ Session::Session(Model* m) : m_(m) {
   }
   xdec_ = dev_alloc<float>(H_);
   xdec2_ = dev_alloc<float>(H_);
+  xdec_save_ = dev_alloc<float>(H_);
   xndec_ = dev_alloc<float>(std::max(H_, qmax));
   qd_ = dev_alloc<float>(qmax);
   kd_ = dev_alloc<float>(kvmax);
@@ -104,17 +104,11 @@ Session::Session(Model* m) : m_(m) {
   launch_fill_u64(d_key_, 0ull, 1, st_);
   launch_fill_i32(d_flag_, 0, 1, st_);
   launch_fill_i32(d_cnt_, 0, 2 * c.n_kv_heads, st_);
-  d_bar_ = dev_alloc<unsigned>(step_bar_words());
-  d_err_ = dev_alloc<int>(1);
-  launch_fill_i32((int*)d_bar_, 0, step_bar_words(), st_);
-  launch_fill_i32(d_err_, 0, 1, st_);
-  prepare_step();
   reset();
 }
 
 Session::~Session() {
   if (st_) (void)hipStreamSynchronize(st_);
-  dump_step_trace();
   if (step_exec_) (void)hipGraphExecDestroy(step_exec_);
   if (step_graph_) (void)hipGraphDestroy(step_graph_);
   if (st_) (void)hipStreamSynchronize(st_);
@@ -124,7 +118,7 @@ Session::~Session() {
                   (void*)d_step_, (void*)d_flags_, (void*)d_tok_, (void*)d_ids_, (void*)d_gen_, (void*)d_key_,
                   (void*)d_flag_, (void*)d_cnt_, (void*)xs_, (void*)xsum_, kv_blob_, (void*)ple_tok_,
                   (void*)ple_proj_, (void*)ple_pack_, (void*)ple_tokd_, (void*)ple_projd_, (void*)ple_packd_,
-                  (void*)d_bar_, (void*)d_err_, step_layers_, (void*)d_trace_, (void*)xdec2_})
+                  (void*)xdec2_, (void*)xdec_save_})
     dev_free(p);
   if (st_) (void)hipStreamDestroy(st_);
 }
@@ -185,10 +179,10 @@ void Session::ensure_rows(int rows) {
   rows_cap_ = rows;
 }
 
-// The weight copy the decode matvec streams: the regrouped layout when the model built one (the
-// Q6_K one only with the int8-staged path, which it requires), else the native blocks.
+// The weight copy the decode matvec streams: the regrouped layout when the model built one, else
+// the native blocks.
 static const void* mv_weight(const DevTensor& t, int K, int* dt) {
-  if (t.dev_r && K <= 16384 && (t.dtype_r != DT_Q6K_R || mv_int8_staging())) {
+  if (t.dev_r && K <= 16384) {
     *dt = t.dtype_r;
     return t.dev_r;
   }
@@ -444,59 +438,6 @@ void Session::layer_decode(int li, bool last) {
   launch_mv(dts[2], f, st_);
   dn.pos_inc = last ? d_pos_ : nullptr;
   launch_mv(dts[3], dn, st_);
-}
-
-// IEK_DECODE_STEP=1 selects the persistent decode step (every layer of a token in one launch) when
-// every layer takes the fused path with the int8-staged matvec traits it is built for (Q4_K Q/K/V,
-// O, gate/up and the regrouped Q6_K down), one head dim of 64 or 128 and no sliding window. It is
-// not the default: its grid barriers and coherent activation traffic cost more than the kernel
-// boundaries they replace (2.84 ms against 2.01 ms per C2 token, measured with IEK_STEP_TRACE).
-void Session::prepare_step() {
-  const Config& c = m_->cfg;
-  const char* e = getenv("IEK_DECODE_STEP");
-  if (!e || atoi(e) != 1) return;
-  if (gemma_ || c.n_layers <= 0) return;
-  const int hd = c.layers[0].head_dim;
-  if (hd != 64 && hd != 128) return;
-  if (c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads != 0 || c.n_heads / c.n_kv_heads > 8) return;
-  std::vector<uint8_t> host((size_t)c.n_layers * step_layer_bytes());
-  size_t lds = 0;
-  for (int li = 0; li < c.n_layers; ++li) {
-    const LayerSpec& S = c.layers[li];
-    if (!fused_ok(li) || S.head_dim != hd || S.window > 0 || S.kv_borrow >= 0) return;
-    MvArgs ph[4];
-    int dts[4];
-    decode_args(li, ph[0], ph[1], ph[2], ph[3], dts);
-    const int want[4] = {DT_Q4K, DT_Q4K, DT_Q4K, DT_Q6K_R};
-    for (int i = 0; i < 4; ++i) {
-      mv_finalize(ph[i]);
-      if (dts[i] != want[i] || !mv_stream_i8_ok(dts[i], ph[i])) return;
-      lds = std::max(lds, mv_lds_bytes_i8(ph[i]));
-    }
-    step_layer_pack(host.data() + (size_t)li * step_layer_bytes(), ph[0], ph[1], ph[2], ph[3],
-                    (const __half*)kc_[li], (const __half*)vc_[li], qd_, attd_, S.window);
-  }
-  IEK_HIP(hipMalloc(&step_layers_, host.size()));
-  IEK_HIP(hipMemcpy(step_layers_, host.data(), host.size(), hipMemcpyHostToDevice));
-  step_lds_ = lds;
-  // IEK_STEP_TRACE=1: record workgroup 0's clock at every phase boundary of the last step and print
-  // the per-phase durations when the session ends (a profiling aid; the step does the same work)
-  const char* t = getenv("IEK_STEP_TRACE");
-  if (t && atoi(t) != 0) d_trace_ = dev_alloc<unsigned long long>(16 * (size_t)c.n_layers + 4);
-}
-
-void Session::dump_step_trace() {
-  if (!d_trace_) return;
-  const int nl = m_->cfg.n_layers, n = 1 + 10 * nl;
-  std::vector<unsigned long long> h(n);
-  if (hipMemcpy(h.data(), d_trace_, n * 8, hipMemcpyDeviceToHost) != hipSuccess) return;
-  const char* names[10] = {"qkv", "bar1", "attn", "bar2", "o", "bar3", "gateup", "bar4", "down", "bar5"};
-  double sum[10] = {0};
-  for (int l = 0; l < nl; ++l)
-    for (int k = 0; k < 10; ++k) sum[k] += (double)(h[1 + 10 * l + k] - h[10 * l + k]) * 0.01;  // 100 MHz
-  fprintf(stderr, "[step trace] per-layer average us:");
-  for (int k = 0; k < 10; ++k) fprintf(stderr, " %s %.2f", names[k], sum[k] / nl);
-  fprintf(stderr, " | step %.1f us\n", (double)(h[n - 1] - h[0]) * 0.01);
 }
 
 void Session::layer_decode_unfused(int li) {
@@ -830,27 +771,8 @@ void Session::decode_body() {
     if (pend.t) launch_rmsnorm_add(xr, pend.t, pend.w, 1, H_, c.rms_eps, pend.has_scale, pend.scale, st_, xdec_);
     else if (xr != xdec_) launch_copy_f32(xr, xdec_, H_, st_);
     launch_add_int(d_pos_, 1, st_);
-  } else if (step_layers_) {
-    launch_decode_step(step_layers_, c.n_layers, c.n_heads, c.n_kv_heads, c.layers[0].head_dim, ctx_,
-                       1.0f / sqrtf((float)c.layers[0].head_dim), part_, d_cnt_, d_pos_, d_pos_, d_bar_, d_err_,
-                       step_lds_, d_trace_, st_);
   } else {
     for (int li = 0; li < c.n_layers; ++li) layer_decode(li, li == c.n_layers - 1);
-  }
-}
-
-// A grid-barrier timeout in the persistent decode step leaves its flag set; the session reports
-// it as a device error (its state is then undefined, as after any failed step).
-void Session::check_step_error() {
-  if (!step_layers_) return;
-  int err = 0;
-  IEK_HIP(hipMemcpyAsync(&err, d_err_, 4, hipMemcpyDeviceToHost, st_));
-  sync();
-  if (err) {
-    launch_fill_i32((int*)d_bar_, 0, step_bar_words(), st_);
-    launch_fill_i32(d_err_, 0, 1, st_);
-    sync();
-    fail(ST_DEVICE, "decode step: a grid barrier wait timed out");
   }
 }
 
@@ -866,7 +788,6 @@ void Session::decode_token(uint32_t id) {
   state_rows_ = 1;
   state_prefill_ = false;
   sync();
-  check_step_error();
 }
 
 void Session::check_state() const {
@@ -937,6 +858,7 @@ void Session::generate_greedy(int n, uint32_t* out_ids, bool use_graph) {
   if (pos_ + n > ctx_) fail(ST_KVCACHE, "KVCache is Full: max len is " + std::to_string(ctx_) + ".");
   launch_fill_i32(d_flags_, 0, n + 1, st_);
   launch_set_int(d_step_, 0, st_);
+  launch_copy_f32(xdec_, xdec_save_, H_, st_);  // the state to restore if the first step fails
   if (use_graph) {
     if (!step_exec_) {
       sync();
@@ -964,12 +886,31 @@ void Session::generate_greedy(int n, uint32_t* out_ids, bool use_graph) {
   IEK_HIP(hipMemcpyAsync(out_ids, d_gen_, (size_t)n * 4, hipMemcpyDeviceToHost, st_));
   IEK_HIP(hipMemcpyAsync(flags.data(), d_flags_, (size_t)n * 4, hipMemcpyDeviceToHost, st_));
   sync();
+  const int pos0 = pos_;
   pos_ += n;
   state_rows_ = 1;
   state_prefill_ = false;
-  check_step_error();
-  for (int i = 0; i < n; ++i)
-    if (flags[i]) fail(ST_SAMPLING, "invalid logits for argmax (empty or non-finite) at step " + std::to_string(i));
+  for (int i = 0; i < n; ++i) {
+    if (!flags[i]) continue;
+    // The reference loop (src/main.rs:100-116) stops at the first failing greedy_next_token: the KV
+    // cache then holds pos0 + i positions and the state is the output of step i - 1's decode. The
+    // replayed steps from i on decoded an arbitrary token, so the state is rebuilt: step i - 1's
+    // decode runs again at its own position (it rewrites the same KV row with the same values), or,
+    // for i == 0, the state from before the loop is restored.
+    if (i == 0) {
+      launch_copy_f32(xdec_save_, xdec_, H_, st_);
+      pos_ = pos0;
+      launch_set_int(d_pos_, pos_, st_);
+    } else {
+      pos_ = pos0 + i - 1;
+      launch_set_int(d_pos_, pos_, st_);
+      IEK_HIP(hipMemcpyAsync(d_tok_, &out_ids[i - 1], 4, hipMemcpyHostToDevice, st_));
+      decode_body();
+      pos_ += 1;
+    }
+    sync();
+    fail(ST_SAMPLING, "invalid logits for argmax (empty or non-finite) at step " + std::to_string(i));
+  }
 }
 
 void Session::copy_hidden(float* out, size_t cap, int* rows) {

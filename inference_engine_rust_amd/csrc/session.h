@@ -46,9 +46,6 @@ class Session {
   bool quant_ready(const DevTensor* const* ws, int nseg, int M, int K) const;
   bool fused_ok(int li) const;
   void decode_args(int li, MvArgs& qkv, MvArgs& o, MvArgs& gate_up, MvArgs& down, int* dts);
-  void prepare_step();
-  void check_step_error();
-  void dump_step_trace();
   void layer_decode(int li, bool last);
   void layer_decode_unfused(int li);
   // Gemma-4 family (attention.rs / ffn.rs Gemma branches, gemma4_ple.rs)
@@ -78,19 +75,12 @@ class Session {
   size_t xs_halves_ = 0;
   size_t xs_halves() const { return xs_halves_; }
   float* xsum_ = nullptr;  // its per-32 row sums (Q4_K min term)
-  float *xdec_ = nullptr, *xdec2_ = nullptr, *xndec_ = nullptr, *qd_ = nullptr, *kd_ = nullptr, *vd_ = nullptr, *attd_ = nullptr;
+  float *xdec_ = nullptr, *xdec2_ = nullptr, *xdec_save_ = nullptr, *xndec_ = nullptr, *qd_ = nullptr, *kd_ = nullptr, *vd_ = nullptr, *attd_ = nullptr;
   float *actd_ = nullptr, *logits_ = nullptr, *part_ = nullptr, *tmpd_ = nullptr;
   // per-layer embeddings (Gemma-4): token rows, model projection and packed inputs, [rows][L*pd]
   float *ple_tok_ = nullptr, *ple_proj_ = nullptr, *ple_pack_ = nullptr;
   float *ple_tokd_ = nullptr, *ple_projd_ = nullptr, *ple_packd_ = nullptr;
   bool gemma_ = false;
-  // persistent decode step: device array of per-layer launch arguments (null: per-launch path),
-  // its LDS size, the grid-barrier counters and the barrier timeout flag
-  void* step_layers_ = nullptr;
-  size_t step_lds_ = 0;
-  unsigned* d_bar_ = nullptr;
-  int* d_err_ = nullptr;
-  unsigned long long* d_trace_ = nullptr;
   // device-side loop state
   int* d_pos_ = nullptr;
   int* d_step_ = nullptr;

@@ -189,32 +189,6 @@ def test_qk_unpack_path_matches_oracle(gpu, c0_path, monkeypatch):
         r.decode(t)
 
 
-def test_persistent_decode_step_matches_per_launch_path(gpu, mid_path, monkeypatch):
-    """IEK_DECODE_STEP=1 runs the Mistral-width model's decode as the persistent step (all layers
-    in one launch, grid barriers between phases). Every phase runs the same device code with the
-    same per-row arithmetic as the per-launch kernels, so tokens, logits and the KV cache must be
-    bit-identical to the default per-launch path, stepwise and under graph replay."""
-    m = E.LoadedModel.load(mid_path)
-    prompt = synth.prompt_ids(5, 24)
-    monkeypatch.setenv("IEK_DECODE_STEP", "1")
-    a = E.InferenceSession(m)
-    monkeypatch.delenv("IEK_DECODE_STEP")
-    b = E.InferenceSession(m)
-    for s in (a, b):
-        s.prefill(prompt)
-    for _ in range(3):
-        ta, tb = E.greedy_next_token(a), E.greedy_next_token(b)
-        assert ta == tb
-        a.decode_token(ta)
-        b.decode_token(tb)
-        np.testing.assert_array_equal(a.logits_last_token(), b.logits_last_token())
-    ga, gb = a.generate_greedy(12), b.generate_greedy(12)
-    assert ga == gb
-    np.testing.assert_array_equal(a.logits_last_token(), b.logits_last_token())
-    for layer in (0, 1):
-        np.testing.assert_array_equal(a.kv(layer, False), b.kv(layer, False))
-        np.testing.assert_array_equal(a.kv(layer, True), b.kv(layer, True))
-
 
 def test_long_context_decode_matches_oracle(gpu, model_dir):
     """A 4096-token cache makes the decode attention process several 64-key slices per workgroup
