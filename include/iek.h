@@ -99,6 +99,10 @@ iek_status iek_greedy_next_token(iek_session* s, uint32_t* out_token);
 iek_status iek_session_generate_greedy(iek_session* s, size_t n_steps, uint32_t* out_ids);
 /* KVCache::current_pos (attention.rs:49-52). */
 iek_status iek_session_kv_len(const iek_session* s, uint64_t* out);
+/* Which decode implementation the session runs (no reference counterpart; a diagnostic): 0 = one
+ * launch per matvec and attention, 1 = the decode chain (Q/K/V, O, gate/up and down as phases of
+ * persistent launches, two launches per layer). Both compute the same function. */
+iek_status iek_session_decode_path(const iek_session* s, int* out);
 /* Hidden rows of the current ForwardState ([rows, hidden], src/engine/state.rs:7-175). */
 iek_status iek_session_hidden(iek_session* s, float* out, size_t cap, uint64_t* rows);
 /* KVCache::get_k_slice/get_v_slice for every stored position (attention.rs:77-110), widened to

@@ -35,6 +35,7 @@ SOURCES = [
     "kernels/gemm_mfma.hip",
     "kernels/gemm_q.hip",
     "kernels/gemma.hip",
+    "kernels/chain.hip",
     "model.cpp",
     "session.cpp",
     "api.cpp",

@@ -161,6 +161,8 @@ iek_status iek_session_generate_greedy(iek_session* s, size_t n, uint32_t* out) 
 
 iek_status iek_session_kv_len(const iek_session* s, uint64_t* out) { IEK_API_TRY(*out = (uint64_t)s->s->kv_len()) }
 
+iek_status iek_session_decode_path(const iek_session* s, int* out) { IEK_API_TRY(*out = s->s->decode_path()) }
+
 iek_status iek_session_hidden(iek_session* s, float* out, size_t cap, uint64_t* rows) {
   IEK_API_TRY({
     int r = 0;

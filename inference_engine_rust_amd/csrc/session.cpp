@@ -8,6 +8,7 @@
 //                                                src/layers/gemma4_ple.rs:27-109; embed.rs:53-149
 #include "session.h"
 
+#include "kernels/chain.h"
 #include "kernels/mv_args.h"
 
 #include <cmath>
@@ -104,6 +105,7 @@ Session::Session(Model* m) : m_(m) {
   launch_fill_u64(d_key_, 0ull, 1, st_);
   launch_fill_i32(d_flag_, 0, 1, st_);
   launch_fill_i32(d_cnt_, 0, 2 * c.n_kv_heads, st_);
+  prepare_chain();
   reset();
 }
 
@@ -118,7 +120,7 @@ Session::~Session() {
                   (void*)d_step_, (void*)d_flags_, (void*)d_tok_, (void*)d_ids_, (void*)d_gen_, (void*)d_key_,
                   (void*)d_flag_, (void*)d_cnt_, (void*)xs_, (void*)xsum_, kv_blob_, (void*)ple_tok_,
                   (void*)ple_proj_, (void*)ple_pack_, (void*)ple_tokd_, (void*)ple_projd_, (void*)ple_packd_,
-                  (void*)xdec2_, (void*)xdec_save_})
+                  (void*)xdec2_, (void*)xdec_save_, chain_blob_, (void*)d_chain_cnt_, (void*)d_chain_err_})
     dev_free(p);
   if (st_) (void)hipStreamDestroy(st_);
 }
@@ -440,6 +442,174 @@ void Session::layer_decode(int li, bool last) {
   launch_mv(dts[3], dn, st_);
 }
 
+static size_t embedding_hidden(const DevTensor& t, size_t* vocab) {
+  // lookup_embedding_rows (embeddings.rs:108-116): hidden = the smaller dim.
+  if (t.dims.size() != 2) fail(ST_TENSOR, "expected 2D embedding tensor");
+  size_t h = std::min(t.dims[0], t.dims[1]);
+  *vocab = std::max(t.dims[0], t.dims[1]);
+  return h;
+}
+
+// Decode chain path (Mistral/Llama family): the decode step as 2 launches per layer, each chain
+// launch running the O projection, gate/up, down and the next layer's Q/K/V as phases of one
+// persistent kernel (kernels/chain.hip), the attention in between. Taken when every layer is on
+// the fused path with Q4_K Q/K/V, O, gate/up, a Q4_K or regrouped Q6_K down projection and LM head,
+// and widths the chain kernel supports; otherwise decode runs the per-launch kernels.
+void Session::prepare_chain() {
+  const Config& c = m_->cfg;
+  if (gemma_ || c.n_layers <= 0 || c.unpack_qk) return;
+  const int G = num_cus();
+  auto wdt = [](const DevTensor& t, int* dt) -> const uint8_t* {
+    if (t.dev_r && t.dtype_r == DT_Q6K_R) {
+      *dt = DT_Q6K_R;
+      return (const uint8_t*)t.dev_r;
+    }
+    *dt = t.dtype;
+    return (const uint8_t*)t.dev;
+  };
+  auto dims_ok = [](const DevTensor& t, int K, int N) {
+    return t.dims.size() == 2 && (int)t.dims[0] == K && (int)t.dims[1] == N && N % 2 == 0;
+  };
+  auto phase_ok = [&](int dt, int K, bool norm, int units) {
+    if (!chain_phase_ok(dt, K, norm)) return false;
+    const int npass = (K + 4095) / 4096;
+    return (long long)units * G < (1ll << 31) && ((units + G - 1) / G) * 2 * npass <= 512;
+  };
+  for (int li = 0; li < c.n_layers; ++li) {
+    const LayerSpec& S = c.layers[li];
+    const LayerTensors& L = m_->layers[li];
+    int dq, dk, dv, dd;
+    wdt(L.wq, &dq);
+    wdt(L.wk, &dk);
+    wdt(L.wv, &dv);
+    wdt(L.down, &dd);
+    if (!fused_ok(li) || dq != DT_Q4K || dk != DT_Q4K || dv != DT_Q4K || L.wo.dtype != DT_Q4K ||
+        L.gate.dtype != DT_Q4K || L.up.dtype != DT_Q4K || (dd != DT_Q4K && dd != DT_Q6K_R))
+      return;
+    if (!dims_ok(L.wq, H_, S.q_dim) || !dims_ok(L.wk, H_, S.kv_dim) || !dims_ok(L.wv, H_, S.kv_dim) ||
+        !dims_ok(L.wo, S.q_dim, H_) || !dims_ok(L.gate, H_, S.ffn_dim) || !dims_ok(L.up, H_, S.ffn_dim) ||
+        !dims_ok(L.down, S.ffn_dim, H_) || S.head_dim % 2 != 0 || S.rotary_dim > S.head_dim)
+      return;
+    if (!phase_ok(DT_Q4K, H_, true, (S.q_dim + 2 * S.kv_dim) / 2) || !phase_ok(DT_Q4K, S.q_dim, false, H_ / 2) ||
+        !phase_ok(DT_Q4K, H_, true, S.ffn_dim) || !phase_ok(dd, S.ffn_dim, false, H_ / 2))
+      return;
+  }
+  int dh;
+  const uint8_t* head_w = wdt(m_->lm_head, &dh);
+  if ((dh != DT_Q4K && dh != DT_Q6K_R) || !dims_ok(m_->lm_head, H_, c.vocab) || !phase_ok(dh, H_, true, c.vocab / 2))
+    return;
+  size_t vocab;
+  embedding_hidden(m_->token_embd, &vocab);
+  chain_embed_ = m_->token_embd.dtype == DT_Q4K && H_ % 256 == 0 && c.embed_scale == 1.0f;
+  auto base = [&](int dt, int K, int epi, int units, const float* x, const float* norm, int wait_prev) {
+    ChainPhase P{};
+    P.dt = dt;
+    P.K = K;
+    P.npass = (K + 4095) / 4096;
+    P.epi = epi;
+    P.units = units;
+    P.x = x;
+    P.norm_w = norm;
+    P.eps = c.rms_eps;
+    P.wait_prev = wait_prev;
+    P.x_mode = CX_F32;
+    return P;
+  };
+  auto qkv = [&](int li, int wait_prev, bool embed) {
+    const LayerSpec& S = c.layers[li];
+    const LayerTensors& L = m_->layers[li];
+    ChainPhase P = base(DT_Q4K, H_, CE_QKV, (S.q_dim + 2 * S.kv_dim) / 2, xdec_, (const float*)L.attn_norm.dev,
+                        wait_prev);
+    P.nseg = 3;
+    P.seg[0] = ChainSeg{(const uint8_t*)L.wq.dev, qd_, S.q_dim, 0};
+    P.seg[1] = ChainSeg{(const uint8_t*)L.wk.dev, nullptr, S.kv_dim, 0};
+    P.seg[2] = ChainSeg{(const uint8_t*)L.wv.dev, nullptr, S.kv_dim, 0};
+    P.rope_cs = m_->rope_tables[L.rope_table].dev;
+    P.npairs = S.rotary_dim / 2;
+    P.head_dim = S.head_dim;
+    P.ctx = ctx_;
+    P.kc = (__half*)kc_[li];
+    P.vc = (__half*)vc_[li];
+    if (embed) {
+      P.x_mode = CX_EMBED_Q4K;
+      P.emb = (const uint8_t*)m_->token_embd.dev;
+      P.emb_out = xdec_;
+    }
+    return P;
+  };
+  auto ffn = [&](int li, std::vector<ChainPhase>& v) {
+    const LayerSpec& S = c.layers[li];
+    const LayerTensors& L = m_->layers[li];
+    ChainPhase o = base(DT_Q4K, S.q_dim, CE_RESID, H_ / 2, attd_, nullptr, 0);
+    o.nseg = 1;
+    o.seg[0] = ChainSeg{(const uint8_t*)L.wo.dev, xdec_, H_, 0};
+    o.resid = xdec_;
+    v.push_back(o);
+    ChainPhase g = base(DT_Q4K, H_, CE_SWIGLU, S.ffn_dim, xdec_, (const float*)L.ffn_norm.dev, 1);
+    g.nseg = 2;
+    g.seg[0] = ChainSeg{(const uint8_t*)L.gate.dev, actd_, S.ffn_dim, 0};
+    g.seg[1] = ChainSeg{(const uint8_t*)L.up.dev, nullptr, S.ffn_dim, 0};
+    v.push_back(g);
+    int dd;
+    const uint8_t* dw = wdt(L.down, &dd);
+    ChainPhase d = base(dd, S.ffn_dim, CE_RESID, H_ / 2, actd_, nullptr, 1);
+    d.nseg = 1;
+    d.seg[0] = ChainSeg{dw, xdec_, H_, 0};
+    d.resid = xdec_;
+    v.push_back(d);
+  };
+  std::vector<std::vector<ChainPhase>> launches;
+  launches.push_back({qkv(0, 0, chain_embed_)});
+  for (int li = 0; li < c.n_layers; ++li) {
+    std::vector<ChainPhase> v;
+    ffn(li, v);
+    if (li + 1 < c.n_layers) v.push_back(qkv(li + 1, 1, false));
+    launches.push_back(v);
+  }
+  {
+    std::vector<ChainPhase> v = launches.back();
+    ChainPhase h = base(dh, H_, CE_ARGMAX, c.vocab / 2, xdec_, (const float*)m_->output_norm.dev, 1);
+    h.nseg = 1;
+    h.seg[0] = ChainSeg{head_w, logits_, c.vocab, 0};
+    h.softcap = c.has_softcap ? c.softcap : 0.f;
+    v.push_back(h);
+    launches.push_back(v);
+  }
+  size_t total = 0;
+  for (auto& v : launches) total += v.size();
+  std::vector<ChainPhase> host;
+  host.reserve(total);
+  for (auto& v : launches) host.insert(host.end(), v.begin(), v.end());
+  IEK_HIP(hipMalloc(&chain_blob_, total * sizeof(ChainPhase)));
+  IEK_HIP(hipMemcpy(chain_blob_, host.data(), total * sizeof(ChainPhase), hipMemcpyHostToDevice));
+  size_t off = 0;
+  for (auto& v : launches) {
+    chain_ph_.push_back(static_cast<const char*>(chain_blob_) + off * sizeof(ChainPhase));
+    chain_np_.push_back((int)v.size());
+    off += v.size();
+  }
+  d_chain_cnt_ = dev_alloc<unsigned>(CHAIN_COUNTER_WORDS);
+  d_chain_err_ = dev_alloc<int>(1);
+  launch_fill_i32((int*)d_chain_cnt_, 0, CHAIN_COUNTER_WORDS, st_);
+  launch_fill_i32(d_chain_err_, 0, 1, st_);
+  chain_ = true;
+}
+
+// A bounded wait that ran out in a chain launch leaves its flag set; the counters are cleared and
+// the step reports a device error (the session state is then undefined, as after any failed step).
+void Session::check_chain_error() {
+  if (!chain_) return;
+  int err = 0;
+  IEK_HIP(hipMemcpyAsync(&err, d_chain_err_, 4, hipMemcpyDeviceToHost, st_));
+  sync();
+  if (err) {
+    launch_fill_i32((int*)d_chain_cnt_, 0, CHAIN_COUNTER_WORDS, st_);
+    launch_fill_i32(d_chain_err_, 0, 1, st_);
+    sync();
+    fail(ST_DEVICE, "decode chain: a bounded wait ran out (code " + std::to_string(err) + ")");
+  }
+}
+
 void Session::layer_decode_unfused(int li) {
   const Config& c = m_->cfg;
   const LayerSpec& S = c.layers[li];
@@ -717,13 +887,6 @@ void Session::layer_decode_gemma(int li, float*& xr, ResidUpdate& pend) {
   }
 }
 
-static size_t embedding_hidden(const DevTensor& t, size_t* vocab) {
-  // lookup_embedding_rows (embeddings.rs:108-116): hidden = the smaller dim.
-  if (t.dims.size() != 2) fail(ST_TENSOR, "expected 2D embedding tensor");
-  size_t h = std::min(t.dims[0], t.dims[1]);
-  *vocab = std::max(t.dims[0], t.dims[1]);
-  return h;
-}
 
 void Session::prefill(const uint32_t* ids, int n) {
   const Config& c = m_->cfg;
@@ -757,10 +920,43 @@ void Session::prefill(const uint32_t* ids, int n) {
   sync();
 }
 
-void Session::decode_body() {
+void Session::decode_body(bool head) {
   const Config& c = m_->cfg;
   size_t vocab;
   size_t hid = embedding_hidden(m_->token_embd, &vocab);
+  if (chain_) {
+    if (!chain_embed_) launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, d_tok_, 1, c.embed_scale, xdec_, st_);
+    const int L = c.n_layers;
+    for (int li = 0; li <= L; ++li) {
+      if (li > 0) {
+        const LayerSpec& S = c.layers[li - 1];
+        launch_attn_decode(qd_, kc_[li - 1], vc_[li - 1], kv_f32_, attd_, part_, d_cnt_, c.n_heads, c.n_kv_heads,
+                           S.head_dim, ctx_, d_pos_, S.window, 1.0f / sqrtf((float)S.head_dim), ctx_, st_);
+      }
+      const int k = (li == L && head) ? L + 1 : li;
+      ChainArgs a{};
+      a.phases = static_cast<const ChainPhase*>(chain_ph_[k]);
+      a.nphase = chain_np_[k];
+      a.pos = d_pos_;
+      a.tok = d_tok_;
+      a.counters = d_chain_cnt_;
+      a.err = d_chain_err_;
+      if (li == L) {
+        a.pos_inc = d_pos_;
+        if (head) {
+          a.finish_argmax = 1;
+          a.amax_key = d_key_;
+          a.amax_flag = d_flag_;
+          a.out_tok = d_tok_;
+          a.gen = d_gen_;
+          a.flags = d_flags_;
+          a.step = d_step_;
+        }
+      }
+      launch_chain(a, st_);
+    }
+    return;
+  }
   launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, d_tok_, 1, c.embed_scale, xdec_, st_);
   if (gemma_) {
     embed_ple(d_tok_, 1, xdec_, nullptr, ple_tokd_, ple_projd_, ple_packd_);
@@ -776,6 +972,17 @@ void Session::decode_body() {
   }
 }
 
+// One greedy step of the loop in generate_greedy: decode the token in d_tok_, then the LM head and
+// argmax of the new state (the argmax of the first state runs before the loop).
+void Session::step_body() {
+  if (chain_) {
+    decode_body(true);
+  } else {
+    decode_body(false);
+    argmax_body(true);
+  }
+}
+
 void Session::decode_token(uint32_t id) {
   size_t vocab;
   embedding_hidden(m_->token_embd, &vocab);
@@ -788,6 +995,7 @@ void Session::decode_token(uint32_t id) {
   state_rows_ = 1;
   state_prefill_ = false;
   sync();
+  check_chain_error();
 }
 
 void Session::check_state() const {
@@ -859,13 +1067,15 @@ void Session::generate_greedy(int n, uint32_t* out_ids, bool use_graph) {
   launch_fill_i32(d_flags_, 0, n + 1, st_);
   launch_set_int(d_step_, 0, st_);
   launch_copy_f32(xdec_, xdec_save_, H_, st_);  // the state to restore if the first step fails
+  // greedy token of the current state (step 0), then n x { decode it; greedy token of the new
+  // state (step i + 1) }: the last step's token is computed and not returned
+  argmax_body(true);
   if (use_graph) {
     if (!step_exec_) {
       sync();
       IEK_HIP(hipStreamBeginCapture(st_, hipStreamCaptureModeThreadLocal));
       try {
-        argmax_body(true);
-        decode_body();
+        step_body();
       } catch (...) {
         hipGraph_t g;
         (void)hipStreamEndCapture(st_, &g);
@@ -877,15 +1087,13 @@ void Session::generate_greedy(int n, uint32_t* out_ids, bool use_graph) {
     }
     for (int i = 0; i < n; ++i) IEK_HIP(hipGraphLaunch(step_exec_, st_));
   } else {
-    for (int i = 0; i < n; ++i) {
-      argmax_body(true);
-      decode_body();
-    }
+    for (int i = 0; i < n; ++i) step_body();
   }
   std::vector<int> flags(n);
   IEK_HIP(hipMemcpyAsync(out_ids, d_gen_, (size_t)n * 4, hipMemcpyDeviceToHost, st_));
   IEK_HIP(hipMemcpyAsync(flags.data(), d_flags_, (size_t)n * 4, hipMemcpyDeviceToHost, st_));
   sync();
+  check_chain_error();
   const int pos0 = pos_;
   pos_ += n;
   state_rows_ = 1;

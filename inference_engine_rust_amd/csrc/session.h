@@ -32,6 +32,7 @@ class Session {
   void generate_greedy(int n, uint32_t* out_ids, bool use_graph = true);
 
   int kv_len() const { return pos_; }
+  int decode_path() const { return chain_ ? 1 : 0; }
   int state_rows() const { return state_rows_; }
   void copy_hidden(float* out, size_t cap, int* rows);
   void copy_kv(int layer, bool v, float* out, size_t cap);  // [n_kv][pos][head_dim] -> f32
@@ -53,7 +54,12 @@ class Session {
   void embed_ple(const uint32_t* d_ids, int n, const float* x, const __half* xs, float* tok, float* proj, float* pack);
   void layer_prefill_gemma(int li, int M);
   void layer_decode_gemma(int li, float*& xr, ResidUpdate& pend);
-  void decode_body();           // embed(d_tok) + every layer + pos++; no host sync
+  // embed(d_tok) + every layer + pos++ (and, with `head` on the chain path, the LM head and
+  // greedy argmax of the new state, recorded like argmax_body(true)); no host sync
+  void decode_body(bool head = false);
+  void step_body();  // one greedy step: decode d_tok + argmax of the new state (recorded)
+  void prepare_chain();
+  void check_chain_error();
   void logits_body(bool argmax);  // final norm + LM head (+ softcap) into logits_
   void argmax_body(bool record);
   void sync();
@@ -94,6 +100,16 @@ class Session {
   int pos_ = 0;
   int state_rows_ = 0;  // rows of the last ForwardState (0 = none)
   bool state_prefill_ = false;
+  // decode chain path (kernels/chain.hip): device ChainPhase arrays per launch; launch 0 holds
+  // layer 0's Q/K/V, launch l + 1 layer l's O, gate/up, down and layer l + 1's Q/K/V; the last
+  // layer's launch comes in two forms, without and with the LM head + argmax
+  bool chain_ = false;
+  bool chain_embed_ = false;  // launch 0 dequantises the token's embedding row itself
+  void* chain_blob_ = nullptr;
+  std::vector<const void*> chain_ph_;
+  std::vector<int> chain_np_;
+  unsigned* d_chain_cnt_ = nullptr;
+  int* d_chain_err_ = nullptr;
   hipGraphExec_t step_exec_ = nullptr;
   hipGraph_t step_graph_ = nullptr;
 };

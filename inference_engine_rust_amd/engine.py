@@ -70,6 +70,7 @@ EXPORTS = {
     "iek_greedy_next_token": ([_P, ctypes.POINTER(ctypes.c_uint32)], ctypes.c_int),
     "iek_session_generate_greedy": ([_P, _SZ, _P], ctypes.c_int),
     "iek_session_kv_len": ([_P, ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
+    "iek_session_decode_path": ([_P, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
     "iek_session_hidden": ([_P, _P, _SZ, ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
     "iek_session_kv": ([_P, ctypes.c_uint64, ctypes.c_int, _P, _SZ], ctypes.c_int),
     "iek_dequantize": ([ctypes.c_int, _P, _SZ, _P, _P], ctypes.c_int),
@@ -188,6 +189,12 @@ class InferenceSession:
         out = np.zeros(max(n_steps, 1), np.uint32)
         _check(lib().iek_session_generate_greedy(self._h, n_steps, _np_ptr(out)))
         return [int(x) for x in out[:n_steps]]
+
+    def decode_path(self) -> int:
+        """0: per-launch decode kernels; 1: the decode chain (persistent phase launches)."""
+        v = ctypes.c_int(0)
+        _check(lib().iek_session_decode_path(self._h, ctypes.byref(v)))
+        return int(v.value)
 
     def kv_len(self) -> int:
         v = ctypes.c_uint64()
