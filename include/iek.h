@@ -6,10 +6,12 @@
  * repository root). Conventions:
  *   - Every function returns an iek_status (0 = OK); iek_last_error() gives a thread-local
  *     message. Status values are the reference's EngineError variants (src/error.rs:5-38).
- *   - Engine-level calls take host buffers and are synchronous on return.
- *   - Op-level calls take DEVICE pointers plus an optional hipStream_t (NULL = the library's
- *     default stream) and are asynchronous, like any HIP launch; iek_synchronize() waits.
- *   - Handles are not thread-safe; one session per host thread.
+ *   - Engine-, forward- and op-level calls (iek_session_*, iek_matmul, iek_rmsnorm, ...) take
+ *     caller-owned HOST buffers and are synchronous on return, like the reference's functions.
+ *   - The iek_dev_* variants of the ops take DEVICE pointers plus an optional hipStream_t (NULL =
+ *     the null stream) and are asynchronous, like any HIP launch; iek_synchronize() waits.
+ *   - Handles are not thread-safe; one session per host thread. The host-buffer op entries may be
+ *     called from several threads (they take turns on one staging stream per device).
  */
 #ifndef IEK_H
 #define IEK_H
@@ -36,8 +38,9 @@ typedef enum iek_status {
   IEK_ERR_DEVICE = 11    /* HIP runtime failure (no reference counterpart: the reference is CPU-only) */
 } iek_status;
 
-/* Tensor dtypes: the reference's TensorType (src/core/tensor.rs:13-23). */
-typedef enum iek_dtype { IEK_F32 = 0, IEK_Q4K = 1, IEK_Q6K = 2, IEK_Q8_0 = 3 } iek_dtype;
+/* Tensor dtypes: the reference's TensorType (src/core/tensor.rs:13-23); IEK_F16 is the device KV
+ * cache's element type (iek_dev_attention_decode). */
+typedef enum iek_dtype { IEK_F32 = 0, IEK_Q4K = 1, IEK_Q6K = 2, IEK_Q8_0 = 3, IEK_F16 = 4 } iek_dtype;
 
 typedef struct iek_model iek_model;
 typedef struct iek_session iek_session;
@@ -62,6 +65,15 @@ const char* iek_last_error(void);
  * (names.rs:52-276), then one upload of every tensor's native blocks to HBM on `device`. */
 iek_status iek_model_load(const char* gguf_path, int device, iek_model** out);
 void iek_model_free(iek_model* model);
+/* Wall times of iek_model_load's stages, named after the cold-start regions of
+ * src/bench_metrics.rs:199-296 (run_cold_start): GGUF header + tables (read_file), ModelConfig +
+ * name resolution, tensor bytes from the memory-mapped file to HBM through pinned staging
+ * (names.load_all), and the derived device tables (model.weights()). hbm_bytes: weight bytes. */
+typedef struct iek_load_timings {
+  double gguf_metadata_ms, config_and_resolve_ms, tensor_load_ms, weights_build_ms;
+  uint64_t hbm_bytes;
+} iek_load_timings;
+iek_status iek_model_load_timings(const iek_model* model, iek_load_timings* out);
 /* LoadedModel::config (src/loaded_model.rs:51-53). */
 iek_status iek_model_config_get(const iek_model* model, iek_model_config* out);
 /* Per-layer LayerAttentionSpec + LayerDims (model_config.rs:72-100, :484-629): window -1 = none,
@@ -109,32 +121,99 @@ iek_status iek_session_hidden(iek_session* s, float* out, size_t cap, uint64_t* 
  * f32 as [n_kv][kv_len][head_dim]. */
 iek_status iek_session_kv(iek_session* s, uint64_t layer, int which_v, float* out, size_t cap);
 
-/* ---- op level (device pointers) ------------------------------------------------------------ */
+/* ---- forward level (src/engine/runtime.rs, src/layers/block.rs) ---------------------------
+ * The session's ForwardState ([rows, hidden], src/engine/state.rs:7-175) stays in HBM; read it
+ * with iek_session_hidden and the logits of its last row with iek_session_logits_last_token
+ * (final_logits_last_token, runtime.rs:76-116). A layer-level forward runs layers 0, 1, ...,
+ * n_layers - 1 in order (IEK_ERR_MODEL for another layer); after the last one the KV length grows
+ * by the state's rows. While one is part way, iek_session_decode_token, iek_greedy_next_token,
+ * iek_session_generate_greedy and iek_session_logits_last_token fail with IEK_ERR_MODEL. */
+/* prefill_from_tokens_loaded (src/engine/embed.rs:104-138): state = the ids' embedding rows (and,
+ * for Gemma-4, their per-layer inputs, gemma4_ple.rs:27-109); n = 1 is the decode-token state of
+ * prefill_state_for_single_token_loaded (embed.rs:53-98). */
+iek_status iek_session_embed(iek_session* s, const uint32_t* token_ids, size_t n);
+/* ForwardState::from_flat (state.rs:107-113): state = `rows` x hidden_dim floats, without
+ * per-layer inputs (Gemma-4 layers with per-layer embeddings then fail with IEK_ERR_MODEL). */
+iek_status iek_session_set_hidden(iek_session* s, const float* hidden, size_t rows);
+/* prefill_layer_block (src/layers/block.rs:12-47) of layer `layer` over every row of the state:
+ * prefill_attention_with_norm (attention.rs:696-824) + prefill_ffn_with_norm (ffn.rs:66-167) +
+ * the Gemma-4 tails (ffn.rs:170-278); K/V rows go to the layer's cache at kv_len, kv_len + 1, ... */
+iek_status iek_session_prefill_layer_block(iek_session* s, uint64_t layer);
+/* decode_layer_block (block.rs:50-89) on a one-row state (IEK_ERR_MODEL otherwise), RoPE at kv_len. */
+iek_status iek_session_decode_layer_block(iek_session* s, uint64_t layer);
+/* prefill_forward (runtime.rs:14-32): every layer's prefill block over the state. */
+iek_status iek_session_prefill_forward(iek_session* s);
+/* decode_forward (runtime.rs:37-61): every layer's decode block; the state must have one row. */
+iek_status iek_session_decode_forward(iek_session* s);
+
+/* ---- op level, host buffers (synchronous) -------------------------------------------------- */
+/* A matmul weight: native block bytes in ggml layout (element (k, n) at flat k + n*K), as the
+ * reference's Tensor holds them (src/core/tensor.rs:8-23). on_device = 0: `data` is host memory,
+ * uploaded per call; on_device = 1: `data` is an HBM address (e.g. from iek_model_tensor). */
+typedef struct iek_weight {
+  int32_t dtype; /* iek_dtype: F32, Q4K, Q6K or Q8_0 */
+  const void* data;
+  uint64_t bytes;
+  int32_t on_device;
+} iek_weight;
+/* matmul (src/ops/matmul.rs:18-415): out[m, n] = sum_k a[m, k] * W(k, n). IEK_ERR_MATMUL for an
+ * unsupported dtype or when w->bytes < div_ceil(K*N, block) * block_bytes. */
+iek_status iek_matmul(const float* a, size_t m, size_t k, const iek_weight* w, size_t n, float* out);
 /* dequantize_{q4k,q6k,q8_0}_block over n consecutive blocks (quant_k_handler.rs:21-135). */
-iek_status iek_dequantize(int dtype, const void* blocks, size_t nblocks, float* out, void* stream);
-/* matmul (src/ops/matmul.rs:18-415): out[m,n] = sum_k a[m,k] * W(k,n), W in ggml layout
- * (element (k,n) at flat k + n*K) and native block bytes. w_bytes is checked against
- * div_ceil(K*N, block) * block_bytes like the reference. */
-iek_status iek_matmul(const float* a, size_t m, size_t k, int w_dtype, const void* w, size_t w_bytes, size_t n,
-                      float* out, void* stream);
+iek_status iek_dequantize(int dtype, const void* blocks, size_t nblocks, float* out);
 /* rmsnorm over `rows` rows of `dim` (src/ops/rmsnorm.rs:25-50). */
-iek_status iek_rmsnorm(const float* in, const float* weight, size_t rows, size_t dim, float eps, float* out,
-                       void* stream);
-/* rope (src/ops/rope.rs:11-59) on n_heads contiguous heads of head_dim, at position `pos`;
- * freq_factors: HOST pointer or NULL. */
+iek_status iek_rmsnorm(const float* in, const float* weight, size_t rows, size_t dim, float eps, float* out);
+/* rope (src/ops/rope.rs:11-59) in place on n_heads contiguous heads of head_dim at position `pos`;
+ * freq_factors may be NULL. IEK_ERR_OP: rotary_dim > head_dim, an odd rotary span, or fewer
+ * freq_factors than pairs. */
 iek_status iek_rope(float* vec, size_t n_heads, uint32_t head_dim, uint32_t rotary_dim, float base, uint32_t pos,
-                    const float* freq_factors, size_t ff_len, void* stream);
-/* softmax (src/ops/softmax.rs:3-28). */
-iek_status iek_softmax(const float* in, float* out, size_t n, void* stream);
-/* swiglu (src/ops/swiglu.rs:24-36). */
-iek_status iek_swiglu(const float* gate, const float* up, float* out, size_t n, void* stream);
-/* out = gelu_tanh(gate) * up, or gelu_tanh(gate) when up is NULL (src/ops/gelu.rs:5-11). */
-iek_status iek_gelu_tanh(const float* gate, const float* up, float* out, size_t n, void* stream);
+                    const float* freq_factors, size_t ff_len);
+/* softmax (src/ops/softmax.rs:3-28); IEK_ERR_OP when n == 0. */
+iek_status iek_softmax(const float* in, float* out, size_t n);
+/* swiglu (src/ops/swiglu.rs:24-36): out = silu(gate) * up. */
+iek_status iek_swiglu(const float* gate, const float* up, float* out, size_t n);
+/* out = gelu_tanh(gate) * up, or gelu_tanh(gate) when up is NULL (src/ops/gelu.rs:5-18). */
+iek_status iek_gelu_tanh(const float* gate, const float* up, float* out, size_t n);
 /* residual_add (src/ops/residual_add.rs:3-12). */
-iek_status iek_residual_add(const float* a, const float* b, float* out, size_t n, void* stream);
-/* argmax_index / sample_greedy (src/engine/sampling.rs:25-49). Synchronous; *out_index gets the
- * first maximal index. IEK_ERR_SAMPLING when n == 0 or any logit is non-finite. */
-iek_status iek_argmax(const float* logits, size_t n, uint32_t* out_index, void* stream);
+iek_status iek_residual_add(const float* a, const float* b, float* out, size_t n);
+/* argmax_index / sample_greedy (src/engine/sampling.rs:25-49): first maximal index;
+ * IEK_ERR_SAMPLING when n == 0 or any logit is non-finite. */
+iek_status iek_argmax(const float* logits, size_t n, uint32_t* out_index);
+/* The attention of decode_attention_layer (src/layers/attention.rs:608-650) for one new token,
+ * its K/V already appended: for every query head h (KV head h / (n_heads / n_kv_heads)),
+ * out[h] = softmax(scale * q[h] . K[j]) . V[j] over positions j in [j_min, total_pos), j_min =
+ * total_pos - sliding_window when 0 < sliding_window < total_pos, else 0. k_cache and v_cache are
+ * the reference KVCache's buffers (attention.rs:16-24): [total_pos][n_kv_heads][head_dim] f32.
+ * Supported: head_dim 64, 128, 256 or 512 and n_heads / n_kv_heads <= 8 (IEK_ERR_OP otherwise);
+ * total_pos == 0 is IEK_ERR_OP (the reference's empty softmax). */
+iek_status iek_attention_decode(const float* q, const float* k_cache, const float* v_cache, size_t n_heads,
+                                size_t n_kv_heads, size_t head_dim, size_t total_pos, size_t sliding_window,
+                                float scale, float* out);
+
+/* ---- op level, device pointers (asynchronous on `stream`) ---------------------------------
+ * Same functions and errors as the host entries above; operands live in HBM. */
+iek_status iek_dev_dequantize(int dtype, const void* blocks, size_t nblocks, float* out, void* stream);
+/* w: w_bytes of native blocks in HBM; w_dtype an iek_dtype (F32, Q4K, Q6K, Q8_0). */
+iek_status iek_dev_matmul(const float* a, size_t m, size_t k, int w_dtype, const void* w, size_t w_bytes, size_t n,
+                          float* out, void* stream);
+iek_status iek_dev_rmsnorm(const float* in, const float* weight, size_t rows, size_t dim, float eps, float* out,
+                           void* stream);
+/* freq_factors: HOST pointer or NULL. Waits for the stream before returning. */
+iek_status iek_dev_rope(float* vec, size_t n_heads, uint32_t head_dim, uint32_t rotary_dim, float base, uint32_t pos,
+                        const float* freq_factors, size_t ff_len, void* stream);
+iek_status iek_dev_softmax(const float* in, float* out, size_t n, void* stream);
+iek_status iek_dev_swiglu(const float* gate, const float* up, float* out, size_t n, void* stream);
+iek_status iek_dev_gelu_tanh(const float* gate, const float* up, float* out, size_t n, void* stream);
+iek_status iek_dev_residual_add(const float* a, const float* b, float* out, size_t n, void* stream);
+/* Waits for the stream; *out_index is a host location. */
+iek_status iek_dev_argmax(const float* logits, size_t n, uint32_t* out_index, void* stream);
+/* iek_attention_decode over the session's cache layout: k_cache / v_cache are
+ * [n_kv_heads][max_seq_len][head_dim] of kv_dtype (IEK_F16 or IEK_F32) with positions
+ * [0, total_pos) filled; total_pos <= max_seq_len (IEK_ERR_KV_CACHE otherwise). The partial
+ * buffers are allocated per call; waits for the stream before returning. */
+iek_status iek_dev_attention_decode(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
+                                    size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t max_seq_len,
+                                    size_t total_pos, size_t sliding_window, float scale, float* out, void* stream);
 
 /* ---- device memory helpers for FFI callers without a HIP binding ---------------------------- */
 iek_status iek_device_alloc(size_t bytes, void** out);

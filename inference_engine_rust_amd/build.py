@@ -1,6 +1,9 @@
 """Build recipe for the native libraries (in-tree, so they travel with the repository snapshot).
 
 * ``libiek.so``        — the product: HIP kernels for gfx950 + the C++ host runtime + C ABI.
+* ``libiek.a``         — the same objects as a static archive (link with ``-lamdhip64``).
+* ``bin/iek_bench_compare`` — the bench_compare CLI over the C ABI (g++, static libiek.a).
+* ``bin/iek_abi_test`` — C++ caller of the C ABI used by the GPU tests (g++, static libiek.a).
 * ``libiek_synth.so``  — seeded synthetic GGUF writer / quantisers (host C++).
 
 Objects go to ``inference_engine_rust_amd/_build``; each translation unit compiles in its own
@@ -18,6 +21,10 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libiek.so")
+LIB_A = os.path.join(PKG, "libiek.a")
+BIN = os.path.join(PKG, "bin")
+REPO = os.path.dirname(PKG)
+ROCM_LIB = "/opt/rocm/lib"
 SYNTH_LIB = os.path.join(PKG, "libiek_synth.so")
 ARCH = os.environ.get("IEK_OFFLOAD_ARCH", "gfx950")
 
@@ -73,12 +80,33 @@ def build_lib(jobs: int | None = None) -> str:
     tmp = LIB + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, LIB)
+    tmp_a = LIB_A + ".tmp"
+    if os.path.exists(tmp_a):
+        os.remove(tmp_a)
+    _run(["ar", "rcs", tmp_a, *objs])
+    os.replace(tmp_a, LIB_A)
     return LIB
+
+
+def _link_tool(src: str, out: str) -> str:
+    """A C++ caller of include/iek.h built with g++ against the static archive."""
+    os.makedirs(BIN, exist_ok=True)
+    tmp = out + ".tmp"
+    _run(["g++", "-std=c++17", "-O2", "-Wall", "-I", os.path.join(REPO, "include"), src, LIB_A, "-L", ROCM_LIB,
+          "-lamdhip64", f"-Wl,-rpath,{ROCM_LIB}", "-pthread", "-o", tmp])
+    os.replace(tmp, out)
+    return out
+
+
+def build_tools() -> None:
+    _link_tool(os.path.join(PKG, "cli", "bench_compare.cpp"), os.path.join(BIN, "iek_bench_compare"))
+    _link_tool(os.path.join(REPO, "tests", "abi", "iek_abi_test.cpp"), os.path.join(BIN, "iek_abi_test"))
 
 
 def build_all() -> None:
     build_synth()
     build_lib()
+    build_tools()
 
 
 if __name__ == "__main__":

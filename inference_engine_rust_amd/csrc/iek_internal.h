@@ -104,11 +104,14 @@ void launch_unpack_qk(const float* src, float* dst, int rows, int row_stride, in
                       hipStream_t st);
 void launch_copy_f32(const float* src, float* dst, size_t n, hipStream_t st);
 void launch_fill_i32(int* p, int v, int n, hipStream_t st);
-// `counters` holds n_kv zero-initialised ints; the kernel leaves them zero again.
+// `counters` holds 2 * n_kv zero-initialised ints (one per KV head and query-head group); the
+// kernel leaves them zero again.
 // The cache is fp16, or f32 when kv_f32 (Gemma-4 sessions).
 void launch_attn_decode(const float* q, const void* kc, const void* vc, bool kv_f32, float* out, float* part,
                         int* counters, int n_heads, int n_kv, int head_dim, int ctx, const int* pos_dev, int window,
                         float scale, int max_len, hipStream_t st);
+// Floats of `part` that launch_attn_decode needs at most for a cache of max_len keys.
+size_t attn_decode_part_floats(int n_heads, int head_dim, int max_len);
 // With a scratch buffer of attn_prefill_scratch_halves() halves (head_dim 64 or 128), each K/V block
 // is staged once for all the query heads of its KV head; otherwise one workgroup per query head.
 size_t attn_prefill_scratch_halves(int M, int n_kv, int head_dim);

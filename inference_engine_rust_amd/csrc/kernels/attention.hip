@@ -188,6 +188,11 @@ static void attn_decode_hd(dim3 grid, hipStream_t st, const float* q, const void
   }
 }
 
+size_t attn_decode_part_floats(int n_heads, int head_dim, int max_len) {
+  // one (max, sum, o[head_dim]) slot per query head and 64-key slice bounds both kernels' partials
+  return (size_t)n_heads * ((max_len + SPLIT - 1) / SPLIT) * (head_dim + 2);
+}
+
 void launch_attn_decode(const float* q, const void* kc, const void* vc, bool kv_f32, float* out, float* part,
                         int* counters, int n_heads, int n_kv, int head_dim, int ctx, const int* pos_dev, int window,
                         float scale, int max_len, hipStream_t st) {

@@ -5,8 +5,17 @@
 //   src/model_loader/file_loader.rs:11-65   header, KV table, tensor table, aligned data offset
 //   src/model_loader/reader.rs:94-157       value encodings (bool must be 0/1, nested arrays)
 //   src/model_loader/tensor_loader.rs:27-88 raw block bytes, BF16 -> F32, div_ceil byte lengths
+// One extension: F16 tensors (ggml type 1), which the reference rejects (tensor.rs:87-97), are
+// widened to F32 at load like BF16; their values are exactly representable, so a model with F16
+// norms or embeddings runs as the same model stored in F32.
 //   src/model_config.rs:143-730             family detection, dims, attention specs, QK unpack
 //   src/model_weights/names.rs:52-336       tensor-name fallbacks, tied LM head
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -345,7 +354,7 @@ std::string resolve(const GgufFile& g, std::initializer_list<std::string> cands,
 
 int dtype_of(uint32_t ggml) {
   switch (ggml) {
-    case 0: case 30: return DT_F32;
+    case 0: case 1: case 30: return DT_F32;
     case 12: return DT_Q4K;
     case 14: return DT_Q6K;
     case 8: return DT_Q8_0;
@@ -373,6 +382,38 @@ Model::~Model() {
   if (blob_r) (void)hipFree(blob_r);
 }
 
+static double ms_since(std::chrono::steady_clock::time_point t0) {
+  return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+}
+
+// Read-only mapping of the whole GGUF file (the tensor bytes are copied out of it once).
+struct FileMap {
+  const uint8_t* p = nullptr;
+  size_t n = 0;
+  explicit FileMap(const std::string& path) {
+    int fd = open(path.c_str(), O_RDONLY);
+    if (fd < 0) fail(ST_IO, "cannot open " + path);
+    struct stat sb;
+    if (fstat(fd, &sb) != 0) {
+      close(fd);
+      fail(ST_IO, "cannot stat " + path);
+    }
+    n = (size_t)sb.st_size;
+    void* a = n ? mmap(nullptr, n, PROT_READ, MAP_PRIVATE, fd, 0) : nullptr;
+    close(fd);
+    if (n && a == MAP_FAILED) fail(ST_IO, "cannot map " + path);
+    p = static_cast<const uint8_t*>(a);
+    if (n) madvise(a, n, MADV_SEQUENTIAL);
+  }
+  ~FileMap() {
+    if (p) munmap(const_cast<uint8_t*>(p), n);
+  }
+  const uint8_t* at(uint64_t off, size_t bytes) const {
+    if (off > n || bytes > n - off) fail(ST_IO, "failed to fill whole buffer");
+    return p + off;
+  }
+};
+
 Model* load_model(const std::string& path, int device) {
   FILE* probe = fopen(path.c_str(), "rb");
   if (!probe) fail(ST_MODEL, "model file not found: " + path);
@@ -380,7 +421,10 @@ Model* load_model(const std::string& path, int device) {
   std::unique_ptr<Model> m(new Model());
   m->device = device;
   m->path = path;
+  auto t0 = std::chrono::steady_clock::now();
   GgufFile g = read_gguf(path);
+  m->timings.gguf_metadata_ms = ms_since(t0);
+  t0 = std::chrono::steady_clock::now();
   m->cfg = config_from_gguf(g);
   const Config& c = m->cfg;
 
@@ -434,6 +478,9 @@ Model* load_model(const std::string& path, int device) {
     want(&m->ple_proj_norm, resolve(g, {"per_layer_proj_norm.weight"}));
   }
 
+  m->timings.config_and_resolve_ms = ms_since(t0);
+  t0 = std::chrono::steady_clock::now();
+
   // Layout: every distinct tensor once, each at a 256-byte aligned offset of one HBM blob.
   struct Slot {
     const TensorMeta* meta;
@@ -448,7 +495,7 @@ Model* load_model(const std::string& path, int device) {
     const TensorMeta* t = g.tensor(w.name);
     Slot s{t, dtype_of(t->ggml_type), 1, 0, 0, 0};
     for (size_t d : t->dims) s.nelem *= d;
-    s.file_bytes = t->ggml_type == 30 ? s.nelem * 2 : byte_len(s.dtype, s.nelem);
+    s.file_bytes = (t->ggml_type == 30 || t->ggml_type == 1) ? s.nelem * 2 : byte_len(s.dtype, s.nelem);
     s.dev_bytes = byte_len(s.dtype, s.nelem);
     s.off = total;
     total += (s.dev_bytes + 255) & ~size_t(255);
@@ -459,62 +506,66 @@ Model* load_model(const std::string& path, int device) {
   m->blob_bytes = total;
   IEK_HIP(hipMalloc(&m->blob, std::max<size_t>(total, 256)));
 
-  // Stream tensors in file order through a pinned staging buffer.
+  // Stream tensors in file order out of the mapped file through two pinned staging buffers: the
+  // copy of chunk i + 1 into one overlaps the DMA of chunk i from the other.
   std::vector<size_t> order(slots.size());
   for (size_t i = 0; i < order.size(); ++i) order[i] = i;
   std::sort(order.begin(), order.end(), [&](size_t a, size_t b) { return slots[a].meta->offset < slots[b].meta->offset; });
-  FILE* f = fopen(path.c_str(), "rb");
-  if (!f) fail(ST_IO, "cannot open " + path);
+  FileMap fm(path);
   std::vector<std::vector<float>> host_f32(slots.size());
   const size_t CH = 64u << 20;
   void* stage[2] = {nullptr, nullptr};
   hipStream_t st;
   IEK_HIP(hipStreamCreate(&st));
-  IEK_HIP(hipHostMalloc(&stage[0], CH));
-  IEK_HIP(hipHostMalloc(&stage[1], CH));
-  hipEvent_t ev[2];
-  IEK_HIP(hipEventCreate(&ev[0]));
-  IEK_HIP(hipEventCreate(&ev[1]));
+  hipEvent_t ev[2] = {nullptr, nullptr};
   bool ev_used[2] = {false, false};
   int cur = 0;
   auto cleanup = [&]() {
     (void)hipStreamSynchronize(st);
-    (void)hipEventDestroy(ev[0]);
-    (void)hipEventDestroy(ev[1]);
-    (void)hipHostFree(stage[0]);
-    (void)hipHostFree(stage[1]);
+    for (int i = 0; i < 2; ++i) {
+      if (ev[i]) (void)hipEventDestroy(ev[i]);
+      if (stage[i]) (void)hipHostFree(stage[i]);
+    }
     (void)hipStreamDestroy(st);
-    fclose(f);
   };
   try {
+    IEK_HIP(hipHostMalloc(&stage[0], CH));
+    IEK_HIP(hipHostMalloc(&stage[1], CH));
+    IEK_HIP(hipEventCreate(&ev[0]));
+    IEK_HIP(hipEventCreate(&ev[1]));
     for (size_t oi : order) {
       Slot& s = slots[oi];
-      if (fseeko(f, (off_t)(g.data_offset + s.meta->offset), SEEK_SET) != 0) fail(ST_GGUF, "seek failed");
+      const uint8_t* src = fm.at(g.data_offset + s.meta->offset, s.file_bytes);
       bool small_f32 = s.dtype == DT_F32 && s.nelem <= (1u << 20);
-      if (s.meta->ggml_type == 30) {  // BF16 -> F32 widening (tensor_loader.rs:11-16)
-        std::vector<uint16_t> raw(s.nelem);
-        if (s.nelem && fread(raw.data(), 2, s.nelem, f) != s.nelem) fail(ST_IO, "failed to fill whole buffer");
+      const uint32_t gt = s.meta->ggml_type;
+      if (gt == 30 || gt == 1) {  // BF16 (tensor_loader.rs:11-16) or F16 -> F32 widening
         std::vector<float> wide(s.nelem);
         for (size_t e = 0; e < s.nelem; ++e) {
-          uint32_t bits = (uint32_t)raw[e] << 16;
-          memcpy(&wide[e], &bits, 4);
+          uint16_t h;
+          memcpy(&h, src + 2 * e, 2);
+          if (gt == 30) {
+            uint32_t bits = (uint32_t)h << 16;
+            memcpy(&wide[e], &bits, 4);
+          } else {
+            wide[e] = __half2float(__ushort_as_half(h));
+          }
         }
         IEK_HIP(hipMemcpy((char*)m->blob + s.off, wide.data(), s.nelem * 4, hipMemcpyHostToDevice));
         if (small_f32) host_f32[oi] = std::move(wide);
         continue;
       }
+      if (small_f32) {
+        host_f32[oi].resize(s.nelem);
+        memcpy(host_f32[oi].data(), src, s.nelem * 4);
+      }
       size_t done = 0;
       while (done < s.file_bytes) {
         size_t n = std::min(CH, s.file_bytes - done);
         if (ev_used[cur]) IEK_HIP(hipEventSynchronize(ev[cur]));
-        if (fread(stage[cur], 1, n, f) != n) fail(ST_IO, "failed to fill whole buffer");
+        memcpy(stage[cur], src + done, n);
         IEK_HIP(hipMemcpyAsync((char*)m->blob + s.off + done, stage[cur], n, hipMemcpyHostToDevice, st));
         IEK_HIP(hipEventRecord(ev[cur], st));
         ev_used[cur] = true;
-        if (small_f32) {
-          host_f32[oi].resize(s.nelem);
-          memcpy((char*)host_f32[oi].data() + done, stage[cur], n);
-        }
         done += n;
         cur ^= 1;
       }
@@ -524,6 +575,8 @@ Model* load_model(const std::string& path, int device) {
     throw;
   }
   cleanup();
+  m->timings.tensor_load_ms = ms_since(t0);
+  t0 = std::chrono::steady_clock::now();
 
   for (auto& w : wants) {
     const Slot& s = slots[slot_of[w.name]];
@@ -644,6 +697,7 @@ Model* load_model(const std::string& path, int device) {
     }
     L.rope_table = found;
   }
+  m->timings.weights_build_ms = ms_since(t0);
   return m.release();
 }
 

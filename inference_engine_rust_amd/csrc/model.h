@@ -106,8 +106,17 @@ struct RopeTable {
   float* dev;  // [ctx][rotary_dim/2][2] (cos, sin)
 };
 
+// Wall times of the load stages, named after the cold-start regions of src/bench_metrics.rs:199-296.
+struct LoadTimings {
+  double gguf_metadata_ms = 0;        // header, KV table and tensor table
+  double config_and_resolve_ms = 0;   // ModelConfig + tensor-name resolution
+  double tensor_load_ms = 0;          // tensor bytes from the mapped file into HBM
+  double weights_build_ms = 0;        // regrouped matvec copies, shape checks, RoPE tables
+};
+
 struct Model {
   int device = 0;
+  LoadTimings timings;
   Config cfg;
   std::string path;
   void* blob = nullptr;  // one HBM allocation for every weight

@@ -135,6 +135,8 @@ void Session::reset() {
   pos_ = 0;
   state_rows_ = 0;
   state_prefill_ = false;
+  state_ple_ = false;
+  layer_cursor_ = 0;
   sync();
 }
 
@@ -917,6 +919,100 @@ void Session::prefill(const uint32_t* ids, int n) {
   launch_set_int(d_pos_, pos_, st_);
   state_rows_ = n;
   state_prefill_ = true;
+  state_ple_ = gemma_ && c.ple_dim > 0;
+  layer_cursor_ = 0;
+  sync();
+}
+
+// ---- forward-level steps -------------------------------------------------------------------------
+
+void Session::embed(const uint32_t* ids, int n) {
+  const Config& c = m_->cfg;
+  if (n <= 0) fail(ST_MODEL, "prefill: empty token list");
+  if (n > c.context_length)
+    fail(ST_MODEL, "prefill: token length " + std::to_string(n) + " exceeds context length " +
+                       std::to_string(c.context_length));
+  size_t vocab;
+  size_t hid = embedding_hidden(m_->token_embd, &vocab);
+  for (int i = 0; i < n; ++i)
+    if ((size_t)ids[i] >= vocab)
+      fail(ST_MODEL, "token ID " + std::to_string(ids[i]) + " out of vocabulary range [0, " + std::to_string(vocab) + ")");
+  if ((int)hid != H_) fail(ST_MODEL, "ForwardState: embedding dim mismatch");
+  ensure_rows(n);
+  IEK_HIP(hipMemcpyAsync(d_ids_, ids, (size_t)n * 4, hipMemcpyHostToDevice, st_));
+  launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, d_ids_, n, c.embed_scale, x_, st_);
+  if (gemma_) embed_ple(d_ids_, n, x_, split_rows(x_, n, H_), ple_tok_, ple_proj_, ple_pack_);
+  launch_copy_f32(x_ + (size_t)(n - 1) * H_, xdec_, H_, st_);  // the last row, read by the LM head
+  state_rows_ = n;
+  state_prefill_ = true;
+  state_ple_ = gemma_ && c.ple_dim > 0;
+  layer_cursor_ = 0;
+  sync();
+}
+
+void Session::set_hidden(const float* rows, int n) {
+  if (n <= 0) fail(ST_MODEL, "ForwardState: empty input");
+  ensure_rows(n);
+  IEK_HIP(hipMemcpyAsync(x_, rows, (size_t)n * H_ * 4, hipMemcpyHostToDevice, st_));
+  launch_copy_f32(x_ + (size_t)(n - 1) * H_, xdec_, H_, st_);
+  state_rows_ = n;
+  state_prefill_ = true;
+  state_ple_ = false;
+  layer_cursor_ = 0;
+  sync();
+}
+
+void Session::prefill_layer(int li) {
+  const Config& c = m_->cfg;
+  if (li < 0 || li >= c.n_layers) fail(ST_MODEL, "layer index out of range");
+  if (li != layer_cursor_)
+    fail(ST_MODEL, "layer-level forward: expected layer " + std::to_string(layer_cursor_) + ", got " +
+                       std::to_string(li));
+  if (!state_prefill_ || state_rows_ <= 0) fail(ST_MODEL, "prefill_layer_block: no prompt state");
+  if (gemma_ && c.ple_dim > 0 && !state_ple_) fail(ST_MODEL, "PLE: per-layer inputs missing from the state");
+  const int M = state_rows_;
+  if (pos_ + M > ctx_) fail(ST_KVCACHE, "KVCache is Full: max len is " + std::to_string(ctx_) + ".");
+  if (gemma_) layer_prefill_gemma(li, M);
+  else layer_prefill(li, M);
+  launch_copy_f32(x_ + (size_t)(M - 1) * H_, xdec_, H_, st_);
+  if (++layer_cursor_ == c.n_layers) {
+    pos_ += M;
+    launch_set_int(d_pos_, pos_, st_);
+    layer_cursor_ = 0;
+  }
+  sync();
+}
+
+void Session::decode_layer(int li) {
+  const Config& c = m_->cfg;
+  if (li < 0 || li >= c.n_layers) fail(ST_MODEL, "layer index out of range");
+  if (li != layer_cursor_)
+    fail(ST_MODEL, "layer-level forward: expected layer " + std::to_string(layer_cursor_) + ", got " +
+                       std::to_string(li));
+  if (state_rows_ != 1) fail(ST_MODEL, "decode_layer_block: seq_len must be 1");
+  if (pos_ >= ctx_) fail(ST_KVCACHE, "KVCache is Full: max len is " + std::to_string(ctx_) + ".");
+  if (gemma_ && c.ple_dim > 0 && !state_ple_) fail(ST_MODEL, "PLE: per-layer inputs missing from the state");
+  if (li == 0 && state_prefill_) {
+    // a one-row prompt state becomes the decode state (and its per-layer inputs the decode ones)
+    launch_copy_f32(x_, xdec_, H_, st_);
+    if (state_ple_) launch_copy_f32(ple_pack_, ple_packd_, (size_t)c.n_layers * c.ple_dim, st_);
+    state_prefill_ = false;
+  }
+  const bool last = li == c.n_layers - 1;
+  if (gemma_) {
+    float* xr = xdec_;
+    ResidUpdate pend{};
+    layer_decode_gemma(li, xr, pend);
+    if (pend.t) launch_rmsnorm_add(xr, pend.t, pend.w, 1, H_, c.rms_eps, pend.has_scale, pend.scale, st_, xdec_);
+    else if (xr != xdec_) launch_copy_f32(xr, xdec_, H_, st_);
+    if (last) launch_add_int(d_pos_, 1, st_);
+  } else {
+    layer_decode(li, last);
+  }
+  if (++layer_cursor_ == c.n_layers) {
+    pos_ += 1;
+    layer_cursor_ = 0;
+  }
   sync();
 }
 
@@ -989,17 +1085,28 @@ void Session::decode_token(uint32_t id) {
   if ((size_t)id >= vocab)
     fail(ST_MODEL, "token ID " + std::to_string(id) + " out of vocabulary range [0, " + std::to_string(vocab) + ")");
   if (pos_ >= ctx_) fail(ST_KVCACHE, "KVCache is Full: max len is " + std::to_string(ctx_) + ".");
+  check_no_layer_forward();
   IEK_HIP(hipMemcpyAsync(d_tok_, &id, 4, hipMemcpyHostToDevice, st_));
   decode_body();
   pos_ += 1;
   state_rows_ = 1;
   state_prefill_ = false;
+  state_ple_ = gemma_ && m_->cfg.ple_dim > 0;
+  layer_cursor_ = 0;
   sync();
   check_chain_error();
 }
 
 void Session::check_state() const {
   if (state_rows_ == 0) fail(ST_MODEL, "final_logits_last_token: empty input");
+  check_no_layer_forward();
+}
+
+// Session-level calls need every layer of the state done: a layer-level forward stopped part way
+// has appended its rows to the KV caches of some layers only.
+void Session::check_no_layer_forward() const {
+  if (layer_cursor_ != 0)
+    fail(ST_MODEL, "a layer-level forward is in progress (next layer " + std::to_string(layer_cursor_) + ")");
 }
 
 // Final RMSNorm (last row) + LM head (+ soft cap). With `argmax`, the LM-head epilogue also folds

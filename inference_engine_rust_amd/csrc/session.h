@@ -31,6 +31,17 @@ class Session {
   // replayed as one captured decode-step graph. Returns the n chosen ids.
   void generate_greedy(int n, uint32_t* out_ids, bool use_graph = true);
 
+  // Forward-level steps over the session's ForwardState (src/engine/runtime.rs:14-61,
+  // src/layers/block.rs:12-89, src/engine/embed.rs:53-149). Layers run in order: the next call
+  // must be for layer `next_layer()`; after the last layer the KV length grows by the state rows.
+  void embed(const uint32_t* ids, int n);           // prefill_from_tokens_loaded: state = embeddings
+  void set_hidden(const float* rows, int n);        // ForwardState::from_flat (no PLE payload)
+  void prefill_layer(int li);                       // prefill_layer_block
+  void decode_layer(int li);                        // decode_layer_block (one-row state)
+  int next_layer() const { return layer_cursor_; }
+  int n_layers() const { return m_->cfg.n_layers; }
+  void check_no_layer_forward() const;  // IEK_ERR_MODEL while a layer-level forward is part way
+
   int kv_len() const { return pos_; }
   int decode_path() const { return chain_ ? 1 : 0; }
   int state_rows() const { return state_rows_; }
@@ -100,6 +111,8 @@ class Session {
   int pos_ = 0;
   int state_rows_ = 0;  // rows of the last ForwardState (0 = none)
   bool state_prefill_ = false;
+  bool state_ple_ = false;   // the state carries its per-layer-embedding payload (Gemma-4)
+  int layer_cursor_ = 0;     // next layer of a layer-level forward
   // decode chain path (kernels/chain.hip): device ChainPhase arrays per launch; launch 0 holds
   // layer 0's Q/K/V, launch l + 1 layer l's O, gate/up, down and layer l + 1's Q/K/V; the last
   // layer's launch comes in two forms, without and with the LM head + argmax

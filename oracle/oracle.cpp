@@ -1209,6 +1209,32 @@ static std::vector<float> prefill_attention(Session& s, const float* input, size
 }
 
 // decode_attention_layer (attention.rs:462-655)
+// The head loop of decode_attention_layer (attention.rs:608-650): per query head h (KV head
+// h / group), scores q.K[j] * scale for j in [j_min, total) and -inf below j_min, the reference
+// softmax over all `total` scores, then out[h] = sum_j w[j] V[j] accumulated in j order.
+static void decode_heads(const float* q, const KVCache& src, size_t n_heads, size_t total, size_t j_min, float scale,
+                         float* out, int threads) {
+  const size_t hd = src.head_dim, group = n_heads / src.n_kv_heads;
+  parallel_for(n_heads, threads, [&](size_t h) {
+    size_t kvh = h / group;
+    const float* qv = &q[h * hd];
+    std::vector<float> sc(total, -INFINITY), wts(total, 0.0f);
+    for (size_t j = j_min; j < total; ++j) {
+      const float* kk = kslice(src, j, kvh);
+      float dot = 0.0f;
+      for (size_t e = 0; e < hd; ++e) dot += qv[e] * kk[e];
+      sc[j] = dot * scale;
+    }
+    softmax(sc.data(), wts.data(), total);
+    float* o = &out[h * hd];
+    for (size_t j = j_min; j < total; ++j) {
+      float wt = wts[j];
+      const float* vv = vslice(src, j, kvh);
+      for (size_t e = 0; e < hd; ++e) o[e] += wt * vv[e];
+    }
+  });
+}
+
 static std::vector<float> decode_attention(Session& s, const float* input, size_t li) {
   const Model& m = *s.model;
   const ModelConfig& c = m.cfg;
@@ -1228,7 +1254,6 @@ static std::vector<float> decode_attention(Session& s, const float* input, size_
   } else {
     rope_pos = (uint32_t)own.current_pos;
   }
-  size_t group = c.n_heads / c.n_kv_heads;
   std::vector<float> q(qd), k(kvd, 0.0f), v(kvd, 0.0f);
   matmul(input, 1, c.hidden_dim, *w.wq, q.data(), 1, qd, s.mode, s.threads);
   if (borrow < 0) {
@@ -1258,24 +1283,7 @@ static std::vector<float> decode_attention(Session& s, const float* input, size_
   if (la.sliding_window >= 0) j_min = total > (size_t)la.sliding_window ? total - (size_t)la.sliding_window : 0;
   float scale = c.family == GEMMA4 ? 1.0f : 1.0f / sqrtf((float)hd);
   std::vector<float> out(qd, 0.0f);
-  parallel_for(c.n_heads, s.threads, [&](size_t h) {
-    size_t kvh = h / group;
-    const float* qv = &q[h * hd];
-    std::vector<float> sc(total, -INFINITY), wts(total, 0.0f);
-    for (size_t j = j_min; j < total; ++j) {
-      const float* kk = kslice(src, j, kvh);
-      float dot = 0.0f;
-      for (size_t e = 0; e < hd; ++e) dot += qv[e] * kk[e];
-      sc[j] = dot * scale;
-    }
-    softmax(sc.data(), wts.data(), total);
-    float* o = &out[h * hd];
-    for (size_t j = j_min; j < total; ++j) {
-      float wt = wts[j];
-      const float* vv = vslice(src, j, kvh);
-      for (size_t e = 0; e < hd; ++e) o[e] += wt * vv[e];
-    }
-  });
+  decode_heads(q.data(), src, c.n_heads, total, j_min, scale, out.data(), s.threads);
   std::vector<float> proj(c.hidden_dim);
   matmul(out.data(), 1, qd, *w.wo, proj.data(), 1, c.hidden_dim, s.mode, s.threads);
   return proj;
@@ -1496,6 +1504,24 @@ float orc_gelu_tanh(float x) { return gelu_tanh(x); }
 int orc_residual_add(const float* a, const float* b, float* out, size_t n) { ORC_TRY(residual_add(a, b, out, n)) }
 long orc_argmax(const float* l, size_t n) { return argmax(l, n); }
 int orc_unpack_qk_row(float* row, size_t ng, size_t hd) { ORC_TRY(unpack_qk_row(row, ng, hd)) }
+// decode_heads over a KVCache holding `total` positions ([total][n_kv][head_dim] k and v);
+// sliding_window < 0 = none.
+int orc_attention_decode(const float* q, const float* k, const float* v, size_t n_heads, size_t n_kv, size_t hd,
+                         size_t total, long sliding_window, float scale, float* out) {
+  ORC_TRY({
+    if (n_kv == 0 || n_heads % n_kv != 0) fail(E_MODEL, "attention: n_heads % n_kv_heads != 0");
+    KVCache kv;
+    kv.n_kv_heads = n_kv;
+    kv.head_dim = hd;
+    kv.max_seq_len = kv.current_pos = total;
+    kv.k.assign(k, k + total * n_kv * hd);
+    kv.v.assign(v, v + total * n_kv * hd);
+    size_t j_min = 0;
+    if (sliding_window >= 0) j_min = total > (size_t)sliding_window ? total - (size_t)sliding_window : 0;
+    std::fill(out, out + n_heads * hd, 0.0f);
+    decode_heads(q, kv, n_heads, total, j_min, scale, out, 1);
+  })
+}
 
 // ---- model / session ----
 struct orc_cfg {

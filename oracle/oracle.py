@@ -62,6 +62,8 @@ def lib():
         L.orc_argmax.argtypes = [_f, ctypes.c_size_t]
         L.orc_argmax.restype = ctypes.c_long
         L.orc_unpack_qk_row.argtypes = [_f, ctypes.c_size_t, ctypes.c_size_t]
+        L.orc_attention_decode.argtypes = [_f, _f, _f, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
+                                           ctypes.c_size_t, ctypes.c_long, ctypes.c_float, _f]
         L.orc_model_load.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)]
         L.orc_model_free.argtypes = [_f]
         L.orc_model_config.argtypes = [_f, ctypes.POINTER(Cfg)]
@@ -188,6 +190,18 @@ def unpack_qk_row(row, n_groups, head_dim):
     r = np.array(row, np.float32)
     _check(lib().orc_unpack_qk_row(_p(r), n_groups, head_dim))
     return r
+
+
+def attention_decode(q, k, v, n_heads, n_kv, head_dim, total, sliding_window, scale):
+    """Head loop of decode_attention_layer (attention.rs:608-650) over a KVCache of `total`
+    positions, k and v as [total][n_kv][head_dim]; sliding_window < 0 = none."""
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    out = np.empty(n_heads * head_dim, np.float32)
+    _check(lib().orc_attention_decode(_p(q), _p(k), _p(v), n_heads, n_kv, head_dim, total, sliding_window, scale,
+                                      _p(out)))
+    return out
 
 
 class Model:

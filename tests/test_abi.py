@@ -19,7 +19,9 @@ def _declared():
 def test_header_declares_entry_points():
     names = _declared()
     for n in ["iek_model_load", "iek_session_prefill", "iek_session_decode_token", "iek_session_logits_last_token",
-              "iek_greedy_next_token", "iek_matmul", "iek_dequantize"]:
+              "iek_greedy_next_token", "iek_matmul", "iek_dequantize", "iek_attention_decode",
+              "iek_session_prefill_forward", "iek_session_decode_forward", "iek_session_prefill_layer_block",
+              "iek_session_decode_layer_block", "iek_dev_matmul", "iek_dev_attention_decode"]:
         assert n in names
 
 

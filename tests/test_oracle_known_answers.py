@@ -277,3 +277,62 @@ def test_matmul_sequential_order_bitwise():
                 acc = np.float32(acc + np.float32(a[i, kk] * W[j, kk]))
             want[i, j] = acc
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# ---- decode attention head loop (attention.rs:608-650) ------------------------------------------
+
+def _attn_f64(q, k, v, n_heads, n_kv, hd, total, window, scale):
+    """Textbook softmax attention in float64 over [total][n_kv][hd] caches."""
+    q = q.reshape(n_heads, hd).astype(np.float64)
+    k = k.reshape(total, n_kv, hd).astype(np.float64)
+    v = v.reshape(total, n_kv, hd).astype(np.float64)
+    j0 = total - window if 0 <= window < total else 0
+    out = np.zeros((n_heads, hd))
+    g = n_heads // n_kv
+    for h in range(n_heads):
+        s = k[j0:, h // g, :] @ q[h] * scale
+        w = np.exp(s - s.max())
+        out[h] = (w / w.sum()) @ v[j0:, h // g, :]
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hd,total,window", [(8, 2, 64, 37, -1), (8, 8, 32, 5, -1),
+                                                          (6, 1, 16, 40, 7), (4, 2, 128, 300, 299)])
+def test_attention_decode_matches_float64_softmax(n_heads, n_kv, hd, total, window):
+    rng = np.random.default_rng(total)
+    q = rng.standard_normal(n_heads * hd).astype(np.float32)
+    k = rng.standard_normal(total * n_kv * hd).astype(np.float32)
+    v = rng.standard_normal(total * n_kv * hd).astype(np.float32)
+    scale = 1.0 / math.sqrt(hd)
+    got = O.attention_decode(q, k, v, n_heads, n_kv, hd, total, window, scale)
+    want = _attn_f64(q, k, v, n_heads, n_kv, hd, total, window, scale)
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5)
+
+
+def test_attention_decode_closed_forms():
+    n_heads, n_kv, hd, total = 8, 2, 16, 9
+    rng = np.random.default_rng(3)
+    # V constant per (position, KV head): head h must read KV head h // 4
+    v = np.zeros((total, n_kv, hd), np.float32)
+    for j in range(total):
+        for kv in range(n_kv):
+            v[j, kv, :] = 100 * kv + j
+    k = rng.standard_normal((total, n_kv, hd)).astype(np.float32)
+    # q = 0: uniform weights -> the mean of the live positions' V
+    out = O.attention_decode(np.zeros(n_heads * hd), k, v, n_heads, n_kv, hd, total, -1, 1.0).reshape(n_heads, hd)
+    for h in range(n_heads):
+        np.testing.assert_allclose(out[h], 100 * (h // 4) + (total - 1) / 2.0, rtol=1e-6)
+    # window 3 keeps positions 6, 7, 8 only
+    out = O.attention_decode(np.zeros(n_heads * hd), k, v, n_heads, n_kv, hd, total, 3, 1.0).reshape(n_heads, hd)
+    np.testing.assert_allclose(out[5], 100 * 1 + 7.0, rtol=1e-6)
+    # one live position (window 1): the output is exactly that position's V
+    q = rng.standard_normal(n_heads * hd).astype(np.float32)
+    out = O.attention_decode(q, k, v, n_heads, n_kv, hd, total, 1, 0.5).reshape(n_heads, hd)
+    assert np.array_equal(out[0], v[total - 1, 0]) and np.array_equal(out[7], v[total - 1, 1])
+    # a dominant key takes all the weight
+    q1 = np.zeros(n_heads * hd, np.float32)
+    q1[:hd] = 1.0
+    k2 = np.zeros((total, n_kv, hd), np.float32)
+    k2[4, 0, :] = 50.0
+    out = O.attention_decode(q1, k2, v, n_heads, n_kv, hd, total, -1, 1.0).reshape(n_heads, hd)
+    np.testing.assert_allclose(out[0], 4.0, rtol=1e-6)
