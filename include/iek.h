@@ -214,6 +214,18 @@ iek_status iek_dev_argmax(const float* logits, size_t n, uint32_t* out_index, vo
 iek_status iek_dev_attention_decode(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
                                     size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t max_seq_len,
                                     size_t total_pos, size_t sliding_window, float scale, float* out, void* stream);
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): iek_dev_attention_decode
+ * with the same arguments, results and errors, but its partials, arrival counters and position live
+ * in a 16 MiB scratch array the library holds per device until the process ends; it calls no
+ * allocator and does not wait for the stream. Limit: n_heads * ceil(max_seq_len / 64) *
+ * (head_dim + 2) * 4 bytes <= 16 MiB - 4 KiB (e.g. 32 heads of 128 up to 32K keys), IEK_ERR_OP
+ * beyond. Every call on a device shares that device's scratch: calls that overlap on one GPU (two
+ * streams, or two threads) race and must be ordered by the caller. */
+iek_status iek_dev_attention_decode_noalloc(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
+                                            size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t max_seq_len,
+                                            size_t total_pos, size_t sliding_window, float scale, float* out,
+                                            void* stream);
 
 /* ---- device memory helpers for FFI callers without a HIP binding ---------------------------- */
 iek_status iek_device_alloc(size_t bytes, void** out);

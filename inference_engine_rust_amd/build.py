@@ -43,6 +43,7 @@ SOURCES = [
     "kernels/gemm_q.hip",
     "kernels/gemma.hip",
     "kernels/chain.hip",
+    "kernels/noalloc.hip",
     "model.cpp",
     "session.cpp",
     "api.cpp",

@@ -419,6 +419,27 @@ iek_status iek_dev_attention_decode(const float* q, const void* k_cache, const v
   })
 }
 
+iek_status iek_dev_attention_decode_noalloc(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
+                                            size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t max_seq_len,
+                                            size_t total_pos, size_t sliding_window, float scale, float* out,
+                                            void* stream) {
+  IEK_API_TRY({
+    if (kv_dtype != IEK_F16 && kv_dtype != IEK_F32) fail(ST_OP, "attention: KV cache dtype must be F16 or F32");
+    const size_t pf = attention_check(n_heads, n_kv_heads, head_dim, max_seq_len, total_pos);
+    const size_t part_cap = NOALLOC_SCRATCH_BYTES - NOALLOC_COUNTER_BYTES;
+    if (pf * 4 > part_cap)
+      fail(ST_OP, "attention (no-alloc): partials of " + std::to_string(pf * 4) + " bytes exceed the " +
+                      std::to_string(part_cap) + "-byte scratch (n_heads * ceil(max_seq_len / 64) * (head_dim + 2) "
+                      "floats); use iek_dev_attention_decode");
+    if ((2 * n_kv_heads + 1) * 4 > NOALLOC_COUNTER_BYTES) fail(ST_OP, "attention (no-alloc): too many KV heads");
+    char* base = static_cast<char*>(noalloc_scratch());
+    int* cnt = reinterpret_cast<int*>(base);
+    float* part = reinterpret_cast<float*>(base + NOALLOC_COUNTER_BYTES);
+    attention_launch(q, k_cache, v_cache, kv_dtype == IEK_F32, n_heads, n_kv_heads, head_dim, max_seq_len, total_pos,
+                     sliding_window, scale, out, part, cnt, cnt + 2 * n_kv_heads, as_stream(stream));
+  })
+}
+
 }  // extern "C"
 
 // ---- op level, host buffers (synchronous) ----

@@ -112,6 +112,12 @@ void launch_attn_decode(const float* q, const void* kc, const void* vc, bool kv_
                         float scale, int max_len, hipStream_t st);
 // Floats of `part` that launch_attn_decode needs at most for a cache of max_len keys.
 size_t attn_decode_part_floats(int n_heads, int head_dim, int max_len);
+// The no-allocation scratch (kernels/noalloc.hip): a file-scope device array of this many bytes
+// per device, [counters + position: NOALLOC_COUNTER_BYTES][attention partials: the rest].
+constexpr size_t NOALLOC_SCRATCH_BYTES = 16u << 20;
+constexpr size_t NOALLOC_COUNTER_BYTES = 4096;
+// Device address of the current device's scratch array (resolved once per device).
+void* noalloc_scratch();
 // With a scratch buffer of attn_prefill_scratch_halves() halves (head_dim 64 or 128), each K/V block
 // is staged once for all the query heads of its KV head; otherwise one workgroup per query head.
 size_t attn_prefill_scratch_halves(int M, int n_kv, int head_dim);

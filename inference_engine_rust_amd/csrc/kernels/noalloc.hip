@@ -1,0 +1,32 @@
+// Device scratch for the no-allocation decode attention entry point: one file-scope array per
+// device, resolved to its device address once per device with hipGetSymbolAddress. The host-side
+// name `scratch` is not a device address; only the resolved pointer is passed to kernels.
+#include <mutex>
+
+#include "../iek_internal.h"
+
+namespace iek {
+
+static __device__ __align__(256) char scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_mu;
+void* g_ptr[kMaxDevices] = {};
+}  // namespace
+
+void* noalloc_scratch() {
+  int dev = 0;
+  IEK_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) fail(ST_DEVICE, "device index out of range");
+  std::lock_guard<std::mutex> lock(g_mu);
+  if (!g_ptr[dev]) {
+    void* p = nullptr;
+    IEK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) fail(ST_DEVICE, "hipGetSymbolAddress returned a null scratch address");
+    g_ptr[dev] = p;
+  }
+  return g_ptr[dev];
+}
+
+}  // namespace iek

@@ -109,6 +109,8 @@ EXPORTS = {
     "iek_dev_argmax": ([_P, _SZ, ctypes.POINTER(ctypes.c_uint32), _P], ctypes.c_int),
     "iek_dev_attention_decode": ([_P, _P, _P, ctypes.c_int, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P, _P],
                                  ctypes.c_int),
+    "iek_dev_attention_decode_noalloc": ([_P, _P, _P, ctypes.c_int, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P,
+                                          _P], ctypes.c_int),
     "iek_device_alloc": ([_SZ, ctypes.POINTER(_P)], ctypes.c_int),
     "iek_device_free": ([_P], ctypes.c_int),
     "iek_memcpy_h2d": ([_P, _P, _SZ], ctypes.c_int),
@@ -442,6 +444,15 @@ def attention_decode(q_ptr: int, k_ptr: int, v_ptr: int, kv_dtype: int, n_heads:
     """Decode attention over a [n_kv_heads][max_seq_len][head_dim] cache (F16 = 4 or F32 = 0)."""
     _check(lib().iek_dev_attention_decode(q_ptr, k_ptr, v_ptr, kv_dtype, n_heads, n_kv_heads, head_dim, max_seq_len,
                                           total_pos, sliding_window, scale, out_ptr, stream or None))
+
+
+def attention_decode_noalloc(q_ptr: int, k_ptr: int, v_ptr: int, kv_dtype: int, n_heads: int, n_kv_heads: int,
+                             head_dim: int, max_seq_len: int, total_pos: int, sliding_window: int, scale: float,
+                             out_ptr: int, stream: int = 0) -> None:
+    """attention_decode without any device allocation (the library's per-device scratch)."""
+    _check(lib().iek_dev_attention_decode_noalloc(q_ptr, k_ptr, v_ptr, kv_dtype, n_heads, n_kv_heads, head_dim,
+                                                  max_seq_len, total_pos, sliding_window, scale, out_ptr,
+                                                  stream or None))
 
 
 def synchronize() -> None:
