@@ -53,7 +53,7 @@ def weight_bytes_per_token(model, cfg, specs):
 def kv_bytes_per_token(cfg, specs, ctx_len):
     """KV bytes one decode step reads (keys/values visible to each layer at context length
     ctx_len, borrowed caches included) and writes (one row per layer that owns a cache)."""
-    esz = 4 if int(cfg.family) == 1 else 2  # Gemma-4 sessions keep an f32 cache
+    esz = 4  # the sessions keep the reference's f32 cache
     rd = wr = 0
     for sp in specs:
         row = 2 * cfg.n_kv_heads * sp["head_dim"] * esz
@@ -84,7 +84,10 @@ def prefill_flops(cfg, specs, prompt):
     return lin_flops + attn + 2.0 * H * cfg.vocab_size
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "c2_matvec_traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "c2_chain_traffic.json")
+MFMA_PEAK_TFLOPS = 2500.0  # dense fp16/bf16 MFMA
+GOLDEN_TOKENS = os.path.join(ROOT, "tests", "golden", "c2_seed0_tokens.json")
+GAP_EXACT = 1e-2
 
 
 def measured_traffic(algo_bytes):
@@ -96,87 +99,130 @@ def measured_traffic(algo_bytes):
             t = json.load(f)
     except (OSError, ValueError):
         return None
-    if t.get("algorithmic_bytes") != algo_bytes:
+    if abs(t.get("algorithmic_bytes", -1) - algo_bytes) > 1:
         return None
     return int(round(t["fetch_bytes"] + t["write_bytes"]))
-
-
-def probe_traffic(E, model, cfg, reps):
-    """Launches only what the --pmc runs count: one plain copy of COPY_BYTES (torch's copy
-    kernel), then `reps` roofline-kernel launches rotating over the gate/up tensors."""
-    import torch
-
-    n = COPY_BYTES // 4
-    a = torch.ones(n, device="cuda", dtype=torch.float32)
-    b = torch.empty_like(a)
-    torch.cuda.synchronize()
-    b.copy_(a)
-    torch.cuda.synchronize()
-    kernel_roofline(E, model, cfg, reps)
-    torch.cuda.synchronize()
 
 
 COPY_BYTES = 256 << 20
 
 
-def kernel_roofline(E, model, cfg, reps):
-    """Average duration of the decode matvec on the FFN gate/up weights (Q4_K, 14336x4096, the
-    largest weight class), launched on torch's current stream between HIP events and rotating over
-    all 2*n_layers tensors so every launch streams from HBM rather than the 256 MB MALL."""
+def probe_traffic(E, model, cfg, prompt, reps):
+    """Launches only what the --pmc runs count (besides the prefill that gives the chain a state):
+    one plain copy of COPY_BYTES (torch's copy kernel), then `reps` decode chain launches."""
     import torch
 
-    names = [f"blk.{li}.ffn_{w}.weight" for li in range(cfg.n_layers) for w in ("gate", "up")]
-    ts = [model.tensor(n) for n in names]
-    K, N = int(ts[0]["ne0"]), int(ts[0]["ne1"])
-    x = torch.randn(K, device="cuda", dtype=torch.float32)
-    y = torch.empty(N, device="cuda", dtype=torch.float32)
-    st = torch.cuda.current_stream()
-    sid = st.cuda_stream
-    for t in ts[:4]:
-        E.matmul(x.data_ptr(), 1, K, t["dtype"], t["ptr"], t["bytes"], N, y.data_ptr(), sid)
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n = COPY_BYTES // 4
+    a = torch.ones(n, device="cuda", dtype=torch.float32)
+    b = torch.empty_like(a)
+    sess = E.InferenceSession(model)
+    sess.prefill(prompt)
     torch.cuda.synchronize()
-    ev0.record(st)
-    for i in range(reps):
-        t = ts[i % len(ts)]
-        E.matmul(x.data_ptr(), 1, K, t["dtype"], t["ptr"], t["bytes"], N, y.data_ptr(), sid)
-    ev1.record(st)
-    ev1.synchronize()
-    avg_ms = ev0.elapsed_time(ev1) / reps
-    algo = ts[0]["bytes"] + 4 * (K + N)
-    gbs = algo / (avg_ms * 1e-3) / 1e9
-    return {"kernel": "mv_stream<Q4Tr,2,false,true,256,4> (decode matvec, Q4_K 14336x4096, f32 activations)", "bound": "hbm", "achieved": round(gbs, 1),
+    b.copy_(a)
+    torch.cuda.synchronize()
+    sess.bench_kernel(0, reps)
+    torch.cuda.synchronize()
+
+
+def kernel_roofline(E, model, prompt, reps):
+    """The decode step's dominant kernel: the chain launch (layer k-1's O projection + residual,
+    RMSNorm + gate/up + SwiGLU, down + residual, then layer k's RMSNorm + Q/K/V + RoPE + KV
+    append), 31 of the step's 33 launches. Timed on the session's stream between HIP events over
+    `reps` launches rotating over the layer pairs (each launch streams its own ~138 MB of weights
+    from HBM). Algorithmic bytes = the phases' weight bytes + their f32 activation vectors."""
+    sess = E.InferenceSession(model)
+    sess.prefill(prompt)
+    us, algo = sess.bench_kernel(0, reps)
+    gbs = algo / (us * 1e-6) / 1e9
+    return {"kernel": "chain_kernel (decode chain launch: O, gate/up, down of layer k-1 + Q/K/V of layer k, "
+                      "Q4_K/Q6_K weights, f32 activations)", "bound": "hbm", "achieved": round(gbs, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(algo),
-            "algorithmic_bytes_per_launch": algo, "avg_launch_us": round(avg_ms * 1e3, 3), "launches": reps}
+            "traffic": measured_traffic(int(algo)),
+            "algorithmic_bytes_per_launch": int(algo), "avg_launch_us": round(us, 3), "launches": reps}
 
 
-def cpu_baseline(path, n_layers_sample):
+def prefill_roofline(E, model, prompt, reps):
+    """The prefill's largest GEMM: gate/up over the prompt rows (M x 4096 x 2*14336, K-quant
+    weights dequantised into LDS, v_mfma_f32_16x16x32_f16), timed like kernel_roofline over
+    `reps` launches rotating over the layers. Algorithmic flops = 2*M*K*N, against the dense
+    fp16/bf16 MFMA peak."""
+    sess = E.InferenceSession(model)
+    sess.prefill(prompt)
+    us, flops = sess.bench_kernel(1, reps)
+    tf = flops / (us * 1e-6) / 1e12
+    return {"kernel": f"gemm_kq gate/up (M={len(prompt)}, Q4_K, fp16 hi/lo activation pair, 2 MFMA per product)",
+            "bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / MFMA_PEAK_TFLOPS, 4), "algorithmic_flops_per_launch": int(flops),
+            "avg_launch_us": round(us, 3), "launches": reps}
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(path, n_layers_sample, prompt):
     """The oracle (C++ restatement of the reference CPU path) in baseline mode — the reference's
-    own Rayon decomposition — on a bounded sample of the same model: one greedy step (LM head +
-    argmax + decode) through the first `n_layers_sample` blocks from an empty cache, scaled to a
-    full-depth token."""
+    own Rayon decomposition, with T = every host core — on bounded samples of the same model:
+    * decode: one greedy step (decode + LM head + argmax) through the first `n_layers_sample`
+      blocks from an empty cache, scaled to a full-depth token;
+    * TTFT: the prompt's prefill through one block, scaled to every block, plus the LM head and
+      argmax of the last row."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
 
-    threads = min(16, os.cpu_count() or 1)
+    threads = os.cpu_count() or 1
     m = O.Model(path)
+    nl = int(m.cfg.n_layers)
     s = O.Session(m, O.BASELINE, threads)
     s.set_layer_limit(n_layers_sample)
     t0 = time.perf_counter()
     s.decode(1)
     t_layers = time.perf_counter() - t0
     t0 = time.perf_counter()
-    lg = s.logits()
-    O.argmax(lg)
+    O.argmax(s.logits())
     t_head = time.perf_counter() - t0
-    nl = int(m.cfg.n_layers)
     per_tok = t_head + t_layers * nl / n_layers_sample
+    s = O.Session(m, O.BASELINE, threads)
+    s.set_layer_limit(1)
+    t0 = time.perf_counter()
+    s.prefill(prompt)
+    t_pf = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    O.argmax(s.logits())
+    t_pf_head = time.perf_counter() - t0
+    ttft_s = t_pf * nl + t_pf_head
     return {"value": round(1.0 / per_tok, 5), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": (f"C++ restatement of the reference Rayon path (decode matvecs single-threaded as in "
-                       f"matmul.rs:206-216, attention over {threads} threads): one greedy step through "
-                       f"{n_layers_sample}/{nl} blocks + LM head, empty KV cache; per-token "
-                       f"{per_tok:.2f} s = head {t_head:.2f} s + blocks {t_layers:.2f} s x {nl}/{n_layers_sample}")}
+            "cpu": cpu_model(), "ttft_ms": round(ttft_s * 1e3, 1),
+            "sample": (f"C++ restatement of the reference Rayon path on {threads} threads ({cpu_model()}): decode = "
+                       f"one greedy step through {n_layers_sample}/{nl} blocks + LM head, empty KV cache, per-token "
+                       f"{per_tok:.2f} s = head {t_head:.2f} s + blocks {t_layers:.2f} s x {nl}/{n_layers_sample}; "
+                       f"TTFT = {len(prompt)}-token prefill through 1/{nl} blocks ({t_pf:.2f} s) x {nl} + LM head "
+                       f"{t_pf_head:.2f} s")}
+
+
+def golden_tokens_match(E, sess, prompt, cfg_name):
+    """The first greedy tokens of the C2 model against the committed oracle run (tests/golden/
+    c2_seed0_tokens.json, same model and prompt): equal wherever the oracle's two best logits are
+    at least GAP_EXACT apart; at a closer step either of the two ends the comparison."""
+    if cfg_name != "c2" or len(prompt) != 512:
+        return None
+    with open(GOLDEN_TOKENS) as f:
+        g = json.load(f)
+    sess.reset()
+    sess.prefill(prompt)
+    for t, t2, gap in zip(g["tokens"], g["runner_up"], g["top2_gap"]):
+        got = E.greedy_next_token(sess)
+        if got != t:
+            return bool(gap < GAP_EXACT and got == t2)
+        sess.decode_token(got)
+    return True
 
 
 def main():
@@ -188,10 +234,11 @@ def main():
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--ttft-runs", type=int, default=3)
     ap.add_argument("--kernel-reps", type=int, default=256)
-    ap.add_argument("--cpu-layers", type=int, default=4)
+    ap.add_argument("--cpu-layers", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--probe", choices=["traffic"], default=None,
-                    help="traffic: run only a plain copy and the roofline kernel (for rocprofv3 --pmc)")
+    ap.add_argument("--probe", choices=["traffic", "mfma"], default=None,
+                    help="traffic: a plain copy and the decode roofline kernel; mfma: the prefill gate/up GEMM "
+                         "(each alone, for rocprofv3 --pmc)")
     ap.add_argument("--model", default=None, help="existing GGUF (default: generate the synthetic config)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -218,14 +265,19 @@ def main():
     model = E.LoadedModel.load(path, device=0)
     print(f"[bench] model load + HBM upload {time.perf_counter() - t0:.1f}s", file=sys.stderr, flush=True)
     cfg = model.config
+    prompt = synth.prompt_ids(0, args.prompt, int(cfg.vocab_size))
     if args.probe == "traffic":
-        probe_traffic(E, model, cfg, args.kernel_reps)
+        probe_traffic(E, model, cfg, prompt, args.kernel_reps)
         print(f"[bench] traffic probe done: 1 copy of {COPY_BYTES} B, {args.kernel_reps} roofline-kernel launches",
+              file=sys.stderr, flush=True)
+        return
+    if args.probe == "mfma":
+        r = prefill_roofline(E, model, prompt, args.kernel_reps)
+        print(f"[bench] mfma probe done: {args.kernel_reps} prefill gate/up GEMM launches, {r['achieved']} TFLOP/s",
               file=sys.stderr, flush=True)
         return
     if args.prompt + args.warmup + args.steps > cfg.context_length:
         sys.exit(f"prompt + warmup + steps exceeds context_length {cfg.context_length}")
-    prompt = synth.prompt_ids(0, args.prompt, int(cfg.vocab_size))
     sess = E.InferenceSession(model)
 
     # TTFT (fresh cache each run).
@@ -265,18 +317,22 @@ def main():
     step_bytes = wbytes + kv_avg
     step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    roof = None
+    roof = roof_pf = match = None
     if not gemma:
-        roof = kernel_roofline(E, model, cfg, args.kernel_reps)
+        match = golden_tokens_match(E, sess, prompt, args.config)
+        roof = kernel_roofline(E, model, prompt, args.kernel_reps)
         print(f"[bench] dominant kernel {roof['achieved']} GB/s ({roof['avg_launch_us']} us/launch)",
+              file=sys.stderr, flush=True)
+        roof_pf = prefill_roofline(E, model, prompt, max(args.kernel_reps // 4, 8))
+        print(f"[bench] prefill gate/up GEMM {roof_pf['achieved']} TFLOP/s ({roof_pf['avg_launch_us']} us/launch)",
               file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu_baseline:
         del sess
         model.close()
-        cpu = cpu_baseline(path, args.cpu_layers)
-        print(f"[bench] cpu baseline {cpu['value']} tok/s", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(path, args.cpu_layers, prompt)
+        print(f"[bench] cpu baseline {cpu['value']} tok/s, TTFT {cpu['ttft_ms']} ms", file=sys.stderr, flush=True)
 
     flops_prefill = prefill_flops(cfg, specs, args.prompt)
     if gemma:
@@ -291,7 +347,7 @@ def main():
                 f"{cfg.n_heads}/{cfg.n_kv_heads} heads, FFN {cfg.ffn_dim}, vocab {cfg.vocab_size}), "
                 f"Q4_K_M-style GGUF")
         data = "synthetic (seeded random-init N(0,0.02) weights quantised Q4_K/Q6_K, uniform random prompt ids)"
-        kv = "fp16 KV cache"
+        kv = "f32 KV cache"
     out = {
         "metric": METRIC, "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
@@ -307,8 +363,10 @@ def main():
         "decode_step_gbs": round(step_gbs, 1),
         "decode_roofline_frac": round(step_gbs / HBM_PEAK_GBS, 4),
         "roofline": roof,
+        "roofline_prefill": roof_pf,
         "cpu_baseline": cpu,
         "first_decode_tokens": toks[:8],
+        "first_tokens_match_oracle": match,
     }
     print(json.dumps(out), flush=True)
 

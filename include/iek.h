@@ -88,7 +88,7 @@ iek_status iek_model_tensor(const iek_model* model, const char* name, const void
                             uint64_t* ne0, uint64_t* ne1, uint64_t* bytes);
 
 /* ---- session (src/engine/session.rs:12-75) -------------------------------------------------- */
-/* InferenceSession::new: KV caches of context_length positions per layer (fp16 in HBM). */
+/* InferenceSession::new: KV caches of context_length positions per layer (the reference's f32 keys and values, in HBM). */
 iek_status iek_session_create(iek_model* model, iek_session** out);
 void iek_session_free(iek_session* s);
 /* InferenceSession::reset (session.rs:40-42). */
@@ -115,6 +115,15 @@ iek_status iek_session_kv_len(const iek_session* s, uint64_t* out);
  * launch per matvec and attention, 1 = the decode chain (Q/K/V, O, gate/up and down as phases of
  * persistent launches, two launches per layer). Both compute the same function. */
 iek_status iek_session_decode_path(const iek_session* s, int* out);
+/* No reference counterpart; a measurement aid for the roofline figures. Times `reps` back-to-back
+ * launches of one hot kernel on the session's stream between two HIP events, launch i on layer
+ * i % n (so that consecutive launches stream different weights from HBM): which = 0, the decode
+ * chain launch of layer pair (k-1, k) (layer k-1's O, gate/up and down phases, layer k's Q/K/V;
+ * needs a state and the chain decode path); which = 1, the prefill gate/up GEMM over the last
+ * prefill's rows (Mistral/Llama, a prefill state of >= 2 rows). *avg_us: mean duration per launch;
+ * *work: algorithmic bytes (0) or flops (1) per launch, averaged over the layers. The session is
+ * reset afterwards. */
+iek_status iek_session_bench_kernel(iek_session* s, int which, int reps, double* avg_us, double* work);
 /* Hidden rows of the current ForwardState ([rows, hidden], src/engine/state.rs:7-175). */
 iek_status iek_session_hidden(iek_session* s, float* out, size_t cap, uint64_t* rows);
 /* KVCache::get_k_slice/get_v_slice for every stored position (attention.rs:77-110), widened to

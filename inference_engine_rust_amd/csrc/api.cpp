@@ -175,6 +175,10 @@ iek_status iek_session_kv_len(const iek_session* s, uint64_t* out) { IEK_API_TRY
 
 iek_status iek_session_decode_path(const iek_session* s, int* out) { IEK_API_TRY(*out = s->s->decode_path()) }
 
+iek_status iek_session_bench_kernel(iek_session* s, int which, int reps, double* avg_us, double* work) {
+  IEK_API_TRY(*avg_us = s->s->bench_kernel(which, reps, work))
+}
+
 iek_status iek_session_hidden(iek_session* s, float* out, size_t cap, uint64_t* rows) {
   IEK_API_TRY({
     int r = 0;

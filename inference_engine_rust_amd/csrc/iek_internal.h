@@ -87,7 +87,8 @@ void launch_rope_rows(float* v, int rows, int row_stride, int n_heads, int head_
                       int half_pairs, hipStream_t st);
 void launch_rope_table(float* v, int n_heads, int head_dim, int npairs, const float* cs, const int* pos_dev,
                        hipStream_t st);
-void launch_kv_store(const float* k, const float* v, int rows, int kv_dim, __half* kc, __half* vc, int n_kv,
+// K/V rows into a [n_kv][ctx][head_dim] cache of f32 (kv_f32) or fp16
+void launch_kv_store(const float* k, const float* v, int rows, int kv_dim, void* kc, void* vc, bool kv_f32, int n_kv,
                      int head_dim, int ctx, const int* pos_dev, int pos0, hipStream_t st);
 void launch_swiglu(const float* g, const float* u, float* out, size_t n, hipStream_t st);
 void launch_gelu_mul(const float* g, const float* u, float* out, size_t n, hipStream_t st);

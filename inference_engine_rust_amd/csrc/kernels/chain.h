@@ -40,9 +40,10 @@ struct ChainPhase {
   const float* resid;  // CE_RESID
   // CE_QKV
   const float* rope_cs;  // [ctx][npairs][2]
-  int npairs, head_dim, ctx, pad1;
-  __half* kc;
-  __half* vc;
+  int npairs, head_dim, ctx;
+  int role0;  // role of seg[0]: 0 = Q (segments Q, K, V), 2 = V (a V-only phase, when V's dtype differs)
+  float* kc;  // f32 KV cache [n_kv][ctx][head_dim]
+  float* vc;
   // CX_EMBED_Q4K
   const uint8_t* emb;
   float* emb_out;  // workgroup 0 also writes the dequantised row here

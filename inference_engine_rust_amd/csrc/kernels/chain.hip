@@ -293,7 +293,7 @@ IEK_DEV void control(const ChainArgs& a, Smem& S, int pos) {
       const int u = u0 + lane;
       if (P->epi == CE_RESID) {
         pre = make_float2(ld_coh(P->resid + 2 * u), ld_coh(P->resid + 2 * u + 1));
-      } else if (P->epi == CE_QKV) {
+      } else if (P->epi == CE_QKV && P->role0 == 0) {
         const int n0 = P->seg[0].n, n1 = P->seg[1].n, g0 = 2 * u;
         const int row = g0 - (g0 >= n0 + n1 ? n0 + n1 : (g0 >= n0 ? n0 : 0));
         const int d = row % P->head_dim;
@@ -402,9 +402,10 @@ IEK_DEV void control(const ChainArgs& a, Smem& S, int pos) {
         continue;
       }
       const int n0 = P->seg[0].n, n1 = P->seg[1].n;
-      const int g0 = 2 * u, s = g0 >= n0 + n1 ? 2 : (g0 >= n0 ? 1 : 0);
-      const int row = g0 - (s == 2 ? n0 + n1 : (s == 1 ? n0 : 0));
-      float* out = s == 0 ? P->seg[0].out : (s == 1 ? P->seg[1].out : P->seg[2].out);
+      const int g0 = 2 * u, si = g0 >= n0 + n1 ? 2 : (g0 >= n0 ? 1 : 0);
+      const int row = g0 - (si == 2 ? n0 + n1 : (si == 1 ? n0 : 0));
+      float* out = si == 0 ? P->seg[0].out : (si == 1 ? P->seg[1].out : P->seg[2].out);
+      const int s = P->epi == CE_QKV ? si + P->role0 : si;  // Q, K or V
       if (P->epi == CE_RESID) {
         const float2 r = lu == lane ? pre : make_float2(ld_coh(P->resid + row), ld_coh(P->resid + row + 1));
         st_coh(out + row, r.x + v[0]);
@@ -421,11 +422,11 @@ IEK_DEV void control(const ChainArgs& a, Smem& S, int pos) {
           st_coh(out + row, o0);
           st_coh(out + row + 1, o1);
         } else {
-          __half* c = s == 1 ? P->kc : P->vc;
+          float* c = s == 1 ? P->kc : P->vc;
           const size_t dst = ((size_t)(row / hd) * P->ctx + pos) * hd + d;
-          __half2 h2 = __halves2half2(__float2half_rn(o0), __float2half_rn(o1));
-          __hip_atomic_store(reinterpret_cast<unsigned*>(c + dst), __builtin_bit_cast(unsigned, h2), __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+          const float2 f2 = make_float2(o0, o1);
+          __hip_atomic_store(reinterpret_cast<unsigned long long*>(c + dst), __builtin_bit_cast(unsigned long long, f2),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       } else if (P->epi == CE_ARGMAX) {
 #pragma unroll

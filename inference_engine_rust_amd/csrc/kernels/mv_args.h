@@ -32,8 +32,9 @@ struct MvArgs {
   const float* rope_cs;  // [ctx][npairs][2] (cos, sin)
   int npairs, head_dim, ctx;
   const int* pos;
-  __half* kc;
-  __half* vc;
+  void* kc;  // [n_kv][ctx][head_dim] of f32 (kv_f32) or fp16
+  void* vc;
+  int kv_f32;
   // EPI_ARGMAX
   unsigned long long* amax_key;
   int* amax_flag;

@@ -395,7 +395,9 @@ IEK_DEV void epilogue(const MvArgs& a, const Lds& L, int s, int lr0, float (&acc
         st_f<false>(a.out[0] + n, v);
       } else {
         const size_t dst = ((size_t)(n / hd) * a.ctx + pos) * hd + d;
-        st_h<false>((s == 1 ? a.kc : a.vc) + dst, __float2half_rn(v));
+        void* c = s == 1 ? a.kc : a.vc;
+        if (a.kv_f32) st_f<false>(static_cast<float*>(c) + dst, v);
+        else st_h<false>(static_cast<__half*>(c) + dst, __float2half_rn(v));
       }
     }
     return;

@@ -236,8 +236,9 @@ void launch_rope_table(float* v, int n_heads, int head_dim, int npairs, const fl
 
 // KV append: rows [r] of k/v ([rows][kv_dim], f32) go to cache position (pos + r) as fp16.
 // Cache layout per layer: [n_kv][ctx][head_dim], so one head's keys are one contiguous stream.
-__global__ void kv_store_kernel(const float* k, const float* v, int rows, int kv_dim, __half* kc, __half* vc,
-                                int head_dim, int ctx, const int* pos_dev, int pos0) {
+template <typename T>
+__global__ void kv_store_kernel(const float* k, const float* v, int rows, int kv_dim, T* kc, T* vc, int head_dim,
+                                int ctx, const int* pos_dev, int pos0) {
   const size_t total = (size_t)rows * kv_dim;
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
@@ -245,17 +246,27 @@ __global__ void kv_store_kernel(const float* k, const float* v, int rows, int kv
   const int h = c / head_dim, d = c % head_dim;
   const int pos = (pos_dev ? *pos_dev : pos0) + r;
   const size_t dst = ((size_t)h * ctx + pos) * head_dim + d;
-  kc[dst] = __float2half_rn(k[i]);
-  vc[dst] = __float2half_rn(v[i]);
+  if constexpr (std::is_same<T, float>::value) {
+    kc[dst] = k[i];
+    vc[dst] = v[i];
+  } else {
+    kc[dst] = __float2half_rn(k[i]);
+    vc[dst] = __float2half_rn(v[i]);
+  }
 }
 
-void launch_kv_store(const float* k, const float* v, int rows, int kv_dim, __half* kc, __half* vc, int n_kv,
+void launch_kv_store(const float* k, const float* v, int rows, int kv_dim, void* kc, void* vc, bool kv_f32, int n_kv,
                      int head_dim, int ctx, const int* pos_dev, int pos0, hipStream_t st) {
   (void)n_kv;
   size_t total = (size_t)rows * kv_dim;
   if (total == 0) return;
-  hipLaunchKernelGGL(kv_store_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, k, v, rows, kv_dim, kc,
-                     vc, head_dim, ctx, pos_dev, pos0);
+  const dim3 grid((unsigned)((total + 255) / 256));
+  if (kv_f32)
+    hipLaunchKernelGGL(kv_store_kernel<float>, grid, dim3(256), 0, st, k, v, rows, kv_dim, (float*)kc, (float*)vc,
+                       head_dim, ctx, pos_dev, pos0);
+  else
+    hipLaunchKernelGGL(kv_store_kernel<__half>, grid, dim3(256), 0, st, k, v, rows, kv_dim, (__half*)kc, (__half*)vc,
+                       head_dim, ctx, pos_dev, pos0);
 }
 
 // swiglu (src/ops/swiglu.rs:24-36): out = (g * sigmoid(g)) * u, two-branch stable sigmoid.

@@ -590,8 +590,8 @@ Model* load_model(const std::string& path, int device) {
   }
 
   // Regrouped copies of the matrices the decode matvec streams, laid out for 16-byte lane loads:
-  // Q6_K ffn_down and LM head (DT_Q6K_R), and every Q8_0 projection and a Q8_0 LM head
-  // (DT_Q8_0_R). Same bytes, rearranged; the native blocks stay in place for every other consumer
+  // every Q6_K projection (ffn_down, and attn_v in Q4_K_M files) and LM head (DT_Q6K_R), and
+  // every Q8_0 projection and a Q8_0 LM head (DT_Q8_0_R). Same bytes, rearranged; the native blocks stay in place for every other consumer
   // (prefill GEMM, embedding lookups, op-level entry points).
   {
     std::vector<DevTensor*> rg;
@@ -602,11 +602,9 @@ Model* load_model(const std::string& path, int device) {
         if (o == &t) return;
       rg.push_back(&t);
     };
-    for (auto& L : m->layers) {
-      if (L.down.dtype == DT_Q6K) consider(L.down);
+    for (auto& L : m->layers)
       for (DevTensor* t : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down, &L.ple_gate, &L.ple_proj})
-        if (t->dtype == DT_Q8_0) consider(*t);
-    }
+        if (t->dtype == DT_Q6K || t->dtype == DT_Q8_0) consider(*t);
     consider(m->lm_head);
     size_t total_r = 0;
     std::vector<size_t> off_r;

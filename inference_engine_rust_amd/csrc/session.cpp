@@ -8,6 +8,8 @@
 //                                                src/layers/gemma4_ple.rs:27-109; embed.rs:53-149
 #include "session.h"
 
+#include <functional>
+
 #include "kernels/chain.h"
 #include "kernels/mv_args.h"
 
@@ -42,9 +44,12 @@ Session::Session(Model* m) : m_(m) {
   // attention.rs:129-135, sizes every cache to context_length).
   // A layer that borrows another layer's KV (Gemma-4 shared-KV layers, model_config.rs:332-372)
   // never appends to its own cache; it gets none and aliases its source's.
-  // Gemma-4 keeps the reference's f32 cache: its attention has q/k head norms and a score scale of
-  // 1, and fp16 keys/values there move the logits by ~1e-2 relative.
-  kv_f32_ = gemma_;
+  // The cache keeps the reference's f32 keys and values (KVCache, attention.rs:16-24). Rounding
+  // them to fp16 is not within the logits bar: applied to the reference's own CPU path (the oracle
+  // with fp16-rounded K and V), it moves the decode logits of the 32-layer Mistral-7B-shaped model
+  // by 2.4e-3 relative L2 (K alone 2.1e-3, V alone 1.3e-3) and of the 2-layer one by 7e-4; Gemma-4
+  // (q/k head norms, score scale 1) moves by ~1e-2.
+  kv_f32_ = true;
   const size_t esz = kv_f32_ ? 4 : 2;
   size_t total = 0;
   for (auto& L : c.layers)
@@ -282,14 +287,18 @@ void Session::layer_prefill(int li, int M) {
     return xs_;
   };
   const DevTensor* wqkv[3] = {&L.wq, &L.wk, &L.wv};
-  const __half* xs = norm_split(L.attn_norm, !quant_ready(wqkv, 3, M, H_));
+  const bool qkv_q = quant_ready(wqkv, 3, M, H_) || (quant_ready(wqkv, 2, M, H_) && quant_ready(wqkv + 2, 1, M, H_));
+  const __half* xs = norm_split(L.attn_norm, !qkv_q);
   {
     const DevTensor* ws[3] = {&L.wq, &L.wk, &L.wv};
     float* outs[3] = {q_, k_, v_};
     if (!xs || !project_q(ws, outs, 3, M, H_, nullptr)) {
-      project(L.wq, xn_, xs, M, H_, qd, q_, nullptr, st_);
-      project(L.wk, xn_, xs, M, H_, kvd, k_, nullptr, st_);
-      project(L.wv, xn_, xs, M, H_, kvd, v_, nullptr, st_);
+      // Q and K share a launch when only V differs (a Q6_K attn_v in a Q4_K_M file)
+      if (!xs || !project_q(ws, outs, 2, M, H_, nullptr)) {
+        project(L.wq, xn_, xs, M, H_, qd, q_, nullptr, st_);
+        project(L.wk, xn_, xs, M, H_, kvd, k_, nullptr, st_);
+      }
+      if (!xs || !project_q(ws + 2, outs + 2, 1, M, H_, nullptr)) project(L.wv, xn_, xs, M, H_, kvd, v_, nullptr, st_);
     }
   }
   if (c.unpack_qk) {
@@ -301,7 +310,7 @@ void Session::layer_prefill(int li, int M) {
   const RopeTable& rt = m_->rope_tables[L.rope_table];
   launch_rope_rows(q_, M, qd, c.n_heads, hd, 0, rt.dev, S.rotary_dim / 2, st_);
   launch_rope_rows(k_, M, kvd, c.n_kv_heads, hd, 0, rt.dev, S.rotary_dim / 2, st_);
-  launch_kv_store(k_, v_, M, kvd, (__half*)kc_[li], (__half*)vc_[li], c.n_kv_heads, hd, ctx_, nullptr, pos_, st_);
+  launch_kv_store(k_, v_, M, kvd, kc_[li], vc_[li], kv_f32_, c.n_kv_heads, hd, ctx_, nullptr, pos_, st_);
   const float scale = 1.0f / sqrtf((float)hd);
   // xs_ (the GEMM input pair, consumed by the Q/K/V projection above) is free until the O
   // projection's split: the shared-K/V attention stages its fp16 K / V planes there
@@ -383,8 +392,9 @@ void Session::decode_args(int li, MvArgs& a, MvArgs& o, MvArgs& f, MvArgs& dn, i
   a.head_dim = hd;
   a.ctx = ctx_;
   a.pos = d_pos_;
-  a.kc = (__half*)kc_[li];
-  a.vc = (__half*)vc_[li];
+  a.kc = kc_[li];
+  a.vc = vc_[li];
+  a.kv_f32 = kv_f32_ ? 1 : 0;
   dts[0] = L.wq.dtype;
   o = MvArgs{};
   o.nseg = 1;
@@ -485,14 +495,17 @@ void Session::prepare_chain() {
     wdt(L.wk, &dk);
     wdt(L.wv, &dv);
     wdt(L.down, &dd);
-    if (!fused_ok(li) || dq != DT_Q4K || dk != DT_Q4K || dv != DT_Q4K || L.wo.dtype != DT_Q4K ||
-        L.gate.dtype != DT_Q4K || L.up.dtype != DT_Q4K || (dd != DT_Q4K && dd != DT_Q6K_R))
+    // Q4_K_M files give some layers a Q6_K attn_v: that layer's V rows run as a phase of their own
+    if (c.unpack_qk || H_ % 256 != 0 || dq != DT_Q4K || dk != DT_Q4K || (dv != DT_Q4K && dv != DT_Q6K_R) ||
+        L.wo.dtype != DT_Q4K || L.gate.dtype != DT_Q4K || L.up.dtype != DT_Q4K || (dd != DT_Q4K && dd != DT_Q6K_R))
       return;
     if (!dims_ok(L.wq, H_, S.q_dim) || !dims_ok(L.wk, H_, S.kv_dim) || !dims_ok(L.wv, H_, S.kv_dim) ||
         !dims_ok(L.wo, S.q_dim, H_) || !dims_ok(L.gate, H_, S.ffn_dim) || !dims_ok(L.up, H_, S.ffn_dim) ||
         !dims_ok(L.down, S.ffn_dim, H_) || S.head_dim % 2 != 0 || S.rotary_dim > S.head_dim)
       return;
-    if (!phase_ok(DT_Q4K, H_, true, (S.q_dim + 2 * S.kv_dim) / 2) || !phase_ok(DT_Q4K, S.q_dim, false, H_ / 2) ||
+    const bool split_v = dv != DT_Q4K;
+    if (!phase_ok(DT_Q4K, H_, true, (S.q_dim + (split_v ? 1 : 2) * S.kv_dim) / 2) ||
+        (split_v && !phase_ok(dv, H_, true, S.kv_dim / 2)) || !phase_ok(DT_Q4K, S.q_dim, false, H_ / 2) ||
         !phase_ok(DT_Q4K, H_, true, S.ffn_dim) || !phase_ok(dd, S.ffn_dim, false, H_ / 2))
       return;
   }
@@ -517,27 +530,43 @@ void Session::prepare_chain() {
     P.x_mode = CX_F32;
     return P;
   };
-  auto qkv = [&](int li, int wait_prev, bool embed) {
+  // Q/K/V of layer li with RMSNorm, RoPE and the KV append: one phase, or a Q/K phase and a V phase
+  // when V's rows are another dtype (the V phase needs no barrier: its input is the Q/K phase's)
+  auto qkv = [&](int li, int wait_prev, bool embed, std::vector<ChainPhase>& v) {
     const LayerSpec& S = c.layers[li];
     const LayerTensors& L = m_->layers[li];
-    ChainPhase P = base(DT_Q4K, H_, CE_QKV, (S.q_dim + 2 * S.kv_dim) / 2, xdec_, (const float*)L.attn_norm.dev,
-                        wait_prev);
-    P.nseg = 3;
+    int dv;
+    const uint8_t* wv = wdt(L.wv, &dv);
+    const bool split_v = dv != DT_Q4K;
+    ChainPhase P = base(DT_Q4K, H_, CE_QKV, (S.q_dim + (split_v ? 1 : 2) * S.kv_dim) / 2, xdec_,
+                        (const float*)L.attn_norm.dev, wait_prev);
+    P.nseg = split_v ? 2 : 3;
     P.seg[0] = ChainSeg{(const uint8_t*)L.wq.dev, qd_, S.q_dim, 0};
     P.seg[1] = ChainSeg{(const uint8_t*)L.wk.dev, nullptr, S.kv_dim, 0};
-    P.seg[2] = ChainSeg{(const uint8_t*)L.wv.dev, nullptr, S.kv_dim, 0};
+    if (!split_v) P.seg[2] = ChainSeg{wv, nullptr, S.kv_dim, 0};
     P.rope_cs = m_->rope_tables[L.rope_table].dev;
     P.npairs = S.rotary_dim / 2;
     P.head_dim = S.head_dim;
     P.ctx = ctx_;
-    P.kc = (__half*)kc_[li];
-    P.vc = (__half*)vc_[li];
+    P.kc = (float*)kc_[li];
+    P.vc = (float*)vc_[li];
     if (embed) {
       P.x_mode = CX_EMBED_Q4K;
       P.emb = (const uint8_t*)m_->token_embd.dev;
       P.emb_out = xdec_;
     }
-    return P;
+    v.push_back(P);
+    if (split_v) {
+      ChainPhase V = P;
+      V.dt = dv;
+      V.units = S.kv_dim / 2;
+      V.nseg = 1;
+      V.seg[0] = ChainSeg{wv, nullptr, S.kv_dim, 0};
+      V.seg[1] = V.seg[2] = ChainSeg{};
+      V.role0 = 2;
+      V.wait_prev = 0;
+      v.push_back(V);
+    }
   };
   auto ffn = [&](int li, std::vector<ChainPhase>& v) {
     const LayerSpec& S = c.layers[li];
@@ -560,12 +589,12 @@ void Session::prepare_chain() {
     d.resid = xdec_;
     v.push_back(d);
   };
-  std::vector<std::vector<ChainPhase>> launches;
-  launches.push_back({qkv(0, 0, chain_embed_)});
+  std::vector<std::vector<ChainPhase>> launches(1);
+  qkv(0, 0, chain_embed_, launches[0]);
   for (int li = 0; li < c.n_layers; ++li) {
     std::vector<ChainPhase> v;
     ffn(li, v);
-    if (li + 1 < c.n_layers) v.push_back(qkv(li + 1, 1, false));
+    if (li + 1 < c.n_layers) qkv(li + 1, 1, false, v);
     launches.push_back(v);
   }
   {
@@ -635,7 +664,7 @@ void Session::layer_decode_unfused(int li) {
   const RopeTable& rt = m_->rope_tables[L.rope_table];
   launch_rope_table(qd_, c.n_heads, hd, S.rotary_dim / 2, rt.dev, d_pos_, st_);
   launch_rope_table(kd_, c.n_kv_heads, hd, S.rotary_dim / 2, rt.dev, d_pos_, st_);
-  launch_kv_store(kd_, vd_, 1, kvd, (__half*)kc_[li], (__half*)vc_[li], c.n_kv_heads, hd, ctx_, d_pos_, 0, st_);
+  launch_kv_store(kd_, vd_, 1, kvd, kc_[li], vc_[li], kv_f32_, c.n_kv_heads, hd, ctx_, d_pos_, 0, st_);
   const float scale = 1.0f / sqrtf((float)hd);
   launch_attn_decode(qd_, kc_[li], vc_[li], kv_f32_, attd_, part_, d_cnt_, c.n_heads, c.n_kv_heads, hd, ctx_, d_pos_, S.window,
                      scale, ctx_, st_);
@@ -922,6 +951,78 @@ void Session::prefill(const uint32_t* ids, int n) {
   state_ple_ = gemma_ && c.ple_dim > 0;
   layer_cursor_ = 0;
   sync();
+}
+
+double Session::bench_kernel(int which, int reps, double* work) {
+  const Config& c = m_->cfg;
+  if (reps <= 0) fail(ST_OP, "bench_kernel: reps must be positive");
+  check_state();
+  const int L = c.n_layers;
+  auto wbytes = [](const DevTensor& t) { return (double)t.bytes; };
+  // Launch i works on layer i % (number of layers) so that consecutive launches stream different
+  // weights from HBM (one layer's weights would stay in the 256 MB last-level cache).
+  std::function<void(int)> launch;
+  double total = 0.0;
+  int period = 0;
+  if (which == 0) {
+    if (!chain_ || L < 2) fail(ST_OP, "bench_kernel: the session does not decode through the chain");
+    if (pos_ >= ctx_) fail(ST_KVCACHE, "KVCache is Full: max len is " + std::to_string(ctx_) + ".");
+    // launch k (1 <= k < L): layer k-1's O, gate/up and down, layer k's Q/K/V
+    period = L - 1;
+    for (int k = 1; k < L; ++k) {
+      const LayerTensors& P = m_->layers[k - 1];
+      const LayerTensors& N = m_->layers[k];
+      const LayerSpec& S = c.layers[k - 1];
+      const LayerSpec& T = c.layers[k];
+      total += wbytes(P.wo) + wbytes(P.gate) + wbytes(P.up) + wbytes(P.down) + wbytes(N.wq) + wbytes(N.wk) +
+               wbytes(N.wv) + 4.0 * ((double)S.q_dim + 4.0 * H_ + 2.0 * S.ffn_dim + T.q_dim + 2.0 * T.kv_dim);
+    }
+    launch = [&](int i) {
+      const int k = 1 + i % (L - 1);
+      ChainArgs a{};
+      a.phases = static_cast<const ChainPhase*>(chain_ph_[k]);
+      a.nphase = chain_np_[k];
+      a.pos = d_pos_;
+      a.tok = d_tok_;
+      a.counters = d_chain_cnt_;
+      a.err = d_chain_err_;
+      launch_chain(a, st_);
+    };
+  } else if (which == 1) {
+    if (gemma_ || !state_prefill_ || state_rows_ < 2) fail(ST_OP, "bench_kernel: needs a Mistral/Llama prefill state");
+    const int M = state_rows_;
+    period = L;
+    for (int li = 0; li < L; ++li) {
+      const DevTensor* ws[2] = {&m_->layers[li].gate, &m_->layers[li].up};
+      if (!quant_ready(ws, 2, M, H_)) fail(ST_OP, "bench_kernel: gate/up do not run on the K-quant GEMM");
+      total += 2.0 * M * H_ * 2.0 * c.layers[li].ffn_dim;
+    }
+    launch = [&, M](int i) {
+      const int li = i % L;
+      const DevTensor* w2[2] = {&m_->layers[li].gate, &m_->layers[li].up};
+      float* outs[2] = {g_, u_};
+      project_q(w2, outs, 2, M, H_, nullptr);
+    };
+  } else {
+    fail(ST_OP, "bench_kernel: which must be 0 or 1");
+  }
+  *work = total / period;
+  hipEvent_t e0, e1;
+  IEK_HIP(hipEventCreate(&e0));
+  IEK_HIP(hipEventCreate(&e1));
+  for (int i = 0; i < 3; ++i) launch(i);
+  IEK_HIP(hipEventRecord(e0, st_));
+  for (int i = 0; i < reps; ++i) launch(i);
+  IEK_HIP(hipEventRecord(e1, st_));
+  IEK_HIP(hipEventSynchronize(e1));
+  float ms = 0.f;
+  IEK_HIP(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  check_chain_error();
+  reset();
+  sync();
+  return 1e3 * (double)ms / reps;
 }
 
 // ---- forward-level steps -------------------------------------------------------------------------

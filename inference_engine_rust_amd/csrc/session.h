@@ -1,4 +1,4 @@
-// Device-resident inference session: owns the fp16 KV cache, activation buffers, the HIP stream
+// Device-resident inference session: owns the f32 KV cache, activation buffers, the HIP stream
 // and the captured decode-step graph. Mirrors InferenceSession (src/engine/session.rs:12-75).
 #pragma once
 #include <vector>
@@ -41,6 +41,12 @@ class Session {
   int next_layer() const { return layer_cursor_; }
   int n_layers() const { return m_->cfg.n_layers; }
   void check_no_layer_forward() const;  // IEK_ERR_MODEL while a layer-level forward is part way
+
+  // Average duration (us) of `reps` back-to-back launches of one hot kernel on the session stream,
+  // between two HIP events, and its algorithmic work per launch (*work: bytes or flops).
+  // which 0: the decode chain launch of a middle layer (O, gate/up, down, next layer's Q/K/V);
+  // which 1: the prefill gate/up GEMM over the last prefill's rows. Leaves the session reset.
+  double bench_kernel(int which, int reps, double* work);
 
   int kv_len() const { return pos_; }
   int decode_path() const { return chain_ ? 1 : 0; }

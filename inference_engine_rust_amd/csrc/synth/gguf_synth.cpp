@@ -200,13 +200,14 @@ void quantize_q8_0(const float* x, uint8_t* b) {
   for (int l = 0; l < 32; ++l) b[2 + l] = (uint8_t)(int8_t)(d > 0 ? std::min(127, std::max(-127, nearest(x[l] / d))) : 0);
 }
 
-enum { T_F32 = 0, T_Q8_0 = 8, T_Q4K = 12, T_Q6K = 14, T_BF16 = 30 };
+// T_F32_H: stored as F32, values rounded to f16 first (the F32 twin of a T_F16 tensor)
+enum { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4K = 12, T_Q6K = 14, T_BF16 = 30, T_F32_H = 1001 };
 
 size_t block_elems(int t) { return t == T_Q8_0 ? 32 : 256; }
 size_t block_bytes(int t) { return t == T_Q4K ? 144 : t == T_Q6K ? 210 : 34; }
 size_t tensor_bytes(int t, size_t n) {
-  if (t == T_F32) return n * 4;
-  if (t == T_BF16) return n * 2;
+  if (t == T_F32 || t == T_F32_H) return n * 4;
+  if (t == T_BF16 || t == T_F16) return n * 2;
   return (n + block_elems(t) - 1) / block_elems(t) * block_bytes(t);
 }
 
@@ -234,6 +235,22 @@ std::vector<uint8_t> make_tensor(uint64_t seed, const std::string& name, int typ
     std::vector<float> v(nelem);
     parallel_chunks(nelem, threads, [&](size_t a, size_t e) { gen_normal(key, a, e - a, mean, stdv, v.data() + a); });
     memcpy(out.data(), v.data(), nelem * 4);
+    return out;
+  }
+  if (type == T_F16 || type == T_F32_H) {  // IEEE half, round to nearest even
+    parallel_chunks(nelem, threads, [&](size_t a, size_t e) {
+      std::vector<float> v(e - a);
+      gen_normal(key, a, e - a, mean, stdv, v.data());
+      for (size_t i = a; i < e; ++i) {
+        const uint16_t h = f32_to_f16(v[i - a]);
+        if (type == T_F16) {
+          memcpy(out.data() + 2 * i, &h, 2);
+        } else {
+          const float w = f16_to_f32(h);
+          memcpy(out.data() + 4 * i, &w, 4);
+        }
+      }
+    });
     return out;
   }
   if (type == T_BF16) {  // round to nearest even on the upper 16 bits
@@ -328,7 +345,7 @@ int write_gguf(const char* path, const std::vector<KV>& kvs, const std::vector<T
     put_str(head, t.name);
     put<uint32_t>(head, (uint32_t)t.dims.size());
     for (auto d : t.dims) put<uint64_t>(head, d);
-    put<uint32_t>(head, t.type);
+    put<uint32_t>(head, t.type == T_F32_H ? (uint32_t)T_F32 : t.type);
     put<uint64_t>(head, off);
     offs.push_back(off);
     size_t n = 1;
@@ -375,7 +392,17 @@ struct iek_synth_spec {
   float rope_theta, rms_eps, weight_std, norm_std;
   uint32_t t_attn, t_ffn_gate_up, t_ffn_down, t_embd, t_output;
   uint32_t tied_output;     // 1: no output.weight (LM head reuses token_embd)
+  // Per-layer attn_v / ffn_down types. 0: t_attn / t_ffn_down everywhere. 1: llama.cpp's Q4_K_M
+  // rule: Q6_K in the layers it gives more bits (i < n/8, i >= 7n/8, (i - n/8) % 3 == 2), Q4_K in
+  // the others. 2: Q6_K in odd layers, Q4_K in even ones (small test models).
+  uint32_t mix;
+  uint32_t t_norm;          // RMSNorm weights: 0 F32, 1 F16, 2 F32 holding f16-rounded values
 };
+
+static bool more_bits(uint32_t mix, uint32_t i, uint32_t n) {
+  if (mix == 2) return i % 2 == 1;
+  return i < n / 8 || i >= 7 * n / 8 || (i >= n / 8 && (i - n / 8) % 3 == 2);
+}
 
 // Writes a Mistral/Llama-family GGUF. Returns 0 on success, nonzero on I/O failure.
 int iek_synth_write_llama(const char* path, const iek_synth_spec* sp, uint64_t seed, int threads) {
@@ -401,17 +428,20 @@ int iek_synth_write_llama(const char* path, const iek_synth_spec* sp, uint64_t s
   tis.push_back({"token_embd.weight", {s.hidden, s.vocab}, s.t_embd, 0.f, ws});
   for (uint32_t l = 0; l < s.n_layers; ++l) {
     std::string p = "blk." + std::to_string(l) + ".";
-    tis.push_back({p + "attn_norm.weight", {s.hidden}, T_F32, 1.f, ns});
+    const uint32_t t_v = s.mix ? (more_bits(s.mix, l, s.n_layers) ? T_Q6K : T_Q4K) : s.t_attn;
+    const uint32_t t_down = s.mix ? (more_bits(s.mix, l, s.n_layers) ? T_Q6K : T_Q4K) : s.t_ffn_down;
+    const uint32_t t_n = s.t_norm == 1 ? T_F16 : (s.t_norm == 2 ? T_F32_H : T_F32);
+    tis.push_back({p + "attn_norm.weight", {s.hidden}, t_n, 1.f, ns});
     tis.push_back({p + "attn_q.weight", {s.hidden, s.n_heads * hd}, s.t_attn, 0.f, ws});
     tis.push_back({p + "attn_k.weight", {s.hidden, s.n_kv_heads * hd}, s.t_attn, 0.f, ws});
-    tis.push_back({p + "attn_v.weight", {s.hidden, s.n_kv_heads * hd}, s.t_attn, 0.f, ws});
+    tis.push_back({p + "attn_v.weight", {s.hidden, s.n_kv_heads * hd}, t_v, 0.f, ws});
     tis.push_back({p + "attn_output.weight", {s.n_heads * hd, s.hidden}, s.t_attn, 0.f, ws});
-    tis.push_back({p + "ffn_norm.weight", {s.hidden}, T_F32, 1.f, ns});
+    tis.push_back({p + "ffn_norm.weight", {s.hidden}, t_n, 1.f, ns});
     tis.push_back({p + "ffn_gate.weight", {s.hidden, s.ffn}, s.t_ffn_gate_up, 0.f, ws});
     tis.push_back({p + "ffn_up.weight", {s.hidden, s.ffn}, s.t_ffn_gate_up, 0.f, ws});
-    tis.push_back({p + "ffn_down.weight", {s.ffn, s.hidden}, s.t_ffn_down, 0.f, ws});
+    tis.push_back({p + "ffn_down.weight", {s.ffn, s.hidden}, t_down, 0.f, ws});
   }
-  tis.push_back({"output_norm.weight", {s.hidden}, T_F32, 1.f, ns});
+  tis.push_back({"output_norm.weight", {s.hidden}, s.t_norm == 1 ? T_F16 : (s.t_norm == 2 ? T_F32_H : T_F32), 1.f, ns});
   if (!s.tied_output) tis.push_back({"output.weight", {s.hidden, s.vocab}, s.t_output, 0.f, ws});
   return write_gguf(path, kvs, tis, seed, threads);
 }

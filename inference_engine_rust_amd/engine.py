@@ -78,6 +78,8 @@ EXPORTS = {
     "iek_session_generate_greedy": ([_P, _SZ, _P], ctypes.c_int),
     "iek_session_kv_len": ([_P, ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
     "iek_session_decode_path": ([_P, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
+    "iek_session_bench_kernel": ([_P, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+                                  ctypes.POINTER(ctypes.c_double)], ctypes.c_int),
     "iek_session_hidden": ([_P, _P, _SZ, ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
     "iek_session_kv": ([_P, ctypes.c_uint64, ctypes.c_int, _P, _SZ], ctypes.c_int),
     "iek_session_embed": ([_P, _P, _SZ], ctypes.c_int),
@@ -247,6 +249,13 @@ class InferenceSession:
 
     def decode_forward(self) -> None:
         _check(lib().iek_session_decode_forward(self._h))
+
+    def bench_kernel(self, which: int, reps: int) -> tuple[float, float]:
+        """(mean us per launch, algorithmic bytes or flops per launch) of the hot kernel `which`
+        (0: middle-layer decode chain launch, 1: prefill gate/up GEMM); resets the session."""
+        us, work = ctypes.c_double(), ctypes.c_double()
+        _check(lib().iek_session_bench_kernel(self._h, which, reps, ctypes.byref(us), ctypes.byref(work)))
+        return us.value, work.value
 
     def decode_path(self) -> int:
         """0: per-launch decode kernels; 1: the decode chain (persistent phase launches)."""

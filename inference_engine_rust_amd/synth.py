@@ -51,6 +51,8 @@ class _Spec(ctypes.Structure):
         ("t_embd", ctypes.c_uint32),
         ("t_output", ctypes.c_uint32),
         ("tied_output", ctypes.c_uint32),
+        ("mix", ctypes.c_uint32),
+        ("t_norm", ctypes.c_uint32),
     ]
 
 
@@ -74,6 +76,11 @@ class LlamaSpec:
     t_embd: int = GGML_Q4_K
     t_output: int = GGML_Q6_K
     tied_output: bool = False
+    # per-layer attn_v / ffn_down types: 0 uniform (t_attn / t_ffn_down), 1 llama.cpp's Q4_K_M
+    # rule (Q6_K in the layers it gives more bits, Q4_K elsewhere), 2 Q6_K in odd layers only
+    mix: int = 0
+    # RMSNorm weights: 0 F32, 1 F16, 2 F32 holding f16-rounded values (the F32 twin of 1)
+    t_norm: int = 0
 
     @property
     def head_dim(self) -> int:
@@ -88,6 +95,8 @@ PRESETS = {
     "c2_l2": LlamaSpec("synthetic-mistral-7b-2layer", 2, 4096, 32, 8, 14336, 32000, 640),
     # c0 with a 4096-token context: long-context decode attention (multi-slice chunks) at parity size
     "c0_long": LlamaSpec("synthetic-mistral-tiny-long", 2, 512, 8, 2, 1408, 32000, 4096),
+    # C4's widths and context with 2 layers: the long-prompt prefill and decode kernels at parity size
+    "c4_l2": LlamaSpec("synthetic-mistral-7b-2layer-long", 2, 4096, 32, 8, 14336, 32000, 8704),
 }
 
 
@@ -148,6 +157,8 @@ PRESETS.update({
     "c3": GemmaSpec("synthetic-gemma-4-e2b", 35, 1536, 8, 1, 256, 512, 6144, 262144, 512, 256, 512, 5, 20,
                     256, 128, rope_freqs=False, q8_layer_scale=False),
     "g0": GemmaSpec("synthetic-gemma-4-tiny", 6, 256, 4, 1, 64, 128, 512, 8192, 96, 32, 16, 3, 2, 64, 32),
+    # C3's head dims (256 sliding / 512 global) and GQA group of 8 at parity size
+    "g1": GemmaSpec("synthetic-gemma-4-hd512", 6, 512, 8, 1, 256, 512, 1024, 8192, 640, 64, 128, 3, 2, 256, 128),
 })
 
 
@@ -185,7 +196,7 @@ def write_llama(path: str, spec: LlamaSpec, seed: int = 0, threads: int | None =
     s = _Spec(spec.name.encode(), spec.n_layers, spec.hidden, spec.n_heads, spec.n_kv_heads, spec.ffn,
               spec.vocab, spec.context_length, spec.rope_theta, spec.rms_eps, spec.weight_std,
               spec.norm_std, spec.t_attn, spec.t_ffn_gate_up, spec.t_ffn_down, spec.t_embd,
-              spec.t_output, 1 if spec.tied_output else 0)
+              spec.t_output, 1 if spec.tied_output else 0, spec.mix, spec.t_norm)
     if threads is None:
         threads = min(16, os.cpu_count() or 1)
     rc = lib().iek_synth_write_llama(path.encode(), ctypes.byref(s), seed, threads)

@@ -213,43 +213,70 @@ static void f32_row_kernel(const float* a, size_t k, const float* w, float* out_
 // Register-blocked GEMM over a k-major weight copy Wt[kk*N + col]. Each output element is still
 // `acc += a*w` in kk order with separate multiply and add, so every element is bit-identical to
 // the reference's scalar loop. Skipping a == 0 is only observable for non-finite weights; the
-// caller routes those to the exact skip loop.
+// caller routes those to the exact skip loop. One work item is one NR-column panel of W over every
+// row of `a`: the panel (k x NR floats) comes from memory once and is reused from cache by each
+// MR-row block.
 static void gemm_kmajor(const float* a, size_t m, size_t k, const float* wt, size_t n, float* out,
-                        int threads) {
-  const size_t MR = 4, NR = 32;
-  size_t mblocks = (m + MR - 1) / MR, nblocks = (n + NR - 1) / NR;
-  parallel_for(mblocks * nblocks, threads, [&](size_t idx) {
-    size_t nb = idx % nblocks, mb = idx / nblocks;
-    size_t m0 = mb * MR, n0 = nb * NR;
-    size_t mr = std::min(MR, m - m0), nr = std::min(NR, n - n0);
-    float acc[MR][NR];
-    for (size_t i = 0; i < MR; ++i)
-      for (size_t j = 0; j < NR; ++j) acc[i][j] = 0.0f;
-    if (mr == MR && nr == NR) {
-      for (size_t kk = 0; kk < k; ++kk) {
-        const float* wr = wt + kk * n + n0;
-        for (size_t i = 0; i < MR; ++i) {
-          float av = a[(m0 + i) * k + kk];
-          for (size_t j = 0; j < NR; ++j) {
-            float p = av * wr[j];
-            acc[i][j] = acc[i][j] + p;
-          }
-        }
-      }
-    } else {
-      for (size_t kk = 0; kk < k; ++kk) {
-        const float* wr = wt + kk * n + n0;
-        for (size_t i = 0; i < mr; ++i) {
-          float av = a[(m0 + i) * k + kk];
-          for (size_t j = 0; j < nr; ++j) {
-            float p = av * wr[j];
-            acc[i][j] = acc[i][j] + p;
-          }
-        }
-      }
+                        int threads, bool reassoc = false) {
+  if (reassoc) {
+    // two halves of K, each summed in order, added at the end
+    const size_t kh = k / 2;
+    std::vector<float> a0(m * kh), a1(m * (k - kh)), o1(m * n);
+    for (size_t i = 0; i < m; ++i) {
+      memcpy(&a0[i * kh], a + i * k, kh * 4);
+      memcpy(&a1[i * (k - kh)], a + i * k + kh, (k - kh) * 4);
     }
-    for (size_t i = 0; i < mr; ++i)
-      for (size_t j = 0; j < nr; ++j) out[(m0 + i) * n + n0 + j] = acc[i][j];
+    gemm_kmajor(a0.data(), m, kh, wt, n, out, threads);
+    gemm_kmajor(a1.data(), m, k - kh, wt + kh * n, n, o1.data(), threads);
+    for (size_t i = 0; i < m * n; ++i) out[i] = out[i] + o1[i];
+    return;
+  }
+  constexpr size_t MR = 6, NR = 16;
+  const size_t nblocks = (n + NR - 1) / NR;
+  parallel_for(nblocks, threads, [&](size_t nb) {
+    const size_t n0 = nb * NR, nr = std::min(NR, n - n0);
+    for (size_t m0 = 0; m0 < m; m0 += MR) {
+      const size_t mr = std::min(MR, m - m0);
+      float acc[MR][NR];
+      for (size_t i = 0; i < MR; ++i)
+        for (size_t j = 0; j < NR; ++j) acc[i][j] = 0.0f;
+      if (mr == MR && nr == NR) {
+        // 8-wide vectors across columns (GCC vector extension): lane j is column n0 + j, still a
+        // separate multiply and add per element in kk order
+        typedef float v8 __attribute__((vector_size(32)));
+        v8 va[MR][2];
+        for (size_t i = 0; i < MR; ++i) va[i][0] = va[i][1] = v8{};
+        for (size_t kk = 0; kk < k; ++kk) {
+          v8 w0, w1;
+          memcpy(&w0, wt + kk * n + n0, 32);
+          memcpy(&w1, wt + kk * n + n0 + 8, 32);
+          for (size_t i = 0; i < MR; ++i) {
+            const float av = a[(m0 + i) * k + kk];
+            const v8 b = {av, av, av, av, av, av, av, av};
+            const v8 p0 = b * w0, p1 = b * w1;
+            va[i][0] = va[i][0] + p0;
+            va[i][1] = va[i][1] + p1;
+          }
+        }
+        for (size_t i = 0; i < MR; ++i) {
+          memcpy(&acc[i][0], &va[i][0], 32);
+          memcpy(&acc[i][8], &va[i][1], 32);
+        }
+      } else {
+        for (size_t kk = 0; kk < k; ++kk) {
+          const float* wr = wt + kk * n + n0;
+          for (size_t i = 0; i < mr; ++i) {
+            const float av = a[(m0 + i) * k + kk];
+            for (size_t j = 0; j < nr; ++j) {
+              float p = av * wr[j];
+              acc[i][j] = acc[i][j] + p;
+            }
+          }
+        }
+      }
+      for (size_t i = 0; i < mr; ++i)
+        for (size_t j = 0; j < nr; ++j) out[(m0 + i) * n + n0 + j] = acc[i][j];
+    }
   });
 }
 
@@ -276,8 +303,8 @@ void matmul(const float* a, size_t m, size_t k, const Tensor& w, float* out, siz
     });
     return;
   }
-  // PARITY mode.
-  if (m <= 4) {
+  // PARITY mode (REASSOC: the k-major GEMM in two halves of K).
+  if (m <= 4 && mode != REASSOC) {
     const size_t CH = 64;
     size_t chunks = (n + CH - 1) / CH;
     parallel_for(m * chunks, threads, [&](size_t idx) {
@@ -298,6 +325,25 @@ void matmul(const float* a, size_t m, size_t k, const Tensor& w, float* out, siz
         float v = wf[kk + col * k];
         if (!std::isfinite(v)) nonfinite = true;
         wt[kk * n + col] = v;
+      }
+    });
+  } else if (k % block_elems(t) == 0) {
+    // every column starts on a block: decode 16 columns' blocks at a time straight into the
+    // k-major copy (rows of 16 contiguous floats)
+    const size_t be = block_elems(t), bb = block_bytes(t), kb_n = k / be;
+    parallel_for((n + 15) / 16, threads, [&](size_t g) {
+      const size_t c0 = g * 16, nc = std::min<size_t>(16, n - c0);
+      float dec[16][256];
+      for (size_t kb = 0; kb < kb_n; ++kb) {
+        for (size_t c = 0; c < nc; ++c) dequant_block(t, w.buf.data() + ((c0 + c) * kb_n + kb) * bb, dec[c]);
+        for (size_t e = 0; e < be; ++e) {
+          float* dst = &wt[(kb * be + e) * n + c0];
+          for (size_t c = 0; c < nc; ++c) {
+            const float v = dec[c][e];
+            if (!std::isfinite(v)) nonfinite = true;
+            dst[c] = v;
+          }
+        }
       }
     });
   } else {
@@ -323,7 +369,7 @@ void matmul(const float* a, size_t m, size_t k, const Tensor& w, float* out, siz
     });
     return;
   }
-  gemm_kmajor(a, m, k, wt.data(), n, out, threads);
+  gemm_kmajor(a, m, k, wt.data(), n, out, threads, mode == REASSOC);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1178,31 +1224,60 @@ static std::vector<float> prefill_attention(Session& s, const float* input, size
   std::vector<float> out(seq * qd, 0.0f);
   float scale = c.family == GEMMA4 ? 1.0f : 1.0f / sqrtf((float)hd);
   size_t src_idx = borrow >= 0 ? (size_t)borrow : li;
-  for (size_t p = 0; p < seq; ++p) {
-    size_t j_min = 0;
-    if (la.sliding_window >= 0) {
-      size_t wm1 = la.sliding_window > 0 ? (size_t)la.sliding_window - 1 : 0;
-      j_min = p > wm1 ? p - wm1 : 0;
+  auto krow = [&](size_t j, size_t kvh) -> const float* {
+    return borrow >= 0 ? kslice(s.kv[src_idx], j, kvh) : &k[j * kvd + kvh * hd];
+  };
+  auto vrow = [&](size_t j, size_t kvh) -> const float* {
+    return borrow >= 0 ? vslice(s.kv[src_idx], j, kvh) : &v[j * kvd + kvh * hd];
+  };
+  // Keys transposed per KV head (kt[kvh][e][j], j padded to a multiple of 8) so that eight
+  // scores are formed at once, lane by lane in the same e order as the scalar dot product.
+  const size_t sp = (seq + 7) / 8 * 8;
+  std::vector<float> kt(c.n_kv_heads * hd * sp, 0.0f);
+  parallel_for(c.n_kv_heads, s.threads, [&](size_t kvh) {
+    for (size_t j = 0; j < seq; ++j) {
+      const float* kr = krow(j, kvh);
+      for (size_t e = 0; e < hd; ++e) kt[(kvh * hd + e) * sp + j] = kr[e];
     }
-    parallel_for(c.n_heads, s.threads, [&](size_t h) {
-      size_t kvh = h / group;
+  });
+  typedef float v8 __attribute__((vector_size(32)));
+  // one work item per query head, positions in order (each output row depends on its own
+  // scores only, so the split does not change any value)
+  parallel_for(c.n_heads, s.threads, [&](size_t h) {
+    const size_t kvh = h / group;
+    std::vector<float> sc(seq), wts(seq);
+    for (size_t p = 0; p < seq; ++p) {
+      size_t j_min = 0;
+      if (la.sliding_window >= 0) {
+        size_t wm1 = la.sliding_window > 0 ? (size_t)la.sliding_window - 1 : 0;
+        j_min = p > wm1 ? p - wm1 : 0;
+      }
       const float* qv = &q[p * qd + h * hd];
-      std::vector<float> sc(p + 1, -INFINITY), wts(p + 1, 0.0f);
-      for (size_t j = j_min; j <= p; ++j) {
-        const float* kv_ = borrow >= 0 ? kslice(s.kv[src_idx], j, kvh) : &k[j * kvd + kvh * hd];
-        float dot = 0.0f;
-        for (size_t e = 0; e < hd; ++e) dot += qv[e] * kv_[e];
-        sc[j] = dot * scale;
+      for (size_t j = 0; j < j_min; ++j) sc[j] = -INFINITY;
+      for (size_t j0 = j_min / 8 * 8; j0 <= p; j0 += 8) {
+        v8 dot = {};
+        for (size_t e = 0; e < hd; ++e) {
+          v8 kk;
+          memcpy(&kk, &kt[(kvh * hd + e) * sp + j0], 32);
+          const float qe = qv[e];
+          const v8 qb = {qe, qe, qe, qe, qe, qe, qe, qe};
+          const v8 prod = qb * kk;
+          dot = dot + prod;
+        }
+        for (size_t l = 0; l < 8; ++l) {
+          const size_t j = j0 + l;
+          if (j >= j_min && j <= p) sc[j] = dot[l] * scale;
+        }
       }
       softmax(sc.data(), wts.data(), p + 1);
       float* o = &out[p * qd + h * hd];
       for (size_t j = j_min; j <= p; ++j) {
-        float wt = wts[j];
-        const float* vv = borrow >= 0 ? vslice(s.kv[src_idx], j, kvh) : &v[j * kvd + kvh * hd];
+        const float wt = wts[j];
+        const float* vv = vrow(j, kvh);
         for (size_t e = 0; e < hd; ++e) o[e] += wt * vv[e];
       }
-    });
-  }
+    }
+  });
   std::vector<float> proj(seq * c.hidden_dim);
   matmul(out.data(), seq, qd, *w.wo, proj.data(), seq, c.hidden_dim, s.mode, s.threads);
   return proj;

@@ -166,7 +166,10 @@ struct State {
 // Execution mode. PARITY: vectorised/threaded but bit-identical per output element.
 // BASELINE: the reference's own Rayon decomposition (rows of a matmul when M*N*K >= 65536,
 // heads in attention), for timing.
-enum Mode : int { PARITY = 0, BASELINE = 1 };
+// REASSOC: PARITY with every matmul dot product summed as two halves of K added at the end — a
+// legitimate f32 reassociation, used to measure how much the model's logits move under rounding
+// differences alone (the conditioning that bounds any reordered implementation).
+enum Mode : int { PARITY = 0, BASELINE = 1, REASSOC = 2 };
 
 struct Session {
   const Model* model = nullptr;

@@ -1,7 +1,7 @@
 """End-to-end GPU parity of the token loop against the CPU oracle (same seeded synthetic GGUF).
 
 Bars (north star): greedy tokens identical; per-step logits within 1e-3 relative L2 (measured
-values are ~1e-6); KV cache within fp16 rounding of the oracle's f32 cache.
+values are ~1e-6); KV cache within f32 reordering of the oracle's (both keep f32 keys and values).
 """
 import json
 import os
@@ -77,7 +77,7 @@ def test_c0_prefill_hidden_and_kv(c0_gpu, c0_orc):
             kg = s.kv(layer, which)  # [n_kv][pos][hd]
             kr = r.kv(layer, which).transpose(1, 0, 2)
             assert kg.shape == kr.shape
-            np.testing.assert_allclose(kg, kr, rtol=2 ** -10, atol=1e-6)
+            np.testing.assert_allclose(kg, kr, rtol=1e-4, atol=1e-5 * np.abs(kr).max())
 
 
 def test_graph_generate_matches_stepwise(c0_gpu):

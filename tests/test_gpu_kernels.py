@@ -134,6 +134,13 @@ def test_gemm_parity(gpu, dt, k, n, m):
     _check_matmul(dt, k, n, m)
 
 
+@pytest.mark.parametrize("dt,k,n", [(E.Q4K, 4096, 4096), (E.Q4K, 4096, 1024), (E.Q4K, 4096, 14336),
+                                    (E.Q6K, 14336, 4096)])
+def test_gemm_parity_mistral_shapes_m512(gpu, dt, k, n):
+    """The four Mistral-7B projection shapes at C1's M = 512 (Q/O, K/V, gate/up, down)."""
+    _check_matmul(dt, k, n, 512)
+
+
 def test_rmsnorm_parity(gpu):
     rows, dim = 5, 4096
     x = synth.normal(1, "x", rows * dim, 0.0, 2.0).reshape(rows, dim)
