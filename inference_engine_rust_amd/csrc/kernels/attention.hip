@@ -1,4 +1,5 @@
-// Attention over an fp16 KV cache laid out per layer as [n_kv][ctx][head_dim].
+// Attention over a KV cache laid out per layer as [n_kv][ctx][head_dim] (f32 in the sessions; fp16
+// through the op-level entry).
 //
 // Decode (src/layers/attention.rs:462-655): split-K flash-decode over 64-key slices, GQA groups
 // sharing one K/V stream; the slice count is fixed by the cache capacity so the launch shape
@@ -13,179 +14,42 @@
 
 namespace iek {
 
-template <int HD, bool EARLY, int SETS, bool COH>
-__global__ __launch_bounds__(256 * SETS) void attn_decode_kernel(const float* __restrict__ q, const __half* __restrict__ kc,
-                                                          const __half* __restrict__ vc, float* __restrict__ part,
-                                                          float* __restrict__ out, int* __restrict__ counters,
-                                                          int n_heads, int n_kv, int ctx, const int* pos_dev,
-                                                          int window, float scale, int nsplit, int spc) {
-  __shared__ __align__(16) char smem[AttnSmem<HD, SETS>::BYTES];
+template <int HD, bool EARLY, int SETS, bool COH, typename T>
+__global__ __launch_bounds__(256 * SETS) void attn_decode_kernel(const float* __restrict__ q, const T* __restrict__ kc,
+                                                                 const T* __restrict__ vc, float* __restrict__ part,
+                                                                 float* __restrict__ out, int* __restrict__ counters,
+                                                                 int n_heads, int n_kv, int ctx, const int* pos_dev,
+                                                                 int window, float scale, int nsplit, int spc) {
+  __shared__ __align__(16) char smem[AttnSmem<HD, SETS, T>::BYTES];
   // all arguments in one batch of scalar loads, ahead of the position they depend on
   asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(part), "s"(out), "s"(counters), "s"(n_heads), "s"(n_kv), "s"(ctx),
                "s"(pos_dev), "s"(window), "s"(scale), "s"(nsplit), "s"(spc));
-  attn_chunk_f16<HD, COH, EARLY, SETS>(q, kc, vc, part, out, counters, n_heads, n_kv, ctx, pos_dev, 0, window, scale, nsplit,
-                                   blockIdx.x, blockIdx.y, spc, smem);
+  attn_chunk<HD, COH, EARLY, SETS, T>(q, kc, vc, part, out, counters, n_heads, n_kv, ctx, pos_dev, 0, window, scale,
+                                      nsplit, blockIdx.x, blockIdx.y, spc, smem);
 }
 
-// f32 KV cache variant (Gemma-4 sessions keep the reference's f32 cache: with q/k head norms
-// and a score scale of 1 the softmax is sharp enough that fp16 keys/values move the logits by
-// ~1e-2). Same grid, partials and merge as the fp16 kernel. The slice's K rows, then its V rows,
-// are staged through one LDS buffer in pieces of up to 256 head dims with cooperative 16-byte
-// loads (every load of a piece in flight at once); lane = key for the scores (two query heads
-// per wave), then for P.V each lane owns DPP consecutive dims of the piece.
-template <int HD>
-__global__ __launch_bounds__(256) void attn_decode_f32_kernel(const float* __restrict__ q, const float* __restrict__ kc,
-                                                              const float* __restrict__ vc, float* __restrict__ part,
-                                                              float* __restrict__ out, int* __restrict__ counters,
-                                                              int n_heads, int n_kv, int ctx, const int* pos_dev,
-                                                              int window, float scale, int nsplit) {
-  constexpr int PD = HD < 256 ? HD : 256;  // dims per staged piece
-  constexpr int NP = HD / PD;
-  // all arguments in one batch of scalar loads, ahead of the position they depend on
-  asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(part), "s"(out), "s"(counters), "s"(n_heads), "s"(n_kv), "s"(ctx),
-               "s"(pos_dev), "s"(window), "s"(scale), "s"(nsplit));
-  constexpr int ROW = PD + 4;               // padded LDS row (floats)
-  constexpr int DPP = PD / 64;              // dims per lane per piece in P.V
-  constexpr int F4 = SPLIT * PD / 4 / 256;  // float4 per thread per piece
-  const int G = n_heads / n_kv;
-  // query heads split over HG workgroups per (KV head, slice) when the group has 8: each
-  // workgroup stages the slice and runs one head per wave
-  const int HG = G == 8 ? 2 : 1, GH = G / HG;
-  const int kvh = blockIdx.x / HG, hg = blockIdx.x % HG, gb = hg * GH;
-  const int sp = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int total = *pos_dev + 1;
-  const int jmin = (window > 0 && total > window) ? total - window : 0;
-  const int j0 = max(sp * SPLIT, jmin), j1 = min(total, (sp + 1) * SPLIT);
-  const int nk = j1 - j0;
-  if (nk <= 0) return;  // uniform across the workgroup
-  __shared__ __align__(16) float qs[8][HD];
-  __shared__ __align__(16) float kv[SPLIT][ROW];
-  __shared__ float ps[8][SPLIT];
-  const float* kb = kc + ((size_t)kvh * ctx + j0) * HD;
-  const float* vb = vc + ((size_t)kvh * ctx + j0) * HD;
-  // cooperative piece load: element e of the piece is row e / (PD/4), float4 column e % (PD/4)
-  typedef float pf4_t __attribute__((ext_vector_type(4)));  // native vectors stay in registers
-  auto stage_piece = [&](const float* base, int p) {
-    pf4_t r[F4];
-#pragma unroll
-    for (int u = 0; u < F4; ++u) {
-      const int e = tid + 256 * u, row = min(e / (PD / 4), nk - 1), c4 = e % (PD / 4);
-      r[u] = *reinterpret_cast<const pf4_t*>(base + (size_t)row * HD + p * PD + 4 * c4);
-    }
-    __syncthreads();  // the previous piece's readers are done
-#pragma unroll
-    for (int u = 0; u < F4; ++u) {
-      const int e = tid + 256 * u, row = e / (PD / 4), c4 = e % (PD / 4);
-      *reinterpret_cast<pf4_t*>(&kv[row][4 * c4]) = r[u];
-    }
-    __syncthreads();
+template <int HD, typename T>
+static void attn_decode_hd(dim3 grid, hipStream_t st, const float* q, const T* kc, const T* vc, float* out, float* part,
+                           int* counters, int n_heads, int n_kv, int ctx, const int* pos_dev, int window, float scale,
+                           int nsplit) {
+  // chunks of spc slices (about 32 chunks per KV head); one partial slot per chunk
+  const int spc = attn_slices_per_chunk(nsplit * SPLIT, window, 32);
+  const int nchunk = (nsplit + spc - 1) / spc;
+  // Chunks of several slices (long contexts) run two slice streams per workgroup (head dims up to
+  // 128: the doubled K / V buffers still fit in LDS), and publish their partials with coherent
+  // stores and a relaxed count (no L2 write-back / invalidate around the arrival, measured faster
+  // there; one-slice chunks are faster with plain stores).
+  const bool two = HD <= 128 && spc >= 2;
+  auto go = [&](auto kern, int nt) {
+    hipLaunchKernelGGL(kern, dim3(grid.x, nchunk), dim3(nt), 0, st, q, kc, vc, part, out, counters, n_heads, n_kv, ctx,
+                       pos_dev, window, scale, nchunk, spc);
   };
-  for (int i = tid; i < GH * HD; i += 256) qs[i / HD][i % HD] = q[(size_t)(kvh * G + gb) * HD + i];
-  float sc[2] = {0.f, 0.f};
-  for (int p = 0; p < NP; ++p) {
-    stage_piece(kb, p);
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int g = wave + 4 * t;
-      if (g < GH) {
-        float acc = 0.f;
-#pragma unroll 8
-        for (int d = 0; d < PD; d += 4) {
-          const float4 k4 = *reinterpret_cast<const float4*>(&kv[lane][d]);
-          const float4 q4 = *reinterpret_cast<const float4*>(&qs[g][p * PD + d]);
-          acc += q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
-        }
-        sc[t] += acc;
-      }
-    }
-  }
-  const bool valid = lane < nk;
-  float m[2], l[2];
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int g = wave + 4 * t;
-    if (g < GH) {
-      const float s = valid ? sc[t] * scale : -INFINITY;
-      m[t] = wave_max(s);
-      const float pr = valid ? expf(s - m[t]) : 0.f;
-      l[t] = wave_sum(pr);
-      ps[g][lane] = pr;
-    }
-  }
-  float o[2][NP][DPP];
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int p = 0; p < NP; ++p)
-#pragma unroll
-      for (int e = 0; e < DPP; ++e) o[t][p][e] = 0.f;
-#pragma unroll
-  for (int p = 0; p < NP; ++p) {
-    stage_piece(vb, p);  // its first barrier also publishes ps
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int g = wave + 4 * t;
-      if (g < GH) {
-#pragma unroll 8
-        for (int j = 0; j < SPLIT; ++j) {
-          const float pj = ps[g][j];
-#pragma unroll
-          for (int e = 0; e < DPP; ++e) o[t][p][e] += pj * kv[j][DPP * lane + e];
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int g = wave + 4 * t;
-    if (g < GH) {
-      float* pr = part + ((size_t)(kvh * G + gb + g) * nsplit + sp) * (HD + 2);
-      if (lane == 0) {
-        pr[0] = m[t];
-        pr[1] = l[t];
-      }
-#pragma unroll
-      for (int p = 0; p < NP; ++p)
-#pragma unroll
-        for (int e = 0; e < DPP; ++e) pr[2 + p * PD + DPP * lane + e] = o[t][p][e];
-    }
-  }
-  __shared__ int last;
-  __shared__ float wsl[4 * 256];
-  merge_if_last<HD>(part, out, counters, kvh, G, nsplit, jmin / SPLIT, (total + SPLIT - 1) / SPLIT, wave, &last, wsl,
-                    gb, GH, kvh * HG + hg);
-}
-
-template <int HD>
-static void attn_decode_hd(dim3 grid, hipStream_t st, const float* q, const void* kc, const void* vc, bool kv_f32,
-                           float* out, float* part, int* counters, int n_heads, int n_kv, int ctx, const int* pos_dev,
-                           int window, float scale, int nsplit) {
-  if (kv_f32) {
-    const int hgroups = n_heads / n_kv == 8 ? 2 : 1;  // the kernel's query-head split
-    hipLaunchKernelGGL(attn_decode_f32_kernel<HD>, dim3(grid.x * hgroups, grid.y), dim3(256), 0, st, q,
-                       (const float*)kc, (const float*)vc, part, out, counters, n_heads, n_kv, ctx, pos_dev, window,
-                       scale, nsplit);
-  } else {
-    // fp16 cache: chunks of spc slices (about 32 chunks per KV head); one partial slot per chunk
-    const int spc = attn_slices_per_chunk(nsplit * SPLIT, window, 32);
-    const int nchunk = (nsplit + spc - 1) / spc;
-    // Chunks of several slices (long contexts) run two slice streams per workgroup (head dims up to
-    // 128: the doubled K / V buffers fit beside a second workgroup on the CU), and publish their
-    // partials with coherent stores and a relaxed count (no L2 write-back / invalidate around the
-    // arrival, measured faster there; one-slice chunks are faster with plain stores).
-    const bool two = HD <= 128 && spc >= 2;
-    auto go = [&](auto kern, int nt) {
-      hipLaunchKernelGGL(kern, dim3(grid.x, nchunk), dim3(nt), 0, st, q, (const __half*)kc, (const __half*)vc, part,
-                         out, counters, n_heads, n_kv, ctx, pos_dev, window, scale, nchunk, spc);
-    };
-    // without a window the first slice's loads go out before the position is known
-    constexpr int S2 = HD <= 128 ? 2 : 1;
-    if (window <= 0)
-      two ? go(attn_decode_kernel<HD, true, S2, true>, 512) : go(attn_decode_kernel<HD, true, 1, false>, 256);
-    else
-      two ? go(attn_decode_kernel<HD, false, S2, true>, 512) : go(attn_decode_kernel<HD, false, 1, false>, 256);
-  }
+  // without a window the first slice's loads go out before the position is known
+  constexpr int S2 = HD <= 128 ? 2 : 1;
+  if (window <= 0)
+    two ? go(attn_decode_kernel<HD, true, S2, true, T>, 512) : go(attn_decode_kernel<HD, true, 1, false, T>, 256);
+  else
+    two ? go(attn_decode_kernel<HD, false, S2, true, T>, 512) : go(attn_decode_kernel<HD, false, 1, false, T>, 256);
 }
 
 size_t attn_decode_part_floats(int n_heads, int head_dim, int max_len) {
@@ -201,9 +65,11 @@ void launch_attn_decode(const float* q, const void* kc, const void* vc, bool kv_
   if (n_kv <= 0 || n_heads % n_kv != 0 || n_heads / n_kv > 8)
     fail(ST_OP, "attention: GQA group must divide the heads and be at most 8");
   switch (head_dim) {
-#define IEK_AD(HD)                                                                                               \
-  attn_decode_hd<HD>(grid, st, q, kc, vc, kv_f32, out, part, counters, n_heads, n_kv, ctx, pos_dev, window, scale, \
-                     nsplit)
+#define IEK_AD(HD)                                                                                                 \
+  kv_f32 ? attn_decode_hd<HD>(grid, st, q, (const float*)kc, (const float*)vc, out, part, counters, n_heads, n_kv, ctx, \
+                              pos_dev, window, scale, nsplit)                                                         \
+         : attn_decode_hd<HD>(grid, st, q, (const __half*)kc, (const __half*)vc, out, part, counters, n_heads, n_kv,   \
+                              ctx, pos_dev, window, scale, nsplit)
     case 64:
       IEK_AD(64);
       break;

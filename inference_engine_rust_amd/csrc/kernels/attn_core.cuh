@@ -1,5 +1,5 @@
-// Decode attention device code over a per-layer KV cache [n_kv][ctx][head_dim], shared by the
-// per-launch kernels (attention.hip) and the persistent decode step (decode_step.hip).
+// Decode attention device code over a per-layer KV cache [n_kv][ctx][head_dim] (f32 or fp16
+// elements), used by the decode attention kernels (attention.hip).
 // src/layers/attention.rs:462-655 (decode_attention_layer): split-K flash-decode over 64-key
 // slices, GQA groups sharing one K/V stream, (max, sum, o[]) partials merged per query head.
 #pragma once
@@ -126,23 +126,24 @@ IEK_DEV void merge_if_last(const float* __restrict__ part, float* __restrict__ o
 // LDS of one slice item: K rows (padded), V rows (HD <= 256), the group's q, the wave's
 // probabilities, the merge weights and the last-arrival flag; K, V and the probabilities once per
 // slice stream (SETS).
-template <int HD, int SETS = 1>
+template <int HD, int SETS = 1, typename T = __half>
 struct AttnSmem {
-  static constexpr int KROW = HD + 8;
+  static constexpr int ES = (int)sizeof(T);
+  static constexpr int KROW = HD + 16 / ES;  // padded K row: 16 bytes
   static constexpr bool VL = HD <= 256;
-  static constexpr size_t KS1 = (size_t)SPLIT * KROW * 2, VS1 = VL ? (size_t)SPLIT * HD * 2 : 16;
+  static constexpr size_t KS1 = (size_t)SPLIT * KROW * ES, VS1 = VL ? (size_t)SPLIT * HD * ES : 16;
   static constexpr size_t KS = SETS * KS1, VS = SETS * VS1, QS = 8 * (size_t)HD * 4, PS = 4 * SETS * SPLIT * 4,
                           WS = 4 * 256 * 4;
   static constexpr size_t BYTES = KS + VS + QS + PS + WS + 16;
-  __half* ks;
-  __half* vs;
+  T* ks;
+  T* vs;
   float* qs;
   float* ps;
   float* wsl;
   int* last;
   IEK_DEV explicit AttnSmem(char* base) {
-    ks = reinterpret_cast<__half*>(base);
-    vs = reinterpret_cast<__half*>(base + KS);
+    ks = reinterpret_cast<T*>(base);
+    vs = reinterpret_cast<T*>(base + KS);
     qs = reinterpret_cast<float*>(base + KS + VS);
     ps = reinterpret_cast<float*>(base + KS + VS + QS);
     wsl = reinterpret_cast<float*>(base + KS + VS + QS + PS);
@@ -150,7 +151,60 @@ struct AttnSmem {
   }
 };
 
-// One (KV head, chunk) item of the fp16-cache decode attention, by one 256-thread workgroup: the
+// Cache elements as floats: N consecutive values of an f32 or fp16 cache row.
+template <int N>
+IEK_DEV void kv_load(const float* p, float* f) {
+  static_assert(N % 2 == 0 || N == 1, "count");
+  if constexpr (N == 1) {
+    f[0] = *p;
+  } else if constexpr (N == 2) {
+    const float2 a = *reinterpret_cast<const float2*>(p);
+    f[0] = a.x;
+    f[1] = a.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      const float4 a = *reinterpret_cast<const float4*>(p + i);
+      f[i] = a.x;
+      f[i + 1] = a.y;
+      f[i + 2] = a.z;
+      f[i + 3] = a.w;
+    }
+  }
+}
+template <int N>
+IEK_DEV void kv_load(const __half* p, float* f) {
+  if constexpr (N == 1) {
+    f[0] = __half2float(*p);
+  } else if constexpr (N == 2) {
+    const float2 a = __half22float2(*reinterpret_cast<const __half2*>(p));
+    f[0] = a.x;
+    f[1] = a.y;
+  } else if constexpr (N == 4) {
+    const uint2 raw = *reinterpret_cast<const uint2*>(p);
+    const __half2* h2 = reinterpret_cast<const __half2*>(&raw);
+    const float2 a0 = __half22float2(h2[0]), a1 = __half22float2(h2[1]);
+    f[0] = a0.x;
+    f[1] = a0.y;
+    f[2] = a1.x;
+    f[3] = a1.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i += 8) {
+      const uint4 raw = *reinterpret_cast<const uint4*>(p + i);
+      const __half2* h2 = reinterpret_cast<const __half2*>(&raw);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const float2 a = __half22float2(h2[d]);
+        f[i + 2 * d] = a.x;
+        f[i + 2 * d + 1] = a.y;
+      }
+    }
+  }
+}
+
+// One (KV head, chunk) item of the decode attention over an f32 or fp16 cache (T), by one
+// 256-thread workgroup: the
 // chunk is `spc` consecutive 64-key slices. Each slice's K and V rows are loaded in one burst of
 // clamped, unconditional 16-byte loads and staged in LDS (V read straight from memory at head dim
 // 512); the loads of slice i+1 are in flight while slice i is computed. Wave w takes query heads
@@ -163,14 +217,15 @@ struct AttnSmem {
 // chunk's slices s, s + SETS, ... with their own LDS buffers and running (max, sum, o); streams
 // 1.. hand their state to stream 0 through LDS at the end, and stream 0 publishes the partial. A
 // chunk that is its KV head's only one (nslot = 1) writes the output itself (o / sum) instead.
-template <int HD, bool COH = false, bool EARLY = false, int SETS = 1>
-IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restrict__ kc, const __half* __restrict__ vc,
-                            float* __restrict__ part, float* __restrict__ out, int* __restrict__ counters,
-                            int n_heads, int n_kv, int ctx, const int* pos_dev, int total_in, int window, float scale,
-                            int nslot, int kvh, int cp, int spc, char* smem) {
-  constexpr int DPL = HD / 64;        // head dims per lane in the PV phase
-  constexpr int KROW = HD + 8;        // padded K row (halves): 16-byte reads of different rows spread banks
-  constexpr int U4 = SPLIT * HD / 8;  // uint4 per K (or V) slice
+template <int HD, bool COH = false, bool EARLY = false, int SETS = 1, typename T = __half>
+IEK_DEV void attn_chunk(const float* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc,
+                        float* __restrict__ part, float* __restrict__ out, int* __restrict__ counters, int n_heads,
+                        int n_kv, int ctx, const int* pos_dev, int total_in, int window, float scale, int nslot,
+                        int kvh, int cp, int spc, char* smem) {
+  constexpr int DPL = HD / 64;                          // head dims per lane in the PV phase
+  constexpr int EPV = 16 / (int)sizeof(T);              // elements per 16-byte load
+  constexpr int KROW = AttnSmem<HD, SETS, T>::KROW;     // padded K row: 16-byte reads of different rows spread banks
+  constexpr int U4 = SPLIT * HD / EPV;                  // 16-byte loads per K (or V) slice
   // V is staged in LDS up to head_dim 256; at 512 the K slice, q and V would not fit together, so
   // the P.V phase reads V rows straight from memory (each row one coalesced 1 KB wave load).
   constexpr bool VL = HD <= 256;
@@ -181,13 +236,13 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
   const int set = SETS == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 8);
   const int G = n_heads / n_kv;
   const int CK = SPLIT * spc;
-  const AttnSmem<HD, SETS> S(smem);
-  auto ks = reinterpret_cast<__half(*)[KROW]>(S.ks + (size_t)set * SPLIT * KROW);
-  auto vs = reinterpret_cast<__half(*)[VL ? HD : 8]>(S.vs + (VL ? (size_t)set * SPLIT * HD : 0));
+  const AttnSmem<HD, SETS, T> S(smem);
+  auto ks = reinterpret_cast<T(*)[KROW]>(S.ks + (size_t)set * SPLIT * KROW);
+  auto vs = reinterpret_cast<T(*)[VL ? HD : 8]>(S.vs + (VL ? (size_t)set * SPLIT * HD : 0));
   auto qs = reinterpret_cast<float(*)[HD]>(S.qs);
   auto ps = reinterpret_cast<float(*)[SPLIT]>(S.ps + (size_t)set * 4 * SPLIT);
-  const __half* kh = kc + (size_t)kvh * ctx * HD;
-  const __half* vh = vc + (size_t)kvh * ctx * HD;
+  const T* kh = kc + (size_t)kvh * ctx * HD;
+  const T* vh = vc + (size_t)kvh * ctx * HD;
   // native vectors (a HIP uint4 array captured by the lambda would not be promoted to registers)
   typedef uint32_t kv4_t __attribute__((ext_vector_type(4)));
   kv4_t kr[U4 / 256], vr[VL ? U4 / 256 : 1];
@@ -196,9 +251,9 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
   auto issue_rows = [&](int j0, int nk) {
 #pragma unroll
     for (int u = 0; u < U4 / 256; ++u) {
-      const int i = tid + 256 * u, row = j0 + min(i / (HD / 8), nk - 1), c8 = i % (HD / 8);
-      kr[u] = *reinterpret_cast<const kv4_t*>(kh + (size_t)row * HD + 8 * c8);
-      if constexpr (VL) vr[u] = *reinterpret_cast<const kv4_t*>(vh + (size_t)row * HD + 8 * c8);
+      const int i = tid + 256 * u, row = j0 + min(i / (HD / EPV), nk - 1), c8 = i % (HD / EPV);
+      kr[u] = *reinterpret_cast<const kv4_t*>(kh + (size_t)row * HD + EPV * c8);
+      if constexpr (VL) vr[u] = *reinterpret_cast<const kv4_t*>(vh + (size_t)row * HD + EPV * c8);
     }
   };
   // EARLY (no window): the chunk's first slice does not depend on the position, so its rows (all
@@ -238,14 +293,14 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
     __syncthreads();  // the previous slice's LDS reads are done
 #pragma unroll
     for (int u = 0; u < U4 / 256; ++u) {
-      const int i = tid + 256 * u, row = i / (HD / 8), c8 = i % (HD / 8);
-      *reinterpret_cast<kv4_t*>(&ks[row][8 * c8]) = kr[u];
-      if constexpr (VL) *reinterpret_cast<kv4_t*>(&vs[row][8 * c8]) = vr[u];
+      const int i = tid + 256 * u, row = i / (HD / EPV), c8 = i % (HD / EPV);
+      *reinterpret_cast<kv4_t*>(&ks[row][EPV * c8]) = kr[u];
+      if constexpr (VL) *reinterpret_cast<kv4_t*>(&vs[row][EPV * c8]) = vr[u];
     }
     __syncthreads();
     if (sb + SETS < sb1) issue(sb + SETS);
     if (SETS > 1 && sb >= sb1) continue;
-    const __half* vb = vh + (size_t)j0 * HD;
+    const T* vb = vh + (size_t)j0 * HD;
     const bool valid = lane < nk;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -255,14 +310,12 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
       float sc = 0.f;
 #pragma unroll
       for (int c = 0; c < HD / 8; ++c) {
-        const uint4 kraw = *reinterpret_cast<const uint4*>(&ks[lane][8 * c]);
-        const __half2* h2 = reinterpret_cast<const __half2*>(&kraw);
+        float k8[8];
+        kv_load<8>(&ks[lane][8 * c], k8);
         const float4 qa = *reinterpret_cast<const float4*>(&qs[g][8 * c]);
         const float4 qb = *reinterpret_cast<const float4*>(&qs[g][8 * c + 4]);
-        const float2 k0 = __half22float2(h2[0]), k1 = __half22float2(h2[1]), k2 = __half22float2(h2[2]),
-                     k3 = __half22float2(h2[3]);
-        sc += qa.x * k0.x + qa.y * k0.y + qa.z * k1.x + qa.w * k1.y + qb.x * k2.x + qb.y * k2.y + qb.z * k3.x +
-              qb.w * k3.y;
+        sc += qa.x * k8[0] + qa.y * k8[1] + qa.z * k8[2] + qa.w * k8[3] + qb.x * k8[4] + qb.y * k8[5] +
+              qb.z * k8[6] + qb.w * k8[7];
       }
       const float s = valid ? sc * scale : -INFINITY;
       const float m_new = fmaxf(m_run[t], wave_max(s));
@@ -283,31 +336,15 @@ IEK_DEV void attn_chunk_f16(const float* __restrict__ q, const __half* __restric
 #pragma unroll 8
       for (int j = 0; j < nk; ++j) {
         const float pj = ps[wave][j];
-        if constexpr (DPL == 1) {
-          o[0] += pj * __half2float(vs[j][lane]);
-        } else if constexpr (DPL == 2) {
-          const float2 v2 = __half22float2(*reinterpret_cast<const __half2*>(&vs[j][2 * lane]));
-          o[0] += pj * v2.x;
-          o[1] += pj * v2.y;
-        } else if constexpr (DPL == 4) {
-          const uint2 raw = *reinterpret_cast<const uint2*>(&vs[j][4 * lane]);
-          const __half2* h2 = reinterpret_cast<const __half2*>(&raw);
-          const float2 a0 = __half22float2(h2[0]), a1 = __half22float2(h2[1]);
-          o[0] += pj * a0.x;
-          o[1] += pj * a0.y;
-          o[2] += pj * a1.x;
-          o[3] += pj * a1.y;
+        float vv[DPL];
+        if constexpr (VL) {
+          kv_load<DPL>(&vs[j][DPL * lane], vv);
         } else {
           // rows past the live slice have p = 0; their address is clamped into the slice
-          const uint4 raw = *reinterpret_cast<const uint4*>(vb + (size_t)min(j, nk - 1) * HD + 8 * lane);
-          const __half2* h2 = reinterpret_cast<const __half2*>(&raw);
-#pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            const float2 a = __half22float2(h2[d]);
-            o[2 * d] += pj * a.x;
-            o[2 * d + 1] += pj * a.y;
-          }
+          kv_load<DPL>(vb + (size_t)min(j, nk - 1) * HD + DPL * lane, vv);
         }
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) o[d] += pj * vv[d];
       }
 #pragma unroll
       for (int d = 0; d < DPL; ++d) o_run[t][d] = o[d];

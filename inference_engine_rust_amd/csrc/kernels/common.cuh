@@ -69,9 +69,9 @@ IEK_DEV float wave_max(float v) {
 }
 
 // Loads and stores coherent across the XCDs' L2 caches without cache maintenance (agent-scope
-// relaxed atomics: sc1 accesses). Used, under a COH template flag, for data that one workgroup
-// writes and another reads within the same launch (the persistent decode step); the per-launch
-// kernels keep plain accesses (kernel boundaries order their data).
+// relaxed atomics: sc1 accesses). Used for data that one workgroup writes and another reads within
+// the same launch (the decode chain's phases, the decode attention's partials under its COH
+// flag); elsewhere kernel boundaries order the data and plain accesses suffice.
 IEK_DEV float ld_coh(const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 IEK_DEV float4 ld_coh4(const float4* p) {
   const unsigned long long* q = reinterpret_cast<const unsigned long long*>(p);

@@ -1,6 +1,6 @@
 // Decode matvec kernels and launchers: the streaming kernel (mv_stream), the generic fallback for
-// any dtype and K, and the one-time regrouping of Q6_K / Q8_0 weights. The device code they share
-// with the persistent decode step is in mv_core.cuh.
+// any dtype and K, and the one-time regrouping of Q6_K / Q8_0 weights. Their device code is in
+// mv_core.cuh (the decode chain, chain.hip, shares its dequantisation helpers).
 #include <type_traits>
 
 #include "mv_core.cuh"

@@ -1,5 +1,5 @@
-// Decode matvec (M = 1) device code, shared by the per-launch kernels (matvec.hip) and the
-// persistent decode step (decode_step.hip).
+// Decode matvec (M = 1) device code of the per-launch kernels (matvec.hip); the decode chain
+// (chain.hip) reuses its dequantisation helpers.
 //
 // Decode matvec (M = 1): y[n] = sum_k x[k] * W(k, n) over weights kept in their native GGUF
 // block layout (ggml order: element (k, n) at flat k + n*K, src/ops/matmul.rs:1-3).
