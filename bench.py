@@ -105,6 +105,8 @@ def measured_traffic(algo_bytes):
 
 
 COPY_BYTES = 256 << 20
+# prompt lengths of the benchmark configurations
+DEFAULT_PROMPT = {"c0": 16, "c2": 512, "c3": 256, "c4": 8192}
 
 
 def probe_traffic(E, model, cfg, prompt, reps):
@@ -231,7 +233,8 @@ def main():
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--config", default="c2")
-    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--prompt", type=int, default=None,
+                    help="prompt tokens (default: the configuration's own: c0 16, c2 512, c3 256, c4 8192)")
     ap.add_argument("--ttft-runs", type=int, default=3)
     ap.add_argument("--kernel-reps", type=int, default=256)
     ap.add_argument("--cpu-layers", type=int, default=2)
@@ -243,7 +246,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
-              "sharding is a design note in DESIGN.md, not a measured path", file=sys.stderr)
+              "sharding is described in the design notes, not a measured path", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
@@ -253,6 +256,8 @@ def main():
     from inference_engine_rust_amd import synth
 
     spec = synth.preset(args.config)
+    if args.prompt is None:
+        args.prompt = DEFAULT_PROMPT.get(args.config, 512)
     path = args.model
     if path is None:
         d = "/dev/shm" if os.path.isdir("/dev/shm") else "/tmp"

@@ -120,9 +120,10 @@ iek_status iek_session_decode_path(const iek_session* s, int* out);
  * i % n (so that consecutive launches stream different weights from HBM): which = 0, the decode
  * chain launch of layer pair (k-1, k) (layer k-1's O, gate/up and down phases, layer k's Q/K/V;
  * needs a state and the chain decode path); which = 1, the prefill gate/up GEMM over the last
- * prefill's rows (Mistral/Llama, a prefill state of >= 2 rows). *avg_us: mean duration per launch;
- * *work: algorithmic bytes (0) or flops (1) per launch, averaged over the layers. The session is
- * reset afterwards. */
+ * prefill's rows (Mistral/Llama, a prefill state of >= 2 rows); which = 2, the prefill down
+ * projection + residual; which = 3, the prefill Q/K/V GEMM (same conditions as 1). *avg_us: mean
+ * duration per launch (a split-K GEMM's reduction pass included); *work: algorithmic bytes (0) or
+ * flops (1-3) per launch, averaged over the layers. The session is reset afterwards. */
 iek_status iek_session_bench_kernel(iek_session* s, int which, int reps, double* avg_us, double* work);
 /* Hidden rows of the current ForwardState ([rows, hidden], src/engine/state.rs:7-175). */
 iek_status iek_session_hidden(iek_session* s, float* out, size_t cap, uint64_t* rows);

@@ -19,13 +19,14 @@ __global__ __launch_bounds__(256 * SETS) void attn_decode_kernel(const float* __
                                                                  const T* __restrict__ vc, float* __restrict__ part,
                                                                  float* __restrict__ out, int* __restrict__ counters,
                                                                  int n_heads, int n_kv, int ctx, const int* pos_dev,
-                                                                 int window, float scale, int nsplit, int spc) {
+                                                                 int window, float scale, int nsplit, int spc,
+                                                                 int HG) {
   __shared__ __align__(16) char smem[AttnSmem<HD, SETS, T>::BYTES];
   // all arguments in one batch of scalar loads, ahead of the position they depend on
   asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(part), "s"(out), "s"(counters), "s"(n_heads), "s"(n_kv), "s"(ctx),
-               "s"(pos_dev), "s"(window), "s"(scale), "s"(nsplit), "s"(spc));
+               "s"(pos_dev), "s"(window), "s"(scale), "s"(nsplit), "s"(spc), "s"(HG));
   attn_chunk<HD, COH, EARLY, SETS, T>(q, kc, vc, part, out, counters, n_heads, n_kv, ctx, pos_dev, 0, window, scale,
-                                      nsplit, blockIdx.x, blockIdx.y, spc, smem);
+                                      nsplit, blockIdx.x / HG, blockIdx.y, spc, smem, blockIdx.x % HG, HG);
 }
 
 template <int HD, typename T>
@@ -40,9 +41,13 @@ static void attn_decode_hd(dim3 grid, hipStream_t st, const float* q, const T* k
   // stores and a relaxed count (no L2 write-back / invalidate around the arrival, measured faster
   // there; one-slice chunks are faster with plain stores).
   const bool two = HD <= 128 && spc >= 2;
+  // A group of 8 query heads splits over two workgroups per chunk (four heads each, one per
+  // wave) when there are few KV heads to spread over the machine (Gemma-4-E2B: one KV head);
+  // each half has its own arrival counter (2 * n_kv counters) and merge.
+  const int HG = (n_heads / n_kv == 8 && n_kv < 4) ? 2 : 1;
   auto go = [&](auto kern, int nt) {
-    hipLaunchKernelGGL(kern, dim3(grid.x, nchunk), dim3(nt), 0, st, q, kc, vc, part, out, counters, n_heads, n_kv, ctx,
-                       pos_dev, window, scale, nchunk, spc);
+    hipLaunchKernelGGL(kern, dim3(grid.x * HG, nchunk), dim3(nt), 0, st, q, kc, vc, part, out, counters, n_heads, n_kv,
+                       ctx, pos_dev, window, scale, nchunk, spc, HG);
   };
   // without a window the first slice's loads go out before the position is known
   constexpr int S2 = HD <= 128 ? 2 : 1;

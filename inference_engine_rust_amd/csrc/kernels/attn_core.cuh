@@ -203,16 +203,18 @@ IEK_DEV void kv_load(const __half* p, float* f) {
   }
 }
 
-// One (KV head, chunk) item of the decode attention over an f32 or fp16 cache (T), by one
-// 256-thread workgroup: the
-// chunk is `spc` consecutive 64-key slices. Each slice's K and V rows are loaded in one burst of
-// clamped, unconditional 16-byte loads and staged in LDS (V read straight from memory at head dim
-// 512); the loads of slice i+1 are in flight while slice i is computed. Wave w takes query heads
-// w and w+4 of the GQA group: lane = key for the scores, lane = head dims [DPL*l, DPL*l + DPL)
-// for P.V, with a running (max, sum, o) across the chunk's slices. The chunk publishes its
-// (max, sum, o[]) partial in slot `cp`; the last chunk of the KV head to finish merges the
-// group's heads. `total` = keys in the cache including this step's; chunks past the live range
-// return at once (uniformly).
+// One (KV head, head group, chunk) item of the decode attention over an f32 or fp16 cache (T), by
+// one 256-thread workgroup: the chunk is `spc` consecutive 64-key slices. Each slice's K and V
+// rows are loaded in one burst of clamped, unconditional 16-byte loads and staged in LDS; the
+// loads of slice i+1 are in flight while slice i is computed. At head dim 512 the K slice fills
+// the LDS, so V goes out once the K rows are staged and is staged in the same buffer after the
+// scores. The GQA group's G query heads split into HG head groups of G / HG (one workgroup each,
+// all streaming the same K / V); wave w takes heads w and w+4 of its group: lane = key for the
+// scores, lane = head dims [DPL*l, DPL*l + DPL) for P.V, with a running (max, sum, o) across the
+// chunk's slices. The chunk publishes its (max, sum, o[]) partials in slot `cp`; the last chunk
+// of the (KV head, head group) to finish merges the group's heads (counter kvh * HG + hg).
+// `total` = keys in the cache including this step's; chunks past the live range return at once
+// (uniformly).
 // SETS = 2 (512 threads): two slice streams, threads [256 s, 256 s + 256) taking the
 // chunk's slices s, s + SETS, ... with their own LDS buffers and running (max, sum, o); streams
 // 1.. hand their state to stream 0 through LDS at the end, and stream 0 publishes the partial. A
@@ -221,7 +223,7 @@ template <int HD, bool COH = false, bool EARLY = false, int SETS = 1, typename T
 IEK_DEV void attn_chunk(const float* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc,
                         float* __restrict__ part, float* __restrict__ out, int* __restrict__ counters, int n_heads,
                         int n_kv, int ctx, const int* pos_dev, int total_in, int window, float scale, int nslot,
-                        int kvh, int cp, int spc, char* smem) {
+                        int kvh, int cp, int spc, char* smem, int hg = 0, int HG = 1) {
   constexpr int DPL = HD / 64;                          // head dims per lane in the PV phase
   constexpr int EPV = 16 / (int)sizeof(T);              // elements per 16-byte load
   constexpr int KROW = AttnSmem<HD, SETS, T>::KROW;     // padded K row: 16-byte reads of different rows spread banks
@@ -234,7 +236,7 @@ IEK_DEV void attn_chunk(const float* __restrict__ q, const T* __restrict__ kc, c
   const int tid = threadIdx.x & 255, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int set = SETS == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 8);
-  const int G = n_heads / n_kv;
+  const int G = n_heads / n_kv, GH = G / HG, gb = hg * GH;  // the group's heads: gb .. gb + GH - 1
   const int CK = SPLIT * spc;
   const AttnSmem<HD, SETS, T> S(smem);
   auto ks = reinterpret_cast<T(*)[KROW]>(S.ks + (size_t)set * SPLIT * KROW);
@@ -256,6 +258,14 @@ IEK_DEV void attn_chunk(const float* __restrict__ q, const T* __restrict__ kc, c
       if constexpr (VL) vr[u] = *reinterpret_cast<const kv4_t*>(vh + (size_t)row * HD + EPV * c8);
     }
   };
+  // head dim 512: the V rows of a slice into the K registers (after the K rows are staged)
+  auto issue_v_rows = [&](int j0, int nk) {
+#pragma unroll
+    for (int u = 0; u < U4 / 256; ++u) {
+      const int i = tid + 256 * u, row = j0 + min(i / (HD / EPV), nk - 1), c8 = i % (HD / EPV);
+      kr[u] = *reinterpret_cast<const kv4_t*>(vh + (size_t)row * HD + EPV * c8);
+    }
+  };
   // EARLY (no window): the chunk's first slice does not depend on the position, so its rows (all
   // 64, within the cache) go out with q before the position load returns; rows past the live keys
   // get score -inf by a select and are skipped by P.V, so whatever they hold never reaches o.
@@ -264,7 +274,7 @@ IEK_DEV void attn_chunk(const float* __restrict__ q, const T* __restrict__ kc, c
   constexpr int QU = (8 * HD + 255) / 256;
   float qv[QU];
 #pragma unroll
-  for (int u = 0; u < QU; ++u) qv[u] = ld_f<COH>(q + (size_t)(kvh * G) * HD + min(tid + 256 * u, G * HD - 1));
+  for (int u = 0; u < QU; ++u) qv[u] = ld_f<COH>(q + (size_t)(kvh * G + gb) * HD + min(tid + 256 * u, GH * HD - 1));
   if constexpr (EARLY) issue_rows(cp * CK + SPLIT * set, min(SPLIT, ctx - cp * CK - SPLIT * set));
   typedef __attribute__((address_space(4))) const int* ConstInt;  // a scalar load
   const int total = pos_dev ? *(ConstInt)pos_dev + 1 : total_in;
@@ -274,7 +284,7 @@ IEK_DEV void attn_chunk(const float* __restrict__ q, const T* __restrict__ kc, c
 #pragma unroll
   for (int u = 0; u < QU; ++u) {
     const int i = tid + 256 * u;
-    if (i < G * HD) qs[i / HD][i % HD] = qv[u];
+    if (i < GH * HD) qs[i / HD][i % HD] = qv[u];
   }
   const int sb0 = c0 / SPLIT, sb1 = (c1 + SPLIT - 1) / SPLIT;
   auto issue = [&](int sb) {
@@ -298,14 +308,72 @@ IEK_DEV void attn_chunk(const float* __restrict__ q, const T* __restrict__ kc, c
       if constexpr (VL) *reinterpret_cast<kv4_t*>(&vs[row][EPV * c8]) = vr[u];
     }
     __syncthreads();
+    if constexpr (!VL) {
+      // head dim 512: this slice's V rows go out while the scores run, then replace K in LDS
+      issue_v_rows(j0, nk);
+      const bool valid = lane < nk;
+      float pv[2] = {0.f, 0.f}, cv[2] = {1.f, 1.f};
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int g = wave + 4 * t;
+        if (g >= GH) break;
+        float sc = 0.f;
+#pragma unroll 8
+        for (int c = 0; c < HD / 8; ++c) {
+          float k8[8];
+          kv_load<8>(&ks[lane][8 * c], k8);
+          const float4 qa = *reinterpret_cast<const float4*>(&qs[g][8 * c]);
+          const float4 qb = *reinterpret_cast<const float4*>(&qs[g][8 * c + 4]);
+          sc += qa.x * k8[0] + qa.y * k8[1] + qa.z * k8[2] + qa.w * k8[3] + qb.x * k8[4] + qb.y * k8[5] +
+                qb.z * k8[6] + qb.w * k8[7];
+        }
+        const float s = valid ? sc * scale : -INFINITY;
+        const float m_new = fmaxf(m_run[t], wave_max(s));
+        cv[t] = m_run[t] == -INFINITY ? 1.f : expf(m_run[t] - m_new);
+        pv[t] = valid ? expf(s - m_new) : 0.f;
+        l_run[t] = l_run[t] * cv[t] + wave_sum(pv[t]);
+        m_run[t] = m_new;
+      }
+      __syncthreads();  // every wave's K reads are done
+#pragma unroll
+      for (int u = 0; u < U4 / 256; ++u) {
+        const int i = tid + 256 * u, row = i / (HD / EPV), c8 = i % (HD / EPV);
+        *reinterpret_cast<kv4_t*>(&ks[row][EPV * c8]) = kr[u];
+      }
+      __syncthreads();
+      if (sb + SETS < sb1) issue(sb + SETS);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int g = wave + 4 * t;
+        if (g >= GH) break;
+        ps[wave][lane] = pv[t];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float o[DPL];
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) o[d] = o_run[t][d] * cv[t];
+#pragma unroll 8
+        for (int j = 0; j < nk; ++j) {
+          const float pj = ps[wave][j];
+          float vv[DPL];
+          kv_load<DPL>(&ks[j][DPL * lane], vv);
+#pragma unroll
+          for (int d = 0; d < DPL; ++d) o[d] += pj * vv[d];
+        }
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) o_run[t][d] = o[d];
+        __builtin_amdgcn_wave_barrier();  // ps[wave] is rewritten by the next head
+      }
+      continue;
+    }
     if (sb + SETS < sb1) issue(sb + SETS);
     if (SETS > 1 && sb >= sb1) continue;
-    const T* vb = vh + (size_t)j0 * HD;
     const bool valid = lane < nk;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int g = wave + 4 * t;
-      if (g >= G) break;
+      if (g >= GH) break;
       // scores: lane = key
       float sc = 0.f;
 #pragma unroll
@@ -337,12 +405,7 @@ IEK_DEV void attn_chunk(const float* __restrict__ q, const T* __restrict__ kc, c
       for (int j = 0; j < nk; ++j) {
         const float pj = ps[wave][j];
         float vv[DPL];
-        if constexpr (VL) {
-          kv_load<DPL>(&vs[j][DPL * lane], vv);
-        } else {
-          // rows past the live slice have p = 0; their address is clamped into the slice
-          kv_load<DPL>(vb + (size_t)min(j, nk - 1) * HD + DPL * lane, vv);
-        }
+        kv_load<DPL>(&vs[j][DPL * lane], vv);
 #pragma unroll
         for (int d = 0; d < DPL; ++d) o[d] += pj * vv[d];
       }
@@ -358,7 +421,7 @@ IEK_DEV void attn_chunk(const float* __restrict__ q, const T* __restrict__ kc, c
     if (set > 0) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        if (wave + 4 * t >= G) break;
+        if (wave + 4 * t >= GH) break;
         float* hp = hand + (size_t)(8 * (set - 1) + 2 * wave + t) * (HD + 2);
         if (lane == 0) {
           hp[0] = m_run[t];
@@ -372,7 +435,7 @@ IEK_DEV void attn_chunk(const float* __restrict__ q, const T* __restrict__ kc, c
     if (set == 0) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        if (wave + 4 * t >= G) break;
+        if (wave + 4 * t >= GH) break;
         for (int s1 = 1; s1 < SETS; ++s1) {
           const float* hp = hand + (size_t)(8 * (s1 - 1) + 2 * wave + t) * (HD + 2);
           const float m1 = hp[0], l1 = hp[1];
@@ -393,9 +456,10 @@ IEK_DEV void attn_chunk(const float* __restrict__ q, const T* __restrict__ kc, c
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const int g = wave + 4 * t;
-        if (g >= G) break;
+        if (g >= GH) break;
 #pragma unroll
-        for (int d = 0; d < DPL; ++d) st_f<COH>(out + (size_t)(kvh * G + g) * HD + DPL * lane + d, o_run[t][d] / l_run[t]);
+        for (int d = 0; d < DPL; ++d)
+          st_f<COH>(out + (size_t)(kvh * G + gb + g) * HD + DPL * lane + d, o_run[t][d] / l_run[t]);
       }
     }
     return;
@@ -403,8 +467,8 @@ IEK_DEV void attn_chunk(const float* __restrict__ q, const T* __restrict__ kc, c
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int g = wave + 4 * t;
-    if (g >= G || set != 0) break;
-    float* pr = part + ((size_t)(kvh * G + g) * nslot + cp) * (HD + 2);
+    if (g >= GH || set != 0) break;
+    float* pr = part + ((size_t)(kvh * G + gb + g) * nslot + cp) * (HD + 2);
     if (lane == 0) {
       st_f<COH>(pr, m_run[t]);
       st_f<COH>(pr + 1, l_run[t]);
@@ -414,7 +478,7 @@ IEK_DEV void attn_chunk(const float* __restrict__ q, const T* __restrict__ kc, c
   }
   // stream 1's waves pass a wave index past the group: they take part in the arrival only
   merge_if_last<HD, COH, (SETS > 1)>(part, out, counters, kvh, G, nslot, jmin / CK, (total + CK - 1) / CK,
-                                      set ? 8 : wave, S.last, S.wsl);
+                                      set ? 8 : wave, S.last, S.wsl, gb, GH, kvh * HG + hg);
 }
 
 // Slices per chunk for a cache of `max_len` keys: one up to `target` slices per KV head, then

@@ -413,6 +413,16 @@ struct Q4KB {
   }
   IEK_DEV static float d(const Hdr& hd, int j) { return half_bits_to_float(hd.h[j].x); }
   IEK_DEV static float dmin(const Hdr& hd, int j) { return half_bits_to_float(hd.h[j].x >> 16); }
+  // A superblock with d = +-0 contributes only its min term: zero its eight scales (the mins,
+  // in z and the high nibbles of w, stay).
+  IEK_DEV static void zero_d_scales(Hdr& hd) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if ((hd.h[j].x & 0x7FFFu) == 0) {
+        hd.h[j].y = 0u;
+        hd.h[j].w &= 0xF0F0F0F0u;
+      }
+  }
   IEK_DEV static qu4_t mins(const Hdr& hd, int j, bool live) { return q4k_mins(hd.h[j], live); }
 };
 
@@ -473,6 +483,11 @@ struct Q6RB {
   }
   IEK_DEV static float d(const Hdr& hd, int j) { return half_bits_to_float(hd.d[j]); }
   IEK_DEV static float dmin(const Hdr&, int) { return 0.f; }
+  IEK_DEV static void zero_d_scales(Hdr& hd) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if ((hd.d[j] & 0x7FFFu) == 0) hd.sc[0][j] = hd.sc[1][j] = 0u;
+  }
   IEK_DEV static qu4_t mins(const Hdr&, int, bool) { return qu4_t{0u, 0u, 0u, 0u}; }
 };
 
@@ -492,9 +507,15 @@ IEK_DEV void kq_deq(int p, int h, const typename T::Hdr& hd, const typename T::R
 
 // TM: 16-row MFMA tiles per wave along M (a wave owns 16 TM x 64); WGM x WGN waves.
 // OCC: waves per SIMD the register allocation must allow (2 caps each wave at 256 registers).
-// FS: apply d per stage (each tile's stage sum is a short MFMA chain folded into the running sum
-// straight away) instead of per superblock (a second full set of partial accumulators).
-template <class T, int WGM, int WGN, int DA, int TM, int OCC = 1, bool FS = false>
+// FM, how the superblock factor d enters the f32 sum:
+//  0: per superblock, acc += d * part (a second full set of accumulators, the partials);
+//  2: rescaled: the MFMAs accumulate straight into acc, which holds sum / D (D = d of the current
+//     superblock); at a superblock end acc = acc * (D / D') - (dmin / D') * mins-term with D' the
+//     next superblock's d, and the output is acc * D. Two VALU ops per element per superblock, no
+//     partials. A superblock with d = 0 keeps D (its scales are zeroed, so only its min term
+//     counts); the rescale's rounding (a few ulp of the running sum per superblock) is far inside
+//     the f32 reordering bound.
+template <class T, int WGM, int WGN, int DA, int TM, int OCC = 1, int FM = 0>
 __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kq_kernel(GemmQArgs g) {
   constexpr int NT = 64 * WGM * WGN;  // threads
   constexpr int WR = 16 * TM;         // rows per wave
@@ -591,6 +612,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kq_kernel(GemmQArgs 
   // wait counts at the loop head are the same on entry and on the back edge.
   const int kt_lo = 4 * sb_lo;
   T::fetch_hdr(rw, vb, lg, sb_lo, nsb, hdr);
+  float Dc[4] = {1.f, 1.f, 1.f, 1.f};  // FM 2: the scale acc is held at, per column tile
 #pragma unroll
   for (int i = 0; i < DB - 1; ++i) T::fetch(rw, vb, lg, min(kt_lo + i, kt_last), rb[i]);
   fetch_a(kt_lo, ra[0]);
@@ -619,17 +641,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kq_kernel(GemmQArgs 
       if (p == 0) T::fetch_hdr(rw, vb, lg, min(sb + 1, sb_hi - 1), nsb, hdrn);
       if (T::MINS && p == 2) fetch_xs(sb);
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (FS) {
+      if constexpr (FM == 2) {
+        if (p == 0) T::zero_d_scales(hdr);
         qu4_t bh[2][4], bl[2][4];
         kq_deq<T>(p, 0, hdr, rb[p % DB], bh[0], bl[0]);
         kq_deq<T>(p, 1, hdr, rb[p % DB], bh[1], bl[1]);
         __builtin_amdgcn_sched_barrier(0);
         T::fetch(rw, vb, lg, min(kt + DB, kt_last), rb[p % DB]);
         __builtin_amdgcn_sched_barrier(0);
-        float dj[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) dj[j] = T::d(hdr, j);
-        // activation operands of both k-halves, one m-tile ahead of the MFMAs that use them
         qu4_t a4[2][4];
         auto rd4 = [&](int i, qu4_t (&x)[4]) {
           const int row = WR * wm + 16 * i + lr;
@@ -647,29 +666,38 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kq_kernel(GemmQArgs 
           const qu4_t(&x)[4] = a4[i & 1];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            qf4_t t = mfma16(x[0], bh[0][j], qf4_t{0.f, 0.f, 0.f, 0.f});
-            t = mfma16(x[1], bh[0][j], t);
-            if constexpr (T::LO) t = mfma16(x[0], bl[0][j], t);
-            t = mfma16(x[2], bh[1][j], t);
-            t = mfma16(x[3], bh[1][j], t);
-            if constexpr (T::LO) t = mfma16(x[2], bl[1][j], t);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[i][j][r] += dj[j] * t[r];
+            acc[i][j] = mfma16(x[0], bh[0][j], acc[i][j]);
+            acc[i][j] = mfma16(x[1], bh[0][j], acc[i][j]);
+            if constexpr (T::LO) acc[i][j] = mfma16(x[0], bl[0][j], acc[i][j]);
+            acc[i][j] = mfma16(x[2], bh[1][j], acc[i][j]);
+            acc[i][j] = mfma16(x[3], bh[1][j], acc[i][j]);
+            if constexpr (T::LO) acc[i][j] = mfma16(x[2], bl[1][j], acc[i][j]);
           }
         }
         if (p == 3) {
-          if constexpr (T::MINS) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const float dmin = T::dmin(hdr, j);
+          for (int j = 0; j < 4; ++j) {
+            const float dcur = T::d(hdr, j), dnext = T::d(hdrn, j);
+            const float D = sb == sb_lo ? (dcur != 0.f ? dcur : 1.f) : Dc[j];
+            const float Dn = dnext != 0.f ? dnext : D;
+            const float inv = __builtin_amdgcn_rcpf(Dn);
+            const float r = D * inv;
+            if constexpr (T::MINS) {
+              const float cm = T::dmin(hdr, j) * inv;
               const qu4_t mb = T::mins(hdr, j, lg < 2);
 #pragma unroll
               for (int i = 0; i < TM; ++i) {
                 const qf4_t mp = mfma16(xsv[i], mb, qf4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-                for (int r = 0; r < 4; ++r) acc[i][j][r] -= dmin * mp[r];
+                for (int e = 0; e < 4; ++e) acc[i][j][e] = acc[i][j][e] * r - cm * mp[e];
               }
+            } else {
+#pragma unroll
+              for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[i][j][e] *= r;
             }
+            Dc[j] = Dn;
           }
           hdr = hdrn;
         }
@@ -743,7 +771,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kq_kernel(GemmQArgs 
       for (int r = 0; r < 4; ++r) {
         const int m = m0 + WR * wm + 16 * i + 4 * lg + r;
         if (m < M && n < N) {
-          float v = acc[i][j][r];
+          float v = FM == 2 ? acc[i][j][r] * Dc[j] : acc[i][j][r];
           if (resid) v = resid[(size_t)m * N + n] + v;
           dst[(size_t)m * N + n] = v;
         }
@@ -798,7 +826,7 @@ static void gemm_q_launch(GemmQArgs g, hipStream_t st) {
   hipLaunchKernelGGL((gemm_q_kernel<DT, BM, BN>), dim3(tiles), dim3(256), 0, st, g);
 }
 
-template <class T, int WGM, int WGN, int DA, int TM = 4, int OCC = 1, bool FS = false>
+template <class T, int WGM, int WGN, int DA, int TM = 4, int OCC = 1, int FM = 0>
 static void gemm_kq_launch(GemmQArgs g, hipStream_t st) {
   constexpr int BM = 16 * TM * WGM, BN = 64 * WGN;
   int t = 0;
@@ -813,7 +841,7 @@ static void gemm_kq_launch(GemmQArgs g, hipStream_t st) {
   // down projections at a 512-token prompt fill half the chip)
   const size_t mn = (size_t)g.M * g.n[0];
   g.ksplit = (g.kpart && g.nseg == 1 && 2 * tiles <= num_cus() && g.K / QK_K >= 2 && mn % 4 == 0) ? 2 : 1;
-  hipLaunchKernelGGL((gemm_kq_kernel<T, WGM, WGN, DA, TM, OCC, FS>), dim3(tiles * g.ksplit), dim3(64 * WGM * WGN),
+  hipLaunchKernelGGL((gemm_kq_kernel<T, WGM, WGN, DA, TM, OCC, FM>), dim3(tiles * g.ksplit), dim3(64 * WGM * WGN),
                      0, st, g);
   if (g.ksplit == 2) {
     const int blocks = (int)std::min<size_t>((mn / 4 + 255) / 256, 2048);
@@ -825,9 +853,11 @@ static void gemm_kq_launch(GemmQArgs g, hipStream_t st) {
 // activation tile is shared) with one activation stage in flight: measured 15% faster than
 // 128 x 128 at the Mistral-7B prefill shapes, and deeper activation prefetch (two or four stages)
 // or eight waves of 32 x 64 gained nothing. Q4_K GEMMs with at least two tiles per CU (gate/up at
-// a 512-token prompt: 896 tiles) apply d per stage, which frees the superblock partials so two
-// waves share each SIMD: 7% faster there, but slower on grids that then pack two workgroups on
-// some CUs and none on others. Q6_K's fp16 weight pairs do not fit two waves per SIMD.
+// a 512-token prompt: 896 tiles) keep a rescaled accumulator instead of superblock partials, so
+// two waves share each SIMD (d applied per 64-wide stage the same way was 3% slower: four times
+// the folding); on smaller grids, which then pack two workgroups on some CUs and none on others,
+// it is slower (Q/K/V at 512 rows: 74 -> 80 us). Q6_K's fp16 weight pairs do not fit two waves
+// per SIMD (the rescaled form spills there and is 30% slower; at one wave per SIMD 7% slower).
 template <class T>
 static void gemm_kq(GemmQArgs g, hipStream_t st) {
   size_t nt = 0;
@@ -835,7 +865,7 @@ static void gemm_kq(GemmQArgs g, hipStream_t st) {
   const size_t tiles = nt * (size_t)((g.M + 63) / 64);
   if constexpr (T::MINS) {
     if (tiles >= 2 * (size_t)num_cus()) {
-      gemm_kq_launch<T, 1, 4, 1, 4, 2, true>(g, st);
+      gemm_kq_launch<T, 1, 4, 1, 4, 2, 2>(g, st);
       return;
     }
   }

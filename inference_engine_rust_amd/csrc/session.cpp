@@ -1003,8 +1003,39 @@ double Session::bench_kernel(int which, int reps, double* work) {
       float* outs[2] = {g_, u_};
       project_q(w2, outs, 2, M, H_, nullptr);
     };
+  } else if (which == 2 || which == 3) {
+    // 2: the down projection + residual (split K where the prefill splits it); 3: Q/K/V. The
+    // input pair is whatever the GEMM input buffer holds (the timing does not depend on values).
+    if (gemma_ || !state_prefill_ || state_rows_ < 2) fail(ST_OP, "bench_kernel: needs a Mistral/Llama prefill state");
+    const int M = state_rows_;
+    period = L;
+    for (int li = 0; li < L; ++li) {
+      const LayerTensors& T = m_->layers[li];
+      const LayerSpec& S = c.layers[li];
+      if (which == 2) {
+        const DevTensor* ws[1] = {&T.down};
+        if (!quant_ready(ws, 1, M, S.ffn_dim)) fail(ST_OP, "bench_kernel: down does not run on the K-quant GEMM");
+        total += 2.0 * M * S.ffn_dim * H_;
+      } else {
+        const DevTensor* ws[3] = {&T.wq, &T.wk, &T.wv};
+        if (!quant_ready(ws, 3, M, H_)) fail(ST_OP, "bench_kernel: Q/K/V do not share one K-quant GEMM");
+        total += 2.0 * M * H_ * ((double)S.q_dim + 2.0 * S.kv_dim);
+      }
+    }
+    launch = [&, M, which](int i) {
+      const LayerTensors& T = m_->layers[i % L];
+      if (which == 2) {
+        const DevTensor* ws[1] = {&T.down};
+        float* outs[1] = {x_};
+        project_q(ws, outs, 1, M, c.layers[i % L].ffn_dim, x_, kpart_ok_ ? tmp_ : nullptr);
+      } else {
+        const DevTensor* ws[3] = {&T.wq, &T.wk, &T.wv};
+        float* outs[3] = {q_, k_, v_};
+        project_q(ws, outs, 3, M, H_, nullptr);
+      }
+    };
   } else {
-    fail(ST_OP, "bench_kernel: which must be 0 or 1");
+    fail(ST_OP, "bench_kernel: which must be 0, 1, 2 or 3");
   }
   *work = total / period;
   hipEvent_t e0, e1;

@@ -252,7 +252,8 @@ class InferenceSession:
 
     def bench_kernel(self, which: int, reps: int) -> tuple[float, float]:
         """(mean us per launch, algorithmic bytes or flops per launch) of the hot kernel `which`
-        (0: middle-layer decode chain launch, 1: prefill gate/up GEMM); resets the session."""
+        (0: middle-layer decode chain launch, 1: prefill gate/up GEMM, 2: prefill down GEMM,
+        3: prefill Q/K/V GEMM); resets the session."""
         us, work = ctypes.c_double(), ctypes.c_double()
         _check(lib().iek_session_bench_kernel(self._h, which, reps, ctypes.byref(us), ctypes.byref(work)))
         return us.value, work.value
