@@ -7,6 +7,10 @@ Timing regions mirror the reference's src/bench_metrics.rs:
   * decode tok/s (:158-186) = n / time of n x (greedy_next_token + decode_token); here the n
     steps run as n replays of the captured decode-step graph (iek_session_generate_greedy).
 A "step" is one greedy decode token. Prints one JSON line.
+
+Configurations (--config): c2 (default, the headline), c3 (Gemma-4-E2B shape, Q8_0), c4 (c2 with
+an 8192-token prompt), c0 (the tiny model: latency, not a roofline fraction) and c1 (the isolated
+matmul kernels at the Mistral-7B shapes, M = 1 and M = 512).
 """
 import argparse
 import json
@@ -105,8 +109,72 @@ def measured_traffic(algo_bytes):
 
 
 COPY_BYTES = 256 << 20
-# prompt lengths of the benchmark configurations
+# prompt lengths, decode steps and warmup steps of the benchmark configurations
 DEFAULT_PROMPT = {"c0": 16, "c2": 512, "c3": 256, "c4": 8192}
+DEFAULT_STEPS = {"c0": 32, "c4": 256}
+DEFAULT_WARMUP = {"c0": 4}
+# C1: (weights, N, K, iek dtype, ggml type); weights N x K as the model's projections hold them
+C1_SHAPES = [("attn_q / attn_output", 4096, 4096, 1, 12), ("attn_k / attn_v", 1024, 4096, 1, 12),
+             ("ffn_gate / ffn_up", 14336, 4096, 1, 12), ("ffn_down", 4096, 14336, 2, 14)]
+C1_ROTATE_BYTES = 320 << 20  # copies of each weight rotated per launch: more than the 256 MB last-level cache
+
+
+def c1_kernels(E, synth, reps):
+    """C1: the op-level device matmul (iek_dev_matmul) at each Mistral-7B projection shape, for
+    M = 1 (the decode matvec, HBM-bound) and M = 512 (the prefill GEMM, MFMA-bound), x ~ N(0, 1)
+    f32 and N(0, 0.02) weights quantised Q4_K / Q6_K. Launch i reads weight copy i % copies, the
+    copies together over C1_ROTATE_BYTES, so HBM, not the last-level cache, feeds the weights.
+    Timed with HIP events on the stream the calls run on, after one warm pass over the copies. At
+    M = 512 a call also splits x into its fp16 pair and per-32 sums and, for Q6_K, regroups the
+    weight (the op-level entry takes native blocks; the model path keeps a regrouped copy)."""
+    import numpy as np
+    import torch
+
+    rng = np.random.default_rng(0)
+    st = torch.cuda.current_stream()
+    rows = []
+    for name, N, K, dt, gt in C1_SHAPES:
+        wq = synth.quantize(gt, rng.normal(0.0, 0.02, size=N * K).astype(np.float32))
+        wb = wq.size
+        slot = (wb + 255) // 256 * 256
+        copies = max(2, -(-C1_ROTATE_BYTES // wb))
+        w1 = torch.from_numpy(wq).to("cuda")
+        wd = torch.empty(copies * slot, dtype=torch.uint8, device="cuda")
+        for c in range(copies):
+            wd[c * slot:c * slot + wb].copy_(w1)
+        del w1
+        for M in (1, 512):
+            a = torch.randn(M, K, device="cuda", dtype=torch.float32, generator=torch.Generator("cuda").manual_seed(1))
+            o = torch.empty(M, N, device="cuda", dtype=torch.float32)
+
+            def call(i):
+                E.matmul(a.data_ptr(), M, K, dt, wd.data_ptr() + (i % copies) * slot, wb, N, o.data_ptr(),
+                         st.cuda_stream)
+
+            for i in range(copies):
+                call(i)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            for i in range(reps):
+                call(i)
+            e1.record(st)
+            e1.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / reps
+            r = {"weights": name, "dtype": "Q4_K" if dt == 1 else "Q6_K", "N": N, "K": K, "M": M,
+                 "weight_bytes": wb, "copies": copies, "avg_us": round(us, 3)}
+            if M == 1:
+                gbs = (wb + 4 * (K + N)) / (us * 1e-6) / 1e9
+                r.update({"bound": "hbm", "achieved": round(gbs, 1), "unit": "GB/s",
+                          "frac": round(gbs / HBM_PEAK_GBS, 4)})
+            else:
+                tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
+                r.update({"bound": "mfma", "achieved": round(tf, 1), "unit": "TFLOP/s",
+                          "frac": round(tf / MFMA_PEAK_TFLOPS, 4)})
+            rows.append(r)
+            print(f"[bench] c1 {name} {N}x{K} M={M}: {us:.2f} us, {r['achieved']} {r['unit']}", file=sys.stderr,
+                  flush=True)
+        del wd
+    return rows
 
 
 def probe_traffic(E, model, cfg, prompt, reps):
@@ -213,6 +281,15 @@ def golden_tokens_match(E, sess, prompt, cfg_name):
     """The first greedy tokens of the C2 model against the committed oracle run (tests/golden/
     c2_seed0_tokens.json, same model and prompt): equal wherever the oracle's two best logits are
     at least GAP_EXACT apart; at a closer step either of the two ends the comparison."""
+    if cfg_name == "c0" and len(prompt) == 16:
+        # C0: the oracle's 32 greedy tokens (tests/golden/c0_seed0.json), exact
+        with open(os.path.join(ROOT, "tests", "golden", "c0_seed0.json")) as f:
+            g = json.load(f)
+        if list(prompt) != g["prompt"]:
+            return None
+        sess.reset()
+        sess.prefill(prompt)
+        return sess.generate_greedy(len(g["tokens"])) == g["tokens"]
     if cfg_name != "c2" or len(prompt) != 512:
         return None
     with open(GOLDEN_TOKENS) as f:
@@ -230,8 +307,8 @@ def golden_tokens_match(E, sess, prompt, cfg_name):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=128)
-    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--steps", type=int, default=None, help="decode steps timed (default 128; c0 32, c4 256)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed decode steps first (default 8; c0 4)")
     ap.add_argument("--config", default="c2")
     ap.add_argument("--prompt", type=int, default=None,
                     help="prompt tokens (default: the configuration's own: c0 16, c2 512, c3 256, c4 8192)")
@@ -255,9 +332,21 @@ def main():
     from inference_engine_rust_amd import engine as E
     from inference_engine_rust_amd import synth
 
+    if args.config == "c1":
+        rows = c1_kernels(E, synth, args.kernel_reps)
+        print(json.dumps({"metric": "C1 isolated matmul kernels, 1x MI355X", "n_gpus": 1, "dtype": "f32",
+                          "data": "synthetic (x ~ N(0,1) f32, N(0,0.02) weights quantised Q4_K / Q6_K)",
+                          "config": {"workload": "c1: the Mistral-7B projection shapes through the op-level "
+                                                 "device matmul, M = 1 and M = 512", "launches": args.kernel_reps},
+                          "kernels": rows}), flush=True)
+        return
     spec = synth.preset(args.config)
     if args.prompt is None:
         args.prompt = DEFAULT_PROMPT.get(args.config, 512)
+    if args.steps is None:
+        args.steps = DEFAULT_STEPS.get(args.config, 128)
+    if args.warmup is None:
+        args.warmup = DEFAULT_WARMUP.get(args.config, 8)
     path = args.model
     if path is None:
         d = "/dev/shm" if os.path.isdir("/dev/shm") else "/tmp"
@@ -325,9 +414,12 @@ def main():
     roof = roof_pf = match = None
     if not gemma:
         match = golden_tokens_match(E, sess, prompt, args.config)
-        roof = kernel_roofline(E, model, prompt, args.kernel_reps)
-        print(f"[bench] dominant kernel {roof['achieved']} GB/s ({roof['avg_launch_us']} us/launch)",
-              file=sys.stderr, flush=True)
+        # the chain launch is the dominant decode kernel where the session decodes through it (the
+        # tiny C0 model, whose FFN width is not a multiple of 256, runs per-launch kernels: latency)
+        if sess.decode_path() == 1:
+            roof = kernel_roofline(E, model, prompt, args.kernel_reps)
+            print(f"[bench] dominant kernel {roof['achieved']} GB/s ({roof['avg_launch_us']} us/launch)",
+                  file=sys.stderr, flush=True)
         roof_pf = prefill_roofline(E, model, prompt, max(args.kernel_reps // 4, 8))
         print(f"[bench] prefill gate/up GEMM {roof_pf['achieved']} TFLOP/s ({roof_pf['avg_launch_us']} us/launch)",
               file=sys.stderr, flush=True)
