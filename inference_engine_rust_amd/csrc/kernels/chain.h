@@ -11,7 +11,7 @@ enum ChainEpi : int {
   CE_STORE = 0,   // out[seg][row] = dot
   CE_RESID = 1,   // out[row] = resid[row] + dot (one segment)
   CE_SWIGLU = 2,  // seg 0 = gate, seg 1 = up: out[row] = silu(gate.x) * (up.x) into seg[0].out
-  CE_QKV = 3,     // segments q, k, v: RoPE on q and k pairs, q -> seg[0].out, k / v -> fp16 cache at pos
+  CE_QKV = 3,     // segments q, k, v: RoPE on q and k pairs, q -> seg[0].out, k / v -> the f32 cache at pos
   CE_ARGMAX = 4,  // logits -> seg[0].out (optional soft cap), packed (value, first index) key maximum
 };
 

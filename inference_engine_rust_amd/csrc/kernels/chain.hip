@@ -19,7 +19,7 @@
 //  * The control wave stages the phase input x into LDS (coherent copies: x was written by other
 //    workgroups in this launch), in the register layout the consumers read (lane l's 64 values
 //    as 16 float4 columns), with the RMSNorm sum of squares when the phase has a norm; it waits
-//    for the consumers' partial dots, runs the epilogue (residual, SwiGLU, RoPE + fp16 KV append,
+//    for the consumers' partial dots, runs the epilogue (residual, SwiGLU, RoPE + f32 KV append,
 //    logits + argmax), stores the outputs with coherent stores and arrives at the phase barrier.
 //  * Phase barrier: two-level arrival counters (eight groups of workgroups, then one counter),
 //    agent-scope relaxed atomics; every wait is bounded and a timeout sets `err` and ends the

@@ -1,5 +1,5 @@
 // Gemma-4 pieces of the token loop that the Mistral path does not have:
-//   per-head RMSNorm of q and k, scale-free RMSNorm of v, then RoPE and the fp16 KV append
+//   per-head RMSNorm of q and k, scale-free RMSNorm of v, then RoPE and the KV append
 //     (src/layers/attention.rs:277-308, 424-455; src/ops/rmsnorm.rs:8-23)
 //   post-norm + residual, with the layer output scale folded into the last one of a layer
 //     (attention.rs:696-940 Gemma branch; src/layers/ffn.rs:120-167, 170-240, 242-278)
@@ -23,9 +23,9 @@ IEK_DEV float rms_value(float ss, int dim, float eps) {
 // [nq + nkv, nq + 2 nkv) v heads (absent when the layer borrows its cache). q/k: RMSNorm with the
 // head weight when one is given, then RoPE on pairs (2p, 2p+1), p < npairs, at the row's position;
 // v: x / rms when vnorm. k and v are written back as f32 (prefill attention reads them) and, when
-// kc is set, appended to the cache as fp16. Positions: a decode step reads both from pos_dev; a
-// prompt rotates row r at rope0 + r (the reference's prompt positions start at 0) and appends it
-// at kv0 + r (the cache's current length).
+// kc is set, appended to the cache (f32, or fp16 when kv_f32 is 0). Positions: a decode step
+// reads both from pos_dev; a prompt rotates row r at rope0 + r (the reference's prompt positions
+// start at 0) and appends it at kv0 + r (the cache's current length).
 template <int EPL>
 __global__ __launch_bounds__(64) void head_prep_kernel(float* __restrict__ q, float* __restrict__ k,
                                                        float* __restrict__ v, int q_stride, int kv_stride, int nq,

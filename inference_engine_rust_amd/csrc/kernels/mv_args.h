@@ -10,7 +10,7 @@ enum MvEpilogue : int {
   EPI_STORE = 0,   // out[s][n] = dot
   EPI_RESID = 1,   // out[0][n] = resid[n] + dot
   EPI_SWIGLU = 2,  // w[0] = gate, w[1] = up: out[0][n] = silu(gate.x) * (up.x)
-  EPI_QKV = 3,     // segments q, k, v: RoPE on q and k pairs, q -> out[0], k/v -> fp16 KV cache at *pos
+  EPI_QKV = 3,     // segments q, k, v: RoPE on q and k pairs, q -> out[0], k/v -> the KV cache (f32 or fp16) at *pos
   EPI_ARGMAX = 4,  // logits -> out[0] (optional soft cap), atomicMax of packed (value, first index)
   EPI_GEGLU = 5,   // w[0] = gate, w[1] = up: out[0][n] = gelu_tanh(gate.x) * (up.x)
   EPI_GELU_MUL = 6,  // out[0][n] = gelu_tanh(dot) * mulv[n]

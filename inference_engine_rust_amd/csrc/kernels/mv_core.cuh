@@ -12,7 +12,7 @@
 //     dequantising in registers; per-sub-block scales are applied once per chunk:
 //        sum_k x_k (d*sc*q_k - dmin*m) = (d*sc) * sum x_k q_k - (dmin*m) * sum x_k;
 //  4. a wave butterfly leaves the R row sums in every lane; lanes 0..R-1 run the epilogue
-//     (store, residual add, SwiGLU pair, RoPE + fp16 KV append, or logits + argmax).
+//     (store, residual add, SwiGLU pair, RoPE + KV append, or logits + argmax).
 // Weights are streamed exactly once per token as 16-byte coalesced loads; x never leaves LDS.
 #pragma once
 #include <algorithm>

@@ -1,4 +1,4 @@
-// Small ops: block dequant, embedding gather, RMSNorm, RoPE (+fp16 KV append), gated
+// Small ops: block dequant, embedding gather, RMSNorm, RoPE (+KV append), gated
 // activations, residual add, softmax and the on-device greedy argmax.
 // Each follows the reference op it replaces (src/ops/*.rs). HIP's __fmul_rn/__fadd_rn are plain
 // operators that clang may still fuse into FMAs, so functions whose f32 steps the reference rounds
