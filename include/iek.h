@@ -56,6 +56,16 @@ typedef struct iek_model_config {
   float final_logit_softcapping;
 } iek_model_config;
 
+/* TokenizerPromptConfig (src/model_config.rs:8-60): BOS/EOS insertion of
+ * Tokenizer::encode_with_prompt_config (src/tokenizer/backend.rs:83-96) and the EOS stop of the
+ * greedy CLI (src/main.rs:100-105). From tokenizer.ggml.{add_bos_token, add_eos_token,
+ * bos_token_id, eos_token_id}; when the add_* keys are absent, tokenizer.ggml.model "llama" adds
+ * BOS and not EOS, any other model neither; ids default to 1 and 2. */
+typedef struct iek_tokenizer_prompt {
+  int32_t add_bos_token, add_eos_token;
+  uint32_t bos_token_id, eos_token_id;
+} iek_tokenizer_prompt;
+
 /* Last error message of the calling thread. */
 const char* iek_last_error(void);
 
@@ -76,6 +86,8 @@ typedef struct iek_load_timings {
 iek_status iek_model_load_timings(const iek_model* model, iek_load_timings* out);
 /* LoadedModel::config (src/loaded_model.rs:51-53). */
 iek_status iek_model_config_get(const iek_model* model, iek_model_config* out);
+/* LoadedModel::tokenizer_prompt (src/loaded_model.rs:80-82). */
+iek_status iek_model_tokenizer_prompt(const iek_model* model, iek_tokenizer_prompt* out);
 /* Per-layer LayerAttentionSpec + LayerDims (model_config.rs:72-100, :484-629): window -1 = none,
  * kv_borrow -1 = none. */
 iek_status iek_model_layer_spec(const iek_model* model, uint64_t layer, int64_t* sliding_window, float* rope_theta,
@@ -105,6 +117,13 @@ iek_status iek_session_logits_last_token(iek_session* s, float* out, size_t out_
 /* greedy_next_token (src/engine/generation.rs:10-16) with argmax on the device
  * (sampling.rs:25-49: first maximal index; IEK_ERR_SAMPLING on any non-finite logit). */
 iek_status iek_greedy_next_token(iek_session* s, uint32_t* out_token);
+/* sample_temperature (src/engine/sampling.rs:54-79) on the session's last-token logits, on the
+ * device: softmax(logits / temperature), then the first index whose cumulative probability
+ * exceeds r, the caller's uniform draw in [0, 1) (the reference's rng.gen_range(0.0..1.0)).
+ * IEK_ERR_SAMPLING for an empty vocabulary or a temperature that is not finite and positive;
+ * IEK_ERR_OP for r outside [0, 1). NaN or +inf among the scaled logits gives the last index, as
+ * the reference's NaN probabilities do. */
+iek_status iek_session_sample_temperature(iek_session* s, float temperature, float r, uint32_t* out_token);
 /* n iterations of { id = greedy_next_token; decode_token(id) } — the loop of src/main.rs:100-116
  * and EngineBench::run_decode_throughput (src/bench_metrics.rs:178-182) — replayed as one
  * captured decode-step graph; token ids never leave the device until the end. */
@@ -189,6 +208,9 @@ iek_status iek_residual_add(const float* a, const float* b, float* out, size_t n
 /* argmax_index / sample_greedy (src/engine/sampling.rs:25-49): first maximal index;
  * IEK_ERR_SAMPLING when n == 0 or any logit is non-finite. */
 iek_status iek_argmax(const float* logits, size_t n, uint32_t* out_index);
+/* sample_temperature (src/engine/sampling.rs:54-79) over host logits; r is the caller's uniform
+ * draw in [0, 1). Errors as iek_session_sample_temperature. */
+iek_status iek_sample_temperature(const float* logits, size_t n, float temperature, float r, uint32_t* out_index);
 /* The attention of decode_attention_layer (src/layers/attention.rs:608-650) for one new token,
  * its K/V already appended: for every query head h (KV head h / (n_heads / n_kv_heads)),
  * out[h] = softmax(scale * q[h] . K[j]) . V[j] over positions j in [j_min, total_pos), j_min =
@@ -217,6 +239,9 @@ iek_status iek_dev_gelu_tanh(const float* gate, const float* up, float* out, siz
 iek_status iek_dev_residual_add(const float* a, const float* b, float* out, size_t n, void* stream);
 /* Waits for the stream; *out_index is a host location. */
 iek_status iek_dev_argmax(const float* logits, size_t n, uint32_t* out_index, void* stream);
+/* Waits for the stream; *out_index is a host location. */
+iek_status iek_dev_sample_temperature(const float* logits, size_t n, float temperature, float r, uint32_t* out_index,
+                                      void* stream);
 /* iek_attention_decode over the session's cache layout: k_cache / v_cache are
  * [n_kv_heads][max_seq_len][head_dim] of kv_dtype (IEK_F16 or IEK_F32) with positions
  * [0, total_pos) filled; total_pos <= max_seq_len (IEK_ERR_KV_CACHE otherwise). The partial

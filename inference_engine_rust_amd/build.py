@@ -44,6 +44,7 @@ SOURCES = [
     "kernels/gemma.hip",
     "kernels/chain.hip",
     "kernels/noalloc.hip",
+    "kernels/sampling.hip",
     "model.cpp",
     "session.cpp",
     "api.cpp",

@@ -103,6 +103,16 @@ iek_status iek_model_config_get(const iek_model* m, iek_model_config* o) {
   })
 }
 
+iek_status iek_model_tokenizer_prompt(const iek_model* m, iek_tokenizer_prompt* o) {
+  IEK_API_TRY({
+    const Config& c = m->m->cfg;
+    o->add_bos_token = c.add_bos;
+    o->add_eos_token = c.add_eos;
+    o->bos_token_id = c.bos_id;
+    o->eos_token_id = c.eos_id;
+  })
+}
+
 iek_status iek_model_layer_spec(const iek_model* m, uint64_t li, int64_t* window, float* theta, uint64_t* rot,
                                 int64_t* borrow, uint64_t* hd, uint64_t* fd) {
   IEK_API_TRY({
@@ -163,6 +173,10 @@ iek_status iek_session_logits_last_token(iek_session* s, float* out, size_t n) {
 }
 
 iek_status iek_greedy_next_token(iek_session* s, uint32_t* out) { IEK_API_TRY(*out = s->s->greedy_next_token()) }
+
+iek_status iek_session_sample_temperature(iek_session* s, float temperature, float r, uint32_t* out) {
+  IEK_API_TRY(*out = s->s->sample_temperature(temperature, r))
+}
 
 iek_status iek_session_generate_greedy(iek_session* s, size_t n, uint32_t* out) {
   IEK_API_TRY({
@@ -400,6 +414,33 @@ iek_status iek_dev_argmax(const float* logits, size_t n, uint32_t* out_index, vo
   })
 }
 
+// sample_temperature over device logits into a 4-byte device word, then to the host
+static uint32_t sample_dev(const float* logits, size_t n, float temperature, float r, uint32_t* word, hipStream_t st) {
+  if (n > (size_t)INT32_MAX) fail(ST_OP, "sample_temperature: too many logits");
+  launch_sample_temperature(logits, (int)n, temperature, r, word, st);
+  after_launch();
+  uint32_t host = 0;
+  IEK_HIP(hipMemcpyAsync(&host, word, 4, hipMemcpyDeviceToHost, st));
+  IEK_HIP(hipStreamSynchronize(st));
+  return host;
+}
+
+iek_status iek_dev_sample_temperature(const float* logits, size_t n, float temperature, float r, uint32_t* out_index,
+                                      void* stream) {
+  IEK_API_TRY({
+    if (n == 0) fail(ST_SAMPLING, "logits slice is empty");
+    uint32_t* word = nullptr;
+    IEK_HIP(hipMalloc(&word, 64));
+    try {
+      *out_index = sample_dev(logits, n, temperature, r, word, as_stream(stream));
+    } catch (...) {
+      (void)hipFree(word);
+      throw;
+    }
+    IEK_HIP(hipFree(word));
+  })
+}
+
 iek_status iek_dev_attention_decode(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
                                     size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t max_seq_len,
                                     size_t total_pos, size_t sliding_window, float scale, float* out, void* stream) {
@@ -620,6 +661,15 @@ iek_status iek_argmax(const float* logits, size_t n, uint32_t* out_index) {
     HostCall hc({n * 4, 64});
     const float* dl = hc.up<float>(0, logits, n * 4);
     *out_index = argmax_dev(dl, n, hc.ptr<unsigned long long>(1), hc.st);
+  })
+}
+
+iek_status iek_sample_temperature(const float* logits, size_t n, float temperature, float r, uint32_t* out_index) {
+  IEK_API_TRY({
+    if (n == 0) fail(ST_SAMPLING, "logits slice is empty");
+    HostCall hc({n * 4, 64});
+    const float* dl = hc.up<float>(0, logits, n * 4);
+    *out_index = sample_dev(dl, n, temperature, r, hc.ptr<uint32_t>(1), hc.st);
   })
 }
 

@@ -98,6 +98,9 @@ void launch_softmax(const float* in, float* out, int n, hipStream_t st);
 void launch_argmax(const float* logits, int n, unsigned long long* key_out, int* flags, const int* step, hipStream_t st);
 // tok[0] = argmax index, flags[step] = *flag; with a step counter also list[*step] = index and
 // ++*step; then *key = 0 and *flag = 0.
+// sample_temperature (src/engine/sampling.rs:54-79) into *out_dev; validates n, T and r.
+void launch_sample_temperature(const float* logits, int n, float temperature, float r, uint32_t* out_dev,
+                               hipStream_t st);
 void launch_argmax_finish(unsigned long long* key, int* flag, uint32_t* tok, uint32_t* list, int* flags, int* step,
                           hipStream_t st);
 void launch_softcap(float* z, int n, float cap, hipStream_t st);

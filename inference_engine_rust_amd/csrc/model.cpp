@@ -121,6 +121,31 @@ bool f32_opt(const GgufFile& g, const std::string& k, float* out) {
   return false;
 }
 
+// get_bool (src/model_config.rs:704-709): a GGUF bool only.
+bool bool_opt(const GgufFile& g, const std::string& k, bool* out) {
+  const MetaValue* v = g.meta(k);
+  if (!v || v->type != 7) return false;
+  *out = v->b;
+  return true;
+}
+
+// get_u32 (src/model_config.rs:711-723): any integer type whose value fits u32; no arrays.
+bool u32_opt(const GgufFile& g, const std::string& k, uint32_t* out) {
+  const MetaValue* v = g.meta(k);
+  if (!v) return false;
+  switch (v->type) {
+    case 0: case 2: case 4: case 10:
+      if (v->u > 0xFFFFFFFFull) return false;
+      *out = (uint32_t)v->u;
+      return true;
+    case 1: case 3: case 5: case 11:
+      if (v->i < 0 || v->i > 0xFFFFFFFFll) return false;
+      *out = (uint32_t)v->i;
+      return true;
+  }
+  return false;
+}
+
 std::string str_meta(const GgufFile& g, const std::string& k) {
   const MetaValue* v = g.meta(k);
   return (v && v->type == 8) ? v->s : std::string();
@@ -339,6 +364,15 @@ Config config_from_gguf(const GgufFile& g) {
     c.has_softcap = true;
     c.softcap = f;
   }
+  // TokenizerPromptConfig::from_gguf (src/model_config.rs:35-60): llama.cpp's implicit defaults
+  // for a SentencePiece ("llama") vocabulary are add BOS, no EOS; keys override them
+  const bool spm = str_meta(g, "tokenizer.ggml.model") == "llama";
+  c.add_bos = spm;
+  c.add_eos = false;
+  bool_opt(g, "tokenizer.ggml.add_bos_token", &c.add_bos);
+  bool_opt(g, "tokenizer.ggml.add_eos_token", &c.add_eos);
+  if (!u32_opt(g, "tokenizer.ggml.bos_token_id", &c.bos_id)) c.bos_id = 1;
+  if (!u32_opt(g, "tokenizer.ggml.eos_token_id", &c.eos_id)) c.eos_id = 2;
   return c;
 }
 

@@ -73,6 +73,9 @@ struct Config {
   float ple_combine_scale = 0.f, ple_proj_scale = 0.f;
   bool has_softcap = false;
   float softcap = 0.f;
+  // TokenizerPromptConfig (src/model_config.rs:8-60)
+  bool add_bos = false, add_eos = false;
+  uint32_t bos_id = 1, eos_id = 2;
 };
 
 Config config_from_gguf(const GgufFile& g);

@@ -1299,6 +1299,17 @@ uint32_t Session::greedy_next_token() {
   return tok;
 }
 
+uint32_t Session::sample_temperature(float temperature, float r) {
+  check_state();
+  if (m_->cfg.vocab == 0) fail(ST_SAMPLING, "logits slice is empty");
+  logits_body(false);
+  launch_sample_temperature(logits_, m_->cfg.vocab, temperature, r, d_tok_, st_);
+  uint32_t tok = 0;
+  IEK_HIP(hipMemcpyAsync(&tok, d_tok_, 4, hipMemcpyDeviceToHost, st_));
+  sync();
+  return tok;
+}
+
 void Session::generate_greedy(int n, uint32_t* out_ids, bool use_graph) {
   if (n <= 0) return;
   check_state();

@@ -27,6 +27,7 @@ class Session {
   void decode_token(uint32_t id);                  // session.rs:58-69 (decode_forward)
   void logits_last_token(float* out, int n);       // session.rs:71-74 (final_logits_last_token)
   uint32_t greedy_next_token();                    // generation.rs:10-16
+  uint32_t sample_temperature(float temperature, float r);  // sampling.rs:54-79 on the device
   // n x (greedy_next_token; decode_token), the loop of main.rs:100-116 / bench_metrics.rs:178-182,
   // replayed as one captured decode-step graph. Returns the n chosen ids.
   void generate_greedy(int n, uint32_t* out_ids, bool use_graph = true);

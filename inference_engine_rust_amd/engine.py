@@ -45,6 +45,12 @@ class Weight(ctypes.Structure):
                 ("on_device", ctypes.c_int32)]
 
 
+class TokenizerPrompt(ctypes.Structure):
+    """TokenizerPromptConfig (src/model_config.rs:8-60)."""
+    _fields_ = [("add_bos_token", ctypes.c_int32), ("add_eos_token", ctypes.c_int32),
+                ("bos_token_id", ctypes.c_uint32), ("eos_token_id", ctypes.c_uint32)]
+
+
 class ModelConfig(ctypes.Structure):
     _fields_ = [("family", ctypes.c_int32), ("context_length", ctypes.c_uint64), ("hidden_dim", ctypes.c_uint64),
                 ("n_layers", ctypes.c_uint64), ("n_heads", ctypes.c_uint64), ("n_kv_heads", ctypes.c_uint64),
@@ -62,6 +68,7 @@ EXPORTS = {
     "iek_model_free": ([_P], None),
     "iek_model_load_timings": ([_P, _P], ctypes.c_int),
     "iek_model_config_get": ([_P, ctypes.POINTER(ModelConfig)], ctypes.c_int),
+    "iek_model_tokenizer_prompt": ([_P, ctypes.POINTER(TokenizerPrompt)], ctypes.c_int),
     "iek_model_layer_spec": ([_P, ctypes.c_uint64, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_float),
                               ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_int64),
                               ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
@@ -75,6 +82,8 @@ EXPORTS = {
     "iek_session_decode_token": ([_P, ctypes.c_uint32], ctypes.c_int),
     "iek_session_logits_last_token": ([_P, _P, _SZ], ctypes.c_int),
     "iek_greedy_next_token": ([_P, ctypes.POINTER(ctypes.c_uint32)], ctypes.c_int),
+    "iek_session_sample_temperature": ([_P, ctypes.c_float, ctypes.c_float, ctypes.POINTER(ctypes.c_uint32)],
+                                       ctypes.c_int),
     "iek_session_generate_greedy": ([_P, _SZ, _P], ctypes.c_int),
     "iek_session_kv_len": ([_P, ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
     "iek_session_decode_path": ([_P, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
@@ -98,6 +107,8 @@ EXPORTS = {
     "iek_gelu_tanh": ([_P, _P, _P, _SZ], ctypes.c_int),
     "iek_residual_add": ([_P, _P, _P, _SZ], ctypes.c_int),
     "iek_argmax": ([_P, _SZ, ctypes.POINTER(ctypes.c_uint32)], ctypes.c_int),
+    "iek_sample_temperature": ([_P, _SZ, ctypes.c_float, ctypes.c_float, ctypes.POINTER(ctypes.c_uint32)],
+                               ctypes.c_int),
     "iek_attention_decode": ([_P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P], ctypes.c_int),
     "iek_dev_dequantize": ([ctypes.c_int, _P, _SZ, _P, _P], ctypes.c_int),
     "iek_dev_matmul": ([_P, _SZ, _SZ, ctypes.c_int, _P, _SZ, _SZ, _P, _P], ctypes.c_int),
@@ -109,6 +120,8 @@ EXPORTS = {
     "iek_dev_gelu_tanh": ([_P, _P, _P, _SZ, _P], ctypes.c_int),
     "iek_dev_residual_add": ([_P, _P, _P, _SZ, _P], ctypes.c_int),
     "iek_dev_argmax": ([_P, _SZ, ctypes.POINTER(ctypes.c_uint32), _P], ctypes.c_int),
+    "iek_dev_sample_temperature": ([_P, _SZ, ctypes.c_float, ctypes.c_float, ctypes.POINTER(ctypes.c_uint32), _P],
+                                   ctypes.c_int),
     "iek_dev_attention_decode": ([_P, _P, _P, ctypes.c_int, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P, _P],
                                  ctypes.c_int),
     "iek_dev_attention_decode_noalloc": ([_P, _P, _P, ctypes.c_int, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P,
@@ -162,6 +175,12 @@ class LoadedModel:
         h = ctypes.c_void_p()
         _check(lib().iek_model_load(os.fsencode(path), device, ctypes.byref(h)))
         return cls(h, path)
+
+    def tokenizer_prompt(self) -> TokenizerPrompt:
+        """LoadedModel::tokenizer_prompt (src/loaded_model.rs:80-82)."""
+        t = TokenizerPrompt()
+        _check(lib().iek_model_tokenizer_prompt(self._h, ctypes.byref(t)))
+        return t
 
     def layer_spec(self, layer: int) -> dict:
         w, t, r, b, hd, fd = (ctypes.c_int64(), ctypes.c_float(), ctypes.c_uint64(), ctypes.c_int64(),
@@ -296,6 +315,14 @@ class InferenceSession:
             pass
 
 
+def sample_temperature_next_token(session: InferenceSession, temperature: float, r: float) -> int:
+    """sample_temperature (src/engine/sampling.rs:54-79) over the session's last-token logits on
+    the device; r is the uniform draw in [0, 1) the reference takes from its rng."""
+    v = ctypes.c_uint32()
+    _check(lib().iek_session_sample_temperature(session._h, temperature, r, ctypes.byref(v)))
+    return v.value
+
+
 def greedy_next_token(session: InferenceSession) -> int:
     """generation::greedy_next_token (src/engine/generation.rs:10-16), argmax on the device."""
     v = ctypes.c_uint32()
@@ -383,6 +410,13 @@ def host_residual_add(a, b) -> np.ndarray:
     return out
 
 
+def host_sample_temperature(logits, temperature: float, r: float) -> int:
+    x = _f32(logits)
+    v = ctypes.c_uint32()
+    _check(lib().iek_sample_temperature(_np_ptr(x), x.size, temperature, r, ctypes.byref(v)))
+    return v.value
+
+
 def host_argmax(logits) -> int:
     x = _f32(logits)
     v = ctypes.c_uint32()
@@ -440,6 +474,12 @@ def gelu_tanh(g_ptr: int, u_ptr, out_ptr: int, n: int, stream: int = 0) -> None:
 
 def residual_add(a_ptr: int, b_ptr: int, out_ptr: int, n: int, stream: int = 0) -> None:
     _check(lib().iek_dev_residual_add(a_ptr, b_ptr, out_ptr, n, stream or None))
+
+
+def sample_temperature(logits_ptr: int, n: int, temperature: float, r: float, stream: int = 0) -> int:
+    v = ctypes.c_uint32()
+    _check(lib().iek_dev_sample_temperature(logits_ptr, n, temperature, r, ctypes.byref(v), stream or None))
+    return v.value
 
 
 def argmax(logits_ptr: int, n: int, stream: int = 0) -> int:

@@ -251,3 +251,78 @@ def prompt_ids(seed: int, n: int, vocab: int = 32000) -> np.ndarray:
     """Uniform token ids in [3, vocab) from seed+1 (the benchmark's prompt recipe)."""
     rng = np.random.default_rng(seed + 1)
     return rng.integers(3, vocab, size=n, dtype=np.int64).astype(np.uint32)
+
+
+# GGUF metadata value types (the container format: gguf_types.rs:4-36)
+GGUF_U8, GGUF_I8, GGUF_U16, GGUF_I16, GGUF_U32, GGUF_I32, GGUF_F32, GGUF_BOOL, GGUF_STR = range(9)
+GGUF_ARR, GGUF_U64, GGUF_I64, GGUF_F64 = 9, 10, 11, 12
+_SCALAR = {GGUF_U8: "<B", GGUF_I8: "<b", GGUF_U16: "<H", GGUF_I16: "<h", GGUF_U32: "<I", GGUF_I32: "<i",
+           GGUF_F32: "<f", GGUF_BOOL: "<B", GGUF_U64: "<Q", GGUF_I64: "<q", GGUF_F64: "<d"}
+
+
+def _skip_value(buf: bytes, o: int, t: int) -> int:
+    import struct
+
+    if t in _SCALAR:
+        return o + struct.calcsize(_SCALAR[t])
+    if t == GGUF_STR:
+        (n,) = struct.unpack_from("<Q", buf, o)
+        return o + 8 + n
+    if t == GGUF_ARR:
+        et, n = struct.unpack_from("<IQ", buf, o)
+        o += 12
+        for _ in range(n):
+            o = _skip_value(buf, o, et)
+        return o
+    raise ValueError(f"unknown GGUF value type {t}")
+
+
+def _pack_kv(key: str, t: int, value) -> bytes:
+    import struct
+
+    k = key.encode()
+    out = struct.pack("<Q", len(k)) + k + struct.pack("<I", t)
+    if t in _SCALAR:
+        return out + struct.pack(_SCALAR[t], int(value) if t == GGUF_BOOL else value)
+    if t == GGUF_STR:
+        v = value.encode()
+        return out + struct.pack("<Q", len(v)) + v
+    raise ValueError("with_metadata writes scalar and string values only")
+
+
+def with_metadata(src: str, dst: str, entries) -> str:
+    """Copy the GGUF `src` to `dst` with metadata entries [(key, gguf type, value)] added (an
+    existing key of the same name is replaced). Tensor infos and data are copied unchanged; the
+    data section is re-aligned to general.alignment (32 by default)."""
+    import struct
+
+    buf = open(src, "rb").read()
+    magic, version, n_t, n_kv = struct.unpack_from("<IIQQ", buf, 0)
+    o = 24
+    kvs, align = [], 32
+    drop = {k for k, _, _ in entries}
+    for _ in range(n_kv):
+        (kl,) = struct.unpack_from("<Q", buf, o)
+        key = buf[o + 8:o + 8 + kl].decode()
+        (t,) = struct.unpack_from("<I", buf, o + 8 + kl)
+        end = _skip_value(buf, o + 12 + kl, t)
+        if key == "general.alignment" and t == GGUF_U32:
+            (align,) = struct.unpack_from("<I", buf, o + 12 + kl)
+        if key not in drop:
+            kvs.append(buf[o:end])
+        o = end
+    t0 = o
+    for _ in range(n_t):
+        (nl,) = struct.unpack_from("<Q", buf, o)
+        o += 8 + nl
+        (nd,) = struct.unpack_from("<I", buf, o)
+        o += 4 + 8 * nd + 4 + 8
+    infos = buf[t0:o]
+    data_start = (o + align - 1) // align * align
+    kvs += [_pack_kv(k, t, v) for k, t, v in entries]
+    head = struct.pack("<IIQQ", magic, version, n_t, len(kvs)) + b"".join(kvs) + infos
+    head += b"\0" * ((-len(head)) % align)
+    with open(dst, "wb") as f:
+        f.write(head)
+        f.write(buf[data_start:])
+    return dst

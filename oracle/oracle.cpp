@@ -458,6 +458,23 @@ void residual_add(const float* a, const float* b, float* out, size_t n) {
   for (size_t i = 0; i < n; ++i) out[i] = a[i] + b[i];
 }
 
+// sample_temperature (src/engine/sampling.rs:54-79) for the uniform draw r the reference takes
+// from rng.gen_range(0.0..1.0): -1 = EmptyLogits, -3 = InvalidTemperature; else the first index
+// whose cumulative f32 probability exceeds r, or the last index.
+long sample_temperature(const float* l, size_t n, float temperature, float r) {
+  if (n == 0) return -1;
+  if (!std::isfinite(temperature) || temperature <= 0.0f) return -3;
+  std::vector<float> scaled(n), probs(n);
+  for (size_t i = 0; i < n; ++i) scaled[i] = l[i] / temperature;
+  softmax(scaled.data(), probs.data(), n);
+  float cum = 0.0f;
+  for (size_t i = 0; i < n; ++i) {
+    cum += probs[i];
+    if (r < cum || i + 1 == n) return (long)i;
+  }
+  return (long)(n - 1);
+}
+
 // argmax_index / sample_greedy (src/engine/sampling.rs:25-49):
 // -1 = EmptyLogits, -2 = InvalidLogits (any non-finite); first index wins ties.
 long argmax(const float* l, size_t n) {
@@ -691,6 +708,18 @@ static std::string get_string(const GGUF& g, const std::string& k) {
   const GVal* v = g.meta(k);
   return (v && v->type == G_STR) ? v->s : std::string();
 }
+// get_u32 (model_config.rs:711-723): an integer of any width whose value fits u32, else `dflt`.
+static uint32_t get_u32_or(const GGUF& g, const std::string& k, uint32_t dflt) {
+  const GVal* v = g.meta(k);
+  if (!v) return dflt;
+  switch (v->type) {
+    case G_U8: case G_U16: case G_U32: case G_U64:
+      return v->u <= 0xFFFFFFFFull ? (uint32_t)v->u : dflt;
+    case G_I8: case G_I16: case G_I32: case G_I64:
+      return (v->i >= 0 && v->i <= 0xFFFFFFFFll) ? (uint32_t)v->i : dflt;
+  }
+  return dflt;
+}
 static std::string lower(std::string s) {
   for (auto& c : s) c = (char)tolower((unsigned char)c);
   return s;
@@ -911,6 +940,15 @@ static ModelConfig config_from_gguf(const GGUF& g) {
     c.has_softcap = true;
     c.softcap = cap;
   }
+  // TokenizerPromptConfig::from_gguf (model_config.rs:35-50) with
+  // defaults_for_tokenizer_model (:53-60): "llama" -> (add BOS, no EOS), otherwise neither
+  const bool llama_vocab = get_string(g, "tokenizer.ggml.model") == "llama";
+  c.add_bos_token = llama_vocab;
+  c.add_eos_token = false;
+  if (const GVal* v = g.meta("tokenizer.ggml.add_bos_token"); v && v->type == G_BOOL) c.add_bos_token = v->b;
+  if (const GVal* v = g.meta("tokenizer.ggml.add_eos_token"); v && v->type == G_BOOL) c.add_eos_token = v->b;
+  c.bos_token_id = get_u32_or(g, "tokenizer.ggml.bos_token_id", 1);
+  c.eos_token_id = get_u32_or(g, "tokenizer.ggml.eos_token_id", 2);
   return c;
 }
 
@@ -1578,6 +1616,18 @@ int orc_swiglu(const float* g, const float* u, float* out, size_t n) { ORC_TRY(s
 float orc_gelu_tanh(float x) { return gelu_tanh(x); }
 int orc_residual_add(const float* a, const float* b, float* out, size_t n) { ORC_TRY(residual_add(a, b, out, n)) }
 long orc_argmax(const float* l, size_t n) { return argmax(l, n); }
+long orc_sample_temperature(const float* l, size_t n, float temperature, float r) {
+  return sample_temperature(l, n, temperature, r);
+}
+int orc_model_tokenizer_prompt(void* mp, int* add_bos, int* add_eos, uint32_t* bos, uint32_t* eos) {
+  ORC_TRY({
+    const ModelConfig& c = ((Model*)mp)->cfg;
+    *add_bos = c.add_bos_token;
+    *add_eos = c.add_eos_token;
+    *bos = c.bos_token_id;
+    *eos = c.eos_token_id;
+  })
+}
 int orc_unpack_qk_row(float* row, size_t ng, size_t hd) { ORC_TRY(unpack_qk_row(row, ng, hd)) }
 // decode_heads over a KVCache holding `total` positions ([total][n_kv][head_dim] k and v);
 // sliding_window < 0 = none.

@@ -61,6 +61,12 @@ def lib():
         L.orc_residual_add.argtypes = [_f, _f, _f, ctypes.c_size_t]
         L.orc_argmax.argtypes = [_f, ctypes.c_size_t]
         L.orc_argmax.restype = ctypes.c_long
+        L.orc_sample_temperature.argtypes = [_f, ctypes.c_size_t, ctypes.c_float, ctypes.c_float]
+        L.orc_sample_temperature.restype = ctypes.c_long
+        u32p = ctypes.POINTER(ctypes.c_uint32)
+        ip = ctypes.POINTER(ctypes.c_int)
+        L.orc_model_tokenizer_prompt.argtypes = [ctypes.c_void_p, ip, ip, u32p, u32p]
+        L.orc_model_tokenizer_prompt.restype = ctypes.c_int
         L.orc_unpack_qk_row.argtypes = [_f, ctypes.c_size_t, ctypes.c_size_t]
         L.orc_attention_decode.argtypes = [_f, _f, _f, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
                                            ctypes.c_size_t, ctypes.c_long, ctypes.c_float, _f]
@@ -186,6 +192,13 @@ def argmax(logits) -> int:
     return int(lib().orc_argmax(_p(l), l.size))
 
 
+def sample_temperature(logits, temperature: float, r: float) -> int:
+    """sample_temperature (src/engine/sampling.rs:54-79) for the uniform draw r: the index, or -1
+    (EmptyLogits) / -3 (InvalidTemperature)."""
+    l = np.ascontiguousarray(logits, np.float32)
+    return int(lib().orc_sample_temperature(_p(l), l.size, temperature, r))
+
+
 def unpack_qk_row(row, n_groups, head_dim):
     r = np.array(row, np.float32)
     _check(lib().orc_unpack_qk_row(_p(r), n_groups, head_dim))
@@ -220,6 +233,14 @@ class Model:
                                           ctypes.byref(b), ctypes.byref(hd), ctypes.byref(fd)))
         return dict(sliding_window=w.value, rope_theta=t.value, rotary_dim=r.value, kv_borrow=b.value,
                     head_dim=hd.value, ffn_dim=fd.value)
+
+    def tokenizer_prompt(self):
+        """TokenizerPromptConfig (src/model_config.rs:8-60): (add_bos, add_eos, bos_id, eos_id)."""
+        ab, ae = ctypes.c_int(), ctypes.c_int()
+        b, e = ctypes.c_uint32(), ctypes.c_uint32()
+        _check(lib().orc_model_tokenizer_prompt(self.h, ctypes.byref(ab), ctypes.byref(ae), ctypes.byref(b),
+                                                ctypes.byref(e)))
+        return bool(ab.value), bool(ae.value), int(b.value), int(e.value)
 
     def tensor(self, name: str):
         """(dtype, raw bytes copy, ne0, ne1) of a loaded tensor."""

@@ -19,6 +19,10 @@
 //   rmsnorm / rope / softmax / swiglu / gelu / argmax / unpack_qk
 //                         the reference's own inline known answers (file:line in each test) plus
 //                         closed forms (rope running product, swiglu two-branch sigmoid)
+//   sample_temperature    the reference's tests (sampling.rs:101-115: deterministic for one draw,
+//                         non-positive temperature rejected), two-logit closed form, uniform
+//                         logits -> floor(r n), float64 brute force of the cumulative search
+//   tokenizer prompt cfg  each metadata key alone and absent, both tokenizer.ggml.model defaults
 //   attention + layer     layer 0 of the tiny model recomposed from the pinned ops around a
 //                         brute-force float64 causal GQA attention; prefill N+1 == prefill N +
 //                         decode; greedy loop == teacher-forced re-prefill
@@ -127,6 +131,9 @@ struct ModelConfig {
   std::vector<long> kv_borrow_from;  // -1 = None
   bool has_softcap = false;
   float softcap = 0.f;
+  // TokenizerPromptConfig (src/model_config.rs:8-60)
+  bool add_bos_token = false, add_eos_token = false;
+  uint32_t bos_token_id = 1, eos_token_id = 2;
 };
 
 struct LayerW {

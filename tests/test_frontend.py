@@ -1,0 +1,220 @@
+"""Text front end (CPU): the prompt styles against the reference's own tests (src/chat_prompt.rs:
+245-345), the tokenizer wrapper (src/tokenizer/backend.rs) on tokenizers trained here, and the
+oracle's sample_temperature (src/engine/sampling.rs:54-79) and TokenizerPromptConfig
+(src/model_config.rs:8-60) restatements, pinned by the reference's tests, closed forms and a
+float64 brute force."""
+import math
+import os
+import random
+
+import numpy as np
+import pytest
+
+import oracle as O
+from inference_engine_rust_amd import frontend as F
+from inference_engine_rust_amd import synth
+
+WORDS = ["alpha", "beta", "gamma", "delta", "rust", "engine", "token", "model", "hello", "world", "the", "will",
+         "rule", "paris", "france", "capital"]
+
+
+@pytest.fixture(scope="module")
+def tok_dir(tmp_path_factory):
+    """A SentencePiece model and a Hugging Face tokenizer.json trained on a seeded word corpus."""
+    import sentencepiece as spm
+    from tokenizers import Tokenizer, decoders, models, pre_tokenizers, trainers
+
+    d = tmp_path_factory.mktemp("tok")
+    corpus = d / "corpus.txt"
+    rng = random.Random(0)
+    corpus.write_text("".join(" ".join(rng.choice(WORDS) for _ in range(8)) + "\n" for _ in range(2000)))
+    spm.SentencePieceTrainer.train(input=str(corpus), model_prefix=str(d / "spm"), vocab_size=96, model_type="bpe",
+                                   bos_id=1, eos_id=2, unk_id=0, pad_id=-1, minloglevel=2)
+    hf = Tokenizer(models.BPE(unk_token="<unk>"))
+    hf.pre_tokenizer = pre_tokenizers.Metaspace()
+    hf.decoder = decoders.Metaspace()
+    hf.train([str(corpus)], trainers.BpeTrainer(vocab_size=96, special_tokens=["<unk>", "<s>", "</s>"]))
+    hf.save(str(d / "tokenizer.JSON"))
+    return d
+
+
+# ---- prompt styles: the reference's tests ------------------------------------------------------
+
+def test_chat_prompt_reference_cases():
+    s = F.ChatPromptStyle.GEMMA4_E2B.wrap("Hello")
+    assert s.startswith("<|turn>user\n") and "Hello" in s and "<turn|>\n" in s and s.endswith("<|turn>model\n")
+    assert F.ChatPromptStyle.MISTRAL_INSTRUCT.wrap("Hi") == "[INST] Hi [/INST]"
+    U, A = F.ChatRole.USER, F.ChatRole.ASSISTANT
+    g = F.ChatPromptStyle.GEMMA4_E2B.render_conversation(
+        [F.ChatMessage(U, "Hi"), F.ChatMessage(A, "Hello."), F.ChatMessage(U, "Bye")])
+    assert "<|turn>user\nHi<turn|>\n" in g and "<|turn>model\nHello.<turn|>\n" in g
+    assert "<|turn>user\nBye<turn|>\n" in g and g.endswith("<|turn>model\n")
+    m = F.ChatPromptStyle.MISTRAL_INSTRUCT.render_conversation(
+        [F.ChatMessage(U, "Hi"), F.ChatMessage(A, "Hey."), F.ChatMessage(U, "Ok")])
+    assert "[INST] Hi [/INST]" in m and " Hey." in m and "[INST] Ok [/INST]" in m
+    assert F.gemma4_e2b_truncate_assistant_at_structure("Hello.<turn|>junk") == "Hello."
+    assert F.gemma4_e2b_truncate_assistant_at_structure("Ok.<|turn>user") == "Ok."
+    assert F.gemma4_e2b_strip_dangling_contraction_tail("That's a very short message! I'") == \
+        "That's a very short message!"
+    assert F.gemma4_e2b_assistant_visible("That's a very short message! I'<|turn>user") == \
+        "That's a very short message!"
+    assert F.gemma4_e2b_assistant_visible("Still typing I'") == "Still typing I'"
+    assert F.gemma4_e2b_assistant_visible("<|channel>thought\ninternal\n<channel|>Paris is the capital of France.") \
+        == "Paris is the capital of France."
+    assert F.gemma4_e2b_assistant_visible("Visible prefix. <|channel>thought\nunfinished") == "Visible prefix."
+
+
+def test_chat_prompt_parse_and_errors():
+    assert F.ChatPromptStyle.parse(" RAW ") is F.ChatPromptStyle.RAW
+    assert F.ChatPromptStyle.parse("") is F.ChatPromptStyle.RAW
+    assert F.ChatPromptStyle.parse("instruct") is F.ChatPromptStyle.MISTRAL_INSTRUCT
+    assert F.ChatPromptStyle.parse("gemma-e2b") is F.ChatPromptStyle.GEMMA4_E2B
+    assert F.ChatPromptStyle.parse("llama3") is None
+    U, A = F.ChatRole.USER, F.ChatRole.ASSISTANT
+    st = F.ChatPromptStyle.MISTRAL_INSTRUCT
+    for msgs, msg in (([], "empty"), ([F.ChatMessage(A, "x")], "start with a user"),
+                      ([F.ChatMessage(U, "a"), F.ChatMessage(A, "b")], "end with a user"),
+                      ([F.ChatMessage(U, "a"), F.ChatMessage(U, "b")], "alternate")):
+        with pytest.raises(ValueError, match=msg):
+            st.render_conversation(msgs)
+    with pytest.raises(ValueError, match="raw prompt style"):
+        F.ChatPromptStyle.RAW.render_conversation([F.ChatMessage(U, "a")])
+    # markers inside a thinking block do not count; a marker after it does
+    assert F.gemma4_e2b_assistant_visible("<|channel>x<turn|><channel|>ok") == "ok"
+    assert F.gemma4_e2b_strip_dangling_contraction_tail("we're") == "we're"
+
+
+# ---- tokenizer wrapper --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["spm.model", "tokenizer.JSON"])
+def test_tokenizer_round_trip_and_prompt_config(tok_dir, name):
+    t = F.Tokenizer.load_from_file(str(tok_dir / name))
+    text = "hello world the rust engine will rule"
+    ids = t.encode(text)
+    assert ids and all(isinstance(i, int) for i in ids)
+    assert t.decode_piece_ids(ids) == text
+    cfg = F.TokenizerPromptConfig(add_bos_token=True, add_eos_token=True, bos_token_id=1, eos_token_id=2)
+    assert t.encode_with_prompt_config(text, cfg) == [1] + ids + [2]
+    assert t.encode_with_prompt_config(text, F.TokenizerPromptConfig()) == ids
+    assert t.encode("") == []
+    if name == "spm.model":
+        assert t.vocab_size() == 0
+        assert t.decode(ids).replace("▁", " ").strip() == text  # the pieces encode has seen
+        with pytest.raises(F.TokenizerError, match="missing piece strings"):
+            F.Tokenizer.load_from_file(str(tok_dir / name)).decode(ids)
+    else:
+        assert t.vocab_size() == 96
+        assert t.decode(ids) == text
+
+
+def test_tokenizer_load_errors(tok_dir, tmp_path):
+    bad = tmp_path / "bad.model"
+    bad.write_bytes(b"not a sentencepiece model")
+    with pytest.raises(F.TokenizerError, match="SentencePiece"):
+        F.Tokenizer.load_from_file(str(bad))
+    badj = tmp_path / "bad.json"
+    badj.write_text("{")
+    with pytest.raises(F.TokenizerError, match="tokenizer.json"):
+        F.Tokenizer.load_from_file(str(badj))
+
+
+def test_cli_argument_errors(capsys, tok_dir):
+    assert F.main(["-t", str(tok_dir / "missing.model"), "hi"]) == 1
+    assert "tokenizer file not found" in capsys.readouterr().err
+    assert F.main(["-t", str(tok_dir / "spm.model"), "   "]) == 1
+    assert "prompt is empty" in capsys.readouterr().err
+    assert F.main(["-t", str(tok_dir / "spm.model"), "--chat", "llama3", "hi"]) == 1
+    assert "unknown --chat" in capsys.readouterr().err
+
+
+# ---- oracle: sample_temperature ---------------------------------------------------------------
+
+def _f64_pick(logits, temperature, r):
+    """float64 brute force of the cumulative search and the distance of r to the boundary."""
+    s = np.asarray(logits, np.float64) / temperature
+    p = np.exp(s - s.max())
+    cum = np.cumsum(p / p.sum())
+    i = int(np.searchsorted(cum, r, side="right"))
+    i = min(i, len(cum) - 1)
+    return i, float(np.min(np.abs(cum - r)))
+
+
+def test_oracle_sample_temperature_reference_tests():
+    # sampling.rs:101-115: one draw gives one answer; non-positive temperatures are rejected
+    assert O.sample_temperature([0.0, 1.0, 0.0], 1.0, 0.37) == O.sample_temperature([0.0, 1.0, 0.0], 1.0, 0.37)
+    assert O.sample_temperature([1.0, 2.0], 0.0, 0.5) == -3
+    assert O.sample_temperature([1.0, 2.0], -1.0, 0.5) == -3
+    assert O.sample_temperature([1.0, 2.0], float("nan"), 0.5) == -3
+    assert O.sample_temperature([1.0, 2.0], float("inf"), 0.5) == -3
+    assert O.sample_temperature([], 1.0, 0.5) == -1
+
+
+def test_oracle_sample_temperature_closed_forms():
+    # two logits 0, ln 3 at T = 1: probabilities 1/4, 3/4
+    two = [0.0, math.log(3.0)]
+    assert [O.sample_temperature(two, 1.0, r) for r in (0.0, 0.2, 0.26, 0.9, 0.999)] == [0, 0, 1, 1, 1]
+    # T = 2 halves the logits: 1 / (1 + sqrt 3) = 0.366
+    assert O.sample_temperature(two, 2.0, 0.36) == 0 and O.sample_temperature(two, 2.0, 0.37) == 1
+    # uniform logits: floor(r n) away from the boundaries
+    for r in (0.01, 0.3, 0.55, 0.99):
+        assert O.sample_temperature(np.zeros(8, np.float32), 0.7, r) == int(r * 8)
+    # -inf logits never sampled; NaN or +inf makes the probabilities NaN -> the last index
+    assert O.sample_temperature([-np.inf, 0.0, -np.inf], 1.0, 0.999) == 1
+    assert O.sample_temperature([0.0, np.nan, 1.0, 2.0], 1.0, 0.1) == 3
+    assert O.sample_temperature([0.0, np.inf, 1.0], 1.0, 0.1) == 2
+    assert O.sample_temperature([-np.inf, -np.inf], 1.0, 0.1) == 1
+
+
+def test_oracle_sample_temperature_brute_force():
+    rng = np.random.default_rng(3)
+    checked = 0
+    for trial in range(40):
+        n = int(rng.integers(2, 300))
+        logits = rng.normal(0, 3, n).astype(np.float32)
+        t = float(rng.uniform(0.2, 2.0))
+        for r in rng.uniform(0, 1, 5):
+            want, margin = _f64_pick(logits, t, float(r))
+            if margin < 1e-5:
+                continue
+            assert O.sample_temperature(logits, t, float(r)) == want, (trial, n, t, r)
+            checked += 1
+    assert checked > 150
+
+
+# ---- oracle: TokenizerPromptConfig ---------------------------------------------------------------
+
+@pytest.fixture(scope="module")
+def c0_plain(tmp_path_factory):
+    return synth.write_model(str(tmp_path_factory.mktemp("c0t") / "c0.gguf"), synth.preset("c0"), seed=0)
+
+
+@pytest.mark.parametrize("entries,want", [
+    ([], (False, False, 1, 2)),
+    ([("tokenizer.ggml.model", synth.GGUF_STR, "llama")], (True, False, 1, 2)),
+    ([("tokenizer.ggml.model", synth.GGUF_STR, "gpt2")], (False, False, 1, 2)),
+    ([("tokenizer.ggml.model", synth.GGUF_STR, "llama"), ("tokenizer.ggml.add_bos_token", synth.GGUF_BOOL, False),
+      ("tokenizer.ggml.add_eos_token", synth.GGUF_BOOL, True)], (False, True, 1, 2)),
+    ([("tokenizer.ggml.add_bos_token", synth.GGUF_U8, 1)], (False, False, 1, 2)),  # not a GGUF bool: ignored
+    ([("tokenizer.ggml.bos_token_id", synth.GGUF_I32, 7), ("tokenizer.ggml.eos_token_id", synth.GGUF_U64, 9)],
+     (False, False, 7, 9)),
+    ([("tokenizer.ggml.bos_token_id", synth.GGUF_I32, -5), ("tokenizer.ggml.eos_token_id", synth.GGUF_U64, 1 << 33)],
+     (False, False, 1, 2)),  # out of u32 range: the defaults
+    ([("tokenizer.ggml.eos_token_id", synth.GGUF_U16, 65535), ("tokenizer.ggml.bos_token_id", synth.GGUF_I8, 3)],
+     (False, False, 3, 65535)),
+    ([("tokenizer.ggml.eos_token_id", synth.GGUF_F32, 3.0)], (False, False, 1, 2)),  # not an integer
+])
+def test_oracle_tokenizer_prompt_config(c0_plain, tmp_path, entries, want):
+    p = synth.with_metadata(c0_plain, str(tmp_path / "m.gguf"), entries)
+    assert O.Model(p).tokenizer_prompt() == want
+
+
+def test_with_metadata_keeps_the_model(c0_plain, tmp_path):
+    p = synth.with_metadata(c0_plain, str(tmp_path / "m.gguf"), [("tokenizer.ggml.eos_token_id", synth.GGUF_U32, 5)])
+    a, b = O.Model(c0_plain), O.Model(p)
+    for name in ("token_embd.weight", "blk.1.ffn_down.weight", "output.weight"):
+        assert np.array_equal(a.tensor(name)[0], b.tensor(name)[0])
+    sa, sb = O.Session(a), O.Session(b)
+    ids = synth.prompt_ids(0, 8)
+    sa.prefill(ids)
+    sb.prefill(ids)
+    assert np.array_equal(sa.logits(), sb.logits())
