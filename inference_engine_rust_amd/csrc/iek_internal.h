@@ -65,9 +65,13 @@ bool gemm_q_ok(int dt, const void* w, int K);
 int num_cus();  // compute units of the current device
 void launch_block_sums(const float* a, int M, int K, float* xs, hipStream_t st);
 // kpart: optional M x N f32 scratch; with it a one-segment K-quant GEMM whose tiles would fill at
-// most half the CUs splits K in two and adds the second half's partial sums in a second pass.
-void launch_gemm_q(int dt, const GemmQSeg* segs, int nseg, const __half* xh, const __half* xl, const float* xs, int M,
-                   int K, const float* resid, hipStream_t st, float* kpart = nullptr);
+// most half the CUs splits K in two and adds the second half's partial sums in a second pass; with
+// defer_add that pass is left to the caller (true is returned while kpart holds the partial sums:
+// out + kpart is the result, e.g. through launch_rmsnorm_split's `part`).
+bool launch_gemm_q(int dt, const GemmQSeg* segs, int nseg, const __half* xh, const __half* xl, const float* xs, int M,
+                   int K, const float* resid, hipStream_t st, float* kpart = nullptr, bool defer_add = false);
+// out[i] += part[i] for i < n (n % 4 == 0, 16-byte aligned)
+void launch_add_f32(float* out, const float* part, size_t n, hipStream_t st);
 void launch_gemm_mfma(int dt, const void* w, const __half* xh, const __half* xl, int M, int K, int N, float* out,
                       const float* resid, hipStream_t st);
 void launch_dequant(int dt, const void* blocks, size_t nblocks, float* out, hipStream_t st);
@@ -77,9 +81,10 @@ void launch_rmsnorm(const float* in, const float* w, int rows, int dim, float ep
 // Producers that also emit a prefill GEMM input: fp16 (hi, lo) planes of their [rows, dim] output
 // and its per-32 sums as an fp16 pair (two planes of rows * dim / 32 halves at `sums`), as
 // launch_split_f16 + launch_block_sums would (dim % 32 == 0, 16-byte aligned rows). A null `out`
-// skips the f32 output.
-void launch_rmsnorm_split(const float* in, const float* w, int rows, int dim, float eps, float* out, __half* hi,
-                          __half* lo, float* sums, hipStream_t st);
+// skips the f32 output. With `part`, in[i] + part[i] (one f32 add, as launch_add_f32) is
+// normalised and written back to `in`.
+void launch_rmsnorm_split(float* in, const float* w, int rows, int dim, float eps, float* out, __half* hi,
+                          __half* lo, float* sums, hipStream_t st, const float* part = nullptr);
 void launch_split_sums(const float* a, int rows, int K, __half* hi, __half* lo, float* sums, hipStream_t st);
 void launch_swiglu_split(const float* g, const float* u, float* out, int rows, int K, __half* hi, __half* lo,
                          float* sums, hipStream_t st);
@@ -125,9 +130,17 @@ void* noalloc_scratch();
 // With a scratch buffer of attn_prefill_scratch_halves() halves (head_dim 64 or 128), each K/V block
 // is staged once for all the query heads of its KV head; otherwise one workgroup per query head.
 size_t attn_prefill_scratch_halves(int M, int n_kv, int head_dim);
+// planes_ready: launch_attn_prefill_prep already wrote the K/V planes into the scratch.
 void launch_attn_prefill(const float* q, const float* k, const float* v, float* out, int M, int n_heads, int n_kv,
                          int head_dim, int window, float scale, hipStream_t st, void* scratch = nullptr,
-                         size_t scratch_halves = 0);
+                         size_t scratch_halves = 0, bool planes_ready = false);
+// RoPE (table `cs`, npairs pairs, prompt positions 0..M-1) on q in place and on k, the KV append of
+// k and v at cache position pos0 and the K/V planes of the shared-K/V path, in one launch (k and v
+// are left as they were). Returns false, launching nothing, when the shared-K/V path does not
+// apply (then the caller runs RoPE, the append and launch_attn_prefill with planes_ready false).
+bool launch_attn_prefill_prep(float* q, const float* k, const float* v, int M, int n_heads, int n_kv, int head_dim,
+                              const float* cs, int npairs, void* kc, void* vc, bool kv_f32, int ctx, int pos0,
+                              void* scratch, size_t scratch_halves, hipStream_t st);
 // Gemma-4 pieces (kernels/gemma.hip).
 void launch_head_prep(float* q, float* k, float* v, int rows, int q_stride, int kv_stride, int nq, int nkv, int hd,
                       const float* qn, const float* kn, float eps, bool vnorm, const float* cs, int npairs,

@@ -303,6 +303,86 @@ __global__ __launch_bounds__(256) void kv_split_kernel(const float* __restrict__
   }
 }
 
+// The prompt's attention inputs in one pass (replaces RoPE on Q and on K, the KV append and
+// kv_split_kernel): workgroup (position tile, 64-dim tile, z). z < n_kv: KV head z, whose K rows
+// get RoPE at the prompt positions 0..M-1 in registers (the pair partner from the neighbouring
+// lane, the arithmetic of rotate() in ops.hip, src/ops/rope.rs:11-59), then go to the cache at
+// pos0 + p (f32 or fp16, as kv_store_kernel) and to the K planes; V goes to the cache and, through
+// LDS, to the transposed V planes. z >= n_kv: query head z - n_kv gets RoPE in place.
+template <typename T>
+__global__ __launch_bounds__(256) void attn_prep_kernel(float* __restrict__ q, const float* __restrict__ k,
+                                                        const float* __restrict__ v, int M, int n_heads, int n_kv,
+                                                        int hd, int Mp, const float* __restrict__ cs, int npairs,
+                                                        T* __restrict__ kc, T* __restrict__ vc, int ctx, int pos0,
+                                                        _Float16* __restrict__ kh, _Float16* __restrict__ kl,
+                                                        _Float16* __restrict__ vh, _Float16* __restrict__ vl) {
+#pragma clang fp contract(off)
+  __shared__ float tile[64][65];
+  const int z = blockIdx.z, d0 = blockIdx.y * 64, p0 = blockIdx.x * 64, tid = threadIdx.x, dl = tid & 63;
+  const int d = d0 + dl;
+  // RoPE of element (p, d) of a head row given its pair partner (the lane d ^ 1 holds it)
+  auto rope = [&](float x, int p) -> float {
+#pragma clang fp contract(off)
+    const float y = __shfl_xor(x, 1, 64);
+    if (d >= 2 * npairs || d >= hd) return x;
+    const float2 e = reinterpret_cast<const float2*>(cs)[(size_t)p * npairs + (d >> 1)];
+    return (d & 1) ? y * e.y + x * e.x : x * e.x - y * e.y;
+  };
+  if (z >= n_kv) {
+    const int h = z - n_kv;
+    const size_t qd = (size_t)n_heads * hd;
+#pragma unroll 4
+    for (int r = 0; r < 16; ++r) {
+      const int p = p0 + (tid >> 6) + 4 * r;
+      const bool live = p < M && d < hd;
+      float* e = q + (size_t)p * qd + (size_t)h * hd + d;
+      const float x = live ? *e : 0.f;
+      const float o = rope(x, p);  // every lane joins the exchange
+      if (live) *e = o;
+    }
+    return;
+  }
+  const int h = z;
+  const size_t kvd = (size_t)n_kv * hd;
+#pragma unroll 4
+  for (int r = 0; r < 16; ++r) {
+    const int pl = (tid >> 6) + 4 * r, p = p0 + pl;
+    const bool live = p < M && d < hd;
+    const size_t src = (size_t)p * kvd + (size_t)h * hd + d;
+    const float kx = live ? k[src] : 0.f;
+    const float vv = live ? v[src] : 0.f;
+    const float kr = rope(kx, p);
+    if (live) {
+      const size_t dst = ((size_t)h * ctx + pos0 + p) * hd + d;
+      if constexpr (std::is_same<T, float>::value) {
+        kc[dst] = kr;
+        vc[dst] = vv;
+      } else {
+        kc[dst] = __float2half_rn(kr);
+        vc[dst] = __float2half_rn(vv);
+      }
+      _Float16 a, b;
+      asplit(kr, a, b);
+      const size_t kd = ((size_t)h * M + p) * hd + d;
+      kh[kd] = a;
+      kl[kd] = b;
+    }
+    tile[pl][dl] = vv;
+  }
+  __syncthreads();
+#pragma unroll 4
+  for (int r = 0; r < 16; ++r) {
+    const int dt = (tid >> 6) + 4 * r, pl = tid & 63, dd = d0 + dt, p = p0 + pl;
+    if (dd < hd && p < Mp) {
+      _Float16 a, b;
+      asplit(tile[pl][dt], a, b);
+      const size_t vd = ((size_t)h * hd + dd) * Mp + p;
+      vh[vd] = a;
+      vl[vd] = b;
+    }
+  }
+}
+
 // One 256-thread workgroup per (KV head, group of up to 4 query heads, query tile): wave w takes
 // query head w % G4 and query sub-tile w / G4 (G4 = min(G, 4)), TMQ 16-row MFMA tiles of it. Each
 // 64-key block of K and V^T is staged once in LDS (16-byte copies of the split planes, the next
@@ -503,17 +583,43 @@ size_t attn_prefill_scratch_halves(int M, int n_kv, int head_dim) {
   return 4 * (size_t)n_kv * head_dim * Mp;
 }
 
+static bool attn_planes_ok(int M, int n_heads, int n_kv, int head_dim, const void* scratch, size_t scratch_halves) {
+  return scratch && M >= 1 && n_kv >= 1 && (head_dim == 64 || head_dim == 128) && n_heads % n_kv == 0 &&
+         scratch_halves >= attn_prefill_scratch_halves(M, n_kv, head_dim);
+}
+
+bool launch_attn_prefill_prep(float* q, const float* k, const float* v, int M, int n_heads, int n_kv, int head_dim,
+                              const float* cs, int npairs, void* kc, void* vc, bool kv_f32, int ctx, int pos0,
+                              void* scratch, size_t scratch_halves, hipStream_t st) {
+  if (!attn_planes_ok(M, n_heads, n_kv, head_dim, scratch, scratch_halves) || npairs < 0 || 2 * npairs > head_dim)
+    return false;
+  if (pos0 < 0 || (size_t)pos0 + (size_t)M > (size_t)ctx) fail(ST_KVCACHE, "attention prep: the prompt does not fit the cache");
+  const int Mp = ((M + 63) / 64) * 64;
+  const size_t plane = (size_t)n_kv * head_dim * Mp;
+  _Float16* s16 = static_cast<_Float16*>(scratch);
+  _Float16 *kh = s16, *kl = s16 + plane, *vh = s16 + 2 * plane, *vl = s16 + 3 * plane;
+  const dim3 grid(Mp / 64, (head_dim + 63) / 64, n_kv + n_heads);
+  if (kv_f32)
+    hipLaunchKernelGGL(attn_prep_kernel<float>, grid, dim3(256), 0, st, q, k, v, M, n_heads, n_kv, head_dim, Mp, cs,
+                       npairs, (float*)kc, (float*)vc, ctx, pos0, kh, kl, vh, vl);
+  else
+    hipLaunchKernelGGL(attn_prep_kernel<__half>, grid, dim3(256), 0, st, q, k, v, M, n_heads, n_kv, head_dim, Mp, cs,
+                       npairs, (__half*)kc, (__half*)vc, ctx, pos0, kh, kl, vh, vl);
+  return true;
+}
+
 void launch_attn_prefill(const float* q, const float* k, const float* v, float* out, int M, int n_heads, int n_kv,
-                         int head_dim, int window, float scale, hipStream_t st, void* scratch, size_t scratch_halves) {
+                         int head_dim, int window, float scale, hipStream_t st, void* scratch, size_t scratch_halves,
+                         bool planes_ready) {
   const int G = n_heads / n_kv;
-  if (scratch && (head_dim == 64 || head_dim == 128) && G >= 1 && n_heads % n_kv == 0 &&
-      scratch_halves >= attn_prefill_scratch_halves(M, n_kv, head_dim)) {
+  if (attn_planes_ok(M, n_heads, n_kv, head_dim, scratch, scratch_halves) && G >= 1) {
     const int Mp = ((M + 63) / 64) * 64;
     const size_t plane = (size_t)n_kv * head_dim * Mp;
     _Float16* s16 = static_cast<_Float16*>(scratch);
     _Float16 *kh = s16, *kl = s16 + plane, *vh = s16 + 2 * plane, *vl = s16 + 3 * plane;
-    hipLaunchKernelGGL(kv_split_kernel, dim3(Mp / 64, (head_dim + 63) / 64, n_kv), dim3(256), 0, st, k, v, M, n_kv,
-                       head_dim, Mp, kh, kl, vh, vl);
+    if (!planes_ready)
+      hipLaunchKernelGGL(kv_split_kernel, dim3(Mp / 64, (head_dim + 63) / 64, n_kv), dim3(256), 0, st, k, v, M, n_kv,
+                         head_dim, Mp, kh, kl, vh, vl);
     const int G4 = std::min(G, 4), HG = (G + 3) / 4;
     if (head_dim == 128) {
       // two row tiles per wave once the grid fills the machine twice over, one below that

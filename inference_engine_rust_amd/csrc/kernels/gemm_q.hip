@@ -827,7 +827,7 @@ static void gemm_q_launch(GemmQArgs g, hipStream_t st) {
 }
 
 template <class T, int WGM, int WGN, int DA, int TM = 4, int OCC = 1, int FM = 0>
-static void gemm_kq_launch(GemmQArgs g, hipStream_t st) {
+static bool gemm_kq_launch(GemmQArgs g, hipStream_t st, bool defer_add) {
   constexpr int BM = 16 * TM * WGM, BN = 64 * WGN;
   int t = 0;
   for (int i = 0; i < g.nseg; ++i) {
@@ -844,9 +844,10 @@ static void gemm_kq_launch(GemmQArgs g, hipStream_t st) {
   hipLaunchKernelGGL((gemm_kq_kernel<T, WGM, WGN, DA, TM, OCC, FM>), dim3(tiles * g.ksplit), dim3(64 * WGM * WGN),
                      0, st, g);
   if (g.ksplit == 2) {
-    const int blocks = (int)std::min<size_t>((mn / 4 + 255) / 256, 2048);
-    hipLaunchKernelGGL(add_part_kernel, dim3(blocks), dim3(256), 0, st, g.out[0], g.kpart, mn / 4);
+    if (defer_add) return true;
+    launch_add_f32(g.out[0], g.kpart, mn, st);
   }
+  return false;
 }
 
 // K-quant tile: 64 x 256 (1 x 4 waves; each wave streams its own 64 weight columns, the
@@ -859,17 +860,14 @@ static void gemm_kq_launch(GemmQArgs g, hipStream_t st) {
 // it is slower (Q/K/V at 512 rows: 74 -> 80 us). Q6_K's fp16 weight pairs do not fit two waves
 // per SIMD (the rescaled form spills there and is 30% slower; at one wave per SIMD 7% slower).
 template <class T>
-static void gemm_kq(GemmQArgs g, hipStream_t st) {
+static bool gemm_kq(GemmQArgs g, hipStream_t st, bool defer_add) {
   size_t nt = 0;
   for (int i = 0; i < g.nseg; ++i) nt += (g.n[i] + 255) / 256;
   const size_t tiles = nt * (size_t)((g.M + 63) / 64);
   if constexpr (T::MINS) {
-    if (tiles >= 2 * (size_t)num_cus()) {
-      gemm_kq_launch<T, 1, 4, 1, 4, 2, 2>(g, st);
-      return;
-    }
+    if (tiles >= 2 * (size_t)num_cus()) return gemm_kq_launch<T, 1, 4, 1, 4, 2, 2>(g, st, defer_add);
   }
-  gemm_kq_launch<T, 1, 4, 1>(g, st);
+  return gemm_kq_launch<T, 1, 4, 1>(g, st, defer_add);
 }
 
 // Tile shape 64 x 64 (measured fastest at the Mistral-7B prefill shapes: the larger tiles lose
@@ -879,8 +877,16 @@ static void gemm_q_dt(GemmQArgs g, hipStream_t st) {
   gemm_q_launch<DT, 64, 64>(g, st);
 }
 
-void launch_gemm_q(int dt, const GemmQSeg* segs, int nseg, const __half* xh, const __half* xl, const float* xs, int M,
-                   int K, const float* resid, hipStream_t st, float* kpart) {
+void launch_add_f32(float* out, const float* part, size_t n, hipStream_t st) {
+  if (n == 0) return;
+  if (n % 4 != 0 || (reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(part)) % 16)
+    fail(ST_OP, "add_f32: n % 4 and 16-byte aligned arrays");
+  const int blocks = (int)std::min<size_t>((n / 4 + 255) / 256, 2048);
+  hipLaunchKernelGGL(add_part_kernel, dim3(blocks), dim3(256), 0, st, out, part, n / 4);
+}
+
+bool launch_gemm_q(int dt, const GemmQSeg* segs, int nseg, const __half* xh, const __half* xl, const float* xs, int M,
+                   int K, const float* resid, hipStream_t st, float* kpart, bool defer_add) {
   if (nseg < 1 || nseg > 3 || M < 1) fail(ST_OP, "gemm_q: 1..3 segments and M >= 1");
   GemmQArgs g{};
   g.nseg = nseg;
@@ -907,10 +913,10 @@ void launch_gemm_q(int dt, const GemmQSeg* segs, int nseg, const __half* xh, con
   }
   if (dt == DT_Q4K && !xs) fail(ST_OP, "gemm_q: Q4_K needs the per-32 activation sums");
   switch (dt) {
-    case DT_Q4K: gemm_kq<Q4KB>(g, st); break;
-    case DT_Q6K: gemm_q_dt<DT_Q6K>(g, st); break;
-    case DT_Q6K_R: gemm_kq<Q6RB>(g, st); break;
-    default: gemm_q_dt<DT_Q8_0>(g, st); break;
+    case DT_Q4K: return gemm_kq<Q4KB>(g, st, defer_add);
+    case DT_Q6K: gemm_q_dt<DT_Q6K>(g, st); return false;
+    case DT_Q6K_R: return gemm_kq<Q6RB>(g, st, defer_add);
+    default: gemm_q_dt<DT_Q8_0>(g, st); return false;
   }
 }
 

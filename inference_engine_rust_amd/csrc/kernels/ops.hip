@@ -120,15 +120,22 @@ IEK_DEV void emit_split8(const float (&v)[8], size_t i, bool live, uint4* __rest
 
 // rmsnorm (as rmsnorm_kernel) that also emits the GEMM input planes of its output (the f32 output
 // itself only when `out` is set).
-__global__ __launch_bounds__(256) void rmsnorm_split_kernel(const float* in, const float* w, int dim, float eps,
+// With `part` the row is in + part (one f32 add per element, as the split-K add pass would do),
+// written back to `in` by the thread that reads it in the second loop, after every read of the
+// first loop (the barrier inside block_sum256).
+__global__ __launch_bounds__(256) void rmsnorm_split_kernel(float* in, const float* w, int dim, float eps,
                                                             float* out, uint4* hi, uint4* lo, _Float16* sh,
-                                                            _Float16* sl) {
+                                                            _Float16* sl, const float* part) {
 #pragma clang fp contract(off)
   __shared__ float red[8];
-  const float* x = in + (size_t)blockIdx.x * dim;
+  float* x = in + (size_t)blockIdx.x * dim;
+  const float* pr = part ? part + (size_t)blockIdx.x * dim : nullptr;
   float* y = out + (size_t)blockIdx.x * dim;
   float ss = 0.f;
-  for (int i = threadIdx.x; i < dim; i += blockDim.x) ss += x[i] * x[i];
+  for (int i = threadIdx.x; i < dim; i += blockDim.x) {
+    const float xv = pr ? x[i] + pr[i] : x[i];
+    ss += xv * xv;
+  }
   ss = block_sum256(ss, red);
   const float rms = sqrtf(ss / (float)dim + eps);
   const int n8 = dim / 8;
@@ -137,7 +144,22 @@ __global__ __launch_bounds__(256) void rmsnorm_split_kernel(const float* in, con
     const bool live = e < n8;
     float v[8];
     const int c = live ? e : 0;
-    const float4 xa = reinterpret_cast<const float4*>(x)[2 * c], xb = reinterpret_cast<const float4*>(x)[2 * c + 1];
+    float4 xa = reinterpret_cast<const float4*>(x)[2 * c], xb = reinterpret_cast<const float4*>(x)[2 * c + 1];
+    if (pr) {
+      const float4 pa = reinterpret_cast<const float4*>(pr)[2 * c], pb = reinterpret_cast<const float4*>(pr)[2 * c + 1];
+      xa.x += pa.x;
+      xa.y += pa.y;
+      xa.z += pa.z;
+      xa.w += pa.w;
+      xb.x += pb.x;
+      xb.y += pb.y;
+      xb.z += pb.z;
+      xb.w += pb.w;
+      if (live) {
+        reinterpret_cast<float4*>(x)[2 * c] = xa;
+        reinterpret_cast<float4*>(x)[2 * c + 1] = xb;
+      }
+    }
     const float4 wa = reinterpret_cast<const float4*>(w)[2 * c], wb = reinterpret_cast<const float4*>(w)[2 * c + 1];
     v[0] = (xa.x * wa.x) / rms;
     v[1] = (xa.y * wa.y) / rms;
@@ -155,15 +177,16 @@ __global__ __launch_bounds__(256) void rmsnorm_split_kernel(const float* in, con
   }
 }
 
-void launch_rmsnorm_split(const float* in, const float* w, int rows, int dim, float eps, float* out, __half* hi,
-                          __half* lo, float* sums, hipStream_t st) {
+void launch_rmsnorm_split(float* in, const float* w, int rows, int dim, float eps, float* out, __half* hi,
+                          __half* lo, float* sums, hipStream_t st, const float* part) {
   if (rows <= 0) return;
-  if (dim % 32 != 0 || (reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out)) % 16)
+  if (dim % 32 != 0 || (reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out) |
+                        reinterpret_cast<uintptr_t>(part)) % 16)
     fail(ST_OP, "rmsnorm_split: dim % 32 and 16-byte aligned rows");
   _Float16* s = reinterpret_cast<_Float16*>(sums);
   const size_t nb = (size_t)rows * (dim / 32);
   hipLaunchKernelGGL(rmsnorm_split_kernel, dim3(rows), dim3(256), 0, st, in, w, dim, eps, out, (uint4*)hi, (uint4*)lo,
-                     s, s + nb);
+                     s, s + nb, part);
 }
 
 // fp16 pair planes and per-32 sums of an existing [rows, K] input in one pass.

@@ -238,7 +238,7 @@ bool Session::quant_ready(const DevTensor* const* ws, int nseg, int M, int K) co
 }
 
 bool Session::project_q(const DevTensor* const* ws, float* const* outs, int nseg, int M, int K, const float* resid,
-                        float* kpart) {
+                        float* kpart, bool* pending) {
   if (M < 2) return false;
   int dt = -1;
   GemmQSeg segs[3];
@@ -256,11 +256,13 @@ bool Session::project_q(const DevTensor* const* ws, float* const* outs, int nseg
     if (!gemm_q_ok(dt, p, K)) return false;
     segs[i] = GemmQSeg{p, outs[i], (int)w.dims[1]};
   }
-  launch_gemm_q(dt, segs, nseg, xs_, xs_ + (size_t)M * K, xsum_, M, K, resid, st_, kpart);
+  const bool left = launch_gemm_q(dt, segs, nseg, xs_, xs_ + (size_t)M * K, xsum_, M, K, resid, st_, kpart,
+                                  pending != nullptr);
+  if (pending) *pending = left;
   return true;
 }
 
-void Session::layer_prefill(int li, int M) {
+bool Session::layer_prefill(int li, int M, bool pend_in) {
   const Config& c = m_->cfg;
   const LayerSpec& S = c.layers[li];
   const LayerTensors& L = m_->layers[li];
@@ -276,19 +278,21 @@ void Session::layer_prefill(int li, int M) {
     launch_split_sums(a, M, K, xs_, xs_ + (size_t)M * K, xsum_, st_);
     return xs_;
   };
-  // (the f32 output is written only when a consumer may fall back to it)
-  auto norm_split = [&](const DevTensor& w, bool need_f32) -> const __half* {
+  // (the f32 output is written only when a consumer may fall back to it). A split-K partial left
+  // in tmp_ by the preceding projection is added into x_ by the norm itself.
+  auto norm_split = [&](const DevTensor& w, bool need_f32, bool pend) -> const __half* {
     if (!wide || H_ % 32 != 0) {
+      if (pend) launch_add_f32(x_, tmp_, (size_t)M * H_, st_);
       launch_rmsnorm(x_, (const float*)w.dev, M, H_, eps, xn_, st_);
       return nullptr;
     }
     launch_rmsnorm_split(x_, (const float*)w.dev, M, H_, eps, need_f32 ? xn_ : nullptr, xs_, xs_ + (size_t)M * H_,
-                         xsum_, st_);
+                         xsum_, st_, pend ? tmp_ : nullptr);
     return xs_;
   };
   const DevTensor* wqkv[3] = {&L.wq, &L.wk, &L.wv};
   const bool qkv_q = quant_ready(wqkv, 3, M, H_) || (quant_ready(wqkv, 2, M, H_) && quant_ready(wqkv + 2, 1, M, H_));
-  const __half* xs = norm_split(L.attn_norm, !qkv_q);
+  const __half* xs = norm_split(L.attn_norm, !qkv_q, pend_in);
   {
     const DevTensor* ws[3] = {&L.wq, &L.wk, &L.wv};
     float* outs[3] = {q_, k_, v_};
@@ -308,23 +312,31 @@ void Session::layer_prefill(int li, int M) {
     launch_copy_f32(tmp_, k_, (size_t)M * kvd, st_);
   }
   const RopeTable& rt = m_->rope_tables[L.rope_table];
-  launch_rope_rows(q_, M, qd, c.n_heads, hd, 0, rt.dev, S.rotary_dim / 2, st_);
-  launch_rope_rows(k_, M, kvd, c.n_kv_heads, hd, 0, rt.dev, S.rotary_dim / 2, st_);
-  launch_kv_store(k_, v_, M, kvd, kc_[li], vc_[li], kv_f32_, c.n_kv_heads, hd, ctx_, nullptr, pos_, st_);
-  const float scale = 1.0f / sqrtf((float)hd);
   // xs_ (the GEMM input pair, consumed by the Q/K/V projection above) is free until the O
-  // projection's split: the shared-K/V attention stages its fp16 K / V planes there
-  launch_attn_prefill(q_, k_, v_, att_, M, c.n_heads, c.n_kv_heads, hd, S.window, scale, st_, xs_, xs_halves());
+  // projection's split: the shared-K/V attention stages its fp16 K / V planes there. RoPE, the KV
+  // append and those planes go in one launch when that path applies.
+  const bool prepped = qd == c.n_heads * hd && kvd == c.n_kv_heads * hd &&
+                       launch_attn_prefill_prep(q_, k_, v_, M, c.n_heads, c.n_kv_heads, hd, rt.dev, S.rotary_dim / 2,
+                                                kc_[li], vc_[li], kv_f32_, ctx_, pos_, xs_, xs_halves(), st_);
+  if (!prepped) {
+    launch_rope_rows(q_, M, qd, c.n_heads, hd, 0, rt.dev, S.rotary_dim / 2, st_);
+    launch_rope_rows(k_, M, kvd, c.n_kv_heads, hd, 0, rt.dev, S.rotary_dim / 2, st_);
+    launch_kv_store(k_, v_, M, kvd, kc_[li], vc_[li], kv_f32_, c.n_kv_heads, hd, ctx_, nullptr, pos_, st_);
+  }
+  const float scale = 1.0f / sqrtf((float)hd);
+  launch_attn_prefill(q_, k_, v_, att_, M, c.n_heads, c.n_kv_heads, hd, S.window, scale, st_, xs_, xs_halves(),
+                      prepped);
+  bool opend = false;
   {
     const __half* xa = split(att_, qd);
     const DevTensor* ws[1] = {&L.wo};
     float* outs[1] = {x_};
-    if (!xa || !project_q(ws, outs, 1, M, qd, x_, kpart_ok_ ? tmp_ : nullptr))
+    if (!xa || !project_q(ws, outs, 1, M, qd, x_, kpart_ok_ ? tmp_ : nullptr, &opend))
       project(L.wo, att_, xa, M, qd, H_, x_, x_, st_);
   }
   // FFN sub-layer: pre-norm, gate/up, SwiGLU, down + residual.
   const DevTensor* wgu[2] = {&L.gate, &L.up};
-  xs = norm_split(L.ffn_norm, M == 1 || !quant_ready(wgu, 2, M, H_));
+  xs = norm_split(L.ffn_norm, M == 1 || !quant_ready(wgu, 2, M, H_), opend);
   const __half* xa = nullptr;
   if (M == 1 && L.gate.dtype == L.up.dtype) {
     MvSegDesc s[2] = {{L.gate.dev, act_, nullptr, S.ffn_dim}, {L.up.dev, nullptr, nullptr, S.ffn_dim}};
@@ -345,12 +357,14 @@ void Session::layer_prefill(int li, int M) {
       launch_swiglu(g_, u_, act_, (size_t)M * S.ffn_dim, st_);
     }
   }
+  bool dpend = false;
   {
     const DevTensor* ws[1] = {&L.down};
     float* outs[1] = {x_};
-    if (!xa || !project_q(ws, outs, 1, M, S.ffn_dim, x_, kpart_ok_ ? tmp_ : nullptr))
+    if (!xa || !project_q(ws, outs, 1, M, S.ffn_dim, x_, kpart_ok_ ? tmp_ : nullptr, &dpend))
       project(L.down, act_, xa, M, S.ffn_dim, H_, x_, x_, st_);
   }
+  return dpend;
 }
 
 // Decode layer, fused path: 5 launches (QKV+norm+RoPE+KV append, attention, O+residual,
@@ -941,7 +955,9 @@ void Session::prefill(const uint32_t* ids, int n) {
     embed_ple(d_ids_, n, x_, split_rows(x_, n, H_), ple_tok_, ple_proj_, ple_pack_);
     for (int li = 0; li < c.n_layers; ++li) layer_prefill_gemma(li, n);
   } else {
-    for (int li = 0; li < c.n_layers; ++li) layer_prefill(li, n);
+    bool pend = false;  // the down projection's split-K partial goes into the next layer's norm
+    for (int li = 0; li < c.n_layers; ++li) pend = layer_prefill(li, n, pend);
+    if (pend) launch_add_f32(x_, tmp_, (size_t)n * H_, st_);
   }
   launch_copy_f32(x_ + (size_t)(n - 1) * H_, xdec_, H_, st_);
   pos_ += n;
@@ -1105,7 +1121,7 @@ void Session::prefill_layer(int li) {
   const int M = state_rows_;
   if (pos_ + M > ctx_) fail(ST_KVCACHE, "KVCache is Full: max len is " + std::to_string(ctx_) + ".");
   if (gemma_) layer_prefill_gemma(li, M);
-  else layer_prefill(li, M);
+  else if (layer_prefill(li, M)) launch_add_f32(x_, tmp_, (size_t)M * H_, st_);
   launch_copy_f32(x_ + (size_t)(M - 1) * H_, xdec_, H_, st_);
   if (++layer_cursor_ == c.n_layers) {
     pos_ += M;
