@@ -213,14 +213,16 @@ def kernel_roofline(E, model, prompt, reps):
 
 def prefill_roofline(E, model, prompt, reps):
     """The prefill's largest GEMM: gate/up over the prompt rows (M x 4096 x 2*14336, K-quant
-    weights dequantised into LDS, v_mfma_f32_16x16x32_f16), timed like kernel_roofline over
+    weights decoded in registers, v_mfma_f32_16x16x32_f16) with SwiGLU and the down projection's
+    fp16 input pair in its epilogue, as the prefill runs it; timed like kernel_roofline over
     `reps` launches rotating over the layers. Algorithmic flops = 2*M*K*N, against the dense
     fp16/bf16 MFMA peak."""
     sess = E.InferenceSession(model)
     sess.prefill(prompt)
     us, flops = sess.bench_kernel(1, reps)
     tf = flops / (us * 1e-6) / 1e12
-    return {"kernel": f"gemm_kq gate/up (M={len(prompt)}, Q4_K, fp16 hi/lo activation pair, 2 MFMA per product)",
+    return {"kernel": f"gemm_kq gate/up + SwiGLU epilogue (M={len(prompt)}, Q4_K, fp16 hi/lo activation pair, "
+                      "2 MFMA per product)",
             "bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(tf / MFMA_PEAK_TFLOPS, 4), "algorithmic_flops_per_launch": int(flops),
             "avg_launch_us": round(us, 3), "launches": reps}

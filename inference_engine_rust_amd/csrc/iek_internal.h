@@ -70,6 +70,14 @@ void launch_block_sums(const float* a, int M, int K, float* xs, hipStream_t st);
 // out + kpart is the result, e.g. through launch_rmsnorm_split's `part`).
 bool launch_gemm_q(int dt, const GemmQSeg* segs, int nseg, const __half* xh, const __half* xl, const float* xs, int M,
                    int K, const float* resid, hipStream_t st, float* kpart = nullptr, bool defer_add = false);
+// Gate/up projection with SwiGLU in its epilogue (K-quant Q4_K or regrouped Q6_K weights of equal
+// shape, N % 32 == 0): writes act = silu(x W_gate^T) * (x W_up^T) as the down projection's input,
+// the fp16 (hi, lo) planes [M][N], optionally their per-32 sums (as launch_swiglu_split's `sums`)
+// and the f32 act; the same bits as launch_gemm_q into gate and up followed by launch_swiglu_split.
+// Returns false, launching nothing, for other weight types or shapes.
+bool launch_gemm_q_glu(int dt, const void* w_gate, const void* w_up, int N, const __half* xh, const __half* xl,
+                       const float* xs, int M, int K, __half* act_hi, __half* act_lo, float* act_sums, float* act_f32,
+                       hipStream_t st);
 // out[i] += part[i] for i < n (n % 4 == 0, 16-byte aligned)
 void launch_add_f32(float* out, const float* part, size_t n, hipStream_t st);
 void launch_gemm_mfma(int dt, const void* w, const __half* xh, const __half* xl, int M, int K, int N, float* out,

@@ -41,6 +41,12 @@ struct GemmQArgs {
   // partial sums to kpart [M, N], which a follow-up pass adds to out
   int ksplit;
   float* kpart;
+  // gate/up + SwiGLU (wave-tiled kernel instantiated with GLU, segments 0 = gate and 1 = up of
+  // equal N): each wave computes 32 gate and the same 32 up columns; the epilogue writes
+  // act = silu(gate) * up as the down projection's input: fp16 (hi, lo) planes [M][N], their
+  // per-32 sums (glu_sums, optional) and the f32 act (glu_out, optional)
+  _Float16 *glu_h, *glu_l, *glu_sums;
+  float* glu_out;
 };
 
 namespace {
@@ -397,14 +403,17 @@ struct Q4KB {
   struct Hdr {
     uint4 h[4];
   };
-  IEK_DEV static void fetch(__amdgpu_buffer_rsrc_t r, const uint32_t (&vb)[4], int lg, int kt, Raw& o) {
+  IEK_DEV static void fetch(__amdgpu_buffer_rsrc_t r0, __amdgpu_buffer_rsrc_t r1, const uint32_t (&vb)[4], int lg,
+                            int kt, Raw& o) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      o.q[j] = ld_b64(r, vb[j] + 16 + 8 * lg, (uint32_t)((kt >> 2) * Q4K_BYTES + 32 * (kt & 3)));
+      o.q[j] = ld_b64(j < 2 ? r0 : r1, vb[j] + 16 + 8 * lg, (uint32_t)((kt >> 2) * Q4K_BYTES + 32 * (kt & 3)));
   }
-  IEK_DEV static void fetch_hdr(__amdgpu_buffer_rsrc_t r, const uint32_t (&vb)[4], int, int sb, int, Hdr& o) {
+  IEK_DEV static void fetch_hdr(__amdgpu_buffer_rsrc_t r0, __amdgpu_buffer_rsrc_t r1, const uint32_t (&vb)[4], int,
+                                int sb, int, Hdr& o) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) o.h[j] = __builtin_bit_cast(uint4, ld_b128(r, vb[j], (uint32_t)(sb * Q4K_BYTES)));
+    for (int j = 0; j < 4; ++j)
+      o.h[j] = __builtin_bit_cast(uint4, ld_b128(j < 2 ? r0 : r1, vb[j], (uint32_t)(sb * Q4K_BYTES)));
   }
   template <int P, int H>
   IEK_DEV static void deq(const Hdr& hd, const Raw& q, qu4_t (&bh)[4], qu4_t (&)[4]) {
@@ -438,19 +447,23 @@ struct Q6RB {
   struct Hdr {
     uint32_t sc[2][4], d[4];
   };
-  IEK_DEV static void fetch(__amdgpu_buffer_rsrc_t r, const uint32_t (&vb)[4], int lg, int kt, Raw& o) {
+  IEK_DEV static void fetch(__amdgpu_buffer_rsrc_t r0, __amdgpu_buffer_rsrc_t r1, const uint32_t (&vb)[4], int lg,
+                            int kt, Raw& o) {
     const uint32_t so = (uint32_t)((kt >> 2) * 192 + 48 * 2 * ((kt & 3) >> 1));
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      const __amdgpu_buffer_rsrc_t r = j < 2 ? r0 : r1;
       const uint32_t v = vb[j] + 48 * (lg >> 1) + 8 * (lg & 1);
       o.l0[j] = ld_b64(r, v, so);
       o.l1[j] = ld_b64(r, v + 16, so);
       o.h[j] = ld_b64(r, v + 32, so);
     }
   }
-  IEK_DEV static void fetch_hdr(__amdgpu_buffer_rsrc_t r, const uint32_t (&vb)[4], int lg, int sb, int nsb, Hdr& o) {
+  IEK_DEV static void fetch_hdr(__amdgpu_buffer_rsrc_t r0, __amdgpu_buffer_rsrc_t r1, const uint32_t (&vb)[4], int lg,
+                                int sb, int nsb, Hdr& o) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      const __amdgpu_buffer_rsrc_t r = j < 2 ? r0 : r1;
       const uint32_t v = vb[j] + (uint32_t)nsb * 192 + 4 * (lg >> 1);
       o.sc[0][j] = ld_b32(r, v, 16u * sb);
       o.sc[1][j] = ld_b32(r, v + 8, 16u * sb);
@@ -505,6 +518,74 @@ IEK_DEV void kq_deq(int p, int h, const typename T::Hdr& hd, const typename T::R
   }
 }
 
+// SwiGLU epilogue of a gate/up tile (GLU): column groups 0-1 of a wave are gate columns and 2-3
+// the same up columns, so each lane holds matching gate / up sums. act = silu(g) * u with the
+// arithmetic of swiglu_split_kernel (src/ops/swiglu.rs:24-36: two-branch stable sigmoid,
+// (g * s) * u), then its fp16 (hi, lo) pair and, per 32 columns, the sum in emit_split8's order
+// (pairs, pairs of pairs, then the eight quarter sums one after the other from zero), so the down
+// projection's input has the bits the separate pass would write.
+// (Staging the fp16 pair through LDS for 16-byte stores measured no faster.)
+template <int TM, typename AccT>
+IEK_DEV void glu_epilogue(const GemmQArgs& g, const AccT& acc, const float (&Dc)[4], bool rescaled, int m0, int wcol,
+                          int lane) {
+#pragma clang fp contract(off)
+  const int lr = lane & 15, lg = lane >> 4;
+  const int M = g.M, N = g.n[0];
+  const size_t nb = (size_t)N / 32;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + 16 * i + 4 * lg + r;
+      float vv[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int n = wcol + 16 * j + lr;
+        const float x = rescaled ? acc[i][j][r] * Dc[j] : acc[i][j][r];
+        const float u = rescaled ? acc[i][j + 2][r] * Dc[j + 2] : acc[i][j + 2][r];
+        float sg;
+        if (x >= 0.0f) {
+          const float z = expf(-x);
+          sg = 1.0f / (1.0f + z);
+        } else {
+          const float z = expf(x);
+          sg = z / (1.0f + z);
+        }
+        const float v = x * sg * u;
+        if (m < M && n < N) {
+          const size_t o = (size_t)m * N + n;
+          const _Float16 h = (_Float16)v;
+          g.glu_h[o] = h;
+          g.glu_l[o] = (_Float16)(v - (float)h);
+          if (g.glu_out) g.glu_out[o] = v;
+        }
+        vv[j] = v;
+      }
+      if (g.glu_sums) {
+        // (v0 + v1) + (v2 + v3) over each aligned group of four columns, at the group's first lane
+        float qs[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const float s1 = vv[j] + __shfl_xor(vv[j], 1, 64);
+          qs[j] = s1 + __shfl_xor(s1, 2, 64);
+        }
+        // the wave's 32 columns are one block; its eight quarter sums sit at lanes 0, 4, 8, 12 of
+        // the lane's row of 16 (same m) for j = 0, then j = 1
+        float sum = 0.f;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) sum += __shfl(qs[j], (lane & ~15) + 4 * t, 64);
+        if (lr == 0 && m < M && wcol < N) {
+          const size_t o = (size_t)m * nb + wcol / 32;
+          const _Float16 h = (_Float16)sum;
+          g.glu_sums[o] = h;
+          g.glu_sums[(size_t)M * nb + o] = (_Float16)(sum - (float)h);
+        }
+      }
+    }
+}
+
 // TM: 16-row MFMA tiles per wave along M (a wave owns 16 TM x 64); WGM x WGN waves.
 // OCC: waves per SIMD the register allocation must allow (2 caps each wave at 256 registers).
 // FM, how the superblock factor d enters the f32 sum:
@@ -515,7 +596,8 @@ IEK_DEV void kq_deq(int p, int h, const typename T::Hdr& hd, const typename T::R
 //     partials. A superblock with d = 0 keeps D (its scales are zeroed, so only its min term
 //     counts); the rescale's rounding (a few ulp of the running sum per superblock) is far inside
 //     the f32 reordering bound.
-template <class T, int WGM, int WGN, int DA, int TM, int OCC = 1, int FM = 0>
+// GLU: gate/up with the SwiGLU epilogue (GemmQArgs::glu); a tile is 32 * WGN act columns.
+template <class T, int WGM, int WGN, int DA, int TM, int OCC = 1, int FM = 0, bool GLU = false>
 __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kq_kernel(GemmQArgs g) {
   constexpr int NT = 64 * WGM * WGN;  // threads
   constexpr int WR = 16 * TM;         // rows per wave
@@ -543,23 +625,27 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kq_kernel(GemmQArgs 
     tile = (tile % 8) * per + tile / 8;
   }
   const int mt = tile % mtiles, ntile = tile / mtiles;
-  const int s = ntile < g.tile_start[1] ? 0 : (ntile < g.tile_start[2] ? 1 : 2);
+  const int s = GLU ? 0 : (ntile < g.tile_start[1] ? 0 : (ntile < g.tile_start[2] ? 1 : 2));
   const uint8_t* w = s == 0 ? g.w[0] : (s == 1 ? g.w[1] : g.w[2]);
   float* out = s == 0 ? g.out[0] : (s == 1 ? g.out[1] : g.out[2]);
   const int N = s == 0 ? g.n[0] : (s == 1 ? g.n[1] : g.n[2]);
   const int ts = s == 0 ? 0 : (s == 1 ? g.tile_start[1] : g.tile_start[2]);
-  const int m0 = mt * BM, n0 = (ntile - ts) * BN;
+  const int m0 = mt * BM;
+  // GLU: the wave's 32 act columns (column groups 0-1 read gate rows, 2-3 the same up rows)
+  const int wcol = GLU ? (BN / 2) * ntile + 32 * wn : (ntile - ts) * BN + 64 * wn;
   const int lr = lane & 15, lg = lane >> 4;
 
   // Operand streams as buffer loads: one descriptor per array, 32-bit per-lane offsets, the
   // stage's advance in the scalar offset.
   const __amdgpu_buffer_rsrc_t rw = buf_rsrc(w, (uint32_t)(g.row_bytes * (size_t)N));
+  const __amdgpu_buffer_rsrc_t rw2 = GLU ? buf_rsrc(g.w[1], (uint32_t)(g.row_bytes * (size_t)N)) : rw;
   const __amdgpu_buffer_rsrc_t rxh = buf_rsrc(g.xh, (uint32_t)((size_t)M * K * 2));
   const __amdgpu_buffer_rsrc_t rxl = buf_rsrc(g.xl, (uint32_t)((size_t)M * K * 2));
   const __amdgpu_buffer_rsrc_t rxs = buf_rsrc(g.xs, T::MINS ? (uint32_t)((size_t)M * kb * 4) : 0u);
   uint32_t vb[4];  // weight row of the lane's column in each 16-column tile
 #pragma unroll
-  for (int j = 0; j < 4; ++j) vb[j] = (uint32_t)((size_t)min(n0 + 64 * wn + 16 * j + lr, N - 1) * g.row_bytes);
+  for (int j = 0; j < 4; ++j)
+    vb[j] = (uint32_t)((size_t)min(wcol + 16 * (GLU ? (j & 1) : j) + lr, N - 1) * g.row_bytes);
   uint32_t va[AR];  // activation rows staged by this thread (both planes)
 #pragma unroll
   for (int u = 0; u < AR; ++u)
@@ -611,17 +697,17 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kq_kernel(GemmQArgs 
   // order the loop's last stage issues them (an activation stage, then a weight stage), so the
   // wait counts at the loop head are the same on entry and on the back edge.
   const int kt_lo = 4 * sb_lo;
-  T::fetch_hdr(rw, vb, lg, sb_lo, nsb, hdr);
+  T::fetch_hdr(rw, rw2, vb, lg, sb_lo, nsb, hdr);
   float Dc[4] = {1.f, 1.f, 1.f, 1.f};  // FM 2: the scale acc is held at, per column tile
 #pragma unroll
-  for (int i = 0; i < DB - 1; ++i) T::fetch(rw, vb, lg, min(kt_lo + i, kt_last), rb[i]);
+  for (int i = 0; i < DB - 1; ++i) T::fetch(rw, rw2, vb, lg, min(kt_lo + i, kt_last), rb[i]);
   fetch_a(kt_lo, ra[0]);
   store_a(0, ra[0]);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int i = 1; i <= DA; ++i) fetch_a(min(kt_lo + i, kt_last), ra[i % DA]);
   __builtin_amdgcn_sched_barrier(0);
-  T::fetch(rw, vb, lg, min(kt_lo + DB - 1, kt_last), rb[DB - 1]);
+  T::fetch(rw, rw2, vb, lg, min(kt_lo + DB - 1, kt_last), rb[DB - 1]);
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
 
@@ -638,7 +724,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kq_kernel(GemmQArgs 
       fetch_a(min(kt + 1 + DA, kt_last), ra[(p + 1) % DA]);
       // the next superblock's factors go out ahead of this stage's weight refill, so waiting
       // for them at the superblock end never waits for a younger load
-      if (p == 0) T::fetch_hdr(rw, vb, lg, min(sb + 1, sb_hi - 1), nsb, hdrn);
+      if (p == 0) T::fetch_hdr(rw, rw2, vb, lg, min(sb + 1, sb_hi - 1), nsb, hdrn);
       if (T::MINS && p == 2) fetch_xs(sb);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (FM == 2) {
@@ -647,7 +733,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kq_kernel(GemmQArgs 
         kq_deq<T>(p, 0, hdr, rb[p % DB], bh[0], bl[0]);
         kq_deq<T>(p, 1, hdr, rb[p % DB], bh[1], bl[1]);
         __builtin_amdgcn_sched_barrier(0);
-        T::fetch(rw, vb, lg, min(kt + DB, kt_last), rb[p % DB]);
+        T::fetch(rw, rw2, vb, lg, min(kt + DB, kt_last), rb[p % DB]);
         __builtin_amdgcn_sched_barrier(0);
         qu4_t a4[2][4];
         auto rd4 = [&](int i, qu4_t (&x)[4]) {
@@ -710,7 +796,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kq_kernel(GemmQArgs 
         kq_deq<T>(p, h, hdr, rb[p % DB], bh, bl);
         if (h == 1) {
           __builtin_amdgcn_sched_barrier(0);
-          T::fetch(rw, vb, lg, min(kt + DB, kt_last), rb[p % DB]);
+          T::fetch(rw, rw2, vb, lg, min(kt + DB, kt_last), rb[p % DB]);
           __builtin_amdgcn_sched_barrier(0);
         }
         // activation operands one m-tile ahead of the MFMAs that use them
@@ -760,13 +846,17 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kq_kernel(GemmQArgs 
     }
   }
 
+  if constexpr (GLU) {
+    glu_epilogue<TM>(g, acc, Dc, FM == 2, m0, wcol, lane);
+    return;
+  }
   const float* resid = s == 0 && ks == 0 ? g.resid : nullptr;
   float* dst = ks == 0 ? out : g.kpart;
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int n = n0 + 64 * wn + 16 * j + lr;
+      const int n = wcol + 16 * j + lr;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = m0 + WR * wm + 16 * i + 4 * lg + r;
@@ -826,22 +916,27 @@ static void gemm_q_launch(GemmQArgs g, hipStream_t st) {
   hipLaunchKernelGGL((gemm_q_kernel<DT, BM, BN>), dim3(tiles), dim3(256), 0, st, g);
 }
 
-template <class T, int WGM, int WGN, int DA, int TM = 4, int OCC = 1, int FM = 0>
+template <class T, int WGM, int WGN, int DA, int TM = 4, int OCC = 1, int FM = 0, bool GLU = false>
 static bool gemm_kq_launch(GemmQArgs g, hipStream_t st, bool defer_add) {
   constexpr int BM = 16 * TM * WGM, BN = 64 * WGN;
   int t = 0;
-  for (int i = 0; i < g.nseg; ++i) {
-    g.tile_start[i] = t;
-    t += (g.n[i] + BN - 1) / BN;
+  if (GLU) {
+    t = (g.n[0] + BN / 2 - 1) / (BN / 2);  // 32 act columns per wave
+    for (int i = 0; i <= 3; ++i) g.tile_start[i] = i == 0 ? 0 : t;
+  } else {
+    for (int i = 0; i < g.nseg; ++i) {
+      g.tile_start[i] = t;
+      t += (g.n[i] + BN - 1) / BN;
+    }
+    for (int i = g.nseg; i <= 3; ++i) g.tile_start[i] = t;
   }
-  for (int i = g.nseg; i <= 3; ++i) g.tile_start[i] = t;
   const int tiles = ((g.M + BM - 1) / BM) * t;
   g.xcd_remap = tiles % 8 == 0 ? 1 : 0;
   // split K in two when one workgroup per tile would leave most CUs idle (the M x N of the O and
   // down projections at a 512-token prompt fill half the chip)
   const size_t mn = (size_t)g.M * g.n[0];
-  g.ksplit = (g.kpart && g.nseg == 1 && 2 * tiles <= num_cus() && g.K / QK_K >= 2 && mn % 4 == 0) ? 2 : 1;
-  hipLaunchKernelGGL((gemm_kq_kernel<T, WGM, WGN, DA, TM, OCC, FM>), dim3(tiles * g.ksplit), dim3(64 * WGM * WGN),
+  g.ksplit = (!GLU && g.kpart && g.nseg == 1 && 2 * tiles <= num_cus() && g.K / QK_K >= 2 && mn % 4 == 0) ? 2 : 1;
+  hipLaunchKernelGGL((gemm_kq_kernel<T, WGM, WGN, DA, TM, OCC, FM, GLU>), dim3(tiles * g.ksplit), dim3(64 * WGM * WGN),
                      0, st, g);
   if (g.ksplit == 2) {
     if (defer_add) return true;
@@ -859,15 +954,15 @@ static bool gemm_kq_launch(GemmQArgs g, hipStream_t st, bool defer_add) {
 // the folding); on smaller grids, which then pack two workgroups on some CUs and none on others,
 // it is slower (Q/K/V at 512 rows: 74 -> 80 us). Q6_K's fp16 weight pairs do not fit two waves
 // per SIMD (the rescaled form spills there and is 30% slower; at one wave per SIMD 7% slower).
-template <class T>
+template <class T, bool GLU = false>
 static bool gemm_kq(GemmQArgs g, hipStream_t st, bool defer_add) {
   size_t nt = 0;
   for (int i = 0; i < g.nseg; ++i) nt += (g.n[i] + 255) / 256;
   const size_t tiles = nt * (size_t)((g.M + 63) / 64);
   if constexpr (T::MINS) {
-    if (tiles >= 2 * (size_t)num_cus()) return gemm_kq_launch<T, 1, 4, 1, 4, 2, 2>(g, st, defer_add);
+    if (tiles >= 2 * (size_t)num_cus()) return gemm_kq_launch<T, 1, 4, 1, 4, 2, 2, GLU>(g, st, defer_add);
   }
-  return gemm_kq_launch<T, 1, 4, 1>(g, st, defer_add);
+  return gemm_kq_launch<T, 1, 4, 1, 4, 1, 0, GLU>(g, st, defer_add);
 }
 
 // Tile shape 64 x 64 (measured fastest at the Mistral-7B prefill shapes: the larger tiles lose
@@ -875,6 +970,33 @@ static bool gemm_kq(GemmQArgs g, hipStream_t st, bool defer_add) {
 template <int DT>
 static void gemm_q_dt(GemmQArgs g, hipStream_t st) {
   gemm_q_launch<DT, 64, 64>(g, st);
+}
+
+bool launch_gemm_q_glu(int dt, const void* w_gate, const void* w_up, int N, const __half* xh, const __half* xl,
+                       const float* xs, int M, int K, __half* act_hi, __half* act_lo, float* act_sums, float* act_f32,
+                       hipStream_t st) {
+  if (dt != DT_Q4K && dt != DT_Q6K_R) return false;
+  if (M < 1 || N < 32 || N % 32 != 0 || !gemm_q_ok(dt, w_gate, K) || !gemm_q_ok(dt, w_up, K)) return false;
+  if (dt == DT_Q4K && !xs) fail(ST_OP, "gemm_q: Q4_K needs the per-32 activation sums");
+  GemmQArgs g{};
+  g.nseg = 2;
+  g.w[0] = (const uint8_t*)w_gate;
+  g.w[1] = (const uint8_t*)w_up;
+  g.n[0] = g.n[1] = N;
+  g.M = M;
+  g.K = K;
+  g.xh = xh;
+  g.xl = xl;
+  g.xs = xs;
+  g.ksplit = 1;
+  g.row_bytes = dt == DT_Q4K ? (size_t)(K / QK_K) * Q4K_BYTES : q6r_row_bytes((size_t)(K / QK_K));
+  g.glu_h = reinterpret_cast<_Float16*>(act_hi);
+  g.glu_l = reinterpret_cast<_Float16*>(act_lo);
+  g.glu_sums = reinterpret_cast<_Float16*>(act_sums);
+  g.glu_out = act_f32;
+  if (dt == DT_Q4K) gemm_kq<Q4KB, true>(g, st, false);
+  else gemm_kq<Q6RB, true>(g, st, false);
+  return true;
 }
 
 void launch_add_f32(float* out, const float* part, size_t n, hipStream_t st) {

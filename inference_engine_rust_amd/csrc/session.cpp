@@ -237,8 +237,18 @@ bool Session::quant_ready(const DevTensor* const* ws, int nseg, int M, int K) co
   return true;
 }
 
+// The weight pointer and layout the K-quant GEMMs read (the regrouped Q6_K copy when there is one).
+static const void* kq_weight(const DevTensor& w, int* dt) {
+  if (w.dev_r && w.dtype_r == DT_Q6K_R) {
+    *dt = DT_Q6K_R;
+    return w.dev_r;
+  }
+  *dt = w.dtype;
+  return w.dev;
+}
+
 bool Session::project_q(const DevTensor* const* ws, float* const* outs, int nseg, int M, int K, const float* resid,
-                        float* kpart, bool* pending) {
+                        float* kpart, bool* pending, const __half* xin, const float* sin) {
   if (M < 2) return false;
   int dt = -1;
   GemmQSeg segs[3];
@@ -256,10 +266,31 @@ bool Session::project_q(const DevTensor* const* ws, float* const* outs, int nseg
     if (!gemm_q_ok(dt, p, K)) return false;
     segs[i] = GemmQSeg{p, outs[i], (int)w.dims[1]};
   }
-  const bool left = launch_gemm_q(dt, segs, nseg, xs_, xs_ + (size_t)M * K, xsum_, M, K, resid, st_, kpart,
+  const __half* xh = xin ? xin : xs_;
+  const bool left = launch_gemm_q(dt, segs, nseg, xh, xh + (size_t)M * K, sin ? sin : xsum_, M, K, resid, st_, kpart,
                                   pending != nullptr);
   if (pending) *pending = left;
   return true;
+}
+
+// Gate/up with SwiGLU in the GEMM epilogue, input in xs_ / xsum_: the act planes go to g_ (as
+// halves) and their per-32 sums to u_ (xs_ and xsum_ still hold the GEMM's own input while it
+// runs); the f32 act goes to act_ only when the down projection cannot take the planes.
+bool Session::gate_up_glu(int li, int M) {
+  const LayerTensors& L = m_->layers[li];
+  const int ffn = m_->cfg.layers[li].ffn_dim;
+  const DevTensor* wgu[2] = {&L.gate, &L.up};
+  if (M < 2 || ffn % 32 != 0 || H_ % 32 != 0 || !quant_ready(wgu, 2, M, H_) || (int)L.gate.dims[1] != ffn ||
+      (int)L.up.dims[1] != ffn)
+    return false;
+  int dg = -1, du = -1;
+  const void* pg = kq_weight(L.gate, &dg);
+  const void* pu = kq_weight(L.up, &du);
+  if (dg != du) return false;
+  const DevTensor* wd[1] = {&L.down};
+  __half* ah = reinterpret_cast<__half*>(g_);
+  return launch_gemm_q_glu(dg, pg, pu, ffn, xs_, xs_ + (size_t)M * H_, xsum_, M, H_, ah, ah + (size_t)M * ffn, u_,
+                           quant_ready(wd, 1, M, ffn) ? nullptr : act_, st_);
 }
 
 bool Session::layer_prefill(int li, int M, bool pend_in) {
@@ -338,7 +369,13 @@ bool Session::layer_prefill(int li, int M, bool pend_in) {
   const DevTensor* wgu[2] = {&L.gate, &L.up};
   xs = norm_split(L.ffn_norm, M == 1 || !quant_ready(wgu, 2, M, H_), opend);
   const __half* xa = nullptr;
-  if (M == 1 && L.gate.dtype == L.up.dtype) {
+  const float* xa_sums = nullptr;  // per-32 sums of the down projection's input (default xsum_)
+  const bool glu = xs && gate_up_glu(li, M);
+  if (glu) {
+    xa = reinterpret_cast<const __half*>(g_);
+    xa_sums = u_;
+    // act is in xa / xa_sums
+  } else if (M == 1 && L.gate.dtype == L.up.dtype) {
     MvSegDesc s[2] = {{L.gate.dev, act_, nullptr, S.ffn_dim}, {L.up.dev, nullptr, nullptr, S.ffn_dim}};
     launch_matvec(L.gate.dtype, s, 2, xn_, H_, 2, st_);
   } else {
@@ -361,7 +398,7 @@ bool Session::layer_prefill(int li, int M, bool pend_in) {
   {
     const DevTensor* ws[1] = {&L.down};
     float* outs[1] = {x_};
-    if (!xa || !project_q(ws, outs, 1, M, S.ffn_dim, x_, kpart_ok_ ? tmp_ : nullptr, &dpend))
+    if (!xa || !project_q(ws, outs, 1, M, S.ffn_dim, x_, kpart_ok_ ? tmp_ : nullptr, &dpend, xa, xa_sums))
       project(L.down, act_, xa, M, S.ffn_dim, H_, x_, x_, st_);
   }
   return dpend;
@@ -1013,8 +1050,10 @@ double Session::bench_kernel(int which, int reps, double* work) {
       if (!quant_ready(ws, 2, M, H_)) fail(ST_OP, "bench_kernel: gate/up do not run on the K-quant GEMM");
       total += 2.0 * M * H_ * 2.0 * c.layers[li].ffn_dim;
     }
+    // the gate/up projection as the prefill runs it (SwiGLU in the epilogue where it applies)
     launch = [&, M](int i) {
       const int li = i % L;
+      if (gate_up_glu(li, M)) return;
       const DevTensor* w2[2] = {&m_->layers[li].gate, &m_->layers[li].up};
       float* outs[2] = {g_, u_};
       project_q(w2, outs, 2, M, H_, nullptr);

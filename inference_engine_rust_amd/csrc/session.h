@@ -62,10 +62,13 @@ class Session {
   // pend_in: tmp_ holds split-K partial sums still to be added into x_ (the previous layer's down
   // projection); returns true when this layer's down projection leaves such partial sums.
   bool layer_prefill(int li, int M, bool pend_in = false);
-  // *pending (when given): a split-K partial was left in kpart for the caller to add into outs[0]
+  // *pending (when given): a split-K partial was left in kpart for the caller to add into outs[0].
+  // xin / sin: the input's fp16 pair planes and per-32 sums (default xs_ and xsum_).
   bool project_q(const DevTensor* const* ws, float* const* outs, int nseg, int M, int K, const float* resid,
-                 float* kpart = nullptr, bool* pending = nullptr);
+                 float* kpart = nullptr, bool* pending = nullptr, const __half* xin = nullptr,
+                 const float* sin = nullptr);
   bool quant_ready(const DevTensor* const* ws, int nseg, int M, int K) const;
+  bool gate_up_glu(int li, int M);
   bool fused_ok(int li) const;
   void decode_args(int li, MvArgs& qkv, MvArgs& o, MvArgs& gate_up, MvArgs& down, int* dts);
   void layer_decode(int li, bool last);

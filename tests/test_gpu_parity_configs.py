@@ -209,6 +209,33 @@ def test_q4_k_m_mixed_layers(gpu, big_dir):
     os.remove(p)
 
 
+def test_q4_k_m_mixed_layers_512_prompt(gpu, big_dir):
+    """The same mix at C2's 512-token prompt: layer 0's gate/up GEMM runs the rescaled two-wave
+    variant with SwiGLU in its epilogue and emits the per-32 sums its Q4_K down projection needs
+    (layer 1's Q6_K down takes none); both split-K partials of layer 0 are added by the next
+    norm, layer 1's down partial at the end of the prefill."""
+    spec = synth.preset("c2_l2", mix=2)
+    p = os.path.join(big_dir, "c2_l2_mix512.gguf")
+    synth.write_llama(p, spec, seed=5)
+    m, om = E.LoadedModel.load(p), O.Model(p)
+    assert m.tensor("blk.0.ffn_down.weight")["dtype"] == E.Q4K and m.tensor("blk.1.ffn_down.weight")["dtype"] == E.Q6K
+    prompt = synth.prompt_ids(17, 512)
+    s, r = E.InferenceSession(m), O.Session(om)
+    s.prefill(prompt)
+    r.prefill(prompt)
+    assert rel_l2(s.hidden(), r.hidden()) < 1e-4
+    worst = 0.0
+    for step in range(3):
+        lg, lr = s.logits_last_token(), r.logits()
+        worst = max(worst, rel_l2(lg, lr))
+        t = O.argmax(lr)
+        assert E.greedy_next_token(s) == t, f"step {step}"
+        s.decode_token(t)
+        r.decode(t)
+    assert worst < LOGIT_REL_L2, worst
+    os.remove(p)
+
+
 def test_f16_tensors_load_as_their_f32_values(gpu, model_dir):
     """F16 tensors (rejected by the reference, src/model_loader/tensor.rs:87-97) are widened to F32
     at load: a model with F16 norm weights runs bit for bit as the same model storing those f16
