@@ -304,11 +304,29 @@ __global__ __launch_bounds__(256) void kv_split_kernel(const float* __restrict__
 }
 
 // The prompt's attention inputs in one pass (replaces RoPE on Q and on K, the KV append and
-// kv_split_kernel): workgroup (position tile, 64-dim tile, z). z < n_kv: KV head z, whose K rows
-// get RoPE at the prompt positions 0..M-1 in registers (the pair partner from the neighbouring
-// lane, the arithmetic of rotate() in ops.hip, src/ops/rope.rs:11-59), then go to the cache at
-// pos0 + p (f32 or fp16, as kv_store_kernel) and to the K planes; V goes to the cache and, through
-// LDS, to the transposed V planes. z >= n_kv: query head z - n_kv gets RoPE in place.
+// kv_split_kernel): workgroup (position tile, 64-dim tile, z); a thread takes four consecutive head
+// dims (two RoPE pairs, the arithmetic of rotate() in ops.hip, src/ops/rope.rs:11-59) of rows
+// (tid >> 4) + 16 r. z < n_kv: KV head z, whose K rows get RoPE at the prompt positions 0..M-1 in
+// registers, then go to the cache at pos0 + p (f32 or fp16, as kv_store_kernel) and to the K
+// planes; V goes to the cache and, through LDS, to the transposed V planes. z >= n_kv: query head
+// z - n_kv gets RoPE in place.
+IEK_DEV void rope4(float4& x, const float* cs, int p, int npairs, int d) {
+#pragma clang fp contract(off)
+  const float2* e = reinterpret_cast<const float2*>(cs) + (size_t)p * npairs + (d >> 1);
+  if (d < 2 * npairs) {
+    const float2 c = e[0];
+    const float t0 = x.x, t1 = x.y;
+    x.x = t0 * c.x - t1 * c.y;
+    x.y = t0 * c.y + t1 * c.x;
+  }
+  if (d + 2 < 2 * npairs) {
+    const float2 c = e[1];
+    const float t0 = x.z, t1 = x.w;
+    x.z = t0 * c.x - t1 * c.y;
+    x.w = t0 * c.y + t1 * c.x;
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void attn_prep_kernel(float* __restrict__ q, const float* __restrict__ k,
                                                         const float* __restrict__ v, int M, int n_heads, int n_kv,
@@ -316,58 +334,62 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(float* __restrict__ q, c
                                                         T* __restrict__ kc, T* __restrict__ vc, int ctx, int pos0,
                                                         _Float16* __restrict__ kh, _Float16* __restrict__ kl,
                                                         _Float16* __restrict__ vh, _Float16* __restrict__ vl) {
-#pragma clang fp contract(off)
   __shared__ float tile[64][65];
-  const int z = blockIdx.z, d0 = blockIdx.y * 64, p0 = blockIdx.x * 64, tid = threadIdx.x, dl = tid & 63;
-  const int d = d0 + dl;
-  // RoPE of element (p, d) of a head row given its pair partner (the lane d ^ 1 holds it)
-  auto rope = [&](float x, int p) -> float {
-#pragma clang fp contract(off)
-    const float y = __shfl_xor(x, 1, 64);
-    if (d >= 2 * npairs || d >= hd) return x;
-    const float2 e = reinterpret_cast<const float2*>(cs)[(size_t)p * npairs + (d >> 1)];
-    return (d & 1) ? y * e.y + x * e.x : x * e.x - y * e.y;
-  };
+  const int z = blockIdx.z, d0 = blockIdx.y * 64, p0 = blockIdx.x * 64, tid = threadIdx.x;
+  const int c4 = 4 * (tid & 15), d = d0 + c4;  // the thread's four head dims
   if (z >= n_kv) {
     const int h = z - n_kv;
     const size_t qd = (size_t)n_heads * hd;
-#pragma unroll 4
-    for (int r = 0; r < 16; ++r) {
-      const int p = p0 + (tid >> 6) + 4 * r;
-      const bool live = p < M && d < hd;
-      float* e = q + (size_t)p * qd + (size_t)h * hd + d;
-      const float x = live ? *e : 0.f;
-      const float o = rope(x, p);  // every lane joins the exchange
-      if (live) *e = o;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int p = p0 + (tid >> 4) + 16 * r;
+      if (p < M && d < hd) {
+        float4* e = reinterpret_cast<float4*>(q + (size_t)p * qd + (size_t)h * hd + d);
+        float4 x = *e;
+        rope4(x, cs, p, npairs, d);
+        *e = x;
+      }
     }
     return;
   }
   const int h = z;
   const size_t kvd = (size_t)n_kv * hd;
-#pragma unroll 4
-  for (int r = 0; r < 16; ++r) {
-    const int pl = (tid >> 6) + 4 * r, p = p0 + pl;
-    const bool live = p < M && d < hd;
-    const size_t src = (size_t)p * kvd + (size_t)h * hd + d;
-    const float kx = live ? k[src] : 0.f;
-    const float vv = live ? v[src] : 0.f;
-    const float kr = rope(kx, p);
-    if (live) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int pl = (tid >> 4) + 16 * r, p = p0 + pl;
+    float4 vv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (p < M && d < hd) {
+      const size_t src = (size_t)p * kvd + (size_t)h * hd + d;
+      float4 kx = *reinterpret_cast<const float4*>(k + src);
+      vv = *reinterpret_cast<const float4*>(v + src);
+      rope4(kx, cs, p, npairs, d);
       const size_t dst = ((size_t)h * ctx + pos0 + p) * hd + d;
       if constexpr (std::is_same<T, float>::value) {
-        kc[dst] = kr;
-        vc[dst] = vv;
+        *reinterpret_cast<float4*>(kc + dst) = kx;
+        *reinterpret_cast<float4*>(vc + dst) = vv;
       } else {
-        kc[dst] = __float2half_rn(kr);
-        vc[dst] = __float2half_rn(vv);
+        kc[dst] = __float2half_rn(kx.x);
+        kc[dst + 1] = __float2half_rn(kx.y);
+        kc[dst + 2] = __float2half_rn(kx.z);
+        kc[dst + 3] = __float2half_rn(kx.w);
+        vc[dst] = __float2half_rn(vv.x);
+        vc[dst + 1] = __float2half_rn(vv.y);
+        vc[dst + 2] = __float2half_rn(vv.z);
+        vc[dst + 3] = __float2half_rn(vv.w);
       }
-      _Float16 a, b;
-      asplit(kr, a, b);
+      _Float16 a[4], b[4];
+      asplit(kx.x, a[0], b[0]);
+      asplit(kx.y, a[1], b[1]);
+      asplit(kx.z, a[2], b[2]);
+      asplit(kx.w, a[3], b[3]);
       const size_t kd = ((size_t)h * M + p) * hd + d;
-      kh[kd] = a;
-      kl[kd] = b;
+      *reinterpret_cast<uint2*>(kh + kd) = make_uint2(apack2(a[0], a[1]), apack2(a[2], a[3]));
+      *reinterpret_cast<uint2*>(kl + kd) = make_uint2(apack2(b[0], b[1]), apack2(b[2], b[3]));
     }
-    tile[pl][dl] = vv;
+    tile[pl][c4] = vv.x;
+    tile[pl][c4 + 1] = vv.y;
+    tile[pl][c4 + 2] = vv.z;
+    tile[pl][c4 + 3] = vv.w;
   }
   __syncthreads();
 #pragma unroll 4
