@@ -121,8 +121,9 @@ IEK_DEV void emit_split8(const float (&v)[8], size_t i, bool live, uint4* __rest
 // rmsnorm (as rmsnorm_kernel) that also emits the GEMM input planes of its output (the f32 output
 // itself only when `out` is set).
 // With `part` the row is in + part (one f32 add per element, as the split-K add pass would do),
-// written back to `in` by the thread that reads it in the second loop, after every read of the
-// first loop (the barrier inside block_sum256).
+// written back to `in`. Each thread keeps its chunks of eight (chunk t, t + 256, ...; CPT of them)
+// in registers between the sum of squares and the scaling, so the row is read once.
+template <int CPT>
 __global__ __launch_bounds__(256) void rmsnorm_split_kernel(float* in, const float* w, int dim, float eps,
                                                             float* out, uint4* hi, uint4* lo, _Float16* sh,
                                                             _Float16* sl, const float* part) {
@@ -131,19 +132,13 @@ __global__ __launch_bounds__(256) void rmsnorm_split_kernel(float* in, const flo
   float* x = in + (size_t)blockIdx.x * dim;
   const float* pr = part ? part + (size_t)blockIdx.x * dim : nullptr;
   float* y = out + (size_t)blockIdx.x * dim;
-  float ss = 0.f;
-  for (int i = threadIdx.x; i < dim; i += blockDim.x) {
-    const float xv = pr ? x[i] + pr[i] : x[i];
-    ss += xv * xv;
-  }
-  ss = block_sum256(ss, red);
-  const float rms = sqrtf(ss / (float)dim + eps);
   const int n8 = dim / 8;
-  for (int i0 = 0; i0 < n8; i0 += 256) {
-    const int e = i0 + threadIdx.x;
-    const bool live = e < n8;
-    float v[8];
-    const int c = live ? e : 0;
+  float4 xv[CPT][2];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int e = 256 * k + threadIdx.x;
+    const int c = e < n8 ? e : 0;
     float4 xa = reinterpret_cast<const float4*>(x)[2 * c], xb = reinterpret_cast<const float4*>(x)[2 * c + 1];
     if (pr) {
       const float4 pa = reinterpret_cast<const float4*>(pr)[2 * c], pb = reinterpret_cast<const float4*>(pr)[2 * c + 1];
@@ -155,12 +150,27 @@ __global__ __launch_bounds__(256) void rmsnorm_split_kernel(float* in, const flo
       xb.y += pb.y;
       xb.z += pb.z;
       xb.w += pb.w;
-      if (live) {
-        reinterpret_cast<float4*>(x)[2 * c] = xa;
-        reinterpret_cast<float4*>(x)[2 * c + 1] = xb;
-      }
+    }
+    xv[k][0] = xa;
+    xv[k][1] = xb;
+    if (e < n8)
+      ss += (((xa.x * xa.x + xa.y * xa.y) + (xa.z * xa.z + xa.w * xa.w)) +
+             ((xb.x * xb.x + xb.y * xb.y) + (xb.z * xb.z + xb.w * xb.w)));
+  }
+  ss = block_sum256(ss, red);  // every read of the row is done
+  const float rms = sqrtf(ss / (float)dim + eps);
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int e = 256 * k + threadIdx.x;
+    const bool live = e < n8;
+    const int c = live ? e : 0;
+    const float4 xa = xv[k][0], xb = xv[k][1];
+    if (pr && live) {
+      reinterpret_cast<float4*>(x)[2 * c] = xa;
+      reinterpret_cast<float4*>(x)[2 * c + 1] = xb;
     }
     const float4 wa = reinterpret_cast<const float4*>(w)[2 * c], wb = reinterpret_cast<const float4*>(w)[2 * c + 1];
+    float v[8];
     v[0] = (xa.x * wa.x) / rms;
     v[1] = (xa.y * wa.y) / rms;
     v[2] = (xa.z * wa.z) / rms;
@@ -173,6 +183,7 @@ __global__ __launch_bounds__(256) void rmsnorm_split_kernel(float* in, const flo
       reinterpret_cast<float4*>(y)[2 * c] = make_float4(v[0], v[1], v[2], v[3]);
       reinterpret_cast<float4*>(y)[2 * c + 1] = make_float4(v[4], v[5], v[6], v[7]);
     }
+    // emit_split8 exchanges across the group of four lanes: every lane joins
     emit_split8(v, (size_t)blockIdx.x * n8 + c, live, hi, lo, sh, sl);
   }
 }
@@ -185,8 +196,16 @@ void launch_rmsnorm_split(float* in, const float* w, int rows, int dim, float ep
     fail(ST_OP, "rmsnorm_split: dim % 32 and 16-byte aligned rows");
   _Float16* s = reinterpret_cast<_Float16*>(sums);
   const size_t nb = (size_t)rows * (dim / 32);
-  hipLaunchKernelGGL(rmsnorm_split_kernel, dim3(rows), dim3(256), 0, st, in, w, dim, eps, out, (uint4*)hi, (uint4*)lo,
-                     s, s + nb, part);
+  const int cpt = (dim / 8 + 255) / 256;  // chunks of eight per thread
+#define IEK_RS(C)                                                                                                   \
+  hipLaunchKernelGGL(rmsnorm_split_kernel<C>, dim3(rows), dim3(256), 0, st, in, w, dim, eps, out, (uint4*)hi,      \
+                     (uint4*)lo, s, s + nb, part)
+  if (cpt <= 1) IEK_RS(1);
+  else if (cpt <= 2) IEK_RS(2);
+  else if (cpt <= 4) IEK_RS(4);
+  else if (cpt <= 8) IEK_RS(8);
+  else fail(ST_OP, "rmsnorm_split: rows wider than 16384");
+#undef IEK_RS
 }
 
 // fp16 pair planes and per-32 sums of an existing [rows, K] input in one pass.
