@@ -36,8 +36,10 @@ namespace iek {
 
 namespace {
 
-constexpr int NC = 8;                 // consumer waves
-constexpr int DSLOT = 3;              // LDS slots (items in flight) per consumer
+// 12 consumers with 2 slots each measured 1.3% faster than 8 with 3 (the same LDS ring bytes):
+// the ring fills early in a phase transition, so more waves reducing beat deeper slots
+constexpr int NC = 12;                // consumer waves
+constexpr int DSLOT = 2;              // LDS slots (items in flight) per consumer
 constexpr bool L2PF = false;          // touch each item's lines DSLOT items before its copy
 constexpr int NT = 64 * (1 + NC);     // threads per workgroup
 constexpr int SLOT = 3584;            // bytes per slot: 3 x 1 KB columns + 16 + 2 columns of 16 B
@@ -670,7 +672,8 @@ bool chain_phase_ok(int dt, int K, bool norm) {
   if (dt != DT_Q4K && dt != DT_Q6K_R) return false;
   if (K % QK_K != 0 || K <= 0) return false;
   const int npass = (K + 4095) / 4096;
-  if (npass > 4 || NC % npass != 0) return false;
+  // a consumer's pass is c & (npass - 1): npass must be a power of two that divides NC
+  if (npass > 4 || (npass & (npass - 1)) != 0 || NC % npass != 0) return false;
   if (norm && 2 * npass > 4) return false;  // x and norm weight columns share the staging region
   return true;
 }
