@@ -90,7 +90,6 @@ def prefill_flops(cfg, specs, prompt):
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "c2_chain_traffic.json")
 MFMA_PEAK_TFLOPS = 2500.0  # dense fp16/bf16 MFMA
-GOLDEN_TOKENS = os.path.join(ROOT, "tests", "golden", "c2_seed0_tokens.json")
 GAP_EXACT = 1e-2
 
 
@@ -280,9 +279,11 @@ def cpu_baseline(path, n_layers_sample, prompt):
 
 
 def golden_tokens_match(E, sess, prompt, cfg_name):
-    """The first greedy tokens of the C2 model against the committed oracle run (tests/golden/
-    c2_seed0_tokens.json, same model and prompt): equal wherever the oracle's two best logits are
-    at least GAP_EXACT apart; at a closer step either of the two ends the comparison."""
+    """The device's greedy tokens against the committed oracle run of the same model and prompt
+    (tests/golden/<config>_seed0.json), teacher-forced: at each step the device's greedy token must
+    equal the oracle's (or be its runner-up where the oracle's two best logits are within
+    GAP_EXACT), then the oracle's token is decoded. Returns (all matched, steps compared), or None
+    when no golden run covers this configuration and prompt."""
     if cfg_name == "c0" and len(prompt) == 16:
         # C0: the oracle's 32 greedy tokens (tests/golden/c0_seed0.json), exact
         with open(os.path.join(ROOT, "tests", "golden", "c0_seed0.json")) as f:
@@ -291,19 +292,24 @@ def golden_tokens_match(E, sess, prompt, cfg_name):
             return None
         sess.reset()
         sess.prefill(prompt)
-        return sess.generate_greedy(len(g["tokens"])) == g["tokens"]
-    if cfg_name != "c2" or len(prompt) != 512:
+        return sess.generate_greedy(len(g["tokens"])) == g["tokens"], len(g["tokens"])
+    path = os.path.join(ROOT, "tests", "golden", f"{cfg_name}_seed0.json")
+    if not os.path.exists(path):
         return None
-    with open(GOLDEN_TOKENS) as f:
+    with open(path) as f:
         g = json.load(f)
+    if g["n_prompt"] != len(prompt) or g["prompt_seed"] != 0:
+        return None
     sess.reset()
     sess.prefill(prompt)
-    for t, t2, gap in zip(g["tokens"], g["runner_up"], g["top2_gap"]):
+    ok = True
+    for i, st in enumerate(g["steps"]):
         got = E.greedy_next_token(sess)
-        if got != t:
-            return bool(gap < GAP_EXACT and got == t2)
-        sess.decode_token(got)
-    return True
+        if got != st["token"] and not (st["gap"] < GAP_EXACT and got == st["runner_up"]):
+            ok = False
+        if i + 1 < len(g["steps"]):
+            sess.decode_token(st["token"])
+    return ok, len(g["steps"])
 
 
 def main():
@@ -413,9 +419,9 @@ def main():
     step_bytes = wbytes + kv_avg
     step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    roof = roof_pf = match = None
+    roof = roof_pf = None
+    match = golden_tokens_match(E, sess, prompt, args.config)
     if not gemma:
-        match = golden_tokens_match(E, sess, prompt, args.config)
         # the chain launch is the dominant decode kernel where the session decodes through it (the
         # tiny C0 model, whose FFN width is not a multiple of 256, runs per-launch kernels: latency)
         if sess.decode_path() == 1:
@@ -451,6 +457,9 @@ def main():
         "metric": METRIC, "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32",
+        "dtype_detail": {"decode": "f32 activations and f32 KV cache",
+                         "prefill": "matrix-core GEMMs on the fp16 (hi, lo) pair of each f32 activation (22 "
+                                    "significant bits), exact integer weight operands, f32 accumulation"},
         "data": data,
         "config": {"workload": f"{args.config}: {arch}, {args.prompt}-token prompt prefill then greedy decode "
                                f"at batch 1, {kv}",
@@ -465,7 +474,8 @@ def main():
         "roofline_prefill": roof_pf,
         "cpu_baseline": cpu,
         "first_decode_tokens": toks[:8],
-        "first_tokens_match_oracle": match,
+        "first_tokens_match_oracle": None if match is None else match[0],
+        "oracle_steps_checked": None if match is None else match[1],
     }
     print(json.dumps(out), flush=True)
 

@@ -134,6 +134,18 @@ iek_status iek_session_kv_len(const iek_session* s, uint64_t* out);
  * launch per matvec and attention, 1 = the decode chain (Q/K/V, O, gate/up and down as phases of
  * persistent launches, two launches per layer). Both compute the same function. */
 iek_status iek_session_decode_path(const iek_session* s, int* out);
+/* No reference counterpart; a test aid for the decode chain's failure path. Sets the iteration
+ * limit of the chain's bounded waits (each ~64 clocks; 0 restores the default, ~0.1-0.2 s). With a
+ * small limit the next chain step gives its waits up: every kernel still exits normally, the call
+ * fails with IEK_ERR_DEVICE, and the session state is undefined until iek_session_reset.
+ * IEK_ERR_OP when the session does not decode through the chain. */
+iek_status iek_session_set_chain_spin(iek_session* s, uint32_t spin);
+/* No reference counterpart; a diagnostic. The prefill GEMMs and attention run on the matrix cores
+ * with each f32 activation held as an fp16 (hi, lo) pair. When a value (or a per-32 sum of a GEMM
+ * input) is beyond that pair's range (|x| > 65504), the prefill (session or layer level) runs again
+ * on f32 activations, so that any finite f32 the reference takes is taken. *out: how many prefills
+ * of this session have done so. */
+iek_status iek_session_f32_prefills(const iek_session* s, int* out);
 /* No reference counterpart; a measurement aid for the roofline figures. Times `reps` back-to-back
  * launches of one hot kernel on the session's stream between two HIP events, launch i on layer
  * i % n (so that consecutive launches stream different weights from HBM): which = 0, the decode

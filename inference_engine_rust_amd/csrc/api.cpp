@@ -188,6 +188,8 @@ iek_status iek_session_generate_greedy(iek_session* s, size_t n, uint32_t* out) 
 iek_status iek_session_kv_len(const iek_session* s, uint64_t* out) { IEK_API_TRY(*out = (uint64_t)s->s->kv_len()) }
 
 iek_status iek_session_decode_path(const iek_session* s, int* out) { IEK_API_TRY(*out = s->s->decode_path()) }
+iek_status iek_session_set_chain_spin(iek_session* s, uint32_t spin) { IEK_API_TRY(s->s->set_chain_spin(spin)) }
+iek_status iek_session_f32_prefills(const iek_session* s, int* out) { IEK_API_TRY(*out = s->s->f32_prefills()) }
 
 iek_status iek_session_bench_kernel(iek_session* s, int which, int reps, double* avg_us, double* work) {
   IEK_API_TRY(*avg_us = s->s->bench_kernel(which, reps, work))
@@ -477,7 +479,7 @@ iek_status iek_dev_attention_decode_noalloc(const float* q, const void* k_cache,
                       std::to_string(part_cap) + "-byte scratch (n_heads * ceil(max_seq_len / 64) * (head_dim + 2) "
                       "floats); use iek_dev_attention_decode");
     if ((2 * n_kv_heads + 1) * 4 > NOALLOC_COUNTER_BYTES) fail(ST_OP, "attention (no-alloc): too many KV heads");
-    char* base = static_cast<char*>(noalloc_scratch());
+    char* base = static_cast<char*>(noalloc_scratch(as_stream(stream)));
     int* cnt = reinterpret_cast<int*>(base);
     float* part = reinterpret_cast<float*>(base + NOALLOC_COUNTER_BYTES);
     attention_launch(q, k_cache, v_cache, kv_dtype == IEK_F32, n_heads, n_kv_heads, head_dim, max_seq_len, total_pos,

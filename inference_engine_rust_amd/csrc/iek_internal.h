@@ -77,7 +77,7 @@ bool launch_gemm_q(int dt, const GemmQSeg* segs, int nseg, const __half* xh, con
 // Returns false, launching nothing, for other weight types or shapes.
 bool launch_gemm_q_glu(int dt, const void* w_gate, const void* w_up, int N, const __half* xh, const __half* xl,
                        const float* xs, int M, int K, __half* act_hi, __half* act_lo, float* act_sums, float* act_f32,
-                       hipStream_t st);
+                       int* ovf, hipStream_t st);
 // out[i] += part[i] for i < n (n % 4 == 0, 16-byte aligned)
 void launch_add_f32(float* out, const float* part, size_t n, hipStream_t st);
 void launch_gemm_mfma(int dt, const void* w, const __half* xh, const __half* xl, int M, int K, int N, float* out,
@@ -90,12 +90,33 @@ void launch_rmsnorm(const float* in, const float* w, int rows, int dim, float ep
 // and its per-32 sums as an fp16 pair (two planes of rows * dim / 32 halves at `sums`), as
 // launch_split_f16 + launch_block_sums would (dim % 32 == 0, 16-byte aligned rows). A null `out`
 // skips the f32 output. With `part`, in[i] + part[i] (one f32 add, as launch_add_f32) is
-// normalised and written back to `in`.
+// normalised and written back to `in`. A value or per-32 sum beyond the pair's range (F16_PAIR_MAX)
+// sets *ovf (when given).
 void launch_rmsnorm_split(float* in, const float* w, int rows, int dim, float eps, float* out, __half* hi,
-                          __half* lo, float* sums, hipStream_t st, const float* part = nullptr);
-void launch_split_sums(const float* a, int rows, int K, __half* hi, __half* lo, float* sums, hipStream_t st);
+                          __half* lo, float* sums, int* ovf, hipStream_t st, const float* part = nullptr);
+void launch_split_sums(const float* a, int rows, int K, __half* hi, __half* lo, float* sums, int* ovf,
+                       hipStream_t st);
 void launch_swiglu_split(const float* g, const float* u, float* out, int rows, int K, __half* hi, __half* lo,
-                         float* sums, hipStream_t st);
+                         float* sums, int* ovf, hipStream_t st);
+// *ovf = 1 when some |a[i]| (i < n) exceeds F16_PAIR_MAX (a prefill attention input the matrix-core
+// kernels split into fp16 pairs themselves).
+void launch_range_flag(const float* a, size_t n, int* ovf, hipStream_t st);
+// Op-level GEMM inputs with any f32 range: per row, the power-of-two factor s (1 unless the row's
+// largest |value| or per-32 sum exceeds 2^15, then the factor that brings it into [2^14, 2^15)),
+// the fp16 (hi, lo) planes of s * a and the per-32 sums of s * a (fp16 pair planes), and
+// inv[m] = 1 / s. Then launch_row_scale multiplies each output row by inv[m]; power-of-two factors
+// make both steps exact.
+void launch_split_scaled(const float* a, int rows, int K, __half* hi, __half* lo, float* sums, float* inv,
+                         hipStream_t st);
+void launch_row_scale(float* out, int rows, int N, const float* inv, hipStream_t st);
+// Prefill attention on f32 inputs (the path taken when an input is beyond the fp16 pair's range):
+// q [M][n_heads*hd], k and v [M][n_kv*hd] (RoPE applied), causal over the M prompt rows with the
+// sliding-window bound; one wave per (query row, head), online softmax in f32.
+void launch_attn_prefill_f32(const float* q, const float* k, const float* v, float* out, int M, int n_heads, int n_kv,
+                             int head_dim, int window, float scale, hipStream_t st);
+// The tiled SIMT GEMM on f32 activations (no fp16 operand), for every weight type.
+void launch_gemm_f32(int dt, const void* w, const float* a, int M, int K, int N, float* out, const float* resid,
+                     hipStream_t st);
 void launch_rope_rows(float* v, int rows, int row_stride, int n_heads, int head_dim, int pos0, const float* cs,
                       int half_pairs, hipStream_t st);
 void launch_rope_table(float* v, int n_heads, int head_dim, int npairs, const float* cs, const int* pos_dev,
@@ -133,22 +154,25 @@ size_t attn_decode_part_floats(int n_heads, int head_dim, int max_len);
 // per device, [counters + position: NOALLOC_COUNTER_BYTES][attention partials: the rest].
 constexpr size_t NOALLOC_SCRATCH_BYTES = 16u << 20;
 constexpr size_t NOALLOC_COUNTER_BYTES = 4096;
-// Device address of the current device's scratch array (resolved once per device).
-void* noalloc_scratch();
+// Device address of the scratch array of the stream's device (the current device for the null
+// stream), resolved once per device.
+void* noalloc_scratch(hipStream_t st);
 // With a scratch buffer of attn_prefill_scratch_halves() halves (head_dim 64 or 128), each K/V block
 // is staged once for all the query heads of its KV head; otherwise one workgroup per query head.
 size_t attn_prefill_scratch_halves(int M, int n_kv, int head_dim);
-// planes_ready: launch_attn_prefill_prep already wrote the K/V planes into the scratch.
+// planes_ready: launch_attn_prefill_prep already wrote the K/V planes into the scratch (and
+// flagged out-of-range inputs); otherwise q, k and v are range-checked here into *ovf (when given).
 void launch_attn_prefill(const float* q, const float* k, const float* v, float* out, int M, int n_heads, int n_kv,
                          int head_dim, int window, float scale, hipStream_t st, void* scratch = nullptr,
-                         size_t scratch_halves = 0, bool planes_ready = false);
+                         size_t scratch_halves = 0, bool planes_ready = false, int* ovf = nullptr);
 // RoPE (table `cs`, npairs pairs, prompt positions 0..M-1) on q in place and on k, the KV append of
 // k and v at cache position pos0 and the K/V planes of the shared-K/V path, in one launch (k and v
 // are left as they were). Returns false, launching nothing, when the shared-K/V path does not
 // apply (then the caller runs RoPE, the append and launch_attn_prefill with planes_ready false).
+// A q, k or v value beyond F16_PAIR_MAX sets *ovf.
 bool launch_attn_prefill_prep(float* q, const float* k, const float* v, int M, int n_heads, int n_kv, int head_dim,
                               const float* cs, int npairs, void* kc, void* vc, bool kv_f32, int ctx, int pos0,
-                              void* scratch, size_t scratch_halves, hipStream_t st);
+                              void* scratch, size_t scratch_halves, int* ovf, hipStream_t st);
 // Gemma-4 pieces (kernels/gemma.hip).
 void launch_head_prep(float* q, float* k, float* v, int rows, int q_stride, int kv_stride, int nq, int nkv, int hd,
                       const float* qn, const float* kn, float eps, bool vnorm, const float* cs, int npairs,

@@ -333,13 +333,18 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(float* __restrict__ q, c
                                                         int hd, int Mp, const float* __restrict__ cs, int npairs,
                                                         T* __restrict__ kc, T* __restrict__ vc, int ctx, int pos0,
                                                         _Float16* __restrict__ kh, _Float16* __restrict__ kl,
-                                                        _Float16* __restrict__ vh, _Float16* __restrict__ vl) {
+                                                        _Float16* __restrict__ vh, _Float16* __restrict__ vl,
+                                                        int* __restrict__ ovf) {
   __shared__ float tile[64][65];
   const int z = blockIdx.z, d0 = blockIdx.y * 64, p0 = blockIdx.x * 64, tid = threadIdx.x;
   const int c4 = 4 * (tid & 15), d = d0 + c4;  // the thread's four head dims
+  auto big4 = [](const float4& x) {
+    return fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))) > F16_PAIR_MAX;
+  };
   if (z >= n_kv) {
     const int h = z - n_kv;
     const size_t qd = (size_t)n_heads * hd;
+    bool big = false;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int p = p0 + (tid >> 4) + 16 * r;
@@ -348,10 +353,13 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(float* __restrict__ q, c
         float4 x = *e;
         rope4(x, cs, p, npairs, d);
         *e = x;
+        big |= big4(x);
       }
     }
+    if (big) *ovf = 1;
     return;
   }
+  bool big = false;
   const int h = z;
   const size_t kvd = (size_t)n_kv * hd;
 #pragma unroll
@@ -363,6 +371,7 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(float* __restrict__ q, c
       float4 kx = *reinterpret_cast<const float4*>(k + src);
       vv = *reinterpret_cast<const float4*>(v + src);
       rope4(kx, cs, p, npairs, d);
+      big |= big4(kx) || big4(vv);
       const size_t dst = ((size_t)h * ctx + pos0 + p) * hd + d;
       if constexpr (std::is_same<T, float>::value) {
         *reinterpret_cast<float4*>(kc + dst) = kx;
@@ -391,6 +400,7 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(float* __restrict__ q, c
     tile[pl][c4 + 2] = vv.z;
     tile[pl][c4 + 3] = vv.w;
   }
+  if (big) *ovf = 1;
   __syncthreads();
 #pragma unroll 4
   for (int r = 0; r < 16; ++r) {
@@ -599,6 +609,75 @@ __global__ __launch_bounds__(256) void attn_prefill_gqa_kernel(const float* __re
     }
 }
 
+// Prefill attention on f32 inputs (taken when a q, k or v value is beyond the fp16 pair's range):
+// the reference's per-(position, head) loop (src/layers/attention.rs:364-415) with an online
+// softmax. One wave per (query row i, head h): keys j in [j_min, i] (j_min = i - (window - 1)
+// with a window) in chunks of 64, lane = key for the scores (dot * scale in f32), lane = head
+// dims for P V. q and k carry RoPE; k and v rows are [M][n_kv * hd], KV head h / (n_heads / n_kv).
+__global__ __launch_bounds__(64) void attn_prefill_f32_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                              const float* __restrict__ v, float* __restrict__ out,
+                                                              int M, int n_heads, int n_kv, int hd, int window,
+                                                              float scale) {
+#pragma clang fp contract(off)
+  constexpr int DPL = 8;  // head dims per lane (hd <= 512)
+  __shared__ float qs[512];
+  __shared__ float ps[64];
+  const int i = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+  const int kvh = h / (n_heads / n_kv);
+  const size_t qd = (size_t)n_heads * hd, kvd = (size_t)n_kv * hd;
+  for (int d = lane; d < hd; d += 64) qs[d] = q[(size_t)i * qd + (size_t)h * hd + d];
+  __syncthreads();
+  const int j0 = window > 0 ? max(0, i - (window - 1)) : 0;
+  float m = -INFINITY, l = 0.f, o[DPL];
+#pragma unroll
+  for (int t = 0; t < DPL; ++t) o[t] = 0.f;
+  for (int jb = j0; jb <= i; jb += 64) {
+    const int j = jb + lane;
+    float sc = -INFINITY;
+    if (j <= i) {
+      const float* kr = k + (size_t)j * kvd + (size_t)kvh * hd;
+      float dot = 0.f;
+      for (int d = 0; d < hd; ++d) dot += qs[d] * kr[d];
+      sc = dot * scale;
+    }
+    const float cm = wave_max(sc);
+    const float mn = fmaxf(m, cm);
+    const float p = j <= i ? expf(sc - mn) : 0.f;
+    const float corr = expf(m - mn);  // 0 on the first chunk (m = -inf)
+    l = l * corr + wave_sum(p);
+#pragma unroll
+    for (int t = 0; t < DPL; ++t) o[t] *= corr;
+    m = mn;
+    ps[lane] = p;
+    __syncthreads();
+    const int nj = min(64, i + 1 - jb);
+    for (int jj = 0; jj < nj; ++jj) {
+      const float pj = ps[jj];
+      const float* vr = v + (size_t)(jb + jj) * kvd + (size_t)kvh * hd;
+#pragma unroll
+      for (int t = 0; t < DPL; ++t) {
+        const int d = lane + 64 * t;
+        if (d < hd) o[t] += pj * vr[d];
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int t = 0; t < DPL; ++t) {
+    const int d = lane + 64 * t;
+    if (d < hd) out[(size_t)i * qd + (size_t)h * hd + d] = o[t] / l;
+  }
+}
+
+void launch_attn_prefill_f32(const float* q, const float* k, const float* v, float* out, int M, int n_heads, int n_kv,
+                             int head_dim, int window, float scale, hipStream_t st) {
+  if (M <= 0) return;
+  if (head_dim <= 0 || head_dim > 512 || n_kv <= 0 || n_heads % n_kv != 0)
+    fail(ST_OP, "prefill attention (f32): head_dim <= 512 and whole GQA groups");
+  hipLaunchKernelGGL(attn_prefill_f32_kernel, dim3(M, n_heads), dim3(64), 0, st, q, k, v, out, M, n_heads, n_kv,
+                     head_dim, window, scale);
+}
+
 // Scratch halves the shared-K/V path needs: four planes of n_kv * HD * Mp.
 size_t attn_prefill_scratch_halves(int M, int n_kv, int head_dim) {
   const size_t Mp = (size_t)((M + 63) / 64) * 64;
@@ -612,8 +691,9 @@ static bool attn_planes_ok(int M, int n_heads, int n_kv, int head_dim, const voi
 
 bool launch_attn_prefill_prep(float* q, const float* k, const float* v, int M, int n_heads, int n_kv, int head_dim,
                               const float* cs, int npairs, void* kc, void* vc, bool kv_f32, int ctx, int pos0,
-                              void* scratch, size_t scratch_halves, hipStream_t st) {
-  if (!attn_planes_ok(M, n_heads, n_kv, head_dim, scratch, scratch_halves) || npairs < 0 || 2 * npairs > head_dim)
+                              void* scratch, size_t scratch_halves, int* ovf, hipStream_t st) {
+  if (!attn_planes_ok(M, n_heads, n_kv, head_dim, scratch, scratch_halves) || npairs < 0 || 2 * npairs > head_dim ||
+      !ovf)
     return false;
   if (pos0 < 0 || (size_t)pos0 + (size_t)M > (size_t)ctx) fail(ST_KVCACHE, "attention prep: the prompt does not fit the cache");
   const int Mp = ((M + 63) / 64) * 64;
@@ -623,17 +703,23 @@ bool launch_attn_prefill_prep(float* q, const float* k, const float* v, int M, i
   const dim3 grid(Mp / 64, (head_dim + 63) / 64, n_kv + n_heads);
   if (kv_f32)
     hipLaunchKernelGGL(attn_prep_kernel<float>, grid, dim3(256), 0, st, q, k, v, M, n_heads, n_kv, head_dim, Mp, cs,
-                       npairs, (float*)kc, (float*)vc, ctx, pos0, kh, kl, vh, vl);
+                       npairs, (float*)kc, (float*)vc, ctx, pos0, kh, kl, vh, vl, ovf);
   else
     hipLaunchKernelGGL(attn_prep_kernel<__half>, grid, dim3(256), 0, st, q, k, v, M, n_heads, n_kv, head_dim, Mp, cs,
-                       npairs, (__half*)kc, (__half*)vc, ctx, pos0, kh, kl, vh, vl);
+                       npairs, (__half*)kc, (__half*)vc, ctx, pos0, kh, kl, vh, vl, ovf);
   return true;
 }
 
 void launch_attn_prefill(const float* q, const float* k, const float* v, float* out, int M, int n_heads, int n_kv,
                          int head_dim, int window, float scale, hipStream_t st, void* scratch, size_t scratch_halves,
-                         bool planes_ready) {
+                         bool planes_ready, int* ovf) {
   const int G = n_heads / n_kv;
+  if (!planes_ready && ovf) {
+    // the kernels below split q, k and v into fp16 pairs themselves (or through kv_split_kernel)
+    launch_range_flag(q, (size_t)M * n_heads * head_dim, ovf, st);
+    launch_range_flag(k, (size_t)M * n_kv * head_dim, ovf, st);
+    launch_range_flag(v, (size_t)M * n_kv * head_dim, ovf, st);
+  }
   if (attn_planes_ok(M, n_heads, n_kv, head_dim, scratch, scratch_halves) && G >= 1) {
     const int Mp = ((M + 63) / 64) * 64;
     const size_t plane = (size_t)n_kv * head_dim * Mp;

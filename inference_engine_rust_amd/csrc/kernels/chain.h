@@ -63,7 +63,8 @@ struct ChainArgs {
   const int* pos;
   const uint32_t* tok;   // token of CX_EMBED_Q4K
   unsigned* counters;    // CHAIN_COUNTER_WORDS, zero at launch; zero again when the launch ends
-  int* err;              // set when a bounded wait runs out (the launch then ends early)
+  int* err;              // [0]: set when a bounded wait runs out (the launch then ends early);
+                         // [1]: the bounded waits' iteration limit (0: the default, ~0.1-0.2 s)
   int* pos_inc;          // when set, the last workgroup adds 1 at the end
   // CE_ARGMAX and its finish (as launch_argmax_finish)
   unsigned long long* amax_key;

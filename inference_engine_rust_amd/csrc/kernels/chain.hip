@@ -13,8 +13,9 @@
 //    LDS slots with global_load_lds_dwordx4 (no registers, no waits until the bytes are needed),
 //    DSLOT items ahead, across phase boundaries, and touches the lines of the item DSLOT further
 //    ahead so that its copy finds them in L2. Its only vector-memory operations are these copies,
-//    so `s_waitcnt vmcnt` counts them exactly: every item is five copy instructions (padded), and
-//    the wait before computing an item is a constant. The copies gather each lane's bytes into
+//    so `s_waitcnt vmcnt` counts them exactly: every item is COPIES_PER_ITEM (four) copy
+//    instructions, padded (five with the L2 touch), and the wait before computing an item is a
+//    constant. The copies gather each lane's bytes into
 //    lane-contiguous 16-byte columns, so the LDS reads are conflict-free.
 //  * The control wave stages the phase input x into LDS (coherent copies: x was written by other
 //    workgroups in this launch), in the register layout the consumers read (lane l's 64 values
@@ -22,8 +23,9 @@
 //    for the consumers' partial dots, runs the epilogue (residual, SwiGLU, RoPE + f32 KV append,
 //    logits + argmax), stores the outputs with coherent stores and arrives at the phase barrier.
 //  * Phase barrier: two-level arrival counters (eight groups of workgroups, then one counter),
-//    agent-scope relaxed atomics; every wait is bounded and a timeout sets `err` and ends the
-//    launch. The last workgroup to leave resets the counters.
+//    agent-scope relaxed atomics; every wait is bounded (err[1] iterations, read at launch, so that
+//    a test can shorten it) and a timeout sets err[0] and ends the launch. The last workgroup to
+//    leave resets the counters.
 //
 // Arithmetic per row (f32 activations throughout, as the reference's f32 dot, src/ops/
 // matmul.rs:176-204, reassociated): Q4_K sub-block sums d*sc*sum(x*q) - dmin*m*sum(x) with the
@@ -45,7 +47,9 @@ constexpr int NT = 64 * (1 + NC);     // threads per workgroup
 constexpr int SLOT = 3584;            // bytes per slot: 3 x 1 KB columns + 16 + 2 columns of 16 B
 constexpr int XF4 = 4 * 16 * 64;      // x staging: up to 4 passes x 16 float4 columns x 64 lanes
 constexpr int MAXPART = 512;          // partial dots per workgroup and phase
-constexpr unsigned SPIN = 1u << 22;   // bounded waits (each iteration sleeps ~64 clocks)
+// copy instructions per item (issue_item), plus the L2 touch when L2PF: the consumers' vmcnt waits
+constexpr int COPIES_PER_ITEM = 4;
+constexpr int VM_PER_ITEM = COPIES_PER_ITEM + (L2PF ? 1 : 0);
 
 typedef const __attribute__((address_space(4))) ChainPhase* CPhase;
 
@@ -132,8 +136,8 @@ IEK_DEV const uint8_t* view_row(const PhaseView& v, int i, int& pass) {
   return reinterpret_cast<const uint8_t*>(b0 + in1 * (b1 - b0) + in2 * (b2 - b1) + (size_t)row * v.rb);
 }
 
-// Four copy instructions per item (the wait counts rely on it): three 1 KB columns of quants and
-// one column of scales.
+// COPIES_PER_ITEM (four) copy instructions per item, on every path (the wait counts rely on it):
+// three 1 KB columns of quants and one column of scales.
 IEK_DEV void issue_item(int dt, int K, const uint8_t* row, int pass, uint32_t slot, int lane) {
   const int nchunk = K / 64, ch = min(lane + 64 * pass, nchunk - 1);
   if (dt == DT_Q4K) {
@@ -261,6 +265,7 @@ struct Smem {
   uint32_t sink[NC][64];  // landing words of the L2 prefetch copies (never read)
   float rms;
   int rows_done, x_ready, norm_done, abort_;
+  unsigned spin;  // bounded-wait limit of this launch (err[1], or 1 << 22 when it is zero)
 };
 
 IEK_DEV void set_abort(Smem& S, int* err, int code) {
@@ -307,7 +312,7 @@ IEK_DEV void control(const ChainArgs& a, Smem& S, int pos) {
       unsigned it = 0;
       while (g_ld(top) < 8u) {
         __builtin_amdgcn_s_sleep(1);
-        if (++it > SPIN) {
+        if (++it > S.spin) {
           set_abort(S, a.err, 1);
           break;
         }
@@ -369,7 +374,7 @@ IEK_DEV void control(const ChainArgs& a, Smem& S, int pos) {
     unsigned it = 0;
     while (lds_ld(&S.rows_done) < seq_end) {
       __builtin_amdgcn_s_sleep(1);
-      if (++it > SPIN || lds_ld(&S.abort_)) {
+      if (++it > S.spin || lds_ld(&S.abort_)) {
         set_abort(S, a.err, 2);
         break;
       }
@@ -380,7 +385,7 @@ IEK_DEV void control(const ChainArgs& a, Smem& S, int pos) {
       it = 0;
       while (lds_ld(&S.norm_done) < NC * nnorm) {
         __builtin_amdgcn_s_sleep(1);
-        if (++it > SPIN || lds_ld(&S.abort_)) {
+        if (++it > S.spin || lds_ld(&S.abort_)) {
           set_abort(S, a.err, 5);
           break;
         }
@@ -547,12 +552,15 @@ IEK_DEV void consumer(const ChainArgs& a, Smem& S, int c) {
     unsigned it = 0;
     while (lds_ld(&S.x_ready) < ph) {
       __builtin_amdgcn_s_sleep(1);
-      if (++it > SPIN || lds_ld(&S.abort_)) {
+      if (++it > S.spin || lds_ld(&S.abort_)) {
         set_abort(S, a.err, 3);
         break;
       }
     }
-    if (lds_ld(&S.abort_)) return;
+    if (lds_ld(&S.abort_)) {
+      vm_wait<0>();  // the copies in flight land before the wave ends
+      return;
+    }
     asm volatile("" ::: "memory");
     if (norm) {
       // y = (x * w) / rms with the reference's two roundings (rmsnorm.rs:46-47), computed once in
@@ -569,12 +577,15 @@ IEK_DEV void consumer(const ChainArgs& a, Smem& S, int c) {
       it = 0;
       while (lds_ld(&S.norm_done) < NC * nnorm) {
         __builtin_amdgcn_s_sleep(1);
-        if (++it > SPIN || lds_ld(&S.abort_)) {
+        if (++it > S.spin || lds_ld(&S.abort_)) {
           set_abort(S, a.err, 4);
           break;
         }
       }
-      if (lds_ld(&S.abort_)) return;
+      if (lds_ld(&S.abort_)) {
+        vm_wait<0>();
+        return;
+      }
       asm volatile("" ::: "memory");
     }
     if (!mine) continue;
@@ -602,7 +613,7 @@ IEK_DEV void consumer(const ChainArgs& a, Smem& S, int c) {
     }
     const int ch = lane + 64 * p;
     for (int i = c; i < cv.n_items; i += NC, ++k) {
-      vm_wait<(L2PF ? 5 : 4) * (DSLOT - 1)>();  // this item's copies have landed
+      vm_wait<VM_PER_ITEM * (DSLOT - 1)>();  // this item's copies have landed
       const uint8_t* slot = &S.ring[c * DSLOT + k % DSLOT][0];
       float v = cv.dt == DT_Q4K ? q4_item(slot, lane, min(ch, nchunk - 1), x, xs_a, xs_b)
                                 : q6_item(slot, lane, min(ch, nchunk - 1), p, x, xq);
@@ -630,6 +641,8 @@ __global__ __launch_bounds__(NT) void chain_kernel(ChainArgs args) {
     S.x_ready = -1;
     S.norm_done = 0;
     S.abort_ = 0;
+    const unsigned lim = (unsigned)__hip_atomic_load(a.err + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    S.spin = lim ? lim : (1u << 22);  // ~0.1-0.2 s: each iteration sleeps ~64 clocks
   }
   __syncthreads();
   typedef const __attribute__((address_space(4))) int* CInt;

@@ -17,6 +17,9 @@ constexpr int Q4K_BYTES = 144;
 constexpr int Q6K_BYTES = 210;
 constexpr int Q8_0_ELEMS = 32;
 constexpr int Q8_0_BYTES = 34;
+// Largest magnitude an fp16 (hi, lo) pair of an f32 holds (the largest finite fp16): prefill GEMM
+// and attention inputs beyond it are flagged and the prefill runs on f32 activations instead.
+constexpr float F16_PAIR_MAX = 65504.f;
 
 // IEEE half bits -> f32. Exact for every non-NaN input (subnormals included), which is what the
 // reference's hand-rolled f16_to_f32 computes (src/ops/quant/utils.rs:2-32).

@@ -57,50 +57,55 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(int dt, const uint8_t* _
     }
 }
 
+void launch_gemm_f32(int dt, const void* w, const float* a, int M, int K, int N, float* out, const float* resid,
+                     hipStream_t st) {
+  dim3 grid((N + GBN - 1) / GBN, (M + GBM - 1) / GBM);
+  hipLaunchKernelGGL(gemm_simt_kernel, grid, dim3(256), 0, st, dt, (const uint8_t*)w, a, M, K, N, out, resid);
+}
+
+// Op-level matmul (M > 1). On the matrix cores the activation enters as an fp16 (hi, lo) pair;
+// each row is first scaled by a power of two that keeps its values and per-32 sums inside the
+// pair's range (launch_split_scaled), and the output row is scaled back afterwards, so any finite
+// f32 activation is taken.
 void launch_gemm(int dt, const void* w, const float* a, int M, int K, int N, float* out, const float* resid,
                  hipStream_t st) {
-  if (gemm_q_ok(dt, w, K) && (reinterpret_cast<uintptr_t>(a) & 15) == 0) {
-    // scale-factored K-quant GEMM: stream-ordered scratch for the fp16 pair and the per-32 sums;
-    // Q6_K is first regrouped (the layout the model path keeps beside the native tensor), which
-    // the wave-tiled matrix-core kernel reads
-    const size_t n = (size_t)M * K;
-    const bool q6r = dt == DT_Q6K && K % QK_K == 0;
-    const size_t wr = q6r ? (size_t)N * q6r_row_bytes((size_t)K / QK_K) : 0;
-    const size_t xbytes = (n * 2 * sizeof(__half) + (n / 32 + 64) * sizeof(float) + 255) / 256 * 256;
-    const size_t pbytes = ((size_t)M * N * sizeof(float) + 255) / 256 * 256;  // split-K partial
-    void* buf = nullptr;
-    check_hip(hipMallocAsync(&buf, xbytes + pbytes + wr, st), "hipMallocAsync");
-    __half* xh = static_cast<__half*>(buf);
-    float* xs = reinterpret_cast<float*>(xh + 2 * n);
-    launch_split_f16(a, n, xh, xh + n, st);
-    launch_block_sums(a, M, K, xs, st);
+  const bool kq = gemm_q_ok(dt, w, K) && (reinterpret_cast<uintptr_t>(a) & 15) == 0;
+  const bool mf = !kq && gemm_mfma_ok(dt, w, K, N) && (reinterpret_cast<uintptr_t>(a) & 15) == 0 && K % 32 == 0;
+  if (resid || !(kq || mf)) {
+    launch_gemm_f32(dt, w, a, M, K, N, out, resid, st);
+    return;
+  }
+  // stream-ordered scratch: the fp16 pair, the per-32 sums, the row factors, a split-K partial and
+  // (Q6_K) the regrouped weights
+  const size_t n = (size_t)M * K;
+  const bool q6r = kq && dt == DT_Q6K && K % QK_K == 0;
+  const size_t wr = q6r ? (size_t)N * q6r_row_bytes((size_t)K / QK_K) : 0;
+  const size_t xbytes = (n * 2 * sizeof(__half) + (n / 32 + 64) * sizeof(float) + 255) / 256 * 256;
+  const size_t ibytes = ((size_t)M * sizeof(float) + 255) / 256 * 256;
+  const size_t pbytes = kq ? ((size_t)M * N * sizeof(float) + 255) / 256 * 256 : 0;  // split-K partial
+  void* buf = nullptr;
+  check_hip(hipMallocAsync(&buf, xbytes + ibytes + pbytes + wr, st), "hipMallocAsync");
+  char* base = static_cast<char*>(buf);
+  __half* xh = reinterpret_cast<__half*>(base);
+  float* xs = reinterpret_cast<float*>(xh + 2 * n);
+  float* inv = reinterpret_cast<float*>(base + xbytes);
+  launch_split_scaled(a, M, K, xh, xh + n, xs, inv, st);
+  if (kq) {
     const void* wq = w;
     int wdt = dt;
     if (q6r) {
-      void* r = static_cast<char*>(buf) + xbytes + pbytes;
+      void* r = base + xbytes + ibytes + pbytes;
       launch_repack_q6k(w, K, N, r, st);
       wq = r;
       wdt = DT_Q6K_R;
     }
     GemmQSeg seg{wq, out, N};
-    launch_gemm_q(wdt, &seg, 1, xh, xh + n, xs, M, K, resid, st,
-                  reinterpret_cast<float*>(static_cast<char*>(buf) + xbytes));
-    check_hip(hipFreeAsync(buf, st), "hipFreeAsync");
-    return;
+    launch_gemm_q(wdt, &seg, 1, xh, xh + n, xs, M, K, nullptr, st, reinterpret_cast<float*>(base + xbytes + ibytes));
+  } else {
+    launch_gemm_mfma(dt, w, xh, xh + n, M, K, N, out, nullptr, st);
   }
-  if (gemm_mfma_ok(dt, w, K, N) && (reinterpret_cast<uintptr_t>(a) & 15) == 0) {
-    // stream-ordered scratch for the fp16 activation pair
-    const size_t n = (size_t)M * K;
-    void* buf = nullptr;
-    check_hip(hipMallocAsync(&buf, n * 2 * sizeof(__half), st), "hipMallocAsync");
-    __half* xh = static_cast<__half*>(buf);
-    launch_split_f16(a, n, xh, xh + n, st);
-    launch_gemm_mfma(dt, w, xh, xh + n, M, K, N, out, resid, st);
-    check_hip(hipFreeAsync(buf, st), "hipFreeAsync");
-    return;
-  }
-  dim3 grid((N + GBN - 1) / GBN, (M + GBM - 1) / GBM);
-  hipLaunchKernelGGL(gemm_simt_kernel, grid, dim3(256), 0, st, dt, (const uint8_t*)w, a, M, K, N, out, resid);
+  launch_row_scale(out, M, N, inv, st);
+  check_hip(hipFreeAsync(buf, st), "hipFreeAsync");
 }
 
 }  // namespace iek

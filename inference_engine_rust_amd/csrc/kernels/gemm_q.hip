@@ -47,6 +47,7 @@ struct GemmQArgs {
   // per-32 sums (glu_sums, optional) and the f32 act (glu_out, optional)
   _Float16 *glu_h, *glu_l, *glu_sums;
   float* glu_out;
+  int* ovf;  // GLU: set when an act value or per-32 sum is beyond the fp16 pair's range
 };
 
 namespace {
@@ -532,6 +533,7 @@ IEK_DEV void glu_epilogue(const GemmQArgs& g, const AccT& acc, const float (&Dc)
   const int lr = lane & 15, lg = lane >> 4;
   const int M = g.M, N = g.n[0];
   const size_t nb = (size_t)N / 32;
+  bool big = false;
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -558,6 +560,7 @@ IEK_DEV void glu_epilogue(const GemmQArgs& g, const AccT& acc, const float (&Dc)
           g.glu_h[o] = h;
           g.glu_l[o] = (_Float16)(v - (float)h);
           if (g.glu_out) g.glu_out[o] = v;
+          big |= fabsf(v) > F16_PAIR_MAX;
         }
         vv[j] = v;
       }
@@ -581,9 +584,11 @@ IEK_DEV void glu_epilogue(const GemmQArgs& g, const AccT& acc, const float (&Dc)
           const _Float16 h = (_Float16)sum;
           g.glu_sums[o] = h;
           g.glu_sums[(size_t)M * nb + o] = (_Float16)(sum - (float)h);
+          big |= fabsf(sum) > F16_PAIR_MAX;
         }
       }
     }
+  if (big && g.ovf) *g.ovf = 1;
 }
 
 // TM: 16-row MFMA tiles per wave along M (a wave owns 16 TM x 64); WGM x WGN waves.
@@ -974,7 +979,7 @@ static void gemm_q_dt(GemmQArgs g, hipStream_t st) {
 
 bool launch_gemm_q_glu(int dt, const void* w_gate, const void* w_up, int N, const __half* xh, const __half* xl,
                        const float* xs, int M, int K, __half* act_hi, __half* act_lo, float* act_sums, float* act_f32,
-                       hipStream_t st) {
+                       int* ovf, hipStream_t st) {
   if (dt != DT_Q4K && dt != DT_Q6K_R) return false;
   if (M < 1 || N < 32 || N % 32 != 0 || !gemm_q_ok(dt, w_gate, K) || !gemm_q_ok(dt, w_up, K)) return false;
   if (dt == DT_Q4K && !xs) fail(ST_OP, "gemm_q: Q4_K needs the per-32 activation sums");
@@ -994,6 +999,7 @@ bool launch_gemm_q_glu(int dt, const void* w_gate, const void* w_up, int N, cons
   g.glu_l = reinterpret_cast<_Float16*>(act_lo);
   g.glu_sums = reinterpret_cast<_Float16*>(act_sums);
   g.glu_out = act_f32;
+  g.ovf = ovf;
   if (dt == DT_Q4K) gemm_kq<Q4KB, true>(g, st, false);
   else gemm_kq<Q6RB, true>(g, st, false);
   return true;

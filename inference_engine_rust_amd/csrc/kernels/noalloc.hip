@@ -15,14 +15,21 @@ std::mutex g_mu;
 void* g_ptr[kMaxDevices] = {};
 }  // namespace
 
-void* noalloc_scratch() {
-  int dev = 0;
-  IEK_HIP(hipGetDevice(&dev));
+// The scratch of the device the work runs on: the stream's device (the current device for the
+// null stream). The first call on a device resolves the array's address with that device current.
+void* noalloc_scratch(hipStream_t st) {
+  int cur = 0, dev = 0;
+  IEK_HIP(hipGetDevice(&cur));
+  dev = cur;
+  if (st) IEK_HIP(hipStreamGetDevice(st, &dev));
   if (dev < 0 || dev >= kMaxDevices) fail(ST_DEVICE, "device index out of range");
   std::lock_guard<std::mutex> lock(g_mu);
   if (!g_ptr[dev]) {
+    if (dev != cur) IEK_HIP(hipSetDevice(dev));
     void* p = nullptr;
-    IEK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) IEK_HIP(hipSetDevice(cur));
+    IEK_HIP(e);
     if (!p) fail(ST_DEVICE, "hipGetSymbolAddress returned a null scratch address");
     g_ptr[dev] = p;
   }

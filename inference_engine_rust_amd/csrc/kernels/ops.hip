@@ -84,14 +84,18 @@ void launch_rmsnorm(const float* in, const float* w, int rows, int dim, float ep
 // stand-alone per-32 sum pass uses (eight float4 partials (x + y) + (z + w), left to right) and
 // stored as an fp16 pair. The four consecutive lanes of one block exchange their partials by
 // shuffles, so every lane of the wave calls this (`live` masks the stores).
+// A value or per-32 sum beyond fp16's range (|x| > 65504: its pair would not hold it) sets *ovf;
+// the prefill then runs again on f32 activations (Session::prefill).
 IEK_DEV void emit_split8(const float (&v)[8], size_t i, bool live, uint4* __restrict__ hi, uint4* __restrict__ lo,
-                         _Float16* __restrict__ sh, _Float16* __restrict__ sl) {
+                         _Float16* __restrict__ sh, _Float16* __restrict__ sl, int* __restrict__ ovf) {
 #pragma clang fp contract(off)
   _Float16 h[8], l[8];
+  bool big = false;
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     h[k] = (_Float16)v[k];
     l[k] = (_Float16)(v[k] - (float)h[k]);
+    big |= fabsf(v[k]) > F16_PAIR_MAX;
   }
   auto pk = [](_Float16 a, _Float16 b) {
     return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
@@ -115,7 +119,9 @@ IEK_DEV void emit_split8(const float (&v)[8], size_t i, bool live, uint4* __rest
     const _Float16 s16 = (_Float16)sum;
     sh[i / 4] = s16;
     sl[i / 4] = (_Float16)(sum - (float)s16);
+    big |= fabsf(sum) > F16_PAIR_MAX;
   }
+  if (live && big && ovf) *ovf = 1;
 }
 
 // rmsnorm (as rmsnorm_kernel) that also emits the GEMM input planes of its output (the f32 output
@@ -126,7 +132,7 @@ IEK_DEV void emit_split8(const float (&v)[8], size_t i, bool live, uint4* __rest
 template <int CPT>
 __global__ __launch_bounds__(256) void rmsnorm_split_kernel(float* in, const float* w, int dim, float eps,
                                                             float* out, uint4* hi, uint4* lo, _Float16* sh,
-                                                            _Float16* sl, const float* part) {
+                                                            _Float16* sl, const float* part, int* ovf) {
 #pragma clang fp contract(off)
   __shared__ float red[8];
   float* x = in + (size_t)blockIdx.x * dim;
@@ -184,12 +190,12 @@ __global__ __launch_bounds__(256) void rmsnorm_split_kernel(float* in, const flo
       reinterpret_cast<float4*>(y)[2 * c + 1] = make_float4(v[4], v[5], v[6], v[7]);
     }
     // emit_split8 exchanges across the group of four lanes: every lane joins
-    emit_split8(v, (size_t)blockIdx.x * n8 + c, live, hi, lo, sh, sl);
+    emit_split8(v, (size_t)blockIdx.x * n8 + c, live, hi, lo, sh, sl, ovf);
   }
 }
 
 void launch_rmsnorm_split(float* in, const float* w, int rows, int dim, float eps, float* out, __half* hi,
-                          __half* lo, float* sums, hipStream_t st, const float* part) {
+                          __half* lo, float* sums, int* ovf, hipStream_t st, const float* part) {
   if (rows <= 0) return;
   if (dim % 32 != 0 || (reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out) |
                         reinterpret_cast<uintptr_t>(part)) % 16)
@@ -199,7 +205,7 @@ void launch_rmsnorm_split(float* in, const float* w, int rows, int dim, float ep
   const int cpt = (dim / 8 + 255) / 256;  // chunks of eight per thread
 #define IEK_RS(C)                                                                                                   \
   hipLaunchKernelGGL(rmsnorm_split_kernel<C>, dim3(rows), dim3(256), 0, st, in, w, dim, eps, out, (uint4*)hi,      \
-                     (uint4*)lo, s, s + nb, part)
+                     (uint4*)lo, s, s + nb, part, ovf)
   if (cpt <= 1) IEK_RS(1);
   else if (cpt <= 2) IEK_RS(2);
   else if (cpt <= 4) IEK_RS(4);
@@ -210,24 +216,120 @@ void launch_rmsnorm_split(float* in, const float* w, int rows, int dim, float ep
 
 // fp16 pair planes and per-32 sums of an existing [rows, K] input in one pass.
 __global__ __launch_bounds__(256) void split_sums_kernel(const float* __restrict__ a, size_t n8, uint4* hi, uint4* lo,
-                                                         _Float16* sh, _Float16* sl) {
+                                                         _Float16* sh, _Float16* sl, int* ovf) {
   for (size_t i0 = (size_t)blockIdx.x * 256; i0 < n8; i0 += (size_t)gridDim.x * 256) {
     const size_t i = i0 + threadIdx.x;
     const bool live = i < n8;
     const size_t c = live ? i : 0;
     const float4 xa = reinterpret_cast<const float4*>(a)[2 * c], xb = reinterpret_cast<const float4*>(a)[2 * c + 1];
     const float v[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-    emit_split8(v, c, live, hi, lo, sh, sl);
+    emit_split8(v, c, live, hi, lo, sh, sl, ovf);
   }
 }
 
-void launch_split_sums(const float* a, int rows, int K, __half* hi, __half* lo, float* sums, hipStream_t st) {
+void launch_split_sums(const float* a, int rows, int K, __half* hi, __half* lo, float* sums, int* ovf,
+                       hipStream_t st) {
   if (rows <= 0) return;
   if (K % 32 != 0 || reinterpret_cast<uintptr_t>(a) % 16) fail(ST_OP, "split_sums: K % 32 and 16-byte aligned input");
   const size_t n8 = (size_t)rows * (K / 8), nb = n8 / 4;
   _Float16* s = reinterpret_cast<_Float16*>(sums);
   const int blocks = (int)std::min<size_t>((n8 + 255) / 256, 4096);
-  hipLaunchKernelGGL(split_sums_kernel, dim3(blocks), dim3(256), 0, st, a, n8, (uint4*)hi, (uint4*)lo, s, s + nb);
+  hipLaunchKernelGGL(split_sums_kernel, dim3(blocks), dim3(256), 0, st, a, n8, (uint4*)hi, (uint4*)lo, s, s + nb, ovf);
+}
+
+// *ovf = 1 when some |a[i]| exceeds the fp16 pair's range (NaN does not count: it stays NaN on
+// either path).
+__global__ __launch_bounds__(256) void range_flag_kernel(const float* __restrict__ a, size_t n, int* ovf) {
+  bool big = false;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+    big |= fabsf(a[i]) > F16_PAIR_MAX;
+  if (big) *ovf = 1;
+}
+
+void launch_range_flag(const float* a, size_t n, int* ovf, hipStream_t st) {
+  if (n == 0 || !ovf) return;
+  const int blocks = (int)std::min<size_t>((n + 255) / 256, 2048);
+  hipLaunchKernelGGL(range_flag_kernel, dim3(blocks), dim3(256), 0, st, a, n, ovf);
+}
+
+// Per-row scaled GEMM input (op level): one workgroup per row. Pass 1 finds the row's largest
+// |value| and |per-32 sum| (sums in the order of block_sums_kernel: (x + y) + (z + w) per float4,
+// left to right); the factor s = 2^e (e <= 0) brings that maximum below 2^15 when it is not
+// already; pass 2 writes the fp16 (hi, lo) planes of s * a and s * sum (exact: a power of two).
+__global__ __launch_bounds__(256) void split_scaled_kernel(const float* __restrict__ a, int K, _Float16* __restrict__ hi,
+                                                           _Float16* __restrict__ lo, _Float16* __restrict__ sh,
+                                                           _Float16* __restrict__ sl, size_t nb_total,
+                                                           float* __restrict__ inv) {
+#pragma clang fp contract(off)
+  __shared__ float red[8];
+  const int r = blockIdx.x, nb = K / 32;
+  const float* x = a + (size_t)r * K;
+  auto bsum = [&](int b) {
+    const float4* p = reinterpret_cast<const float4*>(x + 32 * b);
+    float s = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const float4 v = p[t];
+      s += (v.x + v.y) + (v.z + v.w);
+    }
+    return s;
+  };
+  float m = 0.f;
+  for (int b = threadIdx.x; b < nb; b += 256) {
+    const float4* p = reinterpret_cast<const float4*>(x + 32 * b);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const float4 v = p[t];
+      m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    m = fmaxf(m, fabsf(bsum(b)));
+  }
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  // s = 2^(14 - floor(log2 m)) when m >= 2^15 (finite), else 1
+  float scale = 1.f;
+  if (m >= 32768.f && m <= 3.4028235e38f) {
+    const int e = (int)((__float_as_uint(m) >> 23) & 0xFF) - 127;  // floor(log2 m) for a normal m
+    scale = __uint_as_float((uint32_t)(127 + 14 - e) << 23);
+  }
+  if (threadIdx.x == 0) inv[r] = 1.f / scale;
+  for (int i = threadIdx.x; i < K; i += 256) {
+    const float v = x[i] * scale;
+    const _Float16 h = (_Float16)v;
+    hi[(size_t)r * K + i] = h;
+    lo[(size_t)r * K + i] = (_Float16)(v - (float)h);
+  }
+  for (int b = threadIdx.x; b < nb; b += 256) {
+    const float v = bsum(b) * scale;
+    const _Float16 h = (_Float16)v;
+    sh[(size_t)r * nb + b] = h;
+    sl[(size_t)r * nb + b] = (_Float16)(v - (float)h);
+  }
+  (void)nb_total;
+}
+
+void launch_split_scaled(const float* a, int rows, int K, __half* hi, __half* lo, float* sums, float* inv,
+                         hipStream_t st) {
+  if (rows <= 0) return;
+  if (K % 32 != 0 || reinterpret_cast<uintptr_t>(a) % 16) fail(ST_OP, "split_scaled: K % 32 and 16-byte aligned rows");
+  const size_t nb = (size_t)rows * (K / 32);
+  _Float16* s = reinterpret_cast<_Float16*>(sums);
+  hipLaunchKernelGGL(split_scaled_kernel, dim3(rows), dim3(256), 0, st, a, K, reinterpret_cast<_Float16*>(hi),
+                     reinterpret_cast<_Float16*>(lo), s, s + nb, nb, inv);
+}
+
+__global__ void row_scale_kernel(float* __restrict__ out, int N, const float* __restrict__ inv) {
+  const float f = inv[blockIdx.y];
+  if (f == 1.f) return;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < N; i += gridDim.x * 256) out[(size_t)blockIdx.y * N + i] *= f;
+}
+
+void launch_row_scale(float* out, int rows, int N, const float* inv, hipStream_t st) {
+  if (rows <= 0 || N <= 0) return;
+  hipLaunchKernelGGL(row_scale_kernel, dim3((unsigned)std::min((N + 255) / 256, 64), rows), dim3(256), 0, st, out, N,
+                     inv);
 }
 
 // RoPE on adjacent pairs (src/ops/rope.rs:11-59). `cs` holds (cos, sin) per (position, pair),
@@ -336,7 +438,7 @@ void launch_swiglu(const float* g, const float* u, float* out, size_t n, hipStre
 // output itself only when `out` is set).
 __global__ __launch_bounds__(256) void swiglu_split_kernel(const float* __restrict__ g, const float* __restrict__ u,
                                                            float* __restrict__ out, size_t n8, uint4* hi, uint4* lo,
-                                                           _Float16* sh, _Float16* sl) {
+                                                           _Float16* sh, _Float16* sl, int* ovf) {
 #pragma clang fp contract(off)
   for (size_t i0 = (size_t)blockIdx.x * 256; i0 < n8; i0 += (size_t)gridDim.x * 256) {
     const size_t i = i0 + threadIdx.x;
@@ -364,12 +466,12 @@ __global__ __launch_bounds__(256) void swiglu_split_kernel(const float* __restri
       reinterpret_cast<float4*>(out)[2 * c] = make_float4(v[0], v[1], v[2], v[3]);
       reinterpret_cast<float4*>(out)[2 * c + 1] = make_float4(v[4], v[5], v[6], v[7]);
     }
-    emit_split8(v, c, live, hi, lo, sh, sl);
+    emit_split8(v, c, live, hi, lo, sh, sl, ovf);
   }
 }
 
 void launch_swiglu_split(const float* g, const float* u, float* out, int rows, int K, __half* hi, __half* lo,
-                         float* sums, hipStream_t st) {
+                         float* sums, int* ovf, hipStream_t st) {
   if (rows <= 0) return;
   if (K % 32 != 0 || (reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(u) | reinterpret_cast<uintptr_t>(out)) % 16)
     fail(ST_OP, "swiglu_split: K % 32 and 16-byte aligned inputs");
@@ -377,7 +479,7 @@ void launch_swiglu_split(const float* g, const float* u, float* out, int rows, i
   _Float16* s = reinterpret_cast<_Float16*>(sums);
   const int blocks = (int)std::min<size_t>((n8 + 255) / 256, 4096);
   hipLaunchKernelGGL(swiglu_split_kernel, dim3(blocks), dim3(256), 0, st, g, u, out, n8, (uint4*)hi, (uint4*)lo, s,
-                     s + nb);
+                     s + nb, ovf);
 }
 
 // gelu_tanh(g) * u (src/layers/ffn.rs:49-53); gelu_tanh_dev is in common.cuh.

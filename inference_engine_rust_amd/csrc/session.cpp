@@ -9,6 +9,7 @@
 #include "session.h"
 
 #include <functional>
+#include <mutex>
 
 #include "kernels/chain.h"
 #include "kernels/mv_args.h"
@@ -30,6 +31,38 @@ T* dev_alloc(size_t n) {
 void dev_free(void* p) {
   if (p) (void)hipFree(p);
 }
+
+// A chain launch waits on its own workgroups across the whole GPU, so it needs every compute unit
+// to itself: two sessions' chain steps overlapping on one device would each get part of the CUs,
+// and their bounded waits would run out. Sessions on one device therefore take turns: a step's
+// work waits on its stream for the previous chain step of any session on the device (an event per
+// device), and records that event when its own work is enqueued. Work from another process on the
+// same GPU is not ordered by this; a chain step it starves fails with IEK_ERR_DEVICE.
+struct ChainOrder {
+  std::mutex mu;
+  hipEvent_t last = nullptr;
+};
+ChainOrder g_chain_order[64];
+
+class ChainTurn {
+ public:
+  ChainTurn(int dev, hipStream_t st, bool on) : st_(st) {
+    if (!on) return;
+    if (dev < 0 || dev >= 64) fail(ST_DEVICE, "device index out of range");
+    o_ = &g_chain_order[dev];
+    lock_ = std::unique_lock<std::mutex>(o_->mu);
+    if (!o_->last) IEK_HIP(hipEventCreateWithFlags(&o_->last, hipEventDisableTiming));
+    else IEK_HIP(hipStreamWaitEvent(st, o_->last, 0));
+  }
+  ~ChainTurn() {
+    if (o_) (void)hipEventRecord(o_->last, st_);
+  }
+
+ private:
+  ChainOrder* o_ = nullptr;
+  std::unique_lock<std::mutex> lock_;
+  hipStream_t st_;
+};
 
 }  // namespace
 
@@ -101,6 +134,8 @@ Session::Session(Model* m) : m_(m) {
   d_key_ = dev_alloc<unsigned long long>(1);
   d_flag_ = dev_alloc<int>(1);
   d_cnt_ = dev_alloc<int>(2 * c.n_kv_heads);  // per (KV head, query-head group) arrival counters
+  d_ovf_ = dev_alloc<int>(1);
+  IEK_HIP(hipHostMalloc(reinterpret_cast<void**>(&h_ovf_), sizeof(int), hipHostMallocDefault));
   if (gemma_ && c.ple_dim > 0) {
     const size_t pack = (size_t)c.n_layers * c.ple_dim;
     ple_tokd_ = dev_alloc<float>(pack);
@@ -110,6 +145,7 @@ Session::Session(Model* m) : m_(m) {
   launch_fill_u64(d_key_, 0ull, 1, st_);
   launch_fill_i32(d_flag_, 0, 1, st_);
   launch_fill_i32(d_cnt_, 0, 2 * c.n_kv_heads, st_);
+  launch_fill_i32(d_ovf_, 0, 1, st_);
   prepare_chain();
   reset();
 }
@@ -125,14 +161,24 @@ Session::~Session() {
                   (void*)d_step_, (void*)d_flags_, (void*)d_tok_, (void*)d_ids_, (void*)d_gen_, (void*)d_key_,
                   (void*)d_flag_, (void*)d_cnt_, (void*)xs_, (void*)xsum_, kv_blob_, (void*)ple_tok_,
                   (void*)ple_proj_, (void*)ple_pack_, (void*)ple_tokd_, (void*)ple_projd_, (void*)ple_packd_,
-                  (void*)xdec2_, (void*)xdec_save_, chain_blob_, (void*)d_chain_cnt_, (void*)d_chain_err_})
+                  (void*)xdec2_, (void*)xdec_save_, chain_blob_, (void*)d_chain_cnt_, (void*)d_chain_err_,
+                  (void*)d_ovf_, (void*)x_save_})
     dev_free(p);
+  if (h_ovf_) (void)hipHostFree(h_ovf_);
   if (st_) (void)hipStreamDestroy(st_);
 }
 
 void Session::sync() {
   IEK_HIP(hipGetLastError());
   IEK_HIP(hipStreamSynchronize(st_));
+}
+
+// Whether a prefill kernel flagged an input beyond the fp16 pair's range since d_ovf_ was cleared
+// (waits for the stream).
+bool Session::overflowed() {
+  IEK_HIP(hipMemcpyAsync(h_ovf_, d_ovf_, sizeof(int), hipMemcpyDeviceToHost, st_));
+  sync();
+  return *h_ovf_ != 0;
 }
 
 void Session::reset() {
@@ -201,13 +247,17 @@ static const void* mv_weight(const DevTensor& t, int K, int* dt) {
 
 // One projection over `rows` activation rows: matvec for a single row, GEMM otherwise. `xs` is
 // the fp16 (hi, lo) split of `a` when the caller has made it (rows*K halves each), else null.
+// `f32`: the prefill's f32 mode (an input beyond the fp16 pair's range was seen): the SIMT GEMM
+// on the f32 activation.
 static void project(const DevTensor& w, const float* a, const __half* xs, int rows, int K, int N, float* out,
-                    const float* resid, hipStream_t st) {
+                    const float* resid, hipStream_t st, bool f32 = false) {
   if (w.dims.size() != 2 || (int)w.dims[0] != K || (int)w.dims[1] != N)
     fail(ST_MATMUL, "inner dim mismatch: weight dims do not match the activation width");
   if (rows == 1) {
     MvSegDesc s{w.dev, out, resid, N};
     launch_matvec(w.dtype, &s, 1, a, K, resid ? 1 : 0, st);
+  } else if (f32) {
+    launch_gemm_f32(w.dtype, w.dev, a, rows, K, N, out, resid, st);
   } else if (xs && gemm_mfma_ok(w.dtype, w.dev, K, N)) {
     launch_gemm_mfma(w.dtype, w.dev, xs, xs + (size_t)rows * K, rows, K, N, out, resid, st);
   } else {
@@ -290,7 +340,7 @@ bool Session::gate_up_glu(int li, int M) {
   const DevTensor* wd[1] = {&L.down};
   __half* ah = reinterpret_cast<__half*>(g_);
   return launch_gemm_q_glu(dg, pg, pu, ffn, xs_, xs_ + (size_t)M * H_, xsum_, M, H_, ah, ah + (size_t)M * ffn, u_,
-                           quant_ready(wd, 1, M, ffn) ? nullptr : act_, st_);
+                           quant_ready(wd, 1, M, ffn) ? nullptr : act_, d_ovf_, st_);
 }
 
 bool Session::layer_prefill(int li, int M, bool pend_in) {
@@ -303,10 +353,12 @@ bool Session::layer_prefill(int li, int M, bool pend_in) {
   // cache's current length, causal attention within the prompt, O projection + residual.
   // fp16 pair (and per-32 sums) of a GEMM input, only when it has more than one row and a width
   // the split takes; the pre-norms and SwiGLU emit them as they write their output
-  const bool wide = M >= 2;
+  // In the f32 mode no input is split: every projection runs the SIMT GEMM on f32 activations.
+  const bool wide = M >= 2 && !f32_prefill_;
+  const bool f32 = f32_prefill_;
   auto split = [&](const float* a, int K) -> const __half* {
     if (!wide || K % 32 != 0) return nullptr;
-    launch_split_sums(a, M, K, xs_, xs_ + (size_t)M * K, xsum_, st_);
+    launch_split_sums(a, M, K, xs_, xs_ + (size_t)M * K, xsum_, d_ovf_, st_);
     return xs_;
   };
   // (the f32 output is written only when a consumer may fall back to it). A split-K partial left
@@ -318,7 +370,7 @@ bool Session::layer_prefill(int li, int M, bool pend_in) {
       return nullptr;
     }
     launch_rmsnorm_split(x_, (const float*)w.dev, M, H_, eps, need_f32 ? xn_ : nullptr, xs_, xs_ + (size_t)M * H_,
-                         xsum_, st_, pend ? tmp_ : nullptr);
+                         xsum_, d_ovf_, st_, pend ? tmp_ : nullptr);
     return xs_;
   };
   const DevTensor* wqkv[3] = {&L.wq, &L.wk, &L.wv};
@@ -330,10 +382,11 @@ bool Session::layer_prefill(int li, int M, bool pend_in) {
     if (!xs || !project_q(ws, outs, 3, M, H_, nullptr)) {
       // Q and K share a launch when only V differs (a Q6_K attn_v in a Q4_K_M file)
       if (!xs || !project_q(ws, outs, 2, M, H_, nullptr)) {
-        project(L.wq, xn_, xs, M, H_, qd, q_, nullptr, st_);
-        project(L.wk, xn_, xs, M, H_, kvd, k_, nullptr, st_);
+        project(L.wq, xn_, xs, M, H_, qd, q_, nullptr, st_, f32);
+        project(L.wk, xn_, xs, M, H_, kvd, k_, nullptr, st_, f32);
       }
-      if (!xs || !project_q(ws + 2, outs + 2, 1, M, H_, nullptr)) project(L.wv, xn_, xs, M, H_, kvd, v_, nullptr, st_);
+      if (!xs || !project_q(ws + 2, outs + 2, 1, M, H_, nullptr))
+        project(L.wv, xn_, xs, M, H_, kvd, v_, nullptr, st_, f32);
     }
   }
   if (c.unpack_qk) {
@@ -346,24 +399,27 @@ bool Session::layer_prefill(int li, int M, bool pend_in) {
   // xs_ (the GEMM input pair, consumed by the Q/K/V projection above) is free until the O
   // projection's split: the shared-K/V attention stages its fp16 K / V planes there. RoPE, the KV
   // append and those planes go in one launch when that path applies.
-  const bool prepped = qd == c.n_heads * hd && kvd == c.n_kv_heads * hd &&
+  const bool prepped = !f32 && qd == c.n_heads * hd && kvd == c.n_kv_heads * hd &&
                        launch_attn_prefill_prep(q_, k_, v_, M, c.n_heads, c.n_kv_heads, hd, rt.dev, S.rotary_dim / 2,
-                                                kc_[li], vc_[li], kv_f32_, ctx_, pos_, xs_, xs_halves(), st_);
+                                                kc_[li], vc_[li], kv_f32_, ctx_, pos_, xs_, xs_halves(), d_ovf_, st_);
   if (!prepped) {
     launch_rope_rows(q_, M, qd, c.n_heads, hd, 0, rt.dev, S.rotary_dim / 2, st_);
     launch_rope_rows(k_, M, kvd, c.n_kv_heads, hd, 0, rt.dev, S.rotary_dim / 2, st_);
     launch_kv_store(k_, v_, M, kvd, kc_[li], vc_[li], kv_f32_, c.n_kv_heads, hd, ctx_, nullptr, pos_, st_);
   }
   const float scale = 1.0f / sqrtf((float)hd);
-  launch_attn_prefill(q_, k_, v_, att_, M, c.n_heads, c.n_kv_heads, hd, S.window, scale, st_, xs_, xs_halves(),
-                      prepped);
+  if (f32)
+    launch_attn_prefill_f32(q_, k_, v_, att_, M, c.n_heads, c.n_kv_heads, hd, S.window, scale, st_);
+  else
+    launch_attn_prefill(q_, k_, v_, att_, M, c.n_heads, c.n_kv_heads, hd, S.window, scale, st_, xs_, xs_halves(),
+                        prepped, d_ovf_);
   bool opend = false;
   {
     const __half* xa = split(att_, qd);
     const DevTensor* ws[1] = {&L.wo};
     float* outs[1] = {x_};
     if (!xa || !project_q(ws, outs, 1, M, qd, x_, kpart_ok_ ? tmp_ : nullptr, &opend))
-      project(L.wo, att_, xa, M, qd, H_, x_, x_, st_);
+      project(L.wo, att_, xa, M, qd, H_, x_, x_, st_, f32);
   }
   // FFN sub-layer: pre-norm, gate/up, SwiGLU, down + residual.
   const DevTensor* wgu[2] = {&L.gate, &L.up};
@@ -382,13 +438,13 @@ bool Session::layer_prefill(int li, int M, bool pend_in) {
     const DevTensor* ws[2] = {&L.gate, &L.up};
     float* outs[2] = {g_, u_};
     if (!xs || !project_q(ws, outs, 2, M, H_, nullptr)) {
-      project(L.gate, xn_, xs, M, H_, S.ffn_dim, g_, nullptr, st_);
-      project(L.up, xn_, xs, M, H_, S.ffn_dim, u_, nullptr, st_);
+      project(L.gate, xn_, xs, M, H_, S.ffn_dim, g_, nullptr, st_, f32);
+      project(L.up, xn_, xs, M, H_, S.ffn_dim, u_, nullptr, st_, f32);
     }
     if (wide && S.ffn_dim % 32 == 0) {
       const DevTensor* wd[1] = {&L.down};
       launch_swiglu_split(g_, u_, quant_ready(wd, 1, M, S.ffn_dim) ? nullptr : act_, M, S.ffn_dim, xs_,
-                          xs_ + (size_t)M * S.ffn_dim, xsum_, st_);
+                          xs_ + (size_t)M * S.ffn_dim, xsum_, d_ovf_, st_);
       xa = xs_;
     } else {
       launch_swiglu(g_, u_, act_, (size_t)M * S.ffn_dim, st_);
@@ -399,7 +455,7 @@ bool Session::layer_prefill(int li, int M, bool pend_in) {
     const DevTensor* ws[1] = {&L.down};
     float* outs[1] = {x_};
     if (!xa || !project_q(ws, outs, 1, M, S.ffn_dim, x_, kpart_ok_ ? tmp_ : nullptr, &dpend, xa, xa_sums))
-      project(L.down, act_, xa, M, S.ffn_dim, H_, x_, x_, st_);
+      project(L.down, act_, xa, M, S.ffn_dim, H_, x_, x_, st_, f32);
   }
   return dpend;
 }
@@ -520,7 +576,8 @@ static size_t embedding_hidden(const DevTensor& t, size_t* vocab) {
 // and widths the chain kernel supports; otherwise decode runs the per-launch kernels.
 void Session::prepare_chain() {
   const Config& c = m_->cfg;
-  if (gemma_ || c.n_layers <= 0 || c.unpack_qk) return;
+  // the Q/K/V epilogue appends f32 K and V rows (an fp16 cache would take another epilogue)
+  if (gemma_ || c.n_layers <= 0 || c.unpack_qk || !kv_f32_) return;
   const int G = num_cus();
   auto wdt = [](const DevTensor& t, int* dt) -> const uint8_t* {
     if (t.dev_r && t.dtype_r == DT_Q6K_R) {
@@ -671,9 +728,9 @@ void Session::prepare_chain() {
     off += v.size();
   }
   d_chain_cnt_ = dev_alloc<unsigned>(CHAIN_COUNTER_WORDS);
-  d_chain_err_ = dev_alloc<int>(1);
+  d_chain_err_ = dev_alloc<int>(2);  // [error code, bounded-wait limit (0: default)]
   launch_fill_i32((int*)d_chain_cnt_, 0, CHAIN_COUNTER_WORDS, st_);
-  launch_fill_i32(d_chain_err_, 0, 1, st_);
+  launch_fill_i32(d_chain_err_, 0, 2, st_);
   chain_ = true;
 }
 
@@ -690,6 +747,12 @@ void Session::check_chain_error() {
     sync();
     fail(ST_DEVICE, "decode chain: a bounded wait ran out (code " + std::to_string(err) + ")");
   }
+}
+
+void Session::set_chain_spin(unsigned spin) {
+  if (!chain_) fail(ST_OP, "set_chain_spin: the session does not decode through the chain");
+  launch_set_int(d_chain_err_ + 1, (int)spin, st_);
+  sync();
 }
 
 void Session::layer_decode_unfused(int li) {
@@ -737,8 +800,8 @@ void Session::layer_decode_unfused(int li) {
 // fp16 (hi, lo) pair and per-32 sums of a GEMM input, when it has more than one row and a width
 // the split takes; null otherwise.
 const __half* Session::split_rows(const float* a, int M, int K) {
-  if (M < 2 || K % 32 != 0) return nullptr;
-  launch_split_sums(a, M, K, xs_, xs_ + (size_t)M * K, xsum_, st_);
+  if (M < 2 || K % 32 != 0 || f32_prefill_) return nullptr;
+  launch_split_sums(a, M, K, xs_, xs_ + (size_t)M * K, xsum_, d_ovf_, st_);
   return xs_;
 }
 
@@ -760,7 +823,7 @@ void Session::embed_ple(const uint32_t* d_ids, int n, const float* x, const __ha
   if (m_->ple_proj_norm.host_f32.size() != (size_t)c.ple_dim)
     fail(ST_MODEL, "per_layer_proj_norm len != ple_dim");
   launch_embed(te.dtype, te.dev, row, d_ids, n, 1.0f, tok, st_);
-  project(m_->ple_model_proj, x, xs, n, H_, packn, proj, nullptr, st_);
+  project(m_->ple_model_proj, x, xs, n, H_, packn, proj, nullptr, st_, f32_prefill_);
   launch_ple_pack(proj, tok, (const float*)m_->ple_proj_norm.dev, n, c.n_layers, c.ple_dim, c.rms_eps,
                   c.ple_proj_scale, sqrtf((float)c.ple_dim), c.ple_combine_scale, pack, st_);
 }
@@ -785,10 +848,10 @@ void Session::layer_prefill_gemma(int li, int M) {
     const DevTensor* ws[3] = {&L.wq, &L.wk, &L.wv};
     float* outs[3] = {q_, k_, v_};
     if (!xs || !project_q(ws, outs, borrow ? 1 : 3, M, H_, nullptr)) {
-      project(L.wq, xn_, xs, M, H_, qd, q_, nullptr, st_);
+      project(L.wq, xn_, xs, M, H_, qd, q_, nullptr, st_, f32_prefill_);
       if (!borrow) {
-        project(L.wk, xn_, xs, M, H_, kvd, k_, nullptr, st_);
-        project(L.wv, xn_, xs, M, H_, kvd, v_, nullptr, st_);
+        project(L.wk, xn_, xs, M, H_, kvd, k_, nullptr, st_, f32_prefill_);
+        project(L.wv, xn_, xs, M, H_, kvd, v_, nullptr, st_, f32_prefill_);
       }
     }
   }
@@ -798,12 +861,17 @@ void Session::layer_prefill_gemma(int li, int M) {
                    L.k_norm.present() ? (const float*)L.k_norm.dev : nullptr, eps, true, rt.dev, S.rotary_dim / 2,
                    nullptr, 0, pos_, borrow ? nullptr : kc_[li], borrow ? nullptr : vc_[li], kv_f32_, ctx_, st_);
   if (borrow) launch_kv_load(kc_[li], vc_[li], kv_f32_, M, c.n_kv_heads, hd, ctx_, k_, v_, st_);
-  launch_attn_prefill(q_, k_, v_, att_, M, c.n_heads, c.n_kv_heads, hd, S.window, 1.0f, st_);
+  if (f32_prefill_)
+    launch_attn_prefill_f32(q_, k_, v_, att_, M, c.n_heads, c.n_kv_heads, hd, S.window, 1.0f, st_);
+  else
+    launch_attn_prefill(q_, k_, v_, att_, M, c.n_heads, c.n_kv_heads, hd, S.window, 1.0f, st_, nullptr, 0, false,
+                        d_ovf_);
   {
     const __half* xa = split_rows(att_, M, qd);
     const DevTensor* ws[1] = {&L.wo};
     float* outs[1] = {tmp_};
-    if (!xa || !project_q(ws, outs, 1, M, qd, nullptr)) project(L.wo, att_, xa, M, qd, H_, tmp_, nullptr, st_);
+    if (!xa || !project_q(ws, outs, 1, M, qd, nullptr))
+      project(L.wo, att_, xa, M, qd, H_, tmp_, nullptr, st_, f32_prefill_);
   }
   launch_rmsnorm_add(x_, tmp_, (const float*)L.attn_post_norm.dev, M, H_, eps, false, 1.f, st_);
   launch_rmsnorm(x_, (const float*)L.ffn_norm.dev, M, H_, eps, xn_, st_);
@@ -812,8 +880,8 @@ void Session::layer_prefill_gemma(int li, int M) {
     const DevTensor* ws[2] = {&L.gate, &L.up};
     float* outs[2] = {g_, u_};
     if (!xs || !project_q(ws, outs, 2, M, H_, nullptr)) {
-      project(L.gate, xn_, xs, M, H_, S.ffn_dim, g_, nullptr, st_);
-      project(L.up, xn_, xs, M, H_, S.ffn_dim, u_, nullptr, st_);
+      project(L.gate, xn_, xs, M, H_, S.ffn_dim, g_, nullptr, st_, f32_prefill_);
+      project(L.up, xn_, xs, M, H_, S.ffn_dim, u_, nullptr, st_, f32_prefill_);
     }
   }
   launch_gelu_mul(g_, u_, act_, (size_t)M * S.ffn_dim, st_);
@@ -822,7 +890,7 @@ void Session::layer_prefill_gemma(int li, int M) {
     const DevTensor* ws[1] = {&L.down};
     float* outs[1] = {tmp_};
     if (!xa || !project_q(ws, outs, 1, M, S.ffn_dim, nullptr))
-      project(L.down, act_, xa, M, S.ffn_dim, H_, tmp_, nullptr, st_);
+      project(L.down, act_, xa, M, S.ffn_dim, H_, tmp_, nullptr, st_, f32_prefill_);
   }
   const bool ple = c.ple_dim > 0;
   launch_rmsnorm_add(x_, tmp_, (const float*)L.ffn_post_norm.dev, M, H_, eps, !ple && L.has_out_scale,
@@ -832,10 +900,10 @@ void Session::layer_prefill_gemma(int li, int M) {
     if (!L.ple_gate.present() || !L.ple_proj.present() || !L.ple_post_norm.present())
       fail(ST_MODEL, "PLE: missing inp_gate / proj / post_norm");
     xs = split_rows(x_, M, H_);
-    project(L.ple_gate, x_, xs, M, H_, pd, g_, nullptr, st_);
+    project(L.ple_gate, x_, xs, M, H_, pd, g_, nullptr, st_, f32_prefill_);
     launch_ple_gate(g_, ple_pack_, M, pd, c.n_layers, li, st_);
     const __half* xg = split_rows(g_, M, pd);
-    project(L.ple_proj, g_, xg, M, pd, H_, tmp_, nullptr, st_);
+    project(L.ple_proj, g_, xg, M, pd, H_, tmp_, nullptr, st_, f32_prefill_);
     launch_rmsnorm_add(x_, tmp_, (const float*)L.ple_post_norm.dev, M, H_, eps, L.has_out_scale, L.out_scale_value,
                        st_);
   }
@@ -987,14 +1055,33 @@ void Session::prefill(const uint32_t* ids, int n) {
   if (pos_ + n > ctx_) fail(ST_KVCACHE, "KVCache is Full: max len is " + std::to_string(ctx_) + ".");
   ensure_rows(n);
   IEK_HIP(hipMemcpyAsync(d_ids_, ids, (size_t)n * 4, hipMemcpyHostToDevice, st_));
-  launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, d_ids_, n, c.embed_scale, x_, st_);
-  if (gemma_) {
-    embed_ple(d_ids_, n, x_, split_rows(x_, n, H_), ple_tok_, ple_proj_, ple_pack_);
-    for (int li = 0; li < c.n_layers; ++li) layer_prefill_gemma(li, n);
-  } else {
-    bool pend = false;  // the down projection's split-K partial goes into the next layer's norm
-    for (int li = 0; li < c.n_layers; ++li) pend = layer_prefill(li, n, pend);
-    if (pend) launch_add_f32(x_, tmp_, (size_t)n * H_, st_);
+  auto body = [&] {
+    launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, d_ids_, n, c.embed_scale, x_, st_);
+    if (gemma_) {
+      embed_ple(d_ids_, n, x_, split_rows(x_, n, H_), ple_tok_, ple_proj_, ple_pack_);
+      for (int li = 0; li < c.n_layers; ++li) layer_prefill_gemma(li, n);
+    } else {
+      bool pend = false;  // the down projection's split-K partial goes into the next layer's norm
+      for (int li = 0; li < c.n_layers; ++li) pend = layer_prefill(li, n, pend);
+      if (pend) launch_add_f32(x_, tmp_, (size_t)n * H_, st_);
+    }
+  };
+  // The matrix-core GEMMs and attention take each activation as an fp16 (hi, lo) pair. A value or
+  // per-32 sum beyond the pair's range, which the reference's f32 arithmetic takes, sets d_ovf_ in
+  // the kernel that splits it; the prefill then runs again in the f32 mode (SIMT GEMMs and
+  // attention on f32 activations). The KV rows it appends are rewritten at the same positions.
+  launch_fill_i32(d_ovf_, 0, 1, st_);
+  body();
+  if (overflowed()) {
+    f32_prefill_ = true;
+    try {
+      body();
+    } catch (...) {
+      f32_prefill_ = false;
+      throw;
+    }
+    f32_prefill_ = false;
+    ++f32_prefills_;
   }
   launch_copy_f32(x_ + (size_t)(n - 1) * H_, xdec_, H_, st_);
   pos_ += n;
@@ -1096,10 +1183,13 @@ double Session::bench_kernel(int which, int reps, double* work) {
   hipEvent_t e0, e1;
   IEK_HIP(hipEventCreate(&e0));
   IEK_HIP(hipEventCreate(&e1));
-  for (int i = 0; i < 3; ++i) launch(i);
-  IEK_HIP(hipEventRecord(e0, st_));
-  for (int i = 0; i < reps; ++i) launch(i);
-  IEK_HIP(hipEventRecord(e1, st_));
+  {
+    ChainTurn turn(m_->device, st_, which == 0);
+    for (int i = 0; i < 3; ++i) launch(i);
+    IEK_HIP(hipEventRecord(e0, st_));
+    for (int i = 0; i < reps; ++i) launch(i);
+    IEK_HIP(hipEventRecord(e1, st_));
+  }
   IEK_HIP(hipEventSynchronize(e1));
   float ms = 0.f;
   IEK_HIP(hipEventElapsedTime(&ms, e0, e1));
@@ -1128,7 +1218,21 @@ void Session::embed(const uint32_t* ids, int n) {
   ensure_rows(n);
   IEK_HIP(hipMemcpyAsync(d_ids_, ids, (size_t)n * 4, hipMemcpyHostToDevice, st_));
   launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, d_ids_, n, c.embed_scale, x_, st_);
-  if (gemma_) embed_ple(d_ids_, n, x_, split_rows(x_, n, H_), ple_tok_, ple_proj_, ple_pack_);
+  if (gemma_) {
+    launch_fill_i32(d_ovf_, 0, 1, st_);
+    embed_ple(d_ids_, n, x_, split_rows(x_, n, H_), ple_tok_, ple_proj_, ple_pack_);
+    if (overflowed()) {  // the per-layer inputs again, on f32 activations
+      f32_prefill_ = true;
+      try {
+        embed_ple(d_ids_, n, x_, split_rows(x_, n, H_), ple_tok_, ple_proj_, ple_pack_);
+      } catch (...) {
+        f32_prefill_ = false;
+        throw;
+      }
+      f32_prefill_ = false;
+      ++f32_prefills_;
+    }
+  }
   launch_copy_f32(x_ + (size_t)(n - 1) * H_, xdec_, H_, st_);  // the last row, read by the LM head
   state_rows_ = n;
   state_prefill_ = true;
@@ -1159,8 +1263,32 @@ void Session::prefill_layer(int li) {
   if (gemma_ && c.ple_dim > 0 && !state_ple_) fail(ST_MODEL, "PLE: per-layer inputs missing from the state");
   const int M = state_rows_;
   if (pos_ + M > ctx_) fail(ST_KVCACHE, "KVCache is Full: max len is " + std::to_string(ctx_) + ".");
-  if (gemma_) layer_prefill_gemma(li, M);
-  else if (layer_prefill(li, M)) launch_add_f32(x_, tmp_, (size_t)M * H_, st_);
+  // the layer's input is kept so that the layer can run again in the f32 mode (as Session::prefill)
+  if (x_save_cap_ < (size_t)M * H_) {
+    sync();
+    dev_free(x_save_);
+    x_save_ = dev_alloc<float>((size_t)M * H_);
+    x_save_cap_ = (size_t)M * H_;
+  }
+  launch_copy_f32(x_, x_save_, (size_t)M * H_, st_);
+  launch_fill_i32(d_ovf_, 0, 1, st_);
+  auto run = [&] {
+    if (gemma_) layer_prefill_gemma(li, M);
+    else if (layer_prefill(li, M)) launch_add_f32(x_, tmp_, (size_t)M * H_, st_);
+  };
+  run();
+  if (overflowed()) {
+    launch_copy_f32(x_save_, x_, (size_t)M * H_, st_);
+    f32_prefill_ = true;
+    try {
+      run();
+    } catch (...) {
+      f32_prefill_ = false;
+      throw;
+    }
+    f32_prefill_ = false;
+    ++f32_prefills_;
+  }
   launch_copy_f32(x_ + (size_t)(M - 1) * H_, xdec_, H_, st_);
   if (++layer_cursor_ == c.n_layers) {
     pos_ += M;
@@ -1274,7 +1402,10 @@ void Session::decode_token(uint32_t id) {
   if (pos_ >= ctx_) fail(ST_KVCACHE, "KVCache is Full: max len is " + std::to_string(ctx_) + ".");
   check_no_layer_forward();
   IEK_HIP(hipMemcpyAsync(d_tok_, &id, 4, hipMemcpyHostToDevice, st_));
-  decode_body();
+  {
+    ChainTurn turn(m_->device, st_, chain_);
+    decode_body();
+  }
   pos_ += 1;
   state_rows_ = 1;
   state_prefill_ = false;
@@ -1374,25 +1505,28 @@ void Session::generate_greedy(int n, uint32_t* out_ids, bool use_graph) {
   launch_copy_f32(xdec_, xdec_save_, H_, st_);  // the state to restore if the first step fails
   // greedy token of the current state (step 0), then n x { decode it; greedy token of the new
   // state (step i + 1) }: the last step's token is computed and not returned
-  argmax_body(true);
-  if (use_graph) {
-    if (!step_exec_) {
-      sync();
-      IEK_HIP(hipStreamBeginCapture(st_, hipStreamCaptureModeThreadLocal));
-      try {
-        step_body();
-      } catch (...) {
-        hipGraph_t g;
-        (void)hipStreamEndCapture(st_, &g);
-        if (g) (void)hipGraphDestroy(g);
-        throw;
+  {
+    ChainTurn turn(m_->device, st_, chain_);  // waits before, records after (outside the capture)
+    argmax_body(true);
+    if (use_graph) {
+      if (!step_exec_) {
+        sync();
+        IEK_HIP(hipStreamBeginCapture(st_, hipStreamCaptureModeThreadLocal));
+        try {
+          step_body();
+        } catch (...) {
+          hipGraph_t g;
+          (void)hipStreamEndCapture(st_, &g);
+          if (g) (void)hipGraphDestroy(g);
+          throw;
+        }
+        IEK_HIP(hipStreamEndCapture(st_, &step_graph_));
+        IEK_HIP(hipGraphInstantiate(&step_exec_, step_graph_, nullptr, nullptr, 0));
       }
-      IEK_HIP(hipStreamEndCapture(st_, &step_graph_));
-      IEK_HIP(hipGraphInstantiate(&step_exec_, step_graph_, nullptr, nullptr, 0));
+      for (int i = 0; i < n; ++i) IEK_HIP(hipGraphLaunch(step_exec_, st_));
+    } else {
+      for (int i = 0; i < n; ++i) step_body();
     }
-    for (int i = 0; i < n; ++i) IEK_HIP(hipGraphLaunch(step_exec_, st_));
-  } else {
-    for (int i = 0; i < n; ++i) step_body();
   }
   std::vector<int> flags(n);
   IEK_HIP(hipMemcpyAsync(out_ids, d_gen_, (size_t)n * 4, hipMemcpyDeviceToHost, st_));
@@ -1418,6 +1552,7 @@ void Session::generate_greedy(int n, uint32_t* out_ids, bool use_graph) {
       pos_ = pos0 + i - 1;
       launch_set_int(d_pos_, pos_, st_);
       IEK_HIP(hipMemcpyAsync(d_tok_, &out_ids[i - 1], 4, hipMemcpyHostToDevice, st_));
+      ChainTurn again(m_->device, st_, chain_);
       decode_body();
       pos_ += 1;
     }

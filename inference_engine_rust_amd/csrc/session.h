@@ -51,6 +51,12 @@ class Session {
 
   int kv_len() const { return pos_; }
   int decode_path() const { return chain_ ? 1 : 0; }
+  // Iteration limit of the decode chain's bounded waits (0: the default). A test aid: a small
+  // limit makes the next chain step give up its waits and fail with ST_DEVICE.
+  void set_chain_spin(unsigned spin);
+  // Prefills (session or layer level) that ran again in the f32 mode because an activation was
+  // beyond the fp16 pair's range.
+  int f32_prefills() const { return f32_prefills_; }
   int state_rows() const { return state_rows_; }
   void copy_hidden(float* out, size_t cap, int* rows);
   void copy_kv(int layer, bool v, float* out, size_t cap);  // [n_kv][pos][head_dim] -> f32
@@ -87,6 +93,7 @@ class Session {
   void logits_body(bool argmax);  // final norm + LM head (+ softcap) into logits_
   void argmax_body(bool record);
   void sync();
+  bool overflowed();
   void check_state() const;
 
   Model* m_;
@@ -121,6 +128,15 @@ class Session {
   unsigned long long* d_key_ = nullptr;
   int* d_flag_ = nullptr;  // non-finite logit seen by the fused argmax
   int* d_cnt_ = nullptr;   // per-KV-head slice counters of the decode attention
+  // Prefill inputs beyond the fp16 pair's range: the flag the splitting kernels set, its pinned
+  // host copy, whether the prefill is running in the f32 mode, how often it has, and the layer
+  // input a layer-level prefill keeps for a rerun.
+  int* d_ovf_ = nullptr;
+  int* h_ovf_ = nullptr;
+  bool f32_prefill_ = false;
+  int f32_prefills_ = 0;
+  float* x_save_ = nullptr;
+  size_t x_save_cap_ = 0;
   int pos_ = 0;
   int state_rows_ = 0;  // rows of the last ForwardState (0 = none)
   bool state_prefill_ = false;

@@ -87,6 +87,8 @@ EXPORTS = {
     "iek_session_generate_greedy": ([_P, _SZ, _P], ctypes.c_int),
     "iek_session_kv_len": ([_P, ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
     "iek_session_decode_path": ([_P, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
+    "iek_session_set_chain_spin": ([_P, ctypes.c_uint32], ctypes.c_int),
+    "iek_session_f32_prefills": ([_P, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
     "iek_session_bench_kernel": ([_P, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
                                   ctypes.POINTER(ctypes.c_double)], ctypes.c_int),
     "iek_session_hidden": ([_P, _P, _SZ, ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
@@ -281,6 +283,18 @@ class InferenceSession:
         """0: per-launch decode kernels; 1: the decode chain (persistent phase launches)."""
         v = ctypes.c_int(0)
         _check(lib().iek_session_decode_path(self._h, ctypes.byref(v)))
+        return int(v.value)
+
+    def set_chain_spin(self, spin: int) -> None:
+        """Iteration limit of the decode chain's bounded waits (0: the default); a test aid for
+        the chain's failure path."""
+        _check(lib().iek_session_set_chain_spin(self._h, spin))
+
+    def f32_prefills(self) -> int:
+        """How many prefills of this session ran again on f32 activations (an activation beyond
+        the fp16 pair's range)."""
+        v = ctypes.c_int(0)
+        _check(lib().iek_session_f32_prefills(self._h, ctypes.byref(v)))
         return int(v.value)
 
     def kv_len(self) -> int:

@@ -326,3 +326,57 @@ def with_metadata(src: str, dst: str, entries) -> str:
         f.write(head)
         f.write(buf[data_start:])
     return dst
+
+
+def tensor_offsets(path: str) -> dict:
+    """{tensor name: (absolute byte offset of its data, ggml type, dims)} of a GGUF file (the
+    tensor-info table of gguf_types.rs / tensor_loader.rs: name, n_dims, dims, type, offset
+    relative to the aligned data section)."""
+    import struct
+
+    with open(path, "rb") as f:
+        head = f.read(1 << 20)
+        while True:  # the header of a large vocabulary can exceed the first read
+            try:
+                return _tensor_offsets(head)
+            except struct.error:
+                more = f.read(len(head))
+                if not more:
+                    raise
+                head += more
+
+
+def _tensor_offsets(buf: bytes) -> dict:
+    import struct
+
+    _, _, n_t, n_kv = struct.unpack_from("<IIQQ", buf, 0)
+    o, align = 24, 32
+    for _ in range(n_kv):
+        (kl,) = struct.unpack_from("<Q", buf, o)
+        key = buf[o + 8:o + 8 + kl].decode()
+        (t,) = struct.unpack_from("<I", buf, o + 8 + kl)
+        if key == "general.alignment" and t == GGUF_U32:
+            (align,) = struct.unpack_from("<I", buf, o + 12 + kl)
+        o = _skip_value(buf, o + 12 + kl, t)
+    infos = []
+    for _ in range(n_t):
+        (nl,) = struct.unpack_from("<Q", buf, o)
+        name = buf[o + 8:o + 8 + nl].decode()
+        o += 8 + nl
+        (nd,) = struct.unpack_from("<I", buf, o)
+        dims = list(struct.unpack_from(f"<{nd}Q", buf, o + 4))
+        o += 4 + 8 * nd
+        gt, off = struct.unpack_from("<IQ", buf, o)
+        o += 12
+        infos.append((name, off, gt, dims))
+    data = (o + align - 1) // align * align
+    return {n: (data + off, gt, dims) for n, off, gt, dims in infos}
+
+
+def patch_bytes(path: str, tensor: str, offset: int, data: bytes) -> None:
+    """Overwrite `data` at byte `offset` of tensor `tensor`'s data in the GGUF file `path` (tests
+    plant non-finite block scales this way)."""
+    start, _, _ = tensor_offsets(path)[tensor]
+    with open(path, "r+b") as f:
+        f.seek(start + offset)
+        f.write(data)

@@ -1,0 +1,45 @@
+"""Writes tests/golden/c3_seed0.json from the pinned CPU oracle (run from the repository root; a
+few minutes on 8 cores).
+
+The full C3 model (synthetic GGUF ``c3``, seed 0: the Gemma-4-E2B-style preset at its own
+dimensions — 35 layers, d 1536, 20 KV-borrowing layers, per-layer embeddings of 256, Q8_0
+weights, a tied 262 144-row Q8_0 head with a soft cap of 30) and bench.py's prompt (256 uniform
+ids from seed 0): the prefill state and 32 decode states of the oracle's greedy run, with the
+figures ``golden_run.step_record`` keeps per step.
+"""
+import json
+import os
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+
+import oracle as O  # noqa: E402
+from golden_run import record  # noqa: E402
+from inference_engine_rust_amd import synth  # noqa: E402
+
+N_PROMPT, N_STEPS, PROMPT_SEED = 256, 33, 0
+
+
+def main():
+    t0 = time.time()
+    log = lambda m: print(f"[{time.time() - t0:7.1f}s] {m}", flush=True)  # noqa: E731
+    with tempfile.TemporaryDirectory(dir="/dev/shm" if os.path.isdir("/dev/shm") else None) as d:
+        p = os.path.join(d, "c3.gguf")
+        spec = synth.preset("c3")
+        synth.write_gemma4(p, spec, seed=0)
+        s = O.Session(O.Model(p))
+        s.prefill(synth.prompt_ids(PROMPT_SEED, N_PROMPT, spec.vocab))
+        log("prefill done")
+        steps = record(O, s, N_STEPS, log)
+    out = {"config": "c3", "seed": 0, "prompt_seed": PROMPT_SEED, "n_prompt": N_PROMPT, "steps": steps}
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "c3_seed0.json"), "w") as f:
+        json.dump(out, f)
+
+
+if __name__ == "__main__":
+    main()

@@ -91,9 +91,10 @@ def _q4k_dmin_m(w, k, n):
     return np.repeat(per, 32, axis=1).reshape(-1)[: k * n].reshape(n, k)
 
 
-def _check_matmul(dt, k, n, m, seed=0):
+def _check_matmul(dt, k, n, m, seed=0, a=None):
     w = _weights(dt, k, n, seed)
-    a = synth.normal(seed + 1, f"a{k}", m * k, 0.0, 1.0).reshape(m, k)
+    if a is None:
+        a = synth.normal(seed + 1, f"a{k}", m * k, 0.0, 1.0).reshape(m, k)
     want = O.matmul(ORC[dt], a, w, k, n)
     dw, da = dev(w.view(np.uint8)), dev(a)
     out = torch.empty((m, n), dtype=torch.float32, device="cuda")
@@ -139,6 +140,26 @@ def test_gemm_parity(gpu, dt, k, n, m):
 def test_gemm_parity_mistral_shapes_m512(gpu, dt, k, n):
     """The four Mistral-7B projection shapes at C1's M = 512 (Q/O, K/V, gate/up, down)."""
     _check_matmul(dt, k, n, 512)
+
+
+def _wide_range_rows(m, k, seed):
+    """Activations over the f32 range the reference takes (src/ops/matmul.rs:176-204 multiplies any
+    finite f32): row r is N(0, 1) scaled by 10^(-3 + 9 r / (m - 1)), up to 1e6; every 8th row also
+    has a 32-block of same-sign values near 3000, whose per-32 sum (~1e5) exceeds fp16's 65504."""
+    rng = np.random.default_rng(seed)
+    a = rng.standard_normal((m, k)).astype(np.float32) * np.logspace(-3, 6, m).astype(np.float32)[:, None]
+    for r in range(0, m, 8):
+        b = int(rng.integers(0, k // 32))
+        a[r, 32 * b:32 * b + 32] = (np.abs(rng.normal(3000.0, 100.0, 32)) * (1 if r % 16 else -1)).astype(np.float32)
+    return a
+
+
+@pytest.mark.parametrize("dt,k,n,m", [(E.Q4K, 4096, 1024, 512), (E.Q6K, 4096, 1024, 512), (E.Q8_0, 2048, 200, 64),
+                                      (E.F32, 1024, 136, 33)])
+def test_gemm_parity_full_f32_range(gpu, dt, k, n, m):
+    """The op-level GEMM on activations beyond fp16's range: each row goes onto the matrix cores
+    scaled by a power of two and is scaled back, so the result keeps the f32 reordering bound."""
+    _check_matmul(dt, k, n, m, seed=3, a=_wide_range_rows(m, k, 40 + dt))
 
 
 def test_rmsnorm_parity(gpu):

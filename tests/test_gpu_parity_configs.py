@@ -8,10 +8,12 @@
   grouped-query prefill attention and the two-stream decode attention at head_dim 128.
 * g1 (Gemma-4 with C3's head dims 256 / 512 and a GQA group of 8): the 256- and 512-wide prefill
   attention tiles and the f32-cache decode attention.
-* The full 32-layer C2 and C4 models through the properties the reference's own tests state
-  (tests/prefill_smoke.rs:99-144: prefill of N+1 tokens == prefill of N + decode of one) and graph
-  replay == stepwise decode, plus C2's first greedy tokens against the committed oracle run
-  tests/golden/c2_seed0_tokens.json (bench.py's prompt).
+* The full 32-layer C2 and C4 models and the full C3 model through the properties the reference's
+  own tests state (tests/prefill_smoke.rs:99-144: prefill of N+1 tokens == prefill of N + decode of
+  one) and graph replay == stepwise decode, plus teacher-forced comparisons with committed oracle
+  runs on bench.py's prompts (tests/golden/c2_seed0.json: 33 states; c3_seed0.json: 33 states;
+  c4_seed0.json: 5 states after the 8192-token prompt).
+* The RoPE base read from its reference key with a decoy key present.
 * A Q4_K_M-style mix of Q4_K and Q6_K attn_v / ffn_down across layers, and F16 tensors.
 
 Bars: greedy tokens identical; logits within 1e-3 relative L2 of the oracle (on the 1024 stored
@@ -145,28 +147,63 @@ def _full_model_properties(path, n_prompt, vocab):
     return m
 
 
-def test_full_c2_model_properties_and_golden_tokens(gpu, big_dir):
+def _teacher_forced_golden(s, g):
+    """Every step of a committed oracle run (golden_run.record): the device's logits against the
+    oracle's (first logits within LOGIT_REL_L2, the norm of the whole vector, the 8 largest), its
+    greedy token equal to the oracle's wherever the oracle's top-2 gap is at least GAP_EXACT (else
+    one of the two), then the oracle's token is decoded, so that a near-tie cannot end the
+    comparison."""
+    worst = 0.0
+    for i, st in enumerate(g["steps"]):
+        lg = s.logits_last_token()
+        head = np.array(st["head"])
+        rel = rel_l2(lg[: head.size], head)
+        worst = max(worst, rel)
+        assert rel < LOGIT_REL_L2, (i, rel)
+        assert abs(np.linalg.norm(lg.astype(np.float64)) / st["norm"] - 1) < LOGIT_REL_L2, i
+        np.testing.assert_allclose(lg[st["top_idx"]], st["top_val"], rtol=0, atol=2e-3 * np.max(np.abs(head)))
+        got = E.greedy_next_token(s)
+        if st["gap"] >= GAP_EXACT:
+            assert got == st["token"], f"step {i}"
+        else:
+            assert got in (st["token"], st["runner_up"]), f"step {i}"
+        if i + 1 < len(g["steps"]):
+            s.decode_token(st["token"])
+    assert s.kv_len() == g["n_prompt"] + len(g["steps"]) - 1
+    return worst
+
+
+def test_full_c2_model_properties_and_golden(gpu, big_dir):
     spec = synth.preset("c2")
     p = os.path.join(big_dir, "c2.gguf")
     synth.write_llama(p, spec, seed=0)
     m = _full_model_properties(p, 512, spec.vocab)
-    g = json.load(open(os.path.join(GOLDEN, "c2_seed0_tokens.json")))
+    g = json.load(open(os.path.join(GOLDEN, "c2_seed0.json")))
+    s = E.InferenceSession(m)
+    assert s.decode_path() == 1
+    s.prefill(synth.prompt_ids(g["prompt_seed"], g["n_prompt"], spec.vocab))
+    _teacher_forced_golden(s, g)  # 33 states: the prefill's and 32 decodes'
+    os.remove(p)
+
+
+def test_full_c3_model_properties_and_golden(gpu, big_dir):
+    """C3 at its own dimensions (the Gemma-4-E2B-style preset: 35 layers, d 1536, 20 KV-borrowing
+    layers, per-layer embeddings of 256, Q8_0 projections and a tied 262 144-row Q8_0 head with a
+    soft cap) against the committed oracle run tests/golden/c3_seed0.json (make_c3.py)."""
+    spec = synth.preset("c3")
+    p = os.path.join(big_dir, "c3.gguf")
+    synth.write_gemma4(p, spec, seed=0)
+    m = _full_model_properties(p, 256, spec.vocab)
+    c = m.config
+    assert (c.n_layers, c.hidden_dim, c.vocab_size, c.embedding_length_per_layer) == (35, 1536, 262144, 256)
+    specs = [m.layer_spec(i) for i in range(c.n_layers)]
+    assert sum(sp["kv_borrow"] >= 0 for sp in specs) == 20
+    assert {sp["head_dim"] for sp in specs} == {256, 512}
+    assert m.tensor("token_embd.weight")["dtype"] == E.Q8_0 and c.has_final_logit_softcapping
+    g = json.load(open(os.path.join(GOLDEN, "c3_seed0.json")))
     s = E.InferenceSession(m)
     s.prefill(synth.prompt_ids(g["prompt_seed"], g["n_prompt"], spec.vocab))
-    assert s.decode_path() == 1
-    for i, (t, t2, gap) in enumerate(zip(g["tokens"], g["runner_up"], g["top2_gap"])):
-        lg = s.logits_last_token()  # 32-layer logits against the oracle's (prefill state, then decode states)
-        head = np.array(g["head"][i])
-        assert rel_l2(lg[: head.size], head) < LOGIT_REL_L2, (i, rel_l2(lg[: head.size], head))
-        assert abs(np.linalg.norm(lg.astype(np.float64)) / g["norm"][i] - 1) < LOGIT_REL_L2
-        got = E.greedy_next_token(s)
-        if gap >= GAP_EXACT:
-            assert got == t, f"step {i}"
-        else:  # the oracle's two best logits are within float rounding of the 32-layer sum
-            assert got in (t, t2), f"step {i}"
-            if got != t:
-                break
-        s.decode_token(got)
+    _teacher_forced_golden(s, g)
     os.remove(p)
 
 
@@ -174,8 +211,42 @@ def test_full_c4_model_properties(gpu, big_dir):
     spec = synth.preset("c4")
     p = os.path.join(big_dir, "c4.gguf")
     synth.write_llama(p, spec, seed=0)
-    _full_model_properties(p, 8192, spec.vocab)
+    m = _full_model_properties(p, 8192, spec.vocab)
+    # the full 32-layer C4 model against the committed oracle run (make_c4_full.py): bench.py's
+    # 8192-token prompt, then 4 decode steps over the saturated context
+    g = json.load(open(os.path.join(GOLDEN, "c4_seed0.json")))
+    s = E.InferenceSession(m)
+    s.prefill(synth.prompt_ids(g["prompt_seed"], g["n_prompt"], spec.vocab))
+    _teacher_forced_golden(s, g)
     os.remove(p)
+
+
+def test_rope_theta_read_from_its_reference_key(gpu, model_dir):
+    """model_config.rs:160-162 reads the RoPE base from llama.rope.theta (default 10000). A model
+    whose llama.rope.theta is 50000 and which also carries a decoy llama.rope.freq_base of 10000:
+    the device and the oracle both resolve 50000 and agree; the logits differ from the same
+    weights under the default base, so the key is read and used."""
+    base = str(model_dir / "c0_theta_base.gguf")
+    synth.write_llama(base, synth.preset("c0"), seed=6)
+    p = synth.with_metadata(base, str(model_dir / "c0_theta.gguf"),
+                            [("llama.rope.theta", synth.GGUF_F32, 50000.0),
+                             ("llama.rope.freq_base", synth.GGUF_F32, 10000.0)])
+    m, om = E.LoadedModel.load(p), O.Model(p)
+    assert m.config.rope_theta == 50000.0 and om.cfg.rope_theta == 50000.0
+    prompt = synth.prompt_ids(8, 40)
+    s, r, d = E.InferenceSession(m), O.Session(om), E.InferenceSession(E.LoadedModel.load(base))
+    s.prefill(prompt)
+    r.prefill(prompt)
+    d.prefill(prompt)
+    for step in range(4):
+        lg, lr = s.logits_last_token(), r.logits()
+        assert rel_l2(lg, lr) < LOGIT_REL_L2
+        assert rel_l2(d.logits_last_token(), lr) > 1e-2  # the default base gives other logits
+        t = O.argmax(lr)
+        assert E.greedy_next_token(s) == t
+        s.decode_token(t)
+        r.decode(t)
+        d.decode_token(t)
 
 
 def test_q4_k_m_mixed_layers(gpu, big_dir):

@@ -32,6 +32,27 @@ def test_config_resolution(c0):
     assert spec["sliding_window"] == -1 and spec["rotary_dim"] == 64 and spec["kv_borrow"] == -1
 
 
+def test_rope_theta_key_resolution(c0_path, tmp_path):
+    """model_config.rs:160-162: llama.rope.theta, else gemma4.rope.freq_base, else 10000; a
+    llama.rope.freq_base key (llama.cpp's name) is not read."""
+    F = synth.GGUF_F32
+    cases = [([("llama.rope.theta", F, 50000.0), ("llama.rope.freq_base", F, 10000.0)], 50000.0),
+             ([("llama.rope.freq_base", F, 77000.0)], 10000.0),
+             ([("gemma4.rope.freq_base", F, 30000.0)], 10000.0),  # the synthetic file holds llama.rope.theta
+             ([("llama.rope.theta", F, 20000.0), ("gemma4.rope.freq_base", F, 30000.0)], 20000.0)]
+    logits = {}
+    ids = synth.prompt_ids(1, 24)
+    for i, (entries, want) in enumerate(cases):
+        p = synth.with_metadata(c0_path, str(tmp_path / f"theta{i}.gguf"), entries)
+        m = O.Model(p)
+        assert m.cfg.rope_theta == want and m.layer_spec(0)["rope_theta"] == want, (entries, m.cfg.rope_theta)
+        s = O.Session(m)
+        s.prefill(ids)
+        logits[want] = s.logits()
+    # the base reaches the rotation: another base gives other logits
+    assert np.max(np.abs(logits[50000.0] - logits[10000.0])) > 1e-3
+
+
 def test_prefill_vs_prefill_plus_decode(c0):
     ids = synth.prompt_ids(0, 9)
     a = O.Session(c0)

@@ -2,7 +2,9 @@
 allocating one (iek_dev_attention_decode), through the C ABI: identical kernels and launch shapes,
 so the outputs must be bit-identical. Two calls in a row, the second with a smaller input (fewer
 heads, a shorter cache), show that the shared per-device scratch carries nothing over from the
-previous call; a shape whose partials exceed the scratch is rejected with IEK_ERR_OP.
+previous call; a shape whose partials exceed the scratch is rejected with IEK_ERR_OP. Captured
+in a HIP graph after a warm-up call (which resolves the scratch address), the entry point replays
+bit-identically, with other work on the device between the replays.
 """
 import math
 
@@ -53,3 +55,33 @@ def test_noalloc_rejects_oversize(gpu):
         E.attention_decode_noalloc(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), E.F32, 64, 8, 512, 32768, 10, 0, 1.0,
                                    out.data_ptr())
     assert e.value.kind == "Op" and "scratch" in str(e.value)
+
+
+def test_noalloc_replays_from_a_captured_graph(gpu):
+    n_heads, n_kv, hd, max_len, total, window = 32, 8, 128, 2048, 1500, 0
+    q, kc, vc = _case(n_heads, n_kv, hd, max_len, total, True, 4)
+    scale = 1.0 / math.sqrt(hd)
+    want = torch.empty(n_heads * hd, dtype=torch.float32, device="cuda")
+    got = torch.empty(n_heads * hd, dtype=torch.float32, device="cuda")
+    E.attention_decode(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), E.F32, n_heads, n_kv, hd, max_len, total, window,
+                       scale, want.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up: resolves the scratch address before the capture
+        E.attention_decode_noalloc(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), E.F32, n_heads, n_kv, hd, max_len,
+                                   total, window, scale, got.data_ptr(), side.cuda_stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side, capture_error_mode="thread_local"):
+        E.attention_decode_noalloc(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), E.F32, n_heads, n_kv, hd, max_len,
+                                   total, window, scale, got.data_ptr(), side.cuda_stream)
+    for i in range(4):
+        got.fill_(float("nan"))
+        # other work on the device between replays, including the allocating entry point
+        other = torch.empty_like(want)
+        E.attention_decode(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), E.F32, n_heads, n_kv, hd, max_len, total // 2,
+                           window, scale, other.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (i, float((got - want).abs().max()))
