@@ -317,7 +317,10 @@ IEK_DEV void control(const ChainArgs& a, Smem& S, int pos) {
           break;
         }
       }
-      if (lds_ld(&S.abort_)) return;
+      if (lds_ld(&S.abort_)) {
+        vm_wait<0>();  // the norm weight copies in flight land before the wave ends
+        return;
+      }
     }
     // ---- stage x (and the norm weight) in the consumers' register layout
     if (P->x_mode == CX_EMBED_Q4K) {
@@ -391,7 +394,10 @@ IEK_DEV void control(const ChainArgs& a, Smem& S, int pos) {
         }
       }
     }
-    if (lds_ld(&S.abort_)) return;
+    if (lds_ld(&S.abort_)) {
+      vm_wait<0>();
+      return;
+    }
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     // ---- epilogue: lane = row pair
     unsigned long long run_key = 0;
