@@ -83,8 +83,9 @@ void launch_add_f32(float* out, const float* part, size_t n, hipStream_t st);
 void launch_gemm_mfma(int dt, const void* w, const __half* xh, const __half* xl, int M, int K, int N, float* out,
                       const float* resid, hipStream_t st);
 void launch_dequant(int dt, const void* blocks, size_t nblocks, float* out, hipStream_t st);
-void launch_embed(int dt, const void* table, size_t hidden, const uint32_t* ids, int n, float scale, float* out,
-                  hipStream_t st);
+// rows: the table's row count (vocabulary); device-produced ids are clamped below it
+void launch_embed(int dt, const void* table, size_t hidden, size_t rows, const uint32_t* ids, int n, float scale,
+                  float* out, hipStream_t st);
 void launch_rmsnorm(const float* in, const float* w, int rows, int dim, float eps, float* out, hipStream_t st);
 // Producers that also emit a prefill GEMM input: fp16 (hi, lo) planes of their [rows, dim] output
 // and its per-32 sums as an fp16 pair (two planes of rows * dim / 32 halves at `sums`), as

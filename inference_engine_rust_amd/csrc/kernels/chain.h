@@ -36,7 +36,7 @@ struct ChainPhase {
   const float* x;
   const float* norm_w;  // fused RMSNorm of x, or null
   float eps;
-  int pad0;
+  int emb_rows;  // CX_EMBED_Q4K: rows of the embedding table
   const float* resid;  // CE_RESID
   // CE_QKV
   const float* rope_cs;  // [ctx][npairs][2]

@@ -327,7 +327,9 @@ IEK_DEV void control(const ChainArgs& a, Smem& S, int pos) {
       // lane = chunk: dequantise row *tok of the Q4_K table (chunk = superblock ch/4, part ch%4),
       // element by element as the reference (quant_k_handler.rs:38-82, q == 0 -> product 0)
       typedef const __attribute__((address_space(4))) uint32_t* CU32;
-      const uint32_t tok = *(CU32)a.tok;
+      // the host checks the ids it is given; one the previous step produced is clamped to the
+      // table (a flagged step's id is never used)
+      const uint32_t tok = min(*(CU32)a.tok, (uint32_t)P->emb_rows - 1u);
       for (int p = 0; p < npass; ++p) {
         const int ch = min(lane + 64 * p, nchunk - 1);
         const uint8_t* blk = P->emb + ((size_t)tok * K + 64 * (size_t)ch) / QK_K * Q4K_BYTES;
@@ -663,10 +665,12 @@ __global__ __launch_bounds__(NT) void chain_kernel(ChainArgs args) {
     if (old == gridDim.x - 1) {
       if (a.finish_argmax) {
         const unsigned long long key = __hip_atomic_load(a.amax_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t idx = 0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull);
+        // every folded logit leaves a nonzero key; none (the launch gave its waits up before the LM
+        // head) flags the step, and the published id stays a valid one for the next step's lookup
+        const uint32_t idx = key ? 0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull) : 0u;
         a.out_tok[0] = idx;
         const int i = a.step ? *a.step : 0;
-        a.flags[i] = __hip_atomic_load(a.amax_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        a.flags[i] = key ? __hip_atomic_load(a.amax_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1;
         if (a.step) {
           a.gen[i] = idx;
           *a.step = i + 1;

@@ -26,20 +26,24 @@ void launch_dequant(int dt, const void* blocks, size_t nblocks, float* out, hipS
 // the previous step's argmax produced.
 // One thread per element: row r = blockIdx.x, elements blockIdx.y*256 + threadIdx.x (a single
 // decode row spreads over hidden/256 workgroups instead of looping in one).
-__global__ void embed_kernel(int dt, const uint8_t* table, size_t hidden, const uint32_t* ids, float scale, float* out) {
+// The host range-checks the ids it is given; an id the device produced is clamped to the table
+// (a flagged step, whose id is never used, cannot send the read past it).
+__global__ void embed_kernel(int dt, const uint8_t* table, size_t hidden, size_t rows, const uint32_t* ids, float scale,
+                             float* out) {
   const int r = blockIdx.x;
   const size_t h = (size_t)blockIdx.y * 256 + threadIdx.x;
   if (h >= hidden) return;
-  const size_t base = (size_t)ids[r] * hidden;
+  const size_t base = std::min((size_t)ids[r], rows - 1) * hidden;
   float v = flat_elem(dt, table, base + h);
   if (scale != 1.0f) v = v * scale;
   out[(size_t)r * hidden + h] = v;
 }
 
-void launch_embed(int dt, const void* table, size_t hidden, const uint32_t* ids, int n, float scale, float* out,
-                  hipStream_t st) {
+void launch_embed(int dt, const void* table, size_t hidden, size_t rows, const uint32_t* ids, int n, float scale,
+                  float* out, hipStream_t st) {
+  if (rows == 0) fail(ST_TENSOR, "embedding table has no rows");
   hipLaunchKernelGGL(embed_kernel, dim3(n, (unsigned)((hidden + 255) / 256)), dim3(256), 0, st, dt,
-                     (const uint8_t*)table, hidden, ids, scale, out);
+                     (const uint8_t*)table, hidden, rows, ids, scale, out);
 }
 
 // Block-wide sum for 256-thread blocks.
@@ -566,10 +570,13 @@ void launch_argmax(const float* logits, int n, unsigned long long* key_out, int*
 // packed key and the flag are reset for the next LM-head launch.
 __global__ void argmax_finish_kernel(unsigned long long* key, int* flag, uint32_t* tok, uint32_t* list, int* flags,
                                      int* step) {
-  uint32_t idx = 0xFFFFFFFFu - (uint32_t)(*key & 0xFFFFFFFFull);
+  const unsigned long long k = *key;
+  // every folded logit leaves a nonzero key; none (no logit reached the argmax) is an error, and
+  // the published id stays a valid one
+  uint32_t idx = k ? 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull) : 0u;
   tok[0] = idx;
   const int i = step ? *step : 0;
-  flags[i] = *flag;
+  flags[i] = k ? *flag : 1;
   if (step) {
     list[i] = idx;
     *step = i + 1;

@@ -662,6 +662,7 @@ void Session::prepare_chain() {
       P.x_mode = CX_EMBED_Q4K;
       P.emb = (const uint8_t*)m_->token_embd.dev;
       P.emb_out = xdec_;
+      P.emb_rows = (int)vocab;
     }
     v.push_back(P);
     if (split_v) {
@@ -818,11 +819,10 @@ void Session::embed_ple(const uint32_t* d_ids, int n, const float* x, const __ha
   if (te.dims.size() != 2) fail(ST_TENSOR, "expected 2D embedding tensor");
   const size_t row = std::min(te.dims[0], te.dims[1]);
   vocab = std::max(te.dims[0], te.dims[1]);
-  (void)vocab;
   if ((int)row != packn) fail(ST_MODEL, "per_layer_token_embd row width != n_layers*ple_dim");
   if (m_->ple_proj_norm.host_f32.size() != (size_t)c.ple_dim)
     fail(ST_MODEL, "per_layer_proj_norm len != ple_dim");
-  launch_embed(te.dtype, te.dev, row, d_ids, n, 1.0f, tok, st_);
+  launch_embed(te.dtype, te.dev, row, vocab, d_ids, n, 1.0f, tok, st_);
   project(m_->ple_model_proj, x, xs, n, H_, packn, proj, nullptr, st_, f32_prefill_);
   launch_ple_pack(proj, tok, (const float*)m_->ple_proj_norm.dev, n, c.n_layers, c.ple_dim, c.rms_eps,
                   c.ple_proj_scale, sqrtf((float)c.ple_dim), c.ple_combine_scale, pack, st_);
@@ -1056,7 +1056,7 @@ void Session::prefill(const uint32_t* ids, int n) {
   ensure_rows(n);
   IEK_HIP(hipMemcpyAsync(d_ids_, ids, (size_t)n * 4, hipMemcpyHostToDevice, st_));
   auto body = [&] {
-    launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, d_ids_, n, c.embed_scale, x_, st_);
+    launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, vocab, d_ids_, n, c.embed_scale, x_, st_);
     if (gemma_) {
       embed_ple(d_ids_, n, x_, split_rows(x_, n, H_), ple_tok_, ple_proj_, ple_pack_);
       for (int li = 0; li < c.n_layers; ++li) layer_prefill_gemma(li, n);
@@ -1217,7 +1217,7 @@ void Session::embed(const uint32_t* ids, int n) {
   if ((int)hid != H_) fail(ST_MODEL, "ForwardState: embedding dim mismatch");
   ensure_rows(n);
   IEK_HIP(hipMemcpyAsync(d_ids_, ids, (size_t)n * 4, hipMemcpyHostToDevice, st_));
-  launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, d_ids_, n, c.embed_scale, x_, st_);
+  launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, vocab, d_ids_, n, c.embed_scale, x_, st_);
   if (gemma_) {
     launch_fill_i32(d_ovf_, 0, 1, st_);
     embed_ple(d_ids_, n, x_, split_rows(x_, n, H_), ple_tok_, ple_proj_, ple_pack_);
@@ -1336,7 +1336,7 @@ void Session::decode_body(bool head) {
   size_t vocab;
   size_t hid = embedding_hidden(m_->token_embd, &vocab);
   if (chain_) {
-    if (!chain_embed_) launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, d_tok_, 1, c.embed_scale, xdec_, st_);
+    if (!chain_embed_) launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, vocab, d_tok_, 1, c.embed_scale, xdec_, st_);
     const int L = c.n_layers;
     for (int li = 0; li <= L; ++li) {
       if (li > 0) {
@@ -1368,7 +1368,7 @@ void Session::decode_body(bool head) {
     }
     return;
   }
-  launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, d_tok_, 1, c.embed_scale, xdec_, st_);
+  launch_embed(m_->token_embd.dtype, m_->token_embd.dev, hid, vocab, d_tok_, 1, c.embed_scale, xdec_, st_);
   if (gemma_) {
     embed_ple(d_tok_, 1, xdec_, nullptr, ple_tokd_, ple_projd_, ple_packd_);
     float* xr = xdec_;
