@@ -152,18 +152,32 @@ def _teacher_forced_golden(s, g):
     oracle's (first logits within LOGIT_REL_L2, the norm of the whole vector, the 8 largest), its
     greedy token equal to the oracle's wherever the oracle's top-2 gap is at least GAP_EXACT (else
     one of the two), then the oracle's token is decoded, so that a near-tie cannot end the
-    comparison."""
+    comparison.
+
+    Where the golden also holds the reassociated oracle's distances (the oracle with every f32
+    matmul summed as two halves of K: the reference's own arithmetic in another order), a model
+    that amplifies f32 rounding beyond 1e-3 gets bars scaled to them: logits within twice the
+    reordered oracle's relative L2, the 8 largest within twice its largest change there, and exact
+    tokens wherever the top-2 gap is at least four times that change. Returns the worst ratio of
+    the device's distance to the reordered oracle's (or the worst distance without them)."""
     worst = 0.0
     for i, st in enumerate(g["steps"]):
         lg = s.logits_last_token()
         head = np.array(st["head"])
         rel = rel_l2(lg[: head.size], head)
-        worst = max(worst, rel)
-        assert rel < LOGIT_REL_L2, (i, rel)
-        assert abs(np.linalg.norm(lg.astype(np.float64)) / st["norm"] - 1) < LOGIT_REL_L2, i
-        np.testing.assert_allclose(lg[st["top_idx"]], st["top_val"], rtol=0, atol=2e-3 * np.max(np.abs(head)))
+        bar, gap_exact, atol = LOGIT_REL_L2, GAP_EXACT, 2e-3 * np.max(np.abs(head))
+        if "reassoc_rel" in st:
+            bar = max(bar, 2.0 * st["reassoc_rel"])
+            gap_exact = max(gap_exact, 4.0 * st["reassoc_top_dmax"])
+            atol = max(atol, 2.0 * st["reassoc_top_dmax"])
+            worst = max(worst, rel / st["reassoc_rel"])
+        else:
+            worst = max(worst, rel)
+        assert rel < bar, (i, rel, bar)
+        assert abs(np.linalg.norm(lg.astype(np.float64)) / st["norm"] - 1) < bar, i
+        np.testing.assert_allclose(lg[st["top_idx"]], st["top_val"], rtol=0, atol=atol)
         got = E.greedy_next_token(s)
-        if st["gap"] >= GAP_EXACT:
+        if st["gap"] >= gap_exact:
             assert got == st["token"], f"step {i}"
         else:
             assert got in (st["token"], st["runner_up"]), f"step {i}"
@@ -189,7 +203,10 @@ def test_full_c2_model_properties_and_golden(gpu, big_dir):
 def test_full_c3_model_properties_and_golden(gpu, big_dir):
     """C3 at its own dimensions (the Gemma-4-E2B-style preset: 35 layers, d 1536, 20 KV-borrowing
     layers, per-layer embeddings of 256, Q8_0 projections and a tied 262 144-row Q8_0 head with a
-    soft cap) against the committed oracle run tests/golden/c3_seed0.json (make_c3.py)."""
+    soft cap) against the committed oracle run tests/golden/c3_seed0.json (make_c3.py). At this
+    depth the random-weight model amplifies f32 rounding: the oracle reassociated moves its own
+    logits by 4e-3 .. 2e-2 relative L2 (recorded per step in the golden), so the bars follow that
+    measurement (_teacher_forced_golden)."""
     spec = synth.preset("c3")
     p = os.path.join(big_dir, "c3.gguf")
     synth.write_gemma4(p, spec, seed=0)
@@ -203,7 +220,8 @@ def test_full_c3_model_properties_and_golden(gpu, big_dir):
     g = json.load(open(os.path.join(GOLDEN, "c3_seed0.json")))
     s = E.InferenceSession(m)
     s.prefill(synth.prompt_ids(g["prompt_seed"], g["n_prompt"], spec.vocab))
-    _teacher_forced_golden(s, g)
+    ratio = _teacher_forced_golden(s, g)
+    print(f"C3: worst device / reordered-oracle logit distance ratio {ratio:.3f}")
     os.remove(p)
 
 
