@@ -424,7 +424,7 @@ def main():
     if not gemma:
         # the chain launch is the dominant decode kernel where the session decodes through it (the
         # tiny C0 model, whose FFN width is not a multiple of 256, runs per-launch kernels: latency)
-        if sess.decode_path() == 1:
+        if sess.decode_path() >= 1:
             roof = kernel_roofline(E, model, prompt, args.kernel_reps)
             print(f"[bench] dominant kernel {roof['achieved']} GB/s ({roof['avg_launch_us']} us/launch)",
                   file=sys.stderr, flush=True)

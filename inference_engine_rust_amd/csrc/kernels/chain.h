@@ -50,6 +50,12 @@ struct ChainPhase {
   // CE_ARGMAX
   float softcap;  // <= 0: none
   int pad2;
+  // Tiled chain (launch_chain2): the phase whose output is this phase's x (-1: x was written
+  // before the launch), whether a later phase reads this phase's output (its workgroups then
+  // arrive on the per-superblock counters), and per superblock of x the number of workgroups that
+  // write part of it (the arrivals that make it ready).
+  int x_src, arrive;
+  int expect[64];
 };
 
 constexpr int CHAIN_MAX_PHASES = 6;
@@ -79,5 +85,18 @@ struct ChainArgs {
 bool chain_phase_ok(int dt, int K, bool norm);
 void launch_chain(const ChainArgs& a, hipStream_t st);
 size_t chain_row_bytes(int dt, int K);
+
+// Tiled chain (the same phases, ChainArgs and epilogues): each workgroup's rows of a phase are
+// 16-row tiles, a consumer's items are (tile, superblock) pairs, and each superblock of x becomes
+// ready on its own counter (ChainPhase::x_src / arrive / expect). Counter words: per phase and
+// superblock one word, CHAIN2_CNT_STRIDE words apart, then the exit counter.
+constexpr int CHAIN2_MAX_SB = 64;     // superblocks of x per phase (K <= 16384)
+constexpr int CHAIN2_MAX_TILES = 8;   // 16-row tiles per workgroup and phase
+constexpr int CHAIN2_CNT_STRIDE = 16;
+constexpr int CHAIN2_COUNTER_WORDS = (CHAIN_MAX_PHASES * CHAIN2_MAX_SB + 1) * CHAIN2_CNT_STRIDE;
+// The x staging region holds K floats (K + K with a fused norm's weights).
+constexpr int CHAIN2_XS_FLOATS = 14336;
+bool chain2_phase_ok(int dt, int K, bool norm, int rows_per_wg);
+void launch_chain2(const ChainArgs& a, hipStream_t st);
 
 }  // namespace iek

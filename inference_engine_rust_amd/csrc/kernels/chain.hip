@@ -220,13 +220,8 @@ IEK_DEV float q4_item(const uint8_t* slot, int lane, int ch, const float (&x)[64
 // Regrouped Q6_K item: lane chunk ch = (superblock j, k = 2h + j16): weights l = 16*j16..+15 of
 // half h in its four quarters. x[16 qd + t] is the value of quarter qd, l = 16*j16 + t; xq[qd]
 // the quarter sums.
-IEK_DEV float q6_item(const uint8_t* slot, int lane, int ch, int pass, const float (&x)[64], const float (&xq)[4]) {
-  const uint4 qa = *reinterpret_cast<const uint4*>(slot + 16 * lane);
-  const uint4 qb = *reinterpret_cast<const uint4*>(slot + 1024 + 16 * lane);
-  const uint4 qh = *reinterpret_cast<const uint4*>(slot + 2048 + 16 * lane);
-  const int jl = (ch >> 2) - 16 * pass, k = ch & 3;
-  const uint32_t scw = *reinterpret_cast<const uint32_t*>(slot + 3072 + 16 * jl + 4 * k);
-  const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(slot + 3072 + 256 + 2 * jl));
+IEK_DEV float q6_core(const uint4& qa, const uint4& qb, const uint4& qh, uint32_t scw, float d, const float (&x)[64],
+                      const float (&xq)[4]) {
   const uint32_t A[4] = {qa.x, qa.y, qa.z, qa.w}, B[4] = {qb.x, qb.y, qb.z, qb.w}, H[4] = {qh.x, qh.y, qh.z, qh.w};
   float s[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -249,6 +244,16 @@ IEK_DEV float q6_item(const uint8_t* slot, int lane, int ch, int pass, const flo
   for (int qd = 0; qd < 4; ++qd)
     sum += (d * (float)(int8_t)((scw >> (8 * qd)) & 0xFF)) * (16777216.0f * s[qd] - 32.0f * xq[qd]);
   return sum;
+}
+
+IEK_DEV float q6_item(const uint8_t* slot, int lane, int ch, int pass, const float (&x)[64], const float (&xq)[4]) {
+  const uint4 qa = *reinterpret_cast<const uint4*>(slot + 16 * lane);
+  const uint4 qb = *reinterpret_cast<const uint4*>(slot + 1024 + 16 * lane);
+  const uint4 qh = *reinterpret_cast<const uint4*>(slot + 2048 + 16 * lane);
+  const int jl = (ch >> 2) - 16 * pass, k = ch & 3;
+  const uint32_t scw = *reinterpret_cast<const uint32_t*>(slot + 3072 + 16 * jl + 4 * k);
+  const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(slot + 3072 + 256 + 2 * jl));
+  return q6_core(qa, qb, qh, scw, d, x, xq);
 }
 
 // Element offset of value e (0..63) of chunk ch in x (the register layout of each dtype).
@@ -685,6 +690,526 @@ __global__ __launch_bounds__(NT) void chain_kernel(ChainArgs args) {
   }
 }
 
+// ==== Tiled chain (launch_chain2) ================================================================
+// The same phases and epilogues as chain_kernel, with a different decomposition:
+//  * A workgroup's rows of a phase form 16-row tiles; an item is one tile's 16 rows of one
+//    superblock (256 columns): 16 x 144 bytes (Q4_K) or 16 x 210 (regrouped Q6_K). Lane l of a
+//    consumer takes row l & 15 and the 64-value chunk l >> 4 of that superblock, so each lane's dot
+//    is the chain's per-lane arithmetic (q4_item / q6_core) on its own row; the four chunk lanes of
+//    a row are summed with two cross-lane adds per item (no full-wave reduction per row).
+//  * Items go sb-major (every tile of superblock 0, then of 1, ...); consumer c takes a contiguous
+//    range of them and keeps the x values of its current superblock in registers.
+//  * Superblock sb of a phase's x is ready once the workgroups that write part of it (ChainPhase::
+//    expect[sb] of them) have arrived on its counter, so there is no phase-wide barrier: the control
+//    wave polls the counters (lane = superblock), stages each ready superblock into LDS with one
+//    device-coherent copy and flags it; a consumer starts on a superblock as soon as it is flagged.
+//  * A fused RMSNorm no longer sits on that path: the consumers dot the rows with x * w, the control
+//    wave takes sum(x^2) once every superblock is staged, and the epilogue divides the dots by rms
+//    (the reference's (x * w) / rms, reassociated).
+constexpr int NC2 = 12;
+constexpr int DSLOT2 = 2;
+constexpr int NT2 = 64 * (1 + NC2);
+
+struct Smem2 {
+  uint8_t ring[NC2 * DSLOT2][SLOT];
+  float4 xs[CHAIN2_XS_FLOATS / 4];  // x per superblock as [sb][i4][chunk] float4; a norm's w after x
+  float part[CHAIN2_MAX_TILES][NC2][16];
+  int xflag[CHAIN2_MAX_SB];  // superblock staged for phase (value - 1)
+  // consumers finished with each phase: per phase, since a consumer without items in a run of
+  // phases signals them all at once (a cumulative count would let it stand in for a late one)
+  int done[CHAIN_MAX_PHASES];
+  int abort_;
+  unsigned spin;
+};
+
+IEK_DEV unsigned* cnt2(const ChainArgs& a, int ph, int sb) {
+  return a.counters + (size_t)(ph * CHAIN2_MAX_SB + sb) * CHAIN2_CNT_STRIDE;
+}
+
+IEK_DEV void set_abort2(Smem2& S, int* err, int code) {
+  if ((threadIdx.x & 63) == 0) __hip_atomic_store(err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  lds_st(&S.abort_, 1);
+}
+
+// Wave-uniform geometry of one phase for this workgroup.
+struct View2 {
+  const uint8_t *w0, *w1, *w2;
+  size_t rb;
+  int dt, nsb, u0, R, T, n_items, n0, n01, swiglu;
+};
+
+IEK_DEV View2 load_view2(const CPhase P, int b, int G) {
+  View2 v;
+  int u0, u1;
+  unit_range(P->units, b, G, u0, u1);
+  v.w0 = P->seg[0].w;
+  v.w1 = P->seg[1].w;
+  v.w2 = P->seg[2].w;
+  v.dt = P->dt;
+  v.nsb = P->K / QK_K;
+  v.rb = row_bytes_of(v.dt, P->K);
+  v.u0 = u0;
+  v.R = 2 * (u1 - u0);
+  v.T = (v.R + 15) / 16;
+  v.n_items = v.T * v.nsb;
+  v.n0 = P->seg[0].n;
+  v.n01 = v.n0 + P->seg[1].n;
+  v.swiglu = P->epi == CE_SWIGLU;
+  return v;
+}
+
+// Weight row of this workgroup's local row l (0 <= l < R): pair u0 + l / 2, row l & 1 of the pair.
+IEK_DEV const uint8_t* view2_row(const View2& v, int l) {
+  const int u = v.u0 + (l >> 1), r = l & 1;
+  const uintptr_t b0 = reinterpret_cast<uintptr_t>(v.w0), b1 = reinterpret_cast<uintptr_t>(v.w1),
+                  b2 = reinterpret_cast<uintptr_t>(v.w2);
+  if (v.swiglu) return reinterpret_cast<const uint8_t*>(b0 + (uintptr_t)r * (b1 - b0) + (size_t)u * v.rb);
+  const int g = 2 * u + r;
+  const uintptr_t in1 = g >= v.n0, in2 = g >= v.n01;
+  const int row = g - (in2 ? v.n01 : (in1 ? v.n0 : 0));
+  return reinterpret_cast<const uint8_t*>(b0 + in1 * (b1 - b0) + in2 * (b2 - b1) + (size_t)row * v.rb);
+}
+
+IEK_DEV void item2_of(const View2& v, int i, int& sb, int& t) {
+  sb = i / v.T;
+  t = i - sb * v.T;
+}
+
+// COPIES_PER_ITEM copy instructions for item i (the consumer waits rely on the count). Q4_K: lane
+// (n, g) copies the 32 quant bytes of chunk g of row n's superblock and the row's header; regrouped
+// Q6_K: the chunk's three 16-byte quant columns, then lanes 0-15 row n's 16 scale bytes of the
+// superblock and lanes 16-31 the 16 bytes holding its d. Rows past R repeat row R - 1.
+IEK_DEV void issue_item2(const View2& v, int i, uint32_t slot, int lane) {
+  int sb, t;
+  item2_of(v, i, sb, t);
+  const int g = lane >> 4;
+  const uint8_t* row = view2_row(v, min(16 * t + (lane & 15), v.R - 1));
+  if (v.dt == DT_Q4K) {
+    const uint8_t* blk = row + (size_t)sb * Q4K_BYTES;
+    dma16(slot, blk + 16 + 32 * g);
+    dma16(slot + 1024, blk + 32 + 32 * g);
+    dma16(slot + 2048, blk);
+    if (lane == 0) dma16(slot + 3072, blk);  // padding copy
+  } else {
+    const uint8_t* m = row + (size_t)sb * 192 + 48 * g;
+    dma16(slot, m);
+    dma16(slot + 1024, m + 16);
+    dma16(slot + 2048, m + 32);
+    if (lane < 32) {
+      const uint8_t* rn = view2_row(v, min(16 * t + (lane & 15), v.R - 1));
+      const size_t off = lane < 16 ? (size_t)v.nsb * 192 + 16 * (size_t)sb
+                                   : (size_t)v.nsb * 208 + ((2 * (size_t)sb) & ~(size_t)15);
+      dma16(slot + 3072, rn + off);  // lane l lands at slot + 3072 + 16 l
+    }
+  }
+}
+
+IEK_DEV float q6_item2(const uint8_t* slot, int lane, int sb, const float (&x)[64], const float (&xq)[4]) {
+  const uint4 qa = *reinterpret_cast<const uint4*>(slot + 16 * lane);
+  const uint4 qb = *reinterpret_cast<const uint4*>(slot + 1024 + 16 * lane);
+  const uint4 qh = *reinterpret_cast<const uint4*>(slot + 2048 + 16 * lane);
+  const int n = lane & 15, k = lane >> 4;
+  const uint32_t scw = *reinterpret_cast<const uint32_t*>(slot + 3072 + 16 * n + 4 * k);
+  const float d =
+      half_bits_to_float(*reinterpret_cast<const uint16_t*>(slot + 3072 + 256 + 16 * n + ((2 * sb) & 15)));
+  return q6_core(qa, qb, qh, scw, d, x, xq);
+}
+
+// Items [i0, i1) of consumer c among n (contiguous, sb-major).
+IEK_DEV void range2(int n, int c, int& i0, int& i1) {
+  i0 = (n * c) / NC2;
+  i1 = (n * (c + 1)) / NC2;
+}
+
+// Whether consumer c wrote tile t of a phase (its range covers the tile at least once).
+IEK_DEV bool covers2(int n, int T, int c, int t) {
+  int i0, i1;
+  range2(n, c, i0, i1);
+  const int cnt = i1 - i0;
+  if (cnt <= 0) return false;
+  if (cnt >= T) return true;
+  return (t - i0 % T + T) % T < cnt;
+}
+
+// ---- control wave ------------------------------------------------------------------------------
+IEK_DEV void control2(const ChainArgs& a, Smem2& S, int pos) {
+  const int lane = threadIdx.x & 63, b = blockIdx.x, G = gridDim.x;
+  const CPhase phases = (CPhase)a.phases;
+  for (int ph = 0; ph < a.nphase; ++ph) {
+    const CPhase P = phases + ph;
+    const View2 v = load_view2(P, b, G);
+    const int dt = P->dt, K = P->K, nsb = v.nsb;
+    const int u0 = v.u0, npair = v.R / 2;
+    // epilogue inputs that do not depend on this phase's x: the residual pair or RoPE (cos, sin)
+    // for lane = pair
+    float2 pre = make_float2(0.f, 0.f);
+    if (lane < npair) {
+      const int u = u0 + lane;
+      if (P->epi == CE_RESID) {
+        pre = make_float2(ld_coh(P->resid + 2 * u), ld_coh(P->resid + 2 * u + 1));
+      } else if (P->epi == CE_QKV && P->role0 == 0) {
+        const int n0 = P->seg[0].n, n1 = P->seg[1].n, g0 = 2 * u;
+        const int row = g0 - (g0 >= n0 + n1 ? n0 + n1 : (g0 >= n0 ? n0 : 0));
+        const int d = row % P->head_dim;
+        if (d < 2 * P->npairs) pre = reinterpret_cast<const float2*>(P->rope_cs)[(size_t)pos * P->npairs + d / 2];
+      }
+    }
+    // the norm weight: lane l of superblock sb's copy is (i4 = l >> 2, chunk l & 3)
+    const int lc = lane & 3, li4 = lane >> 2;
+    if (P->norm_w)
+      for (int sb = 0; sb < nsb; ++sb)
+        dma16(lds_addr(&S.xs[K / 4 + sb * 64]), P->norm_w + x_elem(dt, 4 * sb + lc, 4 * li4));
+    // ---- stage x, superblock by superblock
+    if (P->x_mode == CX_EMBED_Q4K) {
+      // dequantise row *tok of the Q4_K table (quant_k_handler.rs:38-82, q == 0 -> product 0);
+      // the host checks the ids it is given, and one the previous step produced is clamped
+      typedef const __attribute__((address_space(4))) uint32_t* CU32;
+      const uint32_t tok = min(*(CU32)a.tok, (uint32_t)P->emb_rows - 1u);
+      for (int sb = 0; sb < nsb; ++sb) {
+        const int ch = 4 * sb + lc;
+        const uint8_t* blk = P->emb + ((size_t)tok * K + 64 * (size_t)ch) / QK_K * Q4K_BYTES;
+        const float d = half_bits_to_float(load_u16(blk)), dmin = half_bits_to_float(load_u16(blk + 2));
+        const uint4 hdr = *reinterpret_cast<const uint4*>(blk);
+        float sc0, m0, sc1, m1;
+        scale_min_k4_sel(2 * lc, hdr.y, hdr.z, hdr.w, &sc0, &m0);
+        scale_min_k4_sel(2 * lc + 1, hdr.y, hdr.z, hdr.w, &sc1, &m1);
+        const uint8_t* qs = blk + 16 + 32 * lc;
+        float vv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * li4 + e;
+          const uint32_t byte = qs[i & 31];
+          vv[e] = i < 32 ? q4k_value(d, dmin, sc0, m0, byte & 0xFu) : q4k_value(d, dmin, sc1, m1, byte >> 4);
+        }
+        const float4 f = make_float4(vv[0], vv[1], vv[2], vv[3]);
+        S.xs[sb * 64 + lane] = f;
+        if (b == 0) *reinterpret_cast<float4*>(P->emb_out + 64 * ch + 4 * li4) = f;
+      }
+      vm_wait<0>();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      if (lane < nsb) lds_st(&S.xflag[lane], ph + 1);
+    } else {
+      // lane = superblock: poll its counter; every ready superblock is staged with one
+      // device-coherent copy (x was written by other workgroups in this launch) and flagged
+      bool staged = lane >= nsb;
+      const unsigned need = lane < nsb ? (unsigned)P->expect[lane] : 0u;
+      unsigned it = 0;
+      while (true) {
+        bool ready = false;
+        if (!staged) ready = P->x_src < 0 || g_ld(cnt2(a, P->x_src, lane)) >= need;
+        unsigned long long m = __ballot(ready);
+        if (m) {
+          unsigned long long mm = m;
+          while (mm) {
+            const int sb = __builtin_ctzll(mm);
+            mm &= mm - 1;
+            dma16_coh(lds_addr(&S.xs[sb * 64]), P->x + x_elem(dt, 4 * sb + lc, 4 * li4));
+          }
+          vm_wait<0>();
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+          if (ready) lds_st(&S.xflag[lane], ph + 1);
+          staged = staged || ready;
+        }
+        if (__ballot(!staged) == 0ull) break;
+        if (!m) {
+          __builtin_amdgcn_s_sleep(1);
+          if (++it > S.spin || lds_ld(&S.abort_)) {
+            set_abort2(S, a.err, 1);
+            break;
+          }
+        }
+      }
+      if (lds_ld(&S.abort_)) {
+        vm_wait<0>();
+        return;
+      }
+    }
+    vm_wait<0>();  // the norm weight copies (the embedding path issues none after its wait)
+    float rms = 1.f;
+    if (P->norm_w) {
+      // rms = sqrt(sum(x^2) / K + eps) (src/ops/rmsnorm.rs:44-45) over the staged superblocks
+      float ss = 0.f;
+      for (int sb = 0; sb < nsb; ++sb) {
+        const float4 q = S.xs[sb * 64 + lane];
+        ss += (q.x * q.x + q.y * q.y) + (q.z * q.z + q.w * q.w);
+      }
+      rms = rms_of(wave_sum(ss), K, P->eps);
+    }
+    // ---- wait for the consumers' partial dots
+    unsigned it = 0;
+    while (lds_ld(&S.done[ph]) < NC2) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++it > S.spin || lds_ld(&S.abort_)) {
+        set_abort2(S, a.err, 2);
+        break;
+      }
+    }
+    if (lds_ld(&S.abort_)) {
+      vm_wait<0>();
+      return;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // ---- epilogue: lane = row pair; each row's dot is the sum of the consumers' tile partials
+    unsigned long long run_key = 0;
+    for (int lu = lane; lu < npair; lu += 64) {
+      float vv[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int l = 2 * lu + r, t = l >> 4, n = l & 15;
+        float s = 0.f;
+        for (int c = 0; c < NC2; ++c)
+          if (covers2(v.n_items, v.T, c, t)) s += S.part[t][c][n];
+        vv[r] = P->norm_w ? s / rms : s;
+      }
+      const int u = u0 + lu;
+      if (P->epi == CE_SWIGLU) {
+        st_coh(P->seg[0].out + u, silu_mul(vv[0], vv[1]));
+        continue;
+      }
+      const int n0 = P->seg[0].n, n1 = P->seg[1].n;
+      const int g0 = 2 * u, si = g0 >= n0 + n1 ? 2 : (g0 >= n0 ? 1 : 0);
+      const int row = g0 - (si == 2 ? n0 + n1 : (si == 1 ? n0 : 0));
+      float* out = si == 0 ? P->seg[0].out : (si == 1 ? P->seg[1].out : P->seg[2].out);
+      const int s = P->epi == CE_QKV ? si + P->role0 : si;  // Q, K or V
+      if (P->epi == CE_RESID) {
+        const float2 r = lu == lane ? pre : make_float2(ld_coh(P->resid + row), ld_coh(P->resid + row + 1));
+        st_coh(out + row, r.x + vv[0]);
+        st_coh(out + row + 1, r.y + vv[1]);
+      } else if (P->epi == CE_QKV) {
+        const int hd = P->head_dim, d = row % hd;
+        float o0 = vv[0], o1 = vv[1];
+        if (s < 2 && d < 2 * P->npairs) {
+          const float2 cs = lu == lane ? pre : reinterpret_cast<const float2*>(P->rope_cs)[(size_t)pos * P->npairs + d / 2];
+          o0 = rope_rotate(vv[0], vv[1], cs.x, cs.y, true);
+          o1 = rope_rotate(vv[1], vv[0], cs.x, cs.y, false);
+        }
+        if (s == 0) {
+          st_coh(out + row, o0);
+          st_coh(out + row + 1, o1);
+        } else {
+          float* c = s == 1 ? P->kc : P->vc;
+          const size_t dst = ((size_t)(row / hd) * P->ctx + pos) * hd + d;
+          const float2 f2 = make_float2(o0, o1);
+          __hip_atomic_store(reinterpret_cast<unsigned long long*>(c + dst), __builtin_bit_cast(unsigned long long, f2),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      } else if (P->epi == CE_ARGMAX) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          float z = vv[r];
+          if (P->softcap > 0.f) z = soft_cap(z, P->softcap);
+          out[row + r] = z;
+          const unsigned long long key = argmax_key_dev(z, (uint32_t)(row + r));
+          run_key = key > run_key ? key : run_key;
+          if (!isfinite(z)) atomicOr(a.amax_flag, 1);
+        }
+      } else {
+        st_coh(out + row, vv[0]);
+        st_coh(out + row + 1, vv[1]);
+      }
+    }
+    if (P->epi == CE_ARGMAX) {
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long o = __shfl_xor(run_key, off, WAVE);
+        run_key = o > run_key ? o : run_key;
+      }
+      if (lane == 0 && run_key) atomicMax(a.amax_key, run_key);
+    }
+    // ---- arrive: the stores are complete, then one count on each superblock of the next
+    // phases' x that this workgroup's outputs touch
+    vm_wait<0>();
+    if (P->arrive && npair > 0) {
+      const int lo = P->epi == CE_SWIGLU ? u0 : 2 * u0, hi = P->epi == CE_SWIGLU ? u0 + npair : 2 * (u0 + npair);
+      const int sb0 = lo / QK_K, sb1 = (hi - 1) / QK_K;
+      if (lane <= sb1 - sb0)
+        __hip_atomic_fetch_add(cnt2(a, ph, sb0 + lane), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// ---- consumer waves ----------------------------------------------------------------------------
+struct Cursor2 {
+  View2 v;
+  int ph, i, i1;
+};
+
+// The first item of phase ph or later (i1 = the end of this consumer's range in that phase).
+IEK_DEV Cursor2 cursor2_at(CPhase phases, int nphase, int b, int G, int c, int ph) {
+  Cursor2 q;
+  q.ph = ph;
+  while (true) {
+    q.v = load_view2(phases + q.ph, b, G);
+    range2(q.v.n_items, c, q.i, q.i1);
+    if (q.i < q.i1 || q.ph == nphase - 1) return q;
+    ++q.ph;
+  }
+}
+
+// Next item; at the consumer's last item the cursor stays there (the same item's copies are
+// issued again, keeping the number of copies in flight constant).
+IEK_DEV Cursor2 cursor2_next(Cursor2 q, CPhase phases, int nphase, int b, int G, int c) {
+  if (q.i + 1 < q.i1) {
+    ++q.i;
+    return q;
+  }
+  int ph = q.ph + 1;
+  while (ph < nphase) {
+    const View2 v = load_view2(phases + ph, b, G);
+    int i0, i1;
+    range2(v.n_items, c, i0, i1);
+    if (i0 < i1) {
+      q.v = v;
+      q.ph = ph;
+      q.i = i0;
+      q.i1 = i1;
+      return q;
+    }
+    ++ph;
+  }
+  return q;
+}
+
+IEK_DEV void consumer2(const ChainArgs& a, Smem2& S, int c) {
+  const int lane = threadIdx.x & 63, b = blockIdx.x, G = gridDim.x;
+  const int g = lane >> 4;
+  const CPhase phases = (CPhase)a.phases;
+  const int nph = a.nphase;
+  Cursor2 dq = cursor2_at(phases, nph, b, G, c, 0);
+  const bool any = dq.i < dq.i1;
+  int nissued = 0;
+#define IEK_CHAIN2_ISSUE()                                                                                   \
+  do {                                                                                                       \
+    issue_item2(dq.v, dq.i, lds_addr(&S.ring[c * DSLOT2 + nissued % DSLOT2][0]), lane);                    \
+    ++nissued;                                                                                               \
+    dq = cursor2_next(dq, phases, nph, b, G, c);                                                             \
+  } while (0)
+  if (any)
+    for (int k = 0; k < DSLOT2; ++k) IEK_CHAIN2_ISSUE();
+  float x[64];
+  float xs_a = 0.f, xs_b = 0.f, xq[4] = {0.f, 0.f, 0.f, 0.f};
+  int k = 0;
+  for (int ph = 0; ph < nph; ++ph) {
+    const CPhase P = phases + ph;
+    const View2 cv = load_view2(P, b, G);
+    const bool norm = P->norm_w != nullptr;
+    const int K4 = P->K / 4;
+    int i0, i1;
+    range2(cv.n_items, c, i0, i1);
+    int cur = -1;
+    for (int i = i0; i < i1; ++i, ++k) {
+      int sb, t;
+      item2_of(cv, i, sb, t);
+      if (sb != cur) {
+        unsigned it = 0;
+        while (lds_ld(&S.xflag[sb]) != ph + 1) {
+          __builtin_amdgcn_s_sleep(1);
+          if (++it > S.spin || lds_ld(&S.abort_)) {
+            set_abort2(S, a.err, 3);
+            break;
+          }
+        }
+        if (lds_ld(&S.abort_)) {
+          vm_wait<0>();  // the copies in flight land before the wave ends
+          return;
+        }
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int i4 = 0; i4 < 16; ++i4) {
+          float4 q = S.xs[sb * 64 + 4 * i4 + g];
+          if (norm) {
+            const float4 w = S.xs[K4 + sb * 64 + 4 * i4 + g];
+            q = make_float4(mul_rn(q.x, w.x), mul_rn(q.y, w.y), mul_rn(q.z, w.z), mul_rn(q.w, w.w));
+          }
+          x[4 * i4] = q.x;
+          x[4 * i4 + 1] = q.y;
+          x[4 * i4 + 2] = q.z;
+          x[4 * i4 + 3] = q.w;
+        }
+        xs_a = xs_b = 0.f;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+          xs_a += x[e];
+          xs_b += x[32 + e];
+        }
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          float s4 = 0.f;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) s4 += x[16 * qd + e];
+          xq[qd] = s4;
+        }
+        cur = sb;
+      }
+      vm_wait<VM_PER_ITEM * (DSLOT2 - 1)>();  // this item's copies have landed
+      const uint8_t* slot = &S.ring[c * DSLOT2 + k % DSLOT2][0];
+      float vv = cv.dt == DT_Q4K ? q4_item(slot, lane, g, x, xs_a, xs_b) : q6_item2(slot, lane, sb, x, xq);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot's reads are done before its refill
+      IEK_CHAIN2_ISSUE();
+      vv += __shfl_xor(vv, 16, WAVE);
+      vv += __shfl_xor(vv, 32, WAVE);
+      if (lane < 16) {
+        // the first item of the range on a tile writes it, later ones add (items go sb-major)
+        float* pp = &S.part[t][c][lane];
+        *pp = i - i0 < cv.T ? vv : *pp + vv;
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (lane == 0) __hip_atomic_fetch_add(&S.done[ph], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  vm_wait<0>();
+#undef IEK_CHAIN2_ISSUE
+}
+
+__global__ __launch_bounds__(NT2) void chain2_kernel(ChainArgs args) {
+  __shared__ Smem2 S;
+  __shared__ int last;
+  (void)args;
+  const ChainArgs& a = *(const ChainArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (tid < CHAIN2_MAX_SB) S.xflag[tid] = 0;
+  if (tid < CHAIN_MAX_PHASES) S.done[tid] = 0;
+  if (tid == 0) {
+    S.abort_ = 0;
+    const unsigned lim = (unsigned)__hip_atomic_load(a.err + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    S.spin = lim ? lim : (1u << 22);  // ~0.1-0.2 s: each iteration sleeps ~64 clocks
+  }
+  __syncthreads();
+  typedef const __attribute__((address_space(4))) int* CInt;
+  const int pos = a.pos ? *(CInt)a.pos : 0;
+  if (wave == 0) control2(a, S, pos);
+  else consumer2(a, S, wave - 1);
+  __syncthreads();
+  // leave: the last workgroup publishes the argmax token, bumps the position and clears the counters
+  if (tid == 0) {
+    unsigned* exitc = a.counters + (size_t)CHAIN_MAX_PHASES * CHAIN2_MAX_SB * CHAIN2_CNT_STRIDE;
+    const unsigned old = __hip_atomic_fetch_add(exitc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = old == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  if (tid == 0) {
+    if (a.finish_argmax) {
+      const unsigned long long key = __hip_atomic_load(a.amax_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // every folded logit leaves a nonzero key; none (the launch gave its waits up before the LM
+      // head) flags the step, and the published id stays a valid one for the next step's lookup
+      const uint32_t idx = key ? 0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull) : 0u;
+      a.out_tok[0] = idx;
+      const int i = a.step ? *a.step : 0;
+      a.flags[i] = key ? __hip_atomic_load(a.amax_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1;
+      if (a.step) {
+        a.gen[i] = idx;
+        *a.step = i + 1;
+      }
+      *a.amax_key = 0ull;
+      *a.amax_flag = 0;
+    }
+    if (a.pos_inc) *a.pos_inc += 1;
+  }
+  for (int w = tid; w <= CHAIN_MAX_PHASES * CHAIN2_MAX_SB; w += NT2)
+    __hip_atomic_store(a.counters + (size_t)w * CHAIN2_CNT_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace
 
 size_t chain_row_bytes(int dt, int K) {
@@ -711,6 +1236,29 @@ void launch_chain(const ChainArgs& a, hipStream_t st) {
   }
   if (!ok) fail(ST_OP, "chain: the kernel does not fit on a compute unit");
   hipLaunchKernelGGL(chain_kernel, dim3(num_cus()), dim3(NT), 0, st, a);
+}
+
+}  // namespace iek
+
+namespace iek {
+
+bool chain2_phase_ok(int dt, int K, bool norm, int rows_per_wg) {
+  if (dt != DT_Q4K && dt != DT_Q6K_R) return false;
+  if (K <= 0 || K % QK_K != 0 || K / QK_K > CHAIN2_MAX_SB) return false;
+  if ((norm ? 2 * K : K) > CHAIN2_XS_FLOATS) return false;
+  return rows_per_wg <= 16 * CHAIN2_MAX_TILES;
+}
+
+void launch_chain2(const ChainArgs& a, hipStream_t st) {
+  if (a.nphase < 1 || a.nphase > CHAIN_MAX_PHASES) fail(ST_OP, "chain: 1..6 phases");
+  // one workgroup per CU: the workgroups wait on each other, so all of them must be resident
+  static int ok = -1;
+  if (ok < 0) {
+    int per_cu = 0;
+    ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, chain2_kernel, NT2, 0) == hipSuccess && per_cu >= 1;
+  }
+  if (!ok) fail(ST_OP, "chain: the kernel does not fit on a compute unit");
+  hipLaunchKernelGGL(chain2_kernel, dim3(num_cus()), dim3(NT2), 0, st, a);
 }
 
 }  // namespace iek

@@ -715,6 +715,41 @@ void Session::prepare_chain() {
     v.push_back(h);
     launches.push_back(v);
   }
+  // The tiled chain (launch_chain2): per phase, the phase whose output is its x, whether a later
+  // phase reads its output, and per superblock of x how many workgroups write part of it. It is
+  // taken unless IEK_CHAIN=1 asks for the row-item chain or a phase does not fit it.
+  const char* ev = getenv("IEK_CHAIN");
+  chain2_ = !(ev && ev[0] == '1');
+  auto out_range = [&](const ChainPhase& P, int b, int* lo, int* hi) {
+    const long long u0 = (long long)P.units * b / G, u1 = (long long)P.units * (b + 1) / G;
+    *lo = (int)(P.epi == CE_SWIGLU ? u0 : 2 * u0);
+    *hi = (int)(P.epi == CE_SWIGLU ? u1 : 2 * u1);
+  };
+  for (auto& v : launches) {
+    for (size_t i = 0; i < v.size(); ++i) {
+      ChainPhase& P = v[i];
+      P.x_src = -1;
+      P.arrive = 0;
+      if (P.wait_prev) P.x_src = (int)i - 1;
+      else if (i > 0 && P.epi == CE_QKV && P.role0 == 2) P.x_src = v[i - 1].x_src;  // the V-only phase
+      const int rows = 2 * ((P.units + G - 1) / G);
+      if (!chain2_phase_ok(P.dt, P.K, P.norm_w != nullptr, rows)) chain2_ = false;
+    }
+    for (size_t i = 0; i < v.size(); ++i) {
+      ChainPhase& P = v[i];
+      if (P.x_src < 0) continue;
+      v[P.x_src].arrive = 1;
+      const int nsb = P.K / 256;
+      for (int sb = 0; sb < nsb; ++sb) P.expect[sb] = 0;
+      for (int b = 0; b < G; ++b) {
+        int lo, hi;
+        out_range(v[P.x_src], b, &lo, &hi);
+        if (hi <= lo) continue;
+        if (hi > P.K) chain2_ = false;  // the producer's output is wider than this phase's x
+        for (int sb = lo / 256; sb <= (hi - 1) / 256 && sb < nsb; ++sb) ++P.expect[sb];
+      }
+    }
+  }
   size_t total = 0;
   for (auto& v : launches) total += v.size();
   std::vector<ChainPhase> host;
@@ -728,9 +763,9 @@ void Session::prepare_chain() {
     chain_np_.push_back((int)v.size());
     off += v.size();
   }
-  d_chain_cnt_ = dev_alloc<unsigned>(CHAIN_COUNTER_WORDS);
+  d_chain_cnt_ = dev_alloc<unsigned>(chain_counter_words());
   d_chain_err_ = dev_alloc<int>(2);  // [error code, bounded-wait limit (0: default)]
-  launch_fill_i32((int*)d_chain_cnt_, 0, CHAIN_COUNTER_WORDS, st_);
+  launch_fill_i32((int*)d_chain_cnt_, 0, chain_counter_words(), st_);
   launch_fill_i32(d_chain_err_, 0, 2, st_);
   chain_ = true;
 }
@@ -743,7 +778,7 @@ void Session::check_chain_error() {
   IEK_HIP(hipMemcpyAsync(&err, d_chain_err_, 4, hipMemcpyDeviceToHost, st_));
   sync();
   if (err) {
-    launch_fill_i32((int*)d_chain_cnt_, 0, CHAIN_COUNTER_WORDS, st_);
+    launch_fill_i32((int*)d_chain_cnt_, 0, chain_counter_words(), st_);
     launch_fill_i32(d_chain_err_, 0, 1, st_);
     sync();
     fail(ST_DEVICE, "decode chain: a bounded wait ran out (code " + std::to_string(err) + ")");
@@ -1126,7 +1161,7 @@ double Session::bench_kernel(int which, int reps, double* work) {
       a.tok = d_tok_;
       a.counters = d_chain_cnt_;
       a.err = d_chain_err_;
-      launch_chain(a, st_);
+      chain2_ ? launch_chain2(a, st_) : launch_chain(a, st_);
     };
   } else if (which == 1) {
     if (gemma_ || !state_prefill_ || state_rows_ < 2) fail(ST_OP, "bench_kernel: needs a Mistral/Llama prefill state");
@@ -1364,7 +1399,7 @@ void Session::decode_body(bool head) {
           a.step = d_step_;
         }
       }
-      launch_chain(a, st_);
+      chain2_ ? launch_chain2(a, st_) : launch_chain(a, st_);
     }
     return;
   }

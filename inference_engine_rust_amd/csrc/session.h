@@ -4,6 +4,7 @@
 #include <vector>
 
 #include "model.h"
+#include "kernels/chain.h"
 #include "kernels/mv_args.h"
 
 namespace iek {
@@ -50,7 +51,7 @@ class Session {
   double bench_kernel(int which, int reps, double* work);
 
   int kv_len() const { return pos_; }
-  int decode_path() const { return chain_ ? 1 : 0; }
+  int decode_path() const { return chain_ ? (chain2_ ? 2 : 1) : 0; }
   // Iteration limit of the decode chain's bounded waits (0: the default). A test aid: a small
   // limit makes the next chain step give up its waits and fail with ST_DEVICE.
   void set_chain_spin(unsigned spin);
@@ -147,6 +148,8 @@ class Session {
   // layer's launch comes in two forms, without and with the LM head + argmax
   bool chain_ = false;
   bool chain_embed_ = false;  // launch 0 dequantises the token's embedding row itself
+  bool chain2_ = false;       // the tiled chain kernel (launch_chain2) rather than chain_kernel
+  static int chain_counter_words() { return std::max(CHAIN_COUNTER_WORDS, CHAIN2_COUNTER_WORDS); }
   void* chain_blob_ = nullptr;
   std::vector<const void*> chain_ph_;
   std::vector<int> chain_np_;

@@ -2,6 +2,7 @@
 // Restates the reference's CPU path function by function; each function cites the reference
 // file:line it follows (paths relative to the reference repository root).
 // Never linked by the product library. See oracle_core.h for the arithmetic rules.
+#include <immintrin.h>
 #include "oracle_core.h"
 
 #include <algorithm>
@@ -292,6 +293,19 @@ void matmul(const float* a, size_t m, size_t k, const Tensor& w, float* out, siz
   if (t != T_F32) {
     size_t need = expected_byte_len(t, k * n);
     if (w.buf.size() < need) fail(E_MATMUL, "weight buffer is smaller than expected");
+  }
+  if (mode == PAIR) {
+    if (m > 1) {
+      std::vector<float> r(m * k);
+      for (size_t i = 0; i < m * k; ++i) {
+        // f16 round to nearest even (F16C), as the device's conversion
+        const float h = _cvtsh_ss(_cvtss_sh(a[i], _MM_FROUND_TO_NEAREST_INT));
+        r[i] = h + _cvtsh_ss(_cvtss_sh(a[i] - h, _MM_FROUND_TO_NEAREST_INT));
+      }
+      matmul(r.data(), m, k, w, out, out_m, out_n, REASSOC, threads);
+      return;
+    }
+    mode = REASSOC;
   }
   size_t ops = m * n * k;
   if (mode == BASELINE) {

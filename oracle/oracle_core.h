@@ -176,7 +176,10 @@ struct State {
 // REASSOC: PARITY with every matmul dot product summed as two halves of K added at the end — a
 // legitimate f32 reassociation, used to measure how much the model's logits move under rounding
 // differences alone (the conditioning that bounds any reordered implementation).
-enum Mode : int { PARITY = 0, BASELINE = 1, REASSOC = 2 };
+// PAIR: REASSOC with every activation of a multi-row matmul (the prefill's) first rounded to its
+// fp16 (hi, lo) pair, hi = fp16(x), lo = fp16(x - hi): how far the device prefill's operand
+// rounding alone moves a model (test infrastructure only, like REASSOC).
+enum Mode : int { PARITY = 0, BASELINE = 1, REASSOC = 2, PAIR = 3 };
 
 struct Session {
   const Model* model = nullptr;

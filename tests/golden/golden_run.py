@@ -20,29 +20,33 @@ def step_record(lg: np.ndarray, tok: int) -> dict:
             "top_val": [float(l64[i]) for i in order[:8]], "norm": float(np.linalg.norm(l64))}
 
 
-def record(O, session, n_steps: int, log=None, shadow=None) -> list:
+def record(O, session, n_steps: int, log=None, shadows=None) -> list:
     """Steps 0..n_steps-1: step 0 is the prefill state; step i > 0 follows i decodes of the
-    oracle's greedy tokens. `shadow`, when given, is a second oracle session over the same model
-    and prompt in REASSOC mode (every f32 matmul summed as two halves of K: a legitimate reordering
-    of the reference's arithmetic); it decodes the same tokens, and each step also records how far
-    that reordering moves the logits: the relative L2 over the whole vector (reassoc_rel) and the
-    largest change among the 8 largest logits (reassoc_top_dmax)."""
+    oracle's greedy tokens. `shadows`, when given, maps a name to a second oracle session over the
+    same model and prompt in another arithmetic mode: "reassoc" (REASSOC: every f32 matmul summed
+    as two halves of K, a legitimate reordering of the reference's arithmetic) and "pair" (PAIR:
+    that, with every prefill matmul input first rounded to its fp16 (hi, lo) pair, the device
+    prefill's operands). Each decodes the same tokens, and each step records how far it moves the
+    logits: the relative L2 over the whole vector (<name>_rel) and the largest change among the 8
+    largest logits (<name>_top_dmax)."""
     steps = []
+    shadows = shadows or {}
     for i in range(n_steps):
         lg = session.logits()
         tok = O.argmax(lg)
         steps.append(step_record(lg, tok))
-        if shadow is not None:
-            ls = shadow.logits().astype(np.float64)
-            l64 = lg.astype(np.float64)
-            steps[-1]["reassoc_rel"] = float(np.linalg.norm(ls - l64) / np.linalg.norm(l64))
-            top = steps[-1]["top_idx"]
-            steps[-1]["reassoc_top_dmax"] = float(np.max(np.abs(ls[top] - l64[top])))
+        l64 = lg.astype(np.float64)
+        top = steps[-1]["top_idx"]
+        extra = ""
+        for name, sh in shadows.items():
+            ls = sh.logits().astype(np.float64)
+            steps[-1][f"{name}_rel"] = float(np.linalg.norm(ls - l64) / np.linalg.norm(l64))
+            steps[-1][f"{name}_top_dmax"] = float(np.max(np.abs(ls[top] - l64[top])))
+            extra += f" {name} {steps[-1][f'{name}_rel']:.3g}"
         if log:
-            extra = f" reassoc {steps[-1]['reassoc_rel']:.3g}" if shadow is not None else ""
             log(f"step {i}: token {tok} gap {steps[-1]['gap']:.4g}{extra}")
         if i + 1 < n_steps:
             session.decode(tok)
-            if shadow is not None:
-                shadow.decode(tok)
+            for sh in shadows.values():
+                sh.decode(tok)
     return steps

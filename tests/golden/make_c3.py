@@ -5,11 +5,12 @@ The full C3 model (synthetic GGUF ``c3``, seed 0: the Gemma-4-E2B-style preset a
 dimensions — 35 layers, d 1536, 20 KV-borrowing layers, per-layer embeddings of 256, Q8_0
 weights, a tied 262 144-row Q8_0 head with a soft cap of 30) and bench.py's prompt (256 uniform
 ids from seed 0): the prefill state and 32 decode states of the oracle's greedy run, with the
-figures ``golden_run.step_record`` keeps per step, and per step how far the oracle's own
-reassociated run (REASSOC mode) moves the logits. At this depth the model amplifies f32 rounding
-differences: reordering the reference's sums moves its logits by ~1e-2 relative L2, so the GPU test
-bounds the device's distance by the reordered oracle's (a 1e-3 bar would fail the reference's own
-arithmetic reordered).
+figures ``golden_run.step_record`` keeps per step, and per step how far two perturbed oracle runs
+move the logits: REASSOC (the reference's sums reordered) and PAIR (that, with the prefill matmul
+inputs rounded to fp16 (hi, lo) pairs as the device prefill takes them). At this depth the model
+amplifies rounding differences: reordering the reference's sums alone moves its logits by ~1e-2
+relative L2, so the GPU test bounds the device's distance by the perturbed oracles' (a 1e-3 bar
+would fail the reference's own arithmetic reordered).
 """
 import json
 import os
@@ -37,12 +38,13 @@ def main():
         spec = synth.preset("c3")
         synth.write_gemma4(p, spec, seed=0)
         om = O.Model(p)
-        s, shadow = O.Session(om), O.Session(om, mode=O.REASSOC)
+        s = O.Session(om)
+        shadows = {"reassoc": O.Session(om, mode=O.REASSOC), "pair": O.Session(om, mode=O.PAIR)}
         prompt = synth.prompt_ids(PROMPT_SEED, N_PROMPT, spec.vocab)
-        s.prefill(prompt)
-        shadow.prefill(prompt)
+        for x in [s, *shadows.values()]:
+            x.prefill(prompt)
         log("prefill done")
-        steps = record(O, s, N_STEPS, log, shadow=shadow)
+        steps = record(O, s, N_STEPS, log, shadows=shadows)
     out = {"config": "c3", "seed": 0, "prompt_seed": PROMPT_SEED, "n_prompt": N_PROMPT, "steps": steps}
     with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "c3_seed0.json"), "w") as f:
         json.dump(out, f)

@@ -167,13 +167,13 @@ def test_mistral_width_two_layers_parity(gpu, mid_path):
         s.decode_token(t)
         r.decode(t)
     assert worst < LOGIT_REL_L2, worst
-    assert s.decode_path() == 1, "the Mistral-width model should decode through the chain kernel"
+    assert s.decode_path() >= 1, "the Mistral-width model should decode through a chain kernel"
 
 
 def test_decode_path_selection(gpu, c0_path, mid_path):
     """The decode chain takes the Mistral-width model (K-quant widths multiple of 256); the tiny C0
     model (FFN 1408, blocks straddle rows) stays on the per-launch kernels."""
-    assert E.InferenceSession(E.LoadedModel.load(mid_path)).decode_path() == 1
+    assert E.InferenceSession(E.LoadedModel.load(mid_path)).decode_path() >= 1
     assert E.InferenceSession(E.LoadedModel.load(c0_path)).decode_path() == 0
 
 

@@ -47,8 +47,7 @@ def test_infinite_head_scale_fails_sampling_at_step_zero(gpu, tmp_path, kind):
     p = _model(tmp_path, kind)
     synth.patch_bytes(p, "output.weight", 208, F16_INF)  # Q6_K d of row 0's first superblock
     m, s, r = _sessions(p)
-    expect_path = 1 if kind == "chain" else 0
-    assert s.decode_path() == expect_path
+    assert (s.decode_path() >= 1) == (kind == "chain")
     prompt = synth.prompt_ids(3, N_PROMPT)
     s.prefill(prompt)
     r.prefill(prompt)
@@ -68,9 +67,12 @@ def test_nan_embedding_row_stops_the_loop_after_that_token(gpu, tmp_path, kind):
     p = _model(tmp_path, kind, seed=1)
     prompt = synth.prompt_ids(4, N_PROMPT)
     # the oracle's greedy tokens on the unpatched model; the planted token is the first one, from
-    # the third on, that is neither in the prompt nor generated before it
-    clean, _ = O.greedy_generate(O.Session(O.Model(p)), prompt, 12)
-    k = next(i for i in range(2, len(clean)) if clean[i] not in set(prompt.tolist()) | set(clean[:i]))
+    # the third on, that is neither in the prompt nor generated before it, taken where no earlier
+    # step is a near-tie (a device that sums in another order must reach the same token k)
+    clean, logs = O.greedy_generate(O.Session(O.Model(p)), prompt, 12, record_logits=True)
+    gaps = [float(np.diff(np.sort(lg.astype(np.float64))[-2:])[0]) for lg in logs]
+    ok = [i for i in range(2, len(clean)) if clean[i] not in set(prompt.tolist()) | set(clean[:i])]
+    k = next(i for i in ok if min(gaps[: i + 1]) >= 2e-2)
     hid = SPECS[kind].hidden
     synth.patch_bytes(p, "token_embd.weight", clean[k] * (hid // 256) * Q4K_BYTES, F16_NAN)
     m, s, r = _sessions(p)
@@ -103,7 +105,7 @@ def test_chain_bounded_wait_gives_up_cleanly(gpu, tmp_path):
     p = _model(tmp_path, "chain", seed=2)
     m = E.LoadedModel.load(p)
     s, fresh = E.InferenceSession(m), E.InferenceSession(m)
-    assert s.decode_path() == 1
+    assert s.decode_path() >= 1
     prompt = synth.prompt_ids(5, N_PROMPT)
     fresh.prefill(prompt)
     t0 = E.greedy_next_token(fresh)

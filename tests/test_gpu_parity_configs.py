@@ -63,7 +63,7 @@ def test_c2_widths_512_prompt_decode_past_520(gpu, big_dir):
     s.prefill(prompt)
     r.prefill(prompt)
     assert rel_l2(s.hidden(), r.hidden()) < 1e-4
-    assert s.decode_path() == 1
+    assert s.decode_path() >= 1
     worst = 0.0
     for step in range(12):  # kv_len 512 -> 524
         lg, lr = s.logits_last_token(), r.logits()
@@ -75,6 +75,46 @@ def test_c2_widths_512_prompt_decode_past_520(gpu, big_dir):
     assert s.kv_len() == 524
     assert worst < LOGIT_REL_L2, worst
     os.remove(p)
+
+
+@pytest.mark.parametrize("chain", ["1", "2"])
+def test_both_chain_kernels_match_oracle(gpu, big_dir, chain, monkeypatch):
+    """The row-item chain (IEK_CHAIN=1) and the tiled chain with per-superblock readiness (the
+    default) on C2's widths: decode logits within 1e-3 of the oracle, the same greedy tokens, the
+    K/V rows within the f32 reordering bound, and both kernels agree with each other."""
+    monkeypatch.setenv("IEK_CHAIN", chain)
+    p = os.path.join(big_dir, "c2_l2_chains.gguf")
+    if not os.path.exists(p):
+        synth.write_llama(p, synth.preset("c2_l2", mix=2), seed=8)
+    m, om = E.LoadedModel.load(p), O.Model(p)
+    prompt = synth.prompt_ids(12, 40)
+    s, r = E.InferenceSession(m), O.Session(om)
+    assert s.decode_path() == int(chain)
+    s.prefill(prompt)
+    r.prefill(prompt)
+    worst = 0.0
+    for step in range(10):
+        t = O.argmax(r.logits())
+        assert E.greedy_next_token(s) == t, f"step {step}"
+        s.decode_token(t)
+        r.decode(t)
+        worst = max(worst, rel_l2(s.logits_last_token(), r.logits()))
+    assert worst < LOGIT_REL_L2, worst
+    for layer in range(2):
+        kg = s.kv(layer, False)
+        kr = r.kv(layer, False).transpose(1, 0, 2)
+        np.testing.assert_allclose(kg, kr, rtol=1e-4, atol=1e-5 * np.abs(kr).max())
+    # graph replay == stepwise on this kernel
+    a, b = E.InferenceSession(m), E.InferenceSession(m)
+    a.prefill(prompt)
+    b.prefill(prompt)
+    ids = a.generate_greedy(5)
+    step_ids = []
+    for _ in range(5):
+        step_ids.append(E.greedy_next_token(b))
+        b.decode_token(step_ids[-1])
+    assert ids == step_ids
+    np.testing.assert_array_equal(a.logits_last_token(), b.logits_last_token())
 
 
 def test_c4_widths_8192_prompt_matches_golden(gpu, big_dir):
@@ -194,7 +234,7 @@ def test_full_c2_model_properties_and_golden(gpu, big_dir):
     m = _full_model_properties(p, 512, spec.vocab)
     g = json.load(open(os.path.join(GOLDEN, "c2_seed0.json")))
     s = E.InferenceSession(m)
-    assert s.decode_path() == 1
+    assert s.decode_path() >= 1
     s.prefill(synth.prompt_ids(g["prompt_seed"], g["n_prompt"], spec.vocab))
     _teacher_forced_golden(s, g)  # 33 states: the prefill's and 32 decodes'
     os.remove(p)
@@ -281,7 +321,7 @@ def test_q4_k_m_mixed_layers(gpu, big_dir):
     s, r = E.InferenceSession(m), O.Session(om)
     s.prefill(prompt)
     r.prefill(prompt)
-    assert s.decode_path() == 1
+    assert s.decode_path() >= 1
     worst = 0.0
     for step in range(8):
         lg, lr = s.logits_last_token(), r.logits()
