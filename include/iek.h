@@ -132,9 +132,9 @@ iek_status iek_session_generate_greedy(iek_session* s, size_t n_steps, uint32_t*
 iek_status iek_session_kv_len(const iek_session* s, uint64_t* out);
 /* Which decode implementation the session runs (no reference counterpart; a diagnostic): 0 = one
  * launch per matvec and attention, 1 = the decode chain (Q/K/V, O, gate/up and down as phases of
- * persistent launches, two launches per layer) with row items and phase barriers, 2 = the same
- * chain with 16-row tile items and per-superblock readiness (the default; IEK_CHAIN=1 in the
- * environment at session creation selects 1). All compute the same function. */
+ * persistent launches, two launches per layer) with row items and phase barriers (the default),
+ * 2 = the same chain with 16-row tile items and per-superblock readiness (IEK_CHAIN=2 in the
+ * environment at session creation selects it). All compute the same function. */
 iek_status iek_session_decode_path(const iek_session* s, int* out);
 /* No reference counterpart; a test aid for the decode chain's failure path. Sets the iteration
  * limit of the chain's bounded waits (each ~64 clocks; 0 restores the default, ~0.1-0.2 s). With a

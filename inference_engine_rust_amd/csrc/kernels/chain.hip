@@ -56,18 +56,24 @@ typedef const __attribute__((address_space(4))) ChainPhase* CPhase;
 // No memory clobber: the copy's LDS side is ordered by the explicit waits around it (vm_wait
 // before a slot is read, an lgkmcnt wait before a slot is refilled), and without the clobber the
 // compiler keeps the phase fields in scalar registers across copies.
+// The LDS offset is wave-uniform by construction; readfirstlane puts it in a scalar register even
+// where the compiler cannot prove that.
 IEK_DEV void dma16(uint32_t lds_off, const void* g) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_off), "v"(g));
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(__builtin_amdgcn_readfirstlane(lds_off)),
+               "v"(g));
 }
 // sc1: device-coherent (bypasses the non-coherent per-XCD L2 copy), for data other workgroups
 // wrote in this launch
 IEK_DEV void dma16_coh(uint32_t lds_off, const void* g) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off sc1" ::"s"(lds_off), "v"(g) : "memory");
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off sc1" ::"s"(__builtin_amdgcn_readfirstlane(lds_off)),
+               "v"(g)
+               : "memory");
 }
 // 4-byte copy per lane into LDS, used to touch one 128-byte line per lane so a later copy of the
 // item finds it in L2
 IEK_DEV void dma4(uint32_t lds_off, const void* g) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_off), "v"(g));
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(__builtin_amdgcn_readfirstlane(lds_off)),
+               "v"(g));
 }
 template <int N>
 IEK_DEV void vm_wait() {
@@ -770,9 +776,12 @@ IEK_DEV const uint8_t* view2_row(const View2& v, int l) {
   return reinterpret_cast<const uint8_t*>(b0 + in1 * (b1 - b0) + in2 * (b2 - b1) + (size_t)row * v.rb);
 }
 
+// Items go tile-major (every superblock of tile 0, then of tile 1, ...) and are dealt to the
+// consumers round-robin, so that a workgroup's copies in flight cover whole rows (contiguous
+// bytes) rather than one superblock of many rows.
 IEK_DEV void item2_of(const View2& v, int i, int& sb, int& t) {
-  sb = i / v.T;
-  t = i - sb * v.T;
+  t = i / v.nsb;
+  sb = i - t * v.nsb;
 }
 
 // COPIES_PER_ITEM copy instructions for item i (the consumer waits rely on the count). Q4_K: lane
@@ -815,20 +824,11 @@ IEK_DEV float q6_item2(const uint8_t* slot, int lane, int sb, const float (&x)[6
   return q6_core(qa, qb, qh, scw, d, x, xq);
 }
 
-// Items [i0, i1) of consumer c among n (contiguous, sb-major).
-IEK_DEV void range2(int n, int c, int& i0, int& i1) {
-  i0 = (n * c) / NC2;
-  i1 = (n * (c + 1)) / NC2;
-}
-
-// Whether consumer c wrote tile t of a phase (its range covers the tile at least once).
-IEK_DEV bool covers2(int n, int T, int c, int t) {
-  int i0, i1;
-  range2(n, c, i0, i1);
-  const int cnt = i1 - i0;
-  if (cnt <= 0) return false;
-  if (cnt >= T) return true;
-  return (t - i0 % T + T) % T < cnt;
+// Whether consumer c has an item in tile t (items c, c + NC2, ... of n, nsb per tile).
+IEK_DEV bool covers2(int n, int nsb, int c, int t) {
+  const int start = t * nsb, end = min(n, start + nsb);
+  const int first = start + ((c - start) % NC2 + NC2) % NC2;
+  return first < end;
 }
 
 // ---- control wave ------------------------------------------------------------------------------
@@ -958,7 +958,7 @@ IEK_DEV void control2(const ChainArgs& a, Smem2& S, int pos) {
         const int l = 2 * lu + r, t = l >> 4, n = l & 15;
         float s = 0.f;
         for (int c = 0; c < NC2; ++c)
-          if (covers2(v.n_items, v.T, c, t)) s += S.part[t][c][n];
+          if (covers2(v.n_items, v.nsb, c, t)) s += S.part[t][c][n];
         vv[r] = P->norm_w ? s / rms : s;
       }
       const int u = u0 + lu;
@@ -1031,17 +1031,17 @@ IEK_DEV void control2(const ChainArgs& a, Smem2& S, int pos) {
 // ---- consumer waves ----------------------------------------------------------------------------
 struct Cursor2 {
   View2 v;
-  int ph, i, i1;
+  int ph, i;
 };
 
-// The first item of phase ph or later (i1 = the end of this consumer's range in that phase).
+// The first item of phase ph or later (consumer c's items are c, c + NC2, ... of each phase).
 IEK_DEV Cursor2 cursor2_at(CPhase phases, int nphase, int b, int G, int c, int ph) {
   Cursor2 q;
   q.ph = ph;
+  q.i = c;
   while (true) {
     q.v = load_view2(phases + q.ph, b, G);
-    range2(q.v.n_items, c, q.i, q.i1);
-    if (q.i < q.i1 || q.ph == nphase - 1) return q;
+    if (c < q.v.n_items || q.ph == nphase - 1) return q;
     ++q.ph;
   }
 }
@@ -1049,20 +1049,17 @@ IEK_DEV Cursor2 cursor2_at(CPhase phases, int nphase, int b, int G, int c, int p
 // Next item; at the consumer's last item the cursor stays there (the same item's copies are
 // issued again, keeping the number of copies in flight constant).
 IEK_DEV Cursor2 cursor2_next(Cursor2 q, CPhase phases, int nphase, int b, int G, int c) {
-  if (q.i + 1 < q.i1) {
-    ++q.i;
+  if (q.i + NC2 < q.v.n_items) {
+    q.i += NC2;
     return q;
   }
   int ph = q.ph + 1;
   while (ph < nphase) {
     const View2 v = load_view2(phases + ph, b, G);
-    int i0, i1;
-    range2(v.n_items, c, i0, i1);
-    if (i0 < i1) {
+    if (c < v.n_items) {
       q.v = v;
       q.ph = ph;
-      q.i = i0;
-      q.i1 = i1;
+      q.i = c;
       return q;
     }
     ++ph;
@@ -1076,7 +1073,7 @@ IEK_DEV void consumer2(const ChainArgs& a, Smem2& S, int c) {
   const CPhase phases = (CPhase)a.phases;
   const int nph = a.nphase;
   Cursor2 dq = cursor2_at(phases, nph, b, G, c, 0);
-  const bool any = dq.i < dq.i1;
+  const bool any = c < dq.v.n_items;
   int nissued = 0;
 #define IEK_CHAIN2_ISSUE()                                                                                   \
   do {                                                                                                       \
@@ -1094,10 +1091,8 @@ IEK_DEV void consumer2(const ChainArgs& a, Smem2& S, int c) {
     const View2 cv = load_view2(P, b, G);
     const bool norm = P->norm_w != nullptr;
     const int K4 = P->K / 4;
-    int i0, i1;
-    range2(cv.n_items, c, i0, i1);
     int cur = -1;
-    for (int i = i0; i < i1; ++i, ++k) {
+    for (int i = c; i < cv.n_items; i += NC2, ++k) {
       int sb, t;
       item2_of(cv, i, sb, t);
       if (sb != cur) {
@@ -1149,9 +1144,9 @@ IEK_DEV void consumer2(const ChainArgs& a, Smem2& S, int c) {
       vv += __shfl_xor(vv, 16, WAVE);
       vv += __shfl_xor(vv, 32, WAVE);
       if (lane < 16) {
-        // the first item of the range on a tile writes it, later ones add (items go sb-major)
+        // this consumer's first item of a tile writes its partial, later ones add
         float* pp = &S.part[t][c][lane];
-        *pp = i - i0 < cv.T ? vv : *pp + vv;
+        *pp = i - NC2 < t * cv.nsb ? vv : *pp + vv;
       }
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");

@@ -168,17 +168,6 @@ def gemma4_e2b_assistant_visible(s: str) -> str:
     return t.rstrip()
 
 
-class ChatRole(Enum):
-    USER = "user"
-    ASSISTANT = "assistant"
-
-
-@dataclass
-class ChatMessage:
-    role: ChatRole
-    content: str
-
-
 class ChatPromptStyle(Enum):
     """ChatPromptStyle (chat_prompt.rs:137-200)."""
     RAW = "raw"
@@ -204,32 +193,6 @@ class ChatPromptStyle(Enum):
         if self is ChatPromptStyle.MISTRAL_INSTRUCT:
             return f"[INST] {user} [/INST]"
         return f"<|turn>user\n{user}<turn|>\n<|turn>model\n"
-
-    def render_conversation(self, messages: list[ChatMessage]) -> str:
-        """Multi-turn transcript ending with a user turn (chat_prompt.rs:178-243); ValueError
-        with the reference's message when the transcript is not valid."""
-        if self is ChatPromptStyle.RAW:
-            raise ValueError("raw prompt style does not support chat transcripts")
-        if not messages:
-            raise ValueError("conversation is empty")
-        if messages[0].role is not ChatRole.USER:
-            raise ValueError("conversation must start with a user message")
-        if messages[-1].role is not ChatRole.USER:
-            raise ValueError("conversation must end with a user message (assistant reply not generated yet)")
-        if any(a.role is b.role for a, b in zip(messages, messages[1:])):
-            raise ValueError("user and assistant turns must alternate")
-        out = []
-        if self is ChatPromptStyle.MISTRAL_INSTRUCT:
-            for m in messages:
-                out.append(f" [INST] {m.content.strip()} [/INST]" if m.role is ChatRole.USER else f" {m.content}")
-            return "".join(out)
-        for m in messages:
-            if m.role is ChatRole.USER:
-                out.append(f"<|turn>user\n{m.content.strip()}<turn|>\n")
-            else:
-                out.append(f"<|turn>model\n{m.content.rstrip()}<turn|>\n")
-        out.append("<|turn>model\n")
-        return "".join(out)
 
 
 # ---- generation (src/main.rs:84-126) -------------------------------------------------------------

@@ -44,14 +44,6 @@ def test_chat_prompt_reference_cases():
     s = F.ChatPromptStyle.GEMMA4_E2B.wrap("Hello")
     assert s.startswith("<|turn>user\n") and "Hello" in s and "<turn|>\n" in s and s.endswith("<|turn>model\n")
     assert F.ChatPromptStyle.MISTRAL_INSTRUCT.wrap("Hi") == "[INST] Hi [/INST]"
-    U, A = F.ChatRole.USER, F.ChatRole.ASSISTANT
-    g = F.ChatPromptStyle.GEMMA4_E2B.render_conversation(
-        [F.ChatMessage(U, "Hi"), F.ChatMessage(A, "Hello."), F.ChatMessage(U, "Bye")])
-    assert "<|turn>user\nHi<turn|>\n" in g and "<|turn>model\nHello.<turn|>\n" in g
-    assert "<|turn>user\nBye<turn|>\n" in g and g.endswith("<|turn>model\n")
-    m = F.ChatPromptStyle.MISTRAL_INSTRUCT.render_conversation(
-        [F.ChatMessage(U, "Hi"), F.ChatMessage(A, "Hey."), F.ChatMessage(U, "Ok")])
-    assert "[INST] Hi [/INST]" in m and " Hey." in m and "[INST] Ok [/INST]" in m
     assert F.gemma4_e2b_truncate_assistant_at_structure("Hello.<turn|>junk") == "Hello."
     assert F.gemma4_e2b_truncate_assistant_at_structure("Ok.<|turn>user") == "Ok."
     assert F.gemma4_e2b_strip_dangling_contraction_tail("That's a very short message! I'") == \
@@ -70,15 +62,6 @@ def test_chat_prompt_parse_and_errors():
     assert F.ChatPromptStyle.parse("instruct") is F.ChatPromptStyle.MISTRAL_INSTRUCT
     assert F.ChatPromptStyle.parse("gemma-e2b") is F.ChatPromptStyle.GEMMA4_E2B
     assert F.ChatPromptStyle.parse("llama3") is None
-    U, A = F.ChatRole.USER, F.ChatRole.ASSISTANT
-    st = F.ChatPromptStyle.MISTRAL_INSTRUCT
-    for msgs, msg in (([], "empty"), ([F.ChatMessage(A, "x")], "start with a user"),
-                      ([F.ChatMessage(U, "a"), F.ChatMessage(A, "b")], "end with a user"),
-                      ([F.ChatMessage(U, "a"), F.ChatMessage(U, "b")], "alternate")):
-        with pytest.raises(ValueError, match=msg):
-            st.render_conversation(msgs)
-    with pytest.raises(ValueError, match="raw prompt style"):
-        F.ChatPromptStyle.RAW.render_conversation([F.ChatMessage(U, "a")])
     # markers inside a thinking block do not count; a marker after it does
     assert F.gemma4_e2b_assistant_visible("<|channel>x<turn|><channel|>ok") == "ok"
     assert F.gemma4_e2b_strip_dangling_contraction_tail("we're") == "we're"

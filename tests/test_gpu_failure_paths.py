@@ -65,14 +65,23 @@ def test_infinite_head_scale_fails_sampling_at_step_zero(gpu, tmp_path, kind):
 @pytest.mark.parametrize("kind", ["chain", "per_launch"])
 def test_nan_embedding_row_stops_the_loop_after_that_token(gpu, tmp_path, kind):
     p = _model(tmp_path, kind, seed=1)
-    prompt = synth.prompt_ids(4, N_PROMPT)
     # the oracle's greedy tokens on the unpatched model; the planted token is the first one, from
     # the third on, that is neither in the prompt nor generated before it, taken where no earlier
-    # step is a near-tie (a device that sums in another order must reach the same token k)
-    clean, logs = O.greedy_generate(O.Session(O.Model(p)), prompt, 12, record_logits=True)
-    gaps = [float(np.diff(np.sort(lg.astype(np.float64))[-2:])[0]) for lg in logs]
-    ok = [i for i in range(2, len(clean)) if clean[i] not in set(prompt.tolist()) | set(clean[:i])]
-    k = next(i for i in ok if min(gaps[: i + 1]) >= 2e-2)
+    # step is a near-tie (a device that sums in another order must reach the same token k); the
+    # first prompt seed that has such a step
+    om = O.Model(p)
+    for prompt_seed in range(4, 20):
+        prompt = synth.prompt_ids(prompt_seed, N_PROMPT)
+        clean, logs = O.greedy_generate(O.Session(om), prompt, 12, record_logits=True)
+        gaps = [float(np.diff(np.sort(lg.astype(np.float64))[-2:])[0]) for lg in logs]
+        ok = [i for i in range(2, len(clean)) if clean[i] not in set(prompt.tolist()) | set(clean[:i])]
+        ks = [i for i in ok if min(gaps[: i + 1]) >= 2e-2]
+        if ks:
+            k = ks[0]
+            break
+    else:
+        pytest.fail("no prompt seed in 4..19 has a step without an earlier near-tie")
+    del om
     hid = SPECS[kind].hidden
     synth.patch_bytes(p, "token_embd.weight", clean[k] * (hid // 256) * Q4K_BYTES, F16_NAN)
     m, s, r = _sessions(p)

@@ -79,8 +79,8 @@ def test_c2_widths_512_prompt_decode_past_520(gpu, big_dir):
 
 @pytest.mark.parametrize("chain", ["1", "2"])
 def test_both_chain_kernels_match_oracle(gpu, big_dir, chain, monkeypatch):
-    """The row-item chain (IEK_CHAIN=1) and the tiled chain with per-superblock readiness (the
-    default) on C2's widths: decode logits within 1e-3 of the oracle, the same greedy tokens, the
+    """The row-item chain (the default) and the tiled chain with per-superblock readiness
+    (IEK_CHAIN=2) on C2's widths: decode logits within 1e-3 of the oracle, the same greedy tokens, the
     K/V rows within the f32 reordering bound, and both kernels agree with each other."""
     monkeypatch.setenv("IEK_CHAIN", chain)
     p = os.path.join(big_dir, "c2_l2_chains.gguf")
@@ -194,12 +194,13 @@ def _teacher_forced_golden(s, g):
     one of the two), then the oracle's token is decoded, so that a near-tie cannot end the
     comparison.
 
-    Where the golden also holds the reassociated oracle's distances (the oracle with every f32
-    matmul summed as two halves of K: the reference's own arithmetic in another order), a model
-    that amplifies f32 rounding beyond 1e-3 gets bars scaled to them: logits within twice the
-    reordered oracle's relative L2, the 8 largest within twice its largest change there, and exact
-    tokens wherever the top-2 gap is at least four times that change. Returns the worst ratio of
-    the device's distance to the reordered oracle's (or the worst distance without them)."""
+    Where the golden also holds the perturbed oracles' distances (REASSOC: every f32 matmul summed
+    as two halves of K, the reference's own arithmetic in another order; PAIR: activations rounded
+    to the fp16 (hi, lo) pairs the device's prefill GEMMs take), a model that amplifies f32
+    rounding beyond 1e-3 gets bars scaled to the larger of the two: logits within twice that
+    relative L2, the 8 largest within twice its largest change there, and exact tokens wherever
+    the top-2 gap is at least four times that change. Returns the worst ratio of the device's
+    distance to the larger perturbed-oracle distance (or the worst distance without them)."""
     worst = 0.0
     for i, st in enumerate(g["steps"]):
         lg = s.logits_last_token()
@@ -207,10 +208,12 @@ def _teacher_forced_golden(s, g):
         rel = rel_l2(lg[: head.size], head)
         bar, gap_exact, atol = LOGIT_REL_L2, GAP_EXACT, 2e-3 * np.max(np.abs(head))
         if "reassoc_rel" in st:
-            bar = max(bar, 2.0 * st["reassoc_rel"])
-            gap_exact = max(gap_exact, 4.0 * st["reassoc_top_dmax"])
-            atol = max(atol, 2.0 * st["reassoc_top_dmax"])
-            worst = max(worst, rel / st["reassoc_rel"])
+            spread = max(st["reassoc_rel"], st.get("pair_rel", 0.0))
+            dmax = max(st["reassoc_top_dmax"], st.get("pair_top_dmax", 0.0))
+            bar = max(bar, 2.0 * spread)
+            gap_exact = max(gap_exact, 4.0 * dmax)
+            atol = max(atol, 2.0 * dmax)
+            worst = max(worst, rel / spread)
         else:
             worst = max(worst, rel)
         assert rel < bar, (i, rel, bar)
@@ -244,9 +247,9 @@ def test_full_c3_model_properties_and_golden(gpu, big_dir):
     """C3 at its own dimensions (the Gemma-4-E2B-style preset: 35 layers, d 1536, 20 KV-borrowing
     layers, per-layer embeddings of 256, Q8_0 projections and a tied 262 144-row Q8_0 head with a
     soft cap) against the committed oracle run tests/golden/c3_seed0.json (make_c3.py). At this
-    depth the random-weight model amplifies f32 rounding: the oracle reassociated moves its own
-    logits by 4e-3 .. 2e-2 relative L2 (recorded per step in the golden), so the bars follow that
-    measurement (_teacher_forced_golden)."""
+    depth the random-weight model amplifies f32 rounding: the oracle reassociated, or fed fp16
+    (hi, lo) activation pairs, moves its own logits by 4e-3 .. 2.5e-2 relative L2 (recorded per
+    step in the golden), so the bars follow that measurement (_teacher_forced_golden)."""
     spec = synth.preset("c3")
     p = os.path.join(big_dir, "c3.gguf")
     synth.write_gemma4(p, spec, seed=0)
@@ -261,7 +264,7 @@ def test_full_c3_model_properties_and_golden(gpu, big_dir):
     s = E.InferenceSession(m)
     s.prefill(synth.prompt_ids(g["prompt_seed"], g["n_prompt"], spec.vocab))
     ratio = _teacher_forced_golden(s, g)
-    print(f"C3: worst device / reordered-oracle logit distance ratio {ratio:.3f}")
+    print(f"C3: worst device / perturbed-oracle logit distance ratio {ratio:.3f}")
     os.remove(p)
 
 
