@@ -415,52 +415,58 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(float* __restrict__ q, c
   }
 }
 
-// One 256-thread workgroup per (KV head, group of up to 4 query heads, query tile): wave w takes
-// query head w % G4 and query sub-tile w / G4 (G4 = min(G, 4)), TMQ 16-row MFMA tiles of it. Each
+// One workgroup of NW waves per (KV head, group of up to 4 query heads, query tile): wave w takes
+// query head w % G4 and query sub-tile w / G4 (G4 = min(G, 4)), TMQ 16-query MFMA tiles of it. Each
 // 64-key block of K and V^T is staged once in LDS (16-byte copies of the split planes, the next
 // block's loads in flight during the current block's MFMAs) and serves every query head of the
-// KV head. S = Q K^T and O += P V take three MFMAs per product (hi*hi + hi*lo + lo*hi, exact in
-// f32), with the online softmax of the per-head kernel above. The longest (latest) query tiles
-// are dispatched first.
-template <int HD, int TMQ>
-__global__ __launch_bounds__(256) void attn_prefill_gqa_kernel(const float* __restrict__ q,
-                                                               const _Float16* __restrict__ kh,
-                                                               const _Float16* __restrict__ kl,
-                                                               const _Float16* __restrict__ vh,
-                                                               const _Float16* __restrict__ vl, float* __restrict__ out,
-                                                               int M, int Mp, int n_heads, int n_kv, int window,
-                                                               float scale) {
+// KV head. The scores are computed transposed, S^T = K Q^T with the keys as MFMA rows: a lane's
+// 16 scores of a block then all belong to one query (lane & 15), and with the K rows staged in the
+// order krow() gives, the lane's keys of block steps 2t and 2t + 1 are exactly the 8 consecutive
+// keys 32t + 8(lane >> 4) .. + 7 that it supplies as the B operand of O^T += V^T P^T. P stays in
+// registers (no LDS round trip, no wave barrier), and 72 KB of LDS lets two workgroups share a
+// CU (NW = 4) or gives eight waves one staged block (NW = 8). Every product takes three MFMAs (hi*hi + hi*lo + lo*hi of the fp16 pairs, exact in f32);
+// the softmax is the online form per query. The longest (latest) query tiles are dispatched first.
+template <int HD, int TMQ, int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void attn_prefill_gqa_kernel(const float* __restrict__ q,
+                                                                  const _Float16* __restrict__ kh,
+                                                                  const _Float16* __restrict__ kl,
+                                                                  const _Float16* __restrict__ vh,
+                                                                  const _Float16* __restrict__ vl,
+                                                                  float* __restrict__ out, int M, int Mp, int n_heads,
+                                                                  int n_kv, int window, float scale) {
   constexpr int KB = 64;         // keys per block
-  constexpr int JN = KB / 16;    // 16-key column tiles of S
-  constexpr int KS = HD / 32;    // MFMA K steps of S
-  constexpr int NS = HD / 16;    // 16-wide head-dim tiles of O
+  constexpr int JN = KB / 16;    // 16-key row tiles of S^T
+  constexpr int KS = HD / 32;    // MFMA K steps of S^T
+  constexpr int NS = HD / 16;    // 16-wide head-dim row tiles of O^T
   constexpr int KROW = HD + 8;   // padded LDS rows (halves)
   constexpr int VROW = KB + 8;
   constexpr int QW = 16 * TMQ;   // queries per wave
-  constexpr int CPT = KB * HD / 8 / 256;  // 16-byte chunks per thread per plane of a K (or V^T) block
-  static_assert(CPT >= 1 && (KB * HD / 8) % 256 == 0, "block must divide over the threads");
+  constexpr int NT = 64 * NW;
+  constexpr int CPT = KB * HD / 8 / NT;  // 16-byte chunks per thread per plane of a K (or V^T) block
+  static_assert(CPT >= 1 && (KB * HD / 8) % NT == 0, "block must divide over the threads");
   __shared__ __align__(16) _Float16 ksh[KB][KROW];
   __shared__ __align__(16) _Float16 ksl[KB][KROW];
   __shared__ __align__(16) _Float16 vsh[HD][VROW];
   __shared__ __align__(16) _Float16 vsl[HD][VROW];
-  __shared__ __align__(16) _Float16 ph[4][16][VROW];
-  __shared__ __align__(16) _Float16 pl[4][16][VROW];
 
   const int G = n_heads / n_kv, G4 = min(G, 4), HG = (G + 3) / 4;
   const int kvh = blockIdx.x / HG, hg = blockIdx.x % HG;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = wave % G4, qs = wave / G4, h = 4 * hg + hl;
-  const bool active = h < G && qs < 4 / G4;
-  const int QT = QW * (4 / G4);
+  const bool active = h < G && qs < NW / G4;
+  const int QT = QW * (NW / G4);
   const int qt = gridDim.y - 1 - blockIdx.y;  // latest tiles first
   const int wq0 = qt * QT, wq1 = min(M - 1, wq0 + QT - 1);
   const int q0 = wq0 + qs * QW;
   const int hq = kvh * G + min(h, G - 1);
   const int qd = n_heads * HD;
-  const int fr = lane & 15, fk = 8 * (lane >> 4);
+  const int fr = lane & 15, lg = lane >> 4, fk = 8 * lg;
 
-  // Q fragments (A operand) of the wave's TMQ row tiles, split into fp16 pairs
+  // Q fragments (B operand of S^T: lane = query fr, dims fk .. fk + 7 of each 32-dim step) of the
+  // wave's TMQ query tiles, scaled by scale * log2(e) so that the scores come out in base-2 units
+  // (the softmax below is exp2(s - max), the same function), split into fp16 pairs
+  const float qscale = scale * 1.44269504088896341f;
   au4_t qah[TMQ][KS], qal[TMQ][KS];
 #pragma unroll
   for (int i = 0; i < TMQ; ++i) {
@@ -469,7 +475,8 @@ __global__ __launch_bounds__(256) void attn_prefill_gqa_kernel(const float* __re
     for (int s = 0; s < KS; ++s) {
       const float4 a = *reinterpret_cast<const float4*>(qrow + 32 * s + fk);
       const float4 b = *reinterpret_cast<const float4*>(qrow + 32 * s + fk + 4);
-      const float vv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      const float vv[8] = {a.x * qscale, a.y * qscale, a.z * qscale, a.w * qscale,
+                           b.x * qscale, b.y * qscale, b.z * qscale, b.w * qscale};
       _Float16 hh[8], ll[8];
 #pragma unroll
       for (int t = 0; t < 8; ++t) asplit(vv[t], hh[t], ll[t]);
@@ -477,29 +484,31 @@ __global__ __launch_bounds__(256) void attn_prefill_gqa_kernel(const float* __re
       qal[i][s] = au4_t{apack2(ll[0], ll[1]), apack2(ll[2], ll[3]), apack2(ll[4], ll[5]), apack2(ll[6], ll[7])};
     }
   }
+  // O^T accumulators (lane: query fr, dims 16j + 4lg .. + 3) and the lane's query's softmax state
+  // (running max in base-2 units, running sum)
   af4_t o[TMQ][NS];
-  float mrow[TMQ][4], lrow[TMQ][4];
+  float mrow[TMQ], lrow[TMQ];
 #pragma unroll
   for (int i = 0; i < TMQ; ++i) {
 #pragma unroll
     for (int j = 0; j < NS; ++j) o[i][j] = af4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      mrow[i][r] = -INFINITY;
-      lrow[i][r] = 0.f;
-    }
+    mrow[i] = -INFINITY;
+    lrow[i] = 0.f;
   }
 
-  // staged block: K rows [key][dim] and V^T rows [dim][key], both planes
+  // staged block: K rows [row][dim] in krow order and V^T rows [dim][key], both planes
   const _Float16* khp = kh + (size_t)kvh * M * HD;
   const _Float16* klp = kl + (size_t)kvh * M * HD;
   const _Float16* vhp = vh + (size_t)kvh * HD * Mp;
   const _Float16* vlp = vl + (size_t)kvh * HD * Mp;
+  // LDS row of key j of a block: key 32t + 8g + 4u + e goes to row 16(2t + u) + 4g + e, so that S^T
+  // row tile jn = 2t + u holds, in lane group g's four output rows, keys 32t + 8g + 4u .. + 3
+  auto krow = [](int j) { return (j & 32) + 16 * ((j >> 2) & 1) + 4 * ((j >> 3) & 3) + (j & 3); };
   au4_t rk[2][CPT], rv[2][CPT];
   auto fetch = [&](int kb0) {
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
-      const int e = tid + 256 * c;
+      const int e = tid + NT * c;
       const int j = e / (HD / 8), kc = e % (HD / 8);
       const size_t ks = (size_t)min(kb0 + j, M - 1) * HD + 8 * kc;
       rk[0][c] = *reinterpret_cast<const au4_t*>(khp + ks);
@@ -516,10 +525,10 @@ __global__ __launch_bounds__(256) void attn_prefill_gqa_kernel(const float* __re
     __syncthreads();  // the previous block's LDS reads are done
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
-      const int e = tid + 256 * c;
+      const int e = tid + NT * c;
       const int j = e / (HD / 8), kc = e % (HD / 8);
-      *reinterpret_cast<au4_t*>(&ksh[j][8 * kc]) = rk[0][c];
-      *reinterpret_cast<au4_t*>(&ksl[j][8 * kc]) = rk[1][c];
+      *reinterpret_cast<au4_t*>(&ksh[krow(j)][8 * kc]) = rk[0][c];
+      *reinterpret_cast<au4_t*>(&ksl[krow(j)][8 * kc]) = rk[1][c];
       const int d = e / (KB / 8), vc = e % (KB / 8);
       *reinterpret_cast<au4_t*>(&vsh[d][8 * vc]) = rv[0][c];
       *reinterpret_cast<au4_t*>(&vsl[d][8 * vc]) = rv[1][c];
@@ -528,85 +537,125 @@ __global__ __launch_bounds__(256) void attn_prefill_gqa_kernel(const float* __re
     if (kb0 + KB <= wq1) fetch(kb0 + KB);
     // the wave's queries all precede the block, or the block is older than all their windows
     if (!active || kb0 > q0 + QW - 1 || (window > 0 && kb0 + KB - 1 < q0 - (window - 1))) continue;
+    // query tiles that reach into the block (uniform); each K and V^T fragment is read from LDS
+    // once and serves all of them
+    bool live[TMQ];
+#pragma unroll
+    for (int i = 0; i < TMQ; ++i) live[i] = kb0 <= q0 + 16 * i + 15;
+    af4_t sacc[TMQ][JN];
+#pragma unroll
+    for (int i = 0; i < TMQ; ++i)
+#pragma unroll
+      for (int jn = 0; jn < JN; ++jn) sacc[i][jn] = af4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int jn = 0; jn < JN; ++jn)
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const au4_t ah = *reinterpret_cast<const au4_t*>(&ksh[16 * jn + fr][32 * s + fk]);
+        const au4_t al = *reinterpret_cast<const au4_t*>(&ksl[16 * jn + fr][32 * s + fk]);
+#pragma unroll
+        for (int i = 0; i < TMQ; ++i)
+          if (live[i]) sacc[i][jn] = mma3(ah, al, qah[i][s], qal[i][s], sacc[i][jn]);
+        // keeps the fragment loads next to their MFMAs (hoisted, they would not fit the registers)
+        if (TMQ > 1) __builtin_amdgcn_sched_barrier(0);
+      }
+    // per query tile: the online softmax of the lane's query, then P^T as the B operands of the two
+    // 32-key steps (fp16 pairs); sacc[i][jn][r] is key kb0 + 32(jn >> 1) + 8lg + 4(jn & 1) + r
+    au4_t pbh[TMQ][KB / 32], pbl[TMQ][KB / 32];
 #pragma unroll
     for (int i = 0; i < TMQ; ++i) {
-      const int qi0 = q0 + 16 * i;
-      if (kb0 > qi0 + 15) continue;  // uniform: this row tile precedes the block
-      af4_t sacc[JN];
-#pragma unroll
-      for (int jn = 0; jn < JN; ++jn) {
-        sacc[jn] = af4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          const au4_t bh = *reinterpret_cast<const au4_t*>(&ksh[16 * jn + fr][32 * s + fk]);
-          const au4_t bl = *reinterpret_cast<const au4_t*>(&ksl[16 * jn + fr][32 * s + fk]);
-          sacc[jn] = mma3(qah[i][s], qal[i][s], bh, bl, sacc[jn]);
-        }
-      }
+      if (!live[i]) continue;
+      const int qi0 = q0 + 16 * i, qi = qi0 + fr;
+      // every key of the block is visible to every query of the tile: no per-score mask
+      const bool interior = kb0 + KB - 1 <= qi0 && kb0 + KB <= M && (window <= 0 || kb0 >= qi0 + 16 - window);
       float p[JN][4];
+      float mx = -INFINITY;
+      if (interior) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int qi = qi0 + 4 * (lane >> 4) + r;
+        for (int jn = 0; jn < JN; ++jn)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            p[jn][r] = sacc[i][jn][r];
+            mx = fmaxf(mx, p[jn][r]);
+          }
+      } else {
         const int jlo = window > 0 ? max(0, qi - (window - 1)) : 0;
-        float mx = -INFINITY;
 #pragma unroll
-        for (int jn = 0; jn < JN; ++jn) {
-          const int j = kb0 + 16 * jn + fr;
-          const bool ok = j <= qi && j >= jlo && j < M && qi < M;
-          const float sv = sacc[jn][r] * scale;
-          p[jn][r] = ok ? sv : -INFINITY;
-          mx = fmaxf(mx, p[jn][r]);
-        }
-        mx = row16_max(mx);
-        const float mn = fmaxf(mrow[i][r], mx);
-        const float corr = mn == -INFINITY ? 1.f : expf(mrow[i][r] - mn);
-        float sum = 0.f;
+        for (int jn = 0; jn < JN; ++jn)
 #pragma unroll
-        for (int jn = 0; jn < JN; ++jn) {
-          const float e = p[jn][r] == -INFINITY ? 0.f : expf(p[jn][r] - mn);
-          p[jn][r] = e;
-          sum += e;
-        }
-        sum = row16_sum(sum);
-        lrow[i][r] = lrow[i][r] * corr + sum;
-        mrow[i][r] = mn;
-#pragma unroll
-        for (int j = 0; j < NS; ++j) o[i][j][r] *= corr;
+          for (int r = 0; r < 4; ++r) {
+            const int j = kb0 + 32 * (jn >> 1) + fk + 4 * (jn & 1) + r;
+            const bool ok = j <= qi && j >= jlo && j < M && qi < M;
+            p[jn][r] = ok ? sacc[i][jn][r] : -INFINITY;
+            mx = fmaxf(mx, p[jn][r]);
+          }
       }
-      // P to LDS in A-operand order [query][key] (this wave's 16 rows)
+      // lanes fr, fr + 16, fr + 32, fr + 48 hold the same query
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mn = fmaxf(mrow[i], mx);
+      float sum = 0.f;
+      if (mn == -INFINITY) {  // no visible key yet
 #pragma unroll
-      for (int jn = 0; jn < JN; ++jn)
+        for (int jn = 0; jn < JN; ++jn)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          asplit(p[jn][r], ph[wave][4 * (lane >> 4) + r][16 * jn + fr], pl[wave][4 * (lane >> 4) + r][16 * jn + fr]);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+          for (int r = 0; r < 4; ++r) p[jn][r] = 0.f;
+      } else {
 #pragma unroll
-      for (int ks = 0; ks < KB / 32; ++ks) {
-        const au4_t pah = *reinterpret_cast<const au4_t*>(&ph[wave][fr][32 * ks + fk]);
-        const au4_t pal = *reinterpret_cast<const au4_t*>(&pl[wave][fr][32 * ks + fk]);
+        for (int jn = 0; jn < JN; ++jn)
 #pragma unroll
-        for (int j = 0; j < NS; ++j) {
-          const au4_t bh = *reinterpret_cast<const au4_t*>(&vsh[16 * j + fr][32 * ks + fk]);
-          const au4_t bl = *reinterpret_cast<const au4_t*>(&vsl[16 * j + fr][32 * ks + fk]);
-          o[i][j] = mma3(pah, pal, bh, bl, o[i][j]);
-        }
+          for (int r = 0; r < 4; ++r) {
+            p[jn][r] = __builtin_amdgcn_exp2f(p[jn][r] - mn);  // exp2(-inf) = 0 for a hidden key
+            sum += p[jn][r];
+          }
       }
-      __builtin_amdgcn_wave_barrier();  // ph / pl are rewritten by the next row tile
+      sum += __shfl_xor(sum, 16);
+      sum += __shfl_xor(sum, 32);
+      // the running max grows in a few blocks only: rescale when some lane's did
+      if (__any(mn != mrow[i])) {
+        const float corr = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(mrow[i] - mn);
+        lrow[i] *= corr;
+#pragma unroll
+        for (int j = 0; j < NS; ++j) o[i][j] *= corr;
+      }
+      lrow[i] += sum;
+      mrow[i] = mn;
+#pragma unroll
+      for (int t = 0; t < KB / 32; ++t) {
+        _Float16 ph[8], pl[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) asplit(p[2 * t + (e >> 2)][e & 3], ph[e], pl[e]);
+        pbh[i][t] = au4_t{apack2(ph[0], ph[1]), apack2(ph[2], ph[3]), apack2(ph[4], ph[5]), apack2(ph[6], ph[7])};
+        pbl[i][t] = au4_t{apack2(pl[0], pl[1]), apack2(pl[2], pl[3]), apack2(pl[4], pl[5]), apack2(pl[6], pl[7])};
+      }
     }
+    // O^T += V^T P^T over the block's two 32-key steps; the B operand is the lane's own P
+#pragma unroll
+    for (int t = 0; t < KB / 32; ++t)
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        const au4_t ah = *reinterpret_cast<const au4_t*>(&vsh[16 * j + fr][32 * t + fk]);
+        const au4_t al = *reinterpret_cast<const au4_t*>(&vsl[16 * j + fr][32 * t + fk]);
+#pragma unroll
+        for (int i = 0; i < TMQ; ++i)
+          if (live[i]) o[i][j] = mma3(ah, al, pbh[i][t], pbl[i][t], o[i][j]);
+        if (TMQ > 1) __builtin_amdgcn_sched_barrier(0);
+      }
   }
   if (!active) return;
 #pragma unroll
-  for (int i = 0; i < TMQ; ++i)
+  for (int i = 0; i < TMQ; ++i) {
+    const int qi = q0 + 16 * i + fr;
+    if (qi < M) {
+      const float l = lrow[i];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int qi = q0 + 16 * i + 4 * (lane >> 4) + r;
-      if (qi < M) {
-#pragma unroll
-        for (int j = 0; j < NS; ++j) out[(size_t)qi * qd + (size_t)hq * HD + 16 * j + fr] = o[i][j][r] / lrow[i][r];
+      for (int j = 0; j < NS; ++j) {
+        const af4_t v = o[i][j];
+        *reinterpret_cast<float4*>(out + (size_t)qi * qd + (size_t)hq * HD + 16 * j + 4 * lg) =
+            make_float4(v[0] / l, v[1] / l, v[2] / l, v[3] / l);
       }
     }
+  }
 }
 
 // Prefill attention on f32 inputs (taken when a q, k or v value is beyond the fp16 pair's range):
@@ -729,22 +778,26 @@ void launch_attn_prefill(const float* q, const float* k, const float* v, float* 
       hipLaunchKernelGGL(kv_split_kernel, dim3(Mp / 64, (head_dim + 63) / 64, n_kv), dim3(256), 0, st, k, v, M, n_kv,
                          head_dim, Mp, kh, kl, vh, vl);
     const int G4 = std::min(G, 4), HG = (G + 3) / 4;
+    // eight waves of two query tiles each per staged block once the grid fills the machine twice
+    // over, four waves of one tile below that
+    const int qt8 = 32 * (8 / G4);
+    const bool wide = (size_t)n_kv * HG * ((M + qt8 - 1) / qt8) >= 2 * (size_t)num_cus();
+    const int QT = wide ? qt8 : 16 * (4 / G4);
+    const dim3 grid(n_kv * HG, (M + QT - 1) / QT);
     if (head_dim == 128) {
-      // two row tiles per wave once the grid fills the machine twice over, one below that
-      const int qt2 = 32 * (4 / G4);
-      if ((size_t)n_kv * HG * ((M + qt2 - 1) / qt2) >= 2 * (size_t)num_cus()) {
-        hipLaunchKernelGGL((attn_prefill_gqa_kernel<128, 2>), dim3(n_kv * HG, (M + qt2 - 1) / qt2), dim3(256), 0, st,
-                           q, kh, kl, vh, vl, out, M, Mp, n_heads, n_kv, window, scale);
-      } else {
-        const int qt1 = 16 * (4 / G4);
-        hipLaunchKernelGGL((attn_prefill_gqa_kernel<128, 1>), dim3(n_kv * HG, (M + qt1 - 1) / qt1), dim3(256), 0, st,
-                           q, kh, kl, vh, vl, out, M, Mp, n_heads, n_kv, window, scale);
-      }
+      if (wide)
+        hipLaunchKernelGGL((attn_prefill_gqa_kernel<128, 2, 8>), grid, dim3(512), 0, st, q, kh, kl, vh, vl, out, M, Mp,
+                           n_heads, n_kv, window, scale);
+      else
+        hipLaunchKernelGGL((attn_prefill_gqa_kernel<128, 1, 4>), grid, dim3(256), 0, st, q, kh, kl, vh, vl, out, M, Mp,
+                           n_heads, n_kv, window, scale);
     } else {
-      constexpr int TMQ = 4;
-      const int QT = 16 * TMQ * (4 / G4);
-      hipLaunchKernelGGL((attn_prefill_gqa_kernel<64, TMQ>), dim3(n_kv * HG, (M + QT - 1) / QT), dim3(256), 0, st, q,
-                         kh, kl, vh, vl, out, M, Mp, n_heads, n_kv, window, scale);
+      if (wide)
+        hipLaunchKernelGGL((attn_prefill_gqa_kernel<64, 2, 8>), grid, dim3(512), 0, st, q, kh, kl, vh, vl, out, M, Mp,
+                           n_heads, n_kv, window, scale);
+      else
+        hipLaunchKernelGGL((attn_prefill_gqa_kernel<64, 1, 4>), grid, dim3(256), 0, st, q, kh, kl, vh, vl, out, M, Mp,
+                           n_heads, n_kv, window, scale);
     }
     return;
   }

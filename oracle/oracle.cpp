@@ -294,14 +294,41 @@ void matmul(const float* a, size_t m, size_t k, const Tensor& w, float* out, siz
     size_t need = expected_byte_len(t, k * n);
     if (w.buf.size() < need) fail(E_MATMUL, "weight buffer is smaller than expected");
   }
-  if (mode == PAIR) {
+  if (mode == PAIR || mode == F16) {
     if (m > 1) {
       std::vector<float> r(m * k);
       for (size_t i = 0; i < m * k; ++i) {
         // f16 round to nearest even (F16C), as the device's conversion
         const float h = _cvtsh_ss(_cvtss_sh(a[i], _MM_FROUND_TO_NEAREST_INT));
-        r[i] = h + _cvtsh_ss(_cvtss_sh(a[i] - h, _MM_FROUND_TO_NEAREST_INT));
+        r[i] = mode == F16 ? h : h + _cvtsh_ss(_cvtss_sh(a[i] - h, _MM_FROUND_TO_NEAREST_INT));
       }
+      matmul(r.data(), m, k, w, out, out_m, out_n, REASSOC, threads);
+      return;
+    }
+    mode = REASSOC;
+  }
+  if (mode == I8X2_ROW || mode == I8X2_B32 || mode == I8X3_ROW) {
+    if (m > 1) {
+      const size_t blk = mode == I8X2_B32 ? 32 : k;
+      const int planes = mode == I8X3_ROW ? 3 : 2;
+      std::vector<float> r(m * k);
+      for (size_t row = 0; row < m; ++row)
+        for (size_t b0 = 0; b0 < k; b0 += blk) {
+          const size_t b1 = std::min(k, b0 + blk);
+          const float* x = a + row * k;
+          double mx = 0.0;
+          for (size_t i = b0; i < b1; ++i) mx = std::max(mx, std::fabs((double)x[i]));
+          for (size_t i = b0; i < b1; ++i) {
+            double sc = mx / 127.0, rem = x[i], y = 0.0;
+            for (int pl = 0; pl < planes && sc > 0.0; ++pl) {
+              const double q = std::max(-127.0, std::min(127.0, std::nearbyint(rem / sc)));
+              y += q * sc;
+              rem -= q * sc;
+              sc /= 254.0;
+            }
+            r[row * k + i] = (float)y;
+          }
+        }
       matmul(r.data(), m, k, w, out, out_m, out_n, REASSOC, threads);
       return;
     }

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(_HERE, "liboracle.so")
 
 T_F32, T_Q4K, T_Q6K, T_Q8_0 = 0, 1, 2, 3
 GGML_TO_ORC = {0: T_F32, 12: T_Q4K, 14: T_Q6K, 8: T_Q8_0}
-PARITY, BASELINE, REASSOC, PAIR = 0, 1, 2, 3
+PARITY, BASELINE, REASSOC, PAIR, F16, I8X2_ROW, I8X2_B32, I8X3_ROW = 0, 1, 2, 3, 4, 5, 6, 7
 
 _f = ctypes.c_void_p
 

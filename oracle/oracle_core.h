@@ -179,7 +179,13 @@ struct State {
 // PAIR: REASSOC with every activation of a multi-row matmul (the prefill's) first rounded to its
 // fp16 (hi, lo) pair, hi = fp16(x), lo = fp16(x - hi): how far the device prefill's operand
 // rounding alone moves a model (test infrastructure only, like REASSOC).
-enum Mode : int { PARITY = 0, BASELINE = 1, REASSOC = 2, PAIR = 3 };
+// F16: REASSOC with each such activation rounded to a single fp16 (the one-operand encoding).
+// I8X2_ROW, I8X2_B32, I8X3_ROW: REASSOC with each such activation replaced by its int8-plane
+// encoding x = s*(i1 + i2/254 [+ i3/254^2]), |i| <= 127 round to nearest, s = max|x| / 127 over
+// the row (ROW) or over each aligned block of 32 (B32): the operands of an int8 matrix-core GEMM
+// whose int32 dots are exact, so the encoding is the only rounding it adds. Measurement modes
+// for costing prefill formulations (test infrastructure only).
+enum Mode : int { PARITY = 0, BASELINE = 1, REASSOC = 2, PAIR = 3, F16 = 4, I8X2_ROW = 5, I8X2_B32 = 6, I8X3_ROW = 7 };
 
 struct Session {
   const Model* model = nullptr;
