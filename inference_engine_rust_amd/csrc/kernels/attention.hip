@@ -417,7 +417,7 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(float* __restrict__ q, c
 
 // One workgroup of NW waves per (KV head, group of up to 4 query heads, query tile): wave w takes
 // query head w % G4 and query sub-tile w / G4 (G4 = min(G, 4)), TMQ 16-query MFMA tiles of it. Each
-// 64-key block of K and V^T is staged once in LDS (16-byte copies of the split planes, the next
+// KB-key block (64; 32 at head_dim 256) of K and V^T is staged once in LDS (16-byte copies of the split planes, the next
 // block's loads in flight during the current block's MFMAs) and serves every query head of the
 // KV head. The scores are computed transposed, S^T = K Q^T with the keys as MFMA rows: a lane's
 // 16 scores of a block then all belong to one query (lane & 15), and with the K rows staged in the
@@ -426,7 +426,7 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(float* __restrict__ q, c
 // registers (no LDS round trip, no wave barrier), and 72 KB of LDS lets two workgroups share a
 // CU (NW = 4) or gives eight waves one staged block (NW = 8). Every product takes three MFMAs (hi*hi + hi*lo + lo*hi of the fp16 pairs, exact in f32);
 // the softmax is the online form per query. The longest (latest) query tiles are dispatched first.
-template <int HD, int TMQ, int NW>
+template <int HD, int TMQ, int NW, int KB>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_prefill_gqa_kernel(const float* __restrict__ q,
                                                                   const _Float16* __restrict__ kh,
                                                                   const _Float16* __restrict__ kl,
@@ -434,7 +434,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_prefill_gqa_kernel(const
                                                                   const _Float16* __restrict__ vl,
                                                                   float* __restrict__ out, int M, int Mp, int n_heads,
                                                                   int n_kv, int window, float scale) {
-  constexpr int KB = 64;         // keys per block
+  static_assert(KB == 32 || KB == 64, "keys per block");
   constexpr int JN = KB / 16;    // 16-key row tiles of S^T
   constexpr int KS = HD / 32;    // MFMA K steps of S^T
   constexpr int NS = HD / 16;    // 16-wide head-dim row tiles of O^T
@@ -733,16 +733,18 @@ size_t attn_prefill_scratch_halves(int M, int n_kv, int head_dim) {
   return 4 * (size_t)n_kv * head_dim * Mp;
 }
 
+// The split K / V^T planes and attn_prefill_gqa_kernel: head_dim 64, 128 and (through
+// kv_split_kernel only) 256.
 static bool attn_planes_ok(int M, int n_heads, int n_kv, int head_dim, const void* scratch, size_t scratch_halves) {
-  return scratch && M >= 1 && n_kv >= 1 && (head_dim == 64 || head_dim == 128) && n_heads % n_kv == 0 &&
-         scratch_halves >= attn_prefill_scratch_halves(M, n_kv, head_dim);
+  return scratch && M >= 1 && n_kv >= 1 && (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
+         n_heads % n_kv == 0 && scratch_halves >= attn_prefill_scratch_halves(M, n_kv, head_dim);
 }
 
 bool launch_attn_prefill_prep(float* q, const float* k, const float* v, int M, int n_heads, int n_kv, int head_dim,
                               const float* cs, int npairs, void* kc, void* vc, bool kv_f32, int ctx, int pos0,
                               void* scratch, size_t scratch_halves, int* ovf, hipStream_t st) {
-  if (!attn_planes_ok(M, n_heads, n_kv, head_dim, scratch, scratch_halves) || npairs < 0 || 2 * npairs > head_dim ||
-      !ovf)
+  if (!attn_planes_ok(M, n_heads, n_kv, head_dim, scratch, scratch_halves) || head_dim > 128 || npairs < 0 ||
+      2 * npairs > head_dim || !ovf)
     return false;
   if (pos0 < 0 || (size_t)pos0 + (size_t)M > (size_t)ctx) fail(ST_KVCACHE, "attention prep: the prompt does not fit the cache");
   const int Mp = ((M + 63) / 64) * 64;
@@ -784,20 +786,25 @@ void launch_attn_prefill(const float* q, const float* k, const float* v, float* 
     const bool wide = (size_t)n_kv * HG * ((M + qt8 - 1) / qt8) >= 2 * (size_t)num_cus();
     const int QT = wide ? qt8 : 16 * (4 / G4);
     const dim3 grid(n_kv * HG, (M + QT - 1) / QT);
-    if (head_dim == 128) {
+    if (head_dim == 256) {
+      // 32-key blocks (the K and V^T planes of a block take 75 KB), four waves of one tile
+      const int qt4 = 16 * (4 / G4);
+      hipLaunchKernelGGL((attn_prefill_gqa_kernel<256, 1, 4, 32>), dim3(n_kv * HG, (M + qt4 - 1) / qt4), dim3(256), 0,
+                         st, q, kh, kl, vh, vl, out, M, Mp, n_heads, n_kv, window, scale);
+    } else if (head_dim == 128) {
       if (wide)
-        hipLaunchKernelGGL((attn_prefill_gqa_kernel<128, 2, 8>), grid, dim3(512), 0, st, q, kh, kl, vh, vl, out, M, Mp,
-                           n_heads, n_kv, window, scale);
+        hipLaunchKernelGGL((attn_prefill_gqa_kernel<128, 2, 8, 64>), grid, dim3(512), 0, st, q, kh, kl, vh, vl, out, M,
+                           Mp, n_heads, n_kv, window, scale);
       else
-        hipLaunchKernelGGL((attn_prefill_gqa_kernel<128, 1, 4>), grid, dim3(256), 0, st, q, kh, kl, vh, vl, out, M, Mp,
-                           n_heads, n_kv, window, scale);
+        hipLaunchKernelGGL((attn_prefill_gqa_kernel<128, 1, 4, 64>), grid, dim3(256), 0, st, q, kh, kl, vh, vl, out, M,
+                           Mp, n_heads, n_kv, window, scale);
     } else {
       if (wide)
-        hipLaunchKernelGGL((attn_prefill_gqa_kernel<64, 2, 8>), grid, dim3(512), 0, st, q, kh, kl, vh, vl, out, M, Mp,
-                           n_heads, n_kv, window, scale);
+        hipLaunchKernelGGL((attn_prefill_gqa_kernel<64, 2, 8, 64>), grid, dim3(512), 0, st, q, kh, kl, vh, vl, out, M,
+                           Mp, n_heads, n_kv, window, scale);
       else
-        hipLaunchKernelGGL((attn_prefill_gqa_kernel<64, 1, 4>), grid, dim3(256), 0, st, q, kh, kl, vh, vl, out, M, Mp,
-                           n_heads, n_kv, window, scale);
+        hipLaunchKernelGGL((attn_prefill_gqa_kernel<64, 1, 4, 64>), grid, dim3(256), 0, st, q, kh, kl, vh, vl, out, M,
+                           Mp, n_heads, n_kv, window, scale);
     }
     return;
   }

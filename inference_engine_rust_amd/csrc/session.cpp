@@ -900,8 +900,8 @@ void Session::layer_prefill_gemma(int li, int M) {
   if (f32_prefill_)
     launch_attn_prefill_f32(q_, k_, v_, att_, M, c.n_heads, c.n_kv_heads, hd, S.window, 1.0f, st_);
   else
-    launch_attn_prefill(q_, k_, v_, att_, M, c.n_heads, c.n_kv_heads, hd, S.window, 1.0f, st_, nullptr, 0, false,
-                        d_ovf_);
+    launch_attn_prefill(q_, k_, v_, att_, M, c.n_heads, c.n_kv_heads, hd, S.window, 1.0f, st_, xs_, xs_halves(), false,
+                        d_ovf_);  // xs_ (the Q/K/V input pair, consumed) holds the K / V^T planes
   {
     const __half* xa = split_rows(att_, M, qd);
     const DevTensor* ws[1] = {&L.wo};
