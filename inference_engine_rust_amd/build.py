@@ -100,9 +100,19 @@ def _link_tool(src: str, out: str) -> str:
     return out
 
 
+def _hip_tool(src: str, out: str) -> str:
+    """A stand-alone HIP program (no library)."""
+    os.makedirs(BIN, exist_ok=True)
+    tmp = out + ".tmp"
+    _run([HIPCC, *HIP_FLAGS, src, "-o", tmp])
+    os.replace(tmp, out)
+    return out
+
+
 def build_tools() -> None:
     _link_tool(os.path.join(PKG, "cli", "bench_compare.cpp"), os.path.join(BIN, "iek_bench_compare"))
     _link_tool(os.path.join(REPO, "tests", "abi", "iek_abi_test.cpp"), os.path.join(BIN, "iek_abi_test"))
+    _hip_tool(os.path.join(PKG, "cli", "calibrate.hip"), os.path.join(BIN, "iek_calibrate"))
 
 
 def build_all() -> None:
