@@ -263,6 +263,17 @@ iek_status iek_dev_sample_temperature(const float* logits, size_t n, float tempe
 iek_status iek_dev_attention_decode(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
                                     size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t max_seq_len,
                                     size_t total_pos, size_t sliding_window, float scale, float* out, void* stream);
+/* The head loop of prefill_attention_layer (src/layers/attention.rs:364-415) over the layer's own
+ * K / V: q [seq][n_heads][head_dim] (RoPE applied), k and v [seq][n_kv_heads][head_dim], f32 in
+ * HBM; for every position p and query head h (KV head h / (n_heads / n_kv_heads)),
+ * out[p][h] = softmax(scale * q[p][h] . k[j]) . v[j] over j in [j_min, p], j_min = p -
+ * (sliding_window - 1) when 0 < sliding_window, else 0. Runs the session's prefill kernels (fp16
+ * (hi, lo) operand pairs on the matrix cores; an input beyond the pairs' range reruns on f32).
+ * Supported: head_dim 64, 128, 256 or 512 (IEK_ERR_OP otherwise); seq == 0 is IEK_ERR_OP. Allocates
+ * its scratch per call; waits for the stream before returning. */
+iek_status iek_dev_attention_prefill(const float* q, const float* k, const float* v, size_t seq, size_t n_heads,
+                                     size_t n_kv_heads, size_t head_dim, size_t sliding_window, float scale, float* out,
+                                     void* stream);
 /* No counterpart in the reference. For callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): iek_dev_attention_decode
  * with the same arguments, results and errors, but its partials, arrival counters and position live

@@ -466,6 +466,44 @@ iek_status iek_dev_attention_decode(const float* q, const void* k_cache, const v
   })
 }
 
+iek_status iek_dev_attention_prefill(const float* q, const float* k, const float* v, size_t seq, size_t n_heads,
+                                     size_t n_kv_heads, size_t head_dim, size_t sliding_window, float scale, float* out,
+                                     void* stream) {
+  IEK_API_TRY({
+    if (n_kv_heads == 0 || n_heads == 0 || n_heads % n_kv_heads != 0)
+      fail(ST_OP, "attention: the KV heads must divide the query heads");
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256 && head_dim != 512)
+      fail(ST_OP, "attention: head_dim must be 64, 128, 256 or 512");
+    if (seq == 0) fail(ST_OP, "softmax: empty input");
+    if (seq > (1u << 20) || n_heads > 4096 || sliding_window > (size_t)INT32_MAX) fail(ST_OP, "attention: dims too large");
+    const int M = (int)seq, nh = (int)n_heads, nkv = (int)n_kv_heads, hd = (int)head_dim;
+    const int win = sliding_window >= seq ? 0 : (int)sliding_window;  // a window covering every key is no window
+    hipStream_t st = as_stream(stream);
+    // the K / V^T fp16 planes of the shared-K/V kernel (head_dim up to 256), then the range flag
+    const size_t halves = hd <= 256 ? attn_prefill_scratch_halves(M, nkv, hd) : 0;
+    const size_t ovf_off = (halves * 2 + 255) / 256 * 256;
+    char* scratch = nullptr;
+    IEK_HIP(hipMalloc(&scratch, ovf_off + 256));
+    try {
+      int* ovf = reinterpret_cast<int*>(scratch + ovf_off);
+      launch_fill_i32(ovf, 0, 1, st);
+      launch_attn_prefill(q, k, v, out, M, nh, nkv, hd, win, scale, st, halves ? scratch : nullptr, halves, false, ovf);
+      int flagged = 0;
+      IEK_HIP(hipMemcpyAsync(&flagged, ovf, sizeof(int), hipMemcpyDeviceToHost, st));
+      IEK_HIP(hipStreamSynchronize(st));
+      // an input beyond the fp16 pair's range: the f32 kernel, as the session's prefill reruns
+      if (flagged) {
+        launch_attn_prefill_f32(q, k, v, out, M, nh, nkv, hd, win, scale, st);
+        IEK_HIP(hipStreamSynchronize(st));
+      }
+    } catch (...) {
+      (void)hipFree(scratch);
+      throw;
+    }
+    IEK_HIP(hipFree(scratch));
+  })
+}
+
 iek_status iek_dev_attention_decode_noalloc(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
                                             size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t max_seq_len,
                                             size_t total_pos, size_t sliding_window, float scale, float* out,

@@ -158,8 +158,9 @@ constexpr size_t NOALLOC_COUNTER_BYTES = 4096;
 // Device address of the scratch array of the stream's device (the current device for the null
 // stream), resolved once per device.
 void* noalloc_scratch(hipStream_t st);
-// With a scratch buffer of attn_prefill_scratch_halves() halves (head_dim 64 or 128), each K/V block
-// is staged once for all the query heads of its KV head; otherwise one workgroup per query head.
+// With a scratch buffer of attn_prefill_scratch_halves() halves (head_dim 64, 128 or 256), each K/V
+// block is staged once for all the query heads of its KV head; otherwise one workgroup per query
+// head.
 size_t attn_prefill_scratch_halves(int M, int n_kv, int head_dim);
 // planes_ready: launch_attn_prefill_prep already wrote the K/V planes into the scratch (and
 // flagged out-of-range inputs); otherwise q, k and v are range-checked here into *ovf (when given).

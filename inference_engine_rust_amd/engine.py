@@ -128,6 +128,7 @@ EXPORTS = {
                                  ctypes.c_int),
     "iek_dev_attention_decode_noalloc": ([_P, _P, _P, ctypes.c_int, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P,
                                           _P], ctypes.c_int),
+    "iek_dev_attention_prefill": ([_P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P, _P], ctypes.c_int),
     "iek_device_alloc": ([_SZ, ctypes.POINTER(_P)], ctypes.c_int),
     "iek_device_free": ([_P], ctypes.c_int),
     "iek_memcpy_h2d": ([_P, _P, _SZ], ctypes.c_int),
@@ -517,6 +518,13 @@ def attention_decode_noalloc(q_ptr: int, k_ptr: int, v_ptr: int, kv_dtype: int, 
     _check(lib().iek_dev_attention_decode_noalloc(q_ptr, k_ptr, v_ptr, kv_dtype, n_heads, n_kv_heads, head_dim,
                                                   max_seq_len, total_pos, sliding_window, scale, out_ptr,
                                                   stream or None))
+
+
+def attention_prefill(q_ptr: int, k_ptr: int, v_ptr: int, seq: int, n_heads: int, n_kv_heads: int, head_dim: int,
+                      sliding_window: int, scale: float, out_ptr: int, stream: int = 0) -> None:
+    """Prefill attention over the layer's own q / k / v rows (device pointers, f32)."""
+    _check(lib().iek_dev_attention_prefill(q_ptr, k_ptr, v_ptr, seq, n_heads, n_kv_heads, head_dim, sliding_window,
+                                           scale, out_ptr, stream or None))
 
 
 def synchronize() -> None:

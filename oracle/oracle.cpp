@@ -1252,6 +1252,64 @@ static const float* rope_ff(const LayerW& w, size_t* len) {
   return nullptr;
 }
 
+// The head loop of prefill_attention_layer (attention.rs:364-415): for every position p and
+// query head h (KV head h / group), scores q.K[j] * scale for j in [j_min, p] (j_min = p - (w - 1)
+// with a sliding window w >= 0; -inf below it), the reference softmax over p + 1 scores, then
+// out[p][h] = sum_j w[j] V[j] in j order. krow / vrow give the K and V rows of (position, KV head).
+template <class KRow, class VRow>
+static void prefill_heads(const float* q, size_t seq, size_t n_heads, size_t n_kv, size_t hd, long sliding_window,
+                          float scale, KRow krow, VRow vrow, float* out, int threads) {
+  const size_t qd = n_heads * hd, group = n_heads / n_kv;
+  // Keys transposed per KV head (kt[kvh][e][j], j padded to a multiple of 8) so that eight
+  // scores are formed at once, lane by lane in the same e order as the scalar dot product.
+  const size_t sp = (seq + 7) / 8 * 8;
+  std::vector<float> kt(n_kv * hd * sp, 0.0f);
+  parallel_for(n_kv, threads, [&](size_t kvh) {
+    for (size_t j = 0; j < seq; ++j) {
+      const float* kr = krow(j, kvh);
+      for (size_t e = 0; e < hd; ++e) kt[(kvh * hd + e) * sp + j] = kr[e];
+    }
+  });
+  typedef float v8 __attribute__((vector_size(32)));
+  // one work item per query head, positions in order (each output row depends on its own
+  // scores only, so the split does not change any value)
+  parallel_for(n_heads, threads, [&](size_t h) {
+    const size_t kvh = h / group;
+    std::vector<float> sc(seq), wts(seq);
+    for (size_t p = 0; p < seq; ++p) {
+      size_t j_min = 0;
+      if (sliding_window >= 0) {
+        size_t wm1 = sliding_window > 0 ? (size_t)sliding_window - 1 : 0;
+        j_min = p > wm1 ? p - wm1 : 0;
+      }
+      const float* qv = &q[p * qd + h * hd];
+      for (size_t j = 0; j < j_min; ++j) sc[j] = -INFINITY;
+      for (size_t j0 = j_min / 8 * 8; j0 <= p; j0 += 8) {
+        v8 dot = {};
+        for (size_t e = 0; e < hd; ++e) {
+          v8 kk;
+          memcpy(&kk, &kt[(kvh * hd + e) * sp + j0], 32);
+          const float qe = qv[e];
+          const v8 qb = {qe, qe, qe, qe, qe, qe, qe, qe};
+          const v8 prod = qb * kk;
+          dot = dot + prod;
+        }
+        for (size_t l = 0; l < 8; ++l) {
+          const size_t j = j0 + l;
+          if (j >= j_min && j <= p) sc[j] = dot[l] * scale;
+        }
+      }
+      softmax(sc.data(), wts.data(), p + 1);
+      float* o = &out[p * qd + h * hd];
+      for (size_t j = j_min; j <= p; ++j) {
+        const float wt = wts[j];
+        const float* vv = vrow(j, kvh);
+        for (size_t e = 0; e < hd; ++e) o[e] += wt * vv[e];
+      }
+    }
+  });
+}
+
 // prefill_attention_layer (attention.rs:175-422); input = normed hidden [seq, hidden].
 static std::vector<float> prefill_attention(Session& s, const float* input, size_t seq, size_t li) {
   const Model& m = *s.model;
@@ -1270,7 +1328,6 @@ static std::vector<float> prefill_attention(Session& s, const float* input, size
     if (src.n_kv_heads != c.n_kv_heads || src.head_dim != hd) fail(E_MODEL, "borrow source KV shape mismatch");
     if (src.current_pos != seq) fail(E_MODEL, "prefill attention: borrow source cache len mismatch");
   }
-  size_t group = c.n_heads / c.n_kv_heads;
   std::vector<float> q(seq * qd), k(seq * kvd, 0.0f), v(seq * kvd, 0.0f);
   matmul(input, seq, c.hidden_dim, *w.wq, q.data(), seq, qd, s.mode, s.threads);
   if (borrow < 0) {
@@ -1309,54 +1366,8 @@ static std::vector<float> prefill_attention(Session& s, const float* input, size
   auto vrow = [&](size_t j, size_t kvh) -> const float* {
     return borrow >= 0 ? vslice(s.kv[src_idx], j, kvh) : &v[j * kvd + kvh * hd];
   };
-  // Keys transposed per KV head (kt[kvh][e][j], j padded to a multiple of 8) so that eight
-  // scores are formed at once, lane by lane in the same e order as the scalar dot product.
-  const size_t sp = (seq + 7) / 8 * 8;
-  std::vector<float> kt(c.n_kv_heads * hd * sp, 0.0f);
-  parallel_for(c.n_kv_heads, s.threads, [&](size_t kvh) {
-    for (size_t j = 0; j < seq; ++j) {
-      const float* kr = krow(j, kvh);
-      for (size_t e = 0; e < hd; ++e) kt[(kvh * hd + e) * sp + j] = kr[e];
-    }
-  });
-  typedef float v8 __attribute__((vector_size(32)));
-  // one work item per query head, positions in order (each output row depends on its own
-  // scores only, so the split does not change any value)
-  parallel_for(c.n_heads, s.threads, [&](size_t h) {
-    const size_t kvh = h / group;
-    std::vector<float> sc(seq), wts(seq);
-    for (size_t p = 0; p < seq; ++p) {
-      size_t j_min = 0;
-      if (la.sliding_window >= 0) {
-        size_t wm1 = la.sliding_window > 0 ? (size_t)la.sliding_window - 1 : 0;
-        j_min = p > wm1 ? p - wm1 : 0;
-      }
-      const float* qv = &q[p * qd + h * hd];
-      for (size_t j = 0; j < j_min; ++j) sc[j] = -INFINITY;
-      for (size_t j0 = j_min / 8 * 8; j0 <= p; j0 += 8) {
-        v8 dot = {};
-        for (size_t e = 0; e < hd; ++e) {
-          v8 kk;
-          memcpy(&kk, &kt[(kvh * hd + e) * sp + j0], 32);
-          const float qe = qv[e];
-          const v8 qb = {qe, qe, qe, qe, qe, qe, qe, qe};
-          const v8 prod = qb * kk;
-          dot = dot + prod;
-        }
-        for (size_t l = 0; l < 8; ++l) {
-          const size_t j = j0 + l;
-          if (j >= j_min && j <= p) sc[j] = dot[l] * scale;
-        }
-      }
-      softmax(sc.data(), wts.data(), p + 1);
-      float* o = &out[p * qd + h * hd];
-      for (size_t j = j_min; j <= p; ++j) {
-        const float wt = wts[j];
-        const float* vv = vrow(j, kvh);
-        for (size_t e = 0; e < hd; ++e) o[e] += wt * vv[e];
-      }
-    }
-  });
+  prefill_heads(q.data(), seq, c.n_heads, c.n_kv_heads, hd, la.sliding_window, scale, krow, vrow, out.data(),
+                s.threads);
   std::vector<float> proj(seq * c.hidden_dim);
   matmul(out.data(), seq, qd, *w.wo, proj.data(), seq, c.hidden_dim, s.mode, s.threads);
   return proj;
@@ -1686,6 +1697,21 @@ int orc_attention_decode(const float* q, const float* k, const float* v, size_t 
     if (sliding_window >= 0) j_min = total > (size_t)sliding_window ? total - (size_t)sliding_window : 0;
     std::fill(out, out + n_heads * hd, 0.0f);
     decode_heads(q, kv, n_heads, total, j_min, scale, out, 1);
+  })
+}
+
+// The head loop of prefill_attention_layer over the layer's own k / v ([seq][n_kv][head_dim]),
+// q [seq][n_heads][head_dim] (RoPE already applied); sliding_window < 0 = none.
+int orc_attention_prefill(const float* q, const float* k, const float* v, size_t seq, size_t n_heads, size_t n_kv,
+                          size_t hd, long sliding_window, float scale, float* out) {
+  ORC_TRY({
+    if (n_kv == 0 || n_heads % n_kv != 0) fail(E_MODEL, "attention: n_heads % n_kv_heads != 0");
+    const size_t kvd = n_kv * hd;
+    std::fill(out, out + seq * n_heads * hd, 0.0f);
+    auto krow = [&](size_t j, size_t kvh) -> const float* { return &k[j * kvd + kvh * hd]; };
+    auto vrow = [&](size_t j, size_t kvh) -> const float* { return &v[j * kvd + kvh * hd]; };
+    prefill_heads(q, seq, n_heads, n_kv, hd, sliding_window, scale, krow, vrow, out,
+                  (int)std::max(1u, std::thread::hardware_concurrency()));
   })
 }
 

@@ -70,6 +70,8 @@ def lib():
         L.orc_unpack_qk_row.argtypes = [_f, ctypes.c_size_t, ctypes.c_size_t]
         L.orc_attention_decode.argtypes = [_f, _f, _f, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
                                            ctypes.c_size_t, ctypes.c_long, ctypes.c_float, _f]
+        L.orc_attention_prefill.argtypes = [_f, _f, _f, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
+                                            ctypes.c_size_t, ctypes.c_long, ctypes.c_float, _f]
         L.orc_model_load.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)]
         L.orc_model_free.argtypes = [_f]
         L.orc_model_config.argtypes = [_f, ctypes.POINTER(Cfg)]
@@ -214,6 +216,19 @@ def attention_decode(q, k, v, n_heads, n_kv, head_dim, total, sliding_window, sc
     out = np.empty(n_heads * head_dim, np.float32)
     _check(lib().orc_attention_decode(_p(q), _p(k), _p(v), n_heads, n_kv, head_dim, total, sliding_window, scale,
                                       _p(out)))
+    return out
+
+
+def attention_prefill(q, k, v, seq, n_heads, n_kv, head_dim, sliding_window, scale):
+    """The head loop of prefill_attention_layer (attention.rs:364-415) over the layer's own k / v
+    ([seq][n_kv][head_dim]); q [seq][n_heads][head_dim] after RoPE; sliding_window < 0 = none.
+    Returns [seq][n_heads][head_dim]."""
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    out = np.empty(seq * n_heads * head_dim, np.float32)
+    _check(lib().orc_attention_prefill(_p(q), _p(k), _p(v), seq, n_heads, n_kv, head_dim, sliding_window, scale,
+                                       _p(out)))
     return out
 
 

@@ -188,6 +188,66 @@ def test_attention_decode_errors(gpu):
     assert e.value.kind == "KvCache"
 
 
+# ---- prefill attention ---------------------------------------------------------------------------
+
+PREFILL_ATT_CASES = [  # n_heads, n_kv, head_dim, seq, window
+    (32, 8, 128, 512, 0),    # C2's layer: one 16-query tile per wave, two workgroups per CU
+    (32, 8, 128, 1, 0), (32, 8, 128, 17, 0), (32, 8, 128, 200, 50),  # ragged tiles, a window
+    (32, 8, 128, 4100, 1000),  # eight waves of two query tiles per staged block, a window
+    (8, 2, 64, 333, 0), (8, 2, 64, 4200, 0),  # head_dim 64, both launch shapes
+    (4, 4, 128, 150, 0), (16, 2, 128, 97, 0),  # one query head per KV head; eight per KV head
+    (8, 1, 256, 256, 0), (8, 1, 256, 300, 100), (8, 1, 512, 130, 64),  # Gemma-4 head layouts
+]
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hd,seq,window", PREFILL_ATT_CASES)
+def test_dev_attention_prefill_matches_oracle(gpu, n_heads, n_kv, hd, seq, window):
+    """The session's prefill attention kernels through the op-level entry against the oracle's
+    head loop (attention.rs:364-415): within the fp16-pair operand rounding, 2e-5 relative L2
+    (the pairs keep 22 significant bits; the same bar holds the C2 and C4 prefill tests)."""
+    rng = np.random.default_rng(seq * 7 + hd + window)
+    q = rng.standard_normal(seq * n_heads * hd).astype(np.float32)
+    k = rng.standard_normal(seq * n_kv * hd).astype(np.float32)
+    v = rng.standard_normal(seq * n_kv * hd).astype(np.float32)
+    scale = 1.0 / math.sqrt(hd)
+    want = O.attention_prefill(q, k, v, seq, n_heads, n_kv, hd, window if window > 0 else -1, scale)
+    dq, dk, dv = (torch.from_numpy(a).to("cuda") for a in (q, k, v))
+    out = torch.full((seq * n_heads * hd,), float("nan"), dtype=torch.float32, device="cuda")
+    E.attention_prefill(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), seq, n_heads, n_kv, hd, window, scale,
+                        out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    got = out.cpu().numpy()
+    assert np.isfinite(got).all()
+    assert rel_l2(got, want) < 2e-5, rel_l2(got, want)
+    # per position: the worst row stays within the bar too (a wrong mask shows in single rows)
+    g, w = got.reshape(seq, -1), want.reshape(seq, -1)
+    worst = max(rel_l2(g[p], w[p]) for p in range(0, seq, max(1, seq // 64)))
+    assert worst < 1e-4, worst
+
+
+def test_dev_attention_prefill_beyond_fp16_range_and_errors(gpu):
+    """Scores from inputs past 65 504 (the fp16 pairs' range) take the f32 kernel: still the
+    oracle's result; and the entry's errors."""
+    n_heads, n_kv, hd, seq = 8, 2, 128, 70
+    rng = np.random.default_rng(11)
+    q = rng.standard_normal(seq * n_heads * hd).astype(np.float32)
+    k = (rng.standard_normal(seq * n_kv * hd) * 1e-3).astype(np.float32)
+    v = rng.standard_normal(seq * n_kv * hd).astype(np.float32)
+    q[5 * n_heads * hd + 3] = 2.0e5  # one query value beyond the pair range
+    v[9 * n_kv * hd + 7] = -1.0e6    # one value row too
+    scale = 1.0 / math.sqrt(hd)
+    want = O.attention_prefill(q, k, v, seq, n_heads, n_kv, hd, -1, scale)
+    dq, dk, dv = (torch.from_numpy(a).to("cuda") for a in (q, k, v))
+    out = torch.empty(seq * n_heads * hd, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    E.attention_prefill(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), seq, n_heads, n_kv, hd, 0, scale,
+                        out.data_ptr(), stream)
+    assert rel_l2(out.cpu().numpy(), want) < 1e-5
+    for args in [(seq, 8, 3, hd), (0, 8, 2, hd), (seq, 8, 2, 96)]:
+        with pytest.raises(E.EngineError) as e:
+            E.attention_prefill(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), *args, 0, scale, out.data_ptr(), stream)
+        assert e.value.kind == "Op"
+
+
 # ---- forward level -------------------------------------------------------------------------------
 
 @pytest.fixture(scope="module")

@@ -309,6 +309,41 @@ def test_attention_decode_matches_float64_softmax(n_heads, n_kv, hd, total, wind
     np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5)
 
 
+@pytest.mark.parametrize("n_heads,n_kv,hd,seq,window", [(8, 2, 64, 37, -1), (8, 8, 32, 5, -1),
+                                                        (6, 1, 16, 40, 7), (4, 2, 128, 70, 1), (8, 1, 16, 33, 0)])
+def test_attention_prefill_matches_float64_softmax(n_heads, n_kv, hd, seq, window):
+    """Every position p of the prefill head loop against the float64 softmax over keys
+    [p - (window - 1), p] (window < 0: [0, p]; window 0 keeps position p only, as the reference's
+    saturating j_min does)."""
+    rng = np.random.default_rng(seq + hd)
+    q = rng.standard_normal(seq * n_heads * hd).astype(np.float32)
+    k = rng.standard_normal(seq * n_kv * hd).astype(np.float32)
+    v = rng.standard_normal(seq * n_kv * hd).astype(np.float32)
+    scale = 1.0 / math.sqrt(hd)
+    got = O.attention_prefill(q, k, v, seq, n_heads, n_kv, hd, window, scale).reshape(seq, -1)
+    for p in range(seq):
+        w = -1 if window < 0 else max(window, 1)
+        want = _attn_f64(q[p * n_heads * hd:(p + 1) * n_heads * hd], k[:(p + 1) * n_kv * hd],
+                         v[:(p + 1) * n_kv * hd], n_heads, n_kv, hd, p + 1, w, scale)
+        np.testing.assert_allclose(got[p], want, rtol=1e-4, atol=1e-5, err_msg=f"position {p}")
+
+
+def test_attention_prefill_row_is_the_decode_of_its_prefix():
+    """Position p of the prefill equals the decode head loop over the cache of positions 0..p
+    (the same scores, softmax and accumulation order): bit for bit."""
+    n_heads, n_kv, hd, seq = 8, 2, 64, 29
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal(seq * n_heads * hd).astype(np.float32)
+    k = rng.standard_normal(seq * n_kv * hd).astype(np.float32)
+    v = rng.standard_normal(seq * n_kv * hd).astype(np.float32)
+    for window in (-1, 6):
+        got = O.attention_prefill(q, k, v, seq, n_heads, n_kv, hd, window, 0.125).reshape(seq, -1)
+        for p in range(seq):
+            want = O.attention_decode(q[p * n_heads * hd:(p + 1) * n_heads * hd], k[:(p + 1) * n_kv * hd],
+                                      v[:(p + 1) * n_kv * hd], n_heads, n_kv, hd, p + 1, window, 0.125)
+            assert np.array_equal(got[p], want), (window, p)
+
+
 def test_attention_decode_closed_forms():
     n_heads, n_kv, hd, total = 8, 2, 16, 9
     rng = np.random.default_rng(3)
